@@ -1,0 +1,138 @@
+/*
+ * qwen36_hip.h -- C-ABI of the MI355X (gfx950) attention hot-path library.
+ *
+ * This library replaces the pybind11 module `qwen36_fp8` of the reference
+ * (src/csrc/fp8_linear.cpp:5-21, declared in src/csrc/fp8_linear.h:99-119) and
+ * its loader (src/cuda_loader.py:40-54) for the attention hot path.  Every
+ * entry point takes plain device pointers, sizes, element strides, dtype codes
+ * and a hipStream_t; none takes or returns a torch type.  Callers allocate all
+ * outputs and workspaces; the library never allocates device memory.
+ *
+ * Return value: 0 on success, non-zero on failure; qa_last_error() then holds
+ * a message (per calling thread).  Shape/dtype errors are detected on the host
+ * before any launch.
+ *
+ * Element strides are in elements of the tensor's own dtype.  The innermost
+ * (head_dim / channel) axis is always contiguous.
+ */
+#ifndef QWEN36_HIP_H
+#define QWEN36_HIP_H
+
+#include <stdint.h>
+#include <hip/hip_runtime_api.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* dtype codes */
+enum {
+  QA_F32 = 0,
+  QA_BF16 = 1,
+  QA_F16 = 2,
+  QA_I32 = 3,
+  QA_I64 = 4
+};
+
+/* Paged KV pool descriptor.
+ *
+ * Element (row b, kv head g, physical block p, slot t, dim d) lives at
+ *   base_b + p*stride_block + g*stride_head + t*stride_token + d
+ * where base_b = key + b*stride_batch, or row_key_ptrs[b] when the per-row
+ * pointer arrays are given (the reference's list-of-pools form,
+ * src/fp8_cuda.py:235-250).  The reference's per-request pool layout
+ * (batch, heads, P, bs, D) (src/decode_state.py:37-44) and this library's
+ * shared GQA-native pool (P, H_kv, bs, D) are both expressible.
+ * With per-row pointer arrays and stride_head == 0, row b's head stride is
+ * row_blocks[b]*stride_block: contiguous per-request pools
+ * (1, heads, P_b, bs, D) of different P_b.
+ * Physical ids outside [0, num_blocks) (or row_blocks[b]) are skipped.     */
+typedef struct qa_paged_kv {
+  void* key;
+  void* value;
+  const int64_t* row_key_ptrs;   /* device (B,) or NULL */
+  const int64_t* row_value_ptrs; /* device (B,) or NULL */
+  const int64_t* row_blocks;     /* device (B,) physical block counts or NULL */
+  int64_t num_blocks;
+  int64_t stride_batch;
+  int64_t stride_block;
+  int64_t stride_head;
+  int64_t stride_token;
+  int32_t kv_heads;
+  int32_t dtype;                 /* QA_F32 or QA_BF16 */
+} qa_paged_kv;
+
+/* ---- library ---------------------------------------------------------- */
+const char* qa_last_error(void);
+int32_t qa_version(void);
+const char* qa_arch(void);
+
+/* ---- paged GQA decode ------------------------------------------------- */
+/* Bytes of fp32 workspace the decode entry points need for these sizes.   */
+int64_t qa_paged_attention_decode_workspace(int64_t batch, int32_t heads, int32_t head_dim,
+                                            int64_t max_tokens, int32_t block_size);
+
+/* Single-table decode.  Replaces `paged_attention_decode`
+ * (src/fp8_cuda.py:217-232 -> src/csrc/fp8_linear.h:106-112,
+ * src/csrc/fp8_linear_cuda.cu:1192-1266).  All `batch` rows read the same
+ * block table (len table_len) and attend over `sequence_length` tokens of
+ * their own pool row.  query/output: (batch, heads, head_dim) rows with
+ * element strides q_stride_b / q_stride_h; output is contiguous.
+ * scale <= 0 selects head_dim^-0.5 (src/csrc/fp8_linear_cuda.cu:912).     */
+int qa_paged_attention_decode(const void* query, int32_t q_dtype, int64_t q_stride_b, int64_t q_stride_h,
+                              int64_t batch, int32_t heads, int32_t head_dim,
+                              const qa_paged_kv* kv,
+                              const void* block_table, int32_t table_dtype, int64_t table_len,
+                              int64_t sequence_length, int32_t block_size, float scale,
+                              void* output, void* workspace, int64_t workspace_bytes,
+                              hipStream_t stream);
+
+/* Batched decode with per-row tables (B, max_blocks), -1 padded, and
+ * per-row device lengths (int32 or int64).  Rows with length <= 0 produce
+ * zeros.  Replaces `paged_attention_decode_batched`
+ * (src/fp8_cuda.py:235-250 -> src/csrc/fp8_linear.h:113-119,
+ * src/csrc/fp8_linear_cuda.cu:1269-1365).                                  */
+int qa_paged_attention_decode_batched(const void* query, int32_t q_dtype, int64_t q_stride_b, int64_t q_stride_h,
+                                      int64_t batch, int32_t heads, int32_t head_dim,
+                                      const qa_paged_kv* kv,
+                                      const void* block_tables, int32_t table_dtype, int64_t table_stride,
+                                      int64_t max_blocks,
+                                      const void* sequence_lengths, int32_t lengths_dtype,
+                                      int32_t block_size, float scale,
+                                      void* output, void* workspace, int64_t workspace_bytes,
+                                      hipStream_t stream);
+
+/* ---- paged KV cache --------------------------------------------------- */
+/* Write `new_tokens` tokens of each row into its slots
+ * (table[pos/bs], pos%bs) for pos = start_b .. start_b + count_b - 1.
+ * key_new/value_new: (batch, kv_heads, new_tokens, head_dim) with element
+ * strides (src_stride_b, src_stride_h, src_stride_s).  start positions are
+ * per-row device values (int32/int64) or, when starts == NULL, start_scalar.
+ * counts (device, may be NULL = all new_tokens) limits each row.  Same dtype
+ * as the pool; a bit-exact copy.  Positions whose logical block is past
+ * max_blocks or whose block id is invalid are not written.  Replaces FullAttentionCache.append_blocks
+ * (src/decode_state.py:271-293).                                          */
+int qa_paged_kv_append(const void* key_new, const void* value_new, int32_t dtype,
+                       int64_t src_stride_b, int64_t src_stride_h, int64_t src_stride_s,
+                       int64_t batch, int32_t kv_heads, int64_t new_tokens, int32_t head_dim,
+                       const qa_paged_kv* kv,
+                       const void* block_tables, int32_t table_dtype, int64_t table_stride,
+                       int64_t max_blocks,
+                       const void* starts, int32_t starts_dtype, int64_t start_scalar,
+                       const void* counts, int32_t counts_dtype,
+                       int32_t block_size, hipStream_t stream);
+
+/* Dense logical-order copy of the first `valid` tokens of each row:
+ * out (batch, kv_heads, valid, head_dim) contiguous.  Replaces
+ * FullAttentionCache.as_tensors / _gather_blocks (src/decode_state.py:295-303,
+ * 395-404).  Tokens whose block id is invalid are written as zeros.        */
+int qa_paged_kv_gather(const qa_paged_kv* kv, int32_t head_dim, int64_t batch,
+                       const void* block_tables, int32_t table_dtype, int64_t table_stride,
+                       int64_t max_blocks, int64_t valid, int32_t block_size,
+                       void* key_out, void* value_out, hipStream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* QWEN36_HIP_H */

@@ -1,0 +1,377 @@
+// Paged GQA decode attention for gfx950: split-K partial softmax + combine.
+//
+// One query token per (row, query head) attends over the row's paged KV.
+// Work item = (row b, KV head g, token split s): all G = H / H_kv query heads
+// of the GQA group are processed together so every K/V byte is read once per
+// group (the reference instead reads repeated heads, src/tp_runtime.py:518-525,
+// and serialises every token of a (b, h) pair in one block,
+// src/csrc/fp8_linear_cuda.cu:862-1059).  Each work item writes an
+// unnormalised partial (m, l, o) per head; a combine kernel merges the splits
+// with a log-sum-exp rescale.
+#include "qa_common.h"
+
+#include <algorithm>
+
+namespace qa {
+
+struct DecodeParams {
+  const void* q;
+  int64_t q_sb, q_sh;
+  void* out;  // contiguous (B, H, D)
+  const void* kbase;
+  const void* vbase;
+  const int64_t* row_k;
+  const int64_t* row_v;
+  const int64_t* row_blocks;
+  int64_t num_blocks, sB, sP, sG, sT;
+  const void* tables;
+  int64_t table_stride;
+  int64_t max_blocks;
+  const void* lens;  // nullptr -> len_scalar
+  int64_t len_scalar;
+  int B, H, Hkv, D, bs, G;
+  int table_i64, lens_i64;
+  float scale;
+  int split_tokens, n_splits;
+  float* part_o;   // (B*H, n_splits, D)
+  float* part_ml;  // (B*H, n_splits, 2)
+};
+
+__device__ __forceinline__ int64_t row_length(const DecodeParams& p, int b) {
+  if (p.lens == nullptr) return p.len_scalar;
+  return p.lens_i64 ? reinterpret_cast<const int64_t*>(p.lens)[b] : reinterpret_cast<const int32_t*>(p.lens)[b];
+}
+
+__device__ __forceinline__ int64_t table_entry(const DecodeParams& p, int b, int64_t logical) {
+  if (logical >= p.max_blocks) return -1;
+  const int64_t off = static_cast<int64_t>(b) * p.table_stride + logical;
+  return p.table_i64 ? reinterpret_cast<const int64_t*>(p.tables)[off] : reinterpret_cast<const int32_t*>(p.tables)[off];
+}
+
+// Base pointers, physical block count and head stride of row b's pool.
+template <typename KT>
+__device__ __forceinline__ void row_pool(const DecodeParams& p, int b, const KT*& kb, const KT*& vb, int64_t& nblk, int64_t& sG) {
+  if (p.row_k != nullptr) {
+    kb = reinterpret_cast<const KT*>(p.row_k[b]);
+    vb = reinterpret_cast<const KT*>(p.row_v[b]);
+    nblk = p.row_blocks != nullptr ? p.row_blocks[b] : p.num_blocks;
+    sG = p.sG != 0 ? p.sG : nblk * p.sP;
+  } else {
+    kb = reinterpret_cast<const KT*>(p.kbase) + static_cast<int64_t>(b) * p.sB;
+    vb = reinterpret_cast<const KT*>(p.vbase) + static_cast<int64_t>(b) * p.sB;
+    nblk = p.num_blocks;
+    sG = p.sG;
+  }
+}
+
+// Generic path: any head_dim <= 64*NPL, group size <= GMAX, fp32 or bf16.
+// One wavefront per work item; lanes split head_dim (lane + 64*i), tokens are
+// visited in order with an online softmax per head.
+template <typename QT, typename KT, int GMAX, int NPL>
+__global__ __launch_bounds__(64) void decode_partial_generic(DecodeParams p) {
+  const int split = blockIdx.x;
+  const int bg = blockIdx.y;
+  const int b = bg / p.Hkv;
+  const int g = bg - b * p.Hkv;
+  const int lane = threadIdx.x;
+  const int64_t len = row_length(p, b);
+  const int64_t t0 = static_cast<int64_t>(split) * p.split_tokens;
+  const int64_t t1 = min(len, t0 + p.split_tokens);
+
+  const KT* kb;
+  const KT* vb;
+  int64_t nblk, sG;
+  row_pool(p, b, kb, vb, nblk, sG);
+  kb += static_cast<int64_t>(g) * sG;
+  vb += static_cast<int64_t>(g) * sG;
+
+  float qr[GMAX][NPL];
+  const QT* qbase = reinterpret_cast<const QT*>(p.q) + static_cast<int64_t>(b) * p.q_sb;
+#pragma unroll
+  for (int j = 0; j < GMAX; ++j) {
+#pragma unroll
+    for (int i = 0; i < NPL; ++i) {
+      const int d = lane + 64 * i;
+      qr[j][i] = (j < p.G && d < p.D) ? Elem<QT>::load(qbase + static_cast<int64_t>(g * p.G + j) * p.q_sh + d) * p.scale : 0.f;
+    }
+  }
+  float m[GMAX], l[GMAX], acc[GMAX][NPL];
+#pragma unroll
+  for (int j = 0; j < GMAX; ++j) {
+    m[j] = -INFINITY;
+    l[j] = 0.f;
+#pragma unroll
+    for (int i = 0; i < NPL; ++i) acc[j][i] = 0.f;
+  }
+
+  for (int64_t t = t0; t < t1; ++t) {
+    const int64_t phys = table_entry(p, b, t / p.bs);
+    if (phys < 0 || phys >= nblk) continue;
+    const int64_t off = phys * p.sP + (t % p.bs) * p.sT;
+    float kv[NPL], vv[NPL];
+#pragma unroll
+    for (int i = 0; i < NPL; ++i) {
+      const int d = lane + 64 * i;
+      kv[i] = d < p.D ? Elem<KT>::load(kb + off + d) : 0.f;
+      vv[i] = d < p.D ? Elem<KT>::load(vb + off + d) : 0.f;
+    }
+#pragma unroll
+    for (int j = 0; j < GMAX; ++j) {
+      if (GMAX == 1 || j < p.G) {
+        float part = 0.f;
+#pragma unroll
+        for (int i = 0; i < NPL; ++i) part += qr[j][i] * kv[i];
+        const float s = wave_sum(part);
+        const float m_new = fmaxf(m[j], s);
+        const float c = __expf(m[j] - m_new);
+        const float pr = __expf(s - m_new);
+        l[j] = l[j] * c + pr;
+#pragma unroll
+        for (int i = 0; i < NPL; ++i) acc[j][i] = acc[j][i] * c + pr * vv[i];
+        m[j] = m_new;
+      }
+    }
+  }
+
+#pragma unroll
+  for (int j = 0; j < GMAX; ++j) {
+    if (j >= p.G) continue;
+    const int64_t slot = (static_cast<int64_t>(b) * p.H + g * p.G + j) * p.n_splits + split;
+    float* po = p.part_o + slot * p.D;
+#pragma unroll
+    for (int i = 0; i < NPL; ++i) {
+      const int d = lane + 64 * i;
+      if (d < p.D) po[d] = acc[j][i];
+    }
+    if (lane == 0) {
+      p.part_ml[slot * 2 + 0] = m[j];
+      p.part_ml[slot * 2 + 1] = l[j];
+    }
+  }
+}
+
+// Merge the splits of one (row, head): O = sum_s e^{m_s-M} o_s / sum_s e^{m_s-M} l_s.
+// Rows without any visible token (length <= 0, or only invalid blocks) get 0.
+template <typename QT>
+__global__ __launch_bounds__(256) void decode_combine(DecodeParams p) {
+  const int64_t bh = blockIdx.x;
+  const float* ml = p.part_ml + bh * p.n_splits * 2;
+  const float* po = p.part_o + bh * p.n_splits * p.D;
+  float big = -INFINITY;
+  for (int s = 0; s < p.n_splits; ++s) big = fmaxf(big, ml[2 * s]);
+  QT* out = reinterpret_cast<QT*>(p.out) + bh * p.D;
+  if (big == -INFINITY) {
+    for (int d = threadIdx.x; d < p.D; d += blockDim.x) Elem<QT>::store(out + d, 0.f);
+    return;
+  }
+  float denom = 0.f;
+  for (int s = 0; s < p.n_splits; ++s) {
+    const float ms = ml[2 * s];
+    if (ms != -INFINITY) denom += __expf(ms - big) * ml[2 * s + 1];
+  }
+  const float inv = denom > 0.f ? 1.f / denom : 0.f;
+  for (int d = threadIdx.x; d < p.D; d += blockDim.x) {
+    float acc = 0.f;
+    for (int s = 0; s < p.n_splits; ++s) {
+      const float ms = ml[2 * s];
+      if (ms != -INFINITY) acc += __expf(ms - big) * po[static_cast<int64_t>(s) * p.D + d];
+    }
+    Elem<QT>::store(out + d, acc * inv);
+  }
+}
+
+// Token count handled by one work item.  Shared by the workspace query and
+// the launcher so the two always agree.
+static int choose_split_tokens(int64_t max_tokens, int block_size) {
+  const int64_t lo = ceil_div(64, block_size) * block_size;
+  const int64_t hi = std::max<int64_t>(lo, ceil_div(512, block_size) * block_size);
+  int64_t want = ceil_div(ceil_div(std::max<int64_t>(max_tokens, 1), 16), block_size) * block_size;
+  return static_cast<int>(std::min(hi, std::max(lo, want)));
+}
+
+static int64_t decode_workspace_bytes(int64_t batch, int heads, int head_dim, int64_t max_tokens, int block_size) {
+  const int split = choose_split_tokens(max_tokens, block_size);
+  const int64_t n_splits = std::max<int64_t>(1, ceil_div(std::max<int64_t>(max_tokens, 1), split));
+  return batch * heads * n_splits * (head_dim + 2) * static_cast<int64_t>(sizeof(float));
+}
+
+template <typename QT, typename KT, int GMAX, int NPL>
+static int launch_generic(DecodeParams& p, hipStream_t stream) {
+  dim3 grid(p.n_splits, p.B * p.Hkv);
+  hipLaunchKernelGGL((decode_partial_generic<QT, KT, GMAX, NPL>), grid, dim3(64), 0, stream, p);
+  if (int rc = check_launch("decode_partial_generic")) return rc;
+  hipLaunchKernelGGL((decode_combine<QT>), dim3(p.B * p.H), dim3(256), 0, stream, p);
+  return check_launch("decode_combine");
+}
+
+template <typename QT, typename KT>
+static int dispatch_generic(DecodeParams& p, hipStream_t stream) {
+  const int npl_need = static_cast<int>(ceil_div(p.D, 64));
+  const int npl = npl_need <= 2 ? 2 : npl_need <= 4 ? 4 : npl_need <= 8 ? 8 : 16;
+  const int gmax = p.G <= 1 ? 1 : p.G <= 4 ? 4 : p.G <= 8 ? 8 : 16;
+  if (gmax * npl > 64) return fail("paged decode: group size %d with head_dim %d exceeds the register budget", p.G, p.D);
+#define QA_CASE(GM, NP) \
+  if (gmax == GM && npl == NP) return launch_generic<QT, KT, GM, NP>(p, stream);
+  QA_CASE(1, 2) QA_CASE(1, 4) QA_CASE(1, 8) QA_CASE(1, 16)
+  QA_CASE(4, 2) QA_CASE(4, 4) QA_CASE(4, 8) QA_CASE(4, 16)
+  QA_CASE(8, 2) QA_CASE(8, 4) QA_CASE(8, 8)
+  QA_CASE(16, 2) QA_CASE(16, 4)
+#undef QA_CASE
+  return fail("paged decode: no kernel for group %d head_dim %d", p.G, p.D);
+}
+
+struct DecodeHostArgs {
+  const void* query;
+  int32_t q_dtype;
+  int64_t q_sb, q_sh;
+  int64_t batch;
+  int32_t heads, head_dim;
+  const qa_paged_kv* kv;
+  const void* tables;
+  int32_t table_dtype;
+  int64_t table_stride, max_blocks;
+  const void* lens;
+  int32_t lens_dtype;
+  int64_t len_scalar;
+  int64_t max_tokens;
+  int32_t block_size;
+  float scale;
+  void* output;
+  void* workspace;
+  int64_t workspace_bytes;
+};
+
+static int run_decode(const DecodeHostArgs& a, hipStream_t stream) {
+  QA_REQUIRE(a.kv != nullptr, "paged decode: kv descriptor is null");
+  const qa_paged_kv& kv = *a.kv;
+  QA_REQUIRE(a.query && a.output, "paged decode: query/output pointers must be non-null");
+  QA_REQUIRE(a.q_dtype == QA_F32 || a.q_dtype == QA_BF16, "query must be float32 or bfloat16 (got %s)", dtype_name(a.q_dtype));
+  QA_REQUIRE(kv.dtype == QA_F32 || kv.dtype == QA_BF16, "key/value blocks must be float32 or bfloat16 (got %s)", dtype_name(kv.dtype));
+  QA_REQUIRE(is_index_dtype(a.table_dtype), "block table must be int32 or int64");
+  QA_REQUIRE(a.lens == nullptr || is_index_dtype(a.lens_dtype), "sequence lengths must be int32 or int64");
+  QA_REQUIRE(a.batch > 0 && a.batch <= 0x7fffffff, "batch must be positive and fit int32");
+  QA_REQUIRE(a.heads > 0 && kv.kv_heads > 0, "heads must be positive");
+  QA_REQUIRE(a.heads % kv.kv_heads == 0, "query heads (%d) must be a multiple of KV heads (%d)", a.heads, kv.kv_heads);
+  QA_REQUIRE(a.head_dim > 0 && a.head_dim <= 1024, "head_dim must be in [1, 1024]");
+  QA_REQUIRE(a.block_size > 0, "block_size must be positive");
+  QA_REQUIRE(a.max_blocks > 0, "block table must have at least one entry");
+  QA_REQUIRE(kv.row_key_ptrs != nullptr || (kv.key != nullptr && kv.value != nullptr), "key/value pools must be non-null");
+  QA_REQUIRE((kv.row_key_ptrs == nullptr) == (kv.row_value_ptrs == nullptr), "row key/value pointer arrays must both be given");
+  QA_REQUIRE(kv.stride_head != 0 || (kv.row_key_ptrs != nullptr && kv.row_blocks != nullptr) || kv.kv_heads == 1,
+             "stride_head == 0 needs per-row pools with row_blocks");
+  QA_REQUIRE(kv.stride_token >= a.head_dim || kv.stride_token == 0, "KV token stride smaller than head_dim");
+  QA_REQUIRE(a.max_tokens <= a.max_blocks * a.block_size, "block_table does not cover sequence_length");
+  const int64_t G = a.heads / kv.kv_heads;
+  QA_REQUIRE(G <= 16, "GQA group size %lld is larger than 16", static_cast<long long>(G));
+
+  DecodeParams p{};
+  p.q = a.query;
+  p.q_sb = a.q_sb;
+  p.q_sh = a.q_sh;
+  p.out = a.output;
+  p.kbase = kv.key;
+  p.vbase = kv.value;
+  p.row_k = kv.row_key_ptrs;
+  p.row_v = kv.row_value_ptrs;
+  p.row_blocks = kv.row_blocks;
+  p.num_blocks = kv.num_blocks;
+  p.sB = kv.stride_batch;
+  p.sP = kv.stride_block;
+  p.sG = kv.stride_head;
+  p.sT = kv.stride_token;
+  p.tables = a.tables;
+  p.table_stride = a.table_stride;
+  p.max_blocks = a.max_blocks;
+  p.lens = a.lens;
+  p.len_scalar = a.len_scalar;
+  p.B = static_cast<int>(a.batch);
+  p.H = a.heads;
+  p.Hkv = kv.kv_heads;
+  p.D = a.head_dim;
+  p.bs = a.block_size;
+  p.G = static_cast<int>(G);
+  p.table_i64 = a.table_dtype == QA_I64;
+  p.lens_i64 = a.lens_dtype == QA_I64;
+  p.scale = a.scale > 0.f ? a.scale : 1.0f / sqrtf(static_cast<float>(a.head_dim));
+  p.split_tokens = choose_split_tokens(a.max_tokens, a.block_size);
+  p.n_splits = static_cast<int>(std::max<int64_t>(1, ceil_div(std::max<int64_t>(a.max_tokens, 1), p.split_tokens)));
+  const int64_t need = decode_workspace_bytes(a.batch, a.heads, a.head_dim, a.max_tokens, a.block_size);
+  QA_REQUIRE(a.workspace != nullptr && a.workspace_bytes >= need, "paged decode workspace too small: need %lld bytes", static_cast<long long>(need));
+  p.part_o = reinterpret_cast<float*>(a.workspace);
+  p.part_ml = p.part_o + static_cast<int64_t>(p.B) * p.H * p.n_splits * p.D;
+
+  if (a.q_dtype == QA_F32 && kv.dtype == QA_F32) return dispatch_generic<float, float>(p, stream);
+  if (a.q_dtype == QA_BF16 && kv.dtype == QA_BF16) return dispatch_generic<bf16_t, bf16_t>(p, stream);
+  if (a.q_dtype == QA_F32 && kv.dtype == QA_BF16) return dispatch_generic<float, bf16_t>(p, stream);
+  return dispatch_generic<bf16_t, float>(p, stream);
+}
+
+}  // namespace qa
+
+extern "C" int64_t qa_paged_attention_decode_workspace(int64_t batch, int32_t heads, int32_t head_dim, int64_t max_tokens,
+                                                       int32_t block_size) {
+  if (batch <= 0 || heads <= 0 || head_dim <= 0 || block_size <= 0) return 0;
+  return qa::decode_workspace_bytes(batch, heads, head_dim, max_tokens, block_size);
+}
+
+extern "C" int qa_paged_attention_decode(const void* query, int32_t q_dtype, int64_t q_stride_b, int64_t q_stride_h, int64_t batch,
+                                         int32_t heads, int32_t head_dim, const qa_paged_kv* kv, const void* block_table,
+                                         int32_t table_dtype, int64_t table_len, int64_t sequence_length, int32_t block_size,
+                                         float scale, void* output, void* workspace, int64_t workspace_bytes, hipStream_t stream) {
+  QA_REQUIRE(sequence_length > 0, "sequence_length must be positive");
+  qa::DecodeHostArgs a{};
+  a.query = query;
+  a.q_dtype = q_dtype;
+  a.q_sb = q_stride_b;
+  a.q_sh = q_stride_h;
+  a.batch = batch;
+  a.heads = heads;
+  a.head_dim = head_dim;
+  a.kv = kv;
+  a.tables = block_table;
+  a.table_dtype = table_dtype;
+  a.table_stride = 0;
+  a.max_blocks = table_len;
+  a.lens = nullptr;
+  a.lens_dtype = QA_I64;
+  a.len_scalar = sequence_length;
+  a.max_tokens = sequence_length;
+  a.block_size = block_size;
+  a.scale = scale;
+  a.output = output;
+  a.workspace = workspace;
+  a.workspace_bytes = workspace_bytes;
+  return qa::run_decode(a, stream);
+}
+
+extern "C" int qa_paged_attention_decode_batched(const void* query, int32_t q_dtype, int64_t q_stride_b, int64_t q_stride_h,
+                                                 int64_t batch, int32_t heads, int32_t head_dim, const qa_paged_kv* kv,
+                                                 const void* block_tables, int32_t table_dtype, int64_t table_stride,
+                                                 int64_t max_blocks, const void* sequence_lengths, int32_t lengths_dtype,
+                                                 int32_t block_size, float scale, void* output, void* workspace,
+                                                 int64_t workspace_bytes, hipStream_t stream) {
+  QA_REQUIRE(sequence_lengths != nullptr, "sequence_lengths must be a device array");
+  qa::DecodeHostArgs a{};
+  a.query = query;
+  a.q_dtype = q_dtype;
+  a.q_sb = q_stride_b;
+  a.q_sh = q_stride_h;
+  a.batch = batch;
+  a.heads = heads;
+  a.head_dim = head_dim;
+  a.kv = kv;
+  a.tables = block_tables;
+  a.table_dtype = table_dtype;
+  a.table_stride = table_stride;
+  a.max_blocks = max_blocks;
+  a.lens = sequence_lengths;
+  a.lens_dtype = lengths_dtype;
+  a.len_scalar = 0;
+  a.max_tokens = max_blocks * static_cast<int64_t>(block_size);
+  a.block_size = block_size;
+  a.scale = scale;
+  a.output = output;
+  a.workspace = workspace;
+  a.workspace_bytes = workspace_bytes;
+  return qa::run_decode(a, stream);
+}

@@ -1,0 +1,87 @@
+// Shared device/host helpers of the gfx950 hot-path library.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include <cstdarg>
+#include <cstdio>
+#include <string>
+
+#include "../../include/qwen36_hip.h"
+
+namespace qa {
+
+// ---- error reporting (host) ------------------------------------------------
+void set_error(const char* fmt, ...) __attribute__((format(printf, 1, 2)));
+int fail(const char* fmt, ...) __attribute__((format(printf, 1, 2)));
+int check_launch(const char* what);
+
+#define QA_REQUIRE(cond, ...)          \
+  do {                                 \
+    if (!(cond)) return qa::fail(__VA_ARGS__); \
+  } while (0)
+
+// ---- numeric helpers (device) ----------------------------------------------
+typedef unsigned short bf16_t;  // raw bfloat16 bits
+
+__device__ __forceinline__ float bf16_to_f32(bf16_t x) {
+  return __uint_as_float(static_cast<uint32_t>(x) << 16);
+}
+
+// Round-to-nearest-even float -> bfloat16 (NaN kept quiet).
+__device__ __forceinline__ bf16_t f32_to_bf16(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return static_cast<bf16_t>((u >> 16) | 0x40);
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return static_cast<bf16_t>(u >> 16);
+}
+
+template <typename T>
+struct Elem;
+
+template <>
+struct Elem<float> {
+  __device__ __forceinline__ static float load(const float* p) { return *p; }
+  __device__ __forceinline__ static void store(float* p, float v) { *p = v; }
+};
+
+template <>
+struct Elem<bf16_t> {
+  __device__ __forceinline__ static float load(const bf16_t* p) { return bf16_to_f32(*p); }
+  __device__ __forceinline__ static void store(bf16_t* p, float v) { *p = f32_to_bf16(v); }
+};
+
+template <typename IT>
+__device__ __forceinline__ int64_t load_index(const IT* p) {
+  return static_cast<int64_t>(*p);
+}
+
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
+  return v;
+}
+
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, 64));
+  return v;
+}
+
+inline int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
+
+inline bool is_float_dtype(int32_t d) { return d == QA_F32 || d == QA_BF16; }
+inline bool is_index_dtype(int32_t d) { return d == QA_I32 || d == QA_I64; }
+inline const char* dtype_name(int32_t d) {
+  switch (d) {
+    case QA_F32: return "float32";
+    case QA_BF16: return "bfloat16";
+    case QA_F16: return "float16";
+    case QA_I32: return "int32";
+    case QA_I64: return "int64";
+    default: return "unknown";
+  }
+}
+
+}  // namespace qa

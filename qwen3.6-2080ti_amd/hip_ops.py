@@ -1,0 +1,364 @@
+"""Python operator surface of the gfx950 hot path.
+
+The names, arguments, return shapes and ``RuntimeError`` behaviour of the three
+hot wrappers of the reference's ``src/fp8_cuda.py`` are kept:
+
+* :func:`paged_attention_decode` -- ``src/fp8_cuda.py:217-232``
+* :func:`paged_attention_decode_batched` -- ``src/fp8_cuda.py:235-250``
+* :func:`linear_attention_recurrent_core` -- ``src/fp8_cuda.py:206-214``
+
+so a caller such as ``src/tp_runtime.py:613-643`` / ``:2778-2787`` only changes
+its import.  Beyond the reference they also accept bfloat16 tensors, a shared
+GQA-native block pool ``(P, H_kv, bs, D)`` and int32 tables.  New operators of
+the path sit beside them (KV append/gather, prefill, conv1d, chunked delta
+rule, fused decode step).
+
+Every operator validates on the host and raises ``RuntimeError`` with the
+library's message on failure.  Outputs and workspaces are allocated here with
+torch (its caching allocator owns them); kernels run on torch's current stream.
+"""
+
+from __future__ import annotations
+
+import ctypes
+from typing import Any, Sequence
+
+import torch
+
+import hip_loader as L
+
+_DTYPE_CODES = {
+    torch.float32: L.QA_F32,
+    torch.bfloat16: L.QA_BF16,
+    torch.float16: L.QA_F16,
+    torch.int32: L.QA_I32,
+    torch.int64: L.QA_I64,
+}
+
+
+def _code(tensor: torch.Tensor) -> int:
+    try:
+        return _DTYPE_CODES[tensor.dtype]
+    except KeyError as exc:
+        raise RuntimeError(f"unsupported dtype {tensor.dtype}") from exc
+
+
+def _stream(device: torch.device) -> ctypes.c_void_p:
+    return ctypes.c_void_p(torch.cuda.current_stream(device).cuda_stream)
+
+
+def _ptr(tensor: torch.Tensor | None) -> ctypes.c_void_p:
+    return ctypes.c_void_p(0 if tensor is None else tensor.data_ptr())
+
+
+def _require(cond: bool, message: str) -> None:
+    if not cond:
+        raise RuntimeError(message)
+
+
+def _require_cuda(tensor: Any, name: str, device: torch.device | None = None) -> None:
+    _require(isinstance(tensor, torch.Tensor) and tensor.is_cuda, f"{name} must be CUDA")
+    if device is not None:
+        _require(tensor.device == device, f"{name} must be on same CUDA device as query")
+
+
+def _float_dtype(tensor: torch.Tensor, name: str) -> None:
+    _require(tensor.dtype in (torch.float32, torch.bfloat16), f"{name} must be float32 or bfloat16")
+
+
+def _index_dtype(tensor: torch.Tensor, name: str) -> None:
+    _require(tensor.dtype in (torch.int32, torch.int64), f"{name} must be int64/torch.long or int32")
+
+
+def _pool_descriptor(key_pool: torch.Tensor, value_pool: torch.Tensor, layout: str) -> L.PagedKV:
+    """Descriptor for a reference-layout ``(B, heads, P, bs, D)`` pool or a shared ``(P, H_kv, bs, D)`` pool."""
+    _require(key_pool.shape == value_pool.shape, "key/value physical block count must match")
+    _require(key_pool.dtype == value_pool.dtype, "key/value blocks must have the same dtype")
+    _require(key_pool.stride(-1) == 1 and value_pool.stride(-1) == 1, "key/value blocks must be contiguous in head_dim")
+    _require(key_pool.stride() == value_pool.stride(), "key/value blocks must share strides")
+    desc = L.PagedKV()
+    desc.key = key_pool.data_ptr()
+    desc.value = value_pool.data_ptr()
+    desc.row_key_ptrs = None
+    desc.row_value_ptrs = None
+    desc.row_blocks = None
+    desc.dtype = _code(key_pool)
+    if layout == "reference":  # (B, heads, P, bs, D)
+        desc.num_blocks = key_pool.shape[2]
+        desc.stride_batch = key_pool.stride(0)
+        desc.stride_head = key_pool.stride(1)
+        desc.stride_block = key_pool.stride(2)
+        desc.stride_token = key_pool.stride(3)
+        desc.kv_heads = key_pool.shape[1]
+    else:  # shared (P, H_kv, bs, D)
+        desc.num_blocks = key_pool.shape[0]
+        desc.stride_batch = 0
+        desc.stride_block = key_pool.stride(0)
+        desc.stride_head = key_pool.stride(1)
+        desc.stride_token = key_pool.stride(2)
+        desc.kv_heads = key_pool.shape[1]
+    return desc
+
+
+def _decode_workspace(lib: Any, batch: int, heads: int, head_dim: int, max_tokens: int, block_size: int, device: torch.device) -> torch.Tensor:
+    nbytes = int(lib.qa_paged_attention_decode_workspace(batch, heads, head_dim, max_tokens, block_size))
+    return torch.empty(max(nbytes, 4), dtype=torch.uint8, device=device)
+
+
+def paged_attention_decode(
+    query: torch.Tensor,
+    block_table: torch.Tensor,
+    key_blocks: torch.Tensor,
+    value_blocks: torch.Tensor,
+    sequence_length: int,
+    block_size: int,
+    *,
+    scale: float | None = None,
+) -> torch.Tensor:
+    """Single-token paged attention over one block table.
+
+    ``query`` ``(B, H, 1, D)``; ``block_table`` ``(L,)``; ``key_blocks`` either
+    the reference's per-request pool ``(B, heads, P, bs, D)`` with ``heads`` = H
+    or H_kv (GQA), or a shared pool ``(P, H_kv, bs, D)``.  Returns
+    ``(B, H, 1, D)`` in the query dtype.  Reference:
+    ``src/fp8_cuda.py:217-232`` -> ``src/csrc/fp8_linear_cuda.cu:1192-1266``.
+    """
+    lib = L.load_library()
+    _require_cuda(query, "query")
+    device = query.device
+    _require_cuda(block_table, "block_table", device)
+    _require_cuda(key_blocks, "key_blocks", device)
+    _require_cuda(value_blocks, "value_blocks", device)
+    _float_dtype(query, "query")
+    _float_dtype(key_blocks, "key_blocks")
+    _index_dtype(block_table, "block_table")
+    _require(query.dim() == 4, "query must have shape [batch, heads, 1, head_dim]")
+    _require(query.shape[2] == 1, "query seq_len must be 1 for paged decode")
+    _require(block_table.dim() == 1, "block_table must be rank-1")
+    _require(key_blocks.dim() in (4, 5), "key_blocks must have shape [batch, heads, blocks, block_size, head_dim] or [blocks, kv_heads, block_size, head_dim]")
+    _require(value_blocks.dim() == key_blocks.dim(), "value_blocks must match key_blocks rank")
+    _require(int(sequence_length) > 0, "sequence_length must be positive")
+    _require(int(block_size) > 0, "block_size must be positive")
+    batch, heads, _, head_dim = query.shape
+    layout = "reference" if key_blocks.dim() == 5 else "shared"
+    if layout == "reference":
+        _require(key_blocks.shape[0] == batch and value_blocks.shape[0] == batch, "KV batch must match query")
+    _require(key_blocks.shape[-2] == block_size, "KV block_size mismatch")
+    _require(key_blocks.shape[-1] == head_dim, "KV head_dim must match query")
+    table = block_table.contiguous()
+    _require(table.numel() * int(block_size) >= int(sequence_length), "block_table does not cover sequence_length")
+    q = query.contiguous()
+    desc = _pool_descriptor(key_blocks, value_blocks, layout)
+    _require(heads % desc.kv_heads == 0, "KV heads must divide query heads")
+    out = torch.empty_like(q)
+    ws = _decode_workspace(lib, batch, heads, head_dim, int(sequence_length), int(block_size), device)
+    status = lib.qa_paged_attention_decode(
+        _ptr(q), _code(q), q.stride(0), q.stride(1), batch, heads, head_dim, ctypes.byref(desc), _ptr(table), _code(table),
+        table.numel(), int(sequence_length), int(block_size), float(scale or 0.0), _ptr(out), _ptr(ws), ws.numel(), _stream(device),
+    )
+    L.check(lib, status, "paged_attention_decode")
+    return out
+
+
+def paged_attention_decode_batched(
+    query: torch.Tensor,
+    block_tables: torch.Tensor,
+    key_blocks: Sequence[torch.Tensor] | torch.Tensor,
+    value_blocks: Sequence[torch.Tensor] | torch.Tensor,
+    sequence_lengths: torch.Tensor,
+    block_size: int,
+    *,
+    scale: float | None = None,
+) -> torch.Tensor:
+    """Batched single-token paged attention with per-row tables and lengths.
+
+    ``block_tables`` ``(B, max_blocks)`` padded with -1, ``sequence_lengths``
+    ``(B,)``.  ``key_blocks``/``value_blocks`` are either one shared
+    ``(P, H_kv, bs, D)`` pool, or (as the reference) a list of per-request
+    pools ``(1, heads, P_b, bs, D)``; a list whose entries are all the same
+    tensor is treated as one shared pool.  Rows of length <= 0 give zeros.
+    Reference: ``src/fp8_cuda.py:235-250`` -> ``src/csrc/fp8_linear_cuda.cu:1269-1365``.
+    """
+    lib = L.load_library()
+    _require_cuda(query, "query")
+    device = query.device
+    _require_cuda(block_tables, "block_tables", device)
+    _require_cuda(sequence_lengths, "sequence_lengths", device)
+    _float_dtype(query, "query")
+    _index_dtype(block_tables, "block_tables")
+    _index_dtype(sequence_lengths, "sequence_lengths")
+    _require(query.dim() == 4, "query must have shape [batch, heads, 1, head_dim]")
+    _require(block_tables.dim() == 2, "block_tables must have shape [batch, max_blocks]")
+    _require(sequence_lengths.dim() == 1, "sequence_lengths must be rank-1")
+    _require(query.shape[2] == 1, "query seq_len must be 1 for paged decode")
+    _require(int(block_size) > 0, "block_size must be positive")
+    batch, heads, _, head_dim = query.shape
+    _require(block_tables.shape[0] == batch, "block_tables batch must match query")
+    _require(sequence_lengths.shape[0] == batch, "sequence_lengths batch must match query")
+    _require(block_tables.shape[1] > 0, "max_blocks must be positive and fit int32")
+    keepalive: list[torch.Tensor] = []
+    if isinstance(key_blocks, torch.Tensor):
+        _require(isinstance(value_blocks, torch.Tensor), "value_blocks must match key_blocks")
+        _require(key_blocks.dim() == 4, "shared pools must have shape [blocks, kv_heads, block_size, head_dim]")
+        _require_cuda(key_blocks, "key_blocks", device)
+        _require_cuda(value_blocks, "value_blocks", device)
+        _float_dtype(key_blocks, "key_blocks")
+        desc = _pool_descriptor(key_blocks, value_blocks, "shared")
+        pool_block_size = key_blocks.shape[2]
+    else:
+        key_list = list(key_blocks)
+        value_list = list(value_blocks)
+        _require(len(key_list) == batch, "key_blocks list length must match batch")
+        _require(len(value_list) == batch, "value_blocks list length must match batch")
+        first_k, first_v = key_list[0], value_list[0]
+        for k, v in zip(key_list, value_list):
+            _require(isinstance(k, torch.Tensor) and isinstance(v, torch.Tensor), "key/value blocks must be CUDA")
+            _require(k.is_cuda and v.is_cuda, "key/value blocks must be CUDA")
+            _require(k.device == device and v.device == device, "key/value blocks must be on same CUDA device as query")
+            _require(k.dtype == first_k.dtype and v.dtype == first_k.dtype, "key/value blocks must share one dtype")
+            _float_dtype(k, "key/value blocks")
+            _require(k.dim() == first_k.dim() and v.dim() == first_k.dim(), "key/value blocks must share one rank")
+            _require(k.shape == v.shape, "key/value physical block count must match")
+        shared = all(k is first_k for k in key_list) and all(v is first_v for v in value_list)
+        if shared and first_k.dim() == 4:
+            desc = _pool_descriptor(first_k, first_v, "shared")
+            pool_block_size = first_k.shape[2]
+        else:
+            for k in key_list:
+                _require(k.dim() == 5, "key/value blocks must have shape [1, heads, blocks, block_size, head_dim]")
+                _require(k.shape[0] == 1, "per-request KV pools must have batch dim 1")
+                _require(k.shape[1] == first_k.shape[1], "KV heads must match across pools")
+                _require(k.shape[3:] == first_k.shape[3:], "KV block_size/head_dim must match across pools")
+                _require(k.stride(-1) == 1 and k.is_contiguous(), "key/value blocks must be contiguous")
+            for v in value_list:
+                _require(v.is_contiguous(), "key/value blocks must be contiguous")
+            desc = _per_request_descriptor(key_list, value_list, device, keepalive)
+            pool_block_size = first_k.shape[3]
+    _require(pool_block_size == block_size, "KV block_size mismatch")
+    _require(heads % desc.kv_heads == 0, "KV heads must divide query heads")
+    q = query.contiguous()
+    tables = block_tables.contiguous()
+    lens = sequence_lengths.contiguous()
+    max_blocks = tables.shape[1]
+    out = torch.empty_like(q)
+    ws = _decode_workspace(lib, batch, heads, head_dim, max_blocks * int(block_size), int(block_size), device)
+    status = lib.qa_paged_attention_decode_batched(
+        _ptr(q), _code(q), q.stride(0), q.stride(1), batch, heads, head_dim, ctypes.byref(desc), _ptr(tables), _code(tables),
+        tables.stride(0), max_blocks, _ptr(lens), _code(lens), int(block_size), float(scale or 0.0), _ptr(out), _ptr(ws), ws.numel(),
+        _stream(device),
+    )
+    L.check(lib, status, "paged_attention_decode_batched")
+    return out
+
+
+def _per_request_descriptor(key_list: list[torch.Tensor], value_list: list[torch.Tensor], device: torch.device, keepalive: list[torch.Tensor]) -> L.PagedKV:
+    """Pointer-array descriptor for contiguous per-request pools ``(1, heads, P_b, bs, D)``.
+
+    As the reference host wrapper (``src/csrc/fp8_linear_cuda.cu:1308-1340``),
+    row pointers and block counts are copied to the device for each call.
+    ``stride_head = 0`` tells the kernels that row ``b``'s head stride is
+    ``P_b * stride_block`` (pools of different ``P_b``).
+    """
+    first = key_list[0]
+    key_ptrs = torch.tensor([k.data_ptr() for k in key_list], dtype=torch.int64, device=device)
+    value_ptrs = torch.tensor([v.data_ptr() for v in value_list], dtype=torch.int64, device=device)
+    counts = torch.tensor([k.shape[2] for k in key_list], dtype=torch.int64, device=device)
+    keepalive.extend([key_ptrs, value_ptrs, counts])
+    desc = L.PagedKV()
+    desc.key = None
+    desc.value = None
+    desc.row_key_ptrs = key_ptrs.data_ptr()
+    desc.row_value_ptrs = value_ptrs.data_ptr()
+    desc.row_blocks = counts.data_ptr()
+    desc.num_blocks = max(k.shape[2] for k in key_list)
+    desc.stride_batch = 0
+    desc.stride_head = 0
+    desc.stride_block = first.stride(2)
+    desc.stride_token = first.stride(3)
+    desc.kv_heads = first.shape[1]
+    desc.dtype = _code(first)
+    return desc
+
+
+def paged_kv_append(
+    key: torch.Tensor,
+    value: torch.Tensor,
+    key_pool: torch.Tensor,
+    value_pool: torch.Tensor,
+    block_tables: torch.Tensor,
+    starts: torch.Tensor | int,
+    block_size: int,
+    *,
+    counts: torch.Tensor | None = None,
+) -> None:
+    """Write new K/V ``(B, H_kv, S, D)`` into pool slots in place (bit-exact).
+
+    Row ``b`` token ``s`` goes to slot ``(table[b][(start_b+s)//bs], (start_b+s)%bs)``
+    of the shared pool ``(P, H_kv, bs, D)`` or of the reference-layout pool
+    ``(B, heads, P, bs, D)``.  ``block_tables`` is ``(B, max_blocks)`` or a single
+    ``(max_blocks,)`` table shared by all rows.  Replaces the fragment loop of
+    ``FullAttentionCache.append_blocks`` (``src/decode_state.py:271-293``).
+    """
+    lib = L.load_library()
+    _require_cuda(key, "key")
+    device = key.device
+    for tensor, name in ((value, "value"), (key_pool, "key_pool"), (value_pool, "value_pool"), (block_tables, "block_tables")):
+        _require_cuda(tensor, name, device)
+    _require(key.shape == value.shape and key.dim() == 4, "key/value must have shape [batch, kv_heads, seq, head_dim]")
+    _require(key.dtype == key_pool.dtype and value.dtype == key_pool.dtype, "new KV dtype must match the pool dtype")
+    _require(key.stride() == value.stride() and key.stride(-1) == 1, "key/value must share strides with a contiguous head_dim")
+    _index_dtype(block_tables, "block_tables")
+    layout = "reference" if key_pool.dim() == 5 else "shared"
+    desc = _pool_descriptor(key_pool, value_pool, layout)
+    batch, kv_heads, seq, head_dim = key.shape
+    _require(kv_heads == desc.kv_heads, "new KV heads must match the pool")
+    _require(key_pool.shape[-1] == head_dim and key_pool.shape[-2] == block_size, "pool block_size/head_dim mismatch")
+    tables = block_tables.contiguous()
+    table_stride = tables.stride(0) if tables.dim() == 2 else 0
+    max_blocks = tables.shape[-1]
+    start_ptr, start_code, start_scalar = ctypes.c_void_p(0), L.QA_I64, 0
+    if isinstance(starts, torch.Tensor):
+        _require_cuda(starts, "starts", device)
+        _index_dtype(starts, "starts")
+        starts = starts.contiguous()
+        start_ptr, start_code = _ptr(starts), _code(starts)
+    else:
+        start_scalar = int(starts)
+    count_ptr, count_code = ctypes.c_void_p(0), L.QA_I64
+    if counts is not None:
+        _require_cuda(counts, "counts", device)
+        _index_dtype(counts, "counts")
+        counts = counts.contiguous()
+        count_ptr, count_code = _ptr(counts), _code(counts)
+    status = lib.qa_paged_kv_append(
+        _ptr(key), _ptr(value), _code(key), key.stride(0), key.stride(1), key.stride(2), batch, kv_heads, seq, head_dim,
+        ctypes.byref(desc), _ptr(tables), _code(tables), table_stride, max_blocks, start_ptr, start_code, start_scalar,
+        count_ptr, count_code, int(block_size), _stream(device),
+    )
+    L.check(lib, status, "paged_kv_append")
+
+
+def paged_kv_gather(key_pool: torch.Tensor, value_pool: torch.Tensor, block_tables: torch.Tensor, valid: int, block_size: int) -> tuple[torch.Tensor, torch.Tensor]:
+    """Dense ``(B, H_kv, valid, D)`` logical-order K/V (``src/decode_state.py:295-303,395-404``)."""
+    lib = L.load_library()
+    _require_cuda(key_pool, "key_pool")
+    device = key_pool.device
+    _require_cuda(value_pool, "value_pool", device)
+    _require_cuda(block_tables, "block_tables", device)
+    _index_dtype(block_tables, "block_tables")
+    layout = "reference" if key_pool.dim() == 5 else "shared"
+    desc = _pool_descriptor(key_pool, value_pool, layout)
+    tables = block_tables.contiguous()
+    if tables.dim() == 1:
+        tables = tables.unsqueeze(0)
+    batch = tables.shape[0] if layout == "shared" else key_pool.shape[0]
+    table_stride = tables.stride(0) if tables.shape[0] > 1 else 0
+    head_dim = key_pool.shape[-1]
+    key_out = torch.empty((batch, desc.kv_heads, int(valid), head_dim), dtype=key_pool.dtype, device=device)
+    value_out = torch.empty_like(key_out)
+    status = lib.qa_paged_kv_gather(
+        ctypes.byref(desc), head_dim, batch, _ptr(tables), _code(tables), table_stride, tables.shape[1], int(valid), int(block_size),
+        _ptr(key_out), _ptr(value_out), _stream(device),
+    )
+    L.check(lib, status, "paged_kv_gather")
+    return key_out, value_out

@@ -1,0 +1,225 @@
+"""GPU parity of paged GQA decode against the CPU oracle.
+
+The first group restates the reference's own native-kernel tests
+(``tests/unit/test_fp8_cuda.py:37-200``; same seeds, shapes and tolerances,
+fp32).  The second group covers the bf16 GQA-native product path on the
+shared pool: BASELINE config 1 (B=4, 16 q heads, 2 KV heads, D=256, ctx 512,
+bs 16, table = seeded permutation of 128 blocks, seed 0) and edge cases.
+Tolerance for bf16 outputs: ``atol = rtol = 2e-2``.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import attention as oracle_attn
+
+pytestmark = pytest.mark.gpu
+
+DEV = "cuda:0"
+
+
+def _ops():
+    import hip_ops
+
+    return hip_ops
+
+
+def _dense_ref(query: torch.Tensor, dense_key: torch.Tensor, dense_value: torch.Tensor) -> torch.Tensor:
+    # tests/unit/test_fp8_cuda.py:1042-1045 (fp32 probabilities, no cast)
+    return oracle_attn.dense_attention(query.cpu(), dense_key.cpu(), dense_value.cpu(), position_offset=dense_key.shape[2] - 1, cast_probs=False)
+
+
+def _pack(dense_key, dense_value, block_table, block_size, *, physical_blocks=None, fill=0.0):
+    # tests/unit/test_fp8_cuda.py:1048-1071 (reference pool layout (B, heads, P, bs, D))
+    batch, heads, seq_len, head_dim = dense_key.shape
+    if physical_blocks is None:
+        physical_blocks = int(block_table.max().item()) + 1
+    key_blocks = torch.full((batch, heads, physical_blocks, block_size, head_dim), fill, device=dense_key.device, dtype=dense_key.dtype)
+    value_blocks = torch.full_like(key_blocks, fill)
+    for token in range(seq_len):
+        physical = int(block_table[token // block_size].item())
+        key_blocks[:, :, physical, token % block_size] = dense_key[:, :, token]
+        value_blocks[:, :, physical, token % block_size] = dense_value[:, :, token]
+    return key_blocks, value_blocks
+
+
+def test_decode_matches_dense_contiguous_blocks() -> None:
+    ops = _ops()
+    torch.manual_seed(101)
+    batch, heads, seq_len, head_dim, block_size = 1, 3, 5, 8, 2
+    query = torch.randn((batch, heads, 1, head_dim), device=DEV)
+    dense_key = torch.randn((batch, heads, seq_len, head_dim), device=DEV)
+    dense_value = torch.randn((batch, heads, seq_len, head_dim), device=DEV)
+    table = torch.arange(3, device=DEV, dtype=torch.long)
+    kb, vb = _pack(dense_key, dense_value, table, block_size)
+    out = ops.paged_attention_decode(query, table, kb, vb, seq_len, block_size)
+    torch.testing.assert_close(out.cpu(), _dense_ref(query, dense_key, dense_value), atol=2e-5, rtol=2e-5)
+
+
+def test_decode_non_contiguous_blocks_ignore_padding() -> None:
+    ops = _ops()
+    torch.manual_seed(102)
+    batch, heads, seq_len, head_dim, block_size = 1, 2, 5, 8, 2
+    query = torch.randn((batch, heads, 1, head_dim), device=DEV)
+    dense_key = torch.randn((batch, heads, seq_len, head_dim), device=DEV)
+    dense_value = torch.randn((batch, heads, seq_len, head_dim), device=DEV)
+    table = torch.tensor([2, 0, 3], device=DEV, dtype=torch.long)
+    kb, vb = _pack(dense_key, dense_value, table, block_size, physical_blocks=4, fill=1000.0)
+    out = ops.paged_attention_decode(query, table, kb, vb, seq_len, block_size)
+    torch.testing.assert_close(out.cpu(), _dense_ref(query, dense_key, dense_value), atol=2e-5, rtol=2e-5)
+
+
+def test_decode_rejects_float16_query() -> None:
+    ops = _ops()
+    query = torch.zeros((1, 1, 1, 8), device=DEV, dtype=torch.float16)
+    table = torch.tensor([0], device=DEV, dtype=torch.long)
+    kb = torch.zeros((1, 1, 1, 2, 8), device=DEV)
+    with pytest.raises(RuntimeError, match="query must be float32"):
+        ops.paged_attention_decode(query, table, kb, kb.clone(), 1, 2)
+
+
+def test_batched_matches_dense_per_request_pools() -> None:
+    ops = _ops()
+    torch.manual_seed(103)
+    heads, head_dim, block_size = 3, 8, 2
+    seq_lens = (3, 5, 8)
+    rows = [torch.tensor(t, device=DEV) for t in ([1, 0], [2, 0, 1], [0, 3, 1, 2])]
+    block_tables = torch.full((3, 4), -1, device=DEV, dtype=torch.long)
+    query = torch.randn((3, heads, 1, head_dim), device=DEV)
+    kbs, vbs, refs = [], [], []
+    for row, seq_len in enumerate(seq_lens):
+        dk = torch.randn((1, heads, seq_len, head_dim), device=DEV)
+        dv = torch.randn((1, heads, seq_len, head_dim), device=DEV)
+        block_tables[row, : rows[row].numel()] = rows[row]
+        k, v = _pack(dk, dv, rows[row], block_size, physical_blocks=int(rows[row].max()) + 1 + row, fill=1000.0)
+        kbs.append(k)
+        vbs.append(v)
+        refs.append(_dense_ref(query[row : row + 1], dk, dv))
+    lens = torch.tensor(seq_lens, device=DEV, dtype=torch.long)
+    out = ops.paged_attention_decode_batched(query, block_tables, kbs, vbs, lens, block_size)
+    torch.testing.assert_close(out.cpu(), torch.cat(refs), atol=2e-5, rtol=2e-5)
+
+
+def test_batched_matches_single_request_kernel() -> None:
+    ops = _ops()
+    torch.manual_seed(104)
+    heads, head_dim, block_size = 2, 16, 4
+    seq_lens = (1, 7)
+    query = torch.randn((2, heads, 1, head_dim), device=DEV)
+    block_tables = torch.full((2, 2), -1, device=DEV, dtype=torch.long)
+    kbs, vbs, singles = [], [], []
+    for row, seq_len in enumerate(seq_lens):
+        logical = (seq_len + block_size - 1) // block_size
+        table = torch.arange(logical, device=DEV, dtype=torch.long)
+        block_tables[row, :logical] = table
+        k = torch.randn((1, heads, logical, block_size, head_dim), device=DEV)
+        v = torch.randn((1, heads, logical, block_size, head_dim), device=DEV)
+        kbs.append(k)
+        vbs.append(v)
+        singles.append(ops.paged_attention_decode(query[row : row + 1], table, k, v, seq_len, block_size))
+    lens = torch.tensor(seq_lens, device=DEV, dtype=torch.long)
+    out = ops.paged_attention_decode_batched(query, block_tables, kbs, vbs, lens, block_size)
+    torch.testing.assert_close(out, torch.cat(singles), atol=2e-5, rtol=2e-5)
+
+
+def test_batched_rejects_mismatched_pool_count() -> None:
+    ops = _ops()
+    query = torch.zeros((2, 1, 1, 8), device=DEV)
+    tables = torch.zeros((2, 1), device=DEV, dtype=torch.long)
+    pools = [torch.zeros((1, 1, 1, 2, 8), device=DEV)]
+    with pytest.raises(RuntimeError, match="key_blocks list length must match batch"):
+        ops.paged_attention_decode_batched(query, tables, pools, pools, torch.ones(2, device=DEV, dtype=torch.long), 2)
+
+
+# ---- bf16 GQA-native shared pool ------------------------------------------------
+
+
+def _config1_inputs():
+    """seed 0, B=4, H=16, H_kv=2, D=256, ctx 512, bs 16, 128 shuffled blocks."""
+    torch.manual_seed(0)
+    batch, heads, kv_heads, dim, ctx, bs = 4, 16, 2, 256, 512, 16
+    blocks = 128
+    perm = torch.randperm(blocks)
+    tables = perm.reshape(batch, ctx // bs)
+    q = torch.randn(batch, heads, 1, dim).to(torch.bfloat16)
+    key_pool = torch.randn(blocks, kv_heads, bs, dim).to(torch.bfloat16)
+    value_pool = torch.randn(blocks, kv_heads, bs, dim).to(torch.bfloat16)
+    return q, key_pool, value_pool, tables, [ctx] * batch, bs
+
+
+def test_config1_bf16_shared_pool_matches_oracle() -> None:
+    ops = _ops()
+    q, kp, vp, tables, lens, bs = _config1_inputs()
+    ref = oracle_attn.paged_decode(q, [kp] * 4, [vp] * 4, tables.tolist(), lens, block_size=bs, pool_layout="phbd")
+    out = ops.paged_attention_decode_batched(
+        q.to(DEV), tables.to(DEV, torch.int32), kp.to(DEV), vp.to(DEV), torch.tensor(lens, device=DEV, dtype=torch.int32), bs
+    )
+    assert out.dtype == torch.bfloat16 and out.shape == q.shape
+    torch.testing.assert_close(out.cpu().float(), ref.float(), atol=2e-2, rtol=2e-2)
+    # fp32-probability restatement (no bf16 cast) is closer still
+    ref32 = oracle_attn.paged_decode(q, [kp] * 4, [vp] * 4, tables.tolist(), lens, block_size=bs, pool_layout="phbd", cast_probs=False)
+    assert (out.cpu().float() - ref32).abs().max().item() < 1e-2
+
+
+@pytest.mark.parametrize("table_dtype", [torch.int32, torch.int64])
+def test_bf16_ragged_lengths_empty_rows_and_invalid_blocks(table_dtype) -> None:
+    ops = _ops()
+    gen = torch.Generator().manual_seed(11)
+    heads, kv_heads, dim, bs, pool_blocks = 16, 2, 256, 16, 40
+    lens = [0, 1, 17, 100, 255]
+    kp = torch.randn(pool_blocks, kv_heads, bs, dim, generator=gen).to(torch.bfloat16)
+    vp = torch.randn(pool_blocks, kv_heads, bs, dim, generator=gen).to(torch.bfloat16)
+    q = torch.randn(len(lens), heads, 1, dim, generator=gen).to(torch.bfloat16)
+    perm = torch.randperm(pool_blocks, generator=gen).tolist()
+    max_blocks = 16
+    tables = torch.full((len(lens), max_blocks), -1, dtype=torch.long)
+    cursor = 0
+    py_tables = []
+    for row, n in enumerate(lens):
+        need = (n + bs - 1) // bs
+        t = perm[cursor : cursor + need]
+        cursor += need
+        tables[row, :need] = torch.tensor(t, dtype=torch.long)
+        py_tables.append(t)
+    ref = oracle_attn.paged_decode(q, [kp] * 5, [vp] * 5, py_tables, lens, block_size=bs, pool_layout="phbd")
+    out = ops.paged_attention_decode_batched(
+        q.to(DEV), tables.to(DEV, table_dtype), kp.to(DEV), vp.to(DEV), torch.tensor(lens, device=DEV), bs
+    )
+    assert torch.count_nonzero(out[0]) == 0
+    torch.testing.assert_close(out.cpu().float(), ref.float(), atol=2e-2, rtol=2e-2)
+
+
+def test_decode_is_invariant_to_physical_block_permutation() -> None:
+    ops = _ops()
+    q, kp, vp, tables, lens, bs = _config1_inputs()
+    out1 = ops.paged_attention_decode_batched(q.to(DEV), tables.to(DEV), kp.to(DEV), vp.to(DEV), torch.tensor(lens, device=DEV), bs)
+    # move every block to a new physical id and rewrite the tables accordingly
+    perm = torch.randperm(kp.shape[0], generator=torch.Generator().manual_seed(3))
+    kp2 = torch.empty_like(kp)
+    vp2 = torch.empty_like(vp)
+    kp2[perm] = kp
+    vp2[perm] = vp
+    tables2 = perm[tables]
+    out2 = ops.paged_attention_decode_batched(q.to(DEV), tables2.to(DEV), kp2.to(DEV), vp2.to(DEV), torch.tensor(lens, device=DEV), bs)
+    torch.testing.assert_close(out1, out2, atol=0, rtol=0)
+
+
+def test_gqa_pool_equals_repeated_reference_layout() -> None:
+    """GQA shared pool == the reference's repeated-head per-request pools (fp32)."""
+    ops = _ops()
+    gen = torch.Generator().manual_seed(12)
+    heads, kv_heads, dim, bs, n = 8, 2, 64, 4, 13
+    kp = torch.randn(6, kv_heads, bs, dim, generator=gen)
+    vp = torch.randn(6, kv_heads, bs, dim, generator=gen)
+    table = [4, 1, 5, 0]
+    q = torch.randn(1, heads, 1, dim, generator=gen)
+    # reference layout: (1, H, P, bs, D) with heads repeated (src/tp_runtime.py:518-525)
+    ref_k = kp.permute(1, 0, 2, 3).repeat_interleave(heads // kv_heads, dim=0).unsqueeze(0).contiguous()
+    ref_v = vp.permute(1, 0, 2, 3).repeat_interleave(heads // kv_heads, dim=0).unsqueeze(0).contiguous()
+    t = torch.tensor(table, device=DEV)
+    out_ref_layout = ops.paged_attention_decode(q.to(DEV), t, ref_k.to(DEV), ref_v.to(DEV), n, bs)
+    out_shared = ops.paged_attention_decode(q.to(DEV), t, kp.to(DEV), vp.to(DEV), n, bs)
+    torch.testing.assert_close(out_ref_layout, out_shared, atol=1e-5, rtol=1e-5)
