@@ -37,6 +37,8 @@ struct DecodeParams {
   float* part_ml;  // (B*H, n_splits, 2)
 };
 
+__device__ __forceinline__ int64_t ceil_div_dev(int64_t a, int64_t b) { return (a + b - 1) / b; }
+
 __device__ __forceinline__ int64_t row_length(const DecodeParams& p, int b) {
   if (p.lens == nullptr) return p.len_scalar;
   return p.lens_i64 ? reinterpret_cast<const int64_t*>(p.lens)[b] : reinterpret_cast<const int32_t*>(p.lens)[b];
@@ -150,6 +152,224 @@ __global__ __launch_bounds__(64) void decode_partial_generic(DecodeParams p) {
   }
 }
 
+// ---------------------------------------------------------------------------
+// MFMA path: bf16 Q and KV, block_size 16, head_dim D in {128, 256}, group <= 16.
+//
+// Work item = (row b, KV head g, split of split_tokens tokens) on a 4-wave
+// workgroup; wave w takes logical blocks lb0 + w, lb0 + w + 4, ...  Per 16-token
+// block and wave:
+//   S[t][h]   = sum_d K[t][d] Q[h][d]      v_mfma_f32_16x16x32_bf16, M = token,
+//                                          N = query head of the group (padded
+//                                          to 16), K = 32 dims per instruction
+//   online softmax per head (column of S) in fp32, p rounded to bf16
+//   O^T[d][h] += sum_t V[t][d] P[t][h]     v_mfma_f32_16x16x16_bf16, M = dim,
+//                                          N = head, K = the block's 16 tokens
+// The S accumulator layout (lane l: tokens 4(l/16)+r, head l%16) is exactly the
+// B-operand layout of the PV product, so P never leaves registers.  V is
+// transposed through a wave-private LDS tile: each lane loads 4 consecutive
+// tokens x 8 dims (coalesced 16-byte row loads), packs them into 4-token
+// columns with v_perm_b32 and stores 8-byte units; the PV A-operand is then one
+// 8-byte LDS read per 16-dim tile.  Units are XOR-swizzled so neither the
+// stores nor the reads conflict on LDS banks.
+typedef __attribute__((__vector_size__(8 * sizeof(__bf16)))) __bf16 bf16x8_v;
+typedef short short4_v __attribute__((ext_vector_type(4)));
+typedef float floatx4_v __attribute__((ext_vector_type(4)));
+
+constexpr int kMfmaWaves = 4;
+constexpr int kVtPad = 16;  // 8-byte units of padding per token quad
+
+__device__ __forceinline__ int vt_swizzle(int d) { return d ^ ((d >> 5) & 7); }
+
+template <int D>
+struct MfmaDecodeSmem {
+  static constexpr int kVtUnits = 4 * (D + kVtPad);                        // per wave
+  static constexpr int kVtBytes = kMfmaWaves * kVtUnits * 8;
+  static constexpr int kMergeBytes = kMfmaWaves * 2048 * 4 + kMfmaWaves * 16 * 2 * 4;  // G * D <= 2048
+  static constexpr int kBytes = kVtBytes > kMergeBytes ? kVtBytes : kMergeBytes;
+};
+
+template <int D>
+__global__ __launch_bounds__(256) void decode_partial_mfma(DecodeParams p) {
+  constexpr int KCH = D / 32;  // QK^T k-chunks
+  constexpr int MT = D / 16;   // PV output tiles (16 dims each)
+  extern __shared__ __align__(16) unsigned char smem[];
+
+  const int split = blockIdx.x;
+  const int bg = blockIdx.y;
+  const int b = bg / p.Hkv;
+  const int g = bg - b * p.Hkv;
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int64_t len = row_length(p, b);
+  const int64_t t0 = static_cast<int64_t>(split) * p.split_tokens;
+  if (t0 >= len) return;  // whole workgroup: nothing of this row in the split
+  const int64_t t1 = min(len, t0 + p.split_tokens);
+  const int64_t lb_begin = t0 / 16;
+  const int64_t lb_end = (t1 + 15) / 16;
+
+  const bf16_t* kb;
+  const bf16_t* vb;
+  int64_t nblk, sG;
+  row_pool(p, b, kb, vb, nblk, sG);
+  kb += static_cast<int64_t>(g) * sG;
+  vb += static_cast<int64_t>(g) * sG;
+
+  // Q^T as the B operand of S = K Q^T: lane l holds head l%16, dims 32i + 8(l/16) + [0, 8).
+  const int head = lane & 15;
+  const int quad = lane >> 4;
+  bf16x8_v qreg[KCH];
+  {
+    const bf16_t* qrow = reinterpret_cast<const bf16_t*>(p.q) + static_cast<int64_t>(b) * p.q_sb +
+                         static_cast<int64_t>(g * p.G + head) * p.q_sh + 8 * quad;
+#pragma unroll
+    for (int i = 0; i < KCH; ++i) {
+      uint4 raw = make_uint4(0, 0, 0, 0);
+      if (head < p.G) raw = *reinterpret_cast<const uint4*>(qrow + 32 * i);
+      qreg[i] = __builtin_bit_cast(bf16x8_v, raw);
+    }
+  }
+
+  floatx4_v o[MT];
+#pragma unroll
+  for (int t = 0; t < MT; ++t) o[t] = floatx4_v{0.f, 0.f, 0.f, 0.f};
+  float m_run = -INFINITY;  // running max of head l%16
+  float l_part = 0.f;       // this lane's share of the softmax denominator
+
+  uint2* vt = reinterpret_cast<uint2*>(smem) + wave * MfmaDecodeSmem<D>::kVtUnits;
+  const int vc = lane & 31;        // 8-dim chunk of V this lane loads
+  const int vq0 = lane >> 5;       // token quads vq0 and vq0 + 2
+  const int ktok = lane & 15;      // K row this lane loads
+  const float scale = p.scale;
+
+  for (int64_t lb = lb_begin + wave; lb < lb_end; lb += kMfmaWaves) {
+    const int64_t phys = table_entry(p, b, lb);
+    const bool ok = phys >= 0 && phys < nblk;
+    uint4 kreg[KCH];
+    uint4 vreg[2][4];
+    if (ok) {
+      const bf16_t* kblk = kb + phys * p.sP;
+      const bf16_t* vblk = vb + phys * p.sP;
+#pragma unroll
+      for (int i = 0; i < KCH; ++i)
+        kreg[i] = *reinterpret_cast<const uint4*>(kblk + ktok * p.sT + 32 * i + 8 * quad);
+#pragma unroll
+      for (int qq = 0; qq < 2; ++qq)
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+          vreg[qq][r] = *reinterpret_cast<const uint4*>(vblk + (4 * (vq0 + 2 * qq) + r) * p.sT + 8 * vc);
+    } else {
+#pragma unroll
+      for (int i = 0; i < KCH; ++i) kreg[i] = make_uint4(0, 0, 0, 0);
+#pragma unroll
+      for (int qq = 0; qq < 2; ++qq)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) vreg[qq][r] = make_uint4(0, 0, 0, 0);
+    }
+
+    // S = K Q^T over the block's 16 tokens.
+    floatx4_v sacc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int i = 0; i < KCH; ++i)
+      sacc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_v, kreg[i]), qreg[i], sacc, 0, 0, 0);
+
+    // Online softmax for head l%16; this lane holds tokens 16*lb + 4*quad + r.
+    float sv[4];
+    float mx = -INFINITY;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int64_t t = lb * 16 + 4 * quad + r;
+      sv[r] = (ok && t < t1) ? sacc[r] * scale : -INFINITY;
+      mx = fmaxf(mx, sv[r]);
+    }
+    mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
+    mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+    const float m_new = fmaxf(m_run, mx);
+    const float m_use = m_new == -INFINITY ? 0.f : m_new;
+    const float alpha = __expf(m_run - m_use);
+    float pr[4];
+    float psum = 0.f;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      pr[r] = __expf(sv[r] - m_use);
+      psum += pr[r];
+    }
+    l_part = l_part * alpha + psum;
+    m_run = m_new;
+#pragma unroll
+    for (int t = 0; t < MT; ++t) o[t] *= alpha;
+    short4_v pb;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) pb[r] = static_cast<short>(f32_to_bf16(pr[r]));
+
+    // V -> LDS as 4-token columns: unit (quad q, dim d) = V[4q..4q+3][d].
+#pragma unroll
+    for (int qq = 0; qq < 2; ++qq) {
+      const int q = vq0 + 2 * qq;
+      const uint32_t* r0 = reinterpret_cast<const uint32_t*>(&vreg[qq][0]);
+      const uint32_t* r1 = reinterpret_cast<const uint32_t*>(&vreg[qq][1]);
+      const uint32_t* r2 = reinterpret_cast<const uint32_t*>(&vreg[qq][2]);
+      const uint32_t* r3 = reinterpret_cast<const uint32_t*>(&vreg[qq][3]);
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        const int d = 8 * vc + 2 * k;
+        uint2 lo, hi;
+        lo.x = __builtin_amdgcn_perm(r1[k], r0[k], 0x05040100u);
+        lo.y = __builtin_amdgcn_perm(r3[k], r2[k], 0x05040100u);
+        hi.x = __builtin_amdgcn_perm(r1[k], r0[k], 0x07060302u);
+        hi.y = __builtin_amdgcn_perm(r3[k], r2[k], 0x07060302u);
+        vt[q * (D + kVtPad) + vt_swizzle(d)] = lo;
+        vt[q * (D + kVtPad) + vt_swizzle(d + 1)] = hi;
+      }
+    }
+    // O^T += V^T P: A operand = 4 tokens of quad l/16 at dim 16t + l%16.
+#pragma unroll
+    for (int t = 0; t < MT; ++t) {
+      const uint2 a = vt[quad * (D + kVtPad) + vt_swizzle(16 * t + head)];
+      o[t] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(__builtin_bit_cast(short4_v, a), pb, o[t], 0, 0, 0);
+    }
+  }
+
+  // Per-wave softmax denominators: lanes {h, h+16, h+32, h+48} hold head h.
+  l_part += __shfl_xor(l_part, 16, 64);
+  l_part += __shfl_xor(l_part, 32, 64);
+
+  __syncthreads();  // LDS now reused for the cross-wave merge
+  float* om = reinterpret_cast<float*>(smem);                  // [wave][G heads][D]
+  float* mlw = om + kMfmaWaves * 2048;                         // [wave][16][2]
+  if (head < p.G) {
+#pragma unroll
+    for (int t = 0; t < MT; ++t)
+      *reinterpret_cast<floatx4_v*>(om + (wave * p.G + head) * D + 16 * t + 4 * quad) = o[t];
+    if (quad == 0) {
+      mlw[(wave * 16 + head) * 2 + 0] = m_run;
+      mlw[(wave * 16 + head) * 2 + 1] = l_part;
+    }
+  }
+  __syncthreads();
+  const int64_t slot0 = static_cast<int64_t>(b) * p.H + g * p.G;
+  for (int idx = threadIdx.x; idx < p.G * D; idx += blockDim.x) {
+    const int h = idx / D;
+    const int d = idx - h * D;
+    float big = -INFINITY;
+#pragma unroll
+    for (int w = 0; w < kMfmaWaves; ++w) big = fmaxf(big, mlw[(w * 16 + h) * 2]);
+    const float use = big == -INFINITY ? 0.f : big;
+    float acc = 0.f, den = 0.f;
+#pragma unroll
+    for (int w = 0; w < kMfmaWaves; ++w) {
+      const float f = __expf(mlw[(w * 16 + h) * 2] - use);
+      acc += f * om[(w * p.G + h) * D + d];
+      den += f * mlw[(w * 16 + h) * 2 + 1];
+    }
+    const int64_t slot = (slot0 + h) * p.n_splits + split;
+    p.part_o[slot * D + d] = acc;
+    if (d == 0) {
+      p.part_ml[slot * 2 + 0] = big;
+      p.part_ml[slot * 2 + 1] = den;
+    }
+  }
+}
+
 // Merge the splits of one (row, head): O = sum_s e^{m_s-M} o_s / sum_s e^{m_s-M} l_s.
 // Rows without any visible token (length <= 0, or only invalid blocks) get 0.
 template <typename QT>
@@ -157,22 +377,24 @@ __global__ __launch_bounds__(256) void decode_combine(DecodeParams p) {
   const int64_t bh = blockIdx.x;
   const float* ml = p.part_ml + bh * p.n_splits * 2;
   const float* po = p.part_o + bh * p.n_splits * p.D;
+  const int64_t len = row_length(p, static_cast<int>(bh / p.H));
+  const int n_active = static_cast<int>(min<int64_t>(p.n_splits, len > 0 ? ceil_div_dev(len, p.split_tokens) : 0));
   float big = -INFINITY;
-  for (int s = 0; s < p.n_splits; ++s) big = fmaxf(big, ml[2 * s]);
+  for (int s = 0; s < n_active; ++s) big = fmaxf(big, ml[2 * s]);
   QT* out = reinterpret_cast<QT*>(p.out) + bh * p.D;
   if (big == -INFINITY) {
     for (int d = threadIdx.x; d < p.D; d += blockDim.x) Elem<QT>::store(out + d, 0.f);
     return;
   }
   float denom = 0.f;
-  for (int s = 0; s < p.n_splits; ++s) {
+  for (int s = 0; s < n_active; ++s) {
     const float ms = ml[2 * s];
     if (ms != -INFINITY) denom += __expf(ms - big) * ml[2 * s + 1];
   }
   const float inv = denom > 0.f ? 1.f / denom : 0.f;
   for (int d = threadIdx.x; d < p.D; d += blockDim.x) {
     float acc = 0.f;
-    for (int s = 0; s < p.n_splits; ++s) {
+    for (int s = 0; s < n_active; ++s) {
       const float ms = ml[2 * s];
       if (ms != -INFINITY) acc += __expf(ms - big) * po[static_cast<int64_t>(s) * p.D + d];
     }
@@ -220,6 +442,24 @@ static int dispatch_generic(DecodeParams& p, hipStream_t stream) {
   return fail("paged decode: no kernel for group %d head_dim %d", p.G, p.D);
 }
 
+template <int D>
+static int launch_mfma_d(DecodeParams& p, hipStream_t stream) {
+  dim3 grid(p.n_splits, p.B * p.Hkv);
+  const size_t smem = MfmaDecodeSmem<D>::kBytes;
+  hipLaunchKernelGGL((decode_partial_mfma<D>), grid, dim3(64 * kMfmaWaves), smem, stream, p);
+  if (int rc = check_launch("decode_partial_mfma")) return rc;
+  hipLaunchKernelGGL((decode_combine<bf16_t>), dim3(p.B * p.H), dim3(256), 0, stream, p);
+  return check_launch("decode_combine");
+}
+
+static int launch_mfma(DecodeParams& p, hipStream_t stream) {
+  if (p.D == 256) return launch_mfma_d<256>(p, stream);
+  return launch_mfma_d<128>(p, stream);
+}
+
+struct DecodeHostArgs;
+static bool mfma_eligible(const DecodeParams& p, const struct DecodeHostArgs& a, const qa_paged_kv& kv);
+
 struct DecodeHostArgs {
   const void* query;
   int32_t q_dtype;
@@ -240,6 +480,20 @@ struct DecodeHostArgs {
   void* workspace;
   int64_t workspace_bytes;
 };
+
+// The MFMA path needs 16-token blocks, D in {128, 256}, G * D <= 2048, 16-byte
+// aligned rows (token stride and head stride multiples of 8 elements) and a
+// split length that is a multiple of 16.
+static bool mfma_eligible(const DecodeParams& p, const DecodeHostArgs& a, const qa_paged_kv& kv) {
+  if (p.bs != 16 || (p.D != 128 && p.D != 256) || p.G > 16 || p.G * p.D > 2048 || p.split_tokens % 16 != 0) return false;
+  if (kv.stride_token % 8 != 0 || kv.stride_block % 8 != 0 || kv.stride_batch % 8 != 0) return false;
+  if (kv.stride_head % 8 != 0) return false;
+  if (a.q_sb % 8 != 0 || a.q_sh % 8 != 0) return false;
+  if ((reinterpret_cast<uintptr_t>(a.query) & 15u) != 0) return false;
+  if (kv.row_key_ptrs == nullptr && (((reinterpret_cast<uintptr_t>(kv.key) | reinterpret_cast<uintptr_t>(kv.value)) & 15u) != 0)) return false;
+  if (kv.row_key_ptrs != nullptr) return false;  // per-row pools: alignment not checkable on the host
+  return true;
+}
 
 static int run_decode(const DecodeHostArgs& a, hipStream_t stream) {
   QA_REQUIRE(a.kv != nullptr, "paged decode: kv descriptor is null");
@@ -300,6 +554,7 @@ static int run_decode(const DecodeHostArgs& a, hipStream_t stream) {
   p.part_o = reinterpret_cast<float*>(a.workspace);
   p.part_ml = p.part_o + static_cast<int64_t>(p.B) * p.H * p.n_splits * p.D;
 
+  if (a.q_dtype == QA_BF16 && kv.dtype == QA_BF16 && mfma_eligible(p, a, kv)) return launch_mfma(p, stream);
   if (a.q_dtype == QA_F32 && kv.dtype == QA_F32) return dispatch_generic<float, float>(p, stream);
   if (a.q_dtype == QA_BF16 && kv.dtype == QA_BF16) return dispatch_generic<bf16_t, bf16_t>(p, stream);
   if (a.q_dtype == QA_F32 && kv.dtype == QA_BF16) return dispatch_generic<float, bf16_t>(p, stream);
