@@ -11,6 +11,7 @@
 #include "qa_common.h"
 
 #include <algorithm>
+#include <cstdlib>
 
 namespace qa {
 
@@ -189,9 +190,28 @@ struct MfmaDecodeSmem {
 };
 
 template <int D>
-__global__ __launch_bounds__(256) void decode_partial_mfma(DecodeParams p) {
+__device__ __forceinline__ void load_k_block(uint4 (&kreg)[D / 32], const bf16_t* kblk, int64_t sT, int ktok, int quad) {
+#pragma unroll
+  for (int i = 0; i < D / 32; ++i) kreg[i] = *reinterpret_cast<const uint4*>(kblk + ktok * sT + 32 * i + 8 * quad);
+}
+
+__device__ __forceinline__ void load_v_block(uint4 (&vreg)[2][4], const bf16_t* vblk, int64_t sT, int vq0, int vc) {
+#pragma unroll
+  for (int qq = 0; qq < 2; ++qq)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) vreg[qq][r] = *reinterpret_cast<const uint4*>(vblk + (4 * (vq0 + 2 * qq) + r) * sT + 8 * vc);
+}
+
+// Blocks one wave handles inside a split (split_tokens <= 512 -> 32 blocks / 4 waves).
+constexpr int kMfmaBlocksPerWave = 8;
+// Blocks loaded ahead of the one being consumed (register ring of kPrefetch + 1 tiles).
+constexpr int kPrefetch = 1;
+
+template <int D>
+__global__ __launch_bounds__(256, 2) void decode_partial_mfma(DecodeParams p) {
   constexpr int KCH = D / 32;  // QK^T k-chunks
   constexpr int MT = D / 16;   // PV output tiles (16 dims each)
+  constexpr int NBW = kMfmaBlocksPerWave;
   extern __shared__ __align__(16) unsigned char smem[];
 
   const int split = blockIdx.x;
@@ -204,8 +224,10 @@ __global__ __launch_bounds__(256) void decode_partial_mfma(DecodeParams p) {
   const int64_t t0 = static_cast<int64_t>(split) * p.split_tokens;
   if (t0 >= len) return;  // whole workgroup: nothing of this row in the split
   const int64_t t1 = min(len, t0 + p.split_tokens);
-  const int64_t lb_begin = t0 / 16;
+  const int64_t lb_first = t0 / 16 + wave;
   const int64_t lb_end = (t1 + 15) / 16;
+  // blocks of this wave: lb_first + 4 j for j < nbw
+  const int nbw = lb_first < lb_end ? static_cast<int>((lb_end - lb_first + kMfmaWaves - 1) / kMfmaWaves) : 0;
 
   const bf16_t* kb;
   const bf16_t* vb;
@@ -214,11 +236,25 @@ __global__ __launch_bounds__(256) void decode_partial_mfma(DecodeParams p) {
   kb += static_cast<int64_t>(g) * sG;
   vb += static_cast<int64_t>(g) * sG;
 
-  // Q^T as the B operand of S = K Q^T: lane l holds head l%16, dims 32i + 8(l/16) + [0, 8).
   const int head = lane & 15;
   const int quad = lane >> 4;
-  bf16x8_v qreg[KCH];
+  const int vc = lane & 31;   // 8-dim chunk of V this lane loads
+  const int vq0 = lane >> 5;  // token quads vq0 and vq0 + 2
+  const int ktok = lane & 15; // K row this lane loads
+
+  int64_t phys[NBW];
+  bool ok[NBW];
+#pragma unroll
+  for (int j = 0; j < NBW; ++j) {
+    phys[j] = j < nbw ? table_entry(p, b, lb_first + kMfmaWaves * j) : -1;
+    ok[j] = phys[j] >= 0 && phys[j] < nblk;
+    if (!ok[j]) phys[j] = 0;
+  }
+
+  // ---- phase 1: scores of every block of this wave (K streamed, one block ahead)
+  float sreg[NBW][4];
   {
+    bf16x8_v qreg[KCH];
     const bf16_t* qrow = reinterpret_cast<const bf16_t*>(p.q) + static_cast<int64_t>(b) * p.q_sb +
                          static_cast<int64_t>(g * p.G + head) * p.q_sh + 8 * quad;
 #pragma unroll
@@ -227,105 +263,88 @@ __global__ __launch_bounds__(256) void decode_partial_mfma(DecodeParams p) {
       if (head < p.G) raw = *reinterpret_cast<const uint4*>(qrow + 32 * i);
       qreg[i] = __builtin_bit_cast(bf16x8_v, raw);
     }
+    // ring of kPrefetch + 1 register tiles: block j + kPrefetch is in flight while j is consumed
+    uint4 kbuf[kPrefetch + 1][KCH];
+#pragma unroll
+    for (int j = 0; j < kPrefetch; ++j)
+      if (j < nbw) load_k_block<D>(kbuf[j], kb + phys[j] * p.sP, p.sT, ktok, quad);
+#pragma unroll
+    for (int j = 0; j < NBW; ++j) {
+      if (j + kPrefetch < nbw) load_k_block<D>(kbuf[(j + kPrefetch) % (kPrefetch + 1)], kb + phys[j + kPrefetch] * p.sP, p.sT, ktok, quad);
+      floatx4_v sacc = {0.f, 0.f, 0.f, 0.f};
+      if (j < nbw) {
+#pragma unroll
+        for (int i = 0; i < KCH; ++i)
+          sacc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_v, kbuf[j % (kPrefetch + 1)][i]), qreg[i], sacc, 0, 0, 0);
+      }
+      const int64_t tbase = (lb_first + kMfmaWaves * j) * 16 + 4 * quad;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) sreg[j][r] = (j < nbw && ok[j] && tbase + r < t1) ? sacc[r] * p.scale : -INFINITY;
+    }
   }
 
+  // First V tiles go out before the softmax so phase 3 does not start cold.
+  uint4 vbuf[kPrefetch + 1][2][4];
+#pragma unroll
+  for (int j = 0; j < kPrefetch; ++j)
+    if (j < nbw) load_v_block(vbuf[j], vb + phys[j] * p.sP, p.sT, vq0, vc);
+
+  // ---- phase 2: softmax statistics of head l%16 over the wave's tokens
+  float mx = -INFINITY;
+#pragma unroll
+  for (int j = 0; j < NBW; ++j)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) mx = fmaxf(mx, sreg[j][r]);
+  mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
+  mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+  const float m_use = mx == -INFINITY ? 0.f : mx;
+  float l_part = 0.f;
+  short4_v pb[NBW];
+#pragma unroll
+  for (int j = 0; j < NBW; ++j)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const float pr = __expf(sreg[j][r] - m_use);
+      l_part += pr;
+      pb[j][r] = static_cast<short>(f32_to_bf16(pr));
+    }
+
+  // ---- phase 3: O^T += V^T P (V streamed one block ahead, transposed via LDS)
   floatx4_v o[MT];
 #pragma unroll
   for (int t = 0; t < MT; ++t) o[t] = floatx4_v{0.f, 0.f, 0.f, 0.f};
-  float m_run = -INFINITY;  // running max of head l%16
-  float l_part = 0.f;       // this lane's share of the softmax denominator
-
   uint2* vt = reinterpret_cast<uint2*>(smem) + wave * MfmaDecodeSmem<D>::kVtUnits;
-  const int vc = lane & 31;        // 8-dim chunk of V this lane loads
-  const int vq0 = lane >> 5;       // token quads vq0 and vq0 + 2
-  const int ktok = lane & 15;      // K row this lane loads
-  const float scale = p.scale;
-
-  for (int64_t lb = lb_begin + wave; lb < lb_end; lb += kMfmaWaves) {
-    const int64_t phys = table_entry(p, b, lb);
-    const bool ok = phys >= 0 && phys < nblk;
-    uint4 kreg[KCH];
-    uint4 vreg[2][4];
-    if (ok) {
-      const bf16_t* kblk = kb + phys * p.sP;
-      const bf16_t* vblk = vb + phys * p.sP;
+  {
 #pragma unroll
-      for (int i = 0; i < KCH; ++i)
-        kreg[i] = *reinterpret_cast<const uint4*>(kblk + ktok * p.sT + 32 * i + 8 * quad);
+    for (int j = 0; j < NBW; ++j) {
+      if (j < nbw) {
+        if (j + kPrefetch < nbw) load_v_block(vbuf[(j + kPrefetch) % (kPrefetch + 1)], vb + phys[j + kPrefetch] * p.sP, p.sT, vq0, vc);
+        uint4 (&vcur)[2][4] = vbuf[j % (kPrefetch + 1)];
 #pragma unroll
-      for (int qq = 0; qq < 2; ++qq)
+        for (int qq = 0; qq < 2; ++qq) {
+          const int q = vq0 + 2 * qq;
+          const uint32_t* r0 = reinterpret_cast<const uint32_t*>(&vcur[qq][0]);
+          const uint32_t* r1 = reinterpret_cast<const uint32_t*>(&vcur[qq][1]);
+          const uint32_t* r2 = reinterpret_cast<const uint32_t*>(&vcur[qq][2]);
+          const uint32_t* r3 = reinterpret_cast<const uint32_t*>(&vcur[qq][3]);
 #pragma unroll
-        for (int r = 0; r < 4; ++r)
-          vreg[qq][r] = *reinterpret_cast<const uint4*>(vblk + (4 * (vq0 + 2 * qq) + r) * p.sT + 8 * vc);
-    } else {
+          for (int k = 0; k < 4; ++k) {
+            const int d = 8 * vc + 2 * k;
+            uint2 lo, hi;
+            lo.x = __builtin_amdgcn_perm(r1[k], r0[k], 0x05040100u);
+            lo.y = __builtin_amdgcn_perm(r3[k], r2[k], 0x05040100u);
+            hi.x = __builtin_amdgcn_perm(r1[k], r0[k], 0x07060302u);
+            hi.y = __builtin_amdgcn_perm(r3[k], r2[k], 0x07060302u);
+            vt[q * (D + kVtPad) + vt_swizzle(d)] = lo;
+            vt[q * (D + kVtPad) + vt_swizzle(d + 1)] = hi;
+          }
+        }
 #pragma unroll
-      for (int i = 0; i < KCH; ++i) kreg[i] = make_uint4(0, 0, 0, 0);
-#pragma unroll
-      for (int qq = 0; qq < 2; ++qq)
-#pragma unroll
-        for (int r = 0; r < 4; ++r) vreg[qq][r] = make_uint4(0, 0, 0, 0);
-    }
-
-    // S = K Q^T over the block's 16 tokens.
-    floatx4_v sacc = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int i = 0; i < KCH; ++i)
-      sacc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_v, kreg[i]), qreg[i], sacc, 0, 0, 0);
-
-    // Online softmax for head l%16; this lane holds tokens 16*lb + 4*quad + r.
-    float sv[4];
-    float mx = -INFINITY;
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int64_t t = lb * 16 + 4 * quad + r;
-      sv[r] = (ok && t < t1) ? sacc[r] * scale : -INFINITY;
-      mx = fmaxf(mx, sv[r]);
-    }
-    mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
-    mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-    const float m_new = fmaxf(m_run, mx);
-    const float m_use = m_new == -INFINITY ? 0.f : m_new;
-    const float alpha = __expf(m_run - m_use);
-    float pr[4];
-    float psum = 0.f;
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      pr[r] = __expf(sv[r] - m_use);
-      psum += pr[r];
-    }
-    l_part = l_part * alpha + psum;
-    m_run = m_new;
-#pragma unroll
-    for (int t = 0; t < MT; ++t) o[t] *= alpha;
-    short4_v pb;
-#pragma unroll
-    for (int r = 0; r < 4; ++r) pb[r] = static_cast<short>(f32_to_bf16(pr[r]));
-
-    // V -> LDS as 4-token columns: unit (quad q, dim d) = V[4q..4q+3][d].
-#pragma unroll
-    for (int qq = 0; qq < 2; ++qq) {
-      const int q = vq0 + 2 * qq;
-      const uint32_t* r0 = reinterpret_cast<const uint32_t*>(&vreg[qq][0]);
-      const uint32_t* r1 = reinterpret_cast<const uint32_t*>(&vreg[qq][1]);
-      const uint32_t* r2 = reinterpret_cast<const uint32_t*>(&vreg[qq][2]);
-      const uint32_t* r3 = reinterpret_cast<const uint32_t*>(&vreg[qq][3]);
-#pragma unroll
-      for (int k = 0; k < 4; ++k) {
-        const int d = 8 * vc + 2 * k;
-        uint2 lo, hi;
-        lo.x = __builtin_amdgcn_perm(r1[k], r0[k], 0x05040100u);
-        lo.y = __builtin_amdgcn_perm(r3[k], r2[k], 0x05040100u);
-        hi.x = __builtin_amdgcn_perm(r1[k], r0[k], 0x07060302u);
-        hi.y = __builtin_amdgcn_perm(r3[k], r2[k], 0x07060302u);
-        vt[q * (D + kVtPad) + vt_swizzle(d)] = lo;
-        vt[q * (D + kVtPad) + vt_swizzle(d + 1)] = hi;
+        for (int t = 0; t < MT; ++t) {
+          const uint2 a = vt[quad * (D + kVtPad) + vt_swizzle(16 * t + head)];
+          o[t] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(__builtin_bit_cast(short4_v, a), pb[j], o[t], 0, 0, 0);
+        }
       }
-    }
-    // O^T += V^T P: A operand = 4 tokens of quad l/16 at dim 16t + l%16.
-#pragma unroll
-    for (int t = 0; t < MT; ++t) {
-      const uint2 a = vt[quad * (D + kVtPad) + vt_swizzle(16 * t + head)];
-      o[t] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(__builtin_bit_cast(short4_v, a), pb, o[t], 0, 0, 0);
     }
   }
 
@@ -334,14 +353,14 @@ __global__ __launch_bounds__(256) void decode_partial_mfma(DecodeParams p) {
   l_part += __shfl_xor(l_part, 32, 64);
 
   __syncthreads();  // LDS now reused for the cross-wave merge
-  float* om = reinterpret_cast<float*>(smem);                  // [wave][G heads][D]
-  float* mlw = om + kMfmaWaves * 2048;                         // [wave][16][2]
+  float* om = reinterpret_cast<float*>(smem);  // [wave][G heads][D]
+  float* mlw = om + kMfmaWaves * 2048;         // [wave][16][2]
   if (head < p.G) {
 #pragma unroll
     for (int t = 0; t < MT; ++t)
       *reinterpret_cast<floatx4_v*>(om + (wave * p.G + head) * D + 16 * t + 4 * quad) = o[t];
     if (quad == 0) {
-      mlw[(wave * 16 + head) * 2 + 0] = m_run;
+      mlw[(wave * 16 + head) * 2 + 0] = mx;
       mlw[(wave * 16 + head) * 2 + 1] = l_part;
     }
   }
@@ -372,41 +391,71 @@ __global__ __launch_bounds__(256) void decode_partial_mfma(DecodeParams p) {
 
 // Merge the splits of one (row, head): O = sum_s e^{m_s-M} o_s / sum_s e^{m_s-M} l_s.
 // Rows without any visible token (length <= 0, or only invalid blocks) get 0.
+// Split weights are computed once per split into LDS; each thread then owns
+// head_dim/blockDim columns and streams the partials with independent loads.
+constexpr int kCombineMaxSplits = 1024;
+
 template <typename QT>
 __global__ __launch_bounds__(256) void decode_combine(DecodeParams p) {
+  __shared__ float weight[kCombineMaxSplits];
+  __shared__ float red[256 / 64];
   const int64_t bh = blockIdx.x;
   const float* ml = p.part_ml + bh * p.n_splits * 2;
   const float* po = p.part_o + bh * p.n_splits * p.D;
   const int64_t len = row_length(p, static_cast<int>(bh / p.H));
   const int n_active = static_cast<int>(min<int64_t>(p.n_splits, len > 0 ? ceil_div_dev(len, p.split_tokens) : 0));
-  float big = -INFINITY;
-  for (int s = 0; s < n_active; ++s) big = fmaxf(big, ml[2 * s]);
   QT* out = reinterpret_cast<QT*>(p.out) + bh * p.D;
-  if (big == -INFINITY) {
-    for (int d = threadIdx.x; d < p.D; d += blockDim.x) Elem<QT>::store(out + d, 0.f);
-    return;
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+
+  float big = -INFINITY;
+  for (int s = threadIdx.x; s < n_active; s += blockDim.x) big = fmaxf(big, ml[2 * s]);
+  big = wave_max(big);
+  if (lane == 0) red[wave] = big;
+  __syncthreads();
+  big = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+  __syncthreads();
+  const float use = big == -INFINITY ? 0.f : big;
+  float den = 0.f;
+  for (int s = threadIdx.x; s < n_active; s += blockDim.x) {
+    const float f = __expf(ml[2 * s] - use);
+    weight[s] = f;
+    den += f * ml[2 * s + 1];
   }
-  float denom = 0.f;
-  for (int s = 0; s < n_active; ++s) {
-    const float ms = ml[2 * s];
-    if (ms != -INFINITY) denom += __expf(ms - big) * ml[2 * s + 1];
-  }
-  const float inv = denom > 0.f ? 1.f / denom : 0.f;
+  den = wave_sum(den);
+  if (lane == 0) red[wave] = den;
+  __syncthreads();
+  den = red[0] + red[1] + red[2] + red[3];
+  const float inv = den > 0.f ? 1.f / den : 0.f;
   for (int d = threadIdx.x; d < p.D; d += blockDim.x) {
-    float acc = 0.f;
-    for (int s = 0; s < n_active; ++s) {
-      const float ms = ml[2 * s];
-      if (ms != -INFINITY) acc += __expf(ms - big) * po[static_cast<int64_t>(s) * p.D + d];
+    float acc0 = 0.f, acc1 = 0.f, acc2 = 0.f, acc3 = 0.f;
+    int s = 0;
+    for (; s + 4 <= n_active; s += 4) {
+      acc0 += weight[s + 0] * po[static_cast<int64_t>(s + 0) * p.D + d];
+      acc1 += weight[s + 1] * po[static_cast<int64_t>(s + 1) * p.D + d];
+      acc2 += weight[s + 2] * po[static_cast<int64_t>(s + 2) * p.D + d];
+      acc3 += weight[s + 3] * po[static_cast<int64_t>(s + 3) * p.D + d];
     }
-    Elem<QT>::store(out + d, acc * inv);
+    for (; s < n_active; ++s) acc0 += weight[s] * po[static_cast<int64_t>(s) * p.D + d];
+    Elem<QT>::store(out + d, ((acc0 + acc1) + (acc2 + acc3)) * inv);
   }
 }
 
 // Token count handled by one work item.  Shared by the workspace query and
 // the launcher so the two always agree.
+// QA_DECODE_SPLIT_TOKENS (read once) overrides the upper bound of 512 tokens.
+static int64_t split_upper_bound() {
+  static const int64_t value = [] {
+    const char* env = getenv("QA_DECODE_SPLIT_TOKENS");
+    const long v = env != nullptr ? strtol(env, nullptr, 10) : 0;
+    return v >= 16 && v <= 512 ? static_cast<int64_t>(v) : int64_t{512};
+  }();
+  return value;
+}
+
 static int choose_split_tokens(int64_t max_tokens, int block_size) {
   const int64_t lo = ceil_div(64, block_size) * block_size;
-  const int64_t hi = std::max<int64_t>(lo, ceil_div(512, block_size) * block_size);
+  const int64_t hi = std::max<int64_t>(lo, ceil_div(split_upper_bound(), block_size) * block_size);
   int64_t want = ceil_div(ceil_div(std::max<int64_t>(max_tokens, 1), 16), block_size) * block_size;
   return static_cast<int>(std::min(hi, std::max(lo, want)));
 }
@@ -486,6 +535,7 @@ struct DecodeHostArgs {
 // split length that is a multiple of 16.
 static bool mfma_eligible(const DecodeParams& p, const DecodeHostArgs& a, const qa_paged_kv& kv) {
   if (p.bs != 16 || (p.D != 128 && p.D != 256) || p.G > 16 || p.G * p.D > 2048 || p.split_tokens % 16 != 0) return false;
+  if (p.split_tokens > 16 * kMfmaWaves * kMfmaBlocksPerWave) return false;
   if (kv.stride_token % 8 != 0 || kv.stride_block % 8 != 0 || kv.stride_batch % 8 != 0) return false;
   if (kv.stride_head % 8 != 0) return false;
   if (a.q_sb % 8 != 0 || a.q_sh % 8 != 0) return false;
@@ -549,6 +599,7 @@ static int run_decode(const DecodeHostArgs& a, hipStream_t stream) {
   p.scale = a.scale > 0.f ? a.scale : 1.0f / sqrtf(static_cast<float>(a.head_dim));
   p.split_tokens = choose_split_tokens(a.max_tokens, a.block_size);
   p.n_splits = static_cast<int>(std::max<int64_t>(1, ceil_div(std::max<int64_t>(a.max_tokens, 1), p.split_tokens)));
+  QA_REQUIRE(p.n_splits <= kCombineMaxSplits, "paged decode: %lld tokens need more than %d splits", static_cast<long long>(a.max_tokens), kCombineMaxSplits);
   const int64_t need = decode_workspace_bytes(a.batch, a.heads, a.head_dim, a.max_tokens, a.block_size);
   QA_REQUIRE(a.workspace != nullptr && a.workspace_bytes >= need, "paged decode workspace too small: need %lld bytes", static_cast<long long>(need));
   p.part_o = reinterpret_cast<float*>(a.workspace);
