@@ -131,6 +131,58 @@ int qa_paged_kv_gather(const qa_paged_kv* kv, int32_t head_dim, int64_t batch,
                        int64_t max_blocks, int64_t valid, int32_t block_size,
                        void* key_out, void* value_out, hipStream_t stream);
 
+/* ---- gated delta-rule linear attention --------------------------------- */
+/* Depthwise causal conv1d over `seq` tokens (+ optional SiLU), fp32 math.
+ * x: (batch, seq, channels) with element strides (x_stride_b, x_stride_t),
+ * channels contiguous, float32 or bfloat16.  initial_state/final_state:
+ * (rows, channels, kernel-1) fp32 (row = slots[b] when slots != NULL, else
+ * b); a NULL initial_state means zeros.  weight: (channels, kernel) fp32.
+ * out: (batch, seq, channels) float32 or bfloat16.  Replaces the conv of
+ * linear_attention (src/reference_ops.py:240-258, src/tp_runtime.py:2635-2659). */
+int qa_causal_conv1d_prefill(const void* x, int32_t x_dtype, int64_t x_stride_b, int64_t x_stride_t,
+                             const float* initial_state, float* final_state, int64_t state_stride_b,
+                             const void* slots, int32_t slots_dtype,
+                             const float* weight, int64_t batch, int64_t seq, int32_t channels, int32_t kernel,
+                             void* out, int32_t out_dtype, int64_t out_stride_b, int64_t out_stride_t,
+                             int32_t apply_silu, hipStream_t stream);
+
+/* Single-token conv update with the (rows, channels, kernel-1) conv state
+ * updated in place (the cache's conv_tail, src/reference_ops.py:253-257).   */
+int qa_causal_conv1d_update(const void* x, int32_t x_dtype, int64_t x_stride_b,
+                            float* conv_state, int64_t state_stride_b, const void* slots, int32_t slots_dtype,
+                            const float* weight, int64_t batch, int32_t channels, int32_t kernel,
+                            void* out, int32_t out_dtype, int64_t out_stride_b, int32_t apply_silu,
+                            hipStream_t stream);
+
+/* Token-serial gated delta rule on prepared inputs: query/key (B, H, S, dk),
+ * value (B, H, S, dv), g/beta (B, H, S), initial_state (B, H, dk, dv), all
+ * contiguous fp32; output (B, H, S, dv) and final_state (B, H, dk, dv) fp32
+ * (final_state may alias initial_state).  Replaces
+ * `linear_attention_recurrent_core` (src/fp8_cuda.py:206-214 ->
+ * src/csrc/fp8_linear.h:99-105, src/csrc/fp8_linear_cuda.cu:2491-2573).   */
+int qa_linear_attention_recurrent_core(const float* query, const float* key, const float* value,
+                                       const float* g, const float* beta, const float* initial_state,
+                                       float* output, float* final_state,
+                                       int64_t batch, int32_t heads, int64_t seq_len,
+                                       int32_t key_dim, int32_t value_dim, hipStream_t stream);
+
+/* Fused single-token decode step of a linear-attention layer after its conv:
+ * qkv (B, 2*Hqk*dk + Hv*dv) fp32 = SiLU(conv) output; a, b (B, Hv) raw
+ * projection outputs; a_log, dt_bias (Hv) fp32.  Computes
+ * beta = sigmoid(b), g = -exp(a_log) softplus(a + dt_bias), L2-normalised
+ * q*dk^-0.5 and k (value head j reads key head j / (Hv/Hqk)), one recurrence
+ * step on state[slot(b)] (slots, Hv, dk, dv) fp32 in place, and writes
+ * out (B, Hv, dv).  dk = dv = 128.  Replaces the per-request state stacking
+ * and recurrence of src/tp_runtime.py:2613-2717 with a slot-indexed pool
+ * (src/reference_ops.py:271-283, :291-322).                               */
+int qa_gated_delta_step(const float* qkv, int64_t qkv_stride_b,
+                        const void* a, const void* b, int32_t ab_dtype, int64_t ab_stride_b,
+                        const float* a_log, const float* dt_bias,
+                        float* state, int64_t state_stride_slot, const void* slots, int32_t slots_dtype,
+                        void* out, int32_t out_dtype, int64_t out_stride_b,
+                        int64_t batch, int32_t key_heads, int32_t value_heads,
+                        int32_t key_dim, int32_t value_dim, hipStream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

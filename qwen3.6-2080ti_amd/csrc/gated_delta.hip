@@ -1,0 +1,457 @@
+// Gated delta-rule linear attention on gfx950: causal depthwise conv1d (prefill
+// and single-token update), the token-serial recurrence (reference-compatible
+// core), and the fused single-token decode step.
+//
+// Recurrence per (sequence, value head), state S (dk x dv) fp32
+// (src/reference_ops.py:310-318):
+//   S <- S * exp(g_t);  kv = S^T k_t;  delta = (v_t - kv) * beta_t;
+//   S <- S + k_t delta^T;  o_t = S^T q_t
+// The 128x128 fast path keeps S in registers: 256 threads, thread (wave w,
+// lane = 16*rg + cg) owns rows 32w + 8rg + [0,8) and columns 8cg + [0,8); the
+// two reductions over dk per token run as a 2-step shuffle inside each wave
+// plus a 4-way LDS sum across waves.
+#include "qa_common.h"
+
+namespace qa {
+
+__device__ __forceinline__ float softplus_ref(float x) {
+  // torch.nn.functional.softplus with beta = 1, threshold = 20
+  return x > 20.f ? x : log1pf(__expf(x));
+}
+
+__device__ __forceinline__ float sigmoid_ref(float x) { return 1.f / (1.f + __expf(-x)); }
+
+__device__ __forceinline__ float silu_ref(float x) { return x / (1.f + __expf(-x)); }
+
+__device__ __forceinline__ float load_any(const void* base, int dtype, int64_t i) {
+  return dtype == QA_BF16 ? bf16_to_f32(reinterpret_cast<const bf16_t*>(base)[i]) : reinterpret_cast<const float*>(base)[i];
+}
+
+__device__ __forceinline__ void store_any(void* base, int dtype, int64_t i, float v) {
+  if (dtype == QA_BF16)
+    reinterpret_cast<bf16_t*>(base)[i] = f32_to_bf16(v);
+  else
+    reinterpret_cast<float*>(base)[i] = v;
+}
+
+__device__ __forceinline__ int64_t slot_of(const void* slots, int is64, int64_t b) {
+  if (slots == nullptr) return b;
+  return is64 ? reinterpret_cast<const int64_t*>(slots)[b] : reinterpret_cast<const int32_t*>(slots)[b];
+}
+
+// ---------------------------------------------------------------------------
+// causal depthwise conv1d (src/reference_ops.py:245-258)
+
+struct ConvParams {
+  const void* x;
+  int x_dtype;
+  int64_t x_sb, x_st;  // element strides of (batch, token); channels contiguous
+  const float* state_in;  // (rows, C, K-1) or null (zeros)
+  float* state_out;       // (rows, C, K-1) or null
+  int64_t state_sb;
+  const void* slots;
+  int slots_i64;
+  const float* weight;  // (C, K)
+  int64_t batch, seq;
+  int C, K;
+  void* out;
+  int out_dtype;
+  int64_t out_sb, out_st;
+  int silu;
+};
+
+constexpr int kConvMaxK = 8;
+
+// One thread per (row, channel); tokens in order with the window in registers.
+__global__ __launch_bounds__(256) void conv1d_kernel(ConvParams p) {
+  const int c = blockIdx.x * blockDim.x + threadIdx.x;
+  const int64_t b = blockIdx.y;
+  if (c >= p.C) return;
+  const int64_t row = slot_of(p.slots, p.slots_i64, b);
+  float win[kConvMaxK];
+  float w[kConvMaxK];
+#pragma unroll
+  for (int i = 0; i < kConvMaxK; ++i) {
+    w[i] = i < p.K ? p.weight[static_cast<int64_t>(c) * p.K + i] : 0.f;
+    win[i] = 0.f;
+  }
+  // window slots 0..K-2 hold the K-1 previous inputs (oldest first)
+  if (p.state_in != nullptr) {
+    const float* st = p.state_in + row * p.state_sb + static_cast<int64_t>(c) * (p.K - 1);
+    for (int i = 0; i < p.K - 1; ++i) win[i] = st[i];
+  }
+  for (int64_t t = 0; t < p.seq; ++t) {
+    const float x = load_any(p.x, p.x_dtype, b * p.x_sb + t * p.x_st + c);
+    win[p.K - 1] = x;
+    float acc = 0.f;
+#pragma unroll
+    for (int i = 0; i < kConvMaxK; ++i)
+      if (i < p.K) acc += w[i] * win[i];
+    store_any(p.out, p.out_dtype, b * p.out_sb + t * p.out_st + c, p.silu ? silu_ref(acc) : acc);
+#pragma unroll
+    for (int i = 0; i < kConvMaxK - 1; ++i)
+      if (i < p.K - 1) win[i] = win[i + 1];
+  }
+  if (p.state_out != nullptr) {
+    float* st = p.state_out + row * p.state_sb + static_cast<int64_t>(c) * (p.K - 1);
+    for (int i = 0; i < p.K - 1; ++i) st[i] = win[i];
+  }
+}
+
+// ---------------------------------------------------------------------------
+// recurrence
+
+struct DeltaParams {
+  // reference-compatible prepared inputs (B, H, S, d), fp32, contiguous
+  const float* q;
+  const float* k;
+  const float* v;
+  const float* g;
+  const float* beta;
+  // fused decode inputs
+  const float* qkv;  // (B, C) post conv + SiLU
+  int64_t qkv_sb;
+  const void* a;
+  const void* bb;
+  int ab_dtype;
+  int64_t ab_sb;
+  const float* a_log;
+  const float* dt_bias;
+  // state
+  const float* state_in;
+  float* state_out;
+  int64_t state_sb;  // per batch row / slot (elements)
+  const void* slots;
+  int slots_i64;
+  // output
+  void* out;
+  int out_dtype;
+  int64_t out_sb;  // fused: per batch row
+  int64_t B, S;
+  int H, Hqk, dk, dv;
+};
+
+// Generic shapes: one thread per value column, its state column kept in the
+// output state buffer (read-modify-write).  Used for small or unusual dims.
+__global__ __launch_bounds__(128) void delta_recurrent_generic(DeltaParams p) {
+  const int64_t bh = blockIdx.x;
+  const int j = blockIdx.y * blockDim.x + threadIdx.x;
+  if (j >= p.dv) return;
+  const int64_t plane = static_cast<int64_t>(p.dk) * p.dv;
+  const float* s_in = p.state_in + bh * plane;
+  float* s = p.state_out + bh * plane;
+  for (int i = 0; i < p.dk; ++i) s[static_cast<int64_t>(i) * p.dv + j] = s_in[static_cast<int64_t>(i) * p.dv + j];
+  for (int64_t t = 0; t < p.S; ++t) {
+    const int64_t tok = bh * p.S + t;
+    const float* kt = p.k + tok * p.dk;
+    const float* qt = p.q + tok * p.dk;
+    const float decay = __expf(p.g[tok]);
+    float kv = 0.f;
+    for (int i = 0; i < p.dk; ++i) {
+      const int64_t idx = static_cast<int64_t>(i) * p.dv + j;
+      const float sv = s[idx] * decay;
+      s[idx] = sv;
+      kv += sv * kt[i];
+    }
+    const float delta = (p.v[tok * p.dv + j] - kv) * p.beta[tok];
+    float o = 0.f;
+    for (int i = 0; i < p.dk; ++i) {
+      const int64_t idx = static_cast<int64_t>(i) * p.dv + j;
+      const float sv = s[idx] + kt[i] * delta;
+      s[idx] = sv;
+      o += sv * qt[i];
+    }
+    reinterpret_cast<float*>(p.out)[tok * p.dv + j] = o;
+  }
+}
+
+// dk = dv = 128: register-resident state, see the file header for the layout.
+template <bool FUSED>
+__global__ __launch_bounds__(256) void delta_recurrent_128(DeltaParams p) {
+  constexpr int DK = 128, DV = 128;
+  __shared__ float red[2][4][DV];
+  __shared__ float nrm[2][4];
+  const int64_t b = blockIdx.x / p.H;
+  const int h = blockIdx.x - static_cast<int>(b) * p.H;
+  const int w = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63;
+  const int rg = lane >> 4;
+  const int cg = lane & 15;
+  const int row0 = 32 * w + 8 * rg;
+  const int col0 = 8 * cg;
+
+  const float* s_in;
+  float* s_out;
+  if (FUSED) {
+    const int64_t slot = slot_of(p.slots, p.slots_i64, b);
+    s_in = p.state_in + slot * p.state_sb + static_cast<int64_t>(h) * DK * DV;
+    s_out = p.state_out + slot * p.state_sb + static_cast<int64_t>(h) * DK * DV;
+  } else {
+    s_in = p.state_in + (b * p.H + h) * DK * DV;
+    s_out = p.state_out + (b * p.H + h) * DK * DV;
+  }
+  float S[8][8];
+#pragma unroll
+  for (int r = 0; r < 8; ++r) {
+    const float4 lo = *reinterpret_cast<const float4*>(s_in + (row0 + r) * DV + col0);
+    const float4 hi = *reinterpret_cast<const float4*>(s_in + (row0 + r) * DV + col0 + 4);
+    S[r][0] = lo.x; S[r][1] = lo.y; S[r][2] = lo.z; S[r][3] = lo.w;
+    S[r][4] = hi.x; S[r][5] = hi.y; S[r][6] = hi.z; S[r][7] = hi.w;
+  }
+
+  const int T = FUSED ? 1 : static_cast<int>(p.S);
+  for (int t = 0; t < T; ++t) {
+    float kr[8], qr[8], vc[8];
+    float decay, beta;
+    if (FUSED) {
+      const int qh = h / (p.H / p.Hqk);
+      const float* base = p.qkv + b * p.qkv_sb;
+      const float* qv = base + qh * DK;
+      const float* kvv = base + p.Hqk * DK + qh * DK;
+      const float* vv = base + 2 * p.Hqk * DK + h * DV;
+      float sq = 0.f, sk = 0.f;
+#pragma unroll
+      for (int r = 0; r < 8; ++r) {
+        qr[r] = qv[row0 + r];
+        kr[r] = kvv[row0 + r];
+        sq += qr[r] * qr[r];
+        sk += kr[r] * kr[r];
+      }
+#pragma unroll
+      for (int c = 0; c < 8; ++c) vc[c] = vv[col0 + c];
+      // sum over the 4 row groups of this wave (lanes xor 16, 32), then the 4 waves
+      sq += __shfl_xor(sq, 16, 64);
+      sq += __shfl_xor(sq, 32, 64);
+      sk += __shfl_xor(sk, 16, 64);
+      sk += __shfl_xor(sk, 32, 64);
+      if (lane == 0) {
+        nrm[0][w] = sq;
+        nrm[1][w] = sk;
+      }
+      __syncthreads();
+      sq = (nrm[0][0] + nrm[0][1]) + (nrm[0][2] + nrm[0][3]);
+      sk = (nrm[1][0] + nrm[1][1]) + (nrm[1][2] + nrm[1][3]);
+      // l2_norm (src/reference_ops.py:181-183) and q * dk^-0.5 (:304)
+      const float rq = rsqrtf(sq + 1e-6f) * rsqrtf(static_cast<float>(DK));
+      const float rk = rsqrtf(sk + 1e-6f);
+#pragma unroll
+      for (int r = 0; r < 8; ++r) {
+        qr[r] *= rq;
+        kr[r] *= rk;
+      }
+      // gating (src/reference_ops.py:271-275)
+      const float av = load_any(p.a, p.ab_dtype, b * p.ab_sb + h);
+      const float bv = load_any(p.bb, p.ab_dtype, b * p.ab_sb + h);
+      const float gval = -__expf(p.a_log[h]) * softplus_ref(av + p.dt_bias[h]);
+      decay = __expf(gval);
+      beta = sigmoid_ref(bv);
+    } else {
+      const int64_t tok = (b * p.H + h) * p.S + t;
+#pragma unroll
+      for (int r = 0; r < 8; ++r) {
+        qr[r] = p.q[tok * DK + row0 + r];
+        kr[r] = p.k[tok * DK + row0 + r];
+      }
+#pragma unroll
+      for (int c = 0; c < 8; ++c) vc[c] = p.v[tok * DV + col0 + c];
+      decay = __expf(p.g[tok]);
+      beta = p.beta[tok];
+    }
+
+    float part[8];
+#pragma unroll
+    for (int c = 0; c < 8; ++c) {
+      float acc = 0.f;
+#pragma unroll
+      for (int r = 0; r < 8; ++r) {
+        S[r][c] *= decay;
+        acc += S[r][c] * kr[r];
+      }
+      part[c] = acc;
+    }
+#pragma unroll
+    for (int c = 0; c < 8; ++c) {
+      part[c] += __shfl_xor(part[c], 16, 64);
+      part[c] += __shfl_xor(part[c], 32, 64);
+    }
+    if (rg == 0) {
+#pragma unroll
+      for (int c = 0; c < 8; ++c) red[0][w][col0 + c] = part[c];
+    }
+    __syncthreads();
+    float delta[8];
+#pragma unroll
+    for (int c = 0; c < 8; ++c) {
+      const float kv = (red[0][0][col0 + c] + red[0][1][col0 + c]) + (red[0][2][col0 + c] + red[0][3][col0 + c]);
+      delta[c] = (vc[c] - kv) * beta;
+    }
+#pragma unroll
+    for (int c = 0; c < 8; ++c) {
+      float acc = 0.f;
+#pragma unroll
+      for (int r = 0; r < 8; ++r) {
+        S[r][c] += kr[r] * delta[c];
+        acc += S[r][c] * qr[r];
+      }
+      part[c] = acc;
+    }
+#pragma unroll
+    for (int c = 0; c < 8; ++c) {
+      part[c] += __shfl_xor(part[c], 16, 64);
+      part[c] += __shfl_xor(part[c], 32, 64);
+    }
+    if (rg == 0) {
+#pragma unroll
+      for (int c = 0; c < 8; ++c) red[1][w][col0 + c] = part[c];
+    }
+    __syncthreads();
+    if (w == 0 && rg == 0) {
+#pragma unroll
+      for (int c = 0; c < 8; ++c) {
+        const float o = (red[1][0][col0 + c] + red[1][1][col0 + c]) + (red[1][2][col0 + c] + red[1][3][col0 + c]);
+        if (FUSED)
+          store_any(p.out, p.out_dtype, b * p.out_sb + static_cast<int64_t>(h) * DV + col0 + c, o);
+        else
+          reinterpret_cast<float*>(p.out)[((b * p.H + h) * p.S + t) * DV + col0 + c] = o;
+      }
+    }
+  }
+
+#pragma unroll
+  for (int r = 0; r < 8; ++r) {
+    *reinterpret_cast<float4*>(s_out + (row0 + r) * DV + col0) = make_float4(S[r][0], S[r][1], S[r][2], S[r][3]);
+    *reinterpret_cast<float4*>(s_out + (row0 + r) * DV + col0 + 4) = make_float4(S[r][4], S[r][5], S[r][6], S[r][7]);
+  }
+}
+
+static bool aligned16(const void* ptr) { return (reinterpret_cast<uintptr_t>(ptr) & 15u) == 0; }
+
+}  // namespace qa
+
+// ---------------------------------------------------------------------------
+// C ABI
+
+extern "C" int qa_causal_conv1d_prefill(const void* x, int32_t x_dtype, int64_t x_stride_b, int64_t x_stride_t,
+                                        const float* initial_state, float* final_state, int64_t state_stride_b,
+                                        const void* slots, int32_t slots_dtype, const float* weight, int64_t batch,
+                                        int64_t seq, int32_t channels, int32_t kernel, void* out, int32_t out_dtype,
+                                        int64_t out_stride_b, int64_t out_stride_t, int32_t apply_silu, hipStream_t stream) {
+  using namespace qa;
+  QA_REQUIRE(x && weight && out, "conv1d: x, weight and out must be non-null");
+  QA_REQUIRE(x_dtype == QA_F32 || x_dtype == QA_BF16, "conv1d: x must be float32 or bfloat16");
+  QA_REQUIRE(out_dtype == QA_F32 || out_dtype == QA_BF16, "conv1d: out must be float32 or bfloat16");
+  QA_REQUIRE(kernel >= 1 && kernel <= kConvMaxK, "conv1d: kernel size must be in [1, %d]", kConvMaxK);
+  QA_REQUIRE(channels > 0 && batch > 0 && batch <= 65535, "conv1d: bad batch/channels");
+  QA_REQUIRE(seq >= 0, "conv1d: seq must be non-negative");
+  QA_REQUIRE(slots == nullptr || is_index_dtype(slots_dtype), "conv1d: slots must be int32/int64");
+  ConvParams p{};
+  p.x = x;
+  p.x_dtype = x_dtype;
+  p.x_sb = x_stride_b;
+  p.x_st = x_stride_t;
+  p.state_in = initial_state;
+  p.state_out = final_state;
+  p.state_sb = state_stride_b;
+  p.slots = slots;
+  p.slots_i64 = slots_dtype == QA_I64;
+  p.weight = weight;
+  p.batch = batch;
+  p.seq = seq;
+  p.C = channels;
+  p.K = kernel;
+  p.out = out;
+  p.out_dtype = out_dtype;
+  p.out_sb = out_stride_b;
+  p.out_st = out_stride_t;
+  p.silu = apply_silu;
+  dim3 grid(static_cast<unsigned>(ceil_div(channels, 256)), static_cast<unsigned>(batch));
+  hipLaunchKernelGGL(conv1d_kernel, grid, dim3(256), 0, stream, p);
+  return check_launch("conv1d_kernel");
+}
+
+extern "C" int qa_causal_conv1d_update(const void* x, int32_t x_dtype, int64_t x_stride_b, float* conv_state,
+                                       int64_t state_stride_b, const void* slots, int32_t slots_dtype, const float* weight,
+                                       int64_t batch, int32_t channels, int32_t kernel, void* out, int32_t out_dtype,
+                                       int64_t out_stride_b, int32_t apply_silu, hipStream_t stream) {
+  QA_REQUIRE(conv_state != nullptr, "conv1d update: conv_state must be non-null");
+  return qa_causal_conv1d_prefill(x, x_dtype, x_stride_b, 0, conv_state, conv_state, state_stride_b, slots, slots_dtype,
+                                  weight, batch, 1, channels, kernel, out, out_dtype, out_stride_b, 0, apply_silu, stream);
+}
+
+extern "C" int qa_linear_attention_recurrent_core(const float* query, const float* key, const float* value, const float* g,
+                                                  const float* beta, const float* initial_state, float* output,
+                                                  float* final_state, int64_t batch, int32_t heads, int64_t seq_len,
+                                                  int32_t key_dim, int32_t value_dim, hipStream_t stream) {
+  using namespace qa;
+  QA_REQUIRE(query && key && value && g && beta && initial_state && output && final_state,
+             "linear_attention_recurrent_core: all pointers must be non-null");
+  QA_REQUIRE(batch > 0 && heads > 0 && seq_len > 0 && key_dim > 0 && value_dim > 0,
+             "linear_attention_recurrent_core: sizes must be positive");
+  QA_REQUIRE(batch * heads <= 0x7fffffff, "linear_attention_recurrent_core: batch*heads too large");
+  DeltaParams p{};
+  p.q = query;
+  p.k = key;
+  p.v = value;
+  p.g = g;
+  p.beta = beta;
+  p.state_in = initial_state;
+  p.state_out = final_state;
+  p.out = output;
+  p.out_dtype = QA_F32;
+  p.B = batch;
+  p.S = seq_len;
+  p.H = heads;
+  p.Hqk = heads;
+  p.dk = key_dim;
+  p.dv = value_dim;
+  const bool fast = key_dim == 128 && value_dim == 128 && aligned16(initial_state) && aligned16(final_state);
+  if (fast) {
+    hipLaunchKernelGGL(delta_recurrent_128<false>, dim3(static_cast<unsigned>(batch * heads)), dim3(256), 0, stream, p);
+    return check_launch("delta_recurrent_128");
+  }
+  dim3 grid(static_cast<unsigned>(batch * heads), static_cast<unsigned>(ceil_div(value_dim, 128)));
+  hipLaunchKernelGGL(delta_recurrent_generic, grid, dim3(128), 0, stream, p);
+  return check_launch("delta_recurrent_generic");
+}
+
+extern "C" int qa_gated_delta_step(const float* qkv, int64_t qkv_stride_b, const void* a, const void* b, int32_t ab_dtype,
+                                   int64_t ab_stride_b, const float* a_log, const float* dt_bias, float* state,
+                                   int64_t state_stride_slot, const void* slots, int32_t slots_dtype, void* out,
+                                   int32_t out_dtype, int64_t out_stride_b, int64_t batch, int32_t key_heads,
+                                   int32_t value_heads, int32_t key_dim, int32_t value_dim, hipStream_t stream) {
+  using namespace qa;
+  QA_REQUIRE(qkv && a && b && a_log && dt_bias && state && out, "gated_delta_step: pointers must be non-null");
+  QA_REQUIRE(key_dim == 128 && value_dim == 128, "gated_delta_step: only key_dim = value_dim = 128 is built");
+  QA_REQUIRE(key_heads > 0 && value_heads % key_heads == 0, "gated_delta_step: value heads must be a multiple of key heads");
+  QA_REQUIRE(ab_dtype == QA_F32 || ab_dtype == QA_BF16, "gated_delta_step: a/b must be float32 or bfloat16");
+  QA_REQUIRE(out_dtype == QA_F32 || out_dtype == QA_BF16, "gated_delta_step: out must be float32 or bfloat16");
+  QA_REQUIRE(slots == nullptr || is_index_dtype(slots_dtype), "gated_delta_step: slots must be int32/int64");
+  QA_REQUIRE(batch > 0 && batch * value_heads <= 0x7fffffff, "gated_delta_step: bad batch");
+  QA_REQUIRE(aligned16(state) && state_stride_slot % 4 == 0 && qkv_stride_b >= 2 * key_heads * key_dim + value_heads * value_dim,
+             "gated_delta_step: state must be 16-byte aligned and qkv rows complete");
+  DeltaParams p{};
+  p.qkv = qkv;
+  p.qkv_sb = qkv_stride_b;
+  p.a = a;
+  p.bb = b;
+  p.ab_dtype = ab_dtype;
+  p.ab_sb = ab_stride_b;
+  p.a_log = a_log;
+  p.dt_bias = dt_bias;
+  p.state_in = state;
+  p.state_out = state;
+  p.state_sb = state_stride_slot;
+  p.slots = slots;
+  p.slots_i64 = slots_dtype == QA_I64;
+  p.out = out;
+  p.out_dtype = out_dtype;
+  p.out_sb = out_stride_b;
+  p.B = batch;
+  p.S = 1;
+  p.H = value_heads;
+  p.Hqk = key_heads;
+  p.dk = key_dim;
+  p.dv = value_dim;
+  hipLaunchKernelGGL(delta_recurrent_128<true>, dim3(static_cast<unsigned>(batch * value_heads)), dim3(256), 0, stream, p);
+  return check_launch("delta_recurrent_128(fused step)");
+}

@@ -76,6 +76,26 @@ SIGNATURES: dict[str, tuple[Any, list[Any]]] = {
         [ctypes.POINTER(PagedKV), c_int32, c_int64, c_void_p, c_int32, c_int64, c_int64, c_int64, c_int32, c_void_p, c_void_p,
          c_void_p],
     ),
+    "qa_causal_conv1d_prefill": (
+        c_int32,
+        [c_void_p, c_int32, c_int64, c_int64, c_void_p, c_void_p, c_int64, c_void_p, c_int32, c_void_p, c_int64, c_int64, c_int32,
+         c_int32, c_void_p, c_int32, c_int64, c_int64, c_int32, c_void_p],
+    ),
+    "qa_causal_conv1d_update": (
+        c_int32,
+        [c_void_p, c_int32, c_int64, c_void_p, c_int64, c_void_p, c_int32, c_void_p, c_int64, c_int32, c_int32, c_void_p, c_int32,
+         c_int64, c_int32, c_void_p],
+    ),
+    "qa_linear_attention_recurrent_core": (
+        c_int32,
+        [c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_int64, c_int32, c_int64, c_int32, c_int32,
+         c_void_p],
+    ),
+    "qa_gated_delta_step": (
+        c_int32,
+        [c_void_p, c_int64, c_void_p, c_void_p, c_int32, c_int64, c_void_p, c_void_p, c_void_p, c_int64, c_void_p, c_int32, c_void_p,
+         c_int32, c_int64, c_int64, c_int32, c_int32, c_int32, c_int32, c_void_p],
+    ),
 }
 
 

@@ -362,3 +362,171 @@ def paged_kv_gather(key_pool: torch.Tensor, value_pool: torch.Tensor, block_tabl
     )
     L.check(lib, status, "paged_kv_gather")
     return key_out, value_out
+
+
+# --------------------------------------------------------------------------- gated delta rule
+
+
+def _f32_contig(tensor: torch.Tensor, name: str, device: torch.device) -> torch.Tensor:
+    _require_cuda(tensor, name, device)
+    _require(tensor.dtype == torch.float32, f"{name} must be float32")
+    return tensor.contiguous()
+
+
+def linear_attention_recurrent_core(query: torch.Tensor, key: torch.Tensor, value: torch.Tensor, g: torch.Tensor, beta: torch.Tensor, initial_state: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
+    """Token-serial gated delta rule on prepared inputs.
+
+    ``query``/``key`` ``(B, H, S, dk)``, ``value`` ``(B, H, S, dv)``,
+    ``g``/``beta`` ``(B, H, S)``, ``initial_state`` ``(B, H, dk, dv)``, all
+    float32 (already L2-normalised and scaled, ``src/tp_runtime.py:2790-2805``).
+    Returns ``(output (B, H, S, dv), final_state)`` fp32.  Reference:
+    ``src/fp8_cuda.py:206-214`` -> ``src/csrc/fp8_linear_cuda.cu:2491-2573``.
+    """
+    lib = L.load_library()
+    _require_cuda(query, "query")
+    device = query.device
+    q = _f32_contig(query, "query", device)
+    k = _f32_contig(key, "key", device)
+    v = _f32_contig(value, "value", device)
+    gg = _f32_contig(g, "g", device)
+    bb = _f32_contig(beta, "beta", device)
+    s0 = _f32_contig(initial_state, "initial_state", device)
+    _require(q.dim() == 4, "query must have shape [batch, heads, seq_len, key_dim]")
+    _require(k.dim() == 4, "key must have shape [batch, heads, seq_len, key_dim]")
+    _require(v.dim() == 4, "value must have shape [batch, heads, seq_len, value_dim]")
+    _require(gg.dim() == 3, "g must have shape [batch, heads, seq_len]")
+    _require(bb.dim() == 3, "beta must have shape [batch, heads, seq_len]")
+    _require(s0.dim() == 4, "initial_state must have shape [batch, heads, key_dim, value_dim]")
+    batch, heads, seq, key_dim = q.shape
+    value_dim = v.shape[3]
+    _require(batch > 0 and heads > 0 and seq > 0 and key_dim > 0 and value_dim > 0, "seq_len must be positive and fit int32")
+    _require(k.shape == q.shape, "key shape must match query shape")
+    _require(tuple(v.shape[:3]) == (batch, heads, seq), "value batch/head/seq must match query")
+    _require(tuple(gg.shape) == (batch, heads, seq), "g shape must match [batch, heads, seq_len]")
+    _require(tuple(bb.shape) == (batch, heads, seq), "beta shape must match [batch, heads, seq_len]")
+    _require(tuple(s0.shape[:2]) == (batch, heads), "initial_state batch/head must match query")
+    _require(tuple(s0.shape[2:]) == (key_dim, value_dim), "initial_state key/value dims must match query/value")
+    out = torch.empty((batch, heads, seq, value_dim), dtype=torch.float32, device=device)
+    final = torch.empty_like(s0)
+    status = lib.qa_linear_attention_recurrent_core(
+        _ptr(q), _ptr(k), _ptr(v), _ptr(gg), _ptr(bb), _ptr(s0), _ptr(out), _ptr(final), batch, heads, seq, key_dim, value_dim, _stream(device)
+    )
+    L.check(lib, status, "linear_attention_recurrent_core")
+    return out, final
+
+
+def _conv_weight(weight: torch.Tensor, channels: int, device: torch.device) -> torch.Tensor:
+    _require_cuda(weight, "conv weight", device)
+    w = weight.reshape(weight.shape[0], weight.shape[-1]).float().contiguous()
+    _require(w.shape[0] == channels, "conv weight must have one row per channel")
+    return w
+
+
+def causal_conv1d_prefill(
+    x: torch.Tensor, weight: torch.Tensor, conv_state: torch.Tensor | None = None, *, apply_silu: bool = True, out_dtype: torch.dtype = torch.float32
+) -> tuple[torch.Tensor, torch.Tensor]:
+    """Depthwise causal conv1d (+SiLU) over a token-major ``(B, T, C)`` input.
+
+    ``conv_state`` ``(B, C, K-1)`` holds the previous K-1 inputs (zeros when
+    None).  Returns ``(out (B, T, C), new_state (B, C, K-1))``; the math is the
+    fp32 ``F.conv1d`` of ``src/reference_ops.py:245-258``.
+    """
+    lib = L.load_library()
+    _require_cuda(x, "x")
+    device = x.device
+    _require(x.dim() == 3 and x.stride(-1) == 1, "x must be (batch, seq, channels) with contiguous channels")
+    _float_dtype(x, "x")
+    batch, seq, channels = x.shape
+    w = _conv_weight(weight, channels, device)
+    kernel = w.shape[1]
+    state_in = None
+    if conv_state is not None:
+        state_in = _f32_contig(conv_state, "conv_state", device)
+        _require(tuple(state_in.shape) == (batch, channels, kernel - 1), "conv_state must be (batch, channels, kernel-1)")
+    new_state = torch.empty((batch, channels, kernel - 1), dtype=torch.float32, device=device)
+    out = torch.empty((batch, seq, channels), dtype=out_dtype, device=device)
+    status = lib.qa_causal_conv1d_prefill(
+        _ptr(x), _code(x), x.stride(0), x.stride(1), _ptr(state_in), _ptr(new_state), channels * (kernel - 1), ctypes.c_void_p(0), L.QA_I32,
+        _ptr(w), batch, seq, channels, kernel, _ptr(out), _code(out), out.stride(0), out.stride(1), int(apply_silu), _stream(device),
+    )
+    L.check(lib, status, "causal_conv1d_prefill")
+    return out, new_state
+
+
+def causal_conv1d_update(x: torch.Tensor, conv_state: torch.Tensor, weight: torch.Tensor, slots: torch.Tensor | None = None, *, apply_silu: bool = True) -> torch.Tensor:
+    """One token ``x`` ``(B, C)`` through the conv; ``conv_state`` ``(rows, C, K-1)`` updated in place.
+
+    Row ``b`` uses state row ``slots[b]`` (or ``b``).  Returns fp32 ``(B, C)``.
+    """
+    lib = L.load_library()
+    _require_cuda(x, "x")
+    device = x.device
+    _require(x.dim() == 2 and x.stride(-1) == 1, "x must be (batch, channels)")
+    _float_dtype(x, "x")
+    batch, channels = x.shape
+    w = _conv_weight(weight, channels, device)
+    kernel = w.shape[1]
+    _require_cuda(conv_state, "conv_state", device)
+    _require(conv_state.dtype == torch.float32 and conv_state.is_contiguous(), "conv_state must be contiguous float32")
+    _require(tuple(conv_state.shape[1:]) == (channels, kernel - 1), "conv_state must be (rows, channels, kernel-1)")
+    slot_ptr, slot_code = ctypes.c_void_p(0), L.QA_I32
+    if slots is not None:
+        _require_cuda(slots, "slots", device)
+        _index_dtype(slots, "slots")
+        slots = slots.contiguous()
+        slot_ptr, slot_code = _ptr(slots), _code(slots)
+    out = torch.empty((batch, channels), dtype=torch.float32, device=device)
+    status = lib.qa_causal_conv1d_update(
+        _ptr(x), _code(x), x.stride(0), _ptr(conv_state), channels * (kernel - 1), slot_ptr, slot_code, _ptr(w), batch, channels, kernel,
+        _ptr(out), L.QA_F32, out.stride(0), int(apply_silu), _stream(device),
+    )
+    L.check(lib, status, "causal_conv1d_update")
+    return out
+
+
+def gated_delta_step(
+    qkv: torch.Tensor,
+    a: torch.Tensor,
+    b: torch.Tensor,
+    a_log: torch.Tensor,
+    dt_bias: torch.Tensor,
+    state: torch.Tensor,
+    *,
+    key_heads: int,
+    slots: torch.Tensor | None = None,
+    out_dtype: torch.dtype = torch.bfloat16,
+) -> torch.Tensor:
+    """Fused single-token recurrence of a linear-attention layer.
+
+    ``qkv`` ``(B, 2*Hqk*dk + Hv*dv)`` fp32 is the conv+SiLU output; ``a``/``b``
+    ``(B, Hv)`` the raw ``in_proj_a``/``in_proj_b`` outputs; ``state``
+    ``(slots, Hv, dk, dv)`` fp32 is updated in place at ``slots[b]`` (or ``b``).
+    Returns ``(B, Hv, dv)`` in ``out_dtype``.  Follows
+    ``src/reference_ops.py:271-283,291-322`` for one token.
+    """
+    lib = L.load_library()
+    _require_cuda(qkv, "qkv")
+    device = qkv.device
+    _require(qkv.dtype == torch.float32 and qkv.dim() == 2 and qkv.stride(-1) == 1, "qkv must be (batch, channels) float32")
+    _require_cuda(state, "state", device)
+    _require(state.dtype == torch.float32 and state.dim() == 4 and state.is_contiguous(), "state must be contiguous (slots, Hv, dk, dv) float32")
+    _, value_heads, key_dim, value_dim = state.shape
+    batch = qkv.shape[0]
+    _require(a.shape == (batch, value_heads) and b.shape == (batch, value_heads), "a/b must be (batch, value_heads)")
+    _require(a.dtype == b.dtype and a.dtype in (torch.float32, torch.bfloat16), "a/b must share a float32/bfloat16 dtype")
+    a_c, b_c = a.contiguous(), b.contiguous()
+    alog = _f32_contig(a_log.reshape(-1), "a_log", device)
+    dtb = _f32_contig(dt_bias.reshape(-1), "dt_bias", device)
+    slot_ptr, slot_code = ctypes.c_void_p(0), L.QA_I32
+    if slots is not None:
+        _require_cuda(slots, "slots", device)
+        _index_dtype(slots, "slots")
+        slots = slots.contiguous()
+        slot_ptr, slot_code = _ptr(slots), _code(slots)
+    out = torch.empty((batch, value_heads, value_dim), dtype=out_dtype, device=device)
+    status = lib.qa_gated_delta_step(
+        _ptr(qkv), qkv.stride(0), _ptr(a_c), _ptr(b_c), _code(a_c), a_c.stride(0), _ptr(alog), _ptr(dtb), _ptr(state), state.stride(0),
+        slot_ptr, slot_code, _ptr(out), _code(out), out.stride(0), batch, int(key_heads), value_heads, key_dim, value_dim, _stream(device),
+    )
+    L.check(lib, status, "gated_delta_step")
+    return out

@@ -1,0 +1,161 @@
+"""GPU parity of the gated delta-rule kernels against ``oracle/gated_delta.py``.
+
+Tolerances: fp32 recurrent states within 1e-3 relative (Frobenius), bf16
+outputs within 2e-2 absolute/relative; the restated reference test keeps its
+own 2e-5 (``tests/unit/test_fp8_cuda.py:999-1029``).
+"""
+
+from __future__ import annotations
+
+import pytest
+import torch
+
+from oracle import gated_delta as gd
+
+pytestmark = pytest.mark.gpu
+
+DEV = "cuda:0"
+
+
+def _ops():
+    import hip_ops
+
+    return hip_ops
+
+
+def _rel(a: torch.Tensor, b: torch.Tensor) -> float:
+    a = a.detach().double().cpu()
+    b = b.detach().double().cpu()
+    return float((a - b).norm() / b.norm().clamp_min(1e-30))
+
+
+def test_recurrent_core_matches_reference_small_shapes() -> None:
+    # tests/unit/test_fp8_cuda.py:999-1029 (seed 2, B2 H3 dk4 dv5)
+    ops = _ops()
+    torch.manual_seed(2)
+    for seq_len, use_state in ((1, False), (1, True), (5, False), (5, True)):
+        b, h, dk, dv = 2, 3, 4, 5
+        q_raw = torch.randn((b, seq_len, h, dk))
+        k_raw = torch.randn((b, seq_len, h, dk))
+        v_raw = torch.randn((b, seq_len, h, dv))
+        g_raw = -torch.rand((b, seq_len, h))
+        beta_raw = torch.rand((b, seq_len, h))
+        state0 = torch.randn((b, h, dk, dv)) * 0.1 if use_state else None
+        q, k, v, g, beta, state = gd.prepare_inputs(q_raw, k_raw, v_raw, g_raw, beta_raw, state0)
+        out, final = ops.linear_attention_recurrent_core(*(x.to(DEV) for x in (q, k, v, g, beta, state)))
+        ref_out, ref_state = gd.recurrent_core(q, k, v, g, beta, state)
+        torch.testing.assert_close(out.cpu(), ref_out, atol=2e-5, rtol=2e-5)
+        torch.testing.assert_close(final.cpu(), ref_state, atol=2e-5, rtol=2e-5)
+
+
+def test_recurrent_core_rejects_bf16() -> None:
+    ops = _ops()
+    x = torch.zeros((1, 1, 1, 4), device=DEV, dtype=torch.bfloat16)
+    with pytest.raises(RuntimeError, match="query must be float32"):
+        ops.linear_attention_recurrent_core(x, x, x, x[..., 0], x[..., 0], torch.zeros((1, 1, 4, 4), device=DEV))
+
+
+def test_recurrent_core_128_register_path_matches_oracle() -> None:
+    ops = _ops()
+    gen = torch.Generator().manual_seed(31)
+    b, h, s, d = 2, 4, 37, 128
+    q_raw = torch.randn(b, s, h, d, generator=gen)
+    k_raw = torch.randn(b, s, h, d, generator=gen)
+    v_raw = torch.randn(b, s, h, d, generator=gen)
+    g_raw = -torch.rand(b, s, h, generator=gen)
+    beta_raw = torch.rand(b, s, h, generator=gen)
+    state0 = torch.randn(b, h, d, d, generator=gen) * 0.1
+    q, k, v, g, beta, state = gd.prepare_inputs(q_raw, k_raw, v_raw, g_raw, beta_raw, state0)
+    out, final = ops.linear_attention_recurrent_core(*(x.to(DEV) for x in (q, k, v, g, beta, state)))
+    ref_out, ref_state = gd.recurrent_core(q, k, v, g, beta, state)
+    assert _rel(final, ref_state) < 1e-5
+    assert _rel(out, ref_out) < 1e-5
+
+
+def test_conv1d_prefill_matches_oracle_with_and_without_state() -> None:
+    ops = _ops()
+    gen = torch.Generator().manual_seed(32)
+    b, t, c, kk = 3, 19, 300, 4
+    x = torch.randn(b, t, c, generator=gen).to(torch.bfloat16)
+    w = torch.randn(c, 1, kk, generator=gen)
+    tail = torch.randn(b, c, kk - 1, generator=gen)
+    for state in (None, tail):
+        ref, ref_tail = gd.causal_conv1d(x.transpose(1, 2).float(), w, state)
+        out, new_tail = ops.causal_conv1d_prefill(x.to(DEV), w.to(DEV), None if state is None else state.to(DEV))
+        torch.testing.assert_close(out.cpu(), ref.transpose(1, 2), atol=1e-5, rtol=1e-5)
+        torch.testing.assert_close(new_tail.cpu(), ref_tail, atol=0, rtol=0)
+
+
+def test_conv1d_update_streams_like_prefill_with_slots() -> None:
+    ops = _ops()
+    gen = torch.Generator().manual_seed(33)
+    b, t, c, kk = 2, 6, 130, 4
+    x = torch.randn(b, t, c, generator=gen)
+    w = torch.randn(c, kk, generator=gen)
+    full, _ = gd.causal_conv1d(x.transpose(1, 2), w, None)
+    pool = torch.zeros(5, c, kk - 1, device=DEV)
+    slots = torch.tensor([3, 1], device=DEV, dtype=torch.int32)
+    outs = []
+    for step in range(t):
+        outs.append(ops.causal_conv1d_update(x[:, step].contiguous().to(DEV), pool, w.to(DEV), slots).cpu())
+    torch.testing.assert_close(torch.stack(outs, dim=1), full.transpose(1, 2), atol=1e-5, rtol=1e-5)
+    torch.testing.assert_close(pool[3].cpu(), x[0, -3:].T.contiguous(), atol=0, rtol=0)
+    assert torch.count_nonzero(pool[0]) == 0
+
+
+def _layer_inputs(seed: int, batch: int, seq: int, shape: gd.LinearShape):
+    gen = torch.Generator().manual_seed(seed)
+    mixed = torch.randn(batch, seq, shape.qkv_dim, generator=gen).to(torch.bfloat16)
+    a = torch.randn(batch, seq, shape.value_heads, generator=gen)
+    b = torch.randn(batch, seq, shape.value_heads, generator=gen)
+    a_log = torch.randn(shape.value_heads, generator=gen) * 0.5
+    dt_bias = torch.randn(shape.value_heads, generator=gen) * 0.5
+    w = torch.randn(shape.qkv_dim, 1, shape.conv_kernel_dim, generator=gen) * 0.5
+    return mixed, a, b, a_log, dt_bias, w
+
+
+def test_fused_decode_steps_match_oracle_layer_core() -> None:
+    """T decode steps (conv update + fused step) == the reference layer core over T tokens."""
+    ops = _ops()
+    shape = gd.LinearShape(key_heads=4, value_heads=8, key_head_dim=128, value_head_dim=128, conv_kernel_dim=4)
+    batch, seq = 3, 6
+    mixed, a, b, a_log, dt_bias, w = _layer_inputs(34, batch, seq, shape)
+    gen = torch.Generator().manual_seed(35)
+    state0 = torch.randn(batch, shape.value_heads, 128, 128, generator=gen) * 0.05
+    tail0 = torch.randn(batch, shape.qkv_dim, 3, generator=gen)
+    ref_core, ref_state, ref_tail = gd.linear_attention_core(mixed.float(), a, b, a_log, dt_bias, w, shape, conv_tail=tail0, initial_state=state0)
+    slots = torch.tensor([4, 0, 2], device=DEV)
+    state_pool = torch.zeros(5, shape.value_heads, 128, 128, device=DEV)
+    conv_pool = torch.zeros(5, shape.qkv_dim, 3, device=DEV)
+    state_pool[slots] = state0.to(DEV)
+    conv_pool[slots] = tail0.to(DEV)
+    outs = []
+    for step in range(seq):
+        act = ops.causal_conv1d_update(mixed[:, step].contiguous().to(DEV), conv_pool, w.to(DEV), slots)
+        outs.append(
+            ops.gated_delta_step(
+                act, a[:, step].contiguous().to(DEV), b[:, step].contiguous().to(DEV), a_log.to(DEV), dt_bias.to(DEV), state_pool,
+                key_heads=shape.key_heads, slots=slots, out_dtype=torch.float32,
+            ).cpu()
+        )
+    core = torch.stack(outs, dim=1)
+    assert _rel(state_pool[slots], ref_state) < 1e-3
+    torch.testing.assert_close(core, ref_core, atol=2e-3, rtol=2e-3)
+    torch.testing.assert_close(conv_pool[slots].cpu(), ref_tail, atol=0, rtol=0)
+    assert torch.count_nonzero(state_pool[1]) == 0 and torch.count_nonzero(state_pool[3]) == 0
+
+
+def test_fused_step_bf16_output_and_bf16_gates() -> None:
+    ops = _ops()
+    shape = gd.LinearShape(key_heads=16, value_heads=32, key_head_dim=128, value_head_dim=128, conv_kernel_dim=4)
+    batch = 4
+    mixed, a, b, a_log, dt_bias, w = _layer_inputs(36, batch, 1, shape)
+    ref_core, ref_state, _ = gd.linear_attention_core(mixed.float(), a.to(torch.bfloat16).float(), b.to(torch.bfloat16).float(), a_log, dt_bias, w, shape)
+    act = ops.causal_conv1d_update(mixed[:, 0].contiguous().to(DEV), torch.zeros(batch, shape.qkv_dim, 3, device=DEV), w.to(DEV))
+    state = torch.zeros(batch, 32, 128, 128, device=DEV)
+    out = ops.gated_delta_step(
+        act, a[:, 0].to(torch.bfloat16).to(DEV), b[:, 0].to(torch.bfloat16).to(DEV), a_log.to(DEV), dt_bias.to(DEV), state, key_heads=16
+    )
+    assert out.dtype == torch.bfloat16
+    torch.testing.assert_close(out.cpu().float(), ref_core[:, 0].float(), atol=2e-2, rtol=2e-2)
+    assert _rel(state, ref_state) < 1e-3
