@@ -1,0 +1,585 @@
+// Chunked gated delta-rule prefill for gfx950 (dk = dv = 128, conv kernel 4,
+// chunk 64), with the conv1d + SiLU + L2-norm + gating prologue fused in.
+//
+// Algorithm (per sequence and value head; chunk of C tokens, initial state S0,
+// cumulative log-decay G inside the chunk, gamma = exp(G)) -- the WY/UT form of
+// Yang et al., "Gated Delta Networks" (ICLR 2025):
+//   A[i][l]  = beta_i exp(G_i - G_l) (k_i . k_l)         l < i
+//   T        = (I + A)^-1                                 (unit lower triangular)
+//   W        = T (beta*gamma*K),  U = T (beta*V)
+//   delta    = U - W S0
+//   O        = gamma * (Q S0) + Aqk delta,  Aqk[i][l] = exp(G_i - G_l) (q_i . k_l), l <= i
+//   S_end    = gamma_C S0 + K^T (exp(G_C - G) * delta)
+// which equals the per-token recurrence of src/reference_ops.py:310-318.
+//
+// Mapping: one workgroup (8 waves) per (batch row, value head, half of dv);
+// chunks run in order, the fp32 state slice S[dk][dv/2] stays in registers.
+// Matrix products use v_mfma_f32_16x16x32_f16 on 16x16 output tiles with fp16
+// operands in LDS (fp32 accumulation).  Every LDS operand is stored "K-major"
+// (the reduction axis contiguous); an output is written in whichever
+// orientation its consumer needs by choosing C or C^T (swapped operands).
+// T is computed in fp32 (blocked 16x16 inverse) and fed to the MFMA as a
+// hi + lo fp16 pair, keeping the state update within fp32-state tolerance.
+#include "qa_common.h"
+
+namespace qa {
+
+typedef _Float16 half_t;
+typedef __attribute__((__vector_size__(8 * sizeof(_Float16)))) _Float16 f16x8_v;
+typedef __attribute__((__vector_size__(4 * sizeof(_Float16)))) _Float16 f16x4_v;
+typedef float cfloat4 __attribute__((ext_vector_type(4)));
+
+namespace cgd {
+
+constexpr int CH = 64;      // tokens per chunk
+constexpr int DK = 128;
+constexpr int DV = 128;
+constexpr int DVS = 64;     // dv columns per workgroup
+constexpr int NW = 8;       // waves per workgroup
+constexpr int NT = NW * 64;
+constexpr int KCONV = 4;
+constexpr int LD128 = 136;  // padded leading dims (halfs) of 128- and 64-wide fp16 tiles
+constexpr int LD64 = 72;
+constexpr int LDF = 65;     // fp32 64x64 leading dim
+
+// LDS layout (bytes)
+constexpr int OFF_R1 = 0;                               // Qs | Ks   -> later Wn | T16hi | T16lo
+constexpr int OFF_QS = OFF_R1;
+constexpr int OFF_KS = OFF_R1 + CH * LD128 * 2;
+constexpr int OFF_WN = OFF_R1;
+constexpr int OFF_THI = OFF_R1 + CH * LD128 * 2;
+constexpr int OFF_TLO = OFF_THI + CH * LD64 * 2;
+constexpr int SZ_R1 = CH * LD128 * 2 + 2 * CH * LD64 * 2;  // 35840 >= 2 * 17408
+constexpr int OFF_R2 = OFF_R1 + SZ_R1;                  // Vstage | Amat | Tb  -> later Dt | DDt
+constexpr int OFF_VST = OFF_R2;
+constexpr int OFF_AM = OFF_R2;
+constexpr int OFF_TB = OFF_R2 + CH * LDF * 4;
+constexpr int OFF_DT = OFF_R2;
+constexpr int OFF_DDT = OFF_R2 + DVS * LD64 * 2;
+constexpr int SZ_R2 = 2 * CH * LDF * 4;                 // 33280
+constexpr int OFF_KT = OFF_R2 + SZ_R2;                  // Kt [dk][tok]
+constexpr int OFF_XT = OFF_KT + DK * LD64 * 2;          // Xt [dk][tok] = beta*gamma*K^T
+constexpr int OFF_YT = OFF_XT + DK * LD64 * 2;          // Yt [dv][tok] = beta*V^T
+constexpr int OFF_ST = OFF_YT + DVS * LD64 * 2;         // St [dv][dk] (fp16 state)
+constexpr int OFF_AQK = OFF_ST + DVS * LD128 * 2;       // Aqk [i][l]
+constexpr int OFF_SC = OFF_AQK + CH * LD64 * 2;         // scalars
+constexpr int OFF_WCONV = OFF_SC + 4 * CH * 4;          // conv weights of this workgroup's 320 channels
+constexpr int NCH = 2 * DK + DVS;                       // 320
+constexpr int LDS_BYTES = OFF_WCONV + NCH * KCONV * 4;
+
+static_assert(CH * LD128 * 2 * 2 <= SZ_R1, "R1 too small for Qs|Ks");
+static_assert(CH * LDF * 4 <= SZ_R2, "R2 too small for Vstage");
+static_assert(2 * DVS * LD64 * 2 <= SZ_R2, "R2 too small for Dt|DDt");
+static_assert(LDS_BYTES <= 160 * 1024, "LDS budget");
+
+struct Params {
+  const void* x;  // (B, T, C) mixed qkv
+  int x_dtype;
+  int64_t x_sb, x_st;
+  const void* a;
+  const void* bb;
+  int ab_dtype;
+  int64_t ab_sb, ab_st;
+  const float* a_log;
+  const float* dt_bias;
+  const float* conv_w;  // (C, 4)
+  const float* conv_in;   // (B, C, 3) or null
+  float* conv_out;        // (B, C, 3) or null
+  const float* state_in;  // (B, Hv, dk, dv) or null
+  float* state_out;       // (B, Hv, dk, dv) or null
+  void* out;
+  int out_dtype;
+  int64_t out_sb, out_st;
+  int64_t T;
+  int Hqk, Hv, C;
+};
+
+__device__ __forceinline__ float load_x(const Params& p, int64_t i) {
+  return p.x_dtype == QA_BF16 ? bf16_to_f32(reinterpret_cast<const bf16_t*>(p.x)[i]) : reinterpret_cast<const float*>(p.x)[i];
+}
+
+__device__ __forceinline__ float load_ab(const void* base, int dtype, int64_t i) {
+  return dtype == QA_BF16 ? bf16_to_f32(reinterpret_cast<const bf16_t*>(base)[i]) : reinterpret_cast<const float*>(base)[i];
+}
+
+// C(16x16) += A(16 x K) * B(K x 16); A stored [m][k] (lda), B stored [n][k] (ldb), fp16.
+// Lane l gets C[4(l/16) + r][l % 16].
+template <int K>
+__device__ __forceinline__ cfloat4 mma(const half_t* A, int lda, const half_t* B, int ldb, cfloat4 acc, int lane) {
+  const int row = lane & 15;
+  const int kq = lane >> 4;
+#pragma unroll
+  for (int k0 = 0; k0 < K; k0 += 32) {
+    const f16x8_v av = *reinterpret_cast<const f16x8_v*>(A + row * lda + k0 + 8 * kq);
+    const f16x8_v bv = *reinterpret_cast<const f16x8_v*>(B + row * ldb + k0 + 8 * kq);
+    acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, bv, acc, 0, 0, 0);
+  }
+  return acc;
+}
+
+__device__ __forceinline__ void store4h(half_t* dst, float a, float b, float c, float d) {
+  f16x4_v v;
+  v[0] = static_cast<half_t>(a);
+  v[1] = static_cast<half_t>(b);
+  v[2] = static_cast<half_t>(c);
+  v[3] = static_cast<half_t>(d);
+  *reinterpret_cast<f16x4_v*>(dst) = v;
+}
+
+__device__ __forceinline__ float softplus_ref(float x) { return x > 20.f ? x : log1pf(__expf(x)); }
+__device__ __forceinline__ float silu_ref(float x) { return x / (1.f + __expf(-x)); }
+
+__global__ __launch_bounds__(NT) void chunk_kernel(Params p) {
+  extern __shared__ __align__(16) unsigned char smem[];
+  half_t* Qs = reinterpret_cast<half_t*>(smem + OFF_QS);
+  half_t* Ks = reinterpret_cast<half_t*>(smem + OFF_KS);
+  half_t* Wn = reinterpret_cast<half_t*>(smem + OFF_WN);
+  half_t* Thi = reinterpret_cast<half_t*>(smem + OFF_THI);
+  half_t* Tlo = reinterpret_cast<half_t*>(smem + OFF_TLO);
+  float* Vst = reinterpret_cast<float*>(smem + OFF_VST);
+  float* Am = reinterpret_cast<float*>(smem + OFF_AM);
+  float* Tb = reinterpret_cast<float*>(smem + OFF_TB);
+  half_t* Dt = reinterpret_cast<half_t*>(smem + OFF_DT);
+  half_t* DDt = reinterpret_cast<half_t*>(smem + OFF_DDT);
+  half_t* Kt = reinterpret_cast<half_t*>(smem + OFF_KT);
+  half_t* Xt = reinterpret_cast<half_t*>(smem + OFF_XT);
+  half_t* Yt = reinterpret_cast<half_t*>(smem + OFF_YT);
+  half_t* St = reinterpret_cast<half_t*>(smem + OFF_ST);
+  half_t* Aqk = reinterpret_cast<half_t*>(smem + OFF_AQK);
+  float* s_beta = reinterpret_cast<float*>(smem + OFF_SC);
+  float* s_G = s_beta + CH;
+  float* s_gam = s_G + CH;
+  float* s_misc = s_gam + CH;
+  float* wconv = reinterpret_cast<float*>(smem + OFF_WCONV);
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int half_id = blockIdx.x & 1;
+  const int j = (blockIdx.x >> 1) % p.Hv;           // value head
+  const int64_t b = (blockIdx.x >> 1) / p.Hv;       // batch row
+  const int qh = j / (p.Hv / p.Hqk);                // key head of this value head
+  const int q_ch0 = qh * DK;
+  const int k_ch0 = p.Hqk * DK + qh * DK;
+  const int v_ch0 = 2 * p.Hqk * DK + j * DV + half_id * DVS;
+  const int lq = lane >> 4;  // quad of the MFMA output layout
+  const int lc = lane & 15;  // column of the MFMA output layout
+
+  // conv weights of the 320 channels this workgroup uses: [q 128 | k 128 | v 64]
+  for (int idx = tid; idx < NCH * KCONV; idx += NT) {
+    const int lch = idx / KCONV;
+    const int tap = idx - lch * KCONV;
+    const int ch = lch < DK ? q_ch0 + lch : lch < 2 * DK ? k_ch0 + (lch - DK) : v_ch0 + (lch - 2 * DK);
+    wconv[idx] = p.conv_w[static_cast<int64_t>(ch) * KCONV + tap];
+  }
+
+  // state slice S[dk][dv] in registers: wave w owns tiles (tk, tv) = (w, 0..3)
+  cfloat4 S[4];
+  const float* s_in = p.state_in == nullptr ? nullptr : p.state_in + ((b * p.Hv + j) * DK) * DV + half_id * DVS;
+#pragma unroll
+  for (int tv = 0; tv < 4; ++tv) {
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int dk = 16 * wave + 4 * lq + r;
+      const int dv = 16 * tv + lc;
+      S[tv][r] = s_in == nullptr ? 0.f : s_in[static_cast<int64_t>(dk) * DV + dv];
+    }
+    store4h(St + (16 * tv + lc) * LD128 + 16 * wave + 4 * lq, S[tv][0], S[tv][1], S[tv][2], S[tv][3]);
+  }
+  const float alog = -__expf(p.a_log[j]);
+  const float dtb = p.dt_bias[j];
+  __syncthreads();
+
+  const int64_t nchunks = (p.T + CH - 1) / CH;
+  for (int64_t ci = 0; ci < nchunks; ++ci) {
+    const int64_t t0 = ci * CH;
+
+    // ---------------- prologue: conv + SiLU + L2 norm (q, k), conv + SiLU (v), gating
+    {
+      const int tok = tid >> 3;
+      const int grp = tid & 7;  // 0-3: q channels 32*grp, 4-7: k channels 32*(grp-4)
+      const int64_t tg = t0 + tok;
+      const int lch0 = grp < 4 ? 32 * grp : DK + 32 * (grp - 4);
+      const int ch0 = grp < 4 ? q_ch0 + 32 * grp : k_ch0 + 32 * (grp - 4);
+      float y[32];
+#pragma unroll
+      for (int c = 0; c < 32; ++c) y[c] = 0.f;
+      if (tg < p.T) {
+#pragma unroll
+        for (int tap = 0; tap < KCONV; ++tap) {
+          const int64_t ts = tg - (KCONV - 1) + tap;
+          if (ts >= 0) {
+#pragma unroll
+            for (int c = 0; c < 32; ++c) y[c] += wconv[(lch0 + c) * KCONV + tap] * load_x(p, b * p.x_sb + ts * p.x_st + ch0 + c);
+          } else if (p.conv_in != nullptr) {
+#pragma unroll
+            for (int c = 0; c < 32; ++c)
+              y[c] += wconv[(lch0 + c) * KCONV + tap] * p.conv_in[(b * p.C + ch0 + c) * (KCONV - 1) + (KCONV - 1) + ts];
+          }
+        }
+      }
+      float ss = 0.f;
+#pragma unroll
+      for (int c = 0; c < 32; ++c) {
+        y[c] = silu_ref(y[c]);
+        ss += y[c] * y[c];
+      }
+      ss += __shfl_xor(ss, 1, 64);
+      ss += __shfl_xor(ss, 2, 64);
+      const float scale = rsqrtf(ss + 1e-6f) * (grp < 4 ? rsqrtf(static_cast<float>(DK)) : 1.f);
+      half_t* dst = (grp < 4 ? Qs + tok * LD128 + 32 * grp : Ks + tok * LD128 + 32 * (grp - 4));
+#pragma unroll
+      for (int c = 0; c < 32; c += 4) store4h(dst + c, y[c] * scale, y[c + 1] * scale, y[c + 2] * scale, y[c + 3] * scale);
+    }
+    if (tid < 2 * CH) {
+      const int tok = tid >> 1;
+      const int vg = tid & 1;
+      const int64_t tg = t0 + tok;
+      const int lch0 = 2 * DK + 32 * vg;
+      const int ch0 = v_ch0 + 32 * vg;
+      float y[32];
+#pragma unroll
+      for (int c = 0; c < 32; ++c) y[c] = 0.f;
+      if (tg < p.T) {
+#pragma unroll
+        for (int tap = 0; tap < KCONV; ++tap) {
+          const int64_t ts = tg - (KCONV - 1) + tap;
+          if (ts >= 0) {
+#pragma unroll
+            for (int c = 0; c < 32; ++c) y[c] += wconv[(lch0 + c) * KCONV + tap] * load_x(p, b * p.x_sb + ts * p.x_st + ch0 + c);
+          } else if (p.conv_in != nullptr) {
+#pragma unroll
+            for (int c = 0; c < 32; ++c)
+              y[c] += wconv[(lch0 + c) * KCONV + tap] * p.conv_in[(b * p.C + ch0 + c) * (KCONV - 1) + (KCONV - 1) + ts];
+          }
+        }
+#pragma unroll
+        for (int c = 0; c < 32; ++c) y[c] = silu_ref(y[c]);
+      }
+#pragma unroll
+      for (int c = 0; c < 32; ++c) Vst[tok * LDF + 32 * vg + c] = y[c];
+    }
+    if (wave == NW - 1) {
+      // gating and the inclusive prefix sum of g over the chunk (src/reference_ops.py:271-275)
+      const int tok = lane;
+      const int64_t tg = t0 + tok;
+      float g = 0.f, beta = 0.f;
+      if (tg < p.T) {
+        const float av = load_ab(p.a, p.ab_dtype, b * p.ab_sb + tg * p.ab_st + j);
+        const float bv = load_ab(p.bb, p.ab_dtype, b * p.ab_sb + tg * p.ab_st + j);
+        g = alog * softplus_ref(av + dtb);
+        beta = 1.f / (1.f + __expf(-bv));
+      }
+      float G = g;
+#pragma unroll
+      for (int off = 1; off < 64; off <<= 1) {
+        const float up = __shfl_up(G, off, 64);
+        if (lane >= off) G += up;
+      }
+      s_beta[tok] = beta;
+      s_G[tok] = G;
+      s_gam[tok] = __expf(G);
+    }
+    __syncthreads();
+
+    // transposed, scaled copies: Kt = K^T, Xt = beta*gamma*K^T, Yt = beta*V^T
+    for (int idx = tid; idx < DK * (CH / 4); idx += NT) {
+      const int dk = idx >> 4;
+      const int tq = idx & 15;
+      float kv[4], xv[4];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int tok = 4 * tq + r;
+        kv[r] = static_cast<float>(Ks[tok * LD128 + dk]);
+        xv[r] = kv[r] * s_beta[tok] * s_gam[tok];
+      }
+      store4h(Kt + dk * LD64 + 4 * tq, kv[0], kv[1], kv[2], kv[3]);
+      store4h(Xt + dk * LD64 + 4 * tq, xv[0], xv[1], xv[2], xv[3]);
+    }
+    for (int idx = tid; idx < DVS * (CH / 4); idx += NT) {
+      const int dv = idx >> 4;
+      const int tq = idx & 15;
+      float yv[4];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int tok = 4 * tq + r;
+        yv[r] = Vst[tok * LDF + dv] * s_beta[tok];
+      }
+      store4h(Yt + dv * LD64 + 4 * tq, yv[0], yv[1], yv[2], yv[3]);
+    }
+    __syncthreads();
+
+    // ---------------- A = beta_i exp(G_i - G_l) K K^T (strictly lower), fp32
+    for (int tile = wave; tile < 16; tile += NW) {
+      const int ti = tile >> 2;
+      const int tl = tile & 3;
+      if (tl > ti) continue;
+      cfloat4 acc = {0.f, 0.f, 0.f, 0.f};
+      acc = mma<DK>(Ks + 16 * ti * LD128, LD128, Ks + 16 * tl * LD128, LD128, acc, lane);
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int i = 16 * ti + 4 * lq + r;
+        const int l = 16 * tl + lc;
+        Am[i * LDF + l] = l < i ? s_beta[i] * __expf(s_G[i] - s_G[l]) * acc[r] : 0.f;
+      }
+    }
+    __syncthreads();
+
+    // ---------------- wave 0: diagonal 16x16 blocks of T = (I + A)^-1 by column
+    // forward substitution; the other waves: Aqk and O^T = gamma * S0^T Q^T.
+    cfloat4 O[2];
+    if (wave == 0) {
+      const int qb = lane >> 4;
+      const int c = lane & 15;
+      float x[16];
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        float acc = i == c ? 1.f : 0.f;
+        const float* arow = Am + (16 * qb + i) * LDF + 16 * qb;
+#pragma unroll
+        for (int l = 0; l < i; ++l) acc -= arow[l] * x[l];
+        x[i] = acc;
+      }
+#pragma unroll
+      for (int i = 0; i < 16; ++i) Tb[(16 * qb + i) * LDF + 16 * qb + c] = x[i];
+    } else {
+      // Aqk[i][l] = exp(G_i - G_l) (q_i . k_l), l <= i, computed as (K Q^T)[l][i]
+      for (int tile = wave - 1; tile < 16; tile += NW - 1) {
+        const int tl = tile >> 2;
+        const int ti = tile & 3;
+        cfloat4 acc = {0.f, 0.f, 0.f, 0.f};
+        if (tl <= ti) acc = mma<DK>(Ks + 16 * tl * LD128, LD128, Qs + 16 * ti * LD128, LD128, acc, lane);
+        const int i = 16 * ti + lc;
+        float v[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int l = 16 * tl + 4 * lq + r;
+          v[r] = l <= i ? __expf(s_G[i] - s_G[l]) * acc[r] : 0.f;
+        }
+        store4h(Aqk + i * LD64 + 16 * tl + 4 * lq, v[0], v[1], v[2], v[3]);
+      }
+    }
+    // O^T tiles (dv tile td, token tile tt): tile index ot = 2*wave + s, two per wave
+#pragma unroll
+    for (int s = 0; s < 2; ++s) {
+      const int ot = 2 * wave + s;
+      const int td = ot >> 2;
+      const int tt = ot & 3;
+      cfloat4 acc = {0.f, 0.f, 0.f, 0.f};
+      acc = mma<DK>(St + 16 * td * LD128, LD128, Qs + 16 * tt * LD128, LD128, acc, lane);
+      const float gam = s_gam[16 * tt + lc];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) O[s][r] = acc[r] * gam;
+    }
+    __syncthreads();
+
+    // ---------------- off-diagonal blocks of T: T_pq = -D_p sum_{k=q}^{p-1} A_pk T_kq
+    // level d handles blocks (q + d, q); the partial sum M is parked in the
+    // unused upper block (q, p) of Tb.
+#pragma unroll
+    for (int d = 1; d <= 3; ++d) {
+      const int nblk = 4 - d;
+      for (int idx = tid; idx < nblk * 256; idx += NT) {
+        const int q = idx >> 8;
+        const int pb = q + d;
+        const int r = (idx >> 4) & 15;
+        const int c = idx & 15;
+        float acc = 0.f;
+        for (int k = q; k < pb; ++k) {
+          const float* arow = Am + (16 * pb + r) * LDF + 16 * k;
+#pragma unroll
+          for (int e = 0; e < 16; ++e) acc += arow[e] * Tb[(16 * k + e) * LDF + 16 * q + c];
+        }
+        Tb[(16 * q + r) * LDF + 16 * pb + c] = acc;
+      }
+      __syncthreads();
+      for (int idx = tid; idx < nblk * 256; idx += NT) {
+        const int q = idx >> 8;
+        const int pb = q + d;
+        const int r = (idx >> 4) & 15;
+        const int c = idx & 15;
+        float acc = 0.f;
+        const float* drow = Tb + (16 * pb + r) * LDF + 16 * pb;
+#pragma unroll
+        for (int e = 0; e < 16; ++e) acc += drow[e] * Tb[(16 * q + e) * LDF + 16 * pb + c];
+        Tb[(16 * pb + r) * LDF + 16 * q + c] = -acc;
+      }
+      __syncthreads();
+    }
+    // T as fp16 hi + lo, zero above the diagonal
+    for (int idx = tid; idx < CH * (CH / 4); idx += NT) {
+      const int i = idx >> 4;
+      const int lq4 = idx & 15;
+      float hi[4], lo[4];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int l = 4 * lq4 + r;
+        const float v = l <= i ? Tb[i * LDF + l] : 0.f;
+        hi[r] = static_cast<float>(static_cast<half_t>(v));
+        lo[r] = v - hi[r];
+      }
+      store4h(Thi + i * LD64 + 4 * lq4, hi[0], hi[1], hi[2], hi[3]);
+      store4h(Tlo + i * LD64 + 4 * lq4, lo[0], lo[1], lo[2], lo[3]);
+    }
+    __syncthreads();
+
+    // ---------------- W^T = Xt T^T -> Wn[i][dk] = -W; U = T Yt^T (registers)
+    for (int tile = wave; tile < 32; tile += NW) {
+      const int td = tile >> 2;  // dk tile
+      const int ti = tile & 3;   // token tile
+      cfloat4 acc = {0.f, 0.f, 0.f, 0.f};
+      acc = mma<CH>(Xt + 16 * td * LD64, LD64, Thi + 16 * ti * LD64, LD64, acc, lane);
+      acc = mma<CH>(Xt + 16 * td * LD64, LD64, Tlo + 16 * ti * LD64, LD64, acc, lane);
+      store4h(Wn + (16 * ti + lc) * LD128 + 16 * td + 4 * lq, -acc[0], -acc[1], -acc[2], -acc[3]);
+    }
+    cfloat4 Dl[2];  // delta tiles (token tile, dv tile) = ((2*wave+s)>>2, (2*wave+s)&3)
+#pragma unroll
+    for (int s = 0; s < 2; ++s) {
+      const int dt = 2 * wave + s;
+      const int ti = dt >> 2;
+      const int tv = dt & 3;
+      cfloat4 acc = {0.f, 0.f, 0.f, 0.f};
+      acc = mma<CH>(Thi + 16 * ti * LD64, LD64, Yt + 16 * tv * LD64, LD64, acc, lane);
+      acc = mma<CH>(Tlo + 16 * ti * LD64, LD64, Yt + 16 * tv * LD64, LD64, acc, lane);
+      Dl[s] = acc;
+    }
+    __syncthreads();
+
+    // ---------------- delta = U - W S0; keep delta^T and exp(G_C - G) delta^T in LDS
+    const float gC = s_G[CH - 1];
+#pragma unroll
+    for (int s = 0; s < 2; ++s) {
+      const int dt = 2 * wave + s;
+      const int ti = dt >> 2;
+      const int tv = dt & 3;
+      Dl[s] = mma<DK>(Wn + 16 * ti * LD128, LD128, St + 16 * tv * LD128, LD128, Dl[s], lane);
+      const int dv = 16 * tv + lc;
+      const int i0 = 16 * ti + 4 * lq;
+      store4h(Dt + dv * LD64 + i0, Dl[s][0], Dl[s][1], Dl[s][2], Dl[s][3]);
+      float sc[4];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) sc[r] = __expf(gC - s_G[i0 + r]) * Dl[s][r];
+      store4h(DDt + dv * LD64 + i0, sc[0], sc[1], sc[2], sc[3]);
+    }
+    __syncthreads();
+
+    // ---------------- O^T += delta^T Aqk^T -> output; S = gamma_C S + K^T (D delta)
+#pragma unroll
+    for (int s = 0; s < 2; ++s) {
+      const int ot = 2 * wave + s;
+      const int td = ot >> 2;
+      const int tt = ot & 3;
+      O[s] = mma<CH>(Dt + 16 * td * LD64, LD64, Aqk + 16 * tt * LD64, LD64, O[s], lane);
+      const int tok = 16 * tt + lc;
+      const int64_t tg = t0 + tok;
+      if (tg < p.T) {
+        const int64_t base = b * p.out_sb + tg * p.out_st + static_cast<int64_t>(j) * DV + half_id * DVS + 16 * td + 4 * lq;
+        if (p.out_dtype == QA_BF16) {
+          bf16_t* o = reinterpret_cast<bf16_t*>(p.out) + base;
+          uint2 packed;
+          packed.x = static_cast<uint32_t>(f32_to_bf16(O[s][0])) | (static_cast<uint32_t>(f32_to_bf16(O[s][1])) << 16);
+          packed.y = static_cast<uint32_t>(f32_to_bf16(O[s][2])) | (static_cast<uint32_t>(f32_to_bf16(O[s][3])) << 16);
+          *reinterpret_cast<uint2*>(o) = packed;
+        } else {
+          *reinterpret_cast<float4*>(reinterpret_cast<float*>(p.out) + base) = make_float4(O[s][0], O[s][1], O[s][2], O[s][3]);
+        }
+      }
+    }
+    const float gamC = s_gam[CH - 1];
+#pragma unroll
+    for (int tv = 0; tv < 4; ++tv) {
+      cfloat4 acc = S[tv] * gamC;
+      S[tv] = mma<CH>(Kt + 16 * wave * LD64, LD64, DDt + 16 * tv * LD64, LD64, acc, lane);
+      store4h(St + (16 * tv + lc) * LD128 + 16 * wave + 4 * lq, S[tv][0], S[tv][1], S[tv][2], S[tv][3]);
+    }
+    __syncthreads();
+  }
+
+  if (p.state_out != nullptr) {
+    float* s_out = p.state_out + ((b * p.Hv + j) * DK) * DV + half_id * DVS;
+#pragma unroll
+    for (int tv = 0; tv < 4; ++tv)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) s_out[static_cast<int64_t>(16 * wave + 4 * lq + r) * DV + 16 * tv + lc] = S[tv][r];
+  }
+  if (p.conv_out != nullptr) {
+    // last K-1 raw inputs of this workgroup's channels (q/k written by half 0 of
+    // the even value head of the pair, v by every workgroup for its own slice)
+    const bool owns_qk = half_id == 0 && (j % (p.Hv / p.Hqk)) == 0;
+    for (int idx = tid; idx < NCH * (KCONV - 1); idx += NT) {
+      const int lch = idx / (KCONV - 1);
+      const int slot = idx - lch * (KCONV - 1);
+      if (lch < 2 * DK && !owns_qk) continue;
+      const int ch = lch < DK ? q_ch0 + lch : lch < 2 * DK ? k_ch0 + (lch - DK) : v_ch0 + (lch - 2 * DK);
+      const int64_t ts = p.T - (KCONV - 1) + slot;
+      float v = 0.f;
+      if (ts >= 0)
+        v = load_x(p, b * p.x_sb + ts * p.x_st + ch);
+      else if (p.conv_in != nullptr)
+        v = p.conv_in[(b * p.C + ch) * (KCONV - 1) + (KCONV - 1) + ts];
+      p.conv_out[(b * p.C + ch) * (KCONV - 1) + slot] = v;
+    }
+  }
+}
+
+}  // namespace cgd
+}  // namespace qa
+
+extern "C" int64_t qa_chunk_gated_delta_lds_bytes(void) { return qa::cgd::LDS_BYTES; }
+
+extern "C" int qa_chunk_gated_delta_rule(const void* mixed_qkv, int32_t x_dtype, int64_t x_stride_b, int64_t x_stride_t,
+                                         const void* a, const void* b, int32_t ab_dtype, int64_t ab_stride_b,
+                                         int64_t ab_stride_t, const float* a_log, const float* dt_bias,
+                                         const float* conv_weight, const float* conv_state_in, float* conv_state_out,
+                                         const float* initial_state, float* final_state, void* out, int32_t out_dtype,
+                                         int64_t out_stride_b, int64_t out_stride_t, int64_t batch, int64_t seq,
+                                         int32_t key_heads, int32_t value_heads, int32_t key_dim, int32_t value_dim,
+                                         int32_t conv_kernel, hipStream_t stream) {
+  using namespace qa;
+  using namespace qa::cgd;
+  QA_REQUIRE(mixed_qkv && a && b && a_log && dt_bias && conv_weight && out, "chunk_gated_delta_rule: pointers must be non-null");
+  QA_REQUIRE(key_dim == DK && value_dim == DV && conv_kernel == KCONV,
+             "chunk_gated_delta_rule: built for key_dim = value_dim = 128 and conv kernel 4");
+  QA_REQUIRE(key_heads > 0 && value_heads % key_heads == 0, "chunk_gated_delta_rule: value heads must be a multiple of key heads");
+  QA_REQUIRE(x_dtype == QA_F32 || x_dtype == QA_BF16, "chunk_gated_delta_rule: mixed_qkv must be float32 or bfloat16");
+  QA_REQUIRE(ab_dtype == QA_F32 || ab_dtype == QA_BF16, "chunk_gated_delta_rule: a/b must be float32 or bfloat16");
+  QA_REQUIRE(out_dtype == QA_F32 || out_dtype == QA_BF16, "chunk_gated_delta_rule: out must be float32 or bfloat16");
+  QA_REQUIRE(batch > 0 && seq > 0, "chunk_gated_delta_rule: batch and seq must be positive");
+  QA_REQUIRE(batch * value_heads * 2 <= 0x7fffffff, "chunk_gated_delta_rule: too many workgroups");
+  QA_REQUIRE(out_stride_t % 4 == 0 && out_stride_b % 4 == 0 && (reinterpret_cast<uintptr_t>(out) & 15u) == 0,
+             "chunk_gated_delta_rule: output rows must be 16-byte aligned");
+  Params p{};
+  p.x = mixed_qkv;
+  p.x_dtype = x_dtype;
+  p.x_sb = x_stride_b;
+  p.x_st = x_stride_t;
+  p.a = a;
+  p.bb = b;
+  p.ab_dtype = ab_dtype;
+  p.ab_sb = ab_stride_b;
+  p.ab_st = ab_stride_t;
+  p.a_log = a_log;
+  p.dt_bias = dt_bias;
+  p.conv_w = conv_weight;
+  p.conv_in = conv_state_in;
+  p.conv_out = conv_state_out;
+  p.state_in = initial_state;
+  p.state_out = final_state;
+  p.out = out;
+  p.out_dtype = out_dtype;
+  p.out_sb = out_stride_b;
+  p.out_st = out_stride_t;
+  p.T = seq;
+  p.Hqk = key_heads;
+  p.Hv = value_heads;
+  p.C = 2 * key_heads * key_dim + value_heads * value_dim;
+  static bool attr_set = false;
+  if (!attr_set) {
+    hipError_t err = hipFuncSetAttribute(reinterpret_cast<const void*>(&chunk_kernel), hipFuncAttributeMaxDynamicSharedMemorySize, LDS_BYTES);
+    if (err != hipSuccess) return fail("chunk_gated_delta_rule: cannot reserve %d bytes of LDS: %s", LDS_BYTES, hipGetErrorString(err));
+    attr_set = true;
+  }
+  dim3 grid(static_cast<unsigned>(batch * value_heads * 2));
+  hipLaunchKernelGGL(chunk_kernel, grid, dim3(NT), LDS_BYTES, stream, p);
+  return check_launch("chunk_gated_delta_rule");
+}

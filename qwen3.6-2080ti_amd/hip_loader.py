@@ -96,6 +96,13 @@ SIGNATURES: dict[str, tuple[Any, list[Any]]] = {
         [c_void_p, c_int64, c_void_p, c_void_p, c_int32, c_int64, c_void_p, c_void_p, c_void_p, c_int64, c_void_p, c_int32, c_void_p,
          c_int32, c_int64, c_int64, c_int32, c_int32, c_int32, c_int32, c_void_p],
     ),
+    "qa_chunk_gated_delta_rule": (
+        c_int32,
+        [c_void_p, c_int32, c_int64, c_int64, c_void_p, c_void_p, c_int32, c_int64, c_int64, c_void_p, c_void_p, c_void_p, c_void_p,
+         c_void_p, c_void_p, c_void_p, c_void_p, c_int32, c_int64, c_int64, c_int64, c_int64, c_int32, c_int32, c_int32, c_int32,
+         c_int32, c_void_p],
+    ),
+    "qa_chunk_gated_delta_lds_bytes": (c_int64, []),
 }
 
 

@@ -530,3 +530,62 @@ def gated_delta_step(
     )
     L.check(lib, status, "gated_delta_step")
     return out
+
+
+def chunk_gated_delta_rule(
+    mixed_qkv: torch.Tensor,
+    a: torch.Tensor,
+    b: torch.Tensor,
+    a_log: torch.Tensor,
+    dt_bias: torch.Tensor,
+    conv_weight: torch.Tensor,
+    *,
+    key_heads: int,
+    value_heads: int,
+    conv_state: torch.Tensor | None = None,
+    initial_state: torch.Tensor | None = None,
+    out_dtype: torch.dtype = torch.bfloat16,
+    keep_conv_state: bool = True,
+) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor | None]:
+    """Chunked prefill of a linear-attention layer from its raw projections.
+
+    ``mixed_qkv`` ``(B, T, 2*Hqk*128 + Hv*128)`` (the ``in_proj_qkv`` output),
+    ``a``/``b`` ``(B, T, Hv)``, ``a_log``/``dt_bias`` ``(Hv,)``, ``conv_weight``
+    ``(C, 1, 4)`` or ``(C, 4)``.  Returns ``(core (B, T, Hv, 128), final_state
+    (B, Hv, 128, 128) fp32, conv_state (B, C, 3) fp32 or None)``; ``core`` is
+    the recurrence output before the gated RMSNorm
+    (``src/reference_ops.py:240-283`` with the recurrence ``:291-322``).
+    """
+    lib = L.load_library()
+    _require_cuda(mixed_qkv, "mixed_qkv")
+    device = mixed_qkv.device
+    _float_dtype(mixed_qkv, "mixed_qkv")
+    _require(mixed_qkv.dim() == 3 and mixed_qkv.stride(-1) == 1, "mixed_qkv must be (batch, seq, channels) with contiguous channels")
+    batch, seq, channels = mixed_qkv.shape
+    dk = dv = 128
+    _require(channels == 2 * key_heads * dk + value_heads * dv, "mixed_qkv channels must be 2*key_heads*128 + value_heads*128")
+    _require(a.shape == (batch, seq, value_heads) and b.shape == a.shape, "a/b must be (batch, seq, value_heads)")
+    _require(a.dtype == b.dtype and a.dtype in (torch.float32, torch.bfloat16), "a/b must share a float32/bfloat16 dtype")
+    _require(a.stride() == b.stride() and a.stride(-1) == 1, "a/b must share strides with contiguous heads")
+    alog = _f32_contig(a_log.reshape(-1), "a_log", device)
+    dtb = _f32_contig(dt_bias.reshape(-1), "dt_bias", device)
+    w = _conv_weight(conv_weight, channels, device)
+    _require(w.shape[1] == 4, "conv kernel must be 4")
+    conv_in = None
+    if conv_state is not None:
+        conv_in = _f32_contig(conv_state, "conv_state", device)
+        _require(tuple(conv_in.shape) == (batch, channels, 3), "conv_state must be (batch, channels, 3)")
+    state_in = None
+    if initial_state is not None:
+        state_in = _f32_contig(initial_state, "initial_state", device)
+        _require(tuple(state_in.shape) == (batch, value_heads, dk, dv), "initial_state must be (batch, value_heads, 128, 128)")
+    out = torch.empty((batch, seq, value_heads, dv), dtype=out_dtype, device=device)
+    final = torch.empty((batch, value_heads, dk, dv), dtype=torch.float32, device=device)
+    conv_out = torch.empty((batch, channels, 3), dtype=torch.float32, device=device) if keep_conv_state else None
+    status = lib.qa_chunk_gated_delta_rule(
+        _ptr(mixed_qkv), _code(mixed_qkv), mixed_qkv.stride(0), mixed_qkv.stride(1), _ptr(a), _ptr(b), _code(a), a.stride(0), a.stride(1),
+        _ptr(alog), _ptr(dtb), _ptr(w), _ptr(conv_in), _ptr(conv_out), _ptr(state_in), _ptr(final), _ptr(out), _code(out), out.stride(0),
+        out.stride(1), batch, seq, int(key_heads), int(value_heads), dk, dv, 4, _stream(device),
+    )
+    L.check(lib, status, "chunk_gated_delta_rule")
+    return out, final, conv_out
