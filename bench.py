@@ -153,6 +153,58 @@ def cpu_baseline_decode(w, budget_s: float = 12.0):
     }
 
 
+# ----------------------------------------------------------------------------- config 4
+
+
+def delta_flops(batch: int, seq: int, value_heads: int, chunk: int = 64, dk: int = 128, dv: int = 128) -> float:
+    """Algorithmic FLOP of the chunked prefill (BASELINE config-4 formula).
+
+    Per (chunk, value head): 2C^2(3dk + 2dv) + 6 C dk dv + C^3/3.
+    """
+    per = 2 * chunk * chunk * (3 * dk + 2 * dv) + 6 * chunk * dk * dv + chunk**3 / 3
+    return per * batch * value_heads * (seq / chunk)
+
+
+def delta_workload(device: str, *, seed: int = 0, batch: int = 4, seq: int = 8192, key_heads: int = 16, value_heads: int = 32):
+    import torch
+
+    channels = 2 * key_heads * 128 + value_heads * 128
+    gen = torch.Generator(device=device).manual_seed(seed)
+    mixed = torch.randn((batch, seq, channels), generator=gen, device=device, dtype=torch.bfloat16)
+    a = torch.randn((batch, seq, value_heads), generator=gen, device=device, dtype=torch.bfloat16)
+    b = torch.randn((batch, seq, value_heads), generator=gen, device=device, dtype=torch.bfloat16)
+    # config 4: beta = sigmoid(N(0,1)), alpha = exp(-softplus(N(0,1))) -> A_log = 0, dt_bias = 0
+    a_log = torch.zeros(value_heads, device=device)
+    dt_bias = torch.zeros(value_heads, device=device)
+    conv_w = torch.randn((channels, 4), generator=gen, device=device) * 0.5
+    algo_bytes = mixed.numel() * 2 + 2 * a.numel() * 2 + batch * seq * value_heads * 128 * 2 + batch * value_heads * 128 * 128 * 4
+    return {"mixed": mixed, "a": a, "b": b, "a_log": a_log, "dt_bias": dt_bias, "conv_w": conv_w, "key_heads": key_heads,
+            "value_heads": value_heads, "batch": batch, "seq": seq, "flops": delta_flops(batch, seq, value_heads), "algo_bytes": algo_bytes}
+
+
+def time_delta(w, steps: int, warmup: int) -> float:
+    import torch
+
+    import hip_ops
+
+    def step():
+        return hip_ops.chunk_gated_delta_rule(w["mixed"], w["a"], w["b"], w["a_log"], w["dt_bias"], w["conv_w"], key_heads=w["key_heads"],
+                                              value_heads=w["value_heads"], keep_conv_state=False)
+
+    for _ in range(warmup):
+        step()
+    torch.cuda.synchronize()
+    stream = torch.cuda.current_stream()
+    start = torch.cuda.Event(enable_timing=True)
+    end = torch.cuda.Event(enable_timing=True)
+    start.record(stream)
+    for _ in range(steps):
+        step()
+    end.record(stream)
+    torch.cuda.synchronize()
+    return start.elapsed_time(end) / steps
+
+
 # ----------------------------------------------------------------------------- main
 
 
@@ -162,6 +214,7 @@ def main() -> int:
     parser.add_argument("--steps", type=int, default=20)
     parser.add_argument("--warmup", type=int, default=5)
     parser.add_argument("--no-cpu-baseline", action="store_true")
+    parser.add_argument("--no-delta", action="store_true", help="skip the config-4 secondary measurement")
     parser.add_argument("--cpu-budget", type=float, default=12.0)
     args = parser.parse_args()
     if args.gpus != 1:
@@ -178,6 +231,7 @@ def main() -> int:
     w = decode_workload(device)
     _log(f"bench: pool {w['pool_blocks']} blocks, sum ctx {int(w['ctx'].sum())}, algo bytes {w['algo_bytes']/1e9:.3f} GB")
     ms = time_decode(w, args.steps, args.warmup)
+    wc = {k: w[k] for k in ("query", "tables_cpu", "key_pool", "value_pool", "ctx", "bs")}
     gbs = w["algo_bytes"] / (ms * 1e-3) / 1e9
     _log(f"bench: decode {ms:.4f} ms/step, {gbs:.1f} GB/s ({gbs / HBM_PEAK_GBS:.1%} of HBM peak)")
     record = {
@@ -215,9 +269,31 @@ def main() -> int:
             "algo_bytes_per_launch": w["algo_bytes"],
         },
     }
+    del w
+    torch.cuda.empty_cache()
+    if not args.no_delta:
+        _log("bench: building config-4 workload (gated delta-rule chunked prefill)")
+        dw = delta_workload(device)
+        dms = time_delta(dw, max(2, args.steps // 2), max(1, args.warmup // 2))
+        tflops = dw["flops"] / (dms * 1e-3) / 1e12
+        tok_s = dw["batch"] * dw["seq"] / (dms * 1e-3)
+        _log(f"bench: delta prefill {dms:.3f} ms, {tok_s:,.0f} tokens/s, {tflops:.1f} TFLOP/s ({tflops / MFMA_BF16_PEAK_TFLOPS:.1%} of MFMA peak)")
+        record["secondary"] = {
+            "metric": "gated-delta chunked prefill tokens/s (BASELINE config 4)",
+            "value": round(tok_s, 1),
+            "unit": "tokens/s",
+            "ms_per_step": round(dms, 4),
+            "config": {"workload": "gated delta-rule chunked prefill (BASELINE config 4)", "batch": 4, "seq_len": 8192, "key_heads": 16,
+                       "value_heads": 32, "head_dim": 128, "chunk": 64, "conv_kernel": 4},
+            "roofline": {"bound": "mfma", "achieved": round(tflops, 2), "peak": MFMA_BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
+                         "frac": round(tflops / MFMA_BF16_PEAK_TFLOPS, 4), "traffic": None, "algo_flop_per_launch": dw["flops"],
+                         "algo_bytes_per_launch": dw["algo_bytes"], "kernel": "qa::cgd::chunk_kernel (fp16 MFMA, fp32 accumulate)"},
+        }
+        del dw
+        torch.cuda.empty_cache()
     if not args.no_cpu_baseline:
         _log("bench: CPU baseline (reference path restatement)")
-        record["cpu_baseline"] = cpu_baseline_decode(w, args.cpu_budget)
+        record["cpu_baseline"] = cpu_baseline_decode(wc, args.cpu_budget)
     print(json.dumps(record), flush=True)
     return 0
 

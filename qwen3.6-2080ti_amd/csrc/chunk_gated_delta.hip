@@ -20,6 +20,9 @@
 // orientation its consumer needs by choosing C or C^T (swapped operands).
 // T is computed in fp32 (blocked 16x16 inverse) and fed to the MFMA as a
 // hi + lo fp16 pair, keeping the state update within fp32-state tolerance.
+// q and k are held unnormalised in fp16; their per-token L2 scales are folded
+// into the fp32 epilogues of the products (and into Xt and exp(G_C-G)*delta),
+// so every fp16 operand is rounded once.
 #include "qa_common.h"
 
 namespace qa {
@@ -63,9 +66,11 @@ constexpr int OFF_YT = OFF_XT + DK * LD64 * 2;          // Yt [dv][tok] = beta*V
 constexpr int OFF_ST = OFF_YT + DVS * LD64 * 2;         // St [dv][dk] (fp16 state)
 constexpr int OFF_AQK = OFF_ST + DVS * LD128 * 2;       // Aqk [i][l]
 constexpr int OFF_SC = OFF_AQK + CH * LD64 * 2;         // scalars
-constexpr int OFF_WCONV = OFF_SC + 4 * CH * 4;          // conv weights of this workgroup's 320 channels
+constexpr int OFF_WCONV = OFF_SC + 6 * CH * 4;          // conv weights of this workgroup's 320 channels
 constexpr int NCH = 2 * DK + DVS;                       // 320
-constexpr int LDS_BYTES = OFF_WCONV + NCH * KCONV * 4;
+constexpr int OFF_HALO = OFF_WCONV + NCH * KCONV * 4;   // raw inputs of the 3 tokens before the chunk, fp32 [3][320]
+constexpr int OFF_NRM = OFF_HALO + (KCONV - 1) * NCH * 4;  // per-wave sum of squares [8 waves][64 tokens]
+constexpr int LDS_BYTES = OFF_NRM + NW * CH * 4;
 
 static_assert(CH * LD128 * 2 * 2 <= SZ_R1, "R1 too small for Qs|Ks");
 static_assert(CH * LDF * 4 <= SZ_R2, "R2 too small for Vstage");
@@ -117,6 +122,23 @@ __device__ __forceinline__ cfloat4 mma(const half_t* A, int lda, const half_t* B
   return acc;
 }
 
+// Raw in_proj row slice (bf16) of token tg for this wave: 32 q/k channels and 8 v channels.
+__device__ __forceinline__ void load_raw(const Params& p, int64_t b, int64_t tg, int q_ch0, int k_ch0, int v_ch0, int wave, uint4 (&raw_qk)[4], uint4& raw_v) {
+  const int ch_qk = wave < 4 ? q_ch0 + 32 * wave : k_ch0 + 32 * (wave - 4);
+  const int ch_v = v_ch0 + 8 * wave;
+  if (tg >= p.T) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) raw_qk[i] = make_uint4(0, 0, 0, 0);
+    raw_v = make_uint4(0, 0, 0, 0);
+    return;
+  }
+  const int64_t row = b * p.x_sb + tg * p.x_st;
+  const bf16_t* x = reinterpret_cast<const bf16_t*>(p.x) + row;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) raw_qk[i] = *reinterpret_cast<const uint4*>(x + ch_qk + 8 * i);
+  raw_v = *reinterpret_cast<const uint4*>(x + ch_v);
+}
+
 __device__ __forceinline__ void store4h(half_t* dst, float a, float b, float c, float d) {
   f16x4_v v;
   v[0] = static_cast<half_t>(a);
@@ -149,8 +171,11 @@ __global__ __launch_bounds__(NT) void chunk_kernel(Params p) {
   float* s_beta = reinterpret_cast<float*>(smem + OFF_SC);
   float* s_G = s_beta + CH;
   float* s_gam = s_G + CH;
-  float* s_misc = s_gam + CH;
+  float* s_rq = s_gam + CH;  // per-token L2 scale of q (times dk^-0.5)
+  float* s_rk = s_rq + CH;   // per-token L2 scale of k
   float* wconv = reinterpret_cast<float*>(smem + OFF_WCONV);
+  float* halo = reinterpret_cast<float*>(smem + OFF_HALO);
+  float* nrm = reinterpret_cast<float*>(smem + OFF_NRM);
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -188,76 +213,93 @@ __global__ __launch_bounds__(NT) void chunk_kernel(Params p) {
   }
   const float alog = -__expf(p.a_log[j]);
   const float dtb = p.dt_bias[j];
+  // halo of chunk 0: the conv state (oldest first) or zeros
+  for (int idx = tid; idx < (KCONV - 1) * NCH; idx += NT) {
+    const int hs = idx / NCH;
+    const int lch = idx - hs * NCH;
+    const int ch = lch < DK ? q_ch0 + lch : lch < 2 * DK ? k_ch0 + (lch - DK) : v_ch0 + (lch - 2 * DK);
+    halo[idx] = p.conv_in != nullptr ? p.conv_in[(b * p.C + ch) * (KCONV - 1) + hs] : 0.f;
+  }
+  uint4 raw_qk[4];
+  uint4 raw_v;
+  load_raw(p, b, static_cast<int64_t>(lane), q_ch0, k_ch0, v_ch0, wave, raw_qk, raw_v);
+  float a_cur = 0.f, b_cur = 0.f;
+  if (wave == NW - 1 && lane < p.T) {
+    a_cur = load_ab(p.a, p.ab_dtype, b * p.ab_sb + lane * p.ab_st + j);
+    b_cur = load_ab(p.bb, p.ab_dtype, b * p.ab_sb + lane * p.ab_st + j);
+  }
   __syncthreads();
 
   const int64_t nchunks = (p.T + CH - 1) / CH;
   for (int64_t ci = 0; ci < nchunks; ++ci) {
     const int64_t t0 = ci * CH;
 
-    // ---------------- prologue: conv + SiLU + L2 norm (q, k), conv + SiLU (v), gating
+    // ---------------- prologue: conv + SiLU + L2 norm (q, k), conv + SiLU (v), gating.
+    // Lane = token, wave w = channel slice: q/k channels [32w, 32w+32) of the
+    // workgroup's 256 (q for w < 4, k for w >= 4) and v channels [8w, 8w+8).
+    // Taps of earlier tokens come from lanes tok-1..tok-3 (shuffles) or, for
+    // the first three lanes, from the halo of the previous chunk.
     {
-      const int tok = tid >> 3;
-      const int grp = tid & 7;  // 0-3: q channels 32*grp, 4-7: k channels 32*(grp-4)
+      const int tok = lane;
       const int64_t tg = t0 + tok;
-      const int lch0 = grp < 4 ? 32 * grp : DK + 32 * (grp - 4);
-      const int ch0 = grp < 4 ? q_ch0 + 32 * grp : k_ch0 + 32 * (grp - 4);
-      float y[32];
-#pragma unroll
-      for (int c = 0; c < 32; ++c) y[c] = 0.f;
-      if (tg < p.T) {
-#pragma unroll
-        for (int tap = 0; tap < KCONV; ++tap) {
-          const int64_t ts = tg - (KCONV - 1) + tap;
-          if (ts >= 0) {
-#pragma unroll
-            for (int c = 0; c < 32; ++c) y[c] += wconv[(lch0 + c) * KCONV + tap] * load_x(p, b * p.x_sb + ts * p.x_st + ch0 + c);
-          } else if (p.conv_in != nullptr) {
-#pragma unroll
-            for (int c = 0; c < 32; ++c)
-              y[c] += wconv[(lch0 + c) * KCONV + tap] * p.conv_in[(b * p.C + ch0 + c) * (KCONV - 1) + (KCONV - 1) + ts];
-          }
-        }
-      }
+      const bool live = tg < p.T;
+      // Packed bf16 pairs of this token and of tokens tok-1..tok-3 (shuffles;
+      // lanes 0..2 take the missing ones from the halo).  dword i < 16: q/k
+      // channels 2i, 2i+1 of this wave's slice; i >= 16: v channels 2(i-16), +1.
+      // q/k are stored unnormalised; the per-token L2 scales are applied to
+      // the fp32 products later (every operand keeps a single fp16 rounding).
       float ss = 0.f;
+      half_t* qk_row = wave < 4 ? Qs + tok * LD128 + 32 * wave : Ks + tok * LD128 + 32 * (wave - 4);
 #pragma unroll
-      for (int c = 0; c < 32; ++c) {
-        y[c] = silu_ref(y[c]);
-        ss += y[c] * y[c];
-      }
-      ss += __shfl_xor(ss, 1, 64);
-      ss += __shfl_xor(ss, 2, 64);
-      const float scale = rsqrtf(ss + 1e-6f) * (grp < 4 ? rsqrtf(static_cast<float>(DK)) : 1.f);
-      half_t* dst = (grp < 4 ? Qs + tok * LD128 + 32 * grp : Ks + tok * LD128 + 32 * (grp - 4));
+      for (int i = 0; i < 20; ++i) {
+        const uint32_t own = i < 16 ? reinterpret_cast<const uint32_t*>(&raw_qk[i / 4])[i % 4] : reinterpret_cast<const uint32_t*>(&raw_v)[i - 16];
+        const int lch = i < 16 ? 32 * wave + 2 * i : 2 * DK + 8 * wave + 2 * (i - 16);
+        float lo[4], hi[4];  // tap order: tok-3, tok-2, tok-1, tok
+        lo[3] = __uint_as_float(own << 16);
+        hi[3] = __uint_as_float(own & 0xffff0000u);
 #pragma unroll
-      for (int c = 0; c < 32; c += 4) store4h(dst + c, y[c] * scale, y[c + 1] * scale, y[c + 2] * scale, y[c + 3] * scale);
-    }
-    if (tid < 2 * CH) {
-      const int tok = tid >> 1;
-      const int vg = tid & 1;
-      const int64_t tg = t0 + tok;
-      const int lch0 = 2 * DK + 32 * vg;
-      const int ch0 = v_ch0 + 32 * vg;
-      float y[32];
-#pragma unroll
-      for (int c = 0; c < 32; ++c) y[c] = 0.f;
-      if (tg < p.T) {
-#pragma unroll
-        for (int tap = 0; tap < KCONV; ++tap) {
-          const int64_t ts = tg - (KCONV - 1) + tap;
-          if (ts >= 0) {
-#pragma unroll
-            for (int c = 0; c < 32; ++c) y[c] += wconv[(lch0 + c) * KCONV + tap] * load_x(p, b * p.x_sb + ts * p.x_st + ch0 + c);
-          } else if (p.conv_in != nullptr) {
-#pragma unroll
-            for (int c = 0; c < 32; ++c)
-              y[c] += wconv[(lch0 + c) * KCONV + tap] * p.conv_in[(b * p.C + ch0 + c) * (KCONV - 1) + (KCONV - 1) + ts];
+        for (int back = 1; back <= KCONV - 1; ++back) {
+          const uint32_t u = __shfl_up(own, back, 64);
+          if (tok >= back) {
+            lo[3 - back] = __uint_as_float(u << 16);
+            hi[3 - back] = __uint_as_float(u & 0xffff0000u);
+          } else {
+            const int hs = KCONV - 1 - back + tok;
+            lo[3 - back] = halo[hs * NCH + lch];
+            hi[3 - back] = halo[hs * NCH + lch + 1];
           }
         }
-#pragma unroll
-        for (int c = 0; c < 32; ++c) y[c] = silu_ref(y[c]);
+        const float4 w0 = *reinterpret_cast<const float4*>(wconv + lch * KCONV);
+        const float4 w1 = *reinterpret_cast<const float4*>(wconv + (lch + 1) * KCONV);
+        const float a0 = w0.x * lo[0] + w0.y * lo[1] + w0.z * lo[2] + w0.w * lo[3];
+        const float a1 = w1.x * hi[0] + w1.y * hi[1] + w1.z * hi[2] + w1.w * hi[3];
+        const float y0 = live ? silu_ref(a0) : 0.f;
+        const float y1 = live ? silu_ref(a1) : 0.f;
+        if (i < 16) {
+          ss += y0 * y0 + y1 * y1;
+          __attribute__((ext_vector_type(2))) _Float16 pr;
+          pr[0] = static_cast<half_t>(y0);
+          pr[1] = static_cast<half_t>(y1);
+          *reinterpret_cast<decltype(pr)*>(qk_row + 2 * i) = pr;
+        } else {
+          Vst[tok * LDF + 8 * wave + 2 * (i - 16)] = y0;
+          Vst[tok * LDF + 8 * wave + 2 * (i - 16) + 1] = y1;
+        }
       }
+      nrm[wave * CH + tok] = ss;
+      __syncthreads();  // every halo read is done before lanes 61..63 overwrite it
+      if (tok >= CH - (KCONV - 1)) {
+        const int hs = tok - (CH - (KCONV - 1));
 #pragma unroll
-      for (int c = 0; c < 32; ++c) Vst[tok * LDF + 32 * vg + c] = y[c];
+        for (int i = 0; i < 20; ++i) {
+          const uint32_t own = i < 16 ? reinterpret_cast<const uint32_t*>(&raw_qk[i / 4])[i % 4] : reinterpret_cast<const uint32_t*>(&raw_v)[i - 16];
+          const int lch = i < 16 ? 32 * wave + 2 * i : 2 * DK + 8 * wave + 2 * (i - 16);
+          halo[hs * NCH + lch] = __uint_as_float(own << 16);
+          halo[hs * NCH + lch + 1] = __uint_as_float(own & 0xffff0000u);
+        }
+      }
+      // prefetch the next chunk's raw rows; they stay in flight through this chunk's compute
+      if (ci + 1 < nchunks) load_raw(p, b, t0 + CH + tok, q_ch0, k_ch0, v_ch0, wave, raw_qk, raw_v);
     }
     if (wave == NW - 1) {
       // gating and the inclusive prefix sum of g over the chunk (src/reference_ops.py:271-275)
@@ -265,10 +307,12 @@ __global__ __launch_bounds__(NT) void chunk_kernel(Params p) {
       const int64_t tg = t0 + tok;
       float g = 0.f, beta = 0.f;
       if (tg < p.T) {
-        const float av = load_ab(p.a, p.ab_dtype, b * p.ab_sb + tg * p.ab_st + j);
-        const float bv = load_ab(p.bb, p.ab_dtype, b * p.ab_sb + tg * p.ab_st + j);
-        g = alog * softplus_ref(av + dtb);
-        beta = 1.f / (1.f + __expf(-bv));
+        g = alog * softplus_ref(a_cur + dtb);
+        beta = 1.f / (1.f + __expf(-b_cur));
+      }
+      if (ci + 1 < nchunks && tg + CH < p.T) {
+        a_cur = load_ab(p.a, p.ab_dtype, b * p.ab_sb + (tg + CH) * p.ab_st + j);
+        b_cur = load_ab(p.bb, p.ab_dtype, b * p.ab_sb + (tg + CH) * p.ab_st + j);
       }
       float G = g;
 #pragma unroll
@@ -279,6 +323,11 @@ __global__ __launch_bounds__(NT) void chunk_kernel(Params p) {
       s_beta[tok] = beta;
       s_G[tok] = G;
       s_gam[tok] = __expf(G);
+      // l2_norm scales (src/reference_ops.py:181-183) and q * dk^-0.5 (:304)
+      const float sq = (nrm[0 * CH + tok] + nrm[1 * CH + tok]) + (nrm[2 * CH + tok] + nrm[3 * CH + tok]);
+      const float sk = (nrm[4 * CH + tok] + nrm[5 * CH + tok]) + (nrm[6 * CH + tok] + nrm[7 * CH + tok]);
+      s_rq[tok] = rsqrtf(sq + 1e-6f) * rsqrtf(static_cast<float>(DK));
+      s_rk[tok] = rsqrtf(sk + 1e-6f);
     }
     __syncthreads();
 
@@ -291,7 +340,7 @@ __global__ __launch_bounds__(NT) void chunk_kernel(Params p) {
       for (int r = 0; r < 4; ++r) {
         const int tok = 4 * tq + r;
         kv[r] = static_cast<float>(Ks[tok * LD128 + dk]);
-        xv[r] = kv[r] * s_beta[tok] * s_gam[tok];
+        xv[r] = kv[r] * (s_beta[tok] * s_gam[tok] * s_rk[tok]);
       }
       store4h(Kt + dk * LD64 + 4 * tq, kv[0], kv[1], kv[2], kv[3]);
       store4h(Xt + dk * LD64 + 4 * tq, xv[0], xv[1], xv[2], xv[3]);
@@ -320,7 +369,7 @@ __global__ __launch_bounds__(NT) void chunk_kernel(Params p) {
       for (int r = 0; r < 4; ++r) {
         const int i = 16 * ti + 4 * lq + r;
         const int l = 16 * tl + lc;
-        Am[i * LDF + l] = l < i ? s_beta[i] * __expf(s_G[i] - s_G[l]) * acc[r] : 0.f;
+        Am[i * LDF + l] = l < i ? s_beta[i] * s_rk[i] * s_rk[l] * __expf(s_G[i] - s_G[l]) * acc[r] : 0.f;
       }
     }
     __syncthreads();
@@ -331,17 +380,15 @@ __global__ __launch_bounds__(NT) void chunk_kernel(Params p) {
     if (wave == 0) {
       const int qb = lane >> 4;
       const int c = lane & 15;
-      float x[16];
-#pragma unroll
+      // column c of D_qb = (I + A_qb,qb)^-1, rows in order; finished rows are read back from Tb
+      float* tcol = Tb + (16 * qb) * LDF + 16 * qb + c;
+#pragma unroll 1
       for (int i = 0; i < 16; ++i) {
         float acc = i == c ? 1.f : 0.f;
         const float* arow = Am + (16 * qb + i) * LDF + 16 * qb;
-#pragma unroll
-        for (int l = 0; l < i; ++l) acc -= arow[l] * x[l];
-        x[i] = acc;
+        for (int l = 0; l < i; ++l) acc -= arow[l] * tcol[l * LDF];
+        tcol[i * LDF] = acc;
       }
-#pragma unroll
-      for (int i = 0; i < 16; ++i) Tb[(16 * qb + i) * LDF + 16 * qb + c] = x[i];
     } else {
       // Aqk[i][l] = exp(G_i - G_l) (q_i . k_l), l <= i, computed as (K Q^T)[l][i]
       for (int tile = wave - 1; tile < 16; tile += NW - 1) {
@@ -354,7 +401,7 @@ __global__ __launch_bounds__(NT) void chunk_kernel(Params p) {
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
           const int l = 16 * tl + 4 * lq + r;
-          v[r] = l <= i ? __expf(s_G[i] - s_G[l]) * acc[r] : 0.f;
+          v[r] = l <= i ? s_rq[i] * s_rk[l] * __expf(s_G[i] - s_G[l]) * acc[r] : 0.f;
         }
         store4h(Aqk + i * LD64 + 16 * tl + 4 * lq, v[0], v[1], v[2], v[3]);
       }
@@ -367,7 +414,7 @@ __global__ __launch_bounds__(NT) void chunk_kernel(Params p) {
       const int tt = ot & 3;
       cfloat4 acc = {0.f, 0.f, 0.f, 0.f};
       acc = mma<DK>(St + 16 * td * LD128, LD128, Qs + 16 * tt * LD128, LD128, acc, lane);
-      const float gam = s_gam[16 * tt + lc];
+      const float gam = s_gam[16 * tt + lc] * s_rq[16 * tt + lc];
 #pragma unroll
       for (int r = 0; r < 4; ++r) O[s][r] = acc[r] * gam;
     }
@@ -458,7 +505,7 @@ __global__ __launch_bounds__(NT) void chunk_kernel(Params p) {
       store4h(Dt + dv * LD64 + i0, Dl[s][0], Dl[s][1], Dl[s][2], Dl[s][3]);
       float sc[4];
 #pragma unroll
-      for (int r = 0; r < 4; ++r) sc[r] = __expf(gC - s_G[i0 + r]) * Dl[s][r];
+      for (int r = 0; r < 4; ++r) sc[r] = __expf(gC - s_G[i0 + r]) * s_rk[i0 + r] * Dl[s][r];
       store4h(DDt + dv * LD64 + i0, sc[0], sc[1], sc[2], sc[3]);
     }
     __syncthreads();
@@ -541,7 +588,9 @@ extern "C" int qa_chunk_gated_delta_rule(const void* mixed_qkv, int32_t x_dtype,
   QA_REQUIRE(key_dim == DK && value_dim == DV && conv_kernel == KCONV,
              "chunk_gated_delta_rule: built for key_dim = value_dim = 128 and conv kernel 4");
   QA_REQUIRE(key_heads > 0 && value_heads % key_heads == 0, "chunk_gated_delta_rule: value heads must be a multiple of key heads");
-  QA_REQUIRE(x_dtype == QA_F32 || x_dtype == QA_BF16, "chunk_gated_delta_rule: mixed_qkv must be float32 or bfloat16");
+  QA_REQUIRE(x_dtype == QA_BF16, "chunk_gated_delta_rule: mixed_qkv must be bfloat16");
+  QA_REQUIRE(x_stride_t % 8 == 0 && x_stride_b % 8 == 0 && (reinterpret_cast<uintptr_t>(mixed_qkv) & 15u) == 0,
+             "chunk_gated_delta_rule: mixed_qkv rows must be 16-byte aligned");
   QA_REQUIRE(ab_dtype == QA_F32 || ab_dtype == QA_BF16, "chunk_gated_delta_rule: a/b must be float32 or bfloat16");
   QA_REQUIRE(out_dtype == QA_F32 || out_dtype == QA_BF16, "chunk_gated_delta_rule: out must be float32 or bfloat16");
   QA_REQUIRE(batch > 0 && seq > 0, "chunk_gated_delta_rule: batch and seq must be positive");

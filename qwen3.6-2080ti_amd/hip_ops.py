@@ -559,7 +559,7 @@ def chunk_gated_delta_rule(
     lib = L.load_library()
     _require_cuda(mixed_qkv, "mixed_qkv")
     device = mixed_qkv.device
-    _float_dtype(mixed_qkv, "mixed_qkv")
+    _require(mixed_qkv.dtype == torch.bfloat16, "mixed_qkv must be bfloat16")
     _require(mixed_qkv.dim() == 3 and mixed_qkv.stride(-1) == 1, "mixed_qkv must be (batch, seq, channels) with contiguous channels")
     batch, seq, channels = mixed_qkv.shape
     dk = dv = 128
