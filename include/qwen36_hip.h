@@ -131,6 +131,24 @@ int qa_paged_kv_gather(const qa_paged_kv* kv, int32_t head_dim, int64_t batch,
                        int64_t max_blocks, int64_t valid, int32_t block_size,
                        void* key_out, void* value_out, hipStream_t stream);
 
+/* ---- paged prefill ------------------------------------------------------ */
+/* Causal attention of packed new tokens over their paged KV (prefix + the
+ * new tokens, already appended): query (total_new, heads, head_dim) bf16
+ * with element strides (q_stride_t, q_stride_h); cu_seqlens (batch+1) and
+ * prefix_lens (batch) device index arrays (int32/int64); new token n of
+ * sequence b sits at position prefix_lens[b] + n.  Optional gate
+ * (total_new, heads*head_dim) bf16 logits: out *= sigmoid(gate).  Writes
+ * output (total_new, heads, head_dim) bf16 contiguous.  bf16 MFMA, head_dim
+ * 128 or 256, block size 16, GQA group <= 8, one shared pool.  Replaces the
+ * reference's dense multi-token fallback (src/tp_runtime.py:551-610 ->
+ * :698-730; src/reference_ops.py:353-360) with a chunked paged kernel.      */
+int qa_paged_attention_prefill(const void* query, int32_t q_dtype, int64_t q_stride_t, int64_t q_stride_h,
+                               const void* cu_seqlens, const void* prefix_lens, int32_t idx_dtype,
+                               int64_t batch, int64_t max_new, int32_t heads, int32_t head_dim,
+                               const qa_paged_kv* kv, const void* block_tables, int32_t table_dtype,
+                               int64_t table_stride, int64_t max_blocks, int32_t block_size, float scale,
+                               const void* gate, int64_t gate_stride_t, void* output, hipStream_t stream);
+
 /* ---- gated delta-rule linear attention --------------------------------- */
 /* Depthwise causal conv1d over `seq` tokens (+ optional SiLU), fp32 math.
  * x: (batch, seq, channels) with element strides (x_stride_b, x_stride_t),

@@ -1,0 +1,310 @@
+// Chunked causal paged prefill attention with the sigmoid output gate, gfx950.
+//
+// New query tokens of each sequence sit at absolute positions prefix_b + n and
+// attend to every cached key at position <= their own (the prefix plus the new
+// tokens, already appended to the paged cache).  Output
+//   out[n][h] = softmax(q K^T * scale, causal) V  * sigmoid(gate[n][h])
+// as the reference's multi-token path (src/reference_ops.py:353-360,
+// src/tp_runtime.py:698-730) computes it densely in fp32 after a gather.
+//
+// Workgroup = (16 new positions, sequence b, KV head g), 8 waves; wave w owns
+// query head g*G + w (w < G) for the 16 positions.  Keys stream in tiles of 64
+// through LDS: K as [key][d] (the A operand of S^T = K Q^T), V transposed to
+// [d][key] with v_perm_b32 so it is the A operand of O^T = V^T P.  S^T in the
+// MFMA accumulator layout (lane: keys 4(l/16)+r, position l%16) is exactly the
+// B-operand layout of the PV product, so P stays in registers.  Online softmax
+// per position (column), fp32; P rounded to bf16 (the reference rounds probs
+// to the query dtype before PV, src/reference_ops.py:358).
+#include "qa_common.h"
+
+namespace qa {
+namespace pfx {
+
+typedef __attribute__((__vector_size__(8 * sizeof(__bf16)))) __bf16 bf16x8_v;
+typedef short short4_v __attribute__((ext_vector_type(4)));
+typedef float floatx4_v __attribute__((ext_vector_type(4)));
+
+constexpr int NW = 8;          // waves
+constexpr int NT = NW * 64;
+constexpr int POS = 16;        // new positions per workgroup
+constexpr int KT = 64;         // keys per tile
+constexpr int BS = 16;         // cache block size
+
+struct Params {
+  const bf16_t* q;
+  int64_t q_st, q_sh;          // element strides of (token, head)
+  const void* cu;              // (B+1) offsets of the packed new tokens
+  const void* prefix;          // (B) cached tokens before the new ones
+  int idx_i64;
+  const bf16_t* kbase;
+  const bf16_t* vbase;
+  int64_t num_blocks, sP, sG, sT;
+  const void* tables;
+  int table_i64;
+  int64_t table_stride, max_blocks;
+  const bf16_t* gate;          // (token, H*D) or null
+  int64_t gate_st;
+  bf16_t* out;                 // (token, H, D) contiguous
+  int64_t B;
+  int H, Hkv, G, D;
+  float scale;
+};
+
+template <int D>
+struct Smem {
+  static constexpr int kLdK = D + 8;                   // halfs per K row (16-byte padded)
+  static constexpr int kVtUnits = (KT / 4) * (D + 16); // 8-byte units: [key quad][d] (+pad)
+  static constexpr int kBytes = KT * kLdK * 2 + kVtUnits * 8;
+};
+
+__device__ __forceinline__ int64_t rd_index(const void* base, int is64, int64_t i) {
+  return is64 ? reinterpret_cast<const int64_t*>(base)[i] : reinterpret_cast<const int32_t*>(base)[i];
+}
+
+__device__ __forceinline__ int vt_swz(int d) { return d ^ ((d >> 5) & 7); }
+
+template <int D>
+__global__ __launch_bounds__(NT) void prefill_kernel(Params p) {
+  constexpr int KCH = D / 32;  // k-chunks of S^T
+  constexpr int MT = D / 16;   // output dim tiles
+  extern __shared__ __align__(16) unsigned char smem[];
+  __shared__ int kvalid[KT];  // key of the staged tile has a valid block
+  bf16_t* Ksm = reinterpret_cast<bf16_t*>(smem);
+  uint2* Vt = reinterpret_cast<uint2*>(smem + KT * Smem<D>::kLdK * 2);
+
+  const int pt = blockIdx.x;
+  const int bg = blockIdx.y;
+  const int b = bg / p.Hkv;
+  const int g = bg - b * p.Hkv;
+  const int64_t tok0 = rd_index(p.cu, p.idx_i64, b);
+  const int64_t n_new = rd_index(p.cu, p.idx_i64, b + 1) - tok0;
+  const int64_t n0 = static_cast<int64_t>(pt) * POS;
+  if (n0 >= n_new) return;
+  const int64_t prefix = rd_index(p.prefix, p.idx_i64, b);
+  const int64_t kv_len = prefix + min(n_new, n0 + POS);  // keys any of the 16 positions may see
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int col = lane & 15;   // position within the tile (MFMA column)
+  const int quad = lane >> 4;
+  const bool active = wave < p.G;
+  const int h = g * p.G + (active ? wave : 0);
+  const int64_t my_pos = prefix + n0 + col;  // absolute position of this lane's column
+  const bool row_live = n0 + col < n_new;
+
+  // Q^T operand (B of S^T = K Q^T): lane holds position col, dims 32i + 8*quad + [0, 8)
+  bf16x8_v qreg[KCH];
+  {
+    const bf16_t* qrow = p.q + (tok0 + n0 + col) * p.q_st + static_cast<int64_t>(h) * p.q_sh + 8 * quad;
+#pragma unroll
+    for (int i = 0; i < KCH; ++i) {
+      uint4 raw = make_uint4(0, 0, 0, 0);
+      if (active && row_live) raw = *reinterpret_cast<const uint4*>(qrow + 32 * i);
+      qreg[i] = __builtin_bit_cast(bf16x8_v, raw);
+    }
+  }
+  floatx4_v o[MT];
+#pragma unroll
+  for (int t = 0; t < MT; ++t) o[t] = floatx4_v{0.f, 0.f, 0.f, 0.f};
+  float m_run = -INFINITY;
+  float l_part = 0.f;
+
+  const bf16_t* kb = p.kbase + static_cast<int64_t>(g) * p.sG;
+  const bf16_t* vb = p.vbase + static_cast<int64_t>(g) * p.sG;
+  const int64_t ntiles = (kv_len + KT - 1) / KT;
+  for (int64_t kt = 0; kt < ntiles; ++kt) {
+    const int64_t key0 = kt * KT;
+    // ---- stage K [key][d] and V^T [key quad][d] of this tile
+    {
+      // K: 64 keys x D/8 chunks of 16 bytes
+      constexpr int KCHUNKS = KT * (D / 8);
+      for (int c = tid; c < KCHUNKS; c += NT) {
+        const int key = c / (D / 8);
+        const int dc = c - key * (D / 8);
+        const int64_t t = key0 + key;
+        uint4 val = make_uint4(0, 0, 0, 0);
+        bool ok = false;
+        if (t < kv_len && t / BS < p.max_blocks) {
+          const int64_t phys = rd_index(p.tables, p.table_i64, b * p.table_stride + t / BS);
+          ok = phys >= 0 && phys < p.num_blocks;
+          if (ok) val = *reinterpret_cast<const uint4*>(kb + phys * p.sP + (t % BS) * p.sT + 8 * dc);
+        }
+        *reinterpret_cast<uint4*>(Ksm + key * Smem<D>::kLdK + 8 * dc) = val;
+        if (dc == 0) kvalid[key] = ok;
+      }
+      // V: (key quad, 8-dim chunk) items; 4 rows loaded, packed into 4-key columns
+      constexpr int VITEMS = (KT / 4) * (D / 8);
+      for (int c = tid; c < VITEMS; c += NT) {
+        const int kq = c / (D / 8);
+        const int dc = c - kq * (D / 8);
+        uint4 r4[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int64_t t = key0 + 4 * kq + r;
+          r4[r] = make_uint4(0, 0, 0, 0);
+          if (t < kv_len && t / BS < p.max_blocks) {
+            const int64_t phys = rd_index(p.tables, p.table_i64, b * p.table_stride + t / BS);
+            if (phys >= 0 && phys < p.num_blocks) r4[r] = *reinterpret_cast<const uint4*>(vb + phys * p.sP + (t % BS) * p.sT + 8 * dc);
+          }
+        }
+        const uint32_t* r0 = reinterpret_cast<const uint32_t*>(&r4[0]);
+        const uint32_t* r1 = reinterpret_cast<const uint32_t*>(&r4[1]);
+        const uint32_t* r2 = reinterpret_cast<const uint32_t*>(&r4[2]);
+        const uint32_t* r3 = reinterpret_cast<const uint32_t*>(&r4[3]);
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+          const int d = 8 * dc + 2 * k;
+          uint2 lo, hi;
+          lo.x = __builtin_amdgcn_perm(r1[k], r0[k], 0x05040100u);
+          lo.y = __builtin_amdgcn_perm(r3[k], r2[k], 0x05040100u);
+          hi.x = __builtin_amdgcn_perm(r1[k], r0[k], 0x07060302u);
+          hi.y = __builtin_amdgcn_perm(r3[k], r2[k], 0x07060302u);
+          Vt[kq * (D + 16) + vt_swz(d)] = lo;
+          Vt[kq * (D + 16) + vt_swz(d + 1)] = hi;
+        }
+      }
+    }
+    __syncthreads();
+
+    if (active) {
+      // ---- S^T = K Q^T for the 4 key sub-tiles; mask; online softmax per position
+      floatx4_v s[KT / 16];
+      float mx = -INFINITY;
+#pragma unroll
+      for (int st = 0; st < KT / 16; ++st) {
+        floatx4_v acc = {0.f, 0.f, 0.f, 0.f};
+        const bf16_t* arow = Ksm + (16 * st + (lane & 15)) * Smem<D>::kLdK + 8 * quad;
+#pragma unroll
+        for (int i = 0; i < KCH; ++i)
+          acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(*reinterpret_cast<const bf16x8_v*>(arow + 32 * i), qreg[i], acc, 0, 0, 0);
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int64_t t = key0 + 16 * st + 4 * quad + r;
+          const float v = (row_live && t <= my_pos && t < kv_len && kvalid[16 * st + 4 * quad + r]) ? acc[r] * p.scale : -INFINITY;
+          s[st][r] = v;
+          mx = fmaxf(mx, v);
+        }
+      }
+      mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
+      mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+      const float m_new = fmaxf(m_run, mx);
+      const float m_use = m_new == -INFINITY ? 0.f : m_new;
+      const float alpha = __expf(m_run - m_use);
+      m_run = m_new;
+      short4_v pb[KT / 16];
+      float psum = 0.f;
+#pragma unroll
+      for (int st = 0; st < KT / 16; ++st)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const float pr = __expf(s[st][r] - m_use);
+          psum += pr;
+          pb[st][r] = static_cast<short>(f32_to_bf16(pr));
+        }
+      l_part = l_part * alpha + psum;
+#pragma unroll
+      for (int t = 0; t < MT; ++t) o[t] *= alpha;
+      // ---- O^T += V^T P over the 4 key sub-tiles
+#pragma unroll
+      for (int st = 0; st < KT / 16; ++st) {
+#pragma unroll
+        for (int t = 0; t < MT; ++t) {
+          const uint2 a = Vt[(4 * st + quad) * (D + 16) + vt_swz(16 * t + col)];
+          o[t] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(__builtin_bit_cast(short4_v, a), pb[st], o[t], 0, 0, 0);
+        }
+      }
+    }
+    __syncthreads();
+  }
+
+  if (!active) return;
+  l_part += __shfl_xor(l_part, 16, 64);
+  l_part += __shfl_xor(l_part, 32, 64);
+  if (!row_live) return;
+  const float inv = l_part > 0.f ? 1.f / l_part : 0.f;
+  const int64_t tok = tok0 + n0 + col;
+  bf16_t* orow = p.out + (tok * p.H + h) * static_cast<int64_t>(D);
+  const bf16_t* grow = p.gate != nullptr ? p.gate + tok * p.gate_st + static_cast<int64_t>(h) * D : nullptr;
+#pragma unroll
+  for (int t = 0; t < MT; ++t) {
+    const int d0 = 16 * t + 4 * quad;
+    float v[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      v[r] = o[t][r] * inv;
+      if (grow != nullptr) v[r] *= 1.f / (1.f + __expf(-bf16_to_f32(grow[d0 + r])));
+    }
+    uint2 packed;
+    packed.x = static_cast<uint32_t>(f32_to_bf16(v[0])) | (static_cast<uint32_t>(f32_to_bf16(v[1])) << 16);
+    packed.y = static_cast<uint32_t>(f32_to_bf16(v[2])) | (static_cast<uint32_t>(f32_to_bf16(v[3])) << 16);
+    *reinterpret_cast<uint2*>(orow + d0) = packed;
+  }
+}
+
+}  // namespace pfx
+}  // namespace qa
+
+extern "C" int qa_paged_attention_prefill(const void* query, int32_t q_dtype, int64_t q_stride_t, int64_t q_stride_h,
+                                          const void* cu_seqlens, const void* prefix_lens, int32_t idx_dtype,
+                                          int64_t batch, int64_t max_new, int32_t heads, int32_t head_dim,
+                                          const qa_paged_kv* kv, const void* block_tables, int32_t table_dtype,
+                                          int64_t table_stride, int64_t max_blocks, int32_t block_size, float scale,
+                                          const void* gate, int64_t gate_stride_t, void* output, hipStream_t stream) {
+  using namespace qa;
+  using namespace qa::pfx;
+  QA_REQUIRE(kv != nullptr && query && cu_seqlens && prefix_lens && block_tables && output, "paged prefill: pointers must be non-null");
+  QA_REQUIRE(q_dtype == QA_BF16 && kv->dtype == QA_BF16, "paged prefill: query and KV must be bfloat16");
+  QA_REQUIRE(is_index_dtype(idx_dtype) && is_index_dtype(table_dtype), "paged prefill: index arrays must be int32/int64");
+  QA_REQUIRE(head_dim == 128 || head_dim == 256, "paged prefill: head_dim must be 128 or 256");
+  QA_REQUIRE(block_size == BS, "paged prefill: block_size must be 16");
+  QA_REQUIRE(kv->kv_heads > 0 && heads % kv->kv_heads == 0, "paged prefill: query heads must be a multiple of KV heads");
+  QA_REQUIRE(heads / kv->kv_heads <= NW, "paged prefill: GQA group larger than %d", NW);
+  QA_REQUIRE(kv->row_key_ptrs == nullptr && kv->key && kv->value, "paged prefill: needs one shared pool");
+  QA_REQUIRE(kv->stride_token % 8 == 0 && kv->stride_block % 8 == 0 && kv->stride_head % 8 == 0 &&
+                 ((reinterpret_cast<uintptr_t>(kv->key) | reinterpret_cast<uintptr_t>(kv->value)) & 15u) == 0,
+             "paged prefill: KV rows must be 16-byte aligned");
+  QA_REQUIRE(q_stride_t % 8 == 0 && q_stride_h % 8 == 0 && (reinterpret_cast<uintptr_t>(query) & 15u) == 0,
+             "paged prefill: query rows must be 16-byte aligned");
+  QA_REQUIRE(batch > 0 && batch * kv->kv_heads <= 65535, "paged prefill: bad batch");
+  if (max_new <= 0) return 0;
+  Params p{};
+  p.q = reinterpret_cast<const bf16_t*>(query);
+  p.q_st = q_stride_t;
+  p.q_sh = q_stride_h;
+  p.cu = cu_seqlens;
+  p.prefix = prefix_lens;
+  p.idx_i64 = idx_dtype == QA_I64;
+  p.kbase = reinterpret_cast<const bf16_t*>(kv->key);
+  p.vbase = reinterpret_cast<const bf16_t*>(kv->value);
+  p.num_blocks = kv->num_blocks;
+  p.sP = kv->stride_block;
+  p.sG = kv->stride_head;
+  p.sT = kv->stride_token;
+  p.tables = block_tables;
+  p.table_i64 = table_dtype == QA_I64;
+  p.table_stride = table_stride;
+  p.max_blocks = max_blocks;
+  p.gate = reinterpret_cast<const bf16_t*>(gate);
+  p.gate_st = gate_stride_t;
+  p.out = reinterpret_cast<bf16_t*>(output);
+  p.B = batch;
+  p.H = heads;
+  p.Hkv = kv->kv_heads;
+  p.G = heads / kv->kv_heads;
+  p.D = head_dim;
+  p.scale = scale > 0.f ? scale : 1.0f / sqrtf(static_cast<float>(head_dim));
+  dim3 grid(static_cast<unsigned>(ceil_div(max_new, POS)), static_cast<unsigned>(batch * kv->kv_heads));
+  static bool attr_set = false;
+  if (!attr_set) {
+    hipError_t err = hipFuncSetAttribute(reinterpret_cast<const void*>(&prefill_kernel<256>), hipFuncAttributeMaxDynamicSharedMemorySize,
+                                         Smem<256>::kBytes);
+    if (err != hipSuccess) return fail("paged prefill: cannot reserve %d bytes of LDS: %s", Smem<256>::kBytes, hipGetErrorString(err));
+    attr_set = true;
+  }
+  if (head_dim == 256) {
+    hipLaunchKernelGGL(prefill_kernel<256>, grid, dim3(NT), Smem<256>::kBytes, stream, p);
+  } else {
+    hipLaunchKernelGGL(prefill_kernel<128>, grid, dim3(NT), Smem<128>::kBytes, stream, p);
+  }
+  return check_launch("paged prefill");
+}

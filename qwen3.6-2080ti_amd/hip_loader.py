@@ -103,6 +103,11 @@ SIGNATURES: dict[str, tuple[Any, list[Any]]] = {
          c_int32, c_void_p],
     ),
     "qa_chunk_gated_delta_lds_bytes": (c_int64, []),
+    "qa_paged_attention_prefill": (
+        c_int32,
+        [c_void_p, c_int32, c_int64, c_int64, c_void_p, c_void_p, c_int32, c_int64, c_int64, c_int32, c_int32, ctypes.POINTER(PagedKV),
+         c_void_p, c_int32, c_int64, c_int64, c_int32, c_float, c_void_p, c_int64, c_void_p, c_void_p],
+    ),
 }
 
 

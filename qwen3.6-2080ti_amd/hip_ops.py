@@ -589,3 +589,55 @@ def chunk_gated_delta_rule(
     )
     L.check(lib, status, "chunk_gated_delta_rule")
     return out, final, conv_out
+
+
+def paged_attention_prefill(
+    query: torch.Tensor,
+    cu_seqlens: torch.Tensor,
+    prefix_lens: torch.Tensor,
+    key_pool: torch.Tensor,
+    value_pool: torch.Tensor,
+    block_tables: torch.Tensor,
+    block_size: int,
+    *,
+    max_new: int,
+    gate: torch.Tensor | None = None,
+    scale: float | None = None,
+) -> torch.Tensor:
+    """Causal attention of packed new tokens over the shared paged pool, with optional gate.
+
+    ``query`` ``(total_new, H, D)`` bf16; ``cu_seqlens`` ``(B+1,)`` and
+    ``prefix_lens`` ``(B,)`` device index arrays; the new tokens' K/V must
+    already be appended to ``key_pool``/``value_pool`` ``(P, H_kv, bs, D)`` at
+    positions ``prefix_b + n``.  ``gate`` ``(total_new, H*D)`` bf16 logits give
+    ``out * sigmoid(gate)`` (``src/reference_ops.py:338-340,360``).  Returns
+    ``(total_new, H, D)`` bf16.
+    """
+    lib = L.load_library()
+    _require_cuda(query, "query")
+    device = query.device
+    _require(query.dtype == torch.bfloat16 and query.dim() == 3 and query.stride(-1) == 1, "query must be (tokens, heads, head_dim) bfloat16")
+    for tensor, name in ((cu_seqlens, "cu_seqlens"), (prefix_lens, "prefix_lens"), (block_tables, "block_tables")):
+        _require_cuda(tensor, name, device)
+        _index_dtype(tensor, name)
+    _require(cu_seqlens.dtype == prefix_lens.dtype, "cu_seqlens and prefix_lens must share a dtype")
+    _require(key_pool.dim() == 4, "prefill needs a shared pool (blocks, kv_heads, block_size, head_dim)")
+    desc = _pool_descriptor(key_pool, value_pool, "shared")
+    batch = prefix_lens.shape[0]
+    _require(cu_seqlens.shape[0] == batch + 1, "cu_seqlens must have batch + 1 entries")
+    tokens, heads, head_dim = query.shape
+    gate_c = None
+    if gate is not None:
+        _require_cuda(gate, "gate", device)
+        _require(gate.dtype == torch.bfloat16 and gate.shape == (tokens, heads * head_dim), "gate must be (tokens, heads*head_dim) bfloat16")
+        gate_c = gate.contiguous()
+    tables = block_tables.contiguous()
+    out = torch.empty((tokens, heads, head_dim), dtype=torch.bfloat16, device=device)
+    status = lib.qa_paged_attention_prefill(
+        _ptr(query), _code(query), query.stride(0), query.stride(1), _ptr(cu_seqlens.contiguous()), _ptr(prefix_lens.contiguous()),
+        _code(cu_seqlens), batch, int(max_new), heads, head_dim, ctypes.byref(desc), _ptr(tables), _code(tables), tables.stride(0),
+        tables.shape[1], int(block_size), float(scale or 0.0), _ptr(gate_c), 0 if gate_c is None else gate_c.stride(0), _ptr(out),
+        _stream(device),
+    )
+    L.check(lib, status, "paged_attention_prefill")
+    return out
