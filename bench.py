@@ -205,6 +205,72 @@ def time_delta(w, steps: int, warmup: int) -> float:
     return start.elapsed_time(end) / steps
 
 
+# ----------------------------------------------------------------------------- config 3
+
+
+def prefill_workload(device: str, *, seed: int = 0, batch: int = 8, new: int = 4096, heads: int = 16, kv_heads: int = 2, dim: int = 256,
+                     bs: int = 16, max_prefix: int = 8192, chunk: int = 512):
+    import torch
+
+    gen = torch.Generator().manual_seed(seed)
+    prefixes = torch.randint(0, max_prefix + 1, (batch,), generator=gen)
+    totals = prefixes + new
+    need = [(int(t) + bs - 1) // bs for t in totals]
+    pool_blocks = math.ceil(sum(need) * 1.25)
+    perm = torch.randperm(pool_blocks, generator=gen)
+    tables = torch.full((batch, max(need)), -1, dtype=torch.int32)
+    cursor = 0
+    for b, n in enumerate(need):
+        tables[b, :n] = perm[cursor : cursor + n].to(torch.int32)
+        cursor += n
+    dgen = torch.Generator(device=device).manual_seed(seed)
+    key_pool = torch.randn((pool_blocks, kv_heads, bs, dim), generator=dgen, device=device, dtype=torch.bfloat16)
+    value_pool = torch.randn((pool_blocks, kv_heads, bs, dim), generator=dgen, device=device, dtype=torch.bfloat16)
+    q = torch.randn((batch * new, heads, dim), generator=dgen, device=device, dtype=torch.bfloat16)
+    gate = torch.randn((batch * new, heads * dim), generator=dgen, device=device, dtype=torch.bfloat16)
+    new_k = torch.randn((batch, kv_heads, new, dim), generator=dgen, device=device, dtype=torch.bfloat16)
+    new_v = torch.randn((batch, kv_heads, new, dim), generator=dgen, device=device, dtype=torch.bfloat16)
+    flops = sum(4 * heads * dim * (new * int(p) + new * (new + 1) / 2) for p in prefixes)
+    return {"q": q, "gate": gate, "new_k": new_k, "new_v": new_v, "key_pool": key_pool, "value_pool": value_pool, "tables": tables.to(device),
+            "prefixes": prefixes, "batch": batch, "new": new, "chunk": chunk, "bs": bs, "flops": flops, "pool_blocks": pool_blocks}
+
+
+def time_prefill(w, steps: int, warmup: int) -> float:
+    """One step = the whole prefill batch in query chunks: append the chunk's K/V, then attend."""
+    import torch
+
+    import hip_ops
+
+    device = w["q"].device
+    batch, new, chunk = w["batch"], w["new"], w["chunk"]
+    plan = []
+    for c0 in range(0, new, chunk):
+        n = min(chunk, new - c0)
+        starts = (w["prefixes"] + c0).to(device=device, dtype=torch.int32)
+        cu = torch.arange(0, batch + 1, device=device, dtype=torch.int32) * n
+        rows = torch.cat([torch.arange(b * new + c0, b * new + c0 + n) for b in range(batch)]).to(device)
+        plan.append((c0, n, starts, cu, w["q"].index_select(0, rows).contiguous(), w["gate"].index_select(0, rows).contiguous()))
+
+    def step():
+        for c0, n, starts, cu, q, gate in plan:
+            hip_ops.paged_kv_append(w["new_k"][:, :, c0 : c0 + n], w["new_v"][:, :, c0 : c0 + n], w["key_pool"], w["value_pool"], w["tables"],
+                                    starts, w["bs"])
+            hip_ops.paged_attention_prefill(q, cu, starts, w["key_pool"], w["value_pool"], w["tables"], w["bs"], max_new=n, gate=gate)
+
+    for _ in range(warmup):
+        step()
+    torch.cuda.synchronize()
+    stream = torch.cuda.current_stream()
+    start = torch.cuda.Event(enable_timing=True)
+    end = torch.cuda.Event(enable_timing=True)
+    start.record(stream)
+    for _ in range(steps):
+        step()
+    end.record(stream)
+    torch.cuda.synchronize()
+    return start.elapsed_time(end) / steps
+
+
 # ----------------------------------------------------------------------------- main
 
 
@@ -215,6 +281,7 @@ def main() -> int:
     parser.add_argument("--warmup", type=int, default=5)
     parser.add_argument("--no-cpu-baseline", action="store_true")
     parser.add_argument("--no-delta", action="store_true", help="skip the config-4 secondary measurement")
+    parser.add_argument("--no-prefill", action="store_true", help="skip the config-3 secondary measurement")
     parser.add_argument("--cpu-budget", type=float, default=12.0)
     args = parser.parse_args()
     if args.gpus != 1:
@@ -290,6 +357,25 @@ def main() -> int:
                          "algo_bytes_per_launch": dw["algo_bytes"], "kernel": "qa::cgd::chunk_kernel (fp16 MFMA, fp32 accumulate)"},
         }
         del dw
+        torch.cuda.empty_cache()
+    if not args.no_prefill:
+        _log("bench: building config-3 workload (chunked paged prefill with gate)")
+        pw = prefill_workload(device)
+        pms = time_prefill(pw, max(2, args.steps // 4), 1)
+        ptf = pw["flops"] / (pms * 1e-3) / 1e12
+        _log(f"bench: paged prefill {pms:.3f} ms, {ptf:.1f} TFLOP/s ({ptf / MFMA_BF16_PEAK_TFLOPS:.1%} of MFMA peak)")
+        record["secondary_prefill"] = {
+            "metric": "chunked paged prefill TFLOP/s (BASELINE config 3)",
+            "value": round(ptf, 2),
+            "unit": "TFLOP/s",
+            "ms_per_step": round(pms, 4),
+            "config": {"workload": "chunked causal paged prefill with sigmoid gate (BASELINE config 3)", "batch": 8, "new_tokens": 4096,
+                       "prefix": "U[0, 8192] seed 0", "q_heads": 16, "kv_heads": 2, "head_dim": 256, "block_size": 16, "query_chunk": 512},
+            "roofline": {"bound": "mfma", "achieved": round(ptf, 2), "peak": MFMA_BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
+                         "frac": round(ptf / MFMA_BF16_PEAK_TFLOPS, 4), "traffic": None, "algo_flop_per_launch": pw["flops"],
+                         "kernel": "qa::pfx::prefill_kernel<256> + kv_append per 512-token query chunk"},
+        }
+        del pw
         torch.cuda.empty_cache()
     if not args.no_cpu_baseline:
         _log("bench: CPU baseline (reference path restatement)")
