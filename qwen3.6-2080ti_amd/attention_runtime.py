@@ -1,0 +1,361 @@
+"""Attention entry points of the hybrid runtime at TP = 1, on the gfx950 kernels.
+
+Mirrors the attention side of the reference's ``src/tp_runtime.py`` so the
+engine and scheduler above it keep their calls:
+
+* ``PagedAttentionDispatchStats`` (``:90-107``) and the dispatch reason ladder
+  ``paged_attention_fallback_reason`` (``:770-805``),
+  ``batched_paged_attention_fallback_reason`` (``:646-669``),
+  ``record_native_paged_dispatch`` (``:747-767``) and
+  ``record_paged_attention_dispatch`` (``:733-744``) -- same reason strings and
+  counters.  One difference: bfloat16 tensors are eligible (the gfx950 decode
+  kernel computes bf16 natively; the reference kernel was fp32-only, so it
+  reported them as ``"shape"``).
+* ``full_attention_paged`` / ``full_attention_paged_batch``: the native branch
+  of ``_tp_full_attention_paged_or_dense`` (``:551-610``) and its batched twin
+  (``:2498-2555``) including the sigmoid output gate (``:673-695``) but not the
+  output projection.  When the ladder says the native kernel does not apply,
+  they return ``None`` and the caller runs its own dense path, as the
+  reference does; a native ``RuntimeError`` is recorded as a fallback and also
+  returns ``None``.
+* ``recurrent_gated_delta_rule`` (``:2744-2787``) on the HIP recurrent core,
+  ``linear_attention_decode_batch`` (the state plumbing of ``:2613-2717``) on a
+  slot-indexed state pool, and ``linear_attention_prefill`` on the chunked
+  kernel.
+
+Host-side tensor preparation (L2 norm, transposes) is PyTorch on the same
+device; every hot loop is a HIP kernel.  There is no CPU or dense fallback in
+this module.
+"""
+
+from __future__ import annotations
+
+import contextlib
+from dataclasses import dataclass, field
+from typing import Any, Iterator, Sequence
+
+from decode_state import FullAttentionCache, LinearStatePool, batch_page_tables
+
+# --------------------------------------------------------------------------- config
+
+
+@dataclass(frozen=True)
+class FullAttentionConfig:
+    """Full-attention fields of ``src/runtime_config.py:33-52`` that the hot path reads."""
+
+    num_heads: int
+    num_key_value_heads: int
+    head_dim: int
+    output_gate: bool = True
+    paged_kv_metadata: bool = True
+    native_paged_attention: bool = False
+
+    @property
+    def attn_dim(self) -> int:
+        return self.num_heads * self.head_dim
+
+
+@dataclass(frozen=True)
+class LinearAttentionConfig:
+    """``LinearAttentionConfig`` of ``src/runtime_config.py:15-30``."""
+
+    key_heads: int
+    value_heads: int
+    key_head_dim: int
+    value_head_dim: int
+    conv_kernel_dim: int
+
+    @property
+    def qkv_dim(self) -> int:
+        return self.key_heads * self.key_head_dim * 2 + self.value_heads * self.value_head_dim
+
+    @property
+    def value_state_dim(self) -> int:
+        return self.value_heads * self.value_head_dim
+
+
+@dataclass(frozen=True)
+class AttentionConfig:
+    full_attention: FullAttentionConfig
+    linear_attention: LinearAttentionConfig
+
+
+def parse_attention_config(config: dict[str, Any]) -> AttentionConfig:
+    """Read the hot-path fields of an HF ``config.json`` (``src/runtime_config.py:92-131``)."""
+    text = config.get("text_config", config)
+
+    def need(key: str) -> Any:
+        if key not in text:
+            raise ValueError(f"missing text_config.{key}")
+        return text[key]
+
+    return AttentionConfig(
+        full_attention=FullAttentionConfig(
+            num_heads=int(need("num_attention_heads")),
+            num_key_value_heads=int(need("num_key_value_heads")),
+            head_dim=int(need("head_dim")),
+            output_gate=bool(need("attn_output_gate")),
+            paged_kv_metadata=bool(text.get("paged_kv_metadata", True)),
+            native_paged_attention=bool(text.get("native_paged_attention", False)),
+        ),
+        linear_attention=LinearAttentionConfig(
+            key_heads=int(need("linear_num_key_heads")),
+            value_heads=int(need("linear_num_value_heads")),
+            key_head_dim=int(need("linear_key_head_dim")),
+            value_head_dim=int(need("linear_value_head_dim")),
+            conv_kernel_dim=int(need("linear_conv_kernel_dim")),
+        ),
+    )
+
+
+# --------------------------------------------------------------------------- dispatch accounting
+
+
+@dataclass
+class PagedAttentionDispatchStats:
+    calls: int = 0
+    eligible: int = 0
+    dense_fallbacks: int = 0
+    native_hits: int = 0
+    fallback_disabled: int = 0
+    fallback_no_kernel: int = 0
+    fallback_prefill_or_multitoken: int = 0
+    fallback_cpu: int = 0
+    fallback_per_request_pools: int = 0
+    fallback_shape: int = 0
+
+    def snapshot(self) -> "PagedAttentionDispatchStats":
+        return PagedAttentionDispatchStats(**vars(self))
+
+    def to_dict(self) -> dict[str, int]:
+        return dict(vars(self))
+
+
+@dataclass
+class HotPathRuntime:
+    """The slice of ``TpRuntime`` the attention entry points use at TP = 1: counters and profile scopes."""
+
+    paged_attention_stats: PagedAttentionDispatchStats = field(default_factory=PagedAttentionDispatchStats)
+    scope_calls: dict[str, int] = field(default_factory=dict)
+
+    @contextlib.contextmanager
+    def profile_scope(self, name: str) -> Iterator[None]:
+        self.scope_calls[name] = self.scope_calls.get(name, 0) + 1
+        yield
+
+
+_FLOAT_DTYPES = ("torch.float32", "torch.bfloat16")
+
+
+def paged_attention_fallback_reason(config: AttentionConfig, query: Any, key: Any, value: Any, *, seq_len: int, batched: bool) -> str:
+    """Reason ladder of ``src/tp_runtime.py:770-805`` (``"no_kernel"`` = eligible)."""
+    full = config.full_attention
+    if not full.paged_kv_metadata or not full.native_paged_attention:
+        return "disabled"
+    if not all(getattr(t, "is_cuda", False) for t in (query, key, value)):
+        return "cpu"
+    if seq_len != 1:
+        return "prefill_or_multitoken"
+    if batched:
+        return "per_request_pools"
+    q_shape = tuple(getattr(query, "shape", ()))
+    k_shape = tuple(getattr(key, "shape", ()))
+    v_shape = tuple(getattr(value, "shape", ()))
+    if len(q_shape) != 4 or len(k_shape) not in (4, 5) or len(v_shape) != len(k_shape):
+        return "shape"
+    if len(k_shape) == 5:
+        # reference per-request layout (batch, heads, P, bs, D): batch and heads follow the query
+        if q_shape[0] != k_shape[0] or q_shape[0] != v_shape[0]:
+            return "shape"
+        if q_shape[1] % k_shape[1] or k_shape[1] != v_shape[1]:
+            return "shape"
+    elif k_shape[1] != v_shape[1] or q_shape[1] % k_shape[1]:
+        return "shape"
+    if q_shape[3] != k_shape[-1] or q_shape[3] != v_shape[-1]:
+        return "shape"
+    q_dtype = getattr(query, "dtype", None)
+    if q_dtype is not None:
+        k_dtype = getattr(key, "dtype", q_dtype)
+        v_dtype = getattr(value, "dtype", q_dtype)
+        if str(q_dtype) not in _FLOAT_DTYPES or str(k_dtype) not in _FLOAT_DTYPES or str(k_dtype) != str(v_dtype):
+            return "shape"
+    return "no_kernel"
+
+
+def batched_paged_attention_fallback_reason(config: AttentionConfig, query: Any, caches: Sequence[FullAttentionCache], page_tables: Any, *, seq_len: int) -> str:
+    """``src/tp_runtime.py:646-669``: every row must be eligible on its own."""
+    if page_tables is None:
+        return "disabled"
+    if not caches:
+        return "shape"
+    for row, cache in enumerate(caches):
+        reason = paged_attention_fallback_reason(config, query[row : row + 1], cache.key_blocks, cache.value_blocks, seq_len=seq_len, batched=False)
+        if reason != "no_kernel":
+            return reason
+    return "no_kernel"
+
+
+def record_native_paged_dispatch(runtime: HotPathRuntime, reason: str, *, native: bool) -> None:
+    """``src/tp_runtime.py:747-767``."""
+    stats = runtime.paged_attention_stats
+    stats.calls += 1
+    if reason == "no_kernel":
+        stats.eligible += 1
+    if native:
+        stats.native_hits += 1
+        return
+    stats.dense_fallbacks += 1
+    counter = {
+        "disabled": "fallback_disabled",
+        "cpu": "fallback_cpu",
+        "prefill_or_multitoken": "fallback_prefill_or_multitoken",
+        "per_request_pools": "fallback_per_request_pools",
+        "shape": "fallback_shape",
+    }.get(reason, "fallback_no_kernel")
+    setattr(stats, counter, getattr(stats, counter) + 1)
+
+
+def record_paged_attention_dispatch(runtime: HotPathRuntime, config: AttentionConfig, query: Any, key: Any, value: Any, *, seq_len: int, batched: bool) -> None:
+    """``src/tp_runtime.py:733-744``."""
+    reason = paged_attention_fallback_reason(config, query, key, value, seq_len=seq_len, batched=batched)
+    record_native_paged_dispatch(runtime, reason, native=False)
+
+
+# --------------------------------------------------------------------------- full attention
+
+
+def _gate_heads(heads: Any, gate: Any) -> Any:
+    """``out * sigmoid(gate)`` on ``(B, H, 1, D)`` heads with ``gate`` ``(B, 1, H*D)`` (``src/tp_runtime.py:689-691``)."""
+    import torch
+
+    batch, num_heads, seq, dim = heads.shape
+    out = heads.transpose(1, 2).reshape(batch, seq, num_heads * dim)
+    return out * torch.sigmoid(gate.to(out.dtype))
+
+
+def full_attention_paged(query: Any, gate: Any | None, cache: FullAttentionCache, config: AttentionConfig, runtime: HotPathRuntime) -> Any | None:
+    """Native branch of ``_tp_full_attention_paged_or_dense`` (``src/tp_runtime.py:551-610``).
+
+    ``query`` ``(B, H, 1, D)`` after RoPE, with the step's K/V already appended
+    to ``cache``.  Returns the gated attention output ``(B, 1, H*D)`` (before
+    ``o_proj``), or ``None`` when the caller must take its dense path.
+    """
+    page_table = cache.page_metadata() if config.full_attention.paged_kv_metadata else None
+    reason = paged_attention_fallback_reason(
+        config, query, None if page_table is None else page_table.key_blocks, None if page_table is None else page_table.value_blocks,
+        seq_len=int(query.shape[2]), batched=False,
+    )
+    if reason != "no_kernel" or page_table is None:
+        record_native_paged_dispatch(runtime, reason, native=False)
+        return None
+    import hip_ops
+
+    try:
+        with runtime.profile_scope("full_attention.native_paged"):
+            heads = hip_ops.paged_attention_decode(
+                query, page_table.block_table, page_table.key_blocks, page_table.value_blocks, page_table.sequence_length, page_table.block_size
+            )
+    except RuntimeError:
+        record_native_paged_dispatch(runtime, "no_kernel", native=False)
+        return None
+    record_native_paged_dispatch(runtime, reason, native=True)
+    return heads if gate is None else _gate_heads(heads, gate)
+
+
+def full_attention_paged_batch(query: Any, gate: Any | None, caches: Sequence[FullAttentionCache], config: AttentionConfig, runtime: HotPathRuntime) -> Any | None:
+    """Native branch of ``_tp_full_attention_batch_paged_or_dense`` (``src/tp_runtime.py:2498-2555``).
+
+    Caches may each own a reference-layout pool or share one
+    ``SharedKVBlockPool``; either way one kernel launch serves the batch.
+    """
+    page_tables = batch_page_tables(caches) if config.full_attention.paged_kv_metadata else None
+    reason = batched_paged_attention_fallback_reason(config, query, caches, page_tables, seq_len=int(query.shape[2]))
+    if reason != "no_kernel" or page_tables is None:
+        record_native_paged_dispatch(runtime, reason, native=False)
+        return None
+    import hip_ops
+
+    try:
+        with runtime.profile_scope("batch.full_attention.native_paged"):
+            heads = hip_ops.paged_attention_decode_batched(
+                query, page_tables.block_tables, list(page_tables.key_blocks), list(page_tables.value_blocks), page_tables.sequence_lengths,
+                page_tables.block_size,
+            )
+    except RuntimeError:
+        record_native_paged_dispatch(runtime, "no_kernel", native=False)
+        return None
+    record_native_paged_dispatch(runtime, reason, native=True)
+    return heads if gate is None else _gate_heads(heads, gate)
+
+
+# --------------------------------------------------------------------------- linear attention
+
+
+def prepare_recurrent_inputs(query: Any, key: Any, value: Any, g: Any, beta: Any, initial_state: Any = None) -> tuple[Any, ...]:
+    """``_prepare_recurrent_gated_delta_inputs`` (``src/tp_runtime.py:2790-2805``), on the inputs' device."""
+    import torch
+
+    def l2(x: Any) -> Any:
+        x = x.float()
+        return x * (x * x).sum(dim=-1, keepdim=True).add(1e-6).rsqrt()
+
+    q = l2(query).transpose(1, 2).float().contiguous()
+    k = l2(key).transpose(1, 2).float().contiguous()
+    v = value.transpose(1, 2).float().contiguous()
+    b = beta.transpose(1, 2).float().contiguous()
+    gg = g.transpose(1, 2).float().contiguous()
+    batch, heads, _, key_dim = k.shape
+    q = (q * (key_dim**-0.5)).contiguous()
+    if initial_state is None:
+        state = torch.zeros(batch, heads, key_dim, v.shape[-1], device=q.device, dtype=torch.float32)
+    else:
+        state = initial_state.to(device=q.device, dtype=torch.float32).contiguous()
+    return q, k, v, gg, b, state
+
+
+def recurrent_gated_delta_rule(query: Any, key: Any, value: Any, g: Any, beta: Any, *, initial_state: Any = None, return_state: bool = False) -> Any:
+    """``_recurrent_gated_delta_rule`` (``src/tp_runtime.py:2744-2787``) on the HIP recurrent core.
+
+    Token-major ``(B, S, H, d)`` inputs; returns ``(B, S, H, dv)`` in the query
+    dtype (and the fp32 final state).  CUDA tensors only: a missing library
+    raises ``RuntimeError`` instead of falling back.
+    """
+    import hip_ops
+
+    initial_dtype = query.dtype
+    q, k, v, gg, b, state = prepare_recurrent_inputs(query, key, value, g, beta, initial_state)
+    output, final_state = hip_ops.linear_attention_recurrent_core(q, k, v, gg, b, state)
+    out = output.transpose(1, 2).contiguous().to(initial_dtype)
+    return (out, final_state) if return_state else out
+
+
+def linear_attention_decode_batch(
+    mixed_qkv: Any, a: Any, b: Any, a_log: Any, dt_bias: Any, conv_weight: Any, pool: LinearStatePool, slots: Any, config: AttentionConfig, *, out_dtype: Any = None
+) -> Any:
+    """One decode token of a linear-attention layer for a batch of requests.
+
+    ``mixed_qkv`` ``(B, qkv_dim)``, ``a``/``b`` ``(B, Hv)`` are the
+    ``in_proj_*`` outputs of the step; request ``r`` keeps its conv and
+    recurrent state in row ``slots[r]`` of ``pool`` (updated in place).
+    Returns the core output ``(B, Hv, dv)`` before the gated RMSNorm.  This
+    replaces the stack / run / scatter of ``src/tp_runtime.py:2613-2717``.
+    """
+    import torch
+
+    import hip_ops
+
+    lin = config.linear_attention
+    act = hip_ops.causal_conv1d_update(mixed_qkv, pool.conv, conv_weight, slots)
+    return hip_ops.gated_delta_step(act, a, b, a_log, dt_bias, pool.state, key_heads=lin.key_heads, slots=slots,
+                                    out_dtype=torch.bfloat16 if out_dtype is None else out_dtype)
+
+
+def linear_attention_prefill(mixed_qkv: Any, a: Any, b: Any, a_log: Any, dt_bias: Any, conv_weight: Any, config: AttentionConfig, *, conv_state: Any = None, initial_state: Any = None) -> tuple[Any, Any, Any]:
+    """Prefill of a linear-attention layer on the chunked kernel (``src/reference_ops.py:240-283``)."""
+    import hip_ops
+
+    lin = config.linear_attention
+    return hip_ops.chunk_gated_delta_rule(
+        mixed_qkv, a, b, a_log, dt_bias, conv_weight, key_heads=lin.key_heads, value_heads=lin.value_heads, conv_state=conv_state,
+        initial_state=initial_state,
+    )

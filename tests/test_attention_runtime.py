@@ -1,0 +1,120 @@
+"""Dispatch ladder and counters against the reference's own tests (CPU).
+
+Restates ``tests/unit/test_tp_runtime.py:627-751`` of the reference on this
+package's ``attention_runtime``; the config dict is the reference's
+``_config()`` (``tests/unit/test_tp_runtime.py:1123-1149``).
+"""
+
+from __future__ import annotations
+
+from dataclasses import replace
+from types import SimpleNamespace
+
+import pytest
+import torch
+
+import attention_runtime as ar
+from decode_state import FullAttentionCache, batch_page_tables
+
+
+def _config(**full_overrides) -> ar.AttentionConfig:
+    text = {
+        "linear_num_key_heads": 1,
+        "linear_num_value_heads": 1,
+        "linear_key_head_dim": 1,
+        "linear_value_head_dim": 1,
+        "linear_conv_kernel_dim": 4,
+        "num_attention_heads": 2,
+        "num_key_value_heads": 1,
+        "head_dim": 1,
+        "attn_output_gate": True,
+    }
+    cfg = ar.parse_attention_config({"text_config": text})
+    return replace(cfg, full_attention=replace(cfg.full_attention, **full_overrides)) if full_overrides else cfg
+
+
+def _enabled() -> ar.AttentionConfig:
+    return _config(paged_kv_metadata=True, native_paged_attention=True)
+
+
+def _fake_cuda(shape):
+    return SimpleNamespace(shape=shape, is_cuda=True)
+
+
+def _stats_after(config, query, key, value, *, seq_len, batched):
+    runtime = ar.HotPathRuntime()
+    ar.record_paged_attention_dispatch(runtime, config, query, key, value, seq_len=seq_len, batched=batched)
+    return runtime.paged_attention_stats
+
+
+def test_disabled_by_default() -> None:  # :627-645
+    stats = _stats_after(_config(), torch.zeros(1, 1, 1, 1), torch.zeros(1, 1, 1, 1), torch.zeros(1, 1, 1, 1), seq_len=1, batched=False)
+    assert (stats.calls, stats.dense_fallbacks, stats.fallback_disabled, stats.eligible, stats.native_hits) == (1, 1, 1, 0, 0)
+
+
+def test_cpu_fallback_when_enabled() -> None:  # :648-666
+    stats = _stats_after(_enabled(), torch.zeros(1, 1, 1, 1), torch.zeros(1, 1, 1, 1), torch.zeros(1, 1, 1, 1), seq_len=1, batched=False)
+    assert (stats.calls, stats.dense_fallbacks, stats.fallback_cpu, stats.eligible) == (1, 1, 1, 0)
+
+
+def test_prefill_or_multitoken_fallback() -> None:  # :669-687
+    f = _fake_cuda((1, 1, 2, 1))
+    stats = _stats_after(_enabled(), f, f, f, seq_len=2, batched=False)
+    assert (stats.dense_fallbacks, stats.fallback_prefill_or_multitoken, stats.eligible) == (1, 1, 0)
+
+
+def test_per_request_pool_fallback_for_batches() -> None:  # :690-708
+    f = _fake_cuda((2, 1, 1, 1))
+    stats = _stats_after(_enabled(), f, f, f, seq_len=1, batched=True)
+    assert (stats.dense_fallbacks, stats.fallback_per_request_pools, stats.eligible) == (1, 1, 0)
+
+
+def test_native_hit() -> None:  # :711-720
+    runtime = ar.HotPathRuntime()
+    ar.record_native_paged_dispatch(runtime, "no_kernel", native=True)
+    s = runtime.paged_attention_stats
+    assert (s.calls, s.eligible, s.native_hits, s.dense_fallbacks, s.fallback_no_kernel) == (1, 1, 1, 0, 0)
+
+
+def test_native_exception_counts_as_no_kernel_fallback() -> None:
+    runtime = ar.HotPathRuntime()
+    ar.record_native_paged_dispatch(runtime, "no_kernel", native=False)
+    s = runtime.paged_attention_stats
+    assert (s.eligible, s.dense_fallbacks, s.fallback_no_kernel) == (1, 1, 1)
+
+
+def test_batched_reason_disabled_without_page_tables() -> None:  # :723-733
+    cache = FullAttentionCache(block_size=2)
+    cache.append_blocks(torch.zeros(1, 2, 1, 4), torch.zeros(1, 2, 1, 4))
+    assert ar.batched_paged_attention_fallback_reason(_enabled(), torch.zeros(1, 2, 1, 4), [cache], None, seq_len=1) == "disabled"
+
+
+def test_batched_reason_cpu_for_cpu_caches() -> None:  # :736-746
+    cache = FullAttentionCache(block_size=2)
+    cache.append_blocks(torch.zeros(1, 2, 1, 4), torch.zeros(1, 2, 1, 4))
+    tables = batch_page_tables([cache])
+    assert ar.batched_paged_attention_fallback_reason(_enabled(), torch.zeros(1, 2, 1, 4), [cache], tables, seq_len=1) == "cpu"
+
+
+@pytest.mark.parametrize(
+    "dtype,expected",
+    [("torch.float32", "no_kernel"), ("torch.bfloat16", "no_kernel"), ("torch.float16", "shape")],
+)
+def test_dtype_eligibility(dtype, expected) -> None:
+    q = SimpleNamespace(shape=(1, 16, 1, 256), is_cuda=True, dtype=dtype)
+    kv = SimpleNamespace(shape=(1, 2, 8, 16, 256), is_cuda=True, dtype=dtype)
+    assert ar.paged_attention_fallback_reason(_enabled(), q, kv, kv, seq_len=1, batched=False) == expected
+
+
+def test_shape_mismatch_reports_shape() -> None:
+    q = _fake_cuda((1, 16, 1, 128))
+    kv = _fake_cuda((1, 2, 8, 16, 256))
+    assert ar.paged_attention_fallback_reason(_enabled(), q, kv, kv, seq_len=1, batched=False) == "shape"
+
+
+def test_full_attention_paged_returns_none_on_cpu_and_counts() -> None:
+    runtime = ar.HotPathRuntime()
+    cache = FullAttentionCache(block_size=2)
+    cache.append_blocks(torch.zeros(1, 2, 3, 4), torch.zeros(1, 2, 3, 4))
+    assert ar.full_attention_paged(torch.zeros(1, 2, 1, 4), None, cache, _enabled(), runtime) is None
+    assert runtime.paged_attention_stats.fallback_cpu == 1
