@@ -271,6 +271,90 @@ def time_prefill(w, steps: int, warmup: int) -> float:
     return start.elapsed_time(end) / steps
 
 
+# ----------------------------------------------------------------------------- config 5
+
+
+def hybrid_workload(device: str, *, seed: int = 0, batch: int = 128, groups: int = 12, lo: int = 256, hi: int = 65536, heads: int = 16,
+                    kv_heads: int = 2, dim: int = 256, bs: int = 16, key_heads: int = 16, value_heads: int = 32):
+    """48 layers = 12 x (3 gated-delta linear layers + 1 paged GQA layer), one decode token per sequence."""
+    import torch
+
+    gen = torch.Generator().manual_seed(seed)
+    ctx = torch.randint(lo, hi + 1, (batch,), generator=gen)
+    dgen = torch.Generator(device=device).manual_seed(seed)
+    need = [(int(c) + 1 + bs - 1) // bs for c in ctx]  # room for the appended token
+    pool_blocks = math.ceil(sum(need) * 1.25)
+    full_layers = []
+    for _ in range(groups):
+        perm = torch.randperm(pool_blocks, generator=gen)
+        tables = torch.full((batch, max(need)), -1, dtype=torch.int32)
+        cursor = 0
+        for b, n in enumerate(need):
+            tables[b, :n] = perm[cursor : cursor + n].to(torch.int32)
+            cursor += n
+        full_layers.append({
+            "key_pool": torch.randn((pool_blocks, kv_heads, bs, dim), generator=dgen, device=device, dtype=torch.bfloat16),
+            "value_pool": torch.randn((pool_blocks, kv_heads, bs, dim), generator=dgen, device=device, dtype=torch.bfloat16),
+            "tables": tables.to(device),
+        })
+    channels = 2 * key_heads * 128 + value_heads * 128
+    linear_layers = []
+    for _ in range(3 * groups):
+        linear_layers.append({
+            "state": torch.randn((batch, value_heads, 128, 128), generator=dgen, device=device) * 0.05,
+            "conv": torch.randn((batch, channels, 3), generator=dgen, device=device),
+            "conv_w": torch.randn((channels, 4), generator=dgen, device=device) * 0.5,
+            "a_log": torch.zeros(value_heads, device=device),
+            "dt_bias": torch.zeros(value_heads, device=device),
+        })
+    step_inputs = {
+        "query": torch.randn((batch, heads, 1, dim), generator=dgen, device=device, dtype=torch.bfloat16),
+        "new_k": torch.randn((batch, kv_heads, 1, dim), generator=dgen, device=device, dtype=torch.bfloat16),
+        "new_v": torch.randn((batch, kv_heads, 1, dim), generator=dgen, device=device, dtype=torch.bfloat16),
+        "mixed": torch.randn((batch, channels), generator=dgen, device=device, dtype=torch.bfloat16),
+        "a": torch.randn((batch, value_heads), generator=dgen, device=device, dtype=torch.bfloat16),
+        "b": torch.randn((batch, value_heads), generator=dgen, device=device, dtype=torch.bfloat16),
+        "positions": ctx.to(device=device, dtype=torch.int32),
+        "lens": (ctx + 1).to(device=device, dtype=torch.int32),
+    }
+    sum_ctx = int(ctx.sum())
+    full_bytes = (sum_ctx + batch) * kv_heads * dim * 2 * 2 + 2 * batch * heads * dim * 2 + sum(need) * 4 + batch * kv_heads * dim * 2 * 2
+    linear_bytes = batch * (2 * value_heads * 128 * 128 * 4 + 2 * channels * 3 * 4 + channels * 2 + value_heads * 128 * 2)
+    return {"full": full_layers, "linear": linear_layers, "inputs": step_inputs, "groups": groups, "bs": bs, "key_heads": key_heads,
+            "algo_bytes": groups * full_bytes + 3 * groups * linear_bytes, "sum_ctx": sum_ctx, "pool_blocks": pool_blocks}
+
+
+def time_hybrid(w, steps: int, warmup: int) -> float:
+    """One step = every layer's attention for one decode token of all sequences (KV append + paged decode, or conv update + fused delta step)."""
+    import torch
+
+    import hip_ops
+
+    x = w["inputs"]
+
+    def step():
+        for g in range(w["groups"]):
+            for lin in w["linear"][3 * g : 3 * g + 3]:
+                act = hip_ops.causal_conv1d_update(x["mixed"], lin["conv"], lin["conv_w"])
+                hip_ops.gated_delta_step(act, x["a"], x["b"], lin["a_log"], lin["dt_bias"], lin["state"], key_heads=w["key_heads"])
+            full = w["full"][g]
+            hip_ops.paged_kv_append(x["new_k"], x["new_v"], full["key_pool"], full["value_pool"], full["tables"], x["positions"], w["bs"])
+            hip_ops.paged_attention_decode_batched(x["query"], full["tables"], full["key_pool"], full["value_pool"], x["lens"], w["bs"])
+
+    for _ in range(warmup):
+        step()
+    torch.cuda.synchronize()
+    stream = torch.cuda.current_stream()
+    start = torch.cuda.Event(enable_timing=True)
+    end = torch.cuda.Event(enable_timing=True)
+    start.record(stream)
+    for _ in range(steps):
+        step()
+    end.record(stream)
+    torch.cuda.synchronize()
+    return start.elapsed_time(end) / steps
+
+
 # ----------------------------------------------------------------------------- main
 
 
@@ -282,6 +366,7 @@ def main() -> int:
     parser.add_argument("--no-cpu-baseline", action="store_true")
     parser.add_argument("--no-delta", action="store_true", help="skip the config-4 secondary measurement")
     parser.add_argument("--no-prefill", action="store_true", help="skip the config-3 secondary measurement")
+    parser.add_argument("--no-hybrid", action="store_true", help="skip the config-5 secondary measurement")
     parser.add_argument("--cpu-budget", type=float, default=12.0)
     args = parser.parse_args()
     if args.gpus != 1:
@@ -376,6 +461,24 @@ def main() -> int:
                          "kernel": "qa::pfx::prefill_kernel<256> + kv_append per 512-token query chunk"},
         }
         del pw
+        torch.cuda.empty_cache()
+    if not args.no_hybrid:
+        _log("bench: building config-5 workload (48-layer hybrid decode step, attention only)")
+        hw = hybrid_workload(device)
+        hms = time_hybrid(hw, 3, 1)
+        hgbs = hw["algo_bytes"] / (hms * 1e-3) / 1e9
+        _log(f"bench: hybrid step {hms:.3f} ms, {hgbs:.1f} GB/s ({hgbs / HBM_PEAK_GBS:.1%} of HBM peak)")
+        record["secondary_hybrid"] = {
+            "metric": "hybrid decode step HBM GB/s (BASELINE config 5)",
+            "value": round(hgbs, 2),
+            "unit": "GB/s",
+            "ms_per_step": round(hms, 4),
+            "config": {"workload": "48-layer hybrid decode step, attention only (BASELINE config 5)", "batch": 128, "layers": "12 x (3 linear + 1 full)",
+                       "context": "U[256, 65536] seed 0", "sum_context": hw["sum_ctx"], "pool_blocks_per_layer": hw["pool_blocks"]},
+            "roofline": {"bound": "hbm", "achieved": round(hgbs, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(hgbs / HBM_PEAK_GBS, 4),
+                         "traffic": None, "algo_bytes_per_launch": hw["algo_bytes"], "kernel": "per-layer launches (see DESIGN.md)"},
+        }
+        del hw
         torch.cuda.empty_cache()
     if not args.no_cpu_baseline:
         _log("bench: CPU baseline (reference path restatement)")
