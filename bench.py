@@ -33,11 +33,35 @@ for _p in (REPO_ROOT, PACKAGE_DIR):
         sys.path.insert(0, str(_p))
 
 HBM_PEAK_GBS = 8000.0  # MI355X HBM3E, GB/s
+# HBM bytes per launch of the decode kernel from rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE
+# (profiles/decode_partial_mfma_config2.md): FETCH_SIZE scaled by 2.0 and WRITE_SIZE by 1.0,
+# the factors a plain 1 GiB device copy reads back in the same runs.
+TRAFFIC_DECODE = None
 MFMA_BF16_PEAK_TFLOPS = 2500.0  # MI355X dense bf16/fp16 MFMA, TFLOP/s
 
 
 def _log(msg: str) -> None:
     print(msg, file=sys.stderr, flush=True)
+
+
+def kernel_times(step, repeats: int, labels: tuple[str, ...]) -> dict[str, dict[str, float]]:
+    """Average duration of each labelled kernel over ``repeats`` steps, from HIP events
+    the library records on the launch stream around each launch (``qa_set_kernel_timing``)."""
+    import torch
+
+    import hip_loader
+
+    torch.cuda.synchronize()
+    with hip_loader.KernelTiming() as timing:
+        for _ in range(repeats):
+            step()
+        torch.cuda.synchronize()
+        out = {}
+        for label in labels:
+            total_ms, launches = timing.read(label)
+            if launches:
+                out[label] = {"avg_ms": total_ms / launches, "launches_per_step": launches / repeats, "total_ms_per_step": total_ms / repeats}
+    return out
 
 
 # ----------------------------------------------------------------------------- config 2
@@ -85,6 +109,13 @@ def time_decode(w, steps: int, warmup: int):
     def step():
         return hip_ops.paged_attention_decode_batched(w["query"], w["tables"], w["key_pool"], w["value_pool"], w["lens"], w["bs"])
 
+    return _timed(step, steps, warmup, ("decode_partial_mfma", "decode_combine"))
+
+
+def _timed(step, steps: int, warmup: int, labels: tuple[str, ...]):
+    """(ms per step over ``steps`` timed steps, per-kernel averages from a separate instrumented pass)."""
+    import torch
+
     for _ in range(warmup):
         step()
     torch.cuda.synchronize()
@@ -96,7 +127,8 @@ def time_decode(w, steps: int, warmup: int):
         step()
     end.record(stream)
     torch.cuda.synchronize()
-    return start.elapsed_time(end) / steps
+    ms = start.elapsed_time(end) / steps
+    return ms, kernel_times(step, max(1, min(steps, 5)), labels)
 
 
 def cpu_baseline_decode(w, budget_s: float = 12.0):
@@ -191,18 +223,7 @@ def time_delta(w, steps: int, warmup: int) -> float:
         return hip_ops.chunk_gated_delta_rule(w["mixed"], w["a"], w["b"], w["a_log"], w["dt_bias"], w["conv_w"], key_heads=w["key_heads"],
                                               value_heads=w["value_heads"], keep_conv_state=False)
 
-    for _ in range(warmup):
-        step()
-    torch.cuda.synchronize()
-    stream = torch.cuda.current_stream()
-    start = torch.cuda.Event(enable_timing=True)
-    end = torch.cuda.Event(enable_timing=True)
-    start.record(stream)
-    for _ in range(steps):
-        step()
-    end.record(stream)
-    torch.cuda.synchronize()
-    return start.elapsed_time(end) / steps
+    return _timed(step, steps, warmup, ("chunk_gated_delta",))
 
 
 # ----------------------------------------------------------------------------- config 3
@@ -257,18 +278,7 @@ def time_prefill(w, steps: int, warmup: int) -> float:
                                     starts, w["bs"])
             hip_ops.paged_attention_prefill(q, cu, starts, w["key_pool"], w["value_pool"], w["tables"], w["bs"], max_new=n, gate=gate)
 
-    for _ in range(warmup):
-        step()
-    torch.cuda.synchronize()
-    stream = torch.cuda.current_stream()
-    start = torch.cuda.Event(enable_timing=True)
-    end = torch.cuda.Event(enable_timing=True)
-    start.record(stream)
-    for _ in range(steps):
-        step()
-    end.record(stream)
-    torch.cuda.synchronize()
-    return start.elapsed_time(end) / steps
+    return _timed(step, steps, warmup, ("paged_prefill",))
 
 
 # ----------------------------------------------------------------------------- config 5
@@ -341,18 +351,7 @@ def time_hybrid(w, steps: int, warmup: int) -> float:
             hip_ops.paged_kv_append(x["new_k"], x["new_v"], full["key_pool"], full["value_pool"], full["tables"], x["positions"], w["bs"])
             hip_ops.paged_attention_decode_batched(x["query"], full["tables"], full["key_pool"], full["value_pool"], x["lens"], w["bs"])
 
-    for _ in range(warmup):
-        step()
-    torch.cuda.synchronize()
-    stream = torch.cuda.current_stream()
-    start = torch.cuda.Event(enable_timing=True)
-    end = torch.cuda.Event(enable_timing=True)
-    start.record(stream)
-    for _ in range(steps):
-        step()
-    end.record(stream)
-    torch.cuda.synchronize()
-    return start.elapsed_time(end) / steps
+    return _timed(step, steps, warmup, ("decode_partial_mfma", "decode_combine", "gated_delta_step", "causal_conv1d"))
 
 
 # ----------------------------------------------------------------------------- main
@@ -367,6 +366,8 @@ def main() -> int:
     parser.add_argument("--no-delta", action="store_true", help="skip the config-4 secondary measurement")
     parser.add_argument("--no-prefill", action="store_true", help="skip the config-3 secondary measurement")
     parser.add_argument("--no-hybrid", action="store_true", help="skip the config-5 secondary measurement")
+    parser.add_argument("--copy-probe-mib", type=int, default=0,
+                        help="first run one plain device copy of this many MiB (reference point for HBM byte counters)")
     parser.add_argument("--cpu-budget", type=float, default=12.0)
     args = parser.parse_args()
     if args.gpus != 1:
@@ -379,13 +380,24 @@ def main() -> int:
         print("bench.py needs a GPU", file=sys.stderr)
         return 2
     device = "cuda:0"
+    if args.copy_probe_mib > 0:
+        src = torch.ones(args.copy_probe_mib << 20, dtype=torch.uint8, device=device)
+        dst = torch.empty_like(src)
+        torch.cuda.synchronize()
+        dst.copy_(src)
+        torch.cuda.synchronize()
+        _log(f"bench: copy probe of {args.copy_probe_mib} MiB done")
+        del src, dst
     _log("bench: building config-2 workload")
     w = decode_workload(device)
     _log(f"bench: pool {w['pool_blocks']} blocks, sum ctx {int(w['ctx'].sum())}, algo bytes {w['algo_bytes']/1e9:.3f} GB")
-    ms = time_decode(w, args.steps, args.warmup)
+    ms, kern = time_decode(w, args.steps, args.warmup)
     wc = {k: w[k] for k in ("query", "tables_cpu", "key_pool", "value_pool", "ctx", "bs")}
     gbs = w["algo_bytes"] / (ms * 1e-3) / 1e9
-    _log(f"bench: decode {ms:.4f} ms/step, {gbs:.1f} GB/s ({gbs / HBM_PEAK_GBS:.1%} of HBM peak)")
+    k_ms = kern["decode_partial_mfma"]["avg_ms"]
+    k_gbs = w["algo_bytes"] / (k_ms * 1e-3) / 1e9
+    _log(f"bench: decode {ms:.4f} ms/step, {gbs:.1f} GB/s ({gbs / HBM_PEAK_GBS:.1%} of HBM peak); "
+         f"main kernel {k_ms * 1e3:.1f} us = {k_gbs:.1f} GB/s ({k_gbs / HBM_PEAK_GBS:.1%})")
     record = {
         "metric": "paged decode attn HBM GB/s (% of 8 TB/s) + gated-delta prefill tokens/s",
         "value": round(gbs, 2),
@@ -412,13 +424,15 @@ def main() -> int:
         },
         "roofline": {
             "bound": "hbm",
-            "achieved": round(gbs, 2),
+            "achieved": round(k_gbs, 2),
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
-            "frac": round(gbs / HBM_PEAK_GBS, 4),
-            "traffic": None,
-            "kernel": "paged decode step (partial + combine launches)",
+            "frac": round(k_gbs / HBM_PEAK_GBS, 4),
+            "traffic": TRAFFIC_DECODE,
+            "kernel": "qa::decode_partial_mfma<256> (split-K partials); the step adds qa::decode_combine",
+            "kernel_avg_us": round(k_ms * 1e3, 2),
             "algo_bytes_per_launch": w["algo_bytes"],
+            "kernels": kern,
         },
     }
     del w
@@ -426,8 +440,8 @@ def main() -> int:
     if not args.no_delta:
         _log("bench: building config-4 workload (gated delta-rule chunked prefill)")
         dw = delta_workload(device)
-        dms = time_delta(dw, max(2, args.steps // 2), max(1, args.warmup // 2))
-        tflops = dw["flops"] / (dms * 1e-3) / 1e12
+        dms, dkern = time_delta(dw, max(2, args.steps // 2), max(1, args.warmup // 2))
+        tflops = dw["flops"] / (dkern["chunk_gated_delta"]["avg_ms"] * 1e-3) / 1e12
         tok_s = dw["batch"] * dw["seq"] / (dms * 1e-3)
         _log(f"bench: delta prefill {dms:.3f} ms, {tok_s:,.0f} tokens/s, {tflops:.1f} TFLOP/s ({tflops / MFMA_BF16_PEAK_TFLOPS:.1%} of MFMA peak)")
         record["secondary"] = {
@@ -439,15 +453,16 @@ def main() -> int:
                        "value_heads": 32, "head_dim": 128, "chunk": 64, "conv_kernel": 4},
             "roofline": {"bound": "mfma", "achieved": round(tflops, 2), "peak": MFMA_BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
                          "frac": round(tflops / MFMA_BF16_PEAK_TFLOPS, 4), "traffic": None, "algo_flop_per_launch": dw["flops"],
-                         "algo_bytes_per_launch": dw["algo_bytes"], "kernel": "qa::cgd::chunk_kernel (fp16 MFMA, fp32 accumulate)"},
+                         "algo_bytes_per_launch": dw["algo_bytes"], "kernel": "qa::cgd::chunk_kernel (fp16 MFMA, fp32 accumulate)",
+                         "kernel_avg_us": round(dkern["chunk_gated_delta"]["avg_ms"] * 1e3, 2)},
         }
         del dw
         torch.cuda.empty_cache()
     if not args.no_prefill:
         _log("bench: building config-3 workload (chunked paged prefill with gate)")
         pw = prefill_workload(device)
-        pms = time_prefill(pw, max(2, args.steps // 4), 1)
-        ptf = pw["flops"] / (pms * 1e-3) / 1e12
+        pms, pkern = time_prefill(pw, max(2, args.steps // 4), 1)
+        ptf = pw["flops"] / (pkern["paged_prefill"]["total_ms_per_step"] * 1e-3) / 1e12
         _log(f"bench: paged prefill {pms:.3f} ms, {ptf:.1f} TFLOP/s ({ptf / MFMA_BF16_PEAK_TFLOPS:.1%} of MFMA peak)")
         record["secondary_prefill"] = {
             "metric": "chunked paged prefill TFLOP/s (BASELINE config 3)",
@@ -458,14 +473,15 @@ def main() -> int:
                        "prefix": "U[0, 8192] seed 0", "q_heads": 16, "kv_heads": 2, "head_dim": 256, "block_size": 16, "query_chunk": 512},
             "roofline": {"bound": "mfma", "achieved": round(ptf, 2), "peak": MFMA_BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
                          "frac": round(ptf / MFMA_BF16_PEAK_TFLOPS, 4), "traffic": None, "algo_flop_per_launch": pw["flops"],
-                         "kernel": "qa::pfx::prefill_kernel<256> + kv_append per 512-token query chunk"},
+                         "kernel": "qa::pfx::prefill_kernel<256>, one launch per 512-token query chunk (kv_append between)",
+                         "kernel_ms_per_step": round(pkern["paged_prefill"]["total_ms_per_step"], 4)},
         }
         del pw
         torch.cuda.empty_cache()
     if not args.no_hybrid:
         _log("bench: building config-5 workload (48-layer hybrid decode step, attention only)")
         hw = hybrid_workload(device)
-        hms = time_hybrid(hw, 3, 1)
+        hms, hkern = time_hybrid(hw, 3, 1)
         hgbs = hw["algo_bytes"] / (hms * 1e-3) / 1e9
         _log(f"bench: hybrid step {hms:.3f} ms, {hgbs:.1f} GB/s ({hgbs / HBM_PEAK_GBS:.1%} of HBM peak)")
         record["secondary_hybrid"] = {
@@ -476,7 +492,8 @@ def main() -> int:
             "config": {"workload": "48-layer hybrid decode step, attention only (BASELINE config 5)", "batch": 128, "layers": "12 x (3 linear + 1 full)",
                        "context": "U[256, 65536] seed 0", "sum_context": hw["sum_ctx"], "pool_blocks_per_layer": hw["pool_blocks"]},
             "roofline": {"bound": "hbm", "achieved": round(hgbs, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(hgbs / HBM_PEAK_GBS, 4),
-                         "traffic": None, "algo_bytes_per_launch": hw["algo_bytes"], "kernel": "per-layer launches (see DESIGN.md)"},
+                         "traffic": None, "algo_bytes_per_step": hw["algo_bytes"], "kernel": "whole step (12 paged-decode + 36 conv/delta-step layers)",
+                         "kernels": hkern},
         }
         del hw
         torch.cuda.empty_cache()

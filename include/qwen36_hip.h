@@ -67,6 +67,15 @@ const char* qa_last_error(void);
 int32_t qa_version(void);
 const char* qa_arch(void);
 
+/* Opt-in timing of each operation's main kernel with HIP events recorded on
+ * the launch stream around the launch (no counterpart in the reference; used
+ * by the benchmark for per-kernel roofline figures).  Enabling or disabling
+ * clears the totals.  Labels: decode_partial_mfma, decode_partial_generic,
+ * decode_combine, paged_prefill, chunk_gated_delta, gated_delta_step,
+ * causal_conv1d.  qa_read_kernel_timing waits for the recorded events.      */
+void qa_set_kernel_timing(int32_t enabled);
+int qa_read_kernel_timing(const char* label, double* total_ms, int64_t* launches);
+
 /* ---- paged GQA decode ------------------------------------------------- */
 /* Bytes of fp32 workspace the decode entry points need for these sizes.   */
 int64_t qa_paged_attention_decode_workspace(int64_t batch, int32_t heads, int32_t head_dim,

@@ -629,6 +629,9 @@ extern "C" int qa_chunk_gated_delta_rule(const void* mixed_qkv, int32_t x_dtype,
     attr_set = true;
   }
   dim3 grid(static_cast<unsigned>(batch * value_heads * 2));
-  hipLaunchKernelGGL(chunk_kernel, grid, dim3(NT), LDS_BYTES, stream, p);
+  {
+    KernelTimer timer_("chunk_gated_delta", stream);
+    hipLaunchKernelGGL(chunk_kernel, grid, dim3(NT), LDS_BYTES, stream, p);
+  }
   return check_launch("chunk_gated_delta_rule");
 }

@@ -365,7 +365,10 @@ extern "C" int qa_causal_conv1d_prefill(const void* x, int32_t x_dtype, int64_t 
   p.out_st = out_stride_t;
   p.silu = apply_silu;
   dim3 grid(static_cast<unsigned>(ceil_div(channels, 256)), static_cast<unsigned>(batch));
-  hipLaunchKernelGGL(conv1d_kernel, grid, dim3(256), 0, stream, p);
+  {
+    KernelTimer timer_("causal_conv1d", stream);
+    hipLaunchKernelGGL(conv1d_kernel, grid, dim3(256), 0, stream, p);
+  }
   return check_launch("conv1d_kernel");
 }
 
@@ -452,6 +455,9 @@ extern "C" int qa_gated_delta_step(const float* qkv, int64_t qkv_stride_b, const
   p.Hqk = key_heads;
   p.dk = key_dim;
   p.dv = value_dim;
-  hipLaunchKernelGGL(delta_recurrent_128<true>, dim3(static_cast<unsigned>(batch * value_heads)), dim3(256), 0, stream, p);
+  {
+    KernelTimer timer_("gated_delta_step", stream);
+    hipLaunchKernelGGL(delta_recurrent_128<true>, dim3(static_cast<unsigned>(batch * value_heads)), dim3(256), 0, stream, p);
+  }
   return check_launch("delta_recurrent_128(fused step)");
 }

@@ -469,9 +469,15 @@ static int64_t decode_workspace_bytes(int64_t batch, int heads, int head_dim, in
 template <typename QT, typename KT, int GMAX, int NPL>
 static int launch_generic(DecodeParams& p, hipStream_t stream) {
   dim3 grid(p.n_splits, p.B * p.Hkv);
-  hipLaunchKernelGGL((decode_partial_generic<QT, KT, GMAX, NPL>), grid, dim3(64), 0, stream, p);
+  {
+    KernelTimer timer_("decode_partial_generic", stream);
+    hipLaunchKernelGGL((decode_partial_generic<QT, KT, GMAX, NPL>), grid, dim3(64), 0, stream, p);
+  }
   if (int rc = check_launch("decode_partial_generic")) return rc;
-  hipLaunchKernelGGL((decode_combine<QT>), dim3(p.B * p.H), dim3(256), 0, stream, p);
+  {
+    KernelTimer timer_("decode_combine", stream);
+    hipLaunchKernelGGL((decode_combine<QT>), dim3(p.B * p.H), dim3(256), 0, stream, p);
+  }
   return check_launch("decode_combine");
 }
 
@@ -495,9 +501,15 @@ template <int D>
 static int launch_mfma_d(DecodeParams& p, hipStream_t stream) {
   dim3 grid(p.n_splits, p.B * p.Hkv);
   const size_t smem = MfmaDecodeSmem<D>::kBytes;
-  hipLaunchKernelGGL((decode_partial_mfma<D>), grid, dim3(64 * kMfmaWaves), smem, stream, p);
+  {
+    KernelTimer timer_("decode_partial_mfma", stream);
+    hipLaunchKernelGGL((decode_partial_mfma<D>), grid, dim3(64 * kMfmaWaves), smem, stream, p);
+  }
   if (int rc = check_launch("decode_partial_mfma")) return rc;
-  hipLaunchKernelGGL((decode_combine<bf16_t>), dim3(p.B * p.H), dim3(256), 0, stream, p);
+  {
+    KernelTimer timer_("decode_combine", stream);
+    hipLaunchKernelGGL((decode_combine<bf16_t>), dim3(p.B * p.H), dim3(256), 0, stream, p);
+  }
   return check_launch("decode_combine");
 }
 

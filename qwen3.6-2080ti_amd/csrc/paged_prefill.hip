@@ -301,10 +301,13 @@ extern "C" int qa_paged_attention_prefill(const void* query, int32_t q_dtype, in
     if (err != hipSuccess) return fail("paged prefill: cannot reserve %d bytes of LDS: %s", Smem<256>::kBytes, hipGetErrorString(err));
     attr_set = true;
   }
-  if (head_dim == 256) {
-    hipLaunchKernelGGL(prefill_kernel<256>, grid, dim3(NT), Smem<256>::kBytes, stream, p);
-  } else {
-    hipLaunchKernelGGL(prefill_kernel<128>, grid, dim3(NT), Smem<128>::kBytes, stream, p);
+  {
+    KernelTimer timer_("paged_prefill", stream);
+    if (head_dim == 256) {
+      hipLaunchKernelGGL(prefill_kernel<256>, grid, dim3(NT), Smem<256>::kBytes, stream, p);
+    } else {
+      hipLaunchKernelGGL(prefill_kernel<128>, grid, dim3(NT), Smem<128>::kBytes, stream, p);
+    }
   }
   return check_launch("paged prefill");
 }

@@ -17,6 +17,20 @@ void set_error(const char* fmt, ...) __attribute__((format(printf, 1, 2)));
 int fail(const char* fmt, ...) __attribute__((format(printf, 1, 2)));
 int check_launch(const char* what);
 
+// Opt-in HIP-event timing of a kernel launch on its stream (qa_set_kernel_timing).
+class KernelTimer {
+ public:
+  KernelTimer(const char* label, hipStream_t stream);
+  ~KernelTimer();
+  KernelTimer(const KernelTimer&) = delete;
+  KernelTimer& operator=(const KernelTimer&) = delete;
+
+ private:
+  const char* label_;
+  hipStream_t stream_;
+  hipEvent_t start_ = nullptr;
+};
+
 #define QA_REQUIRE(cond, ...)          \
   do {                                 \
     if (!(cond)) return qa::fail(__VA_ARGS__); \

@@ -55,6 +55,8 @@ SIGNATURES: dict[str, tuple[Any, list[Any]]] = {
     "qa_last_error": (ctypes.c_char_p, []),
     "qa_version": (c_int32, []),
     "qa_arch": (ctypes.c_char_p, []),
+    "qa_set_kernel_timing": (None, [c_int32]),
+    "qa_read_kernel_timing": (c_int32, [ctypes.c_char_p, ctypes.POINTER(ctypes.c_double), ctypes.POINTER(c_int64)]),
     "qa_paged_attention_decode_workspace": (c_int64, [c_int64, c_int32, c_int32, c_int64, c_int32]),
     "qa_paged_attention_decode": (
         c_int32,
@@ -137,3 +139,25 @@ def last_error(lib: Any) -> str:
 def check(lib: Any, status: int, what: str) -> None:
     if status != 0:
         raise RuntimeError(f"{what}: {last_error(lib)}")
+
+
+class KernelTiming:
+    """Context manager around the library's opt-in kernel timer.
+
+    ``with KernelTiming() as t: ...`` then ``t.read("decode_partial_mfma")``
+    returns ``(total_ms, launches)`` of that kernel inside the block.
+    """
+
+    def __enter__(self) -> "KernelTiming":
+        self._lib = load_library()
+        self._lib.qa_set_kernel_timing(1)
+        return self
+
+    def read(self, label: str) -> tuple[float, int]:
+        total = ctypes.c_double(0.0)
+        count = c_int64(0)
+        self._lib.qa_read_kernel_timing(label.encode(), ctypes.byref(total), ctypes.byref(count))
+        return float(total.value), int(count.value)
+
+    def __exit__(self, *exc: object) -> None:
+        self._lib.qa_set_kernel_timing(0)

@@ -65,3 +65,15 @@ def test_host_validation_errors_need_no_gpu() -> None:
     assert status != 0
     assert "query must be float32" in hip_loader.last_error(lib)
     assert lib.qa_paged_attention_decode_workspace(64, 16, 256, 32768, 16) > 0
+
+
+def test_kernel_timing_reads_zero_without_launches() -> None:
+    _library()
+    lib = hip_loader.load_library()
+    import ctypes
+
+    lib.qa_set_kernel_timing(1)
+    total, launches = ctypes.c_double(-1.0), ctypes.c_int64(-1)
+    assert lib.qa_read_kernel_timing(b"decode_partial_mfma", ctypes.byref(total), ctypes.byref(launches)) == 0
+    lib.qa_set_kernel_timing(0)
+    assert total.value == 0.0 and launches.value == 0
