@@ -34,9 +34,13 @@ for _p in (REPO_ROOT, PACKAGE_DIR):
 
 HBM_PEAK_GBS = 8000.0  # MI355X HBM3E, GB/s
 # HBM bytes per launch of the decode kernel from rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE
-# (profiles/decode_partial_mfma_config2.md): FETCH_SIZE scaled by 2.0 and WRITE_SIZE by 1.0,
-# the factors a plain 1 GiB device copy reads back in the same runs.
-TRAFFIC_DECODE = None
+# (profiles/decode_partial_mfma_config2.md, profiles/chunk_gated_delta_config4.md,
+# profiles/paged_prefill_config3.md): FETCH_SIZE scaled by 2.0 and WRITE_SIZE by 1.0, the factors
+# a plain 1 GiB device copy reads back in the same runs. Counters need rocprofv3, so the figures
+# are the committed profile's, not measured live.
+TRAFFIC_DECODE = 1980739257
+TRAFFIC_DELTA = 1653273865
+TRAFFIC_PREFILL = 891196186  # average over the eight per-chunk launches
 MFMA_BF16_PEAK_TFLOPS = 2500.0  # MI355X dense bf16/fp16 MFMA, TFLOP/s
 
 
@@ -452,7 +456,7 @@ def main() -> int:
             "config": {"workload": "gated delta-rule chunked prefill (BASELINE config 4)", "batch": 4, "seq_len": 8192, "key_heads": 16,
                        "value_heads": 32, "head_dim": 128, "chunk": 64, "conv_kernel": 4},
             "roofline": {"bound": "mfma", "achieved": round(tflops, 2), "peak": MFMA_BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
-                         "frac": round(tflops / MFMA_BF16_PEAK_TFLOPS, 4), "traffic": None, "algo_flop_per_launch": dw["flops"],
+                         "frac": round(tflops / MFMA_BF16_PEAK_TFLOPS, 4), "traffic": TRAFFIC_DELTA, "algo_flop_per_launch": dw["flops"],
                          "algo_bytes_per_launch": dw["algo_bytes"], "kernel": "qa::cgd::chunk_kernel (fp16 MFMA, fp32 accumulate)",
                          "kernel_avg_us": round(dkern["chunk_gated_delta"]["avg_ms"] * 1e3, 2)},
         }
@@ -472,7 +476,7 @@ def main() -> int:
             "config": {"workload": "chunked causal paged prefill with sigmoid gate (BASELINE config 3)", "batch": 8, "new_tokens": 4096,
                        "prefix": "U[0, 8192] seed 0", "q_heads": 16, "kv_heads": 2, "head_dim": 256, "block_size": 16, "query_chunk": 512},
             "roofline": {"bound": "mfma", "achieved": round(ptf, 2), "peak": MFMA_BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
-                         "frac": round(ptf / MFMA_BF16_PEAK_TFLOPS, 4), "traffic": None, "algo_flop_per_launch": pw["flops"],
+                         "frac": round(ptf / MFMA_BF16_PEAK_TFLOPS, 4), "traffic": TRAFFIC_PREFILL, "algo_flop_per_launch": pw["flops"],
                          "kernel": "qa::pfx::prefill_kernel<256>, one launch per 512-token query chunk (kv_append between)",
                          "kernel_ms_per_step": round(pkern["paged_prefill"]["total_ms_per_step"], 4)},
         }
