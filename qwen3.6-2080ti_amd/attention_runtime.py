@@ -248,6 +248,7 @@ def full_attention_paged(query: Any, gate: Any | None, cache: FullAttentionCache
     if reason != "no_kernel" or page_table is None:
         record_native_paged_dispatch(runtime, reason, native=False)
         return None
+    import hip_loader
     import hip_ops
 
     try:
@@ -255,7 +256,11 @@ def full_attention_paged(query: Any, gate: Any | None, cache: FullAttentionCache
             heads = hip_ops.paged_attention_decode(
                 query, page_table.block_table, page_table.key_blocks, page_table.value_blocks, page_table.sequence_length, page_table.block_size
             )
+    except hip_loader.NativeLibraryMissing:
+        raise
     except RuntimeError:
+        # a kernel-side rejection (shape, dtype, workspace): the caller's dense path runs,
+        # as src/tp_runtime.py:591 and :2537 do
         record_native_paged_dispatch(runtime, "no_kernel", native=False)
         return None
     record_native_paged_dispatch(runtime, reason, native=True)
@@ -273,6 +278,7 @@ def full_attention_paged_batch(query: Any, gate: Any | None, caches: Sequence[Fu
     if reason != "no_kernel" or page_tables is None:
         record_native_paged_dispatch(runtime, reason, native=False)
         return None
+    import hip_loader
     import hip_ops
 
     try:
@@ -281,7 +287,11 @@ def full_attention_paged_batch(query: Any, gate: Any | None, caches: Sequence[Fu
                 query, page_tables.block_tables, list(page_tables.key_blocks), list(page_tables.value_blocks), page_tables.sequence_lengths,
                 page_tables.block_size,
             )
+    except hip_loader.NativeLibraryMissing:
+        raise
     except RuntimeError:
+        # a kernel-side rejection (shape, dtype, workspace): the caller's dense path runs,
+        # as src/tp_runtime.py:591 and :2537 do
         record_native_paged_dispatch(runtime, "no_kernel", native=False)
         return None
     record_native_paged_dispatch(runtime, reason, native=True)

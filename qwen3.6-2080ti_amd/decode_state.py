@@ -256,6 +256,7 @@ class FullAttentionCache:
     block_table: list[int] = field(default_factory=list)
     shared_pool: SharedKVBlockPool | None = None
     pool: Any = field(init=False)
+    _table_cache: Any = field(default=None, init=False, repr=False, compare=False)
     append_calls: int = 0
     appended_tokens: int = 0
     growth_events: int = 0
@@ -367,7 +368,14 @@ class FullAttentionCache:
         if device is None and self.pool.key_blocks is not None:
             device = self.pool.key_blocks.device
         self.page_table_tensor_calls += 1
-        return torch.tensor(self.block_table, dtype=torch.long, device=device)
+        key = (str(device), tuple(self.block_table))
+        cached = self._table_cache
+        if cached is None or cached[0] != key:
+            # the device copy is rebuilt only when the table changed (the reference
+            # copies it host to device on every call, src/decode_state.py:87-95)
+            cached = (key, torch.tensor(self.block_table, dtype=torch.long, device=device))
+            self._table_cache = cached
+        return cached[1]
 
     def page_metadata(self) -> FullAttentionPageTable:
         if self.pool.key_blocks is None or self.pool.value_blocks is None:

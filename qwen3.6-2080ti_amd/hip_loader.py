@@ -113,16 +113,23 @@ SIGNATURES: dict[str, tuple[Any, list[Any]]] = {
 }
 
 
+class NativeLibraryMissing(RuntimeError):
+    """The HIP library is not built or cannot be opened.  Never caught by a fallback."""
+
+
 def load_library() -> Any:
-    """Open (once) and return the ctypes handle; ``RuntimeError`` if not built."""
+    """Open (once) and return the ctypes handle; :class:`NativeLibraryMissing` if not built."""
     global _LIB
     if _LIB is not None:
         return _LIB
     if not LIBRARY_PATH.exists():
-        raise RuntimeError(f"qwen36 HIP library is not built ({LIBRARY_PATH}); run `python build_native.py`")
+        raise NativeLibraryMissing(f"qwen36 HIP library is not built ({LIBRARY_PATH}); run `python build_native.py`")
     import torch  # noqa: F401  -- binds libamdhip64.so.7 to torch's HIP runtime first
 
-    lib = ctypes.CDLL(str(LIBRARY_PATH), mode=ctypes.RTLD_GLOBAL)
+    try:
+        lib = ctypes.CDLL(str(LIBRARY_PATH), mode=ctypes.RTLD_GLOBAL)
+    except OSError as exc:
+        raise NativeLibraryMissing(f"cannot open {LIBRARY_PATH}: {exc}") from exc
     for name, (restype, argtypes) in SIGNATURES.items():
         fn = getattr(lib, name)
         fn.restype = restype

@@ -118,3 +118,26 @@ def test_full_attention_paged_returns_none_on_cpu_and_counts() -> None:
     cache.append_blocks(torch.zeros(1, 2, 3, 4), torch.zeros(1, 2, 3, 4))
     assert ar.full_attention_paged(torch.zeros(1, 2, 1, 4), None, cache, _enabled(), runtime) is None
     assert runtime.paged_attention_stats.fallback_cpu == 1
+
+
+def test_missing_native_library_is_raised_not_a_dense_fallback(monkeypatch) -> None:
+    """A kernel-side rejection falls back to the caller's dense path; a missing library never does."""
+    import hip_loader
+    import hip_ops
+
+    def missing(*args, **kwargs):
+        raise hip_loader.NativeLibraryMissing("not built")
+
+    def rejected(*args, **kwargs):
+        raise RuntimeError("paged decode: shape rejected")
+
+    monkeypatch.setattr(ar, "paged_attention_fallback_reason", lambda *a, **k: "no_kernel")
+    cache = FullAttentionCache(block_size=2)
+    cache.append_blocks(torch.zeros(1, 2, 3, 4), torch.zeros(1, 2, 3, 4))
+    runtime = ar.HotPathRuntime()
+    monkeypatch.setattr(hip_ops, "paged_attention_decode", missing)
+    with pytest.raises(hip_loader.NativeLibraryMissing):
+        ar.full_attention_paged(torch.zeros(1, 2, 1, 4), None, cache, _enabled(), runtime)
+    monkeypatch.setattr(hip_ops, "paged_attention_decode", rejected)
+    assert ar.full_attention_paged(torch.zeros(1, 2, 1, 4), None, cache, _enabled(), runtime) is None
+    assert runtime.paged_attention_stats.fallback_no_kernel == 1

@@ -248,3 +248,15 @@ def test_shared_pool_caches_share_storage_and_gather_in_order() -> None:
     assert pool.free_blocks == [0, 1, 5, 6, 7]
     with pytest.raises(RuntimeError, match="exhausted"):
         FullAttentionCache(block_size=2, shared_pool=pool).append_blocks(*_kv(3, seq=20))
+
+
+def test_page_table_tensor_is_reused_until_the_table_changes() -> None:
+    cache = FullAttentionCache(block_size=2)
+    cache.append_blocks(torch.zeros(1, 1, 3, 4), torch.zeros(1, 1, 3, 4))
+    first = cache.page_table_tensor()
+    assert cache.page_table_tensor() is first
+    assert first.tolist() == cache.block_table
+    cache.append_blocks(torch.zeros(1, 1, 2, 4), torch.zeros(1, 1, 2, 4))
+    second = cache.page_table_tensor()
+    assert second is not first and second.tolist() == cache.block_table and len(cache.block_table) >= 3
+    assert cache.page_table_tensor_calls == 3

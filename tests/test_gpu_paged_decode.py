@@ -262,3 +262,44 @@ def test_kernel_timing_counts_decode_launches() -> None:
         cms, cn = timing.read("decode_combine")
     assert n == 3 and cn == 3
     assert ms > 0.0 and cms > 0.0
+
+
+def test_raw_ctypes_binding_matches_hip_ops() -> None:
+    """The C-ABI used with nothing but ctypes (as a reference-side binding would) gives hip_ops' result."""
+    import ctypes
+
+    import hip_loader
+
+    ops = _ops()
+    gen = torch.Generator().manual_seed(5)
+    P, Hkv, bs, D, B, H = 64, 2, 16, 256, 3, 16
+    pool_k = torch.randn(P, Hkv, bs, D, generator=gen).to(torch.bfloat16).to(DEV)
+    pool_v = torch.randn(P, Hkv, bs, D, generator=gen).to(torch.bfloat16).to(DEV)
+    tables = torch.randperm(P, generator=gen)[:60].view(B, 20).to(DEV)
+    lens = torch.tensor([320, 1, 77], device=DEV)
+    query = torch.randn(B, H, 1, D, generator=gen).to(torch.bfloat16).to(DEV)
+    max_tokens = int(lens.max())
+
+    class PagedKV(ctypes.Structure):
+        _fields_ = [("key", ctypes.c_void_p), ("value", ctypes.c_void_p),
+                    ("row_key_ptrs", ctypes.c_void_p), ("row_value_ptrs", ctypes.c_void_p), ("row_blocks", ctypes.c_void_p),
+                    ("num_blocks", ctypes.c_int64), ("stride_batch", ctypes.c_int64), ("stride_block", ctypes.c_int64),
+                    ("stride_head", ctypes.c_int64), ("stride_token", ctypes.c_int64),
+                    ("kv_heads", ctypes.c_int32), ("dtype", ctypes.c_int32)]
+
+    lib = ctypes.CDLL(str(hip_loader.LIBRARY_PATH), mode=ctypes.RTLD_GLOBAL)
+    lib.qa_last_error.restype = ctypes.c_char_p
+    lib.qa_paged_attention_decode_workspace.restype = ctypes.c_int64
+    lib.qa_paged_attention_decode_workspace.argtypes = [ctypes.c_int64, ctypes.c_int32, ctypes.c_int32, ctypes.c_int64, ctypes.c_int32]
+    kv = PagedKV(pool_k.data_ptr(), pool_v.data_ptr(), None, None, None, P, 0, Hkv * bs * D, bs * D, D, Hkv, 1)
+    ws = torch.empty(lib.qa_paged_attention_decode_workspace(B, H, D, max_tokens, bs), dtype=torch.uint8, device=DEV)
+    out = torch.empty_like(query)
+    status = lib.qa_paged_attention_decode_batched(
+        ctypes.c_void_p(query.data_ptr()), 1, ctypes.c_int64(H * D), ctypes.c_int64(D), ctypes.c_int64(B), H, D,
+        ctypes.byref(kv), ctypes.c_void_p(tables.data_ptr()), 4, ctypes.c_int64(tables.stride(0)), ctypes.c_int64(tables.shape[1]),
+        ctypes.c_void_p(lens.data_ptr()), 4, bs, ctypes.c_float(D ** -0.5),
+        ctypes.c_void_p(out.data_ptr()), ctypes.c_void_p(ws.data_ptr()), ctypes.c_int64(ws.numel()),
+        ctypes.c_void_p(torch.cuda.current_stream().cuda_stream))
+    assert status == 0, lib.qa_last_error().decode()
+    expected = ops.paged_attention_decode_batched(query, tables, pool_k, pool_v, lens, bs)
+    torch.testing.assert_close(out, expected, atol=0, rtol=0)
