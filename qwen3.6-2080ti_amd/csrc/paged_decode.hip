@@ -33,9 +33,10 @@ struct DecodeParams {
   int B, H, Hkv, D, bs, G;
   int table_i64, lens_i64;
   float scale;
-  int split_tokens, n_splits;
-  float* part_o;   // (B*H, n_splits, D)
-  float* part_ml;  // (B*H, n_splits, 2)
+  int split_tokens, n_splits;  // generic path: fixed token splits
+  int n_waves;                 // MFMA path: waves of the balanced schedule
+  float* part_o;   // generic: (B*H, n_splits, D); MFMA: (W + B*H_kv, G, D)
+  float* part_ml;  // generic: (B*H, n_splits, 2); MFMA: (W + B*H_kv, G, 2)
 };
 
 __device__ __forceinline__ int64_t ceil_div_dev(int64_t a, int64_t b) { return (a + b - 1) / b; }
@@ -156,236 +157,432 @@ __global__ __launch_bounds__(64) void decode_partial_generic(DecodeParams p) {
 // ---------------------------------------------------------------------------
 // MFMA path: bf16 Q and KV, block_size 16, head_dim D in {128, 256}, group <= 16.
 //
-// Work item = (row b, KV head g, split of split_tokens tokens) on a 4-wave
-// workgroup; wave w takes logical blocks lb0 + w, lb0 + w + 4, ...  Per 16-token
-// block and wave:
+// Balanced schedule.  The tiles (row group rg = b * H_kv + g, logical block) of
+// all rows are laid end to end, rg-major, T tiles in all; wave w of the W
+// launched waves takes the contiguous range [T w / W, T (w + 1) / W).  Every
+// wave therefore streams the same number of 8 KiB K and V tiles whatever the
+// spread of context lengths, with no per-split start-up and no cross-wave
+// merge.  When its range leaves a row group the wave writes that group's
+// unnormalised partial (m, l, o) of the G query heads to slot w + rg; slots are
+// unique because a later wave never covers an earlier row group.
+//
+// A wave walks its blocks in groups of up to NG; per group:
 //   S[t][h]   = sum_d K[t][d] Q[h][d]      v_mfma_f32_16x16x32_bf16, M = token,
 //                                          N = query head of the group (padded
 //                                          to 16), K = 32 dims per instruction
-//   online softmax per head (column of S) in fp32, p rounded to bf16
+//   online softmax per head (column of S) in the log2 domain, p rounded to bf16
 //   O^T[d][h] += sum_t V[t][d] P[t][h]     v_mfma_f32_16x16x16_bf16, M = dim,
 //                                          N = head, K = the block's 16 tokens
+// Loads run kPrefetchTiles tiles ahead in a continuous stream K_0 .. K_{NG-1},
+// V_0 .. V_{NG-1}, K_0 of the next group, ... through a ring of register tiles
+// (one wave per SIMD, so the ring has the register file to itself); the group's
+// table entries are read one group early.
 // The S accumulator layout (lane l: tokens 4(l/16)+r, head l%16) is exactly the
 // B-operand layout of the PV product, so P never leaves registers.  V is
-// transposed through a wave-private LDS tile: each lane loads 4 consecutive
-// tokens x 8 dims (coalesced 16-byte row loads), packs them into 4-token
-// columns with v_perm_b32 and stores 8-byte units; the PV A-operand is then one
-// 8-byte LDS read per 16-dim tile.  Units are XOR-swizzled so neither the
-// stores nor the reads conflict on LDS banks.
+// transposed through a wave-private LDS tile: lane l loads 8 dims (chunk
+// l % (D/8)) of D/128 token quads (coalesced 16-byte row loads), packs them into
+// 4-token columns with v_perm_b32 and stores 8-byte units; the PV A-operand is
+// then one 8-byte LDS read per 16-dim tile.  Units are XOR-swizzled so neither
+// the stores nor the reads conflict on LDS banks.
 typedef __attribute__((__vector_size__(8 * sizeof(__bf16)))) __bf16 bf16x8_v;
 typedef short short4_v __attribute__((ext_vector_type(4)));
 typedef float floatx4_v __attribute__((ext_vector_type(4)));
 
 constexpr int kMfmaWaves = 4;
-constexpr int kVtPad = 16;  // 8-byte units of padding per token quad
+constexpr int kVtPad = 16;            // 8-byte units of padding per token quad
+constexpr int kWaveGroup = 8;         // blocks per two-phase group
+constexpr int kMaxDecodeWaves = 1024; // 256 workgroups: one per CU on MI355X
+constexpr int kMinTilesPerWave = 8;
+constexpr float kLog2e = 1.4426950408889634f;
 
 __device__ __forceinline__ int vt_swizzle(int d) { return d ^ ((d >> 5) & 7); }
 
 template <int D>
 struct MfmaDecodeSmem {
-  static constexpr int kVtUnits = 4 * (D + kVtPad);                        // per wave
-  static constexpr int kVtBytes = kMfmaWaves * kVtUnits * 8;
-  static constexpr int kMergeBytes = kMfmaWaves * 2048 * 4 + kMfmaWaves * 16 * 2 * 4;  // G * D <= 2048
-  static constexpr int kBytes = kVtBytes > kMergeBytes ? kVtBytes : kMergeBytes;
+  static constexpr int kVtUnits = 4 * (D + kVtPad);  // per wave
+  static constexpr int kBytes = kMfmaWaves * kVtUnits * 8;
 };
 
-template <int D>
-__device__ __forceinline__ void load_k_block(uint4 (&kreg)[D / 32], const bf16_t* kblk, int64_t sT, int ktok, int quad) {
-#pragma unroll
-  for (int i = 0; i < D / 32; ++i) kreg[i] = *reinterpret_cast<const uint4*>(kblk + ktok * sT + 32 * i + 8 * quad);
+__device__ __forceinline__ int64_t uniform64(int64_t v) {
+  const uint32_t lo = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(v));
+  const uint32_t hi = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(static_cast<uint64_t>(v) >> 32));
+  return static_cast<int64_t>((static_cast<uint64_t>(hi) << 32) | lo);
 }
 
-__device__ __forceinline__ void load_v_block(uint4 (&vreg)[2][4], const bf16_t* vblk, int64_t sT, int vq0, int vc) {
-#pragma unroll
-  for (int qq = 0; qq < 2; ++qq)
-#pragma unroll
-    for (int r = 0; r < 4; ++r) vreg[qq][r] = *reinterpret_cast<const uint4*>(vblk + (4 * (vq0 + 2 * qq) + r) * sT + 8 * vc);
+// Logical blocks of row b that hold visible tokens (0 for rows of length <= 0).
+__device__ __forceinline__ int64_t row_tiles(const DecodeParams& p, int b) {
+  const int64_t len = row_length(p, b);
+  return len > 0 ? min(ceil_div_dev(len, 16), p.max_blocks) : 0;
 }
 
-// Blocks one wave handles inside a split (split_tokens <= 512 -> 32 blocks / 4 waves).
-constexpr int kMfmaBlocksPerWave = 8;
-// Blocks loaded ahead of the one being consumed (register ring of kPrefetch + 1 tiles).
-constexpr int kPrefetch = 1;
+// T: tiles of all row groups (every lane gets the total).
+__device__ int64_t total_tiles(const DecodeParams& p, int lane) {
+  int64_t sum = 0;
+  for (int b0 = 0; b0 < p.B; b0 += 64) sum += b0 + lane < p.B ? row_tiles(p, b0 + lane) : 0;
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) sum += __shfl_xor(sum, off, 64);
+  return sum * p.Hkv;
+}
+
+// Position of a wave in the tile sequence: row b, kv head g, the tiles before
+// row group (b, g) and that group's tile count.
+struct TileCursor {
+  int b, g;
+  int64_t cum, nb;
+};
+
+// Row group holding tile t (t < T).
+__device__ TileCursor locate_tile(const DecodeParams& p, int64_t t, int lane) {
+  int64_t base = 0;
+  for (int b0 = 0; b0 < p.B; b0 += 64) {
+    const int64_t nb = b0 + lane < p.B ? row_tiles(p, b0 + lane) : 0;
+    int64_t incl = nb * p.Hkv;
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+      const int64_t up = __shfl_up(incl, off, 64);
+      if (lane >= off) incl += up;
+    }
+    const int64_t chunk = __shfl(incl, 63, 64);
+    if (t < base + chunk) {
+      const int first = __ffsll(static_cast<unsigned long long>(__ballot(base + incl > t))) - 1;
+      const int64_t nbf = __shfl(nb, first, 64);
+      const int64_t before = base + __shfl(incl, first, 64) - nbf * p.Hkv;
+      TileCursor c;
+      c.b = b0 + first;
+      c.g = static_cast<int>((t - before) / nbf);
+      c.cum = before + c.g * nbf;
+      c.nb = nbf;
+      return c;
+    }
+    base += chunk;
+  }
+  return TileCursor{p.B, 0, base, 0};
+}
+
+__device__ __forceinline__ void next_row_group(const DecodeParams& p, TileCursor& c) {
+  c.cum += c.nb;
+  if (++c.g < p.Hkv) return;
+  c.g = 0;
+  do {
+    ++c.b;
+    c.nb = c.b < p.B ? row_tiles(p, c.b) : 0;
+  } while (c.nb == 0 && c.b < p.B);
+}
+
+// Table entries of blocks blk .. blk + NG - 1 of row b (-1 past the end or out of the pool).
+template <int NG>
+__device__ __forceinline__ void read_group_entries(const DecodeParams& p, int b, int64_t blk, int n, int64_t nblk, int32_t (&phys)[NG]) {
+#pragma unroll
+  for (int j = 0; j < NG; ++j) {
+    const int64_t e = j < n ? table_entry(p, b, blk + j) : -1;
+    phys[j] = (e >= 0 && e < nblk) ? static_cast<int32_t>(e) : -1;
+  }
+}
+
+// Buffer resource over one (block, kv head) tile; a skipped tile gets zero
+// records, so its loads return zeros without touching memory and every step
+// of the load stream issues the same instructions (fixed wait counts).
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t tile_rsrc(const bf16_t* base, int32_t phys, int64_t sP, int32_t bytes) {
+  const bf16_t* tile = base + static_cast<int64_t>(phys < 0 ? 0 : phys) * sP;
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<bf16_t*>(tile), 0, phys < 0 ? 0 : bytes, 0x00020000);
+}
 
 template <int D>
-__global__ __launch_bounds__(256, 2) void decode_partial_mfma(DecodeParams p) {
-  constexpr int KCH = D / 32;  // QK^T k-chunks
+struct TileLanes {
+  int32_t k;  // byte offset of this lane's first 16 bytes of a K tile; chunk i adds 64 i
+  int32_t v;  // same for a V tile; token-quad pair qq adds vq_step, row r adds row_step
+  int32_t vq_step, row_step;
+};
+
+// Load element `e` of a group's stream (K_0..K_{NG-1}, V_0..V_{NG-1}, then the
+// next group's K_0..) into `dst`: D/32 16-byte loads per lane either way.
+template <int D, int NG>
+__device__ __forceinline__ void issue_tile(uint4 (&dst)[D / 32], int e, const TileLanes<D>& ln, const bf16_t* kb, const bf16_t* vb,
+                                           int64_t sP, int32_t tile_bytes, const int32_t (&phys)[NG], const int32_t (&phys_next)[NG]) {
+  if (e < NG || e >= 2 * NG) {
+    const int32_t ph = e < NG ? phys[e] : phys_next[e - 2 * NG];
+    const __amdgpu_buffer_rsrc_t r = tile_rsrc(kb, ph, sP, tile_bytes);
+#pragma unroll
+    for (int i = 0; i < D / 32; ++i) dst[i] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(r, ln.k + 64 * i, 0, 0));
+  } else {
+    const __amdgpu_buffer_rsrc_t r = tile_rsrc(vb, phys[e - NG], sP, tile_bytes);
+#pragma unroll
+    for (int qq = 0; qq < D / 128; ++qq)
+#pragma unroll
+      for (int rr = 0; rr < 4; ++rr)
+        dst[qq * 4 + rr] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(r, ln.v + qq * ln.vq_step + rr * ln.row_step, 0, 0));
+  }
+}
+
+constexpr int kPrefetchTiles = 3;  // stream elements in flight ahead of the one consumed
+
+template <int D>
+__global__ __launch_bounds__(256, 1) void decode_partial_mfma(DecodeParams p) {
+  constexpr int KCH = D / 32;  // QK^T k-chunks; also 16-byte loads per lane per tile
   constexpr int MT = D / 16;   // PV output tiles (16 dims each)
-  constexpr int NBW = kMfmaBlocksPerWave;
+  constexpr int VQ = D / 128;  // token-quad pairs per lane in a V tile
+  constexpr int VCH = D / 8;   // 8-dim chunks of a V row
+  constexpr int NG = kWaveGroup;
+  constexpr int PF = kPrefetchTiles;
+  constexpr int R = PF + 1;  // ring slots; 2 NG % R == 0 keeps every slot index static
+  static_assert((2 * NG) % R == 0, "ring size must divide the per-group stream");
   extern __shared__ __align__(16) unsigned char smem[];
 
-  const int split = blockIdx.x;
-  const int bg = blockIdx.y;
-  const int b = bg / p.Hkv;
-  const int g = bg - b * p.Hkv;
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int64_t len = row_length(p, b);
-  const int64_t t0 = static_cast<int64_t>(split) * p.split_tokens;
-  if (t0 >= len) return;  // whole workgroup: nothing of this row in the split
-  const int64_t t1 = min(len, t0 + p.split_tokens);
-  const int64_t lb_first = t0 / 16 + wave;
-  const int64_t lb_end = (t1 + 15) / 16;
-  // blocks of this wave: lb_first + 4 j for j < nbw
-  const int nbw = lb_first < lb_end ? static_cast<int>((lb_end - lb_first + kMfmaWaves - 1) / kMfmaWaves) : 0;
-
-  const bf16_t* kb;
-  const bf16_t* vb;
-  int64_t nblk, sG;
-  row_pool(p, b, kb, vb, nblk, sG);
-  kb += static_cast<int64_t>(g) * sG;
-  vb += static_cast<int64_t>(g) * sG;
+  const int64_t wid = static_cast<int64_t>(blockIdx.x) * kMfmaWaves + wave;
+  const int64_t W = p.n_waves;
+  const int64_t T = uniform64(total_tiles(p, lane));
+  const int64_t lo = T * wid / W;
+  const int64_t hi = T * (wid + 1) / W;
+  if (lo >= hi) return;
+  TileCursor cur = locate_tile(p, lo, lane);
+  cur.b = __builtin_amdgcn_readfirstlane(cur.b);
+  cur.g = __builtin_amdgcn_readfirstlane(cur.g);
+  cur.cum = uniform64(cur.cum);
+  cur.nb = uniform64(cur.nb);
 
   const int head = lane & 15;
   const int quad = lane >> 4;
-  const int vc = lane & 31;   // 8-dim chunk of V this lane loads
-  const int vq0 = lane >> 5;  // token quads vq0 and vq0 + 2
-  const int ktok = lane & 15; // K row this lane loads
-
-  int64_t phys[NBW];
-  bool ok[NBW];
-#pragma unroll
-  for (int j = 0; j < NBW; ++j) {
-    phys[j] = j < nbw ? table_entry(p, b, lb_first + kMfmaWaves * j) : -1;
-    ok[j] = phys[j] >= 0 && phys[j] < nblk;
-    if (!ok[j]) phys[j] = 0;
-  }
-
-  // ---- phase 1: scores of every block of this wave (K streamed, one block ahead)
-  float sreg[NBW][4];
-  {
-    bf16x8_v qreg[KCH];
-    const bf16_t* qrow = reinterpret_cast<const bf16_t*>(p.q) + static_cast<int64_t>(b) * p.q_sb +
-                         static_cast<int64_t>(g * p.G + head) * p.q_sh + 8 * quad;
-#pragma unroll
-    for (int i = 0; i < KCH; ++i) {
-      uint4 raw = make_uint4(0, 0, 0, 0);
-      if (head < p.G) raw = *reinterpret_cast<const uint4*>(qrow + 32 * i);
-      qreg[i] = __builtin_bit_cast(bf16x8_v, raw);
-    }
-    // ring of kPrefetch + 1 register tiles: block j + kPrefetch is in flight while j is consumed
-    uint4 kbuf[kPrefetch + 1][KCH];
-#pragma unroll
-    for (int j = 0; j < kPrefetch; ++j)
-      if (j < nbw) load_k_block<D>(kbuf[j], kb + phys[j] * p.sP, p.sT, ktok, quad);
-#pragma unroll
-    for (int j = 0; j < NBW; ++j) {
-      if (j + kPrefetch < nbw) load_k_block<D>(kbuf[(j + kPrefetch) % (kPrefetch + 1)], kb + phys[j + kPrefetch] * p.sP, p.sT, ktok, quad);
-      floatx4_v sacc = {0.f, 0.f, 0.f, 0.f};
-      if (j < nbw) {
-#pragma unroll
-        for (int i = 0; i < KCH; ++i)
-          sacc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_v, kbuf[j % (kPrefetch + 1)][i]), qreg[i], sacc, 0, 0, 0);
-      }
-      const int64_t tbase = (lb_first + kMfmaWaves * j) * 16 + 4 * quad;
-#pragma unroll
-      for (int r = 0; r < 4; ++r) sreg[j][r] = (j < nbw && ok[j] && tbase + r < t1) ? sacc[r] * p.scale : -INFINITY;
-    }
-  }
-
-  // First V tiles go out before the softmax so phase 3 does not start cold.
-  uint4 vbuf[kPrefetch + 1][2][4];
-#pragma unroll
-  for (int j = 0; j < kPrefetch; ++j)
-    if (j < nbw) load_v_block(vbuf[j], vb + phys[j] * p.sP, p.sT, vq0, vc);
-
-  // ---- phase 2: softmax statistics of head l%16 over the wave's tokens
-  float mx = -INFINITY;
-#pragma unroll
-  for (int j = 0; j < NBW; ++j)
-#pragma unroll
-    for (int r = 0; r < 4; ++r) mx = fmaxf(mx, sreg[j][r]);
-  mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
-  mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-  const float m_use = mx == -INFINITY ? 0.f : mx;
-  float l_part = 0.f;
-  short4_v pb[NBW];
-#pragma unroll
-  for (int j = 0; j < NBW; ++j)
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const float pr = __expf(sreg[j][r] - m_use);
-      l_part += pr;
-      pb[j][r] = static_cast<short>(f32_to_bf16(pr));
-    }
-
-  // ---- phase 3: O^T += V^T P (V streamed one block ahead, transposed via LDS)
-  floatx4_v o[MT];
-#pragma unroll
-  for (int t = 0; t < MT; ++t) o[t] = floatx4_v{0.f, 0.f, 0.f, 0.f};
+  const int vc = lane % VCH;   // 8-dim chunk of V rows this lane loads
+  const int vq0 = lane / VCH;  // token quads vq0, vq0 + 512 / D, ...
+  const int ktok = lane & 15;  // K row this lane loads
+  TileLanes<D> ln;
+  ln.k = static_cast<int32_t>((ktok * p.sT + 8 * quad) * 2);
+  ln.v = static_cast<int32_t>((4 * vq0 * p.sT + 8 * vc) * 2);
+  ln.vq_step = static_cast<int32_t>(4 * (512 / D) * p.sT * 2);
+  ln.row_step = static_cast<int32_t>(p.sT * 2);
+  const int32_t tile_bytes = static_cast<int32_t>((15 * p.sT + D) * 2);
   uint2* vt = reinterpret_cast<uint2*>(smem) + wave * MfmaDecodeSmem<D>::kVtUnits;
-  {
+  const float qk_scale = p.scale * kLog2e;
+
+  int64_t tile = lo;
+  while (tile < hi) {
+    const int b = cur.b;
+    const int g = cur.g;
+    const int64_t seg_end = min(hi, cur.cum + cur.nb);
+    const int64_t len = row_length(p, b);
+    const bf16_t* kb;
+    const bf16_t* vb;
+    int64_t nblk, sG;
+    row_pool(p, b, kb, vb, nblk, sG);
+    kb += static_cast<int64_t>(g) * sG;
+    vb += static_cast<int64_t>(g) * sG;
+
+    bf16x8_v qreg[KCH];
+    {
+      const bf16_t* qrow = reinterpret_cast<const bf16_t*>(p.q) + static_cast<int64_t>(b) * p.q_sb +
+                           static_cast<int64_t>(g * p.G + head) * p.q_sh + 8 * quad;
 #pragma unroll
-    for (int j = 0; j < NBW; ++j) {
-      if (j < nbw) {
-        if (j + kPrefetch < nbw) load_v_block(vbuf[(j + kPrefetch) % (kPrefetch + 1)], vb + phys[j + kPrefetch] * p.sP, p.sT, vq0, vc);
-        uint4 (&vcur)[2][4] = vbuf[j % (kPrefetch + 1)];
+      for (int i = 0; i < KCH; ++i) {
+        uint4 raw = make_uint4(0, 0, 0, 0);
+        if (head < p.G) raw = *reinterpret_cast<const uint4*>(qrow + 32 * i);
+        qreg[i] = __builtin_bit_cast(bf16x8_v, raw);
+      }
+    }
+    float m_run = -INFINITY;  // log2 domain
+    float l_run = 0.f;        // this lane's share of the head's denominator
+    floatx4_v o[MT];
 #pragma unroll
-        for (int qq = 0; qq < 2; ++qq) {
-          const int q = vq0 + 2 * qq;
-          const uint32_t* r0 = reinterpret_cast<const uint32_t*>(&vcur[qq][0]);
-          const uint32_t* r1 = reinterpret_cast<const uint32_t*>(&vcur[qq][1]);
-          const uint32_t* r2 = reinterpret_cast<const uint32_t*>(&vcur[qq][2]);
-          const uint32_t* r3 = reinterpret_cast<const uint32_t*>(&vcur[qq][3]);
+    for (int t = 0; t < MT; ++t) o[t] = floatx4_v{0.f, 0.f, 0.f, 0.f};
+
+    const int64_t blk_end = seg_end - cur.cum;
+    int64_t blk = tile - cur.cum;
+    int n = static_cast<int>(min<int64_t>(NG, blk_end - blk));
+    int32_t phys[NG];
+    int32_t phys_next[NG];
+    read_group_entries<NG>(p, b, blk, n, nblk, phys);
+    uint4 ring[R][KCH];
 #pragma unroll
-          for (int k = 0; k < 4; ++k) {
-            const int d = 8 * vc + 2 * k;
-            uint2 lo, hi;
-            lo.x = __builtin_amdgcn_perm(r1[k], r0[k], 0x05040100u);
-            lo.y = __builtin_amdgcn_perm(r3[k], r2[k], 0x05040100u);
-            hi.x = __builtin_amdgcn_perm(r1[k], r0[k], 0x07060302u);
-            hi.y = __builtin_amdgcn_perm(r3[k], r2[k], 0x07060302u);
-            vt[q * (D + kVtPad) + vt_swizzle(d)] = lo;
-            vt[q * (D + kVtPad) + vt_swizzle(d + 1)] = hi;
+    for (int e = 0; e < PF; ++e) issue_tile<D, NG>(ring[e % R], e, ln, kb, vb, p.sP, tile_bytes, phys, phys);
+
+    while (true) {
+      const int64_t blk_next = blk + NG;
+      const int n_next = blk_next < blk_end ? static_cast<int>(min<int64_t>(NG, blk_end - blk_next)) : 0;
+      read_group_entries<NG>(p, b, blk_next, n_next, nblk, phys_next);
+
+      // ---- phase 1: scores of the group's blocks (stream elements 0 .. NG-1)
+      float sreg[NG][4];
+#pragma unroll
+      for (int j = 0; j < NG; ++j) {
+        issue_tile<D, NG>(ring[(j + PF) % R], j + PF, ln, kb, vb, p.sP, tile_bytes, phys, phys_next);
+        floatx4_v sacc = {0.f, 0.f, 0.f, 0.f};
+        if (j < n) {
+#pragma unroll
+          for (int i = 0; i < KCH; ++i)
+            sacc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_v, ring[j % R][i]), qreg[i], sacc, 0, 0, 0);
+        }
+        const int64_t tbase = (blk + j) * 16 + 4 * quad;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) sreg[j][r] = (j < n && phys[j] >= 0 && tbase + r < len) ? sacc[r] * qk_scale : -INFINITY;
+      }
+
+      // ---- phase 2: online softmax statistics of head l%16
+      float mx = -INFINITY;
+#pragma unroll
+      for (int j = 0; j < NG; ++j)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) mx = fmaxf(mx, sreg[j][r]);
+      mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
+      mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+      const float m_new = fmaxf(m_run, mx);
+      const float m_use = m_new == -INFINITY ? 0.f : m_new;
+      const float corr = exp2f(m_run - m_use);
+      m_run = m_new;
+      l_run *= corr;
+#pragma unroll
+      for (int t = 0; t < MT; ++t) o[t] *= corr;
+      short4_v pb[NG];
+#pragma unroll
+      for (int j = 0; j < NG; ++j)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const float pr = exp2f(sreg[j][r] - m_use);
+          l_run += pr;
+          pb[j][r] = static_cast<short>(f32_to_bf16(pr));
+        }
+
+      // ---- phase 3: O^T += V^T P (stream elements NG .. 2 NG - 1)
+#pragma unroll
+      for (int j = 0; j < NG; ++j) {
+        issue_tile<D, NG>(ring[(NG + j + PF) % R], NG + j + PF, ln, kb, vb, p.sP, tile_bytes, phys, phys_next);
+        if (j < n) {
+          uint4 (&vcur)[KCH] = ring[(NG + j) % R];
+#pragma unroll
+          for (int qq = 0; qq < VQ; ++qq) {
+            const int q = vq0 + (64 / VCH) * qq;
+            const uint32_t* r0 = reinterpret_cast<const uint32_t*>(&vcur[qq * 4 + 0]);
+            const uint32_t* r1 = reinterpret_cast<const uint32_t*>(&vcur[qq * 4 + 1]);
+            const uint32_t* r2 = reinterpret_cast<const uint32_t*>(&vcur[qq * 4 + 2]);
+            const uint32_t* r3 = reinterpret_cast<const uint32_t*>(&vcur[qq * 4 + 3]);
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+              const int d = 8 * vc + 2 * k;
+              uint2 lo2, hi2;
+              lo2.x = __builtin_amdgcn_perm(r1[k], r0[k], 0x05040100u);
+              lo2.y = __builtin_amdgcn_perm(r3[k], r2[k], 0x05040100u);
+              hi2.x = __builtin_amdgcn_perm(r1[k], r0[k], 0x07060302u);
+              hi2.y = __builtin_amdgcn_perm(r3[k], r2[k], 0x07060302u);
+              vt[q * (D + kVtPad) + vt_swizzle(d)] = lo2;
+              vt[q * (D + kVtPad) + vt_swizzle(d + 1)] = hi2;
+            }
+          }
+#pragma unroll
+          for (int t = 0; t < MT; ++t) {
+            const uint2 a = vt[quad * (D + kVtPad) + vt_swizzle(16 * t + head)];
+            o[t] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(__builtin_bit_cast(short4_v, a), pb[j], o[t], 0, 0, 0);
           }
         }
+      }
+      if (n_next == 0) break;
+      blk = blk_next;
+      n = n_next;
 #pragma unroll
-        for (int t = 0; t < MT; ++t) {
-          const uint2 a = vt[quad * (D + kVtPad) + vt_swizzle(16 * t + head)];
-          o[t] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(__builtin_bit_cast(short4_v, a), pb[j], o[t], 0, 0, 0);
-        }
+      for (int j = 0; j < NG; ++j) phys[j] = phys_next[j];
+    }
+
+    // Partial of row group (b, g): lanes {h, h+16, h+32, h+48} hold head h.
+    l_run += __shfl_xor(l_run, 16, 64);
+    l_run += __shfl_xor(l_run, 32, 64);
+    const int64_t slot = wid + static_cast<int64_t>(b) * p.Hkv + g;
+    if (head < p.G) {
+      float* po = p.part_o + (slot * p.G + head) * D;
+#pragma unroll
+      for (int t = 0; t < MT; ++t) *reinterpret_cast<floatx4_v*>(po + 16 * t + 4 * quad) = o[t];
+      if (quad == 0) {
+        p.part_ml[(slot * p.G + head) * 2 + 0] = m_run;
+        p.part_ml[(slot * p.G + head) * 2 + 1] = l_run;
       }
     }
+    tile = seg_end;
+    if (tile < hi) next_row_group(p, cur);
   }
+}
 
-  // Per-wave softmax denominators: lanes {h, h+16, h+32, h+48} hold head h.
-  l_part += __shfl_xor(l_part, 16, 64);
-  l_part += __shfl_xor(l_part, 32, 64);
+// Merge the partials of one (row, head) of the balanced schedule: the waves
+// that covered row group rg are those holding its first and last tile, found
+// from the same range formula the partial kernel uses (wave w holds tile t iff
+// floor(T w / W) <= t < floor(T (w + 1) / W), i.e. w = floor(((t + 1) W - 1) / T)).
+// m is in the log2 domain.  Rows without a visible tile get 0.
+template <typename QT>
+__global__ __launch_bounds__(256) void decode_combine_balanced(DecodeParams p) {
+  __shared__ float weight[kMaxDecodeWaves];
+  __shared__ float redf[4];
+  __shared__ int64_t redi[2][4];
+  const int bh = blockIdx.x;
+  const int b = bh / p.H;
+  const int h = bh - b * p.H;
+  const int g = h / p.G;
+  const int hh = h - g * p.G;
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  QT* out = reinterpret_cast<QT*>(p.out) + static_cast<int64_t>(bh) * p.D;
 
-  __syncthreads();  // LDS now reused for the cross-wave merge
-  float* om = reinterpret_cast<float*>(smem);  // [wave][G heads][D]
-  float* mlw = om + kMfmaWaves * 2048;         // [wave][16][2]
-  if (head < p.G) {
+  int64_t before = 0, total = 0;
+  for (int r = threadIdx.x; r < p.B; r += blockDim.x) {
+    const int64_t nb = row_tiles(p, r);
+    total += nb;
+    if (r < b) before += nb;
+  }
 #pragma unroll
-    for (int t = 0; t < MT; ++t)
-      *reinterpret_cast<floatx4_v*>(om + (wave * p.G + head) * D + 16 * t + 4 * quad) = o[t];
-    if (quad == 0) {
-      mlw[(wave * 16 + head) * 2 + 0] = mx;
-      mlw[(wave * 16 + head) * 2 + 1] = l_part;
-    }
+  for (int off = 32; off > 0; off >>= 1) {
+    total += __shfl_xor(total, off, 64);
+    before += __shfl_xor(before, off, 64);
+  }
+  if (lane == 0) {
+    redi[0][wave] = total;
+    redi[1][wave] = before;
   }
   __syncthreads();
-  const int64_t slot0 = static_cast<int64_t>(b) * p.H + g * p.G;
-  for (int idx = threadIdx.x; idx < p.G * D; idx += blockDim.x) {
-    const int h = idx / D;
-    const int d = idx - h * D;
-    float big = -INFINITY;
-#pragma unroll
-    for (int w = 0; w < kMfmaWaves; ++w) big = fmaxf(big, mlw[(w * 16 + h) * 2]);
-    const float use = big == -INFINITY ? 0.f : big;
-    float acc = 0.f, den = 0.f;
-#pragma unroll
-    for (int w = 0; w < kMfmaWaves; ++w) {
-      const float f = __expf(mlw[(w * 16 + h) * 2] - use);
-      acc += f * om[(w * p.G + h) * D + d];
-      den += f * mlw[(w * 16 + h) * 2 + 1];
+  total = redi[0][0] + redi[0][1] + redi[0][2] + redi[0][3];
+  before = redi[1][0] + redi[1][1] + redi[1][2] + redi[1][3];
+  const int64_t nbb = row_tiles(p, b);
+  if (nbb == 0) {
+    for (int d = threadIdx.x; d < p.D; d += blockDim.x) Elem<QT>::store(out + d, 0.f);
+    return;
+  }
+  const int64_t T = total * p.Hkv;
+  const int64_t W = p.n_waves;
+  const int64_t cum = before * p.Hkv + g * nbb;
+  const int64_t w_first = ((cum + 1) * W - 1) / T;
+  const int64_t w_last = ((cum + nbb) * W - 1) / T;
+  const int n = static_cast<int>(w_last - w_first + 1);
+  const int64_t slot0 = w_first + static_cast<int64_t>(b) * p.Hkv + g;
+  const float* ml = p.part_ml + (slot0 * p.G + hh) * 2;
+  const float* po = p.part_o + (slot0 * p.G + hh) * p.D;
+  const int64_t sml = 2 * static_cast<int64_t>(p.G);
+  const int64_t so = static_cast<int64_t>(p.G) * p.D;
+
+  float big = -INFINITY;
+  for (int s = threadIdx.x; s < n; s += blockDim.x) big = fmaxf(big, ml[s * sml]);
+  big = wave_max(big);
+  if (lane == 0) redf[wave] = big;
+  __syncthreads();
+  big = fmaxf(fmaxf(redf[0], redf[1]), fmaxf(redf[2], redf[3]));
+  __syncthreads();
+  const float use = big == -INFINITY ? 0.f : big;
+  float den = 0.f;
+  for (int s = threadIdx.x; s < n; s += blockDim.x) {
+    const float f = exp2f(ml[s * sml] - use);
+    weight[s] = f;
+    den += f * ml[s * sml + 1];
+  }
+  den = wave_sum(den);
+  if (lane == 0) redf[wave] = den;
+  __syncthreads();
+  den = redf[0] + redf[1] + redf[2] + redf[3];
+  const float inv = den > 0.f ? 1.f / den : 0.f;
+  for (int d = threadIdx.x; d < p.D; d += blockDim.x) {
+    float acc0 = 0.f, acc1 = 0.f, acc2 = 0.f, acc3 = 0.f;
+    int s = 0;
+    for (; s + 4 <= n; s += 4) {
+      acc0 += weight[s + 0] * po[(s + 0) * so + d];
+      acc1 += weight[s + 1] * po[(s + 1) * so + d];
+      acc2 += weight[s + 2] * po[(s + 2) * so + d];
+      acc3 += weight[s + 3] * po[(s + 3) * so + d];
     }
-    const int64_t slot = (slot0 + h) * p.n_splits + split;
-    p.part_o[slot * D + d] = acc;
-    if (d == 0) {
-      p.part_ml[slot * 2 + 0] = big;
-      p.part_ml[slot * 2 + 1] = den;
-    }
+    for (; s < n; ++s) acc0 += weight[s] * po[s * so + d];
+    Elem<QT>::store(out + d, ((acc0 + acc1) + (acc2 + acc3)) * inv);
   }
 }
 
@@ -460,10 +657,24 @@ static int choose_split_tokens(int64_t max_tokens, int block_size) {
   return static_cast<int>(std::min(hi, std::max(lo, want)));
 }
 
+// Waves of the balanced MFMA schedule for `row_groups` rows of up to max_tokens
+// tokens: at least kMinTilesPerWave tiles each when every row is full, at most
+// kMaxDecodeWaves, a whole number of 4-wave workgroups.
+static int64_t balanced_waves(int64_t row_groups, int64_t max_tokens) {
+  const int64_t tiles = row_groups * ceil_div(std::max<int64_t>(max_tokens, 1), 16);
+  const int64_t wgs = std::min<int64_t>(kMaxDecodeWaves / kMfmaWaves, std::max<int64_t>(1, ceil_div(tiles, kMfmaWaves * kMinTilesPerWave)));
+  return wgs * kMfmaWaves;
+}
+
+// Bytes of workspace either path may need.  The generic path stores
+// (B*H, n_splits, D + 2) floats; the MFMA path (W + B*H_kv) slots of G heads,
+// bounded here with H_kv <= H and W computed for H row groups per row.
 static int64_t decode_workspace_bytes(int64_t batch, int heads, int head_dim, int64_t max_tokens, int block_size) {
   const int split = choose_split_tokens(max_tokens, block_size);
   const int64_t n_splits = std::max<int64_t>(1, ceil_div(std::max<int64_t>(max_tokens, 1), split));
-  return batch * heads * n_splits * (head_dim + 2) * static_cast<int64_t>(sizeof(float));
+  const int64_t generic = batch * heads * n_splits * (head_dim + 2);
+  const int64_t balanced = (balanced_waves(batch * heads, max_tokens) + batch) * heads * (head_dim + 2);
+  return std::max(generic, balanced) * static_cast<int64_t>(sizeof(float));
 }
 
 template <typename QT, typename KT, int GMAX, int NPL>
@@ -499,7 +710,7 @@ static int dispatch_generic(DecodeParams& p, hipStream_t stream) {
 
 template <int D>
 static int launch_mfma_d(DecodeParams& p, hipStream_t stream) {
-  dim3 grid(p.n_splits, p.B * p.Hkv);
+  const dim3 grid(p.n_waves / kMfmaWaves);
   const size_t smem = MfmaDecodeSmem<D>::kBytes;
   {
     KernelTimer timer_("decode_partial_mfma", stream);
@@ -508,7 +719,7 @@ static int launch_mfma_d(DecodeParams& p, hipStream_t stream) {
   if (int rc = check_launch("decode_partial_mfma")) return rc;
   {
     KernelTimer timer_("decode_combine", stream);
-    hipLaunchKernelGGL((decode_combine<bf16_t>), dim3(p.B * p.H), dim3(256), 0, stream, p);
+    hipLaunchKernelGGL((decode_combine_balanced<bf16_t>), dim3(p.B * p.H), dim3(256), 0, stream, p);
   }
   return check_launch("decode_combine");
 }
@@ -542,12 +753,10 @@ struct DecodeHostArgs {
   int64_t workspace_bytes;
 };
 
-// The MFMA path needs 16-token blocks, D in {128, 256}, G * D <= 2048, 16-byte
-// aligned rows (token stride and head stride multiples of 8 elements) and a
-// split length that is a multiple of 16.
+// The MFMA path needs 16-token blocks, D in {128, 256}, G <= 16 and 16-byte
+// aligned rows (token stride and head stride multiples of 8 elements).
 static bool mfma_eligible(const DecodeParams& p, const DecodeHostArgs& a, const qa_paged_kv& kv) {
-  if (p.bs != 16 || (p.D != 128 && p.D != 256) || p.G > 16 || p.G * p.D > 2048 || p.split_tokens % 16 != 0) return false;
-  if (p.split_tokens > 16 * kMfmaWaves * kMfmaBlocksPerWave) return false;
+  if (p.bs != 16 || (p.D != 128 && p.D != 256) || p.G > 16) return false;
   if (kv.stride_token % 8 != 0 || kv.stride_block % 8 != 0 || kv.stride_batch % 8 != 0) return false;
   if (kv.stride_head % 8 != 0) return false;
   if (a.q_sb % 8 != 0 || a.q_sh % 8 != 0) return false;
@@ -614,10 +823,14 @@ static int run_decode(const DecodeHostArgs& a, hipStream_t stream) {
   QA_REQUIRE(p.n_splits <= kCombineMaxSplits, "paged decode: %lld tokens need more than %d splits", static_cast<long long>(a.max_tokens), kCombineMaxSplits);
   const int64_t need = decode_workspace_bytes(a.batch, a.heads, a.head_dim, a.max_tokens, a.block_size);
   QA_REQUIRE(a.workspace != nullptr && a.workspace_bytes >= need, "paged decode workspace too small: need %lld bytes", static_cast<long long>(need));
+  p.n_waves = static_cast<int>(balanced_waves(static_cast<int64_t>(p.B) * p.Hkv, a.max_tokens));
   p.part_o = reinterpret_cast<float*>(a.workspace);
+  if (a.q_dtype == QA_BF16 && kv.dtype == QA_BF16 && mfma_eligible(p, a, kv)) {
+    p.part_ml = p.part_o + (static_cast<int64_t>(p.n_waves) + static_cast<int64_t>(p.B) * p.Hkv) * p.G * p.D;
+    return launch_mfma(p, stream);
+  }
   p.part_ml = p.part_o + static_cast<int64_t>(p.B) * p.H * p.n_splits * p.D;
 
-  if (a.q_dtype == QA_BF16 && kv.dtype == QA_BF16 && mfma_eligible(p, a, kv)) return launch_mfma(p, stream);
   if (a.q_dtype == QA_F32 && kv.dtype == QA_F32) return dispatch_generic<float, float>(p, stream);
   if (a.q_dtype == QA_BF16 && kv.dtype == QA_BF16) return dispatch_generic<bf16_t, bf16_t>(p, stream);
   if (a.q_dtype == QA_F32 && kv.dtype == QA_BF16) return dispatch_generic<float, bf16_t>(p, stream);

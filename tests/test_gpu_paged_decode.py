@@ -303,3 +303,37 @@ def test_raw_ctypes_binding_matches_hip_ops() -> None:
     assert status == 0, lib.qa_last_error().decode()
     expected = ops.paged_attention_decode_batched(query, tables, pool_k, pool_v, lens, bs)
     torch.testing.assert_close(out, expected, atol=0, rtol=0)
+
+
+@pytest.mark.parametrize("dim,heads,kv_heads", [(128, 8, 2), (256, 16, 2), (128, 16, 1), (256, 4, 4)])
+def test_bf16_head_dims_groups_and_invalid_blocks_inside_rows(dim, heads, kv_heads) -> None:
+    """Both MFMA head dims and group sizes 1..16; a table entry outside the pool (or -1) inside a row's
+    valid range is skipped, so the row attends over its remaining tokens (decode has no positional term)."""
+    ops = _ops()
+    gen = torch.Generator().manual_seed(17 + dim + heads)
+    bs, pool_blocks = 16, 200
+    lens = [0, 1, 17, 300, 512, 1000]
+    kp = torch.randn(pool_blocks, kv_heads, bs, dim, generator=gen).to(torch.bfloat16)
+    vp = torch.randn(pool_blocks, kv_heads, bs, dim, generator=gen).to(torch.bfloat16)
+    q = torch.randn(len(lens), heads, 1, dim, generator=gen).to(torch.bfloat16)
+    perm = torch.randperm(pool_blocks, generator=gen).tolist()
+    max_blocks = 64
+    tables = torch.full((len(lens), max_blocks), -1, dtype=torch.long)
+    cursor, kept_tables, kept_lens = 0, [], []
+    for row, n in enumerate(lens):
+        need = (n + bs - 1) // bs
+        t = perm[cursor : cursor + need]
+        cursor += need
+        tables[row, :need] = torch.tensor(t, dtype=torch.long)
+        kept_tables.append(list(t))
+        kept_lens.append(n)
+    tables[3, 5] = pool_blocks + 7  # out of the pool
+    tables[5, 20] = -1              # padding marker inside the row
+    for row, blk in ((3, 5), (5, 20)):
+        del kept_tables[row][blk]
+        kept_lens[row] -= bs
+    ref = oracle_attn.paged_decode(q, [kp] * len(lens), [vp] * len(lens), kept_tables, kept_lens, block_size=bs, pool_layout="phbd",
+                                   cast_probs=False)
+    out = ops.paged_attention_decode_batched(q.to(DEV), tables.to(DEV), kp.to(DEV), vp.to(DEV), torch.tensor(lens, device=DEV), bs)
+    assert torch.count_nonzero(out[0]) == 0
+    torch.testing.assert_close(out.cpu().float(), ref.float(), atol=2e-2, rtol=2e-2)
