@@ -37,6 +37,7 @@ struct DecodeParams {
   int n_waves;                 // MFMA path: waves of the balanced schedule
   float* part_o;   // generic: (B*H, n_splits, D); MFMA: (W + B*H_kv, G, D)
   float* part_ml;  // generic: (B*H, n_splits, 2); MFMA: (W + B*H_kv, G, 2)
+  int32_t* rg_waves;  // MFMA: (B*H_kv, 2) first and last wave that covered each row group
 };
 
 __device__ __forceinline__ int64_t ceil_div_dev(int64_t a, int64_t b) { return (a + b - 1) / b; }
@@ -190,8 +191,17 @@ typedef float floatx4_v __attribute__((ext_vector_type(4)));
 
 constexpr int kMfmaWaves = 4;
 constexpr int kVtPad = 16;            // 8-byte units of padding per token quad
-constexpr int kWaveGroup = 8;         // blocks per two-phase group
-constexpr int kMaxDecodeWaves = 1024; // 256 workgroups: one per CU on MI355X
+#ifndef QA_DECODE_GROUP
+#define QA_DECODE_GROUP 4
+#endif
+#ifndef QA_DECODE_PREFETCH
+#define QA_DECODE_PREFETCH 1
+#endif
+#ifndef QA_DECODE_WAVES_PER_SIMD
+#define QA_DECODE_WAVES_PER_SIMD 1
+#endif
+constexpr int kWaveGroup = QA_DECODE_GROUP;  // blocks per two-phase group
+constexpr int kMaxDecodeWaves = 1024 * QA_DECODE_WAVES_PER_SIMD;  // all resident at once on 256 CUs
 constexpr int kMinTilesPerWave = 8;
 constexpr float kLog2e = 1.4426950408889634f;
 
@@ -314,10 +324,10 @@ __device__ __forceinline__ void issue_tile(uint4 (&dst)[D / 32], int e, const Ti
   }
 }
 
-constexpr int kPrefetchTiles = 3;  // stream elements in flight ahead of the one consumed
+constexpr int kPrefetchTiles = QA_DECODE_PREFETCH;  // stream elements in flight ahead of the one consumed
 
 template <int D>
-__global__ __launch_bounds__(256, 1) void decode_partial_mfma(DecodeParams p) {
+__global__ __launch_bounds__(256, QA_DECODE_WAVES_PER_SIMD) void decode_partial_mfma(DecodeParams p) {
   constexpr int KCH = D / 32;  // QK^T k-chunks; also 16-byte loads per lane per tile
   constexpr int MT = D / 16;   // PV output tiles (16 dims each)
   constexpr int VQ = D / 128;  // token-quad pairs per lane in a V tile
@@ -326,6 +336,7 @@ __global__ __launch_bounds__(256, 1) void decode_partial_mfma(DecodeParams p) {
   constexpr int PF = kPrefetchTiles;
   constexpr int R = PF + 1;  // ring slots; 2 NG % R == 0 keeps every slot index static
   static_assert((2 * NG) % R == 0, "ring size must divide the per-group stream");
+  static_assert(PF <= NG, "the stream looks ahead at most to the next group's K tiles");
   extern __shared__ __align__(16) unsigned char smem[];
 
   const int lane = threadIdx.x & 63;
@@ -494,21 +505,28 @@ __global__ __launch_bounds__(256, 1) void decode_partial_mfma(DecodeParams p) {
         p.part_ml[(slot * p.G + head) * 2 + 1] = l_run;
       }
     }
+    if (lane == 0) {
+      const int64_t rg = static_cast<int64_t>(b) * p.Hkv + g;
+      if (tile == cur.cum) p.rg_waves[2 * rg] = static_cast<int32_t>(wid);
+      if (seg_end == cur.cum + cur.nb) p.rg_waves[2 * rg + 1] = static_cast<int32_t>(wid);
+    }
     tile = seg_end;
     if (tile < hi) next_row_group(p, cur);
   }
 }
 
-// Merge the partials of one (row, head) of the balanced schedule: the waves
-// that covered row group rg are those holding its first and last tile, found
-// from the same range formula the partial kernel uses (wave w holds tile t iff
-// floor(T w / W) <= t < floor(T (w + 1) / W), i.e. w = floor(((t + 1) W - 1) / T)).
-// m is in the log2 domain.  Rows without a visible tile get 0.
+// Merge the partials of one (row, head) of the balanced schedule.  The partial
+// kernel records, per row group, the first and the last wave that covered it;
+// those waves wrote slots first + rg .. last + rg.  m is in the log2 domain.
+// The first kCombinePrefetch partial rows are loaded before the weights are
+// known so their latency overlaps the reductions.  Rows without a visible
+// tile get 0 (their row-group record is stale and not read).
+constexpr int kCombinePrefetch = 8;
+
 template <typename QT>
 __global__ __launch_bounds__(256) void decode_combine_balanced(DecodeParams p) {
   __shared__ float weight[kMaxDecodeWaves];
   __shared__ float redf[4];
-  __shared__ int64_t redi[2][4];
   const int bh = blockIdx.x;
   const int b = bh / p.H;
   const int h = bh - b * p.H;
@@ -518,40 +536,23 @@ __global__ __launch_bounds__(256) void decode_combine_balanced(DecodeParams p) {
   const int wave = threadIdx.x >> 6;
   QT* out = reinterpret_cast<QT*>(p.out) + static_cast<int64_t>(bh) * p.D;
 
-  int64_t before = 0, total = 0;
-  for (int r = threadIdx.x; r < p.B; r += blockDim.x) {
-    const int64_t nb = row_tiles(p, r);
-    total += nb;
-    if (r < b) before += nb;
-  }
-#pragma unroll
-  for (int off = 32; off > 0; off >>= 1) {
-    total += __shfl_xor(total, off, 64);
-    before += __shfl_xor(before, off, 64);
-  }
-  if (lane == 0) {
-    redi[0][wave] = total;
-    redi[1][wave] = before;
-  }
-  __syncthreads();
-  total = redi[0][0] + redi[0][1] + redi[0][2] + redi[0][3];
-  before = redi[1][0] + redi[1][1] + redi[1][2] + redi[1][3];
-  const int64_t nbb = row_tiles(p, b);
-  if (nbb == 0) {
+  const int64_t rg = static_cast<int64_t>(b) * p.Hkv + g;
+  const int32_t w_first = p.rg_waves[2 * rg];
+  const int32_t w_last = p.rg_waves[2 * rg + 1];
+  if (row_tiles(p, b) == 0) {
     for (int d = threadIdx.x; d < p.D; d += blockDim.x) Elem<QT>::store(out + d, 0.f);
     return;
   }
-  const int64_t T = total * p.Hkv;
-  const int64_t W = p.n_waves;
-  const int64_t cum = before * p.Hkv + g * nbb;
-  const int64_t w_first = ((cum + 1) * W - 1) / T;
-  const int64_t w_last = ((cum + nbb) * W - 1) / T;
-  const int n = static_cast<int>(w_last - w_first + 1);
-  const int64_t slot0 = w_first + static_cast<int64_t>(b) * p.Hkv + g;
+  const int n = w_last - w_first + 1;
+  const int64_t slot0 = w_first + rg;
   const float* ml = p.part_ml + (slot0 * p.G + hh) * 2;
   const float* po = p.part_o + (slot0 * p.G + hh) * p.D;
   const int64_t sml = 2 * static_cast<int64_t>(p.G);
   const int64_t so = static_cast<int64_t>(p.G) * p.D;
+  const int d0 = threadIdx.x;  // D <= 256: one column per thread
+  float pre[kCombinePrefetch];
+#pragma unroll
+  for (int s = 0; s < kCombinePrefetch; ++s) pre[s] = (s < n && d0 < p.D) ? po[s * so + d0] : 0.f;
 
   float big = -INFINITY;
   for (int s = threadIdx.x; s < n; s += blockDim.x) big = fmaxf(big, ml[s * sml]);
@@ -572,17 +573,21 @@ __global__ __launch_bounds__(256) void decode_combine_balanced(DecodeParams p) {
   __syncthreads();
   den = redf[0] + redf[1] + redf[2] + redf[3];
   const float inv = den > 0.f ? 1.f / den : 0.f;
-  for (int d = threadIdx.x; d < p.D; d += blockDim.x) {
-    float acc0 = 0.f, acc1 = 0.f, acc2 = 0.f, acc3 = 0.f;
-    int s = 0;
-    for (; s + 4 <= n; s += 4) {
-      acc0 += weight[s + 0] * po[(s + 0) * so + d];
-      acc1 += weight[s + 1] * po[(s + 1) * so + d];
-      acc2 += weight[s + 2] * po[(s + 2) * so + d];
-      acc3 += weight[s + 3] * po[(s + 3) * so + d];
+  if (d0 < p.D) {
+    float acc0 = 0.f, acc1 = 0.f;
+#pragma unroll
+    for (int s = 0; s < kCombinePrefetch; s += 2) {
+      if (s < n) acc0 += weight[s] * pre[s];
+      if (s + 1 < n) acc1 += weight[s + 1] * pre[s + 1];
     }
-    for (; s < n; ++s) acc0 += weight[s] * po[s * so + d];
-    Elem<QT>::store(out + d, ((acc0 + acc1) + (acc2 + acc3)) * inv);
+    float acc2 = 0.f, acc3 = 0.f;
+    int s = kCombinePrefetch;
+    for (; s + 2 <= n; s += 2) {
+      acc2 += weight[s] * po[s * so + d0];
+      acc3 += weight[s + 1] * po[(s + 1) * so + d0];
+    }
+    if (s < n) acc2 += weight[s] * po[s * so + d0];
+    Elem<QT>::store(out + d0, ((acc0 + acc1) + (acc2 + acc3)) * inv);
   }
 }
 
@@ -667,13 +672,14 @@ static int64_t balanced_waves(int64_t row_groups, int64_t max_tokens) {
 }
 
 // Bytes of workspace either path may need.  The generic path stores
-// (B*H, n_splits, D + 2) floats; the MFMA path (W + B*H_kv) slots of G heads,
-// bounded here with H_kv <= H and W computed for H row groups per row.
+// (B*H, n_splits, D + 2) floats; the MFMA path (W + B*H_kv) slots of G heads
+// plus two int32 per row group, bounded here with H_kv <= H and W computed
+// for H row groups per row.
 static int64_t decode_workspace_bytes(int64_t batch, int heads, int head_dim, int64_t max_tokens, int block_size) {
   const int split = choose_split_tokens(max_tokens, block_size);
   const int64_t n_splits = std::max<int64_t>(1, ceil_div(std::max<int64_t>(max_tokens, 1), split));
   const int64_t generic = batch * heads * n_splits * (head_dim + 2);
-  const int64_t balanced = (balanced_waves(batch * heads, max_tokens) + batch) * heads * (head_dim + 2);
+  const int64_t balanced = (balanced_waves(batch * heads, max_tokens) + batch) * heads * (head_dim + 2) + 2 * batch * heads;
   return std::max(generic, balanced) * static_cast<int64_t>(sizeof(float));
 }
 
@@ -826,7 +832,9 @@ static int run_decode(const DecodeHostArgs& a, hipStream_t stream) {
   p.n_waves = static_cast<int>(balanced_waves(static_cast<int64_t>(p.B) * p.Hkv, a.max_tokens));
   p.part_o = reinterpret_cast<float*>(a.workspace);
   if (a.q_dtype == QA_BF16 && kv.dtype == QA_BF16 && mfma_eligible(p, a, kv)) {
-    p.part_ml = p.part_o + (static_cast<int64_t>(p.n_waves) + static_cast<int64_t>(p.B) * p.Hkv) * p.G * p.D;
+    const int64_t slots = static_cast<int64_t>(p.n_waves) + static_cast<int64_t>(p.B) * p.Hkv;
+    p.part_ml = p.part_o + slots * p.G * p.D;
+    p.rg_waves = reinterpret_cast<int32_t*>(p.part_ml + slots * p.G * 2);
     return launch_mfma(p, stream);
   }
   p.part_ml = p.part_o + static_cast<int64_t>(p.B) * p.H * p.n_splits * p.D;
