@@ -122,6 +122,17 @@ __device__ __forceinline__ cfloat4 mma(const half_t* A, int lda, const half_t* B
   return acc;
 }
 
+// C(16x16) += A(16x16) * B(16x16), fp32 operands in LDS with leading dim LDF,
+// by v_mfma_f32_16x16x4_f32 (lane l: A[l%16][k0 + l/16], B[k0 + l/16][l%16]).
+// Lane l gets C[4(l/16) + r][l % 16].
+__device__ __forceinline__ cfloat4 mma_f32_16(const float* A, const float* B, cfloat4 acc, int lane) {
+  const int i = lane & 15;
+  const int kq = lane >> 4;
+#pragma unroll
+  for (int k0 = 0; k0 < 16; k0 += 4) acc = __builtin_amdgcn_mfma_f32_16x16x4f32(A[i * LDF + k0 + kq], B[(k0 + kq) * LDF + i], acc, 0, 0, 0);
+  return acc;
+}
+
 // Raw in_proj row slice (bf16) of token tg for this wave: 32 q/k channels and 8 v channels.
 __device__ __forceinline__ void load_raw(const Params& p, int64_t b, int64_t tg, int q_ch0, int k_ch0, int v_ch0, int wave, uint4 (&raw_qk)[4], uint4& raw_v) {
   const int ch_qk = wave < 4 ? q_ch0 + 32 * wave : k_ch0 + 32 * (wave - 4);
@@ -149,7 +160,8 @@ __device__ __forceinline__ void store4h(half_t* dst, float a, float b, float c, 
 }
 
 __device__ __forceinline__ float softplus_ref(float x) { return x > 20.f ? x : log1pf(__expf(x)); }
-__device__ __forceinline__ float silu_ref(float x) { return x / (1.f + __expf(-x)); }
+// x * sigmoid(x); the reciprocal is v_rcp_f32 (1 ulp), not the IEEE division sequence.
+__device__ __forceinline__ float silu_ref(float x) { return x * __builtin_amdgcn_rcpf(1.f + __expf(-x)); }
 
 __global__ __launch_bounds__(NT) void chunk_kernel(Params p) {
   extern __shared__ __align__(16) unsigned char smem[];
@@ -287,7 +299,7 @@ __global__ __launch_bounds__(NT) void chunk_kernel(Params p) {
         }
       }
       nrm[wave * CH + tok] = ss;
-      __syncthreads();  // every halo read is done before lanes 61..63 overwrite it
+      lds_barrier();  // every halo read is done before lanes 61..63 overwrite it
       if (tok >= CH - (KCONV - 1)) {
         const int hs = tok - (CH - (KCONV - 1));
 #pragma unroll
@@ -329,7 +341,7 @@ __global__ __launch_bounds__(NT) void chunk_kernel(Params p) {
       s_rq[tok] = rsqrtf(sq + 1e-6f) * rsqrtf(static_cast<float>(DK));
       s_rk[tok] = rsqrtf(sk + 1e-6f);
     }
-    __syncthreads();
+    lds_barrier();
 
     // transposed, scaled copies: Kt = K^T, Xt = beta*gamma*K^T, Yt = beta*V^T
     for (int idx = tid; idx < DK * (CH / 4); idx += NT) {
@@ -356,7 +368,7 @@ __global__ __launch_bounds__(NT) void chunk_kernel(Params p) {
       }
       store4h(Yt + dv * LD64 + 4 * tq, yv[0], yv[1], yv[2], yv[3]);
     }
-    __syncthreads();
+    lds_barrier();
 
     // ---------------- A = beta_i exp(G_i - G_l) K K^T (strictly lower), fp32
     for (int tile = wave; tile < 16; tile += NW) {
@@ -372,23 +384,26 @@ __global__ __launch_bounds__(NT) void chunk_kernel(Params p) {
         Am[i * LDF + l] = l < i ? s_beta[i] * s_rk[i] * s_rk[l] * __expf(s_G[i] - s_G[l]) * acc[r] : 0.f;
       }
     }
-    __syncthreads();
+    lds_barrier();
 
     // ---------------- wave 0: diagonal 16x16 blocks of T = (I + A)^-1 by column
-    // forward substitution; the other waves: Aqk and O^T = gamma * S0^T Q^T.
+    // forward substitution in registers (lane = block qb, column c; x_i final
+    // once every x_l, l < i, has been subtracted); the other waves: Aqk and
+    // O^T = gamma * S0^T Q^T.
     cfloat4 O[2];
     if (wave == 0) {
       const int qb = lane >> 4;
       const int c = lane & 15;
-      // column c of D_qb = (I + A_qb,qb)^-1, rows in order; finished rows are read back from Tb
-      float* tcol = Tb + (16 * qb) * LDF + 16 * qb + c;
-#pragma unroll 1
-      for (int i = 0; i < 16; ++i) {
-        float acc = i == c ? 1.f : 0.f;
-        const float* arow = Am + (16 * qb + i) * LDF + 16 * qb;
-        for (int l = 0; l < i; ++l) acc -= arow[l] * tcol[l * LDF];
-        tcol[i * LDF] = acc;
-      }
+      const float* ab = Am + (16 * qb) * LDF + 16 * qb;
+      float x[16];
+#pragma unroll
+      for (int i = 0; i < 16; ++i) x[i] = i == c ? 1.f : 0.f;
+#pragma unroll
+      for (int l = 0; l < 16; ++l)
+#pragma unroll
+        for (int i = l + 1; i < 16; ++i) x[i] -= ab[i * LDF + l] * x[l];
+#pragma unroll
+      for (int i = 0; i < 16; ++i) Tb[(16 * qb + i) * LDF + 16 * qb + c] = x[i];
     } else {
       // Aqk[i][l] = exp(G_i - G_l) (q_i . k_l), l <= i, computed as (K Q^T)[l][i]
       for (int tile = wave - 1; tile < 16; tile += NW - 1) {
@@ -406,7 +421,30 @@ __global__ __launch_bounds__(NT) void chunk_kernel(Params p) {
         store4h(Aqk + i * LD64 + 16 * tl + 4 * lq, v[0], v[1], v[2], v[3]);
       }
     }
-    // O^T tiles (dv tile td, token tile tt): tile index ot = 2*wave + s, two per wave
+    lds_barrier();
+
+    // ---------------- off-diagonal blocks of T: T_pq = -D_p sum_{k=q}^{p-1} A_pk T_kq
+    // level d: wave q < 4 - d builds block (p, q) = (q + d, q) with fp32 MFMAs;
+    // the partial sum M is parked in the unused upper block (q, p) of Tb and read
+    // back by the same wave (LDS is in order within a wave).
+#pragma unroll
+    for (int d = 1; d <= 3; ++d) {
+      if (wave < 4 - d) {
+        const int q = wave;
+        const int pb = q + d;
+        cfloat4 m = {0.f, 0.f, 0.f, 0.f};
+        for (int k = q; k < pb; ++k) m = mma_f32_16(Am + (16 * pb) * LDF + 16 * k, Tb + (16 * k) * LDF + 16 * q, m, lane);
+#pragma unroll
+        for (int r = 0; r < 4; ++r) Tb[(16 * q + 4 * lq + r) * LDF + 16 * pb + lc] = m[r];
+        cfloat4 t = {0.f, 0.f, 0.f, 0.f};
+        t = mma_f32_16(Tb + (16 * pb) * LDF + 16 * pb, Tb + (16 * q) * LDF + 16 * pb, t, lane);
+#pragma unroll
+        for (int r = 0; r < 4; ++r) Tb[(16 * pb + 4 * lq + r) * LDF + 16 * q + lc] = -t[r];
+      }
+      lds_barrier();
+    }
+    // O^T tiles (dv tile td, token tile tt): tile index ot = 2*wave + s, two per wave;
+    // Qs is overwritten by the fp16 copies of T below
 #pragma unroll
     for (int s = 0; s < 2; ++s) {
       const int ot = 2 * wave + s;
@@ -418,41 +456,8 @@ __global__ __launch_bounds__(NT) void chunk_kernel(Params p) {
 #pragma unroll
       for (int r = 0; r < 4; ++r) O[s][r] = acc[r] * gam;
     }
-    __syncthreads();
+    lds_barrier();
 
-    // ---------------- off-diagonal blocks of T: T_pq = -D_p sum_{k=q}^{p-1} A_pk T_kq
-    // level d handles blocks (q + d, q); the partial sum M is parked in the
-    // unused upper block (q, p) of Tb.
-#pragma unroll
-    for (int d = 1; d <= 3; ++d) {
-      const int nblk = 4 - d;
-      for (int idx = tid; idx < nblk * 256; idx += NT) {
-        const int q = idx >> 8;
-        const int pb = q + d;
-        const int r = (idx >> 4) & 15;
-        const int c = idx & 15;
-        float acc = 0.f;
-        for (int k = q; k < pb; ++k) {
-          const float* arow = Am + (16 * pb + r) * LDF + 16 * k;
-#pragma unroll
-          for (int e = 0; e < 16; ++e) acc += arow[e] * Tb[(16 * k + e) * LDF + 16 * q + c];
-        }
-        Tb[(16 * q + r) * LDF + 16 * pb + c] = acc;
-      }
-      __syncthreads();
-      for (int idx = tid; idx < nblk * 256; idx += NT) {
-        const int q = idx >> 8;
-        const int pb = q + d;
-        const int r = (idx >> 4) & 15;
-        const int c = idx & 15;
-        float acc = 0.f;
-        const float* drow = Tb + (16 * pb + r) * LDF + 16 * pb;
-#pragma unroll
-        for (int e = 0; e < 16; ++e) acc += drow[e] * Tb[(16 * q + e) * LDF + 16 * pb + c];
-        Tb[(16 * pb + r) * LDF + 16 * q + c] = -acc;
-      }
-      __syncthreads();
-    }
     // T as fp16 hi + lo, zero above the diagonal
     for (int idx = tid; idx < CH * (CH / 4); idx += NT) {
       const int i = idx >> 4;
@@ -468,7 +473,7 @@ __global__ __launch_bounds__(NT) void chunk_kernel(Params p) {
       store4h(Thi + i * LD64 + 4 * lq4, hi[0], hi[1], hi[2], hi[3]);
       store4h(Tlo + i * LD64 + 4 * lq4, lo[0], lo[1], lo[2], lo[3]);
     }
-    __syncthreads();
+    lds_barrier();
 
     // ---------------- W^T = Xt T^T -> Wn[i][dk] = -W; U = T Yt^T (registers)
     for (int tile = wave; tile < 32; tile += NW) {
@@ -490,7 +495,7 @@ __global__ __launch_bounds__(NT) void chunk_kernel(Params p) {
       acc = mma<CH>(Tlo + 16 * ti * LD64, LD64, Yt + 16 * tv * LD64, LD64, acc, lane);
       Dl[s] = acc;
     }
-    __syncthreads();
+    lds_barrier();
 
     // ---------------- delta = U - W S0; keep delta^T and exp(G_C - G) delta^T in LDS
     const float gC = s_G[CH - 1];
@@ -508,7 +513,7 @@ __global__ __launch_bounds__(NT) void chunk_kernel(Params p) {
       for (int r = 0; r < 4; ++r) sc[r] = __expf(gC - s_G[i0 + r]) * s_rk[i0 + r] * Dl[s][r];
       store4h(DDt + dv * LD64 + i0, sc[0], sc[1], sc[2], sc[3]);
     }
-    __syncthreads();
+    lds_barrier();
 
     // ---------------- O^T += delta^T Aqk^T -> output; S = gamma_C S + K^T (D delta)
 #pragma unroll
@@ -539,7 +544,7 @@ __global__ __launch_bounds__(NT) void chunk_kernel(Params p) {
       S[tv] = mma<CH>(Kt + 16 * wave * LD64, LD64, DDt + 16 * tv * LD64, LD64, acc, lane);
       store4h(St + (16 * tv + lc) * LD128 + 16 * wave + 4 * lq, S[tv][0], S[tv][1], S[tv][2], S[tv][3]);
     }
-    __syncthreads();
+    lds_barrier();
   }
 
   if (p.state_out != nullptr) {

@@ -71,6 +71,11 @@ __device__ __forceinline__ int64_t load_index(const IT* p) {
   return static_cast<int64_t>(*p);
 }
 
+// Workgroup barrier that orders LDS traffic only.  __syncthreads() also waits
+// for every outstanding global load and store of the wave, which would drain
+// prefetches issued before it; cross-wave data here always goes through LDS.
+__device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+
 __device__ __forceinline__ float wave_sum(float v) {
 #pragma unroll
   for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
