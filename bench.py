@@ -227,7 +227,7 @@ def time_delta(w, steps: int, warmup: int) -> float:
         return hip_ops.chunk_gated_delta_rule(w["mixed"], w["a"], w["b"], w["a_log"], w["dt_bias"], w["conv_w"], key_heads=w["key_heads"],
                                               value_heads=w["value_heads"], keep_conv_state=False)
 
-    return _timed(step, steps, warmup, ("chunk_gated_delta",))
+    return _timed(step, steps, warmup, ("chunk_prep", "chunk_gate", "chunk_gated_delta"))
 
 
 # ----------------------------------------------------------------------------- config 3

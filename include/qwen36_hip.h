@@ -211,16 +211,18 @@ int qa_gated_delta_step(const float* qkv, int64_t qkv_stride_b,
                         int32_t key_dim, int32_t value_dim, hipStream_t stream);
 
 /* Chunked gated delta-rule prefill of one linear-attention layer, from the
- * raw in_proj outputs.  mixed_qkv (B, T, 2*Hqk*dk + Hv*dv) float32/bfloat16,
+ * raw in_proj outputs.  mixed_qkv (B, T, 2*Hqk*dk + Hv*dv) bfloat16,
  * a, b (B, T, Hv), a_log/dt_bias (Hv) fp32, conv_weight (C, 4) fp32,
  * conv_state_in/out (B, C, 3) fp32 (NULL in = zeros, NULL out = not kept),
  * initial_state/final_state (B, Hv, dk, dv) fp32 (NULL in = zeros).  Writes
- * out (B, T, Hv, dv) float32/bfloat16.  Fuses the conv1d + SiLU, L2 norm,
- * q scale and gating of src/reference_ops.py:240-283 with the recurrence of
- * :291-322, computed in 64-token chunks (WY/UT form) on fp16 MFMA with fp32
+ * out (B, T, Hv, dv) float32/bfloat16.  Computes the conv1d + SiLU, L2 norm,
+ * q scale and gating of src/reference_ops.py:240-283 and the recurrence of
+ * :291-322 in 64-token chunks (WY/UT form) on fp16 MFMA with fp32
  * accumulation and an fp32 state.  dk = dv = 128, conv kernel 4.  The
- * reference has no chunked kernel: its prefill runs the token-serial
- * recurrence (src/tp_runtime.py:2744-2787).                               */
+ * workspace (256-byte aligned, qa_chunk_gated_delta_workspace bytes) holds the
+ * normalised fp16 q/k/v and the gates between the launches.  The reference
+ * has no chunked kernel: its prefill runs the token-serial recurrence
+ * (src/tp_runtime.py:2744-2787).                                          */
 int qa_chunk_gated_delta_rule(const void* mixed_qkv, int32_t x_dtype, int64_t x_stride_b, int64_t x_stride_t,
                               const void* a, const void* b, int32_t ab_dtype, int64_t ab_stride_b, int64_t ab_stride_t,
                               const float* a_log, const float* dt_bias, const float* conv_weight,
@@ -228,7 +230,12 @@ int qa_chunk_gated_delta_rule(const void* mixed_qkv, int32_t x_dtype, int64_t x_
                               const float* initial_state, float* final_state,
                               void* out, int32_t out_dtype, int64_t out_stride_b, int64_t out_stride_t,
                               int64_t batch, int64_t seq, int32_t key_heads, int32_t value_heads,
-                              int32_t key_dim, int32_t value_dim, int32_t conv_kernel, hipStream_t stream);
+                              int32_t key_dim, int32_t value_dim, int32_t conv_kernel,
+                              void* workspace, int64_t workspace_bytes, hipStream_t stream);
+
+/* Workspace bytes qa_chunk_gated_delta_rule needs for these sizes (dk = dv = 128);
+ * no counterpart in the reference, whose prefill keeps no intermediate buffers. */
+int64_t qa_chunk_gated_delta_workspace(int64_t batch, int64_t seq, int32_t key_heads, int32_t value_heads);
 
 /* LDS bytes one chunked-prefill workgroup reserves (for capacity planning). */
 int64_t qa_chunk_gated_delta_lds_bytes(void);

@@ -102,8 +102,9 @@ SIGNATURES: dict[str, tuple[Any, list[Any]]] = {
         c_int32,
         [c_void_p, c_int32, c_int64, c_int64, c_void_p, c_void_p, c_int32, c_int64, c_int64, c_void_p, c_void_p, c_void_p, c_void_p,
          c_void_p, c_void_p, c_void_p, c_void_p, c_int32, c_int64, c_int64, c_int64, c_int64, c_int32, c_int32, c_int32, c_int32,
-         c_int32, c_void_p],
+         c_int32, c_void_p, c_int64, c_void_p],
     ),
+    "qa_chunk_gated_delta_workspace": (c_int64, [c_int64, c_int64, c_int32, c_int32]),
     "qa_chunk_gated_delta_lds_bytes": (c_int64, []),
     "qa_paged_attention_prefill": (
         c_int32,

@@ -582,10 +582,12 @@ def chunk_gated_delta_rule(
     out = torch.empty((batch, seq, value_heads, dv), dtype=out_dtype, device=device)
     final = torch.empty((batch, value_heads, dk, dv), dtype=torch.float32, device=device)
     conv_out = torch.empty((batch, channels, 3), dtype=torch.float32, device=device) if keep_conv_state else None
+    ws_bytes = lib.qa_chunk_gated_delta_workspace(batch, seq, int(key_heads), int(value_heads))
+    workspace = torch.empty(ws_bytes, dtype=torch.uint8, device=device)
     status = lib.qa_chunk_gated_delta_rule(
         _ptr(mixed_qkv), _code(mixed_qkv), mixed_qkv.stride(0), mixed_qkv.stride(1), _ptr(a), _ptr(b), _code(a), a.stride(0), a.stride(1),
         _ptr(alog), _ptr(dtb), _ptr(w), _ptr(conv_in), _ptr(conv_out), _ptr(state_in), _ptr(final), _ptr(out), _code(out), out.stride(0),
-        out.stride(1), batch, seq, int(key_heads), int(value_heads), dk, dv, 4, _stream(device),
+        out.stride(1), batch, seq, int(key_heads), int(value_heads), dk, dv, 4, _ptr(workspace), ws_bytes, _stream(device),
     )
     L.check(lib, status, "chunk_gated_delta_rule")
     return out, final, conv_out
