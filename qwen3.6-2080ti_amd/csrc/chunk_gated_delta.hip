@@ -9,7 +9,9 @@
 //     window in registers, and written as fp16 to a workspace: q and k
 //     token-major, k and v also as per-chunk transposed tiles
 //     [channel][token] -- the token-contiguous operands of the products that
-//     reduce over tokens.  It also writes the conv state.
+//     reduce over tokens; those go through a per-wave LDS tile so every
+//     chunk's tile is written as one contiguous block.  It also writes the
+//     conv state.
 //  2. gate_kernel -- g = -exp(A_log) softplus(a + dt_bias), beta = sigmoid(b)
 //     (src/reference_ops.py:271-275) and G, the inclusive sum of g inside each
 //     chunk.
@@ -174,11 +176,16 @@ __device__ __forceinline__ void store4h(half_t* dst, float a, float b, float c, 
 // Wave = (row b, head, run of RUN tokens); lane l holds channels 2l, 2l+1 of
 // the head (one bf16 pair per token, so a wave reads 256 contiguous bytes per
 // token).  Heads are numbered in channel order: q heads, k heads, v heads.
+constexpr int PREP_LD = 72;  // halfs per channel row of a wave's staging tile (16-byte aligned rows)
+
 __global__ __launch_bounds__(256) void prep_kernel(PrepParams p) {
+  __shared__ __align__(16) half_t stage_all[4][128 * PREP_LD];
   const int lane = threadIdx.x & 63;
+  half_t* stage = stage_all[__builtin_amdgcn_readfirstlane(threadIdx.x >> 6)];
   const int NH = 2 * p.Hk + p.Hv;
   const int64_t nruns = (p.tp + RUN - 1) / RUN;
-  const int64_t item = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
+  // the work item is wave-uniform, so its address arithmetic runs on the scalar unit
+  const int64_t item = static_cast<int64_t>(blockIdx.x) * 4 + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   if (item >= static_cast<int64_t>(p.B) * NH * nruns) return;
   const int64_t run = item % nruns;
   const int head = static_cast<int>((item / nruns) % NH);
@@ -214,16 +221,21 @@ __global__ __launch_bounds__(256) void prep_kernel(PrepParams p) {
   const int hk = kind == 1 ? head - p.Hk : head;
   const int hv = head - 2 * p.Hk;
 
-  uint32_t raw[PU];
+  // raw inputs of the next two PU-token groups are in flight while a group is computed
+  uint32_t raw[PU], raw2[PU];
 #pragma unroll
-  for (int jj = 0; jj < PU; ++jj) raw[jj] = t0 + jj < p.T ? *reinterpret_cast<const uint32_t*>(xrow + (t0 + jj) * p.x_st) : 0u;
+  for (int jj = 0; jj < PU; ++jj) {
+    raw[jj] = t0 + jj < p.T ? *reinterpret_cast<const uint32_t*>(xrow + (t0 + jj) * p.x_st) : 0u;
+    raw2[jj] = t0 + PU + jj < p.T ? *reinterpret_cast<const uint32_t*>(xrow + (t0 + PU + jj) * p.x_st) : 0u;
+  }
   for (int64_t t = t0; t < t1; t += PU) {
     uint32_t cur[PU];
 #pragma unroll
-    for (int jj = 0; jj < PU; ++jj) cur[jj] = raw[jj];
-    if (t + PU < t1) {
-#pragma unroll
-      for (int jj = 0; jj < PU; ++jj) raw[jj] = t + PU + jj < p.T ? *reinterpret_cast<const uint32_t*>(xrow + (t + PU + jj) * p.x_st) : 0u;
+    for (int jj = 0; jj < PU; ++jj) {
+      cur[jj] = raw[jj];
+      raw[jj] = raw2[jj];
+      const int64_t tn = t + 2 * PU + jj;
+      raw2[jj] = tn < p.T && tn < t1 ? *reinterpret_cast<const uint32_t*>(xrow + tn * p.x_st) : 0u;
     }
     float y0[PU], y1[PU], ss[PU];
 #pragma unroll
@@ -246,7 +258,7 @@ __global__ __launch_bounds__(256) void prep_kernel(PrepParams p) {
     if (kind < 2) {
 #pragma unroll
       for (int jj = 0; jj < PU; ++jj) {
-        const float r = rsqrtf(wave_sum(ss[jj]) + 1e-6f) * qscale;
+        const float r = rsqrtf(wave_sum_dpp(ss[jj]) + 1e-6f) * qscale;
         y0[jj] *= r;
         y1[jj] *= r;
       }
@@ -260,18 +272,27 @@ __global__ __launch_bounds__(256) void prep_kernel(PrepParams p) {
       }
     }
     if (kind > 0) {
-      // transposed tile [channel][token] of this chunk: 8 tokens = 16 bytes per channel row
-      const int64_t c = t / CH;
-      half_t* tile = kind == 1 ? p.knt + ((b * p.Hk + hk) * p.nch + c) * (DK * CH) : p.vt + ((b * p.Hv + hv) * p.nch + c) * (DV * CH);
+      // transposed tile [channel][token] of this chunk, staged in this wave's LDS
+      // tile (8 tokens = 16 bytes per channel row per step) and written out as one
+      // contiguous 16 KB block once the chunk's 64 tokens are in
       f16x8_v c0, c1;
 #pragma unroll
       for (int jj = 0; jj < PU; ++jj) {
         c0[jj] = static_cast<half_t>(y0[jj]);
         c1[jj] = static_cast<half_t>(y1[jj]);
       }
-      const int tc = static_cast<int>(t - c * CH);
-      *reinterpret_cast<f16x8_v*>(tile + (2 * lane) * CH + tc) = c0;
-      *reinterpret_cast<f16x8_v*>(tile + (2 * lane + 1) * CH + tc) = c1;
+      const int tc = static_cast<int>(t % CH);
+      *reinterpret_cast<f16x8_v*>(stage + (2 * lane) * PREP_LD + tc) = c0;
+      *reinterpret_cast<f16x8_v*>(stage + (2 * lane + 1) * PREP_LD + tc) = c1;
+      if (tc == CH - PU) {
+        const int64_t c = t / CH;
+        half_t* tile = kind == 1 ? p.knt + ((b * p.Hk + hk) * p.nch + c) * (DK * CH) : p.vt + ((b * p.Hv + hv) * p.nch + c) * (DV * CH);
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int pc = lane + 64 * r;  // 1024 pieces of 16 bytes: row pc / 8, column 8 (pc % 8)
+          *reinterpret_cast<f16x8_v*>(tile + 8 * pc) = *reinterpret_cast<const f16x8_v*>(stage + (pc >> 3) * PREP_LD + 8 * (pc & 7));
+        }
+      }
     }
   }
 
@@ -299,7 +320,7 @@ __global__ __launch_bounds__(256) void prep_kernel(PrepParams p) {
 // 2. gating: wave = (row b, value head, chunk), lane = token of the chunk.
 __global__ __launch_bounds__(256) void gate_kernel(GateParams p) {
   const int lane = threadIdx.x & 63;
-  const int64_t item = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
+  const int64_t item = static_cast<int64_t>(blockIdx.x) * 4 + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   if (item >= static_cast<int64_t>(p.B) * p.Hv * p.nch) return;
   const int64_t c = item % p.nch;
   const int hv = static_cast<int>((item / p.nch) % p.Hv);

@@ -82,6 +82,31 @@ __device__ __forceinline__ float wave_sum(float v) {
   return v;
 }
 
+// Sum over the 64 lanes, returned to every lane: DPP quad swaps and row
+// rotations give each 16-lane row its sum, then the four row sums are read out
+// with v_readlane (no LDS round trips).
+__device__ __forceinline__ float wave_sum_dpp(float v) {
+  auto dpp_add = [](float x, int ctrl) -> float {
+    int moved = 0;
+    switch (ctrl) {
+      case 0xB1: moved = __builtin_amdgcn_update_dpp(0, __float_as_int(x), 0xB1, 0xF, 0xF, false); break;  // quad_perm [1,0,3,2]
+      case 0x4E: moved = __builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x4E, 0xF, 0xF, false); break;  // quad_perm [2,3,0,1]
+      case 0x124: moved = __builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x124, 0xF, 0xF, false); break;  // row_ror:4
+      default: moved = __builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x128, 0xF, 0xF, false); break;  // row_ror:8
+    }
+    return x + __int_as_float(moved);
+  };
+  v = dpp_add(v, 0xB1);
+  v = dpp_add(v, 0x4E);
+  v = dpp_add(v, 0x124);
+  v = dpp_add(v, 0x128);
+  const float r0 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 0));
+  const float r1 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 16));
+  const float r2 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 32));
+  const float r3 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 48));
+  return (r0 + r1) + (r2 + r3);
+}
+
 __device__ __forceinline__ float wave_max(float v) {
 #pragma unroll
   for (int off = 32; off > 0; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, 64));
