@@ -176,7 +176,8 @@ __device__ __forceinline__ void store4h(half_t* dst, float a, float b, float c, 
 // Wave = (row b, head, run of RUN tokens); lane l holds channels 2l, 2l+1 of
 // the head (one bf16 pair per token, so a wave reads 256 contiguous bytes per
 // token).  Heads are numbered in channel order: q heads, k heads, v heads.
-constexpr int PREP_LD = 72;  // halfs per channel row of a wave's staging tile (16-byte aligned rows)
+constexpr int PREP_FLUSH = 32;  // tokens staged per channel row before they are written out
+constexpr int PREP_LD = PREP_FLUSH + 8;  // halfs per channel row of a wave's staging tile (16-byte aligned rows)
 
 __global__ __launch_bounds__(256) void prep_kernel(PrepParams p) {
   __shared__ __align__(16) half_t stage_all[4][128 * PREP_LD];
@@ -281,16 +282,20 @@ __global__ __launch_bounds__(256) void prep_kernel(PrepParams p) {
         c0[jj] = static_cast<half_t>(y0[jj]);
         c1[jj] = static_cast<half_t>(y1[jj]);
       }
-      const int tc = static_cast<int>(t % CH);
+      const int tc = static_cast<int>(t % PREP_FLUSH);
       *reinterpret_cast<f16x8_v*>(stage + (2 * lane) * PREP_LD + tc) = c0;
       *reinterpret_cast<f16x8_v*>(stage + (2 * lane + 1) * PREP_LD + tc) = c1;
-      if (tc == CH - PU) {
+      if (tc == PREP_FLUSH - PU) {
         const int64_t c = t / CH;
+        const int tbase = static_cast<int>((t - tc) % CH);
         half_t* tile = kind == 1 ? p.knt + ((b * p.Hk + hk) * p.nch + c) * (DK * CH) : p.vt + ((b * p.Hv + hv) * p.nch + c) * (DV * CH);
+        constexpr int PPR = PREP_FLUSH / 8;  // 16-byte pieces per channel row
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const int pc = lane + 64 * r;  // 1024 pieces of 16 bytes: row pc / 8, column 8 (pc % 8)
-          *reinterpret_cast<f16x8_v*>(tile + 8 * pc) = *reinterpret_cast<const f16x8_v*>(stage + (pc >> 3) * PREP_LD + 8 * (pc & 7));
+        for (int r = 0; r < 128 * PPR / 64; ++r) {
+          const int pc = lane + 64 * r;
+          const int row = pc / PPR;
+          const int col = pc % PPR;
+          *reinterpret_cast<f16x8_v*>(tile + row * CH + tbase + 8 * col) = *reinterpret_cast<const f16x8_v*>(stage + row * PREP_LD + 8 * col);
         }
       }
     }
