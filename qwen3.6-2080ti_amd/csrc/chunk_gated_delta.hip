@@ -32,11 +32,15 @@
 // v_mfma_f32_16x16x32_f16 on 16x16 output tiles with fp16 operands in LDS (fp32
 // accumulation).  Every LDS operand is stored with the reduction axis
 // contiguous; an output is written in whichever orientation its consumer needs
-// by choosing C or C^T (swapped operands).  T is computed in fp32 (register
-// forward substitution for the 16x16 diagonal blocks, fp32 MFMA for the rest)
-// and fed to the fp16 MFMA as a hi + lo pair, keeping the state update within
-// fp32-state tolerance.  The next chunk's tiles are loaded into registers while
-// the current one is computed; barriers order LDS only, so those loads stay in
+// by choosing C or C^T (swapped operands).  W and U are never formed through
+// T: with 16-token blocks, (I + A) W = X gives W_p = D_p (X_p - sum_{k<p} A_pk
+// W_k), D_p = (I + A_pp)^-1 (a register forward substitution in fp32); each
+// wave runs this block recurrence for its own column tiles of X = [beta gamma K
+// | beta V] on v_mfma_f32_16x16x16_f16 with fp16 hi + lo operand pairs, keeping
+// the state update within fp32-state tolerance.  The 16x16 accumulator layout
+// equals the B-operand layout, so every W_k feeds the next block from
+// registers.  The next chunk's tiles are loaded into registers while the
+// current one is computed; barriers order LDS only, so those loads stay in
 // flight across them.
 #include "qa_common.h"
 
@@ -48,6 +52,7 @@ typedef __attribute__((__vector_size__(4 * sizeof(_Float16)))) _Float16 f16x4_v;
 typedef __attribute__((__vector_size__(2 * sizeof(_Float16)))) _Float16 f16x2_v;
 typedef float cfloat4 __attribute__((ext_vector_type(4)));
 typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+typedef _Float16 h4_v __attribute__((ext_vector_type(4)));
 
 namespace cgd {
 
@@ -87,30 +92,27 @@ inline Workspace workspace_layout(int64_t batch, int64_t seq, int64_t hk, int64_
 }
 
 // ---- LDS layout of chunk_kernel (bytes)
-constexpr int OFF_RA = 0;                          // Qs | Ks  -> later Tgh | Tgl | Tbh | Tbl
+constexpr int OFF_RA = 0;                          // Qs | Ks  -> later Wn | Ub (Qs, Ks are dead once D is built)
 constexpr int OFF_QS = OFF_RA;
 constexpr int OFF_KS = OFF_RA + CH * LD128 * 2;
-constexpr int OFF_TGH = OFF_RA;                    // T diag(beta gamma), hi and lo fp16
-constexpr int OFF_TGL = OFF_TGH + CH * LD64 * 2;
-constexpr int OFF_TBH = OFF_TGL + CH * LD64 * 2;   // T diag(beta), hi and lo fp16
-constexpr int OFF_TBL = OFF_TBH + CH * LD64 * 2;
-constexpr int SZ_RA = 4 * CH * LD64 * 2;           // 36864
-constexpr int OFF_RB = OFF_RA + SZ_RA;             // Am | Tb (fp32) -> later Wn | Dt | DDt
+constexpr int OFF_WN = OFF_RA;                     // -W [tok][dk] fp16
+constexpr int OFF_UB = OFF_RA + CH * LD128 * 2;    // U [tok][dv] fp32
+constexpr int SZ_RA = 2 * CH * LD128 * 2;          // 34816
+constexpr int OFF_RB = OFF_RA + SZ_RA;             // Am | Tb (fp32) -> later Dt | DDt (dead once W, U are built)
 constexpr int OFF_AM = OFF_RB;
 constexpr int OFF_TB = OFF_RB + CH * LDF * 4;
-constexpr int OFF_WN = OFF_RB;
-constexpr int OFF_DT = OFF_RB + CH * LD128 * 2;
+constexpr int OFF_DT = OFF_RB;
 constexpr int OFF_DDT = OFF_DT + DVS * LD64 * 2;
-constexpr int SZ_RB = CH * LD128 * 2 + 2 * DVS * LD64 * 2;  // 35840
+constexpr int SZ_RB = 2 * CH * LDF * 4;            // 33280
 constexpr int OFF_KT = OFF_RB + SZ_RB;             // Kt [dk][tok]
 constexpr int OFF_VT = OFF_KT + DK * LD64 * 2;     // Vt [dv][tok] (this workgroup's half)
 constexpr int OFF_ST = OFF_VT + DVS * LD64 * 2;    // St [dv][dk] (fp16 state)
 constexpr int OFF_AQK = OFF_ST + DVS * LD128 * 2;  // Aqk [i][l]
-constexpr int OFF_SC = OFF_AQK + CH * LD64 * 2;    // beta, G, gamma per token
-constexpr int LDS_BYTES = OFF_SC + 3 * CH * 4;
+constexpr int OFF_SC = OFF_AQK + CH * LD64 * 2;    // beta, G, gamma, beta*gamma per token
+constexpr int LDS_BYTES = OFF_SC + 4 * CH * 4;
 
-static_assert(2 * CH * LD128 * 2 <= SZ_RA, "RA too small for Qs|Ks");
-static_assert(2 * CH * LDF * 4 <= SZ_RB, "RB too small for Am|Tb");
+static_assert(CH * LD128 * 2 + CH * LDF * 4 <= SZ_RA, "RA too small for Wn|Ub");
+static_assert(2 * DVS * LD64 * 2 <= SZ_RB, "RB too small for Dt|DDt");
 static_assert(LDS_BYTES <= 160 * 1024, "LDS budget");
 
 struct PrepParams {
@@ -408,13 +410,10 @@ __global__ __launch_bounds__(NT) void chunk_kernel(ChunkParams p) {
   extern __shared__ __align__(16) unsigned char smem[];
   half_t* Qs = reinterpret_cast<half_t*>(smem + OFF_QS);
   half_t* Ks = reinterpret_cast<half_t*>(smem + OFF_KS);
-  half_t* Tgh = reinterpret_cast<half_t*>(smem + OFF_TGH);
-  half_t* Tgl = reinterpret_cast<half_t*>(smem + OFF_TGL);
-  half_t* Tbh = reinterpret_cast<half_t*>(smem + OFF_TBH);
-  half_t* Tbl = reinterpret_cast<half_t*>(smem + OFF_TBL);
   float* Am = reinterpret_cast<float*>(smem + OFF_AM);
   float* Tb = reinterpret_cast<float*>(smem + OFF_TB);
   half_t* Wn = reinterpret_cast<half_t*>(smem + OFF_WN);
+  float* Ub = reinterpret_cast<float*>(smem + OFF_UB);
   half_t* Dt = reinterpret_cast<half_t*>(smem + OFF_DT);
   half_t* DDt = reinterpret_cast<half_t*>(smem + OFF_DDT);
   half_t* Kt = reinterpret_cast<half_t*>(smem + OFF_KT);
@@ -424,6 +423,7 @@ __global__ __launch_bounds__(NT) void chunk_kernel(ChunkParams p) {
   float* s_beta = reinterpret_cast<float*>(smem + OFF_SC);
   float* s_G = s_beta + CH;
   float* s_gam = s_G + CH;
+  float* s_bg = s_gam + CH;  // beta * gamma
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -469,8 +469,12 @@ __global__ __launch_bounds__(NT) void chunk_kernel(ChunkParams p) {
       s_beta[2 * tid] = nx.gb.y;
       s_G[2 * tid + 1] = nx.gb.z;
       s_beta[2 * tid + 1] = nx.gb.w;
-      s_gam[2 * tid] = __expf(nx.gb.x);
-      s_gam[2 * tid + 1] = __expf(nx.gb.z);
+      const float g0 = __expf(nx.gb.x);
+      const float g1 = __expf(nx.gb.z);
+      s_gam[2 * tid] = g0;
+      s_gam[2 * tid + 1] = g1;
+      s_bg[2 * tid] = nx.gb.y * g0;
+      s_bg[2 * tid + 1] = nx.gb.w * g1;
     }
     // (the last chunk reloads itself rather than branching, so nx stays in registers)
     nx = load_chunk(p, b, j, qh, half_id, min(ci + 1, p.nch - 1), tid);
@@ -540,71 +544,97 @@ __global__ __launch_bounds__(NT) void chunk_kernel(ChunkParams p) {
     }
     lds_barrier();
 
-    // ---------------- off-diagonal blocks of T: T_pq = -D_p sum_{k=q}^{p-1} A_pk T_kq
-    // level d: wave q < 4 - d builds block (p, q) = (q + d, q) with fp32 MFMAs;
-    // the partial sum M is parked in the unused upper block (q, p) of Tb and read
-    // back by the same wave (LDS is in order within a wave).
-#pragma unroll 1
-    for (int d = 1; d <= 3; ++d) {
-      if (wave < 4 - d) {
-        const int q = wave;
-        const int pb = q + d;
-        cfloat4 m = {0.f, 0.f, 0.f, 0.f};
-        for (int k = q; k < pb; ++k) m = mma_f32_16(Am + (16 * pb) * LDF + 16 * k, Tb + (16 * k) * LDF + 16 * q, m, lane);
+    // ---------------- W = T diag(beta gamma) K and U = T diag(beta) V by blocked forward
+    // substitution: W_p = D_p (X_p - sum_{k<p} A_pk W_k) over the 16-token blocks p.
+    // Column tiles: 8 of X_W = beta gamma K (dk) and 4 of X_U = beta V (this dv half);
+    // wave w takes W tile w and, for w < 4, U tile w.  A_pk and D_p enter as fp16
+    // hi + lo A operands; R and W_p stay fp32 in registers and are split into
+    // hi + lo B operands (the 16x16 accumulator layout is the B-operand layout).
+    {
+      // A operand slices: lane l holds row l % 16, columns 4 (l / 16) + e of a 16x16 block
+      auto a_operand = [&](const float* blk, h4_v& hi, h4_v& lo) {
 #pragma unroll
-        for (int r = 0; r < 4; ++r) Tb[(16 * q + 4 * lq + r) * LDF + 16 * pb + lc] = m[r];
-        cfloat4 t = {0.f, 0.f, 0.f, 0.f};
-        t = mma_f32_16(Tb + (16 * pb) * LDF + 16 * pb, Tb + (16 * q) * LDF + 16 * pb, t, lane);
+        for (int e = 0; e < 4; ++e) {
+          const float v = blk[lc * LDF + 4 * lq + e];
+          const half_t h = static_cast<half_t>(v);
+          hi[e] = h;
+          lo[e] = static_cast<half_t>(v - static_cast<float>(h));
+        }
+      };
+      auto split = [](const cfloat4& v, h4_v& hi, h4_v& lo) {
 #pragma unroll
-        for (int r = 0; r < 4; ++r) Tb[(16 * pb + 4 * lq + r) * LDF + 16 * q + lc] = -t[r];
-      }
-      lds_barrier();
-    }
+        for (int e = 0; e < 4; ++e) {
+          const half_t h = static_cast<half_t>(v[e]);
+          hi[e] = h;
+          lo[e] = static_cast<half_t>(v[e] - static_cast<float>(h));
+        }
+      };
+      auto mma3 = [](const h4_v& ah, const h4_v& al, const h4_v& bh, const h4_v& bl, cfloat4 acc) {
+        acc = __builtin_amdgcn_mfma_f32_16x16x16f16(ah, bh, acc, 0, 0, 0);
+        acc = __builtin_amdgcn_mfma_f32_16x16x16f16(ah, bl, acc, 0, 0, 0);
+        return __builtin_amdgcn_mfma_f32_16x16x16f16(al, bh, acc, 0, 0, 0);
+      };
+      h4_v dh[4], dl[4];
+#pragma unroll
+      for (int pb = 0; pb < 4; ++pb) a_operand(Tb + (16 * pb) * LDF + 16 * pb, dh[pb], dl[pb]);
+      h4_v ah[6], al[6];  // A_pk for (p, k) = (1,0) (2,0) (2,1) (3,0) (3,1) (3,2)
+#pragma unroll
+      for (int pb = 1, n = 0; pb < 4; ++pb)
+#pragma unroll
+        for (int k = 0; k < pb; ++k, ++n) a_operand(Am + (16 * pb) * LDF + 16 * k, ah[n], al[n]);
 
-    // ---------------- T diag(beta gamma) and T diag(beta) as fp16 hi + lo, zero above the diagonal
-    for (int idx = tid; idx < CH * (CH / 4); idx += NT) {
-      const int i = idx >> 4;
-      const int l0 = 4 * (idx & 15);
-      float gh[4], gl[4], bh[4], bl[4];
+      // the W tile and (waves 0..3) the U tile run their block chains interleaved
+      const bool has_u = wave < 4;
+      const half_t* xw = Kt + (16 * wave + lc) * LD64;
+      const half_t* xu = Vt + (16 * (wave & 3) + lc) * LD64;
+      h4_v wh[4], wl[4], uh[4], ul[4];
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int l = l0 + r;
-        const float v = l <= i ? Tb[i * LDF + l] : 0.f;
-        const float vb = v * s_beta[l];
-        const float vg = vb * s_gam[l];
-        gh[r] = static_cast<float>(static_cast<half_t>(vg));
-        gl[r] = vg - gh[r];
-        bh[r] = static_cast<float>(static_cast<half_t>(vb));
-        bl[r] = vb - bh[r];
+      for (int pb = 0; pb < 4; ++pb) {
+        const int i0 = 16 * pb + 4 * lq;
+        const h4_v xrw = *reinterpret_cast<const h4_v*>(xw + i0);
+        const h4_v xru = *reinterpret_cast<const h4_v*>(xu + i0);
+        cfloat4 accw = {0.f, 0.f, 0.f, 0.f};
+        cfloat4 accu = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int k = 0; k < pb; ++k) {
+          const int n = pb * (pb - 1) / 2 + k;
+          accw = mma3(ah[n], al[n], wh[k], wl[k], accw);
+          if (has_u) accu = mma3(ah[n], al[n], uh[k], ul[k], accu);
+        }
+        cfloat4 rw, ru;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          rw[e] = static_cast<float>(xrw[e]) * s_bg[i0 + e] - accw[e];
+          ru[e] = static_cast<float>(xru[e]) * s_beta[i0 + e] - accu[e];
+        }
+        h4_v rwh, rwl, ruh, rul;
+        split(rw, rwh, rwl);
+        split(ru, ruh, rul);
+        cfloat4 w = {0.f, 0.f, 0.f, 0.f};
+        cfloat4 u = {0.f, 0.f, 0.f, 0.f};
+        w = mma3(dh[pb], dl[pb], rwh, rwl, w);
+        if (has_u) u = mma3(dh[pb], dl[pb], ruh, rul, u);
+        split(w, wh[pb], wl[pb]);
+        split(u, uh[pb], ul[pb]);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) Wn[(i0 + e) * LD128 + 16 * wave + lc] = static_cast<half_t>(-w[e]);
+        if (has_u) {
+#pragma unroll
+          for (int e = 0; e < 4; ++e) Ub[(i0 + e) * LDF + 16 * wave + lc] = u[e];
+        }
       }
-      store4h(Tgh + i * LD64 + l0, gh[0], gh[1], gh[2], gh[3]);
-      store4h(Tgl + i * LD64 + l0, gl[0], gl[1], gl[2], gl[3]);
-      store4h(Tbh + i * LD64 + l0, bh[0], bh[1], bh[2], bh[3]);
-      store4h(Tbl + i * LD64 + l0, bl[0], bl[1], bl[2], bl[3]);
     }
     lds_barrier();
 
-    // ---------------- W^T = K^T (T diag(beta gamma))^T -> Wn[i][dk] = -W; U = T diag(beta) V (registers)
-    for (int tile = wave; tile < 32; tile += NW) {
-      const int td = tile >> 2;  // dk tile
-      const int ti = tile & 3;   // token tile
-      cfloat4 acc = {0.f, 0.f, 0.f, 0.f};
-      acc = mma<CH>(Kt + 16 * td * LD64, LD64, Tgh + 16 * ti * LD64, LD64, acc, lane);
-      acc = mma<CH>(Kt + 16 * td * LD64, LD64, Tgl + 16 * ti * LD64, LD64, acc, lane);
-      store4h(Wn + (16 * ti + lc) * LD128 + 16 * td + 4 * lq, -acc[0], -acc[1], -acc[2], -acc[3]);
-    }
     cfloat4 Dl[2];  // delta tiles (token tile, dv tile) = ((2*wave+s)>>2, (2*wave+s)&3)
 #pragma unroll
     for (int s = 0; s < 2; ++s) {
       const int dt = 2 * wave + s;
       const int ti = dt >> 2;
       const int tv = dt & 3;
-      cfloat4 acc = {0.f, 0.f, 0.f, 0.f};
-      acc = mma<CH>(Tbh + 16 * ti * LD64, LD64, Vt + 16 * tv * LD64, LD64, acc, lane);
-      acc = mma<CH>(Tbl + 16 * ti * LD64, LD64, Vt + 16 * tv * LD64, LD64, acc, lane);
-      Dl[s] = acc;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) Dl[s][r] = Ub[(16 * ti + 4 * lq + r) * LDF + 16 * tv + lc];
     }
-    lds_barrier();
 
     // ---------------- delta = U - W S0; keep delta^T and exp(G_C - G) delta^T in LDS
     const float gC = s_G[CH - 1];
