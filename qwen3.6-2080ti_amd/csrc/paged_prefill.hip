@@ -14,7 +14,10 @@
 // MFMA accumulator layout (lane: keys 4(l/16)+r, position l%16) is exactly the
 // B-operand layout of the PV product, so P stays in registers.  Online softmax
 // per position (column), fp32; P rounded to bf16 (the reference rounds probs
-// to the query dtype before PV, src/reference_ops.py:358).
+// to the query dtype before PV, src/reference_ops.py:358).  The row's block
+// table is read into LDS once; the next key tile is loaded into registers
+// while the current one is computed, and barriers order LDS only, so those
+// loads stay in flight across them.
 #include "qa_common.h"
 
 namespace qa {
@@ -23,12 +26,14 @@ namespace pfx {
 typedef __attribute__((__vector_size__(8 * sizeof(__bf16)))) __bf16 bf16x8_v;
 typedef short short4_v __attribute__((ext_vector_type(4)));
 typedef float floatx4_v __attribute__((ext_vector_type(4)));
+typedef unsigned int u32x4_v __attribute__((ext_vector_type(4)));
 
 constexpr int NW = 8;          // waves
 constexpr int NT = NW * 64;
 constexpr int POS = 16;        // new positions per workgroup
 constexpr int KT = 64;         // keys per tile
 constexpr int BS = 16;         // cache block size
+constexpr int MAXB = 4096;     // block-table entries of a row kept in LDS (65536 keys)
 
 struct Params {
   const bf16_t* q;
@@ -54,7 +59,19 @@ template <int D>
 struct Smem {
   static constexpr int kLdK = D + 8;                   // halfs per K row (16-byte padded)
   static constexpr int kVtUnits = (KT / 4) * (D + 16); // 8-byte units: [key quad][d] (+pad)
-  static constexpr int kBytes = KT * kLdK * 2 + kVtUnits * 8;
+  static constexpr int kBytes = KT * kLdK * 2 + kVtUnits * 8 + MAXB * 4;
+};
+
+// One key tile's K and V pieces in flight: thread c loads K pieces (key, 16-byte
+// chunk) c + j NT and the four rows of V item c (key quad, 8-dim chunk).
+template <int D>
+struct TileRegs {
+  static constexpr int KP = KT * (D / 8) / NT;  // K pieces per thread
+  static constexpr int VITEMS = KT / 4 * (D / 8);
+  static constexpr int VP = (VITEMS + NT - 1) / NT;  // V items per thread (the last may be partial)
+  u32x4_v k[KP];
+  u32x4_v v[VP][4];
+  bool kok[KP];
 };
 
 __device__ __forceinline__ int64_t rd_index(const void* base, int is64, int64_t i) {
@@ -63,14 +80,54 @@ __device__ __forceinline__ int64_t rd_index(const void* base, int is64, int64_t 
 
 __device__ __forceinline__ int vt_swz(int d) { return d ^ ((d >> 5) & 7); }
 
+// Physical block of logical block lb of row b (-1 if absent or outside the pool).
+__device__ __forceinline__ int64_t block_of(const Params& p, int b, int64_t lb, const int* s_phys, int64_t nlb) {
+  if (lb < nlb && lb < MAXB) return s_phys[lb];
+  if (lb >= p.max_blocks) return -1;
+  const int64_t e = rd_index(p.tables, p.table_i64, b * p.table_stride + lb);
+  return e >= 0 && e < p.num_blocks ? e : -1;
+}
+
+template <int D>
+__device__ __forceinline__ void load_tile(const Params& p, int b, int64_t key0, int64_t kv_len, const bf16_t* kb, const bf16_t* vb,
+                                          const int* s_phys, int64_t nlb, int tid, TileRegs<D>& r) {
+  constexpr int DC = D / 8;
+#pragma unroll
+  for (int j = 0; j < TileRegs<D>::KP; ++j) {
+    const int c = tid + j * NT;
+    const int key = c / DC;
+    const int dc = c - key * DC;
+    const int64_t t = key0 + key;
+    const int64_t phys = t < kv_len ? block_of(p, b, t / BS, s_phys, nlb) : -1;
+    r.kok[j] = phys >= 0;
+    r.k[j] = phys >= 0 ? *reinterpret_cast<const u32x4_v*>(kb + phys * p.sP + (t % BS) * p.sT + 8 * dc) : u32x4_v{0u, 0u, 0u, 0u};
+  }
+#pragma unroll
+  for (int j = 0; j < TileRegs<D>::VP; ++j) {
+    const int c = tid + j * NT;
+    const int kq = c / DC;
+    const int dc = c - kq * DC;
+    const int64_t t0 = key0 + 4 * kq;  // four keys of one 16-token block
+    const int64_t phys = c < TileRegs<D>::VITEMS && t0 < kv_len ? block_of(p, b, t0 / BS, s_phys, nlb) : -1;
+#pragma unroll
+    for (int rr = 0; rr < 4; ++rr) {
+      const int64_t t = t0 + rr;
+      r.v[j][rr] = phys >= 0 && t < kv_len ? *reinterpret_cast<const u32x4_v*>(vb + phys * p.sP + (t % BS) * p.sT + 8 * dc)
+                                           : u32x4_v{0u, 0u, 0u, 0u};
+    }
+  }
+}
+
 template <int D>
 __global__ __launch_bounds__(NT) void prefill_kernel(Params p) {
   constexpr int KCH = D / 32;  // k-chunks of S^T
   constexpr int MT = D / 16;   // output dim tiles
+  constexpr int DC = D / 8;
   extern __shared__ __align__(16) unsigned char smem[];
   __shared__ int kvalid[KT];  // key of the staged tile has a valid block
   bf16_t* Ksm = reinterpret_cast<bf16_t*>(smem);
   uint2* Vt = reinterpret_cast<uint2*>(smem + KT * Smem<D>::kLdK * 2);
+  int* s_phys = reinterpret_cast<int*>(smem + KT * Smem<D>::kLdK * 2 + Smem<D>::kVtUnits * 8);
 
   const int pt = blockIdx.x;
   const int bg = blockIdx.y;
@@ -92,6 +149,13 @@ __global__ __launch_bounds__(NT) void prefill_kernel(Params p) {
   const int64_t my_pos = prefix + n0 + col;  // absolute position of this lane's column
   const bool row_live = n0 + col < n_new;
 
+  // the row's block table, once (entries outside the pool become -1)
+  const int64_t nlb = min<int64_t>((kv_len + BS - 1) / BS, p.max_blocks);
+  for (int64_t lb = tid; lb < min<int64_t>(nlb, MAXB); lb += NT) {
+    const int64_t e = rd_index(p.tables, p.table_i64, b * p.table_stride + lb);
+    s_phys[lb] = e >= 0 && e < p.num_blocks ? static_cast<int>(e) : -1;
+  }
+
   // Q^T operand (B of S^T = K Q^T): lane holds position col, dims 32i + 8*quad + [0, 8)
   bf16x8_v qreg[KCH];
   {
@@ -112,59 +176,41 @@ __global__ __launch_bounds__(NT) void prefill_kernel(Params p) {
   const bf16_t* kb = p.kbase + static_cast<int64_t>(g) * p.sG;
   const bf16_t* vb = p.vbase + static_cast<int64_t>(g) * p.sG;
   const int64_t ntiles = (kv_len + KT - 1) / KT;
+  lds_barrier();  // s_phys
+  TileRegs<D> nx;
+  load_tile<D>(p, b, 0, kv_len, kb, vb, s_phys, nlb, tid, nx);
   for (int64_t kt = 0; kt < ntiles; ++kt) {
     const int64_t key0 = kt * KT;
-    // ---- stage K [key][d] and V^T [key quad][d] of this tile
-    {
-      // K: 64 keys x D/8 chunks of 16 bytes
-      constexpr int KCHUNKS = KT * (D / 8);
-      for (int c = tid; c < KCHUNKS; c += NT) {
-        const int key = c / (D / 8);
-        const int dc = c - key * (D / 8);
-        const int64_t t = key0 + key;
-        uint4 val = make_uint4(0, 0, 0, 0);
-        bool ok = false;
-        if (t < kv_len && t / BS < p.max_blocks) {
-          const int64_t phys = rd_index(p.tables, p.table_i64, b * p.table_stride + t / BS);
-          ok = phys >= 0 && phys < p.num_blocks;
-          if (ok) val = *reinterpret_cast<const uint4*>(kb + phys * p.sP + (t % BS) * p.sT + 8 * dc);
-        }
-        *reinterpret_cast<uint4*>(Ksm + key * Smem<D>::kLdK + 8 * dc) = val;
-        if (dc == 0) kvalid[key] = ok;
-      }
-      // V: (key quad, 8-dim chunk) items; 4 rows loaded, packed into 4-key columns
-      constexpr int VITEMS = (KT / 4) * (D / 8);
-      for (int c = tid; c < VITEMS; c += NT) {
-        const int kq = c / (D / 8);
-        const int dc = c - kq * (D / 8);
-        uint4 r4[4];
+    // ---- stage K [key][d] and V^T [key quad][d] of this tile from the registers
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const int64_t t = key0 + 4 * kq + r;
-          r4[r] = make_uint4(0, 0, 0, 0);
-          if (t < kv_len && t / BS < p.max_blocks) {
-            const int64_t phys = rd_index(p.tables, p.table_i64, b * p.table_stride + t / BS);
-            if (phys >= 0 && phys < p.num_blocks) r4[r] = *reinterpret_cast<const uint4*>(vb + phys * p.sP + (t % BS) * p.sT + 8 * dc);
-          }
-        }
-        const uint32_t* r0 = reinterpret_cast<const uint32_t*>(&r4[0]);
-        const uint32_t* r1 = reinterpret_cast<const uint32_t*>(&r4[1]);
-        const uint32_t* r2 = reinterpret_cast<const uint32_t*>(&r4[2]);
-        const uint32_t* r3 = reinterpret_cast<const uint32_t*>(&r4[3]);
+    for (int j = 0; j < TileRegs<D>::KP; ++j) {
+      const int c = tid + j * NT;
+      const int key = c / DC;
+      const int dc = c - key * DC;
+      *reinterpret_cast<u32x4_v*>(Ksm + key * Smem<D>::kLdK + 8 * dc) = nx.k[j];
+      if (dc == 0) kvalid[key] = nx.kok[j];
+    }
 #pragma unroll
-        for (int k = 0; k < 4; ++k) {
-          const int d = 8 * dc + 2 * k;
-          uint2 lo, hi;
-          lo.x = __builtin_amdgcn_perm(r1[k], r0[k], 0x05040100u);
-          lo.y = __builtin_amdgcn_perm(r3[k], r2[k], 0x05040100u);
-          hi.x = __builtin_amdgcn_perm(r1[k], r0[k], 0x07060302u);
-          hi.y = __builtin_amdgcn_perm(r3[k], r2[k], 0x07060302u);
-          Vt[kq * (D + 16) + vt_swz(d)] = lo;
-          Vt[kq * (D + 16) + vt_swz(d + 1)] = hi;
-        }
+    for (int j = 0; j < TileRegs<D>::VP; ++j) {
+      const int c = tid + j * NT;
+      if (c >= TileRegs<D>::VITEMS) continue;
+      const int kq = c / DC;
+      const int dc = c - kq * DC;
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        const int d = 8 * dc + 2 * k;
+        uint2 lo, hi;
+        lo.x = __builtin_amdgcn_perm(nx.v[j][1][k], nx.v[j][0][k], 0x05040100u);
+        lo.y = __builtin_amdgcn_perm(nx.v[j][3][k], nx.v[j][2][k], 0x05040100u);
+        hi.x = __builtin_amdgcn_perm(nx.v[j][1][k], nx.v[j][0][k], 0x07060302u);
+        hi.y = __builtin_amdgcn_perm(nx.v[j][3][k], nx.v[j][2][k], 0x07060302u);
+        Vt[kq * (D + 16) + vt_swz(d)] = lo;
+        Vt[kq * (D + 16) + vt_swz(d + 1)] = hi;
       }
     }
-    __syncthreads();
+    lds_barrier();
+    // next tile's loads go out now and land during this tile's products
+    if (kt + 1 < ntiles) load_tile<D>(p, b, key0 + KT, kv_len, kb, vb, s_phys, nlb, tid, nx);
 
     if (active) {
       // ---- S^T = K Q^T for the 4 key sub-tiles; mask; online softmax per position
@@ -204,17 +250,25 @@ __global__ __launch_bounds__(NT) void prefill_kernel(Params p) {
       l_part = l_part * alpha + psum;
 #pragma unroll
       for (int t = 0; t < MT; ++t) o[t] *= alpha;
-      // ---- O^T += V^T P over the 4 key sub-tiles
+      // ---- O^T += V^T P, 32 keys per v_mfma_f32_16x16x32_bf16: the reduction index
+      // k = 8 (l/16) + e of lane l stands for key 4 (l/16) + e of sub-tile 2j (e < 4)
+      // and of sub-tile 2j + 1 (e >= 4), so the B operand is the lane's own P of the
+      // two sub-tiles and the A operand two 4-key units of V^T
 #pragma unroll
-      for (int st = 0; st < KT / 16; ++st) {
+      for (int jj = 0; jj < KT / 32; ++jj) {
+        short4_v p0 = pb[2 * jj], p1 = pb[2 * jj + 1];
+        const bf16x8_v bop = __builtin_bit_cast(bf16x8_v, __builtin_shufflevector(p0, p1, 0, 1, 2, 3, 4, 5, 6, 7));
 #pragma unroll
         for (int t = 0; t < MT; ++t) {
-          const uint2 a = Vt[(4 * st + quad) * (D + 16) + vt_swz(16 * t + col)];
-          o[t] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(__builtin_bit_cast(short4_v, a), pb[st], o[t], 0, 0, 0);
+          const uint2 a0 = Vt[(8 * jj + quad) * (D + 16) + vt_swz(16 * t + col)];
+          const uint2 a1 = Vt[(8 * jj + 4 + quad) * (D + 16) + vt_swz(16 * t + col)];
+          const uint4 av = make_uint4(a0.x, a0.y, a1.x, a1.y);
+          o[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_v, av), bop, o[t], 0, 0, 0);
+          if ((t & 3) == 3) __builtin_amdgcn_sched_barrier(0);  // bound the operand loads in flight
         }
       }
     }
-    __syncthreads();
+    lds_barrier();
   }
 
   if (!active) return;
