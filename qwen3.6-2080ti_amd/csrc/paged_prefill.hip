@@ -63,7 +63,8 @@ struct Smem {
 };
 
 // One key tile's K and V pieces in flight: thread c loads K pieces (key, 16-byte
-// chunk) c + j NT and the four rows of V item c (key quad, 8-dim chunk).
+// chunk) c + j NT and the four rows of V item c (key quad, 8-dim chunk), plus the
+// physical blocks of the tile's four 16-key blocks (wave-uniform; -1 = absent).
 template <int D>
 struct TileRegs {
   static constexpr int KP = KT * (D / 8) / NT;  // K pieces per thread
@@ -71,8 +72,9 @@ struct TileRegs {
   static constexpr int VP = (VITEMS + NT - 1) / NT;  // V items per thread (the last may be partial)
   u32x4_v k[KP];
   u32x4_v v[VP][4];
-  bool kok[KP];
+  int4 phys;  // blocks of keys [0,16) [16,32) [32,48) [48,64) of the tile
 };
+static_assert(KT == 4 * BS, "a key tile spans four cache blocks");
 
 __device__ __forceinline__ int64_t rd_index(const void* base, int is64, int64_t i) {
   return is64 ? reinterpret_cast<const int64_t*>(base)[i] : reinterpret_cast<const int32_t*>(base)[i];
@@ -88,33 +90,64 @@ __device__ __forceinline__ int64_t block_of(const Params& p, int b, int64_t lb, 
   return e >= 0 && e < p.num_blocks ? e : -1;
 }
 
+// Per-thread element offsets inside a block: the key and chunk of each K piece
+// and V row are fixed by the thread index, only the block changes per tile.
 template <int D>
-__device__ __forceinline__ void load_tile(const Params& p, int b, int64_t key0, int64_t kv_len, const bf16_t* kb, const bf16_t* vb,
-                                          const int* s_phys, int64_t nlb, int tid, TileRegs<D>& r) {
+struct TileLanes {
+  int kblk[TileRegs<D>::KP];   // which of the tile's blocks each K piece lies in
+  int koff[TileRegs<D>::KP];   // element offset inside that block
+  int kkey[TileRegs<D>::KP];   // key index inside the tile
+  int vblk[TileRegs<D>::VP];
+  int voff[TileRegs<D>::VP];   // offset of row 0; rows r add r * sT
+  int vkey[TileRegs<D>::VP];   // first key of the quad (KT when the item does not exist)
+};
+
+template <int D>
+__device__ __forceinline__ TileLanes<D> tile_lanes(const Params& p, int tid) {
   constexpr int DC = D / 8;
+  TileLanes<D> ln;
 #pragma unroll
   for (int j = 0; j < TileRegs<D>::KP; ++j) {
     const int c = tid + j * NT;
     const int key = c / DC;
-    const int dc = c - key * DC;
-    const int64_t t = key0 + key;
-    const int64_t phys = t < kv_len ? block_of(p, b, t / BS, s_phys, nlb) : -1;
-    r.kok[j] = phys >= 0;
-    r.k[j] = phys >= 0 ? *reinterpret_cast<const u32x4_v*>(kb + phys * p.sP + (t % BS) * p.sT + 8 * dc) : u32x4_v{0u, 0u, 0u, 0u};
+    ln.kkey[j] = key;
+    ln.kblk[j] = key / BS;
+    ln.koff[j] = static_cast<int>((key % BS) * p.sT) + 8 * (c % DC);
   }
 #pragma unroll
   for (int j = 0; j < TileRegs<D>::VP; ++j) {
     const int c = tid + j * NT;
     const int kq = c / DC;
-    const int dc = c - kq * DC;
-    const int64_t t0 = key0 + 4 * kq;  // four keys of one 16-token block
-    const int64_t phys = c < TileRegs<D>::VITEMS && t0 < kv_len ? block_of(p, b, t0 / BS, s_phys, nlb) : -1;
+    ln.vkey[j] = c < TileRegs<D>::VITEMS ? 4 * kq : KT;
+    ln.vblk[j] = (4 * kq) / BS;
+    ln.voff[j] = static_cast<int>(((4 * kq) % BS) * p.sT) + 8 * (c % DC);
+  }
+  return ln;
+}
+
+__device__ __forceinline__ int pick(const int4& v, int i) { return i == 0 ? v.x : i == 1 ? v.y : i == 2 ? v.z : v.w; }
+
+template <int D>
+__device__ __forceinline__ void load_tile(const Params& p, int b, int64_t key0, int64_t kv_len, const bf16_t* kb, const bf16_t* vb,
+                                          const int* s_phys, int64_t nlb, const TileLanes<D>& ln, TileRegs<D>& r) {
+  auto blk = [&](int q) {
+    const int64_t t = key0 + BS * q;
+    return __builtin_amdgcn_readfirstlane(t < kv_len ? static_cast<int>(block_of(p, b, t / BS, s_phys, nlb)) : -1);
+  };
+  r.phys = make_int4(blk(0), blk(1), blk(2), blk(3));
 #pragma unroll
-    for (int rr = 0; rr < 4; ++rr) {
-      const int64_t t = t0 + rr;
-      r.v[j][rr] = phys >= 0 && t < kv_len ? *reinterpret_cast<const u32x4_v*>(vb + phys * p.sP + (t % BS) * p.sT + 8 * dc)
-                                           : u32x4_v{0u, 0u, 0u, 0u};
-    }
+  for (int j = 0; j < TileRegs<D>::KP; ++j) {
+    const int phys = pick(r.phys, ln.kblk[j]);
+    r.k[j] = phys >= 0 && key0 + ln.kkey[j] < kv_len ? *reinterpret_cast<const u32x4_v*>(kb + static_cast<int64_t>(phys) * p.sP + ln.koff[j])
+                                                    : u32x4_v{0u, 0u, 0u, 0u};
+  }
+#pragma unroll
+  for (int j = 0; j < TileRegs<D>::VP; ++j) {
+    const int phys = ln.vkey[j] < KT ? pick(r.phys, ln.vblk[j]) : -1;
+    const bf16_t* base = vb + static_cast<int64_t>(phys < 0 ? 0 : phys) * p.sP + ln.voff[j];
+#pragma unroll
+    for (int rr = 0; rr < 4; ++rr)
+      r.v[j][rr] = phys >= 0 && key0 + ln.vkey[j] + rr < kv_len ? *reinterpret_cast<const u32x4_v*>(base + rr * p.sT) : u32x4_v{0u, 0u, 0u, 0u};
   }
 }
 
@@ -124,7 +157,6 @@ __global__ __launch_bounds__(NT) void prefill_kernel(Params p) {
   constexpr int MT = D / 16;   // output dim tiles
   constexpr int DC = D / 8;
   extern __shared__ __align__(16) unsigned char smem[];
-  __shared__ int kvalid[KT];  // key of the staged tile has a valid block
   bf16_t* Ksm = reinterpret_cast<bf16_t*>(smem);
   uint2* Vt = reinterpret_cast<uint2*>(smem + KT * Smem<D>::kLdK * 2);
   int* s_phys = reinterpret_cast<int*>(smem + KT * Smem<D>::kLdK * 2 + Smem<D>::kVtUnits * 8);
@@ -177,8 +209,9 @@ __global__ __launch_bounds__(NT) void prefill_kernel(Params p) {
   const bf16_t* vb = p.vbase + static_cast<int64_t>(g) * p.sG;
   const int64_t ntiles = (kv_len + KT - 1) / KT;
   lds_barrier();  // s_phys
+  const TileLanes<D> ln = tile_lanes<D>(p, tid);
   TileRegs<D> nx;
-  load_tile<D>(p, b, 0, kv_len, kb, vb, s_phys, nlb, tid, nx);
+  load_tile<D>(p, b, 0, kv_len, kb, vb, s_phys, nlb, ln, nx);
   for (int64_t kt = 0; kt < ntiles; ++kt) {
     const int64_t key0 = kt * KT;
     // ---- stage K [key][d] and V^T [key quad][d] of this tile from the registers
@@ -188,7 +221,6 @@ __global__ __launch_bounds__(NT) void prefill_kernel(Params p) {
       const int key = c / DC;
       const int dc = c - key * DC;
       *reinterpret_cast<u32x4_v*>(Ksm + key * Smem<D>::kLdK + 8 * dc) = nx.k[j];
-      if (dc == 0) kvalid[key] = nx.kok[j];
     }
 #pragma unroll
     for (int j = 0; j < TileRegs<D>::VP; ++j) {
@@ -208,9 +240,10 @@ __global__ __launch_bounds__(NT) void prefill_kernel(Params p) {
         Vt[kq * (D + 16) + vt_swz(d + 1)] = hi;
       }
     }
+    const int4 cur_phys = nx.phys;
     lds_barrier();
     // next tile's loads go out now and land during this tile's products
-    if (kt + 1 < ntiles) load_tile<D>(p, b, key0 + KT, kv_len, kb, vb, s_phys, nlb, tid, nx);
+    if (kt + 1 < ntiles) load_tile<D>(p, b, key0 + KT, kv_len, kb, vb, s_phys, nlb, ln, nx);
 
     if (active) {
       // ---- S^T = K Q^T for the 4 key sub-tiles; mask; online softmax per position
@@ -226,7 +259,7 @@ __global__ __launch_bounds__(NT) void prefill_kernel(Params p) {
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
           const int64_t t = key0 + 16 * st + 4 * quad + r;
-          const float v = (row_live && t <= my_pos && t < kv_len && kvalid[16 * st + 4 * quad + r]) ? acc[r] * p.scale : -INFINITY;
+          const float v = (row_live && t <= my_pos && t < kv_len && pick(cur_phys, st) >= 0) ? acc[r] * p.scale : -INFINITY;
           s[st][r] = v;
           mx = fmaxf(mx, v);
         }
