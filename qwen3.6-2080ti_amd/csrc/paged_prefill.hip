@@ -281,8 +281,11 @@ __global__ __launch_bounds__(NT) void prefill_kernel(Params p) {
           pb[st][r] = static_cast<short>(f32_to_bf16(pr));
         }
       l_part = l_part * alpha + psum;
+      // the accumulators only need rescaling when some position's running max moved
+      if (__ballot(alpha != 1.f) != 0) {
 #pragma unroll
-      for (int t = 0; t < MT; ++t) o[t] *= alpha;
+        for (int t = 0; t < MT; ++t) o[t] *= alpha;
+      }
       // ---- O^T += V^T P, 32 keys per v_mfma_f32_16x16x32_bf16: the reduction index
       // k = 8 (l/16) + e of lane l stands for key 4 (l/16) + e of sub-tile 2j (e < 4)
       // and of sub-tile 2j + 1 (e >= 4), so the B operand is the lane's own P of the
