@@ -38,9 +38,9 @@ HBM_PEAK_GBS = 8000.0  # MI355X HBM3E, GB/s
 # profiles/paged_prefill_config3.md): FETCH_SIZE scaled by 2.0 and WRITE_SIZE by 1.0, the factors
 # a plain 1 GiB device copy reads back in the same runs. Counters need rocprofv3, so the figures
 # are the committed profile's, not measured live.
-TRAFFIC_DECODE = 1980739257
-TRAFFIC_DELTA = 1653273865
-TRAFFIC_PREFILL = 891196186  # average over the eight per-chunk launches
+TRAFFIC_DECODE = 1959162882
+TRAFFIC_DELTA = 2172775376
+TRAFFIC_PREFILL = 891747373  # average over the eight per-chunk launches
 MFMA_BF16_PEAK_TFLOPS = 2500.0  # MI355X dense bf16/fp16 MFMA, TFLOP/s
 
 
@@ -457,8 +457,8 @@ def main() -> int:
                        "value_heads": 32, "head_dim": 128, "chunk": 64, "conv_kernel": 4},
             "roofline": {"bound": "mfma", "achieved": round(tflops, 2), "peak": MFMA_BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
                          "frac": round(tflops / MFMA_BF16_PEAK_TFLOPS, 4), "traffic": TRAFFIC_DELTA, "algo_flop_per_launch": dw["flops"],
-                         "algo_bytes_per_launch": dw["algo_bytes"], "kernel": "qa::cgd::chunk_kernel (fp16 MFMA, fp32 accumulate)",
-                         "kernel_avg_us": round(dkern["chunk_gated_delta"]["avg_ms"] * 1e3, 2)},
+                         "algo_bytes_per_launch": dw["algo_bytes"], "kernel": "qa::cgd::chunk_kernel (fp16 MFMA, fp32 accumulate); the step adds prep_kernel and gate_kernel",
+                         "kernel_avg_us": round(dkern["chunk_gated_delta"]["avg_ms"] * 1e3, 2), "kernels": dkern},
         }
         del dw
         torch.cuda.empty_cache()
@@ -478,7 +478,7 @@ def main() -> int:
             "roofline": {"bound": "mfma", "achieved": round(ptf, 2), "peak": MFMA_BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
                          "frac": round(ptf / MFMA_BF16_PEAK_TFLOPS, 4), "traffic": TRAFFIC_PREFILL, "algo_flop_per_launch": pw["flops"],
                          "kernel": "qa::pfx::prefill_kernel<256>, one launch per 512-token query chunk (kv_append between)",
-                         "kernel_ms_per_step": round(pkern["paged_prefill"]["total_ms_per_step"], 4)},
+                         "kernel_ms_per_step": round(pkern["paged_prefill"]["total_ms_per_step"], 4), "kernels": pkern},
         }
         del pw
         torch.cuda.empty_cache()
