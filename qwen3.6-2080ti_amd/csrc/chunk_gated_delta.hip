@@ -6,12 +6,8 @@
 //     norm of q and k per (token, head), q also scaled by dk^-0.5
 //     (src/reference_ops.py:181-183, 240-258, 297-304).  Each (row, head,
 //     token run) is done once, by one wave walking its tokens with the conv
-//     window in registers, and written as fp16 to a workspace: q and k
-//     token-major, k and v also as per-chunk transposed tiles
-//     [channel][token] -- the token-contiguous operands of the products that
-//     reduce over tokens; those go through a per-wave LDS tile so every
-//     chunk's tile is written as one contiguous block.  It also writes the
-//     conv state.
+//     window in registers, and written token-major as fp16 to a workspace.
+//     It also writes the conv state.
 //  2. gate_kernel -- g = -exp(A_log) softplus(a + dt_bias), beta = sigmoid(b)
 //     (src/reference_ops.py:271-275) and G, the inclusive sum of g inside each
 //     chunk.
@@ -41,7 +37,8 @@
 // equals the B-operand layout, so every W_k feeds the next block from
 // registers.  The next chunk's tiles are loaded into registers while the
 // current one is computed; barriers order LDS only, so those loads stay in
-// flight across them.
+// flight across them.  Operands that reduce over tokens are read from the
+// token-major K and V tiles with ds_read_b64_tr_b16 (tr_operand below).
 #include "qa_common.h"
 
 namespace qa {
@@ -67,12 +64,12 @@ constexpr int LD128 = 136;  // padded leading dims (halfs) of 128- and 64-wide f
 constexpr int LD64 = 72;
 constexpr int LDF = 65;     // fp32 64x64 leading dim
 constexpr int RUN = 128;    // tokens one prep wave walks
-constexpr int PU = 8;       // tokens per prep step (one 16-byte transposed store per channel)
+constexpr int PU = 8;       // tokens per prep step
 
 // ---- workspace (fp16 tensors, padded to whole chunks; tokens >= T are zero)
 struct Workspace {
   int64_t tp, nch;
-  int64_t off_qn, off_kn, off_knt, off_vt, off_gb, bytes;
+  int64_t off_qn, off_kn, off_vn, off_gb, bytes;
 };
 
 inline int64_t align256(int64_t v) { return (v + 255) & ~int64_t{255}; }
@@ -81,20 +78,18 @@ inline Workspace workspace_layout(int64_t batch, int64_t seq, int64_t hk, int64_
   Workspace w{};
   w.nch = (seq + CH - 1) / CH;
   w.tp = w.nch * CH;
-  const int64_t qk = batch * w.tp * hk * DK * 2;  // qn, kn: (B, Tp, Hk, 128); knt: (B, Hk, nch, 128, 64)
+  const int64_t qk = batch * w.tp * hk * DK * 2;  // qn, kn: (B, Tp, Hk, 128)
   w.off_qn = 0;
   w.off_kn = align256(w.off_qn + qk);
-  w.off_knt = align256(w.off_kn + qk);
-  w.off_vt = align256(w.off_knt + qk);                            // vt: (B, Hv, nch, 128, 64)
-  w.off_gb = align256(w.off_vt + batch * w.tp * hv * DV * 2);     // gb: (B, Hv, Tp, 2) fp32 (G, beta)
+  w.off_vn = align256(w.off_kn + qk);                             // vn: (B, Tp, Hv, 128)
+  w.off_gb = align256(w.off_vn + batch * w.tp * hv * DV * 2);     // gb: (B, Hv, Tp, 2) fp32 (G, beta)
   w.bytes = align256(w.off_gb + batch * hv * w.tp * 2 * 4);
   return w;
 }
 
 // ---- LDS layout of chunk_kernel (bytes)
-constexpr int OFF_RA = 0;                          // Qs | Ks  -> later Wn | Ub (Qs, Ks are dead once D is built)
+constexpr int OFF_RA = 0;                          // Qs -> later Wn | Ub (Qs is dead once Aqk and Q S0 are built)
 constexpr int OFF_QS = OFF_RA;
-constexpr int OFF_KS = OFF_RA + CH * LD128 * 2;
 constexpr int OFF_WN = OFF_RA;                     // -W [tok][dk] fp16
 constexpr int OFF_UB = OFF_RA + CH * LD128 * 2;    // U [tok][dv] fp32
 constexpr int SZ_RA = 2 * CH * LD128 * 2;          // 34816
@@ -104,9 +99,9 @@ constexpr int OFF_TB = OFF_RB + CH * LDF * 4;
 constexpr int OFF_DT = OFF_RB;
 constexpr int OFF_DDT = OFF_DT + DVS * LD64 * 2;
 constexpr int SZ_RB = 2 * CH * LDF * 4;            // 33280
-constexpr int OFF_KT = OFF_RB + SZ_RB;             // Kt [dk][tok]
-constexpr int OFF_VT = OFF_KT + DK * LD64 * 2;     // Vt [dv][tok] (this workgroup's half)
-constexpr int OFF_ST = OFF_VT + DVS * LD64 * 2;    // St [dv][dk] (fp16 state)
+constexpr int OFF_KS = OFF_RB + SZ_RB;             // Ks [tok][dk]
+constexpr int OFF_VS = OFF_KS + CH * LD128 * 2;    // Vs [tok][dv] (this workgroup's half)
+constexpr int OFF_ST = OFF_VS + CH * LD64 * 2;     // St [dv][dk] (fp16 state)
 constexpr int OFF_AQK = OFF_ST + DVS * LD128 * 2;  // Aqk [i][l]
 constexpr int OFF_SC = OFF_AQK + CH * LD64 * 2;    // beta, G, gamma, beta*gamma per token
 constexpr int LDS_BYTES = OFF_SC + 4 * CH * 4;
@@ -123,8 +118,7 @@ struct PrepParams {
   float* conv_out;        // (B, C, 3) or null
   half_t* qn;
   half_t* kn;
-  half_t* knt;
-  half_t* vt;
+  half_t* vn;
   int64_t T, tp, nch;
   int B, Hk, Hv, C;
 };
@@ -144,8 +138,7 @@ struct GateParams {
 struct ChunkParams {
   const half_t* qn;
   const half_t* kn;
-  const half_t* knt;
-  const half_t* vt;
+  const half_t* vn;
   const float* gb;
   const float* state_in;  // (B, Hv, dk, dv) or null
   float* state_out;       // (B, Hv, dk, dv) or null
@@ -178,13 +171,8 @@ __device__ __forceinline__ void store4h(half_t* dst, float a, float b, float c, 
 // Wave = (row b, head, run of RUN tokens); lane l holds channels 2l, 2l+1 of
 // the head (one bf16 pair per token, so a wave reads 256 contiguous bytes per
 // token).  Heads are numbered in channel order: q heads, k heads, v heads.
-constexpr int PREP_FLUSH = 32;  // tokens staged per channel row before they are written out
-constexpr int PREP_LD = PREP_FLUSH + 8;  // halfs per channel row of a wave's staging tile (16-byte aligned rows)
-
 __global__ __launch_bounds__(256) void prep_kernel(PrepParams p) {
-  __shared__ __align__(16) half_t stage_all[4][128 * PREP_LD];
   const int lane = threadIdx.x & 63;
-  half_t* stage = stage_all[__builtin_amdgcn_readfirstlane(threadIdx.x >> 6)];
   const int NH = 2 * p.Hk + p.Hv;
   const int64_t nruns = (p.tp + RUN - 1) / RUN;
   // the work item is wave-uniform, so its address arithmetic runs on the scalar unit
@@ -265,41 +253,17 @@ __global__ __launch_bounds__(256) void prep_kernel(PrepParams p) {
         y0[jj] *= r;
         y1[jj] *= r;
       }
-      half_t* dst = (kind == 0 ? p.qn : p.kn) + ((b * p.tp + t) * p.Hk + hk) * DK + 2 * lane;
-#pragma unroll
-      for (int jj = 0; jj < PU; ++jj) {
-        f16x2_v pr;
-        pr[0] = static_cast<half_t>(y0[jj]);
-        pr[1] = static_cast<half_t>(y1[jj]);
-        *reinterpret_cast<f16x2_v*>(dst + static_cast<int64_t>(jj) * p.Hk * DK) = pr;
-      }
     }
-    if (kind > 0) {
-      // transposed tile [channel][token] of this chunk, staged in this wave's LDS
-      // tile (8 tokens = 16 bytes per channel row per step) and written out as one
-      // contiguous 16 KB block once the chunk's 64 tokens are in
-      f16x8_v c0, c1;
+    half_t* dst = kind == 0 ? p.qn + ((b * p.tp + t) * p.Hk + hk) * DK
+                : kind == 1 ? p.kn + ((b * p.tp + t) * p.Hk + hk) * DK
+                            : p.vn + ((b * p.tp + t) * p.Hv + hv) * DV;
+    const int64_t tstride = static_cast<int64_t>(kind == 2 ? p.Hv : p.Hk) * DK;
 #pragma unroll
-      for (int jj = 0; jj < PU; ++jj) {
-        c0[jj] = static_cast<half_t>(y0[jj]);
-        c1[jj] = static_cast<half_t>(y1[jj]);
-      }
-      const int tc = static_cast<int>(t % PREP_FLUSH);
-      *reinterpret_cast<f16x8_v*>(stage + (2 * lane) * PREP_LD + tc) = c0;
-      *reinterpret_cast<f16x8_v*>(stage + (2 * lane + 1) * PREP_LD + tc) = c1;
-      if (tc == PREP_FLUSH - PU) {
-        const int64_t c = t / CH;
-        const int tbase = static_cast<int>((t - tc) % CH);
-        half_t* tile = kind == 1 ? p.knt + ((b * p.Hk + hk) * p.nch + c) * (DK * CH) : p.vt + ((b * p.Hv + hv) * p.nch + c) * (DV * CH);
-        constexpr int PPR = PREP_FLUSH / 8;  // 16-byte pieces per channel row
-#pragma unroll
-        for (int r = 0; r < 128 * PPR / 64; ++r) {
-          const int pc = lane + 64 * r;
-          const int row = pc / PPR;
-          const int col = pc % PPR;
-          *reinterpret_cast<f16x8_v*>(tile + row * CH + tbase + 8 * col) = *reinterpret_cast<const f16x8_v*>(stage + row * PREP_LD + 8 * col);
-        }
-      }
+    for (int jj = 0; jj < PU; ++jj) {
+      f16x2_v pr;
+      pr[0] = static_cast<half_t>(y0[jj]);
+      pr[1] = static_cast<half_t>(y1[jj]);
+      *reinterpret_cast<f16x2_v*>(dst + jj * tstride + 2 * lane) = pr;
     }
   }
 
@@ -379,12 +343,25 @@ __device__ __forceinline__ cfloat4 mma_f32_16(const float* A, const float* B, cf
   return acc;
 }
 
+// Four fp16 of a column of a row-major LDS tile X, for each lane, by
+// ds_read_b64_tr_b16: lane i of 16-lane group g reads the 8 bytes at
+// X[row_g + i / 4][c0 + 4 (i % 4)], and the instruction returns to lane j of
+// the group the elements X[row_g + e][c0 + j], e = 0..3.  With row_g = r0 + 4g
+// this is the 16x16x16 B operand of the tile X[r0.., c0..] (k = row); two
+// reads at row_g = k0 + 8g and k0 + 8g + 4 give the 16x16x32 A operand of its
+// transpose.
+__device__ __forceinline__ h4_v tr_read(const half_t* tile, int ld, int row_g, int c0, int lane) {
+  typedef short s4_v __attribute__((ext_vector_type(4)));
+  typedef __attribute__((address_space(3))) s4_v lds_s4;
+  const int i = lane & 15;
+  return __builtin_bit_cast(h4_v, __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s4*)(tile + (row_g + (i >> 2)) * ld + c0 + 4 * (i & 3))));
+}
+
 // One chunk's inputs, staged in registers while the previous chunk is computed:
-// 16-byte pieces of q and k rows, of the transposed k tile, of this
-// workgroup's half of the transposed v tile, and of (G, beta) (used by
-// threads < 32).
+// 16-byte pieces of q and k rows, of this workgroup's half of the v rows, and
+// of (G, beta) (used by threads < 32).
 struct ChunkRegs {
-  u32x4 q0, q1, k0, k1, kt0, kt1, v;
+  u32x4 q0, q1, k0, k1, v;
   cfloat4 gb;
 };
 
@@ -394,14 +371,12 @@ __device__ __forceinline__ ChunkRegs load_chunk(const ChunkParams& p, int64_t b,
   // 1024 pieces of 16 bytes per q/k tile: thread tid takes pieces tid and tid + 512
   const int64_t row_off = ((b * p.tp + t0 + (tid >> 4)) * p.Hk + qh) * DK + 8 * (tid & 15);
   const int64_t row_off2 = row_off + static_cast<int64_t>(NT >> 4) * p.Hk * DK;
-  const half_t* kt = p.knt + ((b * p.Hk + qh) * p.nch + ci) * (DK * CH) + 8 * tid;
   r.q0 = *reinterpret_cast<const u32x4*>(p.qn + row_off);
   r.q1 = *reinterpret_cast<const u32x4*>(p.qn + row_off2);
   r.k0 = *reinterpret_cast<const u32x4*>(p.kn + row_off);
   r.k1 = *reinterpret_cast<const u32x4*>(p.kn + row_off2);
-  r.kt0 = *reinterpret_cast<const u32x4*>(kt);
-  r.kt1 = *reinterpret_cast<const u32x4*>(kt + 8 * NT);
-  r.v = *reinterpret_cast<const u32x4*>(p.vt + ((b * p.Hv + j) * p.nch + ci) * (DV * CH) + half_id * DVS * CH + 8 * tid);
+  // 512 pieces per v half tile: token tid / 8, columns 8 (tid % 8) of this half
+  r.v = *reinterpret_cast<const u32x4*>(p.vn + ((b * p.tp + t0 + (tid >> 3)) * p.Hv + j) * DV + half_id * DVS + 8 * (tid & 7));
   r.gb = *reinterpret_cast<const cfloat4*>(p.gb + ((b * p.Hv + j) * p.tp + t0) * 2 + 4 * (tid & (CH / 2 - 1)));
   return r;
 }
@@ -416,8 +391,7 @@ __global__ __launch_bounds__(NT) void chunk_kernel(ChunkParams p) {
   float* Ub = reinterpret_cast<float*>(smem + OFF_UB);
   half_t* Dt = reinterpret_cast<half_t*>(smem + OFF_DT);
   half_t* DDt = reinterpret_cast<half_t*>(smem + OFF_DDT);
-  half_t* Kt = reinterpret_cast<half_t*>(smem + OFF_KT);
-  half_t* Vt = reinterpret_cast<half_t*>(smem + OFF_VT);
+  half_t* Vs = reinterpret_cast<half_t*>(smem + OFF_VS);
   half_t* St = reinterpret_cast<half_t*>(smem + OFF_ST);
   half_t* Aqk = reinterpret_cast<half_t*>(smem + OFF_AQK);
   float* s_beta = reinterpret_cast<float*>(smem + OFF_SC);
@@ -460,9 +434,7 @@ __global__ __launch_bounds__(NT) void chunk_kernel(ChunkParams p) {
       *reinterpret_cast<u32x4*>(Qs + (c1 >> 4) * LD128 + 8 * (c1 & 15)) = nx.q1;
       *reinterpret_cast<u32x4*>(Ks + (c0 >> 4) * LD128 + 8 * (c0 & 15)) = nx.k0;
       *reinterpret_cast<u32x4*>(Ks + (c1 >> 4) * LD128 + 8 * (c1 & 15)) = nx.k1;
-      *reinterpret_cast<u32x4*>(Kt + (c0 >> 3) * LD64 + 8 * (c0 & 7)) = nx.kt0;
-      *reinterpret_cast<u32x4*>(Kt + (c1 >> 3) * LD64 + 8 * (c1 & 7)) = nx.kt1;
-      *reinterpret_cast<u32x4*>(Vt + (tid >> 3) * LD64 + 8 * (tid & 7)) = nx.v;
+      *reinterpret_cast<u32x4*>(Vs + (tid >> 3) * LD64 + 8 * (tid & 7)) = nx.v;
     }
     if (tid < CH / 2) {
       s_G[2 * tid] = nx.gb.x;
@@ -585,14 +557,12 @@ __global__ __launch_bounds__(NT) void chunk_kernel(ChunkParams p) {
 
       // the W tile and (waves 0..3) the U tile run their block chains interleaved
       const bool has_u = wave < 4;
-      const half_t* xw = Kt + (16 * wave + lc) * LD64;
-      const half_t* xu = Vt + (16 * (wave & 3) + lc) * LD64;
       h4_v wh[4], wl[4], uh[4], ul[4];
 #pragma unroll
       for (int pb = 0; pb < 4; ++pb) {
         const int i0 = 16 * pb + 4 * lq;
-        const h4_v xrw = *reinterpret_cast<const h4_v*>(xw + i0);
-        const h4_v xru = *reinterpret_cast<const h4_v*>(xu + i0);
+        const h4_v xrw = tr_read(Ks, LD128, i0, 16 * wave, lane);
+        const h4_v xru = tr_read(Vs, LD64, i0, 16 * (wave & 3), lane);
         cfloat4 accw = {0.f, 0.f, 0.f, 0.f};
         cfloat4 accu = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
@@ -677,10 +647,21 @@ __global__ __launch_bounds__(NT) void chunk_kernel(ChunkParams p) {
       }
     }
     const float gamC = s_gam[CH - 1];
+    f16x8_v kt[CH / 32];  // K^T rows 16 wave.. (dk) as A operand, k = token
+#pragma unroll
+    for (int k0 = 0; k0 < CH; k0 += 32)
+      kt[k0 / 32] = __builtin_bit_cast(f16x8_v, __builtin_shufflevector(tr_read(Ks, LD128, k0 + 8 * lq, 16 * wave, lane),
+                                                                         tr_read(Ks, LD128, k0 + 8 * lq + 4, 16 * wave, lane),
+                                                                         0, 1, 2, 3, 4, 5, 6, 7));
 #pragma unroll
     for (int tv = 0; tv < 4; ++tv) {
       cfloat4 acc = S[tv] * gamC;
-      S[tv] = mma<CH>(Kt + 16 * wave * LD64, LD64, DDt + 16 * tv * LD64, LD64, acc, lane);
+#pragma unroll
+      for (int k0 = 0; k0 < CH; k0 += 32) {
+        const f16x8_v bv = *reinterpret_cast<const f16x8_v*>(DDt + (16 * tv + lc) * LD64 + k0 + 8 * lq);
+        acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(kt[k0 / 32], bv, acc, 0, 0, 0);
+      }
+      S[tv] = acc;
       store4h(St + (16 * tv + lc) * LD128 + 16 * wave + 4 * lq, S[tv][0], S[tv][1], S[tv][2], S[tv][3]);
     }
     lds_barrier();
@@ -744,8 +725,7 @@ extern "C" int qa_chunk_gated_delta_rule(const void* mixed_qkv, int32_t x_dtype,
   pp.conv_out = conv_state_out;
   pp.qn = reinterpret_cast<half_t*>(wsb + ws.off_qn);
   pp.kn = reinterpret_cast<half_t*>(wsb + ws.off_kn);
-  pp.knt = reinterpret_cast<half_t*>(wsb + ws.off_knt);
-  pp.vt = reinterpret_cast<half_t*>(wsb + ws.off_vt);
+  pp.vn = reinterpret_cast<half_t*>(wsb + ws.off_vn);
   pp.T = seq;
   pp.tp = ws.tp;
   pp.nch = ws.nch;
@@ -784,8 +764,7 @@ extern "C" int qa_chunk_gated_delta_rule(const void* mixed_qkv, int32_t x_dtype,
   ChunkParams p{};
   p.qn = pp.qn;
   p.kn = pp.kn;
-  p.knt = pp.knt;
-  p.vt = pp.vt;
+  p.vn = pp.vn;
   p.gb = gp.gb;
   p.state_in = initial_state;
   p.state_out = final_state;
