@@ -88,17 +88,19 @@ inline Workspace workspace_layout(int64_t batch, int64_t seq, int64_t hk, int64_
 }
 
 // ---- LDS layout of chunk_kernel (bytes)
-constexpr int OFF_RA = 0;                          // Qs -> later Wn | Ub (Qs is dead once Aqk and Q S0 are built)
+constexpr int LDB = 20;                            // row stride (floats) of the 16x16 fp32 diagonal blocks
+constexpr int OFF_RA = 0;                          // Qs -> later Wt | Ub (Qs is dead once Aqk and Q S0 are built)
 constexpr int OFF_QS = OFF_RA;
-constexpr int OFF_WN = OFF_RA;                     // -W [tok][dk] fp16
-constexpr int OFF_UB = OFF_RA + CH * LD128 * 2;    // U [tok][dv] fp32
-constexpr int SZ_RA = 2 * CH * LD128 * 2;          // 34816
-constexpr int OFF_RB = OFF_RA + SZ_RA;             // Am | Tb (fp32) -> later Dt | DDt (dead once W, U are built)
-constexpr int OFF_AM = OFF_RB;
-constexpr int OFF_TB = OFF_RB + CH * LDF * 4;
+constexpr int OFF_WT = OFF_RA;                     // -W^T [dk][tok] fp16
+constexpr int OFF_UB = OFF_RA + DK * LD64 * 2;     // U [tok][dv] fp32
+constexpr int SZ_RA = DK * LD64 * 2 + CH * LDF * 4;  // 35072
+constexpr int OFF_RB = OFF_RA + SZ_RA;             // Adg | Tb | Ahl -> later Dt | DDt (dead once W, U are built)
+constexpr int OFF_ADG = OFF_RB;                    // diagonal 16x16 blocks of A, fp32 [block][row][LDB]
+constexpr int OFF_TB = OFF_ADG + 4 * 16 * LDB * 4; // D_p = (I + A_pp)^-1, fp32 [block][row][LDB]
+constexpr int OFF_AHL = OFF_TB + 4 * 16 * LDB * 4; // 6 off-diagonal blocks of A as fp16 hi | lo, one 16-byte A operand per lane
 constexpr int OFF_DT = OFF_RB;
 constexpr int OFF_DDT = OFF_DT + DVS * LD64 * 2;
-constexpr int SZ_RB = 2 * CH * LDF * 4;            // 33280
+constexpr int SZ_RB = 2 * DVS * LD64 * 2;          // 18432
 constexpr int OFF_KS = OFF_RB + SZ_RB;             // Ks [tok][dk]
 constexpr int OFF_VS = OFF_KS + CH * LD128 * 2;    // Vs [tok][dv] (this workgroup's half)
 constexpr int OFF_ST = OFF_VS + CH * LD64 * 2;     // St [dv][dk] (fp16 state)
@@ -106,8 +108,8 @@ constexpr int OFF_AQK = OFF_ST + DVS * LD128 * 2;  // Aqk [i][l]
 constexpr int OFF_SC = OFF_AQK + CH * LD64 * 2;    // beta, G, gamma, beta*gamma per token
 constexpr int LDS_BYTES = OFF_SC + 4 * CH * 4;
 
-static_assert(CH * LD128 * 2 + CH * LDF * 4 <= SZ_RA, "RA too small for Wn|Ub");
-static_assert(2 * DVS * LD64 * 2 <= SZ_RB, "RB too small for Dt|DDt");
+static_assert(CH * LD128 * 2 <= SZ_RA, "RA too small for Qs");
+static_assert(OFF_AHL + 6 * 64 * 16 <= OFF_RB + SZ_RB, "RB too small for Adg|Tb|Ahl");
 static_assert(LDS_BYTES <= 160 * 1024, "LDS budget");
 
 struct PrepParams {
@@ -332,17 +334,6 @@ __device__ __forceinline__ cfloat4 mma(const half_t* A, int lda, const half_t* B
   return acc;
 }
 
-// C(16x16) += A(16x16) * B(16x16), fp32 operands in LDS with leading dim LDF,
-// by v_mfma_f32_16x16x4_f32 (lane l: A[l%16][k0 + l/16], B[k0 + l/16][l%16]).
-// Lane l gets C[4(l/16) + r][l % 16].
-__device__ __forceinline__ cfloat4 mma_f32_16(const float* A, const float* B, cfloat4 acc, int lane) {
-  const int i = lane & 15;
-  const int kq = lane >> 4;
-#pragma unroll
-  for (int k0 = 0; k0 < 16; k0 += 4) acc = __builtin_amdgcn_mfma_f32_16x16x4f32(A[i * LDF + k0 + kq], B[(k0 + kq) * LDF + i], acc, 0, 0, 0);
-  return acc;
-}
-
 // Four fp16 of a column of a row-major LDS tile X, for each lane, by
 // ds_read_b64_tr_b16: lane i of 16-lane group g reads the 8 bytes at
 // X[row_g + i / 4][c0 + 4 (i % 4)], and the instruction returns to lane j of
@@ -355,6 +346,33 @@ __device__ __forceinline__ h4_v tr_read(const half_t* tile, int ld, int row_g, i
   typedef __attribute__((address_space(3))) s4_v lds_s4;
   const int i = lane & 15;
   return __builtin_bit_cast(h4_v, __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s4*)(tile + (row_g + (i >> 2)) * ld + c0 + 4 * (i & 3))));
+}
+
+// The 16x16x32 A operand of X^T for the row-major tile X: lane (g, j) gets
+// X[k0 + 8g + e][c0 + j], e = 0..7.
+__device__ __forceinline__ f16x8_v tr_operand32(const half_t* tile, int ld, int k0, int c0, int lane) {
+  const int g8 = 8 * (lane >> 4);
+  return __builtin_bit_cast(f16x8_v, __builtin_shufflevector(tr_read(tile, ld, k0 + g8, c0, lane), tr_read(tile, ld, k0 + g8 + 4, c0, lane),
+                                                             0, 1, 2, 3, 4, 5, 6, 7));
+}
+
+// v = hi + lo with hi = fp16(v) and lo = fp16(v - hi) (v - hi is exact in fp32).
+// lo comes from v_fma_mix{lo,hi}_f16, which take hi as an fp16 operand and
+// round the fp32 result once: 1.5 instructions per element instead of 3.5.
+__device__ __forceinline__ void split4(const cfloat4& v, h4_v& hi, h4_v& lo) {
+  typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
+#pragma unroll
+  for (int e = 0; e < 4; ++e) hi[e] = static_cast<half_t>(v[e]);
+  const u32x2 h = __builtin_bit_cast(u32x2, hi);
+  u32x2 l;
+#pragma unroll
+  for (int p = 0; p < 2; ++p) {
+    unsigned int r;
+    asm("v_fma_mixlo_f16 %0, -1.0, %1, %2 op_sel_hi:[0,1,0]" : "=v"(r) : "v"(h[p]), "v"(v[2 * p]));
+    asm("v_fma_mixhi_f16 %0, -1.0, %1, %2 op_sel:[0,1,0] op_sel_hi:[0,1,0]" : "+v"(r) : "v"(h[p]), "v"(v[2 * p + 1]));
+    l[p] = r;
+  }
+  lo = __builtin_bit_cast(h4_v, l);
 }
 
 // One chunk's inputs, staged in registers while the previous chunk is computed:
@@ -385,9 +403,10 @@ __global__ __launch_bounds__(NT) void chunk_kernel(ChunkParams p) {
   extern __shared__ __align__(16) unsigned char smem[];
   half_t* Qs = reinterpret_cast<half_t*>(smem + OFF_QS);
   half_t* Ks = reinterpret_cast<half_t*>(smem + OFF_KS);
-  float* Am = reinterpret_cast<float*>(smem + OFF_AM);
+  float* Adg = reinterpret_cast<float*>(smem + OFF_ADG);
   float* Tb = reinterpret_cast<float*>(smem + OFF_TB);
-  half_t* Wn = reinterpret_cast<half_t*>(smem + OFF_WN);
+  unsigned char* Ahl = smem + OFF_AHL;
+  half_t* Wt = reinterpret_cast<half_t*>(smem + OFF_WT);
   float* Ub = reinterpret_cast<float*>(smem + OFF_UB);
   half_t* Dt = reinterpret_cast<half_t*>(smem + OFF_DT);
   half_t* DDt = reinterpret_cast<half_t*>(smem + OFF_DDT);
@@ -452,18 +471,33 @@ __global__ __launch_bounds__(NT) void chunk_kernel(ChunkParams p) {
     nx = load_chunk(p, b, j, qh, half_id, min(ci + 1, p.nch - 1), tid);
     lds_barrier();
 
-    // ---------------- A = beta_i exp(G_i - G_l) K K^T (strictly lower), fp32
+    // ---------------- A = beta_i exp(G_i - G_l) K K^T (strictly lower).  The tile is
+    // computed as (K_l K_i^T), so lane (lq, lc) holds A[16 ti + lc][16 tl + 4 lq + r]: the
+    // A-operand layout of the 16x16x16 products that consume it.  Diagonal blocks are kept
+    // fp32 for the solve; off-diagonal blocks are split once into fp16 hi + lo here.
     for (int tile = wave; tile < 16; tile += NW) {
       const int ti = tile >> 2;
       const int tl = tile & 3;
       if (tl > ti) continue;
       cfloat4 acc = {0.f, 0.f, 0.f, 0.f};
-      acc = mma<DK>(Ks + 16 * ti * LD128, LD128, Ks + 16 * tl * LD128, LD128, acc, lane);
+      acc = mma<DK>(Ks + 16 * tl * LD128, LD128, Ks + 16 * ti * LD128, LD128, acc, lane);
+      const int i = 16 * ti + lc;
+      const float bi = s_beta[i];
+      const float gi = s_G[i];
+      cfloat4 a;
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        const int i = 16 * ti + 4 * lq + r;
-        const int l = 16 * tl + lc;
-        Am[i * LDF + l] = l < i ? s_beta[i] * __expf(s_G[i] - s_G[l]) * acc[r] : 0.f;
+        const int l = 16 * tl + 4 * lq + r;
+        a[r] = l < i ? bi * __expf(gi - s_G[l]) * acc[r] : 0.f;
+      }
+      if (ti == tl) {
+        *reinterpret_cast<cfloat4*>(Adg + (16 * ti + lc) * LDB + 4 * lq) = a;
+      } else {
+        h4_v hi, lo;
+        split4(a, hi, lo);
+        h4_v* dst = reinterpret_cast<h4_v*>(Ahl + (ti * (ti - 1) / 2 + tl) * 1024 + 16 * lane);
+        dst[0] = hi;
+        dst[1] = lo;
       }
     }
     lds_barrier();
@@ -474,16 +508,17 @@ __global__ __launch_bounds__(NT) void chunk_kernel(ChunkParams p) {
     if (wave == 0) {
       const int qb = lane >> 4;
       const int c = lane & 15;
-      const float* ab = Am + (16 * qb) * LDF + 16 * qb;
+      const float* ab = Adg + (16 * qb) * LDB;
       float x[16];
 #pragma unroll
-      for (int i = 0; i < 16; ++i) x[i] = i == c ? 1.f : 0.f;
+      for (int i = 0; i < 16; ++i) {
+        float v = i == c ? 1.f : 0.f;
 #pragma unroll
-      for (int l = 0; l < 16; ++l)
+        for (int l = 0; l < i; ++l) v -= ab[i * LDB + l] * x[l];
+        x[i] = v;
+      }
 #pragma unroll
-        for (int i = l + 1; i < 16; ++i) x[i] -= ab[i * LDF + l] * x[l];
-#pragma unroll
-      for (int i = 0; i < 16; ++i) Tb[(16 * qb + i) * LDF + 16 * qb + c] = x[i];
+      for (int i = 0; i < 16; ++i) Tb[(16 * qb + i) * LDB + c] = x[i];
     } else {
       // Aqk[i][l] = exp(G_i - G_l) (q_i . k_l), l <= i, computed as (K Q^T)[l][i]
       for (int tile = wave - 1; tile < 16; tile += NW - 1) {
@@ -523,37 +558,22 @@ __global__ __launch_bounds__(NT) void chunk_kernel(ChunkParams p) {
     // hi + lo A operands; R and W_p stay fp32 in registers and are split into
     // hi + lo B operands (the 16x16 accumulator layout is the B-operand layout).
     {
-      // A operand slices: lane l holds row l % 16, columns 4 (l / 16) + e of a 16x16 block
-      auto a_operand = [&](const float* blk, h4_v& hi, h4_v& lo) {
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const float v = blk[lc * LDF + 4 * lq + e];
-          const half_t h = static_cast<half_t>(v);
-          hi[e] = h;
-          lo[e] = static_cast<half_t>(v - static_cast<float>(h));
-        }
-      };
-      auto split = [](const cfloat4& v, h4_v& hi, h4_v& lo) {
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const half_t h = static_cast<half_t>(v[e]);
-          hi[e] = h;
-          lo[e] = static_cast<half_t>(v[e] - static_cast<float>(h));
-        }
-      };
       auto mma3 = [](const h4_v& ah, const h4_v& al, const h4_v& bh, const h4_v& bl, cfloat4 acc) {
         acc = __builtin_amdgcn_mfma_f32_16x16x16f16(ah, bh, acc, 0, 0, 0);
         acc = __builtin_amdgcn_mfma_f32_16x16x16f16(ah, bl, acc, 0, 0, 0);
         return __builtin_amdgcn_mfma_f32_16x16x16f16(al, bh, acc, 0, 0, 0);
       };
+      // A operands: lane l holds row l % 16, columns 4 (l / 16) + e of a 16x16 block
       h4_v dh[4], dl[4];
 #pragma unroll
-      for (int pb = 0; pb < 4; ++pb) a_operand(Tb + (16 * pb) * LDF + 16 * pb, dh[pb], dl[pb]);
+      for (int pb = 0; pb < 4; ++pb) split4(*reinterpret_cast<const cfloat4*>(Tb + (16 * pb + lc) * LDB + 4 * lq), dh[pb], dl[pb]);
       h4_v ah[6], al[6];  // A_pk for (p, k) = (1,0) (2,0) (2,1) (3,0) (3,1) (3,2)
 #pragma unroll
-      for (int pb = 1, n = 0; pb < 4; ++pb)
-#pragma unroll
-        for (int k = 0; k < pb; ++k, ++n) a_operand(Am + (16 * pb) * LDF + 16 * k, ah[n], al[n]);
+      for (int n = 0; n < 6; ++n) {
+        const h4_v* src = reinterpret_cast<const h4_v*>(Ahl + n * 1024 + 16 * lane);
+        ah[n] = src[0];
+        al[n] = src[1];
+      }
 
       // the W tile and (waves 0..3) the U tile run their block chains interleaved
       const bool has_u = wave < 4;
@@ -571,23 +591,25 @@ __global__ __launch_bounds__(NT) void chunk_kernel(ChunkParams p) {
           accw = mma3(ah[n], al[n], wh[k], wl[k], accw);
           if (has_u) accu = mma3(ah[n], al[n], uh[k], ul[k], accu);
         }
+        const cfloat4 bg = *reinterpret_cast<const cfloat4*>(s_bg + i0);
+        const cfloat4 bt = *reinterpret_cast<const cfloat4*>(s_beta + i0);
         cfloat4 rw, ru;
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-          rw[e] = static_cast<float>(xrw[e]) * s_bg[i0 + e] - accw[e];
-          ru[e] = static_cast<float>(xru[e]) * s_beta[i0 + e] - accu[e];
+          rw[e] = __builtin_fmaf(static_cast<float>(xrw[e]), bg[e], -accw[e]);
+          ru[e] = __builtin_fmaf(static_cast<float>(xru[e]), bt[e], -accu[e]);
         }
         h4_v rwh, rwl, ruh, rul;
-        split(rw, rwh, rwl);
-        split(ru, ruh, rul);
+        split4(rw, rwh, rwl);
+        split4(ru, ruh, rul);
         cfloat4 w = {0.f, 0.f, 0.f, 0.f};
         cfloat4 u = {0.f, 0.f, 0.f, 0.f};
         w = mma3(dh[pb], dl[pb], rwh, rwl, w);
         if (has_u) u = mma3(dh[pb], dl[pb], ruh, rul, u);
-        split(w, wh[pb], wl[pb]);
-        split(u, uh[pb], ul[pb]);
-#pragma unroll
-        for (int e = 0; e < 4; ++e) Wn[(i0 + e) * LD128 + 16 * wave + lc] = static_cast<half_t>(-w[e]);
+        split4(w, wh[pb], wl[pb]);
+        split4(u, uh[pb], ul[pb]);
+        // -W^T: the four tokens of this lane are contiguous in row dk = 16 wave + lc
+        *reinterpret_cast<h4_v*>(Wt + (16 * wave + lc) * LD64 + i0) = -wh[pb];
         if (has_u) {
 #pragma unroll
           for (int e = 0; e < 4; ++e) Ub[(i0 + e) * LDF + 16 * wave + lc] = u[e];
@@ -613,7 +635,12 @@ __global__ __launch_bounds__(NT) void chunk_kernel(ChunkParams p) {
       const int dt = 2 * wave + s;
       const int ti = dt >> 2;
       const int tv = dt & 3;
-      Dl[s] = mma<DK>(Wn + 16 * ti * LD128, LD128, St + 16 * tv * LD128, LD128, Dl[s], lane);
+#pragma unroll
+      for (int k0 = 0; k0 < DK; k0 += 32) {
+        const f16x8_v av = tr_operand32(Wt, LD64, k0, 16 * ti, lane);
+        const f16x8_v bv = *reinterpret_cast<const f16x8_v*>(St + (16 * tv + lc) * LD128 + k0 + 8 * lq);
+        Dl[s] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, bv, Dl[s], 0, 0, 0);
+      }
       const int dv = 16 * tv + lc;
       const int i0 = 16 * ti + 4 * lq;
       store4h(Dt + dv * LD64 + i0, Dl[s][0], Dl[s][1], Dl[s][2], Dl[s][3]);
@@ -649,10 +676,7 @@ __global__ __launch_bounds__(NT) void chunk_kernel(ChunkParams p) {
     const float gamC = s_gam[CH - 1];
     f16x8_v kt[CH / 32];  // K^T rows 16 wave.. (dk) as A operand, k = token
 #pragma unroll
-    for (int k0 = 0; k0 < CH; k0 += 32)
-      kt[k0 / 32] = __builtin_bit_cast(f16x8_v, __builtin_shufflevector(tr_read(Ks, LD128, k0 + 8 * lq, 16 * wave, lane),
-                                                                         tr_read(Ks, LD128, k0 + 8 * lq + 4, 16 * wave, lane),
-                                                                         0, 1, 2, 3, 4, 5, 6, 7));
+    for (int k0 = 0; k0 < CH; k0 += 32) kt[k0 / 32] = tr_operand32(Ks, LD128, k0, 16 * wave, lane);
 #pragma unroll
     for (int tv = 0; tv < 4; ++tv) {
       cfloat4 acc = S[tv] * gamC;
