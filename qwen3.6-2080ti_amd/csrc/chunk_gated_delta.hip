@@ -32,10 +32,10 @@
 // T: with 16-token blocks, (I + A) W = X gives W_p = D_p (X_p - sum_{k<p} A_pk
 // W_k), D_p = (I + A_pp)^-1 (a register forward substitution in fp32); each
 // wave runs this block recurrence for its own column tiles of X = [beta gamma K
-// | beta V] on v_mfma_f32_16x16x16_f16 with fp16 hi + lo operand pairs, keeping
-// the state update within fp32-state tolerance.  The 16x16 accumulator layout
-// equals the B-operand layout, so every W_k feeds the next block from
-// registers.  The next chunk's tiles are loaded into registers while the
+// | beta V] with fp16 hi + lo operand pairs (mma3 below), keeping the state
+// update within fp32-state tolerance.  The 16x16 accumulator layout equals the
+// B-operand layout of the 16-deep product, so every W_k feeds the next block
+// from registers.  The next chunk's tiles are loaded into registers while the
 // current one is computed; barriers order LDS only, so those loads stay in
 // flight across them.  Operands that reduce over tokens are read from the
 // token-major K and V tiles with ds_read_b64_tr_b16 (tr_operand below).
@@ -321,17 +321,43 @@ __global__ __launch_bounds__(256) void gate_kernel(GateParams p) {
 
 // C(16x16) += A(16 x K) * B(K x 16); A stored [m][k] (lda), B stored [n][k] (ldb), fp16.
 // Lane l gets C[4(l/16) + r][l % 16].
+// All operand reads are issued before the first product (the scheduler would
+// otherwise pair each read with its product and serialise the LDS latency).
 template <int K>
 __device__ __forceinline__ cfloat4 mma(const half_t* A, int lda, const half_t* B, int ldb, cfloat4 acc, int lane) {
   const int row = lane & 15;
   const int kq = lane >> 4;
+  f16x8_v av[K / 32], bv[K / 32];
 #pragma unroll
-  for (int k0 = 0; k0 < K; k0 += 32) {
-    const f16x8_v av = *reinterpret_cast<const f16x8_v*>(A + row * lda + k0 + 8 * kq);
-    const f16x8_v bv = *reinterpret_cast<const f16x8_v*>(B + row * ldb + k0 + 8 * kq);
-    acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, bv, acc, 0, 0, 0);
+  for (int k = 0; k < K / 32; ++k) {
+    av[k] = *reinterpret_cast<const f16x8_v*>(A + row * lda + 32 * k + 8 * kq);
+    bv[k] = *reinterpret_cast<const f16x8_v*>(B + row * ldb + 32 * k + 8 * kq);
   }
+  __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+  for (int k = 0; k < K / 32; ++k) acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(av[k], bv[k], acc, 0, 0, 0);
   return acc;
+}
+
+// Two tiles that share the A rows: C0 += A B0, C1 += A B1 (B0, B1 stored [n][k]).
+template <int K>
+__device__ __forceinline__ void mma2(const half_t* A, int lda, const half_t* B0, const half_t* B1, int ldb, cfloat4& c0, cfloat4& c1,
+                                     int lane) {
+  const int row = lane & 15;
+  const int kq = lane >> 4;
+  f16x8_v av[K / 32], b0[K / 32], b1[K / 32];
+#pragma unroll
+  for (int k = 0; k < K / 32; ++k) {
+    av[k] = *reinterpret_cast<const f16x8_v*>(A + row * lda + 32 * k + 8 * kq);
+    b0[k] = *reinterpret_cast<const f16x8_v*>(B0 + row * ldb + 32 * k + 8 * kq);
+    b1[k] = *reinterpret_cast<const f16x8_v*>(B1 + row * ldb + 32 * k + 8 * kq);
+  }
+  __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+  for (int k = 0; k < K / 32; ++k) {
+    c0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(av[k], b0[k], c0, 0, 0, 0);
+    c1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(av[k], b1[k], c1, 0, 0, 0);
+  }
 }
 
 // Four fp16 of a column of a row-major LDS tile X, for each lane, by
@@ -359,20 +385,23 @@ __device__ __forceinline__ f16x8_v tr_operand32(const half_t* tile, int ld, int 
 // v = hi + lo with hi = fp16(v) and lo = fp16(v - hi) (v - hi is exact in fp32).
 // lo comes from v_fma_mix{lo,hi}_f16, which take hi as an fp16 operand and
 // round the fp32 result once: 1.5 instructions per element instead of 3.5.
+// The compiler does not see these VALU writes when it inserts the wait states
+// an MFMA needs before reading a VGPR written by VALU, so the asm block ends
+// with s_nop 4.
 __device__ __forceinline__ void split4(const cfloat4& v, h4_v& hi, h4_v& lo) {
   typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
 #pragma unroll
   for (int e = 0; e < 4; ++e) hi[e] = static_cast<half_t>(v[e]);
   const u32x2 h = __builtin_bit_cast(u32x2, hi);
-  u32x2 l;
-#pragma unroll
-  for (int p = 0; p < 2; ++p) {
-    unsigned int r;
-    asm("v_fma_mixlo_f16 %0, -1.0, %1, %2 op_sel_hi:[0,1,0]" : "=v"(r) : "v"(h[p]), "v"(v[2 * p]));
-    asm("v_fma_mixhi_f16 %0, -1.0, %1, %2 op_sel:[0,1,0] op_sel_hi:[0,1,0]" : "+v"(r) : "v"(h[p]), "v"(v[2 * p + 1]));
-    l[p] = r;
-  }
-  lo = __builtin_bit_cast(h4_v, l);
+  unsigned int l0, l1;
+  asm("v_fma_mixlo_f16 %0, -1.0, %2, %4 op_sel_hi:[0,1,0]\n\t"
+      "v_fma_mixhi_f16 %0, -1.0, %2, %5 op_sel:[0,1,0] op_sel_hi:[0,1,0]\n\t"
+      "v_fma_mixlo_f16 %1, -1.0, %3, %6 op_sel_hi:[0,1,0]\n\t"
+      "v_fma_mixhi_f16 %1, -1.0, %3, %7 op_sel:[0,1,0] op_sel_hi:[0,1,0]\n\t"
+      "s_nop 4"
+      : "=&v"(l0), "=&v"(l1)
+      : "v"(h[0]), "v"(h[1]), "v"(v[0]), "v"(v[1]), "v"(v[2]), "v"(v[3]));
+  lo = __builtin_bit_cast(h4_v, u32x2{l0, l1});
 }
 
 // One chunk's inputs, staged in registers while the previous chunk is computed:
@@ -399,7 +428,17 @@ __device__ __forceinline__ ChunkRegs load_chunk(const ChunkParams& p, int64_t b,
   return r;
 }
 
-__global__ __launch_bounds__(NT) void chunk_kernel(ChunkParams p) {
+// acc += ah bh + ah bl + al bh for 16x16 blocks held as fp16 hi + lo pairs in the
+// 16x16x16 operand layouts (lane l: A row l % 16, k = 4 (l / 16) + e; B k =
+// 4 (l / 16) + e, column l % 16).  (Packing the pairs into two 16x16x32 products
+// measured slower: the operand copies cost more than the saved MFMA cycles.)
+__device__ __forceinline__ cfloat4 mma3(const h4_v& ah, const h4_v& al, const h4_v& bh, const h4_v& bl, cfloat4 acc) {
+  acc = __builtin_amdgcn_mfma_f32_16x16x16f16(ah, bh, acc, 0, 0, 0);
+  acc = __builtin_amdgcn_mfma_f32_16x16x16f16(ah, bl, acc, 0, 0, 0);
+  return __builtin_amdgcn_mfma_f32_16x16x16f16(al, bh, acc, 0, 0, 0);
+}
+
+__global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(2, 2))) void chunk_kernel(ChunkParams p) {
   extern __shared__ __align__(16) unsigned char smem[];
   half_t* Qs = reinterpret_cast<half_t*>(smem + OFF_QS);
   half_t* Ks = reinterpret_cast<half_t*>(smem + OFF_KS);
@@ -441,10 +480,19 @@ __global__ __launch_bounds__(NT) void chunk_kernel(ChunkParams p) {
     }
     store4h(St + (16 * tv + lc) * LD128 + 16 * wave + 4 * lq, S[tv][0], S[tv][1], S[tv][2], S[tv][3]);
   }
+  // Aqk tiles above the diagonal are zero for every chunk
+  if (tid < 6 * 64) {
+    const int n = tid >> 6;  // (ti, tl) = (0,1) (0,2) (0,3) (1,2) (1,3) (2,3)
+    const int ti = n < 3 ? 0 : n < 5 ? 1 : 2;
+    const int tl = ti + 1 + (n < 3 ? n : n < 5 ? n - 3 : 0);
+    store4h(Aqk + (16 * ti + lc) * LD64 + 16 * tl + 4 * lq, 0.f, 0.f, 0.f, 0.f);
+  }
   ChunkRegs nx = load_chunk(p, b, j, qh, half_id, 0, tid);
 
   for (int64_t ci = 0; ci < p.nch; ++ci) {
     const int64_t t0 = ci * CH;
+    // The lane index is re-derived opaquely each chunk so the per-lane LDS addresses below are
+    // recomputed inside the loop instead of being hoisted and held in VGPRs across it.
 
     // ---------------- stage this chunk's tiles; the next chunk's loads go out
     {
@@ -479,16 +527,17 @@ __global__ __launch_bounds__(NT) void chunk_kernel(ChunkParams p) {
       const int ti = tile >> 2;
       const int tl = tile & 3;
       if (tl > ti) continue;
-      cfloat4 acc = {0.f, 0.f, 0.f, 0.f};
-      acc = mma<DK>(Ks + 16 * tl * LD128, LD128, Ks + 16 * ti * LD128, LD128, acc, lane);
       const int i = 16 * ti + lc;
       const float bi = s_beta[i];
       const float gi = s_G[i];
+      const cfloat4 gl = *reinterpret_cast<const cfloat4*>(s_G + 16 * tl + 4 * lq);
+      cfloat4 acc = {0.f, 0.f, 0.f, 0.f};
+      acc = mma<DK>(Ks + 16 * tl * LD128, LD128, Ks + 16 * ti * LD128, LD128, acc, lane);
       cfloat4 a;
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        const int l = 16 * tl + 4 * lq + r;
-        a[r] = l < i ? bi * __expf(gi - s_G[l]) * acc[r] : 0.f;
+        const float e = bi * __expf(gi - gl[r]) * acc[r];
+        a[r] = 16 * tl + 4 * lq + r < i ? e : 0.f;
       }
       if (ti == tl) {
         *reinterpret_cast<cfloat4*>(Adg + (16 * ti + lc) * LDB + 4 * lq) = a;
@@ -509,45 +558,70 @@ __global__ __launch_bounds__(NT) void chunk_kernel(ChunkParams p) {
       const int qb = lane >> 4;
       const int c = lane & 15;
       const float* ab = Adg + (16 * qb) * LDB;
+      // the sub-diagonal entries of this lane's block are read 16 bytes at a time ahead of
+      // the substitution, in two batches of rows (1..10, 11..15), so it does not wait on LDS
+      // row by row
       float x[16];
+      cfloat4 arow[16][4];
 #pragma unroll
-      for (int i = 0; i < 16; ++i) {
+      for (int i = 1; i <= 10; ++i)
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+          if (4 * q < i) arow[i][q] = *reinterpret_cast<const cfloat4*>(ab + i * LDB + 4 * q);
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int i = 0; i <= 10; ++i) {
         float v = i == c ? 1.f : 0.f;
 #pragma unroll
-        for (int l = 0; l < i; ++l) v -= ab[i * LDB + l] * x[l];
+        for (int l = 0; l < i; ++l) v -= arow[i][l >> 2][l & 3] * x[l];
+        x[i] = v;
+      }
+#pragma unroll
+      for (int i = 11; i < 16; ++i)
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+          if (4 * q < i) arow[i][q] = *reinterpret_cast<const cfloat4*>(ab + i * LDB + 4 * q);
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int i = 11; i < 16; ++i) {
+        float v = i == c ? 1.f : 0.f;
+#pragma unroll
+        for (int l = 0; l < i; ++l) v -= arow[i][l >> 2][l & 3] * x[l];
         x[i] = v;
       }
 #pragma unroll
       for (int i = 0; i < 16; ++i) Tb[(16 * qb + i) * LDB + c] = x[i];
     } else {
-      // Aqk[i][l] = exp(G_i - G_l) (q_i . k_l), l <= i, computed as (K Q^T)[l][i]
-      for (int tile = wave - 1; tile < 16; tile += NW - 1) {
-        const int tl = tile >> 2;
-        const int ti = tile & 3;
-        cfloat4 acc = {0.f, 0.f, 0.f, 0.f};
-        if (tl <= ti) acc = mma<DK>(Ks + 16 * tl * LD128, LD128, Qs + 16 * ti * LD128, LD128, acc, lane);
+      // Aqk[i][l] = exp(G_i - G_l) (q_i . k_l), l <= i, computed as (K Q^T)[l][i], for
+      // the ten tiles with tl <= ti (the others stay zero from the start)
+      for (int n = wave - 1; n < 10; n += NW - 1) {
+        const int ti = n < 1 ? 0 : n < 3 ? 1 : n < 6 ? 2 : 3;
+        const int tl = n - ti * (ti + 1) / 2;
         const int i = 16 * ti + lc;
+        const float gi = s_G[i];
+        const cfloat4 gl = *reinterpret_cast<const cfloat4*>(s_G + 16 * tl + 4 * lq);
+        cfloat4 acc = {0.f, 0.f, 0.f, 0.f};
+        acc = mma<DK>(Ks + 16 * tl * LD128, LD128, Qs + 16 * ti * LD128, LD128, acc, lane);
         float v[4];
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-          const int l = 16 * tl + 4 * lq + r;
-          v[r] = l <= i ? __expf(s_G[i] - s_G[l]) * acc[r] : 0.f;
+          const float e = __expf(gi - gl[r]) * acc[r];
+          v[r] = 16 * tl + 4 * lq + r <= i ? e : 0.f;
         }
         store4h(Aqk + i * LD64 + 16 * tl + 4 * lq, v[0], v[1], v[2], v[3]);
       }
     }
-    // O^T tiles (dv tile td, token tile tt) = gamma * (S0^T Q^T): tile ot = 2*wave + s
-    cfloat4 O[2];
-#pragma unroll
-    for (int s = 0; s < 2; ++s) {
-      const int ot = 2 * wave + s;
-      const int td = ot >> 2;
-      const int tt = ot & 3;
-      cfloat4 acc = {0.f, 0.f, 0.f, 0.f};
-      acc = mma<DK>(St + 16 * td * LD128, LD128, Qs + 16 * tt * LD128, LD128, acc, lane);
-      const float gam = s_gam[16 * tt + lc];
-#pragma unroll
-      for (int r = 0; r < 4; ++r) O[s][r] = acc[r] * gam;
+    // O^T tiles (dv tile td, token tiles tt0 + s) = gamma * (S0^T Q^T); this wave's
+    // output and delta tiles are (wave / 2, 2 (wave % 2) + s), s = 0, 1
+    const int td = wave >> 1;
+    const int tt0 = 2 * (wave & 1);
+    cfloat4 O[2] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
+    {
+      const float gam0 = s_gam[16 * tt0 + lc];
+      const float gam1 = s_gam[16 * tt0 + 16 + lc];
+      mma2<DK>(St + 16 * td * LD128, LD128, Qs + 16 * tt0 * LD128, Qs + 16 * (tt0 + 1) * LD128, LD128, O[0], O[1], lane);
+      O[0] *= gam0;
+      O[1] *= gam1;
     }
     lds_barrier();
 
@@ -558,11 +632,6 @@ __global__ __launch_bounds__(NT) void chunk_kernel(ChunkParams p) {
     // hi + lo A operands; R and W_p stay fp32 in registers and are split into
     // hi + lo B operands (the 16x16 accumulator layout is the B-operand layout).
     {
-      auto mma3 = [](const h4_v& ah, const h4_v& al, const h4_v& bh, const h4_v& bl, cfloat4 acc) {
-        acc = __builtin_amdgcn_mfma_f32_16x16x16f16(ah, bh, acc, 0, 0, 0);
-        acc = __builtin_amdgcn_mfma_f32_16x16x16f16(ah, bl, acc, 0, 0, 0);
-        return __builtin_amdgcn_mfma_f32_16x16x16f16(al, bh, acc, 0, 0, 0);
-      };
       // A operands: lane l holds row l % 16, columns 4 (l / 16) + e of a 16x16 block
       h4_v dh[4], dl[4];
 #pragma unroll
@@ -581,8 +650,8 @@ __global__ __launch_bounds__(NT) void chunk_kernel(ChunkParams p) {
 #pragma unroll
       for (int pb = 0; pb < 4; ++pb) {
         const int i0 = 16 * pb + 4 * lq;
-        const h4_v xrw = tr_read(Ks, LD128, i0, 16 * wave, lane);
-        const h4_v xru = tr_read(Vs, LD64, i0, 16 * (wave & 3), lane);
+        const h4_v xrw_ = tr_read(Ks, LD128, i0, 16 * wave, lane);
+        const h4_v xru_ = tr_read(Vs, LD64, i0, 16 * (wave & 3), lane);
         cfloat4 accw = {0.f, 0.f, 0.f, 0.f};
         cfloat4 accu = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
@@ -596,8 +665,8 @@ __global__ __launch_bounds__(NT) void chunk_kernel(ChunkParams p) {
         cfloat4 rw, ru;
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-          rw[e] = __builtin_fmaf(static_cast<float>(xrw[e]), bg[e], -accw[e]);
-          ru[e] = __builtin_fmaf(static_cast<float>(xru[e]), bt[e], -accu[e]);
+          rw[e] = __builtin_fmaf(static_cast<float>(xrw_[e]), bg[e], -accw[e]);
+          ru[e] = __builtin_fmaf(static_cast<float>(xru_[e]), bt[e], -accu[e]);
         }
         h4_v rwh, rwl, ruh, rul;
         split4(rw, rwh, rwl);
@@ -618,47 +687,48 @@ __global__ __launch_bounds__(NT) void chunk_kernel(ChunkParams p) {
     }
     lds_barrier();
 
-    cfloat4 Dl[2];  // delta tiles (token tile, dv tile) = ((2*wave+s)>>2, (2*wave+s)&3)
-#pragma unroll
-    for (int s = 0; s < 2; ++s) {
-      const int dt = 2 * wave + s;
-      const int ti = dt >> 2;
-      const int tv = dt & 3;
-#pragma unroll
-      for (int r = 0; r < 4; ++r) Dl[s][r] = Ub[(16 * ti + 4 * lq + r) * LDF + 16 * tv + lc];
-    }
-
-    // ---------------- delta = U - W S0; keep delta^T and exp(G_C - G) delta^T in LDS
-    const float gC = s_G[CH - 1];
-#pragma unroll
-    for (int s = 0; s < 2; ++s) {
-      const int dt = 2 * wave + s;
-      const int ti = dt >> 2;
-      const int tv = dt & 3;
-#pragma unroll
-      for (int k0 = 0; k0 < DK; k0 += 32) {
-        const f16x8_v av = tr_operand32(Wt, LD64, k0, 16 * ti, lane);
-        const f16x8_v bv = *reinterpret_cast<const f16x8_v*>(St + (16 * tv + lc) * LD128 + k0 + 8 * lq);
-        Dl[s] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, bv, Dl[s], 0, 0, 0);
-      }
-      const int dv = 16 * tv + lc;
+    // ---------------- delta = U - W S0 for the tiles (token tile td, dv tiles tt0 + s);
+    // keep delta^T and exp(G_C - G) delta^T in LDS
+    {
+      const int ti = td;
       const int i0 = 16 * ti + 4 * lq;
-      store4h(Dt + dv * LD64 + i0, Dl[s][0], Dl[s][1], Dl[s][2], Dl[s][3]);
-      float sc[4];
+      cfloat4 Dl[2];
 #pragma unroll
-      for (int r = 0; r < 4; ++r) sc[r] = __expf(gC - s_G[i0 + r]) * Dl[s][r];
-      store4h(DDt + dv * LD64 + i0, sc[0], sc[1], sc[2], sc[3]);
+      for (int s = 0; s < 2; ++s)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) Dl[s][r] = Ub[(i0 + r) * LDF + 16 * (tt0 + s) + lc];
+      const float gC = s_G[CH - 1];
+      const cfloat4 gi = *reinterpret_cast<const cfloat4*>(s_G + i0);
+      f16x8_v wa[DK / 32], sb0[DK / 32], sb1[DK / 32];
+#pragma unroll
+      for (int k = 0; k < DK / 32; ++k) {
+        wa[k] = tr_operand32(Wt, LD64, 32 * k, 16 * ti, lane);
+        sb0[k] = *reinterpret_cast<const f16x8_v*>(St + (16 * tt0 + lc) * LD128 + 32 * k + 8 * lq);
+        sb1[k] = *reinterpret_cast<const f16x8_v*>(St + (16 * tt0 + 16 + lc) * LD128 + 32 * k + 8 * lq);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int k = 0; k < DK / 32; ++k) {
+        Dl[0] = __builtin_amdgcn_mfma_f32_16x16x32_f16(wa[k], sb0[k], Dl[0], 0, 0, 0);
+        Dl[1] = __builtin_amdgcn_mfma_f32_16x16x32_f16(wa[k], sb1[k], Dl[1], 0, 0, 0);
+      }
+      cfloat4 dec;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) dec[r] = __expf(gC - gi[r]);
+#pragma unroll
+      for (int s = 0; s < 2; ++s) {
+        const int dv = 16 * (tt0 + s) + lc;
+        store4h(Dt + dv * LD64 + i0, Dl[s][0], Dl[s][1], Dl[s][2], Dl[s][3]);
+        store4h(DDt + dv * LD64 + i0, dec[0] * Dl[s][0], dec[1] * Dl[s][1], dec[2] * Dl[s][2], dec[3] * Dl[s][3]);
+      }
     }
     lds_barrier();
 
     // ---------------- O^T += delta^T Aqk^T -> output; S = gamma_C S + K^T (D delta)
+    mma2<CH>(Dt + 16 * td * LD64, LD64, Aqk + 16 * tt0 * LD64, Aqk + 16 * (tt0 + 1) * LD64, LD64, O[0], O[1], lane);
 #pragma unroll
     for (int s = 0; s < 2; ++s) {
-      const int ot = 2 * wave + s;
-      const int td = ot >> 2;
-      const int tt = ot & 3;
-      O[s] = mma<CH>(Dt + 16 * td * LD64, LD64, Aqk + 16 * tt * LD64, LD64, O[s], lane);
-      const int tok = 16 * tt + lc;
+      const int tok = 16 * (tt0 + s) + lc;
       const int64_t tg = t0 + tok;
       if (tg < p.T) {
         const int64_t base = b * p.out_sb + tg * p.out_st + static_cast<int64_t>(j) * DV + half_id * DVS + 16 * td + 4 * lq;
@@ -674,19 +744,23 @@ __global__ __launch_bounds__(NT) void chunk_kernel(ChunkParams p) {
       }
     }
     const float gamC = s_gam[CH - 1];
-    f16x8_v kt[CH / 32];  // K^T rows 16 wave.. (dk) as A operand, k = token
+    {
+      f16x8_v kt[CH / 32], bd[4][CH / 32];  // K^T rows 16 wave.. (dk) as A operand, k = token
 #pragma unroll
-    for (int k0 = 0; k0 < CH; k0 += 32) kt[k0 / 32] = tr_operand32(Ks, LD128, k0, 16 * wave, lane);
+      for (int k = 0; k < CH / 32; ++k) {
+        kt[k] = tr_operand32(Ks, LD128, 32 * k, 16 * wave, lane);
 #pragma unroll
-    for (int tv = 0; tv < 4; ++tv) {
-      cfloat4 acc = S[tv] * gamC;
-#pragma unroll
-      for (int k0 = 0; k0 < CH; k0 += 32) {
-        const f16x8_v bv = *reinterpret_cast<const f16x8_v*>(DDt + (16 * tv + lc) * LD64 + k0 + 8 * lq);
-        acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(kt[k0 / 32], bv, acc, 0, 0, 0);
+        for (int tv = 0; tv < 4; ++tv) bd[tv][k] = *reinterpret_cast<const f16x8_v*>(DDt + (16 * tv + lc) * LD64 + 32 * k + 8 * lq);
       }
-      S[tv] = acc;
-      store4h(St + (16 * tv + lc) * LD128 + 16 * wave + 4 * lq, S[tv][0], S[tv][1], S[tv][2], S[tv][3]);
+#pragma unroll
+      for (int tv = 0; tv < 4; ++tv) S[tv] *= gamC;
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int k = 0; k < CH / 32; ++k)
+#pragma unroll
+        for (int tv = 0; tv < 4; ++tv) S[tv] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kt[k], bd[tv][k], S[tv], 0, 0, 0);
+#pragma unroll
+      for (int tv = 0; tv < 4; ++tv) store4h(St + (16 * tv + lc) * LD128 + 16 * wave + 4 * lq, S[tv][0], S[tv][1], S[tv][2], S[tv][3]);
     }
     lds_barrier();
   }
