@@ -202,8 +202,9 @@ __global__ __launch_bounds__(NT) void prefill_kernel(Params p) {
   floatx4_v o[MT];
 #pragma unroll
   for (int t = 0; t < MT; ++t) o[t] = floatx4_v{0.f, 0.f, 0.f, 0.f};
-  float m_run = -INFINITY;
+  float m_run = -INFINITY;  // running max of the log2-domain scores
   float l_part = 0.f;
+  const float scale_l2 = p.scale * 1.4426950408889634f;
 
   const bf16_t* kb = p.kbase + static_cast<int64_t>(g) * p.sG;
   const bf16_t* vb = p.vbase + static_cast<int64_t>(g) * p.sG;
@@ -246,9 +247,9 @@ __global__ __launch_bounds__(NT) void prefill_kernel(Params p) {
     if (kt + 1 < ntiles) load_tile<D>(p, b, key0 + KT, kv_len, kb, vb, s_phys, nlb, ln, nx);
 
     if (active) {
-      // ---- S^T = K Q^T for the 4 key sub-tiles; mask; online softmax per position
+      // ---- S^T = K Q^T for the 4 key sub-tiles; mask; online softmax per position in
+      // the log2 domain (scores scaled by scale * log2 e, probabilities by exp2)
       floatx4_v s[KT / 16];
-      float mx = -INFINITY;
 #pragma unroll
       for (int st = 0; st < KT / 16; ++st) {
         floatx4_v acc = {0.f, 0.f, 0.f, 0.f};
@@ -256,19 +257,30 @@ __global__ __launch_bounds__(NT) void prefill_kernel(Params p) {
 #pragma unroll
         for (int i = 0; i < KCH; ++i)
           acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(*reinterpret_cast<const bf16x8_v*>(arow + 32 * i), qreg[i], acc, 0, 0, 0);
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const int64_t t = key0 + 16 * st + 4 * quad + r;
-          const float v = (row_live && t <= my_pos && t < kv_len && pick(cur_phys, st) >= 0) ? acc[r] * p.scale : -INFINITY;
-          s[st][r] = v;
-          mx = fmaxf(mx, v);
-        }
+        s[st] = acc * scale_l2;
       }
+      // only tiles that reach past the workgroup's first position, past the last
+      // visible key or over an absent block need a mask (wave-uniform test)
+      if (!(key0 + KT - 1 <= prefix + n0 && key0 + KT <= kv_len && cur_phys.x >= 0 && cur_phys.y >= 0 && cur_phys.z >= 0 &&
+            cur_phys.w >= 0)) {
+        // last key offset of this tile the lane's column may see (-1: none)
+        const int lim = static_cast<int>(max<int64_t>(-1, min<int64_t>(KT - 1, min(my_pos, kv_len - 1) - key0)));
+#pragma unroll
+        for (int st = 0; st < KT / 16; ++st)
+#pragma unroll
+          for (int r = 0; r < 4; ++r)
+            if (!(row_live && 16 * st + 4 * quad + r <= lim && pick(cur_phys, st) >= 0)) s[st][r] = -INFINITY;
+      }
+      float mx = -INFINITY;
+#pragma unroll
+      for (int st = 0; st < KT / 16; ++st)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) mx = fmaxf(mx, s[st][r]);
       mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
       mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
       const float m_new = fmaxf(m_run, mx);
       const float m_use = m_new == -INFINITY ? 0.f : m_new;
-      const float alpha = __expf(m_run - m_use);
+      const float alpha = __builtin_amdgcn_exp2f(m_run - m_use);
       m_run = m_new;
       short4_v pb[KT / 16];
       float psum = 0.f;
@@ -276,7 +288,7 @@ __global__ __launch_bounds__(NT) void prefill_kernel(Params p) {
       for (int st = 0; st < KT / 16; ++st)
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-          const float pr = __expf(s[st][r] - m_use);
+          const float pr = __builtin_amdgcn_exp2f(s[st][r] - m_use);
           psum += pr;
           pb[st][r] = static_cast<short>(f32_to_bf16(pr));
         }
