@@ -399,7 +399,7 @@ __global__ __launch_bounds__(256, QA_DECODE_WAVES_PER_SIMD) void decode_partial_
 
     const int64_t blk_end = seg_end - cur.cum;
     int64_t blk = tile - cur.cum;
-    int n = static_cast<int>(min<int64_t>(NG, blk_end - blk));
+    int n = static_cast<int>(min64(NG, blk_end - blk));
     int32_t phys[NG];
     int32_t phys_next[NG];
     read_group_entries<NG>(p, b, blk, n, nblk, phys);
@@ -409,7 +409,7 @@ __global__ __launch_bounds__(256, QA_DECODE_WAVES_PER_SIMD) void decode_partial_
 
     while (true) {
       const int64_t blk_next = blk + NG;
-      const int n_next = blk_next < blk_end ? static_cast<int>(min<int64_t>(NG, blk_end - blk_next)) : 0;
+      const int n_next = blk_next < blk_end ? static_cast<int>(min64(NG, blk_end - blk_next)) : 0;
       read_group_entries<NG>(p, b, blk_next, n_next, nblk, phys_next);
 
       // ---- phase 1: scores of the group's blocks (stream elements 0 .. NG-1)
@@ -605,7 +605,7 @@ __global__ __launch_bounds__(256) void decode_combine(DecodeParams p) {
   const float* ml = p.part_ml + bh * p.n_splits * 2;
   const float* po = p.part_o + bh * p.n_splits * p.D;
   const int64_t len = row_length(p, static_cast<int>(bh / p.H));
-  const int n_active = static_cast<int>(min<int64_t>(p.n_splits, len > 0 ? ceil_div_dev(len, p.split_tokens) : 0));
+  const int n_active = static_cast<int>(min64(p.n_splits, len > 0 ? ceil_div_dev(len, p.split_tokens) : 0));
   QT* out = reinterpret_cast<QT*>(p.out) + bh * p.D;
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;

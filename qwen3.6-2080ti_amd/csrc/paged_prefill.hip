@@ -9,14 +9,20 @@
 //
 // Workgroup = (16 new positions, sequence b, KV head g), 8 waves; wave w owns
 // query head g*G + w (w < G) for the 16 positions.  Keys stream in tiles of 64
-// through LDS: K as [key][d] (the A operand of S^T = K Q^T), V transposed to
-// [d][key] with v_perm_b32 so it is the A operand of O^T = V^T P.  S^T in the
-// MFMA accumulator layout (lane: keys 4(l/16)+r, position l%16) is exactly the
-// B-operand layout of the PV product, so P stays in registers.  Online softmax
-// per position (column), fp32; P rounded to bf16 (the reference rounds probs
-// to the query dtype before PV, src/reference_ops.py:358).  The row's block
-// table is read into LDS once; the next key tile is loaded into registers
-// while the current one is computed, and barriers order LDS only, so those
+// through LDS, K and V both as [key][d]: K is the A operand of S^T = K Q^T, and
+// the A operand of O^T = V^T P is read from V with ds_read_b64_tr_b16 (the
+// transposing LDS read), so V is staged as loaded.  S^T in the MFMA accumulator
+// layout (lane: keys 4(l/16)+r, position l%16) is exactly the B-operand layout
+// of the PV product, so P stays in registers.  Online softmax per position
+// (column), fp32; P rounded to bf16 (the reference rounds probs to the query
+// dtype before PV, src/reference_ops.py:358).
+//
+// Pipeline: K and V tiles are double-buffered in LDS with K one tile ahead, so
+// iteration t issues the S products of tile t+1 next to the softmax of tile t
+// (MFMA and VALU work of one wave overlap), then the PV products of tile t,
+// then stages K of tile t+2 and V of tile t+1 from registers and issues the
+// loads of K(t+3) and V(t+2), with one barrier per tile.  The row's block table is read into LDS once; global loads are
+// issued a tile ahead into registers and barriers order LDS only, so those
 // loads stay in flight across them.
 #include "qa_common.h"
 
@@ -57,30 +63,25 @@ struct Params {
 
 template <int D>
 struct Smem {
-  static constexpr int kLdK = D + 8;                   // halfs per K row (16-byte padded)
-  static constexpr int kVtUnits = (KT / 4) * (D + 16); // 8-byte units: [key quad][d] (+pad)
-  static constexpr int kBytes = KT * kLdK * 2 + kVtUnits * 8 + MAXB * 4;
+  static constexpr int kLdK = D + 8;   // halfs per K row (16-byte padded: conflict-free row reads)
+  static constexpr int kLdV = D + 16;  // halfs per V row (32-byte padded: conflict-free transposing reads)
+  static constexpr int kKBytes = KT * kLdK * 2;
+  static constexpr int kVBytes = KT * kLdV * 2;
+  static constexpr int kBytes = 2 * kKBytes + 2 * kVBytes + MAXB * 4;  // two K and two V tiles + block table
 };
 
-// One key tile's K and V pieces in flight: thread c loads K pieces (key, 16-byte
-// chunk) c + j NT and the four rows of V item c (key quad, 8-dim chunk), plus the
-// physical blocks of the tile's four 16-key blocks (wave-uniform; -1 = absent).
+// Pieces of one tile's K (or V) in flight: thread c loads the 16-byte pieces
+// (key, chunk) c + j NT.
 template <int D>
 struct TileRegs {
-  static constexpr int KP = KT * (D / 8) / NT;  // K pieces per thread
-  static constexpr int VITEMS = KT / 4 * (D / 8);
-  static constexpr int VP = (VITEMS + NT - 1) / NT;  // V items per thread (the last may be partial)
+  static constexpr int KP = KT * (D / 8) / NT;  // pieces per thread
   u32x4_v k[KP];
-  u32x4_v v[VP][4];
-  int4 phys;  // blocks of keys [0,16) [16,32) [32,48) [48,64) of the tile
 };
-static_assert(KT == 4 * BS, "a key tile spans four cache blocks");
+
 
 __device__ __forceinline__ int64_t rd_index(const void* base, int is64, int64_t i) {
   return is64 ? reinterpret_cast<const int64_t*>(base)[i] : reinterpret_cast<const int32_t*>(base)[i];
 }
-
-__device__ __forceinline__ int vt_swz(int d) { return d ^ ((d >> 5) & 7); }
 
 // Physical block of logical block lb of row b (-1 if absent or outside the pool).
 __device__ __forceinline__ int64_t block_of(const Params& p, int b, int64_t lb, const int* s_phys, int64_t nlb) {
@@ -90,16 +91,13 @@ __device__ __forceinline__ int64_t block_of(const Params& p, int b, int64_t lb, 
   return e >= 0 && e < p.num_blocks ? e : -1;
 }
 
-// Per-thread element offsets inside a block: the key and chunk of each K piece
-// and V row are fixed by the thread index, only the block changes per tile.
+// Per-thread element offsets inside a block: the key and chunk of each piece are
+// fixed by the thread index, only the block changes per tile.
 template <int D>
 struct TileLanes {
-  int kblk[TileRegs<D>::KP];   // which of the tile's blocks each K piece lies in
+  int kblk[TileRegs<D>::KP];   // which of the tile's blocks each piece lies in
   int koff[TileRegs<D>::KP];   // element offset inside that block
   int kkey[TileRegs<D>::KP];   // key index inside the tile
-  int vblk[TileRegs<D>::VP];
-  int voff[TileRegs<D>::VP];   // offset of row 0; rows r add r * sT
-  int vkey[TileRegs<D>::VP];   // first key of the quad (KT when the item does not exist)
 };
 
 template <int D>
@@ -114,41 +112,57 @@ __device__ __forceinline__ TileLanes<D> tile_lanes(const Params& p, int tid) {
     ln.kblk[j] = key / BS;
     ln.koff[j] = static_cast<int>((key % BS) * p.sT) + 8 * (c % DC);
   }
-#pragma unroll
-  for (int j = 0; j < TileRegs<D>::VP; ++j) {
-    const int c = tid + j * NT;
-    const int kq = c / DC;
-    ln.vkey[j] = c < TileRegs<D>::VITEMS ? 4 * kq : KT;
-    ln.vblk[j] = (4 * kq) / BS;
-    ln.voff[j] = static_cast<int>(((4 * kq) % BS) * p.sT) + 8 * (c % DC);
-  }
   return ln;
 }
 
 __device__ __forceinline__ int pick(const int4& v, int i) { return i == 0 ? v.x : i == 1 ? v.y : i == 2 ? v.z : v.w; }
 
-template <int D>
-__device__ __forceinline__ void load_tile(const Params& p, int b, int64_t key0, int64_t kv_len, const bf16_t* kb, const bf16_t* vb,
-                                          const int* s_phys, int64_t nlb, const TileLanes<D>& ln, TileRegs<D>& r) {
+// Physical blocks of the four 16-key blocks of the tile at key0 (wave-uniform; -1 = absent):
+// one 16-byte LDS read when the whole tile lies in the cached part of the block table.
+__device__ __forceinline__ int4 tile_phys(const Params& p, int b, int64_t key0, int64_t kv_len, const int* s_phys, int64_t nlb) {
+  const int64_t lb0 = key0 / BS;
+  if (lb0 + 4 <= min64(nlb, MAXB)) {
+    const int4 v = *reinterpret_cast<const int4*>(s_phys + lb0);
+    return make_int4(__builtin_amdgcn_readfirstlane(v.x), __builtin_amdgcn_readfirstlane(v.y), __builtin_amdgcn_readfirstlane(v.z),
+                     __builtin_amdgcn_readfirstlane(v.w));
+  }
   auto blk = [&](int q) {
     const int64_t t = key0 + BS * q;
     return __builtin_amdgcn_readfirstlane(t < kv_len ? static_cast<int>(block_of(p, b, t / BS, s_phys, nlb)) : -1);
   };
-  r.phys = make_int4(blk(0), blk(1), blk(2), blk(3));
+  return make_int4(blk(0), blk(1), blk(2), blk(3));
+}
+
+// Loads the pieces of one tile of the pool at base (K or V); keys past kv_len and absent blocks read as zero.
+template <int D>
+__device__ __forceinline__ void load_pieces(const Params& p, int64_t key0, int64_t kv_len, const bf16_t* base, const int4& phys,
+                                            const TileLanes<D>& ln, TileRegs<D>& r) {
 #pragma unroll
   for (int j = 0; j < TileRegs<D>::KP; ++j) {
-    const int phys = pick(r.phys, ln.kblk[j]);
-    r.k[j] = phys >= 0 && key0 + ln.kkey[j] < kv_len ? *reinterpret_cast<const u32x4_v*>(kb + static_cast<int64_t>(phys) * p.sP + ln.koff[j])
-                                                    : u32x4_v{0u, 0u, 0u, 0u};
+    const int blk = pick(phys, ln.kblk[j]);
+    r.k[j] = blk >= 0 && key0 + ln.kkey[j] < kv_len ? *reinterpret_cast<const u32x4_v*>(base + static_cast<int64_t>(blk) * p.sP + ln.koff[j])
+                                                   : u32x4_v{0u, 0u, 0u, 0u};
   }
+}
+
+template <int D, int LD>
+__device__ __forceinline__ void stage_pieces(bf16_t* dst, const TileRegs<D>& r, int tid) {
+  constexpr int DC = D / 8;
 #pragma unroll
-  for (int j = 0; j < TileRegs<D>::VP; ++j) {
-    const int phys = ln.vkey[j] < KT ? pick(r.phys, ln.vblk[j]) : -1;
-    const bf16_t* base = vb + static_cast<int64_t>(phys < 0 ? 0 : phys) * p.sP + ln.voff[j];
-#pragma unroll
-    for (int rr = 0; rr < 4; ++rr)
-      r.v[j][rr] = phys >= 0 && key0 + ln.vkey[j] + rr < kv_len ? *reinterpret_cast<const u32x4_v*>(base + rr * p.sT) : u32x4_v{0u, 0u, 0u, 0u};
+  for (int j = 0; j < TileRegs<D>::KP; ++j) {
+    const int c = tid + j * NT;
+    const int key = c / DC;
+    *reinterpret_cast<u32x4_v*>(dst + key * LD + 8 * (c - key * DC)) = r.k[j];
   }
+}
+
+// Four bf16 of a column of a row-major LDS tile, for each lane, by
+// ds_read_b64_tr_b16: lane i of 16-lane group g reads the 8 bytes at
+// X[row_g + i / 4][c0 + 4 (i % 4)] and receives X[row_g + e][c0 + i], e = 0..3.
+__device__ __forceinline__ short4_v tr_read(const bf16_t* tile, int ld, int row_g, int c0, int lane) {
+  typedef __attribute__((address_space(3))) short4_v lds_s4;
+  const int i = lane & 15;
+  return __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s4*)(tile + (row_g + (i >> 2)) * ld + c0 + 4 * (i & 3)));
 }
 
 template <int D>
@@ -157,9 +171,9 @@ __global__ __launch_bounds__(NT) void prefill_kernel(Params p) {
   constexpr int MT = D / 16;   // output dim tiles
   constexpr int DC = D / 8;
   extern __shared__ __align__(16) unsigned char smem[];
-  bf16_t* Ksm = reinterpret_cast<bf16_t*>(smem);
-  uint2* Vt = reinterpret_cast<uint2*>(smem + KT * Smem<D>::kLdK * 2);
-  int* s_phys = reinterpret_cast<int*>(smem + KT * Smem<D>::kLdK * 2 + Smem<D>::kVtUnits * 8);
+  auto Kbuf = [&](int i) { return reinterpret_cast<bf16_t*>(smem + i * Smem<D>::kKBytes); };
+  auto Vbuf = [&](int i) { return reinterpret_cast<bf16_t*>(smem + 2 * Smem<D>::kKBytes + i * Smem<D>::kVBytes); };
+  int* s_phys = reinterpret_cast<int*>(smem + 2 * Smem<D>::kKBytes + 2 * Smem<D>::kVBytes);
 
   const int pt = blockIdx.x;
   const int bg = blockIdx.y;
@@ -182,8 +196,8 @@ __global__ __launch_bounds__(NT) void prefill_kernel(Params p) {
   const bool row_live = n0 + col < n_new;
 
   // the row's block table, once (entries outside the pool become -1)
-  const int64_t nlb = min<int64_t>((kv_len + BS - 1) / BS, p.max_blocks);
-  for (int64_t lb = tid; lb < min<int64_t>(nlb, MAXB); lb += NT) {
+  const int64_t nlb = min64((kv_len + BS - 1) / BS, p.max_blocks);
+  for (int64_t lb = tid; lb < min64(nlb, MAXB); lb += NT) {
     const int64_t e = rd_index(p.tables, p.table_i64, b * p.table_stride + lb);
     s_phys[lb] = e >= 0 && e < p.num_blocks ? static_cast<int>(e) : -1;
   }
@@ -211,71 +225,69 @@ __global__ __launch_bounds__(NT) void prefill_kernel(Params p) {
   const int64_t ntiles = (kv_len + KT - 1) / KT;
   lds_barrier();  // s_phys
   const TileLanes<D> ln = tile_lanes<D>(p, tid);
-  TileRegs<D> nx;
-  load_tile<D>(p, b, 0, kv_len, kb, vb, s_phys, nlb, ln, nx);
+
+  // S^T of a tile from the K buffer kbuf (unscaled: nothing waits on the products here)
+  auto scores = [&](const bf16_t* kbuf, floatx4_v* s) {
+#pragma unroll
+    for (int st = 0; st < KT / 16; ++st) {
+      floatx4_v acc = {0.f, 0.f, 0.f, 0.f};
+      const bf16_t* arow = kbuf + (16 * st + col) * Smem<D>::kLdK + 8 * quad;
+#pragma unroll
+      for (int i = 0; i < KCH; ++i)
+        acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(*reinterpret_cast<const bf16x8_v*>(arow + 32 * i), qreg[i], acc, 0, 0, 0);
+      s[st] = acc;
+    }
+  };
+
+  // Block ids of tiles kt .. kt+2 (wave-uniform), each looked up once and before any
+  // tile load of the iteration is issued: a table read that misses the LDS copy waits
+  // on global memory, and that wait would also wait for the tile loads in flight.
+  int4 phys_cur = tile_phys(p, b, 0, kv_len, s_phys, nlb);
+  int4 phys_n1 = tile_phys(p, b, KT, kv_len, s_phys, nlb);
+  int4 phys_n2 = tile_phys(p, b, 2 * KT, kv_len, s_phys, nlb);
+
+  // prologue: K and V of tile 0 and K of tile 1 staged; loads of K(2) and V(1) in flight
+  TileRegs<D> rk, rv;
+  load_pieces<D>(p, 0, kv_len, kb, phys_cur, ln, rk);
+  load_pieces<D>(p, 0, kv_len, vb, phys_cur, ln, rv);
+  stage_pieces<D, Smem<D>::kLdK>(Kbuf(0), rk, tid);
+  stage_pieces<D, Smem<D>::kLdV>(Vbuf(0), rv, tid);
+  if (ntiles > 1) {
+    load_pieces<D>(p, KT, kv_len, kb, phys_n1, ln, rk);
+    stage_pieces<D, Smem<D>::kLdK>(Kbuf(1), rk, tid);
+  }
+  lds_barrier();
+  load_pieces<D>(p, 2 * KT, kv_len, kb, phys_n2, ln, rk);
+  load_pieces<D>(p, KT, kv_len, vb, phys_n1, ln, rv);
+  floatx4_v s_cur[KT / 16];
+  if (active) scores(Kbuf(0), s_cur);
+
   for (int64_t kt = 0; kt < ntiles; ++kt) {
     const int64_t key0 = kt * KT;
-    // ---- stage K [key][d] and V^T [key quad][d] of this tile from the registers
-#pragma unroll
-    for (int j = 0; j < TileRegs<D>::KP; ++j) {
-      const int c = tid + j * NT;
-      const int key = c / DC;
-      const int dc = c - key * DC;
-      *reinterpret_cast<u32x4_v*>(Ksm + key * Smem<D>::kLdK + 8 * dc) = nx.k[j];
-    }
-#pragma unroll
-    for (int j = 0; j < TileRegs<D>::VP; ++j) {
-      const int c = tid + j * NT;
-      if (c >= TileRegs<D>::VITEMS) continue;
-      const int kq = c / DC;
-      const int dc = c - kq * DC;
-#pragma unroll
-      for (int k = 0; k < 4; ++k) {
-        const int d = 8 * dc + 2 * k;
-        uint2 lo, hi;
-        lo.x = __builtin_amdgcn_perm(nx.v[j][1][k], nx.v[j][0][k], 0x05040100u);
-        lo.y = __builtin_amdgcn_perm(nx.v[j][3][k], nx.v[j][2][k], 0x05040100u);
-        hi.x = __builtin_amdgcn_perm(nx.v[j][1][k], nx.v[j][0][k], 0x07060302u);
-        hi.y = __builtin_amdgcn_perm(nx.v[j][3][k], nx.v[j][2][k], 0x07060302u);
-        Vt[kq * (D + 16) + vt_swz(d)] = lo;
-        Vt[kq * (D + 16) + vt_swz(d + 1)] = hi;
-      }
-    }
-    const int4 cur_phys = nx.phys;
-    lds_barrier();
-    // next tile's loads go out now and land during this tile's products
-    if (kt + 1 < ntiles) load_tile<D>(p, b, key0 + KT, kv_len, kb, vb, s_phys, nlb, ln, nx);
-
+    const int cb = static_cast<int>(kt & 1);
+    floatx4_v s_nxt[KT / 16];
     if (active) {
-      // ---- S^T = K Q^T for the 4 key sub-tiles; mask; online softmax per position in
-      // the log2 domain (scores scaled by scale * log2 e, probabilities by exp2)
-      floatx4_v s[KT / 16];
+      // ---- S of the next tile (MFMA) next to the softmax of this one (VALU)
+      if (kt + 1 < ntiles) scores(Kbuf(cb ^ 1), s_nxt);
 #pragma unroll
-      for (int st = 0; st < KT / 16; ++st) {
-        floatx4_v acc = {0.f, 0.f, 0.f, 0.f};
-        const bf16_t* arow = Ksm + (16 * st + (lane & 15)) * Smem<D>::kLdK + 8 * quad;
-#pragma unroll
-        for (int i = 0; i < KCH; ++i)
-          acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(*reinterpret_cast<const bf16x8_v*>(arow + 32 * i), qreg[i], acc, 0, 0, 0);
-        s[st] = acc * scale_l2;
-      }
+      for (int st = 0; st < KT / 16; ++st) s_cur[st] *= scale_l2;
       // only tiles that reach past the workgroup's first position, past the last
       // visible key or over an absent block need a mask (wave-uniform test)
-      if (!(key0 + KT - 1 <= prefix + n0 && key0 + KT <= kv_len && cur_phys.x >= 0 && cur_phys.y >= 0 && cur_phys.z >= 0 &&
-            cur_phys.w >= 0)) {
+      if (!(key0 + KT - 1 <= prefix + n0 && key0 + KT <= kv_len && phys_cur.x >= 0 && phys_cur.y >= 0 && phys_cur.z >= 0 &&
+            phys_cur.w >= 0)) {
         // last key offset of this tile the lane's column may see (-1: none)
-        const int lim = static_cast<int>(max<int64_t>(-1, min<int64_t>(KT - 1, min(my_pos, kv_len - 1) - key0)));
+        const int lim = static_cast<int>(max64(-1, min64(KT - 1, min(my_pos, kv_len - 1) - key0)));
 #pragma unroll
         for (int st = 0; st < KT / 16; ++st)
 #pragma unroll
           for (int r = 0; r < 4; ++r)
-            if (!(row_live && 16 * st + 4 * quad + r <= lim && pick(cur_phys, st) >= 0)) s[st][r] = -INFINITY;
+            if (!(row_live && 16 * st + 4 * quad + r <= lim && pick(phys_cur, st) >= 0)) s_cur[st][r] = -INFINITY;
       }
       float mx = -INFINITY;
 #pragma unroll
       for (int st = 0; st < KT / 16; ++st)
 #pragma unroll
-        for (int r = 0; r < 4; ++r) mx = fmaxf(mx, s[st][r]);
+        for (int r = 0; r < 4; ++r) mx = fmaxf(mx, s_cur[st][r]);
       mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
       mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
       const float m_new = fmaxf(m_run, mx);
@@ -288,7 +300,7 @@ __global__ __launch_bounds__(NT) void prefill_kernel(Params p) {
       for (int st = 0; st < KT / 16; ++st)
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-          const float pr = __builtin_amdgcn_exp2f(s[st][r] - m_use);
+          const float pr = __builtin_amdgcn_exp2f(s_cur[st][r] - m_use);
           psum += pr;
           pb[st][r] = static_cast<short>(f32_to_bf16(pr));
         }
@@ -301,22 +313,37 @@ __global__ __launch_bounds__(NT) void prefill_kernel(Params p) {
       // ---- O^T += V^T P, 32 keys per v_mfma_f32_16x16x32_bf16: the reduction index
       // k = 8 (l/16) + e of lane l stands for key 4 (l/16) + e of sub-tile 2j (e < 4)
       // and of sub-tile 2j + 1 (e >= 4), so the B operand is the lane's own P of the
-      // two sub-tiles and the A operand two 4-key units of V^T
+      // two sub-tiles and the A operand two transposing reads of V rows
+      const bf16_t* vt = Vbuf(cb);
 #pragma unroll
       for (int jj = 0; jj < KT / 32; ++jj) {
-        short4_v p0 = pb[2 * jj], p1 = pb[2 * jj + 1];
-        const bf16x8_v bop = __builtin_bit_cast(bf16x8_v, __builtin_shufflevector(p0, p1, 0, 1, 2, 3, 4, 5, 6, 7));
+        const bf16x8_v bop = __builtin_bit_cast(bf16x8_v, __builtin_shufflevector(pb[2 * jj], pb[2 * jj + 1], 0, 1, 2, 3, 4, 5, 6, 7));
 #pragma unroll
         for (int t = 0; t < MT; ++t) {
-          const uint2 a0 = Vt[(8 * jj + quad) * (D + 16) + vt_swz(16 * t + col)];
-          const uint2 a1 = Vt[(8 * jj + 4 + quad) * (D + 16) + vt_swz(16 * t + col)];
-          const uint4 av = make_uint4(a0.x, a0.y, a1.x, a1.y);
-          o[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_v, av), bop, o[t], 0, 0, 0);
+          const short4_v a0 = tr_read(vt, Smem<D>::kLdV, 32 * jj + 4 * quad, 16 * t, lane);
+          const short4_v a1 = tr_read(vt, Smem<D>::kLdV, 32 * jj + 16 + 4 * quad, 16 * t, lane);
+          const bf16x8_v av = __builtin_bit_cast(bf16x8_v, __builtin_shufflevector(a0, a1, 0, 1, 2, 3, 4, 5, 6, 7));
+          o[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, bop, o[t], 0, 0, 0);
           if ((t & 3) == 3) __builtin_amdgcn_sched_barrier(0);  // bound the operand loads in flight
         }
       }
     }
+    // ---- stage K of tile kt+2 and V of tile kt+1 (their buffers were last read before
+    // the previous barrier), then issue the loads of K(kt+3) and V(kt+2)
+    // (unconditional: past the last tile the pieces are zeros and those buffers are never
+    // read; a conditional stage would leave a path on which the compiler makes the loads
+    // below wait for the ones issued just before them)
+    const int4 phys_n3 = tile_phys(p, b, key0 + 3 * KT, kv_len, s_phys, nlb);
+    stage_pieces<D, Smem<D>::kLdK>(Kbuf(cb), rk, tid);
+    stage_pieces<D, Smem<D>::kLdV>(Vbuf(cb ^ 1), rv, tid);
+    load_pieces<D>(p, key0 + 3 * KT, kv_len, kb, phys_n3, ln, rk);
+    load_pieces<D>(p, key0 + 2 * KT, kv_len, vb, phys_n2, ln, rv);
     lds_barrier();
+#pragma unroll
+    for (int st = 0; st < KT / 16; ++st) s_cur[st] = s_nxt[st];
+    phys_cur = phys_n1;
+    phys_n1 = phys_n2;
+    phys_n2 = phys_n3;
   }
 
   if (!active) return;
@@ -400,6 +427,9 @@ extern "C" int qa_paged_attention_prefill(const void* query, int32_t q_dtype, in
   if (!attr_set) {
     hipError_t err = hipFuncSetAttribute(reinterpret_cast<const void*>(&prefill_kernel<256>), hipFuncAttributeMaxDynamicSharedMemorySize,
                                          Smem<256>::kBytes);
+    if (err == hipSuccess)
+      err = hipFuncSetAttribute(reinterpret_cast<const void*>(&prefill_kernel<128>), hipFuncAttributeMaxDynamicSharedMemorySize,
+                                Smem<128>::kBytes);
     if (err != hipSuccess) return fail("paged prefill: cannot reserve %d bytes of LDS: %s", Smem<256>::kBytes, hipGetErrorString(err));
     attr_set = true;
   }

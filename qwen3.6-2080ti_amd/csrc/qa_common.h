@@ -43,6 +43,11 @@ __device__ __forceinline__ float bf16_to_f32(bf16_t x) {
   return __uint_as_float(static_cast<uint32_t>(x) << 16);
 }
 
+// 64-bit integer min / max.  (HIP's min<int64_t>(x, int_constant) resolves to a
+// double-precision minnum with int <-> double conversions.)
+__device__ __forceinline__ int64_t min64(int64_t a, int64_t b) { return a < b ? a : b; }
+__device__ __forceinline__ int64_t max64(int64_t a, int64_t b) { return a > b ? a : b; }
+
 // Round-to-nearest-even float -> bfloat16: gfx950's v_cvt_pk_bf16_f32 (a NaN
 // stays a quiet NaN).
 __device__ __forceinline__ bf16_t f32_to_bf16(float f) {
