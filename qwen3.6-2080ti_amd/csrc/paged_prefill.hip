@@ -20,8 +20,9 @@
 // Pipeline: K and V tiles are double-buffered in LDS with K one tile ahead, so
 // iteration t issues the S products of tile t+1 next to the softmax of tile t
 // (MFMA and VALU work of one wave overlap), then the PV products of tile t,
-// then stages K of tile t+2 and V of tile t+1 from registers and issues the
-// loads of K(t+3) and V(t+2), with one barrier per tile.  The row's block table is read into LDS once; global loads are
+// with K of tile t+2 and V of tile t+1 staged from registers at the start of the
+// iteration and the loads of K(t+3) and V(t+2) issued during it; one barrier per
+// tile.  The row's block table is read into LDS once; global loads are
 // issued a tile ahead into registers and barriers order LDS only, so those
 // loads stay in flight across them.
 #include "qa_common.h"
@@ -137,6 +138,18 @@ __device__ __forceinline__ int4 tile_phys(const Params& p, int b, int64_t key0, 
 template <int D>
 __device__ __forceinline__ void load_pieces(const Params& p, int64_t key0, int64_t kv_len, const bf16_t* base, const int4& phys,
                                             const TileLanes<D>& ln, TileRegs<D>& r) {
+  // A tile whose keys all lie below kv_len in present blocks (all but the last tiles of a
+  // row): unpredicated loads from the block's address (scalar) plus the piece offset.
+  // (D = 256: piece j of every thread lies in block j of the tile)
+  if (D == 256 && key0 + KT <= kv_len && phys.x >= 0 && phys.y >= 0 && phys.z >= 0 && phys.w >= 0) {
+    static_assert(D != 256 || NT / (D / 8) == BS, "one step of pieces is one block");
+#pragma unroll
+    for (int j = 0; j < TileRegs<D>::KP; ++j) {
+      const char* bp = reinterpret_cast<const char*>(base + static_cast<int64_t>(pick(phys, j)) * p.sP);
+      r.k[j] = *reinterpret_cast<const u32x4_v*>(bp + 2u * static_cast<uint32_t>(ln.koff[j]));
+    }
+    return;
+  }
 #pragma unroll
   for (int j = 0; j < TileRegs<D>::KP; ++j) {
     const int blk = pick(phys, ln.kblk[j]);
@@ -261,11 +274,23 @@ __global__ __launch_bounds__(NT) void prefill_kernel(Params p) {
   load_pieces<D>(p, KT, kv_len, vb, phys_n1, ln, rv);
   floatx4_v s_cur[KT / 16];
   if (active) scores(Kbuf(0), s_cur);
+  lds_barrier();  // every wave has read K(0) before iteration 0 stages K(2) over it
 
   for (int64_t kt = 0; kt < ntiles; ++kt) {
     const int64_t key0 = kt * KT;
     const int cb = static_cast<int>(kt & 1);
+    // ---- stage K of tile kt+2 and V of tile kt+1 (loaded during the previous iteration;
+    // their buffers were last read before the previous barrier).  Unconditional: past the
+    // last tile the pieces are zeros and those buffers are never read, and a conditional
+    // stage would leave a path on which the compiler makes later loads wait for earlier ones.
+    stage_pieces<D, Smem<D>::kLdK>(Kbuf(cb), rk, tid);
+    stage_pieces<D, Smem<D>::kLdV>(Vbuf(cb ^ 1), rv, tid);
+    const int4 phys_n3 = tile_phys(p, b, key0 + 3 * KT, kv_len, s_phys, nlb);
+    // the loads of K(kt+3) go out now and those of V(kt+2) after the S products, so their
+    // issue overlaps this iteration's work
+    load_pieces<D>(p, key0 + 3 * KT, kv_len, kb, phys_n3, ln, rk);
     floatx4_v s_nxt[KT / 16];
+    short4_v pb[KT / 16];  // this tile's probabilities, bf16, in the S^T accumulator layout
     if (active) {
       // ---- S of the next tile (MFMA) next to the softmax of this one (VALU)
       if (kt + 1 < ntiles) scores(Kbuf(cb ^ 1), s_nxt);
@@ -294,7 +319,6 @@ __global__ __launch_bounds__(NT) void prefill_kernel(Params p) {
       const float m_use = m_new == -INFINITY ? 0.f : m_new;
       const float alpha = __builtin_amdgcn_exp2f(m_run - m_use);
       m_run = m_new;
-      short4_v pb[KT / 16];
       float psum = 0.f;
 #pragma unroll
       for (int st = 0; st < KT / 16; ++st)
@@ -310,6 +334,9 @@ __global__ __launch_bounds__(NT) void prefill_kernel(Params p) {
 #pragma unroll
         for (int t = 0; t < MT; ++t) o[t] *= alpha;
       }
+    }
+    load_pieces<D>(p, key0 + 2 * KT, kv_len, vb, phys_n2, ln, rv);
+    if (active) {
       // ---- O^T += V^T P, 32 keys per v_mfma_f32_16x16x32_bf16: the reduction index
       // k = 8 (l/16) + e of lane l stands for key 4 (l/16) + e of sub-tile 2j (e < 4)
       // and of sub-tile 2j + 1 (e >= 4), so the B operand is the lane's own P of the
@@ -328,16 +355,6 @@ __global__ __launch_bounds__(NT) void prefill_kernel(Params p) {
         }
       }
     }
-    // ---- stage K of tile kt+2 and V of tile kt+1 (their buffers were last read before
-    // the previous barrier), then issue the loads of K(kt+3) and V(kt+2)
-    // (unconditional: past the last tile the pieces are zeros and those buffers are never
-    // read; a conditional stage would leave a path on which the compiler makes the loads
-    // below wait for the ones issued just before them)
-    const int4 phys_n3 = tile_phys(p, b, key0 + 3 * KT, kv_len, s_phys, nlb);
-    stage_pieces<D, Smem<D>::kLdK>(Kbuf(cb), rk, tid);
-    stage_pieces<D, Smem<D>::kLdV>(Vbuf(cb ^ 1), rv, tid);
-    load_pieces<D>(p, key0 + 3 * KT, kv_len, kb, phys_n3, ln, rk);
-    load_pieces<D>(p, key0 + 2 * KT, kv_len, vb, phys_n2, ln, rv);
     lds_barrier();
 #pragma unroll
     for (int st = 0; st < KT / 16; ++st) s_cur[st] = s_nxt[st];
