@@ -38,9 +38,9 @@ HBM_PEAK_GBS = 8000.0  # MI355X HBM3E, GB/s
 # profiles/paged_prefill_config3.md): FETCH_SIZE scaled by 2.0 and WRITE_SIZE by 1.0, the factors
 # a plain 1 GiB device copy reads back in the same runs. Counters need rocprofv3, so the figures
 # are the committed profile's, not measured live.
-TRAFFIC_DECODE = 1959162882
-TRAFFIC_DELTA = 2172775376
-TRAFFIC_PREFILL = 891747373  # average over the eight per-chunk launches
+TRAFFIC_DECODE = 1959219777
+TRAFFIC_DELTA = 1635882244
+TRAFFIC_PREFILL = 889788105  # average over the eight per-chunk launches
 MFMA_BF16_PEAK_TFLOPS = 2500.0  # MI355X dense bf16/fp16 MFMA, TFLOP/s
 
 
