@@ -491,8 +491,12 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(2, 2))) void
 
   for (int64_t ci = 0; ci < p.nch; ++ci) {
     const int64_t t0 = ci * CH;
-    // The lane index is re-derived opaquely each chunk so the per-lane LDS addresses below are
-    // recomputed inside the loop instead of being hoisted and held in VGPRs across it.
+    // The lane index is re-derived opaquely each chunk, so the per-lane LDS addresses of the
+    // loop body are recomputed in it rather than hoisted out and held in VGPRs across it.
+    int lane = tid & 63;
+    asm volatile("" : "+v"(lane));
+    const int lq = lane >> 4;
+    const int lc = lane & 15;
 
     // ---------------- stage this chunk's tiles; the next chunk's loads go out
     {
@@ -519,120 +523,168 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(2, 2))) void
     nx = load_chunk(p, b, j, qh, half_id, min(ci + 1, p.nch - 1), tid);
     lds_barrier();
 
-    // ---------------- A = beta_i exp(G_i - G_l) K K^T (strictly lower).  The tile is
-    // computed as (K_l K_i^T), so lane (lq, lc) holds A[16 ti + lc][16 tl + 4 lq + r]: the
-    // A-operand layout of the 16x16x16 products that consume it.  Diagonal blocks are kept
-    // fp32 for the solve; off-diagonal blocks are split once into fp16 hi + lo here.
-    for (int tile = wave; tile < 16; tile += NW) {
-      const int ti = tile >> 2;
-      const int tl = tile & 3;
-      if (tl > ti) continue;
-      const int i = 16 * ti + lc;
-      const float bi = s_beta[i];
-      const float gi = s_G[i];
-      const cfloat4 gl = *reinterpret_cast<const cfloat4*>(s_G + 16 * tl + 4 * lq);
-      cfloat4 acc = {0.f, 0.f, 0.f, 0.f};
-      acc = mma<DK>(Ks + 16 * tl * LD128, LD128, Ks + 16 * ti * LD128, LD128, acc, lane);
-      cfloat4 a;
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const float e = bi * __expf(gi - gl[r]) * acc[r];
-        a[r] = 16 * tl + 4 * lq + r < i ? e : 0.f;
-      }
-      if (ti == tl) {
-        *reinterpret_cast<cfloat4*>(Adg + (16 * ti + lc) * LDB + 4 * lq) = a;
-      } else {
-        h4_v hi, lo;
-        split4(a, hi, lo);
-        h4_v* dst = reinterpret_cast<h4_v*>(Ahl + (ti * (ti - 1) / 2 + tl) * 1024 + 16 * lane);
-        dst[0] = hi;
-        dst[1] = lo;
-      }
-    }
-    lds_barrier();
-
-    // ---------------- wave 0: diagonal 16x16 blocks of T = (I + A)^-1 by column
-    // forward substitution in registers (lane = block qb, column c; x_i final
-    // once every x_l, l < i, has been subtracted); the other waves: Aqk.
-    if (wave == 0) {
-      const int qb = lane >> 4;
-      const int c = lane & 15;
-      const float* ab = Adg + (16 * qb) * LDB;
-      // the sub-diagonal entries of this lane's block are read 16 bytes at a time ahead of
-      // the substitution, in two batches of rows (1..10, 11..15), so it does not wait on LDS
-      // row by row
-      float x[16];
-      cfloat4 arow[16][4];
-#pragma unroll
-      for (int i = 1; i <= 10; ++i)
-#pragma unroll
-        for (int q = 0; q < 4; ++q)
-          if (4 * q < i) arow[i][q] = *reinterpret_cast<const cfloat4*>(ab + i * LDB + 4 * q);
-      __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-      for (int i = 0; i <= 10; ++i) {
-        float v = i == c ? 1.f : 0.f;
-#pragma unroll
-        for (int l = 0; l < i; ++l) v -= arow[i][l >> 2][l & 3] * x[l];
-        x[i] = v;
-      }
-#pragma unroll
-      for (int i = 11; i < 16; ++i)
-#pragma unroll
-        for (int q = 0; q < 4; ++q)
-          if (4 * q < i) arow[i][q] = *reinterpret_cast<const cfloat4*>(ab + i * LDB + 4 * q);
-      __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-      for (int i = 11; i < 16; ++i) {
-        float v = i == c ? 1.f : 0.f;
-#pragma unroll
-        for (int l = 0; l < i; ++l) v -= arow[i][l >> 2][l & 3] * x[l];
-        x[i] = v;
-      }
-#pragma unroll
-      for (int i = 0; i < 16; ++i) Tb[(16 * qb + i) * LDB + c] = x[i];
-    } else {
-      // Aqk[i][l] = exp(G_i - G_l) (q_i . k_l), l <= i, computed as (K Q^T)[l][i], for
-      // the ten tiles with tl <= ti (the others stay zero from the start)
-      for (int n = wave - 1; n < 10; n += NW - 1) {
-        const int ti = n < 1 ? 0 : n < 3 ? 1 : n < 6 ? 2 : 3;
-        const int tl = n - ti * (ti + 1) / 2;
-        const int i = 16 * ti + lc;
+    // ---------------- phase 1 (everything that needs only this chunk's inputs and S0)
+    //  waves 0..3 (w): the diagonal block A_ww and D_w = (I + A_ww)^-1, then
+    //    R = diag(beta) (V - diag(gamma) K S0) for dv tile w (all four token blocks), kept in
+    //    registers for the substitution;
+    //  waves 4..7: the six off-diagonal blocks of A (split once into fp16 hi + lo), the ten
+    //    lower tiles of Aqk, and gamma * (S0^T Q^T) for the output tiles they own
+    //    (dv tile w - 4, token tiles 0..3).
+    // A = beta_i exp(G_i - G_l) K K^T (strictly lower) is computed as (K_l K_i^T), so lane
+    // (lq, lc) holds A[16 ti + lc][16 tl + 4 lq + r]: the A-operand layout of the 16x16x16
+    // products that consume it.
+    cfloat4 R[4];  // waves 0..3: R tiles (token block p, dv tile wave), C layout
+    cfloat4 O[4];  // waves 4..7: O^T tiles (dv tile wave - 4, token tile t), C layout
+    if (wave < 4) {
+      const int pb = wave;
+      {
+        const int i = 16 * pb + lc;
+        const float bi = s_beta[i];
         const float gi = s_G[i];
-        const cfloat4 gl = *reinterpret_cast<const cfloat4*>(s_G + 16 * tl + 4 * lq);
+        const cfloat4 gl = *reinterpret_cast<const cfloat4*>(s_G + 16 * pb + 4 * lq);
         cfloat4 acc = {0.f, 0.f, 0.f, 0.f};
-        acc = mma<DK>(Ks + 16 * tl * LD128, LD128, Qs + 16 * ti * LD128, LD128, acc, lane);
-        float v[4];
+        acc = mma<DK>(Ks + 16 * pb * LD128, LD128, Ks + 16 * pb * LD128, LD128, acc, lane);
+        cfloat4 a;
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-          const float e = __expf(gi - gl[r]) * acc[r];
-          v[r] = 16 * tl + 4 * lq + r <= i ? e : 0.f;
+          const float e = bi * __expf(gi - gl[r]) * acc[r];
+          a[r] = 4 * lq + r < lc ? e : 0.f;
         }
-        store4h(Aqk + i * LD64 + 16 * tl + 4 * lq, v[0], v[1], v[2], v[3]);
+        *reinterpret_cast<cfloat4*>(Adg + (16 * pb + lc) * LDB + 4 * lq) = a;
       }
-    }
-    // O^T tiles (dv tile td, token tiles tt0 + s) = gamma * (S0^T Q^T); this wave's
-    // output and delta tiles are (wave / 2, 2 (wave % 2) + s), s = 0, 1
-    const int td = wave >> 1;
-    const int tt0 = 2 * (wave & 1);
-    cfloat4 O[2] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
-    {
-      const float gam0 = s_gam[16 * tt0 + lc];
-      const float gam1 = s_gam[16 * tt0 + 16 + lc];
-      mma2<DK>(St + 16 * td * LD128, LD128, Qs + 16 * tt0 * LD128, Qs + 16 * (tt0 + 1) * LD128, LD128, O[0], O[1], lane);
-      O[0] *= gam0;
-      O[1] *= gam1;
+      // D_pb by column forward substitution (lane column lc; the four lane groups repeat it).
+      // The block was written by this wave just above, and one wave's LDS accesses are
+      // performed in order, so no barrier is needed.  Rows are read 16 bytes at a time
+      // ahead of the substitution, in two batches (rows 1..10, 11..15).
+      {
+        const int c = lc;
+        const float* ab = Adg + (16 * pb) * LDB;
+        float x[16];
+        cfloat4 arow[16][4];
+#pragma unroll
+        for (int i = 1; i <= 10; ++i)
+#pragma unroll
+          for (int q = 0; q < 4; ++q)
+            if (4 * q < i) arow[i][q] = *reinterpret_cast<const cfloat4*>(ab + i * LDB + 4 * q);
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int i = 0; i <= 10; ++i) {
+          float v = i == c ? 1.f : 0.f;
+#pragma unroll
+          for (int l = 0; l < i; ++l) v -= arow[i][l >> 2][l & 3] * x[l];
+          x[i] = v;
+        }
+#pragma unroll
+        for (int i = 11; i < 16; ++i)
+#pragma unroll
+          for (int q = 0; q < 4; ++q)
+            if (4 * q < i) arow[i][q] = *reinterpret_cast<const cfloat4*>(ab + i * LDB + 4 * q);
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int i = 11; i < 16; ++i) {
+          float v = i == c ? 1.f : 0.f;
+#pragma unroll
+          for (int l = 0; l < i; ++l) v -= arow[i][l >> 2][l & 3] * x[l];
+          x[i] = v;
+        }
+        if (lq == 0) {
+#pragma unroll
+          for (int i = 0; i < 16; ++i) Tb[(16 * pb + i) * LDB + c] = x[i];
+        }
+      }
+      // R for dv tile wave: K S0 (the S0 operand rows are shared by the four token blocks)
+      {
+        const int dvt = wave;
+        f16x8_v sb[DK / 32];
+#pragma unroll
+        for (int k = 0; k < DK / 32; ++k) sb[k] = *reinterpret_cast<const f16x8_v*>(St + (16 * dvt + lc) * LD128 + 32 * k + 8 * lq);
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+          f16x8_v ka[DK / 32];
+#pragma unroll
+          for (int k = 0; k < DK / 32; ++k) ka[k] = *reinterpret_cast<const f16x8_v*>(Ks + (16 * t + lc) * LD128 + 32 * k + 8 * lq);
+          const h4_v v4 = tr_read(Vs, LD64, 16 * t + 4 * lq, 16 * dvt, lane);
+          const cfloat4 bt = *reinterpret_cast<const cfloat4*>(s_beta + 16 * t + 4 * lq);
+          const cfloat4 gm = *reinterpret_cast<const cfloat4*>(s_gam + 16 * t + 4 * lq);
+          __builtin_amdgcn_sched_barrier(0);
+          cfloat4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+          for (int k = 0; k < DK / 32; ++k) acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(ka[k], sb[k], acc, 0, 0, 0);
+#pragma unroll
+          for (int r = 0; r < 4; ++r) R[t][r] = bt[r] * __builtin_fmaf(-gm[r], acc[r], static_cast<float>(v4[r]));
+        }
+      }
+    } else {
+      const int w4 = wave - 4;
+      // tiles n = w4, w4 + 4, w4 + 8, w4 + 12 of: six off-diagonal A blocks, then the ten
+      // lower Aqk tiles
+#pragma unroll
+      for (int m = 0; m < 4; ++m) {
+        const int n = w4 + 4 * m;
+        if (n < 6) {
+          const int ti = n < 1 ? 1 : n < 3 ? 2 : 3;
+          const int tl = n - ti * (ti - 1) / 2;
+          const int i = 16 * ti + lc;
+          const float bi = s_beta[i];
+          const float gi = s_G[i];
+          const cfloat4 gl = *reinterpret_cast<const cfloat4*>(s_G + 16 * tl + 4 * lq);
+          cfloat4 acc = {0.f, 0.f, 0.f, 0.f};
+          acc = mma<DK>(Ks + 16 * tl * LD128, LD128, Ks + 16 * ti * LD128, LD128, acc, lane);
+          cfloat4 a;
+#pragma unroll
+          for (int r = 0; r < 4; ++r) a[r] = bi * __expf(gi - gl[r]) * acc[r];
+          h4_v hi, lo;
+          split4(a, hi, lo);
+          h4_v* dst = reinterpret_cast<h4_v*>(Ahl + n * 1024 + 16 * lane);
+          dst[0] = hi;
+          dst[1] = lo;
+        } else {
+          // Aqk[i][l] = exp(G_i - G_l) (q_i . k_l), l <= i, computed as (K Q^T)[l][i]
+          const int na = n - 6;
+          const int ti = na < 1 ? 0 : na < 3 ? 1 : na < 6 ? 2 : 3;
+          const int tl = na - ti * (ti + 1) / 2;
+          const int i = 16 * ti + lc;
+          const float gi = s_G[i];
+          const cfloat4 gl = *reinterpret_cast<const cfloat4*>(s_G + 16 * tl + 4 * lq);
+          cfloat4 acc = {0.f, 0.f, 0.f, 0.f};
+          acc = mma<DK>(Ks + 16 * tl * LD128, LD128, Qs + 16 * ti * LD128, LD128, acc, lane);
+          float v[4];
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const float e = __expf(gi - gl[r]) * acc[r];
+            v[r] = 16 * tl + 4 * lq + r <= i ? e : 0.f;
+          }
+          store4h(Aqk + i * LD64 + 16 * tl + 4 * lq, v[0], v[1], v[2], v[3]);
+        }
+      }
+      // O^T tiles (dv tile w4, token tiles t) = gamma * (S0^T Q^T), the S0 rows shared
+      {
+        f16x8_v sa[DK / 32];
+#pragma unroll
+        for (int k = 0; k < DK / 32; ++k) sa[k] = *reinterpret_cast<const f16x8_v*>(St + (16 * w4 + lc) * LD128 + 32 * k + 8 * lq);
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+          f16x8_v qb[DK / 32];
+#pragma unroll
+          for (int k = 0; k < DK / 32; ++k) qb[k] = *reinterpret_cast<const f16x8_v*>(Qs + (16 * t + lc) * LD128 + 32 * k + 8 * lq);
+          const float gam = s_gam[16 * t + lc];
+          __builtin_amdgcn_sched_barrier(0);
+          cfloat4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+          for (int k = 0; k < DK / 32; ++k) acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(sa[k], qb[k], acc, 0, 0, 0);
+          O[t] = acc * gam;
+        }
+      }
     }
     lds_barrier();
 
-    // ---------------- W = T diag(beta gamma) K and U = T diag(beta) V by blocked forward
-    // substitution: W_p = D_p (X_p - sum_{k<p} A_pk W_k) over the 16-token blocks p.
-    // Column tiles: 8 of X_W = beta gamma K (dk) and 4 of X_U = beta V (this dv half);
-    // wave w takes W tile w and, for w < 4, U tile w.  A_pk and D_p enter as fp16
-    // hi + lo A operands; R and W_p stay fp32 in registers and are split into
-    // hi + lo B operands (the 16x16 accumulator layout is the B-operand layout).
-    {
-      // A operands: lane l holds row l % 16, columns 4 (l / 16) + e of a 16x16 block
+    // ---------------- phase 2: (I + A) delta = R by blocked forward substitution over the
+    // 16-token blocks p, delta_p = D_p (R_p - sum_{k<p} A_pk delta_k), one chain per dv tile
+    // (waves 0..3).  A_pk and D_p enter as fp16 hi + lo A operands; R and delta stay fp32 in
+    // registers and are split into hi + lo B operands (the 16x16 accumulator layout is the
+    // B-operand layout).  delta^T and exp(G_C - G) delta^T go to LDS for phase 3.
+    if (wave < 4) {
+      const int dvt = wave;
       h4_v dh[4], dl[4];
 #pragma unroll
       for (int pb = 0; pb < 4; ++pb) split4(*reinterpret_cast<const cfloat4*>(Tb + (16 * pb + lc) * LDB + 4 * lq), dh[pb], dl[pb]);
@@ -643,103 +695,61 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(2, 2))) void
         ah[n] = src[0];
         al[n] = src[1];
       }
-
-      // the W tile and (waves 0..3) the U tile run their block chains interleaved
-      const bool has_u = wave < 4;
-      h4_v wh[4], wl[4], uh[4], ul[4];
+      const float gC = s_G[CH - 1];
+      h4_v xh[4], xl[4];
 #pragma unroll
       for (int pb = 0; pb < 4; ++pb) {
         const int i0 = 16 * pb + 4 * lq;
-        const h4_v xrw_ = tr_read(Ks, LD128, i0, 16 * wave, lane);
-        const h4_v xru_ = tr_read(Vs, LD64, i0, 16 * (wave & 3), lane);
-        cfloat4 accw = {0.f, 0.f, 0.f, 0.f};
-        cfloat4 accu = {0.f, 0.f, 0.f, 0.f};
+        cfloat4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int k = 0; k < pb; ++k) {
           const int n = pb * (pb - 1) / 2 + k;
-          accw = mma3(ah[n], al[n], wh[k], wl[k], accw);
-          if (has_u) accu = mma3(ah[n], al[n], uh[k], ul[k], accu);
+          acc = mma3(ah[n], al[n], xh[k], xl[k], acc);
         }
-        const cfloat4 bg = *reinterpret_cast<const cfloat4*>(s_bg + i0);
-        const cfloat4 bt = *reinterpret_cast<const cfloat4*>(s_beta + i0);
-        cfloat4 rw, ru;
+        const cfloat4 gi = *reinterpret_cast<const cfloat4*>(s_G + i0);
+        h4_v rh, rl;
+        split4(R[pb] - acc, rh, rl);
+        const cfloat4 zero = {0.f, 0.f, 0.f, 0.f};
+        const cfloat4 d = mma3(dh[pb], dl[pb], rh, rl, zero);
+        split4(d, xh[pb], xl[pb]);
+        const int dv = 16 * dvt + lc;
+        store4h(Dt + dv * LD64 + i0, d[0], d[1], d[2], d[3]);
+        float sc[4];
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          rw[e] = __builtin_fmaf(static_cast<float>(xrw_[e]), bg[e], -accw[e]);
-          ru[e] = __builtin_fmaf(static_cast<float>(xru_[e]), bt[e], -accu[e]);
-        }
-        h4_v rwh, rwl, ruh, rul;
-        split4(rw, rwh, rwl);
-        split4(ru, ruh, rul);
-        cfloat4 w = {0.f, 0.f, 0.f, 0.f};
-        cfloat4 u = {0.f, 0.f, 0.f, 0.f};
-        w = mma3(dh[pb], dl[pb], rwh, rwl, w);
-        if (has_u) u = mma3(dh[pb], dl[pb], ruh, rul, u);
-        split4(w, wh[pb], wl[pb]);
-        split4(u, uh[pb], ul[pb]);
-        // -W^T: the four tokens of this lane are contiguous in row dk = 16 wave + lc
-        *reinterpret_cast<h4_v*>(Wt + (16 * wave + lc) * LD64 + i0) = -wh[pb];
-        if (has_u) {
-#pragma unroll
-          for (int e = 0; e < 4; ++e) Ub[(i0 + e) * LDF + 16 * wave + lc] = u[e];
-        }
+        for (int r = 0; r < 4; ++r) sc[r] = __expf(gC - gi[r]) * d[r];
+        store4h(DDt + dv * LD64 + i0, sc[0], sc[1], sc[2], sc[3]);
       }
     }
     lds_barrier();
 
-    // ---------------- delta = U - W S0 for the tiles (token tile td, dv tiles tt0 + s);
-    // keep delta^T and exp(G_C - G) delta^T in LDS
-    {
-      const int ti = td;
-      const int i0 = 16 * ti + 4 * lq;
-      cfloat4 Dl[2];
+    // ---------------- phase 3: O^T += delta^T Aqk^T -> output (waves 4..7);
+    // S = gamma_C S + K^T (D delta) (every wave, dk tile = wave)
+    if (wave >= 4) {
+      const int td = wave - 4;
+      f16x8_v da[CH / 32];
 #pragma unroll
-      for (int s = 0; s < 2; ++s)
+      for (int k = 0; k < CH / 32; ++k) da[k] = *reinterpret_cast<const f16x8_v*>(Dt + (16 * td + lc) * LD64 + 32 * k + 8 * lq);
 #pragma unroll
-        for (int r = 0; r < 4; ++r) Dl[s][r] = Ub[(i0 + r) * LDF + 16 * (tt0 + s) + lc];
-      const float gC = s_G[CH - 1];
-      const cfloat4 gi = *reinterpret_cast<const cfloat4*>(s_G + i0);
-      f16x8_v wa[DK / 32], sb0[DK / 32], sb1[DK / 32];
+      for (int tt = 0; tt < 4; ++tt) {
+        f16x8_v ab2[CH / 32];
 #pragma unroll
-      for (int k = 0; k < DK / 32; ++k) {
-        wa[k] = tr_operand32(Wt, LD64, 32 * k, 16 * ti, lane);
-        sb0[k] = *reinterpret_cast<const f16x8_v*>(St + (16 * tt0 + lc) * LD128 + 32 * k + 8 * lq);
-        sb1[k] = *reinterpret_cast<const f16x8_v*>(St + (16 * tt0 + 16 + lc) * LD128 + 32 * k + 8 * lq);
-      }
-      __builtin_amdgcn_sched_barrier(0);
+        for (int k = 0; k < CH / 32; ++k) ab2[k] = *reinterpret_cast<const f16x8_v*>(Aqk + (16 * tt + lc) * LD64 + 32 * k + 8 * lq);
+        __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-      for (int k = 0; k < DK / 32; ++k) {
-        Dl[0] = __builtin_amdgcn_mfma_f32_16x16x32_f16(wa[k], sb0[k], Dl[0], 0, 0, 0);
-        Dl[1] = __builtin_amdgcn_mfma_f32_16x16x32_f16(wa[k], sb1[k], Dl[1], 0, 0, 0);
-      }
-      cfloat4 dec;
-#pragma unroll
-      for (int r = 0; r < 4; ++r) dec[r] = __expf(gC - gi[r]);
-#pragma unroll
-      for (int s = 0; s < 2; ++s) {
-        const int dv = 16 * (tt0 + s) + lc;
-        store4h(Dt + dv * LD64 + i0, Dl[s][0], Dl[s][1], Dl[s][2], Dl[s][3]);
-        store4h(DDt + dv * LD64 + i0, dec[0] * Dl[s][0], dec[1] * Dl[s][1], dec[2] * Dl[s][2], dec[3] * Dl[s][3]);
-      }
-    }
-    lds_barrier();
-
-    // ---------------- O^T += delta^T Aqk^T -> output; S = gamma_C S + K^T (D delta)
-    mma2<CH>(Dt + 16 * td * LD64, LD64, Aqk + 16 * tt0 * LD64, Aqk + 16 * (tt0 + 1) * LD64, LD64, O[0], O[1], lane);
-#pragma unroll
-    for (int s = 0; s < 2; ++s) {
-      const int tok = 16 * (tt0 + s) + lc;
-      const int64_t tg = t0 + tok;
-      if (tg < p.T) {
-        const int64_t base = b * p.out_sb + tg * p.out_st + static_cast<int64_t>(j) * DV + half_id * DVS + 16 * td + 4 * lq;
-        if (p.out_dtype == QA_BF16) {
-          bf16_t* o = reinterpret_cast<bf16_t*>(p.out) + base;
-          uint2 packed;
-          packed.x = static_cast<uint32_t>(f32_to_bf16(O[s][0])) | (static_cast<uint32_t>(f32_to_bf16(O[s][1])) << 16);
-          packed.y = static_cast<uint32_t>(f32_to_bf16(O[s][2])) | (static_cast<uint32_t>(f32_to_bf16(O[s][3])) << 16);
-          *reinterpret_cast<uint2*>(o) = packed;
-        } else {
-          *reinterpret_cast<float4*>(reinterpret_cast<float*>(p.out) + base) = make_float4(O[s][0], O[s][1], O[s][2], O[s][3]);
+        for (int k = 0; k < CH / 32; ++k) O[tt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(da[k], ab2[k], O[tt], 0, 0, 0);
+        const int tok = 16 * tt + lc;
+        const int64_t tg = t0 + tok;
+        if (tg < p.T) {
+          const int64_t base = b * p.out_sb + tg * p.out_st + static_cast<int64_t>(j) * DV + half_id * DVS + 16 * td + 4 * lq;
+          if (p.out_dtype == QA_BF16) {
+            bf16_t* o = reinterpret_cast<bf16_t*>(p.out) + base;
+            uint2 packed;
+            packed.x = static_cast<uint32_t>(f32_to_bf16(O[tt][0])) | (static_cast<uint32_t>(f32_to_bf16(O[tt][1])) << 16);
+            packed.y = static_cast<uint32_t>(f32_to_bf16(O[tt][2])) | (static_cast<uint32_t>(f32_to_bf16(O[tt][3])) << 16);
+            *reinterpret_cast<uint2*>(o) = packed;
+          } else {
+            *reinterpret_cast<float4*>(reinterpret_cast<float*>(p.out) + base) = make_float4(O[tt][0], O[tt][1], O[tt][2], O[tt][3]);
+          }
         }
       }
     }
