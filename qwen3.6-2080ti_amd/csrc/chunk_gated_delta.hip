@@ -60,9 +60,8 @@ constexpr int DVS = 64;     // dv columns per workgroup
 constexpr int NW = 8;       // waves per workgroup
 constexpr int NT = NW * 64;
 constexpr int KCONV = 4;
-constexpr int LD128 = 136;  // padded leading dims (halfs) of 128- and 64-wide fp16 tiles
-constexpr int LD64 = 72;
-constexpr int LDF = 65;     // fp32 64x64 leading dim
+constexpr int LD128 = 144;  // padded leading dims (halfs) of 128- and 64-wide fp16 tiles: strides of 8 (mod 16)
+constexpr int LD64 = 80;   // dwords measured to give the fewest LDS bank conflicts (136 / 72 had twice as many)
 constexpr int RUN = 128;    // tokens one prep wave walks
 constexpr int PU = 8;       // tokens per prep step
 
@@ -87,29 +86,25 @@ inline Workspace workspace_layout(int64_t batch, int64_t seq, int64_t hk, int64_
   return w;
 }
 
-// ---- LDS layout of chunk_kernel (bytes)
+// ---- LDS layout of chunk_kernel (bytes).  Per chunk: Qs, Ks, Vs and the scalars are
+// staged first; phase 1 reads them and St and writes Adg, Tb, Ahl and Aqk; phase 2 reads
+// Tb and Ahl and writes Dt and DDt; phase 3 reads Dt, DDt, Aqk and Ks and writes St.
+// No two regions alias.
 constexpr int LDB = 20;                            // row stride (floats) of the 16x16 fp32 diagonal blocks
-constexpr int OFF_RA = 0;                          // Qs -> later Wt | Ub (Qs is dead once Aqk and Q S0 are built)
-constexpr int OFF_QS = OFF_RA;
-constexpr int OFF_WT = OFF_RA;                     // -W^T [dk][tok] fp16
-constexpr int OFF_UB = OFF_RA + DK * LD64 * 2;     // U [tok][dv] fp32
-constexpr int SZ_RA = DK * LD64 * 2 + CH * LDF * 4;  // 35072
-constexpr int OFF_RB = OFF_RA + SZ_RA;             // Adg | Tb | Ahl -> later Dt | DDt (dead once W, U are built)
-constexpr int OFF_ADG = OFF_RB;                    // diagonal 16x16 blocks of A, fp32 [block][row][LDB]
-constexpr int OFF_TB = OFF_ADG + 4 * 16 * LDB * 4; // D_p = (I + A_pp)^-1, fp32 [block][row][LDB]
-constexpr int OFF_AHL = OFF_TB + 4 * 16 * LDB * 4; // 6 off-diagonal blocks of A as fp16 hi | lo, one 16-byte A operand per lane
-constexpr int OFF_DT = OFF_RB;
-constexpr int OFF_DDT = OFF_DT + DVS * LD64 * 2;
-constexpr int SZ_RB = 2 * DVS * LD64 * 2;          // 18432
-constexpr int OFF_KS = OFF_RB + SZ_RB;             // Ks [tok][dk]
+constexpr int OFF_QS = 0;                          // Qs [tok][dk]
+constexpr int OFF_KS = OFF_QS + CH * LD128 * 2;    // Ks [tok][dk]
 constexpr int OFF_VS = OFF_KS + CH * LD128 * 2;    // Vs [tok][dv] (this workgroup's half)
 constexpr int OFF_ST = OFF_VS + CH * LD64 * 2;     // St [dv][dk] (fp16 state)
 constexpr int OFF_AQK = OFF_ST + DVS * LD128 * 2;  // Aqk [i][l]
-constexpr int OFF_SC = OFF_AQK + CH * LD64 * 2;    // beta, G, gamma, beta*gamma per token
+constexpr int OFF_ADG = OFF_AQK + CH * LD64 * 2;   // diagonal 16x16 blocks of A, fp32 [block][row][LDB]
+constexpr int OFF_TB = OFF_ADG + 4 * 16 * LDB * 4; // D_p = (I + A_pp)^-1, fp32 [block][row][LDB]
+constexpr int OFF_AHL = OFF_TB + 4 * 16 * LDB * 4; // 6 off-diagonal blocks of A as fp16 hi | lo, one 16-byte A operand per lane
+constexpr int OFF_DT = OFF_AHL + 6 * 64 * 16;      // delta^T [dv][tok]
+constexpr int OFF_DDT = OFF_DT + DVS * LD64 * 2;   // exp(G_C - G) delta^T [dv][tok]
+constexpr int OFF_SC = OFF_DDT + DVS * LD64 * 2;   // beta, G, gamma, beta*gamma per token
 constexpr int LDS_BYTES = OFF_SC + 4 * CH * 4;
 
-static_assert(CH * LD128 * 2 <= SZ_RA, "RA too small for Qs");
-static_assert(OFF_AHL + 6 * 64 * 16 <= OFF_RB + SZ_RB, "RB too small for Adg|Tb|Ahl");
+static_assert(OFF_ADG % 16 == 0 && OFF_DT % 16 == 0 && OFF_SC % 16 == 0, "16-byte aligned regions");
 static_assert(LDS_BYTES <= 160 * 1024, "LDS budget");
 
 struct PrepParams {
@@ -445,8 +440,6 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(2, 2))) void
   float* Adg = reinterpret_cast<float*>(smem + OFF_ADG);
   float* Tb = reinterpret_cast<float*>(smem + OFF_TB);
   unsigned char* Ahl = smem + OFF_AHL;
-  half_t* Wt = reinterpret_cast<half_t*>(smem + OFF_WT);
-  float* Ub = reinterpret_cast<float*>(smem + OFF_UB);
   half_t* Dt = reinterpret_cast<half_t*>(smem + OFF_DT);
   half_t* DDt = reinterpret_cast<half_t*>(smem + OFF_DDT);
   half_t* Vs = reinterpret_cast<half_t*>(smem + OFF_VS);
@@ -554,39 +547,25 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(2, 2))) void
       }
       // D_pb by column forward substitution (lane column lc; the four lane groups repeat it).
       // The block was written by this wave just above, and one wave's LDS accesses are
-      // performed in order, so no barrier is needed.  Rows are read 16 bytes at a time
-      // ahead of the substitution, in two batches (rows 1..10, 11..15).
+      // performed in order, so no barrier is needed.  All 120 sub-diagonal entries are read
+      // (16 bytes at a time) first; the updates then run column by column, so each step has
+      // 15 - l independent FMAs (each x[i] still accumulates its terms in the order l = 0, 1, ...).
       {
         const int c = lc;
         const float* ab = Adg + (16 * pb) * LDB;
-        float x[16];
         cfloat4 arow[16][4];
 #pragma unroll
-        for (int i = 1; i <= 10; ++i)
+        for (int i = 1; i < 16; ++i)
 #pragma unroll
           for (int q = 0; q < 4; ++q)
             if (4 * q < i) arow[i][q] = *reinterpret_cast<const cfloat4*>(ab + i * LDB + 4 * q);
-        __builtin_amdgcn_sched_barrier(0);
+        float x[16];
 #pragma unroll
-        for (int i = 0; i <= 10; ++i) {
-          float v = i == c ? 1.f : 0.f;
+        for (int i = 0; i < 16; ++i) x[i] = i == c ? 1.f : 0.f;
 #pragma unroll
-          for (int l = 0; l < i; ++l) v -= arow[i][l >> 2][l & 3] * x[l];
-          x[i] = v;
-        }
+        for (int l = 0; l < 15; ++l)
 #pragma unroll
-        for (int i = 11; i < 16; ++i)
-#pragma unroll
-          for (int q = 0; q < 4; ++q)
-            if (4 * q < i) arow[i][q] = *reinterpret_cast<const cfloat4*>(ab + i * LDB + 4 * q);
-        __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-        for (int i = 11; i < 16; ++i) {
-          float v = i == c ? 1.f : 0.f;
-#pragma unroll
-          for (int l = 0; l < i; ++l) v -= arow[i][l >> 2][l & 3] * x[l];
-          x[i] = v;
-        }
+          for (int i = l + 1; i < 16; ++i) x[i] = __builtin_fmaf(-arow[i][l >> 2][l & 3], x[l], x[i]);
         if (lq == 0) {
 #pragma unroll
           for (int i = 0; i < 16; ++i) Tb[(16 * pb + i) * LDB + c] = x[i];
@@ -598,63 +577,91 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(2, 2))) void
         f16x8_v sb[DK / 32];
 #pragma unroll
         for (int k = 0; k < DK / 32; ++k) sb[k] = *reinterpret_cast<const f16x8_v*>(St + (16 * dvt + lc) * LD128 + 32 * k + 8 * lq);
+        f16x8_v ka[4][DK / 32];
+        h4_v v4[4];
+        cfloat4 bt[4], gm[4];
 #pragma unroll
         for (int t = 0; t < 4; ++t) {
-          f16x8_v ka[DK / 32];
 #pragma unroll
-          for (int k = 0; k < DK / 32; ++k) ka[k] = *reinterpret_cast<const f16x8_v*>(Ks + (16 * t + lc) * LD128 + 32 * k + 8 * lq);
-          const h4_v v4 = tr_read(Vs, LD64, 16 * t + 4 * lq, 16 * dvt, lane);
-          const cfloat4 bt = *reinterpret_cast<const cfloat4*>(s_beta + 16 * t + 4 * lq);
-          const cfloat4 gm = *reinterpret_cast<const cfloat4*>(s_gam + 16 * t + 4 * lq);
-          __builtin_amdgcn_sched_barrier(0);
-          cfloat4 acc = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-          for (int k = 0; k < DK / 32; ++k) acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(ka[k], sb[k], acc, 0, 0, 0);
-#pragma unroll
-          for (int r = 0; r < 4; ++r) R[t][r] = bt[r] * __builtin_fmaf(-gm[r], acc[r], static_cast<float>(v4[r]));
+          for (int k = 0; k < DK / 32; ++k) ka[t][k] = *reinterpret_cast<const f16x8_v*>(Ks + (16 * t + lc) * LD128 + 32 * k + 8 * lq);
+          v4[t] = tr_read(Vs, LD64, 16 * t + 4 * lq, 16 * dvt, lane);
+          bt[t] = *reinterpret_cast<const cfloat4*>(s_beta + 16 * t + 4 * lq);
+          gm[t] = *reinterpret_cast<const cfloat4*>(s_gam + 16 * t + 4 * lq);
         }
+        __builtin_amdgcn_sched_barrier(0);
+        cfloat4 acc[4];
+#pragma unroll
+        for (int t = 0; t < 4; ++t) acc[t] = cfloat4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int k = 0; k < DK / 32; ++k)
+#pragma unroll
+          for (int t = 0; t < 4; ++t) acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ka[t][k], sb[k], acc[t], 0, 0, 0);
+#pragma unroll
+        for (int t = 0; t < 4; ++t)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) R[t][r] = bt[t][r] * __builtin_fmaf(-gm[t][r], acc[t][r], static_cast<float>(v4[t][r]));
       }
     } else {
       const int w4 = wave - 4;
       // tiles n = w4, w4 + 4, w4 + 8, w4 + 12 of: six off-diagonal A blocks, then the ten
-      // lower Aqk tiles
+      // lower Aqk tiles.  Tile (ti, tl) is (K_tl X_ti^T) with X = K (A) or Q (Aqk); two tiles
+      // at a time, operands of both read before their products, for latency overlap.
 #pragma unroll
-      for (int m = 0; m < 4; ++m) {
-        const int n = w4 + 4 * m;
-        if (n < 6) {
-          const int ti = n < 1 ? 1 : n < 3 ? 2 : 3;
-          const int tl = n - ti * (ti - 1) / 2;
-          const int i = 16 * ti + lc;
-          const float bi = s_beta[i];
-          const float gi = s_G[i];
-          const cfloat4 gl = *reinterpret_cast<const cfloat4*>(s_G + 16 * tl + 4 * lq);
-          cfloat4 acc = {0.f, 0.f, 0.f, 0.f};
-          acc = mma<DK>(Ks + 16 * tl * LD128, LD128, Ks + 16 * ti * LD128, LD128, acc, lane);
-          cfloat4 a;
+      for (int m2 = 0; m2 < 4; m2 += 2) {
+        int ti[2], tl[2];
+        bool is_a[2];
 #pragma unroll
-          for (int r = 0; r < 4; ++r) a[r] = bi * __expf(gi - gl[r]) * acc[r];
-          h4_v hi, lo;
-          split4(a, hi, lo);
-          h4_v* dst = reinterpret_cast<h4_v*>(Ahl + n * 1024 + 16 * lane);
-          dst[0] = hi;
-          dst[1] = lo;
-        } else {
-          // Aqk[i][l] = exp(G_i - G_l) (q_i . k_l), l <= i, computed as (K Q^T)[l][i]
+        for (int u = 0; u < 2; ++u) {
+          const int n = w4 + 4 * (m2 + u);
+          is_a[u] = n < 6;
           const int na = n - 6;
-          const int ti = na < 1 ? 0 : na < 3 ? 1 : na < 6 ? 2 : 3;
-          const int tl = na - ti * (ti + 1) / 2;
-          const int i = 16 * ti + lc;
-          const float gi = s_G[i];
-          const cfloat4 gl = *reinterpret_cast<const cfloat4*>(s_G + 16 * tl + 4 * lq);
-          cfloat4 acc = {0.f, 0.f, 0.f, 0.f};
-          acc = mma<DK>(Ks + 16 * tl * LD128, LD128, Qs + 16 * ti * LD128, LD128, acc, lane);
-          float v[4];
+          ti[u] = is_a[u] ? (n < 1 ? 1 : n < 3 ? 2 : 3) : (na < 1 ? 0 : na < 3 ? 1 : na < 6 ? 2 : 3);
+          tl[u] = is_a[u] ? n - ti[u] * (ti[u] - 1) / 2 : na - ti[u] * (ti[u] + 1) / 2;
+        }
+        f16x8_v ka[2][DK / 32], xb[2][DK / 32];
+        float gi[2], bi[2];
+        cfloat4 gl[2];
 #pragma unroll
-          for (int r = 0; r < 4; ++r) {
-            const float e = __expf(gi - gl[r]) * acc[r];
-            v[r] = 16 * tl + 4 * lq + r <= i ? e : 0.f;
+        for (int u = 0; u < 2; ++u) {
+          const half_t* X = is_a[u] ? Ks : Qs;
+#pragma unroll
+          for (int k = 0; k < DK / 32; ++k) {
+            ka[u][k] = *reinterpret_cast<const f16x8_v*>(Ks + (16 * tl[u] + lc) * LD128 + 32 * k + 8 * lq);
+            xb[u][k] = *reinterpret_cast<const f16x8_v*>(X + (16 * ti[u] + lc) * LD128 + 32 * k + 8 * lq);
           }
-          store4h(Aqk + i * LD64 + 16 * tl + 4 * lq, v[0], v[1], v[2], v[3]);
+          gi[u] = s_G[16 * ti[u] + lc];
+          bi[u] = s_beta[16 * ti[u] + lc];
+          gl[u] = *reinterpret_cast<const cfloat4*>(s_G + 16 * tl[u] + 4 * lq);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        cfloat4 acc[2] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
+#pragma unroll
+        for (int k = 0; k < DK / 32; ++k)
+#pragma unroll
+          for (int u = 0; u < 2; ++u) acc[u] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ka[u][k], xb[u][k], acc[u], 0, 0, 0);
+#pragma unroll
+        for (int u = 0; u < 2; ++u) {
+          const int n = w4 + 4 * (m2 + u);
+          const int i = 16 * ti[u] + lc;
+          if (is_a[u]) {
+            cfloat4 a;
+#pragma unroll
+            for (int r = 0; r < 4; ++r) a[r] = bi[u] * __expf(gi[u] - gl[u][r]) * acc[u][r];
+            h4_v hi, lo;
+            split4(a, hi, lo);
+            h4_v* dst = reinterpret_cast<h4_v*>(Ahl + n * 1024 + 16 * lane);
+            dst[0] = hi;
+            dst[1] = lo;
+          } else {
+            // Aqk[i][l] = exp(G_i - G_l) (q_i . k_l), l <= i
+            float v[4];
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+              const float e = __expf(gi[u] - gl[u][r]) * acc[u][r];
+              v[r] = 16 * tl[u] + 4 * lq + r <= i ? e : 0.f;
+            }
+            store4h(Aqk + i * LD64 + 16 * tl[u] + 4 * lq, v[0], v[1], v[2], v[3]);
+          }
         }
       }
       // O^T tiles (dv tile w4, token tiles t) = gamma * (S0^T Q^T), the S0 rows shared
@@ -662,18 +669,23 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(2, 2))) void
         f16x8_v sa[DK / 32];
 #pragma unroll
         for (int k = 0; k < DK / 32; ++k) sa[k] = *reinterpret_cast<const f16x8_v*>(St + (16 * w4 + lc) * LD128 + 32 * k + 8 * lq);
+        f16x8_v qb[4][DK / 32];
+        float gam[4];
 #pragma unroll
         for (int t = 0; t < 4; ++t) {
-          f16x8_v qb[DK / 32];
 #pragma unroll
-          for (int k = 0; k < DK / 32; ++k) qb[k] = *reinterpret_cast<const f16x8_v*>(Qs + (16 * t + lc) * LD128 + 32 * k + 8 * lq);
-          const float gam = s_gam[16 * t + lc];
-          __builtin_amdgcn_sched_barrier(0);
-          cfloat4 acc = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-          for (int k = 0; k < DK / 32; ++k) acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(sa[k], qb[k], acc, 0, 0, 0);
-          O[t] = acc * gam;
+          for (int k = 0; k < DK / 32; ++k) qb[t][k] = *reinterpret_cast<const f16x8_v*>(Qs + (16 * t + lc) * LD128 + 32 * k + 8 * lq);
+          gam[t] = s_gam[16 * t + lc];
         }
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int t = 0; t < 4; ++t) O[t] = cfloat4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int k = 0; k < DK / 32; ++k)
+#pragma unroll
+          for (int t = 0; t < 4; ++t) O[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(sa[k], qb[t][k], O[t], 0, 0, 0);
+#pragma unroll
+        for (int t = 0; t < 4; ++t) O[t] *= gam[t];
       }
     }
     lds_barrier();
