@@ -87,8 +87,9 @@ inline Workspace workspace_layout(int64_t batch, int64_t seq, int64_t hk, int64_
 }
 
 // ---- LDS layout of chunk_kernel (bytes).  Per chunk: Qs, Ks, Vs and the scalars are
-// staged first; phase 1 reads them and St and writes Adg, Tb, Ahl and Aqk; phase 2 reads
-// Tb and Ahl and writes Dt and DDt; phase 3 reads Dt, DDt, Aqk and Ks and writes St.
+// staged first; phase 1 reads them and St and writes Adg, Tb and Ahl; phase 2 reads Tb,
+// Ahl, Qs, Ks and St and writes Dt, DDt and Aqk; phase 3 reads Dt, DDt, Aqk and Ks and
+// writes St.
 // No two regions alias.
 constexpr int LDB = 20;                            // row stride (floats) of the 16x16 fp32 diagonal blocks
 constexpr int OFF_QS = 0;                          // Qs [tok][dk]
@@ -433,6 +434,82 @@ __device__ __forceinline__ cfloat4 mma3(const h4_v& ah, const h4_v& al, const h4
   return __builtin_amdgcn_mfma_f32_16x16x16f16(al, bh, acc, 0, 0, 0);
 }
 
+// Two 16x16 tiles of X K^T over dk: lane (lq, lc) gets X[16 ti + lc] . K[16 tl + 4 lq + r]
+// (the row-i A-operand layout of the 16x16x16 products that consume A).  The operands of
+// both tiles are read before the first product, for latency overlap.
+__device__ __forceinline__ void tile_pair(const half_t* Ks, const half_t* X0, int ti0, int tl0, const half_t* X1, int ti1, int tl1,
+                                          cfloat4& a0, cfloat4& a1, int lq, int lc) {
+  f16x8_v k0[DK / 32], x0[DK / 32], k1[DK / 32], x1[DK / 32];
+#pragma unroll
+  for (int k = 0; k < DK / 32; ++k) {
+    k0[k] = *reinterpret_cast<const f16x8_v*>(Ks + (16 * tl0 + lc) * LD128 + 32 * k + 8 * lq);
+    x0[k] = *reinterpret_cast<const f16x8_v*>(X0 + (16 * ti0 + lc) * LD128 + 32 * k + 8 * lq);
+    k1[k] = *reinterpret_cast<const f16x8_v*>(Ks + (16 * tl1 + lc) * LD128 + 32 * k + 8 * lq);
+    x1[k] = *reinterpret_cast<const f16x8_v*>(X1 + (16 * ti1 + lc) * LD128 + 32 * k + 8 * lq);
+  }
+  __builtin_amdgcn_sched_barrier(0);
+  a0 = cfloat4{0.f, 0.f, 0.f, 0.f};
+  a1 = cfloat4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int k = 0; k < DK / 32; ++k) {
+    a0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(k0[k], x0[k], a0, 0, 0, 0);
+    a1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(k1[k], x1[k], a1, 0, 0, 0);
+  }
+}
+
+// v of lane S of each group of four lanes, to all four (DPP quad_perm [S, S, S, S])
+template <int S>
+__device__ __forceinline__ float quad_bcast(float v) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x55 * S, 0xf, 0xf, false));
+}
+__device__ __forceinline__ float quad_bcast(float v, int s) {
+  switch (s) {
+    case 0: return quad_bcast<0>(v);
+    case 1: return quad_bcast<1>(v);
+    case 2: return quad_bcast<2>(v);
+    default: return quad_bcast<3>(v);
+  }
+}
+
+// D = (I + A)^-1 for one 16x16 fp32 block A that is zero on and above the diagonal (row
+// stride LDB), by forward substitution of all 16 columns at once.  Lane L solves column
+// c = L / 4 for the rows i = g + 4 m (g = L % 4, m = 0..3); x_l reaches the other rows of
+// its column by a quad broadcast.  Step l updates the rows m >= l / 4 (for m = l / 4 the
+// rows i <= l multiply a zero of A and stay unchanged), so the 120 updates take 39 FMA
+// instructions.  Each x_i accumulates its terms in the order l = 0, 1, ..., i - 1.
+// D is written to db (row stride LDB).
+__device__ __forceinline__ void solve_unit_lower16(const float* ab, float* db, int lane) {
+  const int c = lane >> 2;
+  const int g = lane & 3;
+  cfloat4 arow[4][4];  // arow[m][q] = A[g + 4 m][4 q .. 4 q + 3], q <= m
+#pragma unroll
+  for (int m = 0; m < 4; ++m)
+#pragma unroll
+    for (int q = 0; q <= m; ++q) arow[m][q] = *reinterpret_cast<const cfloat4*>(ab + (g + 4 * m) * LDB + 4 * q);
+  float x[4];
+#pragma unroll
+  for (int m = 0; m < 4; ++m) x[m] = g + 4 * m == c ? 1.f : 0.f;
+#pragma unroll
+  for (int l = 0; l < 15; ++l) {
+    const float xl = quad_bcast(x[l >> 2], l & 3);
+#pragma unroll
+    for (int m = l >> 2; m < 4; ++m) x[m] = __builtin_fmaf(-arow[m][l >> 2][l & 3], xl, x[m]);
+  }
+#pragma unroll
+  for (int m = 0; m < 4; ++m) db[(g + 4 * m) * LDB + c] = x[m];
+}
+
+// (ti, tl) of the n-th strictly lower 16x16 block, n = 0..5: (1,0) (2,0) (2,1) (3,0) (3,1) (3,2)
+__device__ __forceinline__ void lower_block(int n, int& ti, int& tl) {
+  ti = n < 1 ? 1 : n < 3 ? 2 : 3;
+  tl = n - ti * (ti - 1) / 2;
+}
+// (ti, tl) of the n-th lower 16x16 block including the diagonal, n = 0..9
+__device__ __forceinline__ void lower_block_diag(int n, int& ti, int& tl) {
+  ti = n < 1 ? 0 : n < 3 ? 1 : n < 6 ? 2 : 3;
+  tl = n - ti * (ti + 1) / 2;
+}
+
 __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(2, 2))) void chunk_kernel(ChunkParams p) {
   extern __shared__ __align__(16) unsigned char smem[];
   half_t* Qs = reinterpret_cast<half_t*>(smem + OFF_QS);
@@ -516,18 +593,15 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(2, 2))) void
     nx = load_chunk(p, b, j, qh, half_id, min(ci + 1, p.nch - 1), tid);
     lds_barrier();
 
-    // ---------------- phase 1 (everything that needs only this chunk's inputs and S0)
-    //  waves 0..3 (w): the diagonal block A_ww and D_w = (I + A_ww)^-1, then
-    //    R = diag(beta) (V - diag(gamma) K S0) for dv tile w (all four token blocks), kept in
-    //    registers for the substitution;
-    //  waves 4..7: the six off-diagonal blocks of A (split once into fp16 hi + lo), the ten
-    //    lower tiles of Aqk, and gamma * (S0^T Q^T) for the output tiles they own
-    //    (dv tile w - 4, token tiles 0..3).
+    // ---------------- phase 1: what the substitution of phase 2 reads
+    //  waves 0..3 (w): the diagonal block A_ww and D_w = (I + A_ww)^-1 (to Tb);
+    //  waves 4..7 (w4 = wave - 4): R = diag(beta) (V - diag(gamma) K S0) for dv tile w4 (all
+    //    four token blocks), kept in registers for the same wave's substitution chain, then
+    //    the off-diagonal blocks n = w4 and w4 + 4 (< 6) of A, split once into fp16 hi + lo.
     // A = beta_i exp(G_i - G_l) K K^T (strictly lower) is computed as (K_l K_i^T), so lane
     // (lq, lc) holds A[16 ti + lc][16 tl + 4 lq + r]: the A-operand layout of the 16x16x16
     // products that consume it.
-    cfloat4 R[4];  // waves 0..3: R tiles (token block p, dv tile wave), C layout
-    cfloat4 O[4];  // waves 4..7: O^T tiles (dv tile wave - 4, token tile t), C layout
+    cfloat4 R[4];  // waves 4..7: R tiles (token block p, dv tile wave - 4), C layout
     if (wave < 4) {
       const int pb = wave;
       {
@@ -545,35 +619,14 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(2, 2))) void
         }
         *reinterpret_cast<cfloat4*>(Adg + (16 * pb + lc) * LDB + 4 * lq) = a;
       }
-      // D_pb by column forward substitution (lane column lc; the four lane groups repeat it).
-      // The block was written by this wave just above, and one wave's LDS accesses are
-      // performed in order, so no barrier is needed.  All 120 sub-diagonal entries are read
-      // (16 bytes at a time) first; the updates then run column by column, so each step has
-      // 15 - l independent FMAs (each x[i] still accumulates its terms in the order l = 0, 1, ...).
+      // D_pb.  The block was written by this wave just above, and one wave's LDS accesses
+      // are performed in order, so no barrier is needed.
+      solve_unit_lower16(Adg + (16 * pb) * LDB, Tb + (16 * pb) * LDB, lane);
+    } else {
+      const int w4 = wave - 4;
+      // R for dv tile w4: K S0 (the S0 operand rows are shared by the four token blocks)
       {
-        const int c = lc;
-        const float* ab = Adg + (16 * pb) * LDB;
-        cfloat4 arow[16][4];
-#pragma unroll
-        for (int i = 1; i < 16; ++i)
-#pragma unroll
-          for (int q = 0; q < 4; ++q)
-            if (4 * q < i) arow[i][q] = *reinterpret_cast<const cfloat4*>(ab + i * LDB + 4 * q);
-        float x[16];
-#pragma unroll
-        for (int i = 0; i < 16; ++i) x[i] = i == c ? 1.f : 0.f;
-#pragma unroll
-        for (int l = 0; l < 15; ++l)
-#pragma unroll
-          for (int i = l + 1; i < 16; ++i) x[i] = __builtin_fmaf(-arow[i][l >> 2][l & 3], x[l], x[i]);
-        if (lq == 0) {
-#pragma unroll
-          for (int i = 0; i < 16; ++i) Tb[(16 * pb + i) * LDB + c] = x[i];
-        }
-      }
-      // R for dv tile wave: K S0 (the S0 operand rows are shared by the four token blocks)
-      {
-        const int dvt = wave;
+        const int dvt = w4;
         f16x8_v sb[DK / 32];
 #pragma unroll
         for (int k = 0; k < DK / 32; ++k) sb[k] = *reinterpret_cast<const f16x8_v*>(St + (16 * dvt + lc) * LD128 + 32 * k + 8 * lq);
@@ -601,102 +654,46 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(2, 2))) void
 #pragma unroll
           for (int r = 0; r < 4; ++r) R[t][r] = bt[t][r] * __builtin_fmaf(-gm[t][r], acc[t][r], static_cast<float>(v4[t][r]));
       }
-    } else {
-      const int w4 = wave - 4;
-      // tiles n = w4, w4 + 4, w4 + 8, w4 + 12 of: six off-diagonal A blocks, then the ten
-      // lower Aqk tiles.  Tile (ti, tl) is (K_tl X_ti^T) with X = K (A) or Q (Aqk); two tiles
-      // at a time, operands of both read before their products, for latency overlap.
-#pragma unroll
-      for (int m2 = 0; m2 < 4; m2 += 2) {
+      {
         int ti[2], tl[2];
-        bool is_a[2];
+        lower_block(w4, ti[0], tl[0]);
+        lower_block(w4 + 4 < 6 ? w4 + 4 : w4, ti[1], tl[1]);  // waves 6, 7 own one block
+        cfloat4 acc[2];
+        tile_pair(Ks, Ks, ti[0], tl[0], Ks, ti[1], tl[1], acc[0], acc[1], lq, lc);
 #pragma unroll
         for (int u = 0; u < 2; ++u) {
-          const int n = w4 + 4 * (m2 + u);
-          is_a[u] = n < 6;
-          const int na = n - 6;
-          ti[u] = is_a[u] ? (n < 1 ? 1 : n < 3 ? 2 : 3) : (na < 1 ? 0 : na < 3 ? 1 : na < 6 ? 2 : 3);
-          tl[u] = is_a[u] ? n - ti[u] * (ti[u] - 1) / 2 : na - ti[u] * (ti[u] + 1) / 2;
-        }
-        f16x8_v ka[2][DK / 32], xb[2][DK / 32];
-        float gi[2], bi[2];
-        cfloat4 gl[2];
-#pragma unroll
-        for (int u = 0; u < 2; ++u) {
-          const half_t* X = is_a[u] ? Ks : Qs;
-#pragma unroll
-          for (int k = 0; k < DK / 32; ++k) {
-            ka[u][k] = *reinterpret_cast<const f16x8_v*>(Ks + (16 * tl[u] + lc) * LD128 + 32 * k + 8 * lq);
-            xb[u][k] = *reinterpret_cast<const f16x8_v*>(X + (16 * ti[u] + lc) * LD128 + 32 * k + 8 * lq);
-          }
-          gi[u] = s_G[16 * ti[u] + lc];
-          bi[u] = s_beta[16 * ti[u] + lc];
-          gl[u] = *reinterpret_cast<const cfloat4*>(s_G + 16 * tl[u] + 4 * lq);
-        }
-        __builtin_amdgcn_sched_barrier(0);
-        cfloat4 acc[2] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
-#pragma unroll
-        for (int k = 0; k < DK / 32; ++k)
-#pragma unroll
-          for (int u = 0; u < 2; ++u) acc[u] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ka[u][k], xb[u][k], acc[u], 0, 0, 0);
-#pragma unroll
-        for (int u = 0; u < 2; ++u) {
-          const int n = w4 + 4 * (m2 + u);
-          const int i = 16 * ti[u] + lc;
-          if (is_a[u]) {
+          const int n = w4 + 4 * u;
+          if (n < 6) {
+            const int i = 16 * ti[u] + lc;
+            const float gi = s_G[i];
+            const float bi = s_beta[i];
+            const cfloat4 gl = *reinterpret_cast<const cfloat4*>(s_G + 16 * tl[u] + 4 * lq);
             cfloat4 a;
 #pragma unroll
-            for (int r = 0; r < 4; ++r) a[r] = bi[u] * __expf(gi[u] - gl[u][r]) * acc[u][r];
+            for (int r = 0; r < 4; ++r) a[r] = bi * __expf(gi - gl[r]) * acc[u][r];
             h4_v hi, lo;
             split4(a, hi, lo);
             h4_v* dst = reinterpret_cast<h4_v*>(Ahl + n * 1024 + 16 * lane);
             dst[0] = hi;
             dst[1] = lo;
-          } else {
-            // Aqk[i][l] = exp(G_i - G_l) (q_i . k_l), l <= i
-            float v[4];
-#pragma unroll
-            for (int r = 0; r < 4; ++r) {
-              const float e = __expf(gi[u] - gl[u][r]) * acc[u][r];
-              v[r] = 16 * tl[u] + 4 * lq + r <= i ? e : 0.f;
-            }
-            store4h(Aqk + i * LD64 + 16 * tl[u] + 4 * lq, v[0], v[1], v[2], v[3]);
           }
         }
-      }
-      // O^T tiles (dv tile w4, token tiles t) = gamma * (S0^T Q^T), the S0 rows shared
-      {
-        f16x8_v sa[DK / 32];
-#pragma unroll
-        for (int k = 0; k < DK / 32; ++k) sa[k] = *reinterpret_cast<const f16x8_v*>(St + (16 * w4 + lc) * LD128 + 32 * k + 8 * lq);
-        f16x8_v qb[4][DK / 32];
-        float gam[4];
-#pragma unroll
-        for (int t = 0; t < 4; ++t) {
-#pragma unroll
-          for (int k = 0; k < DK / 32; ++k) qb[t][k] = *reinterpret_cast<const f16x8_v*>(Qs + (16 * t + lc) * LD128 + 32 * k + 8 * lq);
-          gam[t] = s_gam[16 * t + lc];
-        }
-        __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-        for (int t = 0; t < 4; ++t) O[t] = cfloat4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-        for (int k = 0; k < DK / 32; ++k)
-#pragma unroll
-          for (int t = 0; t < 4; ++t) O[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(sa[k], qb[t][k], O[t], 0, 0, 0);
-#pragma unroll
-        for (int t = 0; t < 4; ++t) O[t] *= gam[t];
       }
     }
     lds_barrier();
 
-    // ---------------- phase 2: (I + A) delta = R by blocked forward substitution over the
-    // 16-token blocks p, delta_p = D_p (R_p - sum_{k<p} A_pk delta_k), one chain per dv tile
-    // (waves 0..3).  A_pk and D_p enter as fp16 hi + lo A operands; R and delta stay fp32 in
-    // registers and are split into hi + lo B operands (the 16x16 accumulator layout is the
-    // B-operand layout).  delta^T and exp(G_C - G) delta^T go to LDS for phase 3.
-    if (wave < 4) {
-      const int dvt = wave;
+    // ---------------- phase 2
+    //  waves 4..7: (I + A) delta = R by blocked forward substitution over the 16-token blocks
+    //    p, delta_p = D_p (R_p - sum_{k<p} A_pk delta_k), one chain per dv tile.  A_pk and D_p
+    //    enter as fp16 hi + lo A operands; R and delta stay fp32 in registers and are split
+    //    into hi + lo B operands (the 16x16 accumulator layout is the B-operand layout).
+    //    delta^T and exp(G_C - G) delta^T go to LDS for phase 3.
+    //  waves 0..3 (w), alongside: the lower tiles n = w, w + 4, w + 8 (< 10) of
+    //    Aqk[i][l] = exp(G_i - G_l) (q_i . k_l), l <= i, and gamma * (S0^T Q^T) for the output
+    //    tiles they own in phase 3 (dv tile w, token tiles 0..3).
+    cfloat4 O[4];  // waves 0..3: O^T tiles (dv tile wave, token tile t), C layout
+    if (wave >= 4) {
+      const int dvt = wave - 4;
       h4_v dh[4], dl[4];
 #pragma unroll
       for (int pb = 0; pb < 4; ++pb) split4(*reinterpret_cast<const cfloat4*>(Tb + (16 * pb + lc) * LDB + 4 * lq), dh[pb], dl[pb]);
@@ -731,13 +728,62 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(2, 2))) void
         for (int r = 0; r < 4; ++r) sc[r] = __expf(gC - gi[r]) * d[r];
         store4h(DDt + dv * LD64 + i0, sc[0], sc[1], sc[2], sc[3]);
       }
+    } else {
+#pragma unroll
+      for (int m = 0; m < 2; ++m) {
+        if (m == 1 && wave >= 2) break;
+        int ti[2], tl[2];
+        const int n0 = wave + 8 * m;
+        const int n1 = m == 0 ? wave + 4 : n0;  // the third tile of waves 0, 1 is single
+        lower_block_diag(n0, ti[0], tl[0]);
+        lower_block_diag(n1, ti[1], tl[1]);
+        cfloat4 acc[2];
+        tile_pair(Ks, Qs, ti[0], tl[0], Qs, ti[1], tl[1], acc[0], acc[1], lq, lc);
+#pragma unroll
+        for (int u = 0; u < 2; ++u) {
+          if (u == 1 && m == 1) break;
+          const int i = 16 * ti[u] + lc;
+          const float gi = s_G[i];
+          const cfloat4 gl = *reinterpret_cast<const cfloat4*>(s_G + 16 * tl[u] + 4 * lq);
+          float v[4];
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const float e = __expf(gi - gl[r]) * acc[u][r];
+            v[r] = 16 * tl[u] + 4 * lq + r <= i ? e : 0.f;
+          }
+          store4h(Aqk + i * LD64 + 16 * tl[u] + 4 * lq, v[0], v[1], v[2], v[3]);
+        }
+      }
+      // O^T tiles (dv tile wave, token tiles t) = gamma * (S0^T Q^T), the S0 rows shared
+      {
+        f16x8_v sa[DK / 32];
+#pragma unroll
+        for (int k = 0; k < DK / 32; ++k) sa[k] = *reinterpret_cast<const f16x8_v*>(St + (16 * wave + lc) * LD128 + 32 * k + 8 * lq);
+        f16x8_v qb[4][DK / 32];
+        float gam[4];
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+#pragma unroll
+          for (int k = 0; k < DK / 32; ++k) qb[t][k] = *reinterpret_cast<const f16x8_v*>(Qs + (16 * t + lc) * LD128 + 32 * k + 8 * lq);
+          gam[t] = s_gam[16 * t + lc];
+        }
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int t = 0; t < 4; ++t) O[t] = cfloat4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int k = 0; k < DK / 32; ++k)
+#pragma unroll
+          for (int t = 0; t < 4; ++t) O[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(sa[k], qb[t][k], O[t], 0, 0, 0);
+#pragma unroll
+        for (int t = 0; t < 4; ++t) O[t] *= gam[t];
+      }
     }
     lds_barrier();
 
-    // ---------------- phase 3: O^T += delta^T Aqk^T -> output (waves 4..7);
+    // ---------------- phase 3: O^T += delta^T Aqk^T -> output (waves 0..3);
     // S = gamma_C S + K^T (D delta) (every wave, dk tile = wave)
-    if (wave >= 4) {
-      const int td = wave - 4;
+    if (wave < 4) {
+      const int td = wave;
       f16x8_v da[CH / 32];
 #pragma unroll
       for (int k = 0; k < CH / 32; ++k) da[k] = *reinterpret_cast<const f16x8_v*>(Dt + (16 * td + lc) * LD64 + 32 * k + 8 * lq);
