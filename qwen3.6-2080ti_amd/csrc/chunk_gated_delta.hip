@@ -88,22 +88,20 @@ inline Workspace workspace_layout(int64_t batch, int64_t seq, int64_t hk, int64_
 
 // ---- LDS layout of chunk_kernel (bytes).  Per chunk: Qs, Ks, Vs and the scalars are
 // staged first; phase 1 reads them and St and writes Adg, Tb and Ahl; phase 2 reads Tb,
-// Ahl, Qs, Ks and St and writes Dt, DDt and Aqk; phase 3 reads Dt, DDt, Aqk and Ks and
-// writes St.
+// Ahl, Qs, Ks and the scalars and writes Dt, Aqk and St; phase 3 reads Dt and Aqk.
 // No two regions alias.
 constexpr int LDB = 20;                            // row stride (floats) of the 16x16 fp32 diagonal blocks
 constexpr int OFF_QS = 0;                          // Qs [tok][dk]
 constexpr int OFF_KS = OFF_QS + CH * LD128 * 2;    // Ks [tok][dk]
 constexpr int OFF_VS = OFF_KS + CH * LD128 * 2;    // Vs [tok][dv] (this workgroup's half)
-constexpr int OFF_ST = OFF_VS + CH * LD64 * 2;     // St [dv][dk] (fp16 state)
+constexpr int OFF_ST = OFF_VS + CH * LD64 * 2;     // St [dv][dk] (fp16 copy of the state)
 constexpr int OFF_AQK = OFF_ST + DVS * LD128 * 2;  // Aqk [i][l]
 constexpr int OFF_ADG = OFF_AQK + CH * LD64 * 2;   // diagonal 16x16 blocks of A, fp32 [block][row][LDB]
 constexpr int OFF_TB = OFF_ADG + 4 * 16 * LDB * 4; // D_p = (I + A_pp)^-1, fp32 [block][row][LDB]
 constexpr int OFF_AHL = OFF_TB + 4 * 16 * LDB * 4; // 6 off-diagonal blocks of A as fp16 hi | lo, one 16-byte A operand per lane
 constexpr int OFF_DT = OFF_AHL + 6 * 64 * 16;      // delta^T [dv][tok]
-constexpr int OFF_DDT = OFF_DT + DVS * LD64 * 2;   // exp(G_C - G) delta^T [dv][tok]
-constexpr int OFF_SC = OFF_DDT + DVS * LD64 * 2;   // beta, G, gamma, beta*gamma per token
-constexpr int LDS_BYTES = OFF_SC + 4 * CH * 4;
+constexpr int OFF_SC = OFF_DT + DVS * LD64 * 2;    // beta, G, gamma per token
+constexpr int LDS_BYTES = OFF_SC + 3 * CH * 4;
 
 static_assert(OFF_ADG % 16 == 0 && OFF_DT % 16 == 0 && OFF_SC % 16 == 0, "16-byte aligned regions");
 static_assert(LDS_BYTES <= 160 * 1024, "LDS budget");
@@ -504,12 +502,73 @@ __device__ __forceinline__ void lower_block(int n, int& ti, int& tl) {
   ti = n < 1 ? 1 : n < 3 ? 2 : 3;
   tl = n - ti * (ti - 1) / 2;
 }
-// (ti, tl) of the n-th lower 16x16 block including the diagonal, n = 0..9
-__device__ __forceinline__ void lower_block_diag(int n, int& ti, int& tl) {
-  ti = n < 1 ? 0 : n < 3 ? 1 : n < 6 ? 2 : 3;
-  tl = n - ti * (ti + 1) / 2;
+// Row m of state tile d held by a key wave is dk_of(d, m): tiles 2 s and 2 s + 1 share
+// dk 32 s .. 32 s + 31, lane quad lq holding dk 32 s + 8 lq + 0..3 in tile 2 s and + 4..7 in
+// tile 2 s + 1, so that the eight values a lane holds for k-step s of K S0 are the eight
+// consecutive dk of a 16-byte K operand read.
+__device__ __forceinline__ constexpr int dk_of(int d, int m) { return 32 * (d >> 1) + 8 * (m >> 2) + 4 * (d & 1) + (m & 3); }
+
+// fp16 (a0..a3, b0..b3) as one 16x16x32 operand
+__device__ __forceinline__ f16x8_v pack8h(const cfloat4& a, const cfloat4& b) {
+  f16x8_v r;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    r[e] = static_cast<half_t>(a[e]);
+    r[4 + e] = static_cast<half_t>(b[e]);
+  }
+  return r;
 }
 
+// The 16x16x32 A operand of K^T for state tile d of a key wave: lane (g, j) gets
+// K[row_g + e][dk_of(d, j)] for e = 0..3 and K[row_g + 16 + e][dk_of(d, j)] for e = 4..7
+// (row_g = 32 s + 4 g).  With ds_read_b64_tr_b16, lane j of a 16-lane group receives element
+// j % 4 of the 8 bytes lane 4 e + j / 4 read; here lane i reads row row_g + i / 4 at column
+// dk_of(d, 4 (i % 4)), so lane j receives column dk_of(d, j).
+__device__ __forceinline__ f16x8_v ktr_operand(const half_t* Ks, int row_g, int d, int lane) {
+  typedef short s4_v __attribute__((ext_vector_type(4)));
+  typedef __attribute__((address_space(3))) s4_v lds_s4;
+  const int i = lane & 15;
+  const half_t* p0 = Ks + (row_g + (i >> 2)) * LD128 + dk_of(d, 4 * (i & 3));
+  const h4_v lo = __builtin_bit_cast(h4_v, __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s4*)p0));
+  const h4_v hi = __builtin_bit_cast(h4_v, __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s4*)(p0 + 16 * LD128)));
+  return __builtin_bit_cast(f16x8_v, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
+}
+
+// One chunk's tiles from the registers they were loaded into to LDS, and the next chunk's
+// loads issued; ends with the barrier after which the tiles may be read.
+__device__ __forceinline__ void stage_chunk(const ChunkParams& p, unsigned char* smem, ChunkRegs& nx, int64_t b, int j, int qh,
+                                            int half_id, int64_t ci, int tid) {
+  half_t* Qs = reinterpret_cast<half_t*>(smem + OFF_QS);
+  half_t* Ks = reinterpret_cast<half_t*>(smem + OFF_KS);
+  half_t* Vs = reinterpret_cast<half_t*>(smem + OFF_VS);
+  float* s_beta = reinterpret_cast<float*>(smem + OFF_SC);
+  float* s_G = s_beta + CH;
+  float* s_gam = s_G + CH;
+  const int c0 = tid, c1 = tid + NT;
+  *reinterpret_cast<u32x4*>(Qs + (c0 >> 4) * LD128 + 8 * (c0 & 15)) = nx.q0;
+  *reinterpret_cast<u32x4*>(Qs + (c1 >> 4) * LD128 + 8 * (c1 & 15)) = nx.q1;
+  *reinterpret_cast<u32x4*>(Ks + (c0 >> 4) * LD128 + 8 * (c0 & 15)) = nx.k0;
+  *reinterpret_cast<u32x4*>(Ks + (c1 >> 4) * LD128 + 8 * (c1 & 15)) = nx.k1;
+  *reinterpret_cast<u32x4*>(Vs + (tid >> 3) * LD64 + 8 * (tid & 7)) = nx.v;
+  if (tid < CH / 2) {
+    s_G[2 * tid] = nx.gb.x;
+    s_beta[2 * tid] = nx.gb.y;
+    s_G[2 * tid + 1] = nx.gb.z;
+    s_beta[2 * tid + 1] = nx.gb.w;
+    s_gam[2 * tid] = __expf(nx.gb.x);
+    s_gam[2 * tid + 1] = __expf(nx.gb.z);
+  }
+  // (the last chunk reloads itself rather than branching, so nx stays in registers)
+  nx = load_chunk(p, b, j, qh, half_id, min(ci + 1, p.nch - 1), tid);
+  lds_barrier();
+}
+
+// The workgroup's waves take two roles, each running its own chunk loop with the same
+// barriers (three per chunk), so the registers of one role are not held by the other:
+//  key waves 0..3 (v = wave): the fp32 state columns dv = 16 v + lc, all of K, R and the
+//    substitution chain for dv tile v, the off-diagonal blocks of A, the state update;
+//  query waves 4..7 (v = wave - 4): the diagonal block A_vv and its inverse, all of Q,
+//    gamma Q S0, Aqk, and the output tiles of dv tile v.
 __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(2, 2))) void chunk_kernel(ChunkParams p) {
   extern __shared__ __align__(16) unsigned char smem[];
   half_t* Qs = reinterpret_cast<half_t*>(smem + OFF_QS);
@@ -518,40 +577,25 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(2, 2))) void
   float* Tb = reinterpret_cast<float*>(smem + OFF_TB);
   unsigned char* Ahl = smem + OFF_AHL;
   half_t* Dt = reinterpret_cast<half_t*>(smem + OFF_DT);
-  half_t* DDt = reinterpret_cast<half_t*>(smem + OFF_DDT);
   half_t* Vs = reinterpret_cast<half_t*>(smem + OFF_VS);
   half_t* St = reinterpret_cast<half_t*>(smem + OFF_ST);
   half_t* Aqk = reinterpret_cast<half_t*>(smem + OFF_AQK);
   float* s_beta = reinterpret_cast<float*>(smem + OFF_SC);
   float* s_G = s_beta + CH;
   float* s_gam = s_G + CH;
-  float* s_bg = s_gam + CH;  // beta * gamma
 
   const int tid = threadIdx.x;
-  const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const bool kwave = wave < 4;
+  const int v = wave & 3;  // the dv tile (16 columns) a wave of either role owns
   const int half_id = blockIdx.x & 1;
   const int j = (blockIdx.x >> 1) % p.Hv;      // value head
   const int64_t b = (blockIdx.x >> 1) / p.Hv;  // batch row
   const int qh = j / (p.Hv / p.Hk);            // key head of this value head
-  const int lq = lane >> 4;                    // quad of the MFMA output layout
-  const int lc = lane & 15;                    // column of the MFMA output layout
 
-  // state slice S[dk][dv] in registers: wave w owns tiles (tk, tv) = (w, 0..3)
-  cfloat4 S[4];
-  const float* s_in = p.state_in == nullptr ? nullptr : p.state_in + ((b * p.Hv + j) * DK) * DV + half_id * DVS;
-#pragma unroll
-  for (int tv = 0; tv < 4; ++tv) {
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int dk = 16 * wave + 4 * lq + r;
-      const int dv = 16 * tv + lc;
-      S[tv][r] = s_in == nullptr ? 0.f : s_in[static_cast<int64_t>(dk) * DV + dv];
-    }
-    store4h(St + (16 * tv + lc) * LD128 + 16 * wave + 4 * lq, S[tv][0], S[tv][1], S[tv][2], S[tv][3]);
-  }
   // Aqk tiles above the diagonal are zero for every chunk
   if (tid < 6 * 64) {
+    const int lane = tid & 63, lq = lane >> 4, lc = lane & 15;
     const int n = tid >> 6;  // (ti, tl) = (0,1) (0,2) (0,3) (1,2) (1,3) (2,3)
     const int ti = n < 3 ? 0 : n < 5 ? 1 : 2;
     const int tl = ti + 1 + (n < 3 ? n : n < 5 ? n - 3 : 0);
@@ -559,141 +603,100 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(2, 2))) void
   }
   ChunkRegs nx = load_chunk(p, b, j, qh, half_id, 0, tid);
 
-  for (int64_t ci = 0; ci < p.nch; ++ci) {
-    const int64_t t0 = ci * CH;
-    // The lane index is re-derived opaquely each chunk, so the per-lane LDS addresses of the
-    // loop body are recomputed in it rather than hoisted out and held in VGPRs across it.
-    int lane = tid & 63;
-    asm volatile("" : "+v"(lane));
-    const int lq = lane >> 4;
-    const int lc = lane & 15;
-
-    // ---------------- stage this chunk's tiles; the next chunk's loads go out
+  if (kwave) {
+    // state columns dv = 16 v + lc as eight 16x16 tiles: S[d][r] = S[dk_of(d, 4 lq + r)][16 v + lc]
+    cfloat4 S[8];
     {
-      const int c0 = tid, c1 = tid + NT;
-      *reinterpret_cast<u32x4*>(Qs + (c0 >> 4) * LD128 + 8 * (c0 & 15)) = nx.q0;
-      *reinterpret_cast<u32x4*>(Qs + (c1 >> 4) * LD128 + 8 * (c1 & 15)) = nx.q1;
-      *reinterpret_cast<u32x4*>(Ks + (c0 >> 4) * LD128 + 8 * (c0 & 15)) = nx.k0;
-      *reinterpret_cast<u32x4*>(Ks + (c1 >> 4) * LD128 + 8 * (c1 & 15)) = nx.k1;
-      *reinterpret_cast<u32x4*>(Vs + (tid >> 3) * LD64 + 8 * (tid & 7)) = nx.v;
+      const int lane = tid & 63, lq = lane >> 4, lc = lane & 15;
+      const float* s_in = p.state_in == nullptr ? nullptr : p.state_in + ((b * p.Hv + j) * DK) * DV + half_id * DVS;
+#pragma unroll
+      for (int d = 0; d < 8; ++d) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) S[d][r] = s_in == nullptr ? 0.f : s_in[static_cast<int64_t>(dk_of(d, 4 * lq + r)) * DV + 16 * v + lc];
+        store4h(St + (16 * v + lc) * LD128 + dk_of(d, 4 * lq), S[d][0], S[d][1], S[d][2], S[d][3]);
+      }
     }
-    if (tid < CH / 2) {
-      s_G[2 * tid] = nx.gb.x;
-      s_beta[2 * tid] = nx.gb.y;
-      s_G[2 * tid + 1] = nx.gb.z;
-      s_beta[2 * tid + 1] = nx.gb.w;
-      const float g0 = __expf(nx.gb.x);
-      const float g1 = __expf(nx.gb.z);
-      s_gam[2 * tid] = g0;
-      s_gam[2 * tid + 1] = g1;
-      s_bg[2 * tid] = nx.gb.y * g0;
-      s_bg[2 * tid + 1] = nx.gb.w * g1;
-    }
-    // (the last chunk reloads itself rather than branching, so nx stays in registers)
-    nx = load_chunk(p, b, j, qh, half_id, min(ci + 1, p.nch - 1), tid);
-    lds_barrier();
+    for (int64_t ci = 0; ci < p.nch; ++ci) {
+      // The lane index is re-derived opaquely each chunk, so the per-lane LDS addresses of the
+      // loop body are recomputed in it rather than hoisted out and held in VGPRs across it.
+      int lane = tid & 63;
+      asm volatile("" : "+v"(lane));
+      const int lq = lane >> 4;
+      const int lc = lane & 15;
+      stage_chunk(p, smem, nx, b, j, qh, half_id, ci, tid);
 
-    // ---------------- phase 1: what the substitution of phase 2 reads
-    //  waves 0..3 (w): the diagonal block A_ww and D_w = (I + A_ww)^-1 (to Tb);
-    //  waves 4..7 (w4 = wave - 4): R = diag(beta) (V - diag(gamma) K S0) for dv tile w4 (all
-    //    four token blocks), kept in registers for the same wave's substitution chain, then
-    //    the off-diagonal blocks n = w4 and w4 + 4 (< 6) of A, split once into fp16 hi + lo.
-    // A = beta_i exp(G_i - G_l) K K^T (strictly lower) is computed as (K_l K_i^T), so lane
-    // (lq, lc) holds A[16 ti + lc][16 tl + 4 lq + r]: the A-operand layout of the 16x16x16
-    // products that consume it.
-    cfloat4 R[4];  // waves 4..7: R tiles (token block p, dv tile wave - 4), C layout
-    if (wave < 4) {
-      const int pb = wave;
-      {
-        const int i = 16 * pb + lc;
-        const float bi = s_beta[i];
+      // ---------------- phase 1 (key wave): K (all 64 tokens) into registers; R = diag(beta)
+      // (V - diag(gamma) K S0) for dv tile v, with S0 from this wave's registers, kept for its
+      // substitution chain; the off-diagonal blocks n = v and v + 4 (< 6) of A from the same K
+      // registers, split once into fp16 hi + lo (to Ahl).  A = beta_i exp(G_i - G_l) K K^T
+      // (strictly lower) is computed as (K_l K_i^T), so lane (lq, lc) holds
+      // A[16 ti + lc][16 tl + 4 lq + r]: the A-operand layout of the 16x16x16 products that
+      // consume it.
+      cfloat4 R[4];  // R tiles (token block p, dv tile v), C layout
+      f16x8_v kr[4][DK / 32];
+#pragma unroll
+      for (int t = 0; t < 4; ++t)
+#pragma unroll
+        for (int k = 0; k < DK / 32; ++k) kr[t][k] = *reinterpret_cast<const f16x8_v*>(Ks + (16 * t + lc) * LD128 + 32 * k + 8 * lq);
+      // S0 as the B operand of K S0: slot e of lane (lq, lc) in k-step k is dk 32 k + 8 lq + e,
+      // which tile 2k (e < 4) or 2k + 1 (e >= 4) holds in register e % 4.
+      f16x8_v sb[DK / 32];
+#pragma unroll
+      for (int k = 0; k < DK / 32; ++k) sb[k] = pack8h(S[2 * k], S[2 * k + 1]);
+      __builtin_amdgcn_sched_barrier(0);
+      cfloat4 acc[4];
+#pragma unroll
+      for (int t = 0; t < 4; ++t) acc[t] = cfloat4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int k = 0; k < DK / 32; ++k)
+#pragma unroll
+        for (int t = 0; t < 4; ++t) acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kr[t][k], sb[k], acc[t], 0, 0, 0);
+      // the off-diagonal blocks of A this wave owns
+      cfloat4 aa[2];
+#pragma unroll
+      for (int n = 0; n < 6; ++n) {
+        if (n % 4 != v) continue;
+        int ti, tl;
+        lower_block(n, ti, tl);
+        cfloat4 x = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int k = 0; k < DK / 32; ++k) x = __builtin_amdgcn_mfma_f32_16x16x32_f16(kr[tl][k], kr[ti][k], x, 0, 0, 0);
+        aa[n / 4] = x;
+      }
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
+        const h4_v v4 = tr_read(Vs, LD64, 16 * t + 4 * lq, 16 * v, lane);
+        const cfloat4 bt = *reinterpret_cast<const cfloat4*>(s_beta + 16 * t + 4 * lq);
+        const cfloat4 gm = *reinterpret_cast<const cfloat4*>(s_gam + 16 * t + 4 * lq);
+#pragma unroll
+        for (int r = 0; r < 4; ++r) R[t][r] = bt[r] * __builtin_fmaf(-gm[r], acc[t][r], static_cast<float>(v4[r]));
+      }
+#pragma unroll
+      for (int n = 0; n < 6; ++n) {
+        if (n % 4 != v) continue;
+        int ti, tl;
+        lower_block(n, ti, tl);
+        const int i = 16 * ti + lc;
         const float gi = s_G[i];
-        const cfloat4 gl = *reinterpret_cast<const cfloat4*>(s_G + 16 * pb + 4 * lq);
-        cfloat4 acc = {0.f, 0.f, 0.f, 0.f};
-        acc = mma<DK>(Ks + 16 * pb * LD128, LD128, Ks + 16 * pb * LD128, LD128, acc, lane);
+        const float bi = s_beta[i];
+        const cfloat4 gl = *reinterpret_cast<const cfloat4*>(s_G + 16 * tl + 4 * lq);
         cfloat4 a;
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const float e = bi * __expf(gi - gl[r]) * acc[r];
-          a[r] = 4 * lq + r < lc ? e : 0.f;
-        }
-        *reinterpret_cast<cfloat4*>(Adg + (16 * pb + lc) * LDB + 4 * lq) = a;
+        for (int r = 0; r < 4; ++r) a[r] = bi * __expf(gi - gl[r]) * aa[n / 4][r];
+        h4_v hi, lo;
+        split4(a, hi, lo);
+        h4_v* dst = reinterpret_cast<h4_v*>(Ahl + n * 1024 + 16 * lane);
+        dst[0] = hi;
+        dst[1] = lo;
       }
-      // D_pb.  The block was written by this wave just above, and one wave's LDS accesses
-      // are performed in order, so no barrier is needed.
-      solve_unit_lower16(Adg + (16 * pb) * LDB, Tb + (16 * pb) * LDB, lane);
-    } else {
-      const int w4 = wave - 4;
-      // R for dv tile w4: K S0 (the S0 operand rows are shared by the four token blocks)
-      {
-        const int dvt = w4;
-        f16x8_v sb[DK / 32];
-#pragma unroll
-        for (int k = 0; k < DK / 32; ++k) sb[k] = *reinterpret_cast<const f16x8_v*>(St + (16 * dvt + lc) * LD128 + 32 * k + 8 * lq);
-        f16x8_v ka[4][DK / 32];
-        h4_v v4[4];
-        cfloat4 bt[4], gm[4];
-#pragma unroll
-        for (int t = 0; t < 4; ++t) {
-#pragma unroll
-          for (int k = 0; k < DK / 32; ++k) ka[t][k] = *reinterpret_cast<const f16x8_v*>(Ks + (16 * t + lc) * LD128 + 32 * k + 8 * lq);
-          v4[t] = tr_read(Vs, LD64, 16 * t + 4 * lq, 16 * dvt, lane);
-          bt[t] = *reinterpret_cast<const cfloat4*>(s_beta + 16 * t + 4 * lq);
-          gm[t] = *reinterpret_cast<const cfloat4*>(s_gam + 16 * t + 4 * lq);
-        }
-        __builtin_amdgcn_sched_barrier(0);
-        cfloat4 acc[4];
-#pragma unroll
-        for (int t = 0; t < 4; ++t) acc[t] = cfloat4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-        for (int k = 0; k < DK / 32; ++k)
-#pragma unroll
-          for (int t = 0; t < 4; ++t) acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ka[t][k], sb[k], acc[t], 0, 0, 0);
-#pragma unroll
-        for (int t = 0; t < 4; ++t)
-#pragma unroll
-          for (int r = 0; r < 4; ++r) R[t][r] = bt[t][r] * __builtin_fmaf(-gm[t][r], acc[t][r], static_cast<float>(v4[t][r]));
-      }
-      {
-        int ti[2], tl[2];
-        lower_block(w4, ti[0], tl[0]);
-        lower_block(w4 + 4 < 6 ? w4 + 4 : w4, ti[1], tl[1]);  // waves 6, 7 own one block
-        cfloat4 acc[2];
-        tile_pair(Ks, Ks, ti[0], tl[0], Ks, ti[1], tl[1], acc[0], acc[1], lq, lc);
-#pragma unroll
-        for (int u = 0; u < 2; ++u) {
-          const int n = w4 + 4 * u;
-          if (n < 6) {
-            const int i = 16 * ti[u] + lc;
-            const float gi = s_G[i];
-            const float bi = s_beta[i];
-            const cfloat4 gl = *reinterpret_cast<const cfloat4*>(s_G + 16 * tl[u] + 4 * lq);
-            cfloat4 a;
-#pragma unroll
-            for (int r = 0; r < 4; ++r) a[r] = bi * __expf(gi - gl[r]) * acc[u][r];
-            h4_v hi, lo;
-            split4(a, hi, lo);
-            h4_v* dst = reinterpret_cast<h4_v*>(Ahl + n * 1024 + 16 * lane);
-            dst[0] = hi;
-            dst[1] = lo;
-          }
-        }
-      }
-    }
-    lds_barrier();
+      lds_barrier();
 
-    // ---------------- phase 2
-    //  waves 4..7: (I + A) delta = R by blocked forward substitution over the 16-token blocks
-    //    p, delta_p = D_p (R_p - sum_{k<p} A_pk delta_k), one chain per dv tile.  A_pk and D_p
-    //    enter as fp16 hi + lo A operands; R and delta stay fp32 in registers and are split
-    //    into hi + lo B operands (the 16x16 accumulator layout is the B-operand layout).
-    //    delta^T and exp(G_C - G) delta^T go to LDS for phase 3.
-    //  waves 0..3 (w), alongside: the lower tiles n = w, w + 4, w + 8 (< 10) of
-    //    Aqk[i][l] = exp(G_i - G_l) (q_i . k_l), l <= i, and gamma * (S0^T Q^T) for the output
-    //    tiles they own in phase 3 (dv tile w, token tiles 0..3).
-    cfloat4 O[4];  // waves 0..3: O^T tiles (dv tile wave, token tile t), C layout
-    if (wave >= 4) {
-      const int dvt = wave - 4;
+      // ---------------- phase 2 (key wave): (I + A) delta = R by blocked forward substitution
+      // over the 16-token blocks p, delta_p = D_p (R_p - sum_{k<p} A_pk delta_k).  A_pk and D_p
+      // enter as fp16 hi + lo A operands; R and delta stay fp32 in registers and are split into
+      // hi + lo B operands (the 16x16 accumulator layout is the B-operand layout).  delta^T goes
+      // to LDS for the output; then S = gamma_C S + K^T (exp(G_C - G) delta) from the same
+      // registers, and its fp16 copy to St.
       h4_v dh[4], dl[4];
 #pragma unroll
       for (int pb = 0; pb < 4; ++pb) split4(*reinterpret_cast<const cfloat4*>(Tb + (16 * pb + lc) * LDB + 4 * lq), dh[pb], dl[pb]);
@@ -706,6 +709,7 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(2, 2))) void
       }
       const float gC = s_G[CH - 1];
       h4_v xh[4], xl[4];
+      cfloat4 dd[4];  // exp(G_C - G) delta, C layout
 #pragma unroll
       for (int pb = 0; pb < 4; ++pb) {
         const int i0 = 16 * pb + 4 * lq;
@@ -721,72 +725,51 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(2, 2))) void
         const cfloat4 zero = {0.f, 0.f, 0.f, 0.f};
         const cfloat4 d = mma3(dh[pb], dl[pb], rh, rl, zero);
         split4(d, xh[pb], xl[pb]);
-        const int dv = 16 * dvt + lc;
-        store4h(Dt + dv * LD64 + i0, d[0], d[1], d[2], d[3]);
-        float sc[4];
+        store4h(Dt + (16 * v + lc) * LD64 + i0, d[0], d[1], d[2], d[3]);
 #pragma unroll
-        for (int r = 0; r < 4; ++r) sc[r] = __expf(gC - gi[r]) * d[r];
-        store4h(DDt + dv * LD64 + i0, sc[0], sc[1], sc[2], sc[3]);
+        for (int r = 0; r < 4; ++r) dd[pb][r] = __expf(gC - gi[r]) * d[r];
       }
-    } else {
+      // S update.  k-step s covers tokens 32 s .. 32 s + 31, slot e of lane (lq, lc) being
+      // token 32 s + 4 lq + e (e < 4, block 2 s) or 32 s + 16 + 4 lq + e - 4 (block 2 s + 1):
+      // the registers of dd as they are.  The K^T operand uses the same token order and, for
+      // row lc of tile d, dk = dk_of(d, lc).
+      const float gamC = s_gam[CH - 1];
+      f16x8_v bd[2];
 #pragma unroll
-      for (int m = 0; m < 2; ++m) {
-        if (m == 1 && wave >= 2) break;
-        int ti[2], tl[2];
-        const int n0 = wave + 8 * m;
-        const int n1 = m == 0 ? wave + 4 : n0;  // the third tile of waves 0, 1 is single
-        lower_block_diag(n0, ti[0], tl[0]);
-        lower_block_diag(n1, ti[1], tl[1]);
-        cfloat4 acc[2];
-        tile_pair(Ks, Qs, ti[0], tl[0], Qs, ti[1], tl[1], acc[0], acc[1], lq, lc);
+      for (int s = 0; s < 2; ++s) bd[s] = pack8h(dd[2 * s], dd[2 * s + 1]);
 #pragma unroll
-        for (int u = 0; u < 2; ++u) {
-          if (u == 1 && m == 1) break;
-          const int i = 16 * ti[u] + lc;
-          const float gi = s_G[i];
-          const cfloat4 gl = *reinterpret_cast<const cfloat4*>(s_G + 16 * tl[u] + 4 * lq);
-          float v[4];
+      for (int d = 0; d < 8; ++d) S[d] *= gamC;
 #pragma unroll
-          for (int r = 0; r < 4; ++r) {
-            const float e = __expf(gi - gl[r]) * acc[u][r];
-            v[r] = 16 * tl[u] + 4 * lq + r <= i ? e : 0.f;
-          }
-          store4h(Aqk + i * LD64 + 16 * tl[u] + 4 * lq, v[0], v[1], v[2], v[3]);
-        }
+      for (int d = 0; d < 8; ++d) {
+        f16x8_v ka[2];
+#pragma unroll
+        for (int s = 0; s < 2; ++s) ka[s] = ktr_operand(Ks, 32 * s + 4 * lq, d, lane);
+#pragma unroll
+        for (int s = 0; s < 2; ++s) S[d] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ka[s], bd[s], S[d], 0, 0, 0);
       }
-      // O^T tiles (dv tile wave, token tiles t) = gamma * (S0^T Q^T), the S0 rows shared
-      {
-        f16x8_v sa[DK / 32];
 #pragma unroll
-        for (int k = 0; k < DK / 32; ++k) sa[k] = *reinterpret_cast<const f16x8_v*>(St + (16 * wave + lc) * LD128 + 32 * k + 8 * lq);
-        f16x8_v qb[4][DK / 32];
-        float gam[4];
-#pragma unroll
-        for (int t = 0; t < 4; ++t) {
-#pragma unroll
-          for (int k = 0; k < DK / 32; ++k) qb[t][k] = *reinterpret_cast<const f16x8_v*>(Qs + (16 * t + lc) * LD128 + 32 * k + 8 * lq);
-          gam[t] = s_gam[16 * t + lc];
-        }
-        __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-        for (int t = 0; t < 4; ++t) O[t] = cfloat4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-        for (int k = 0; k < DK / 32; ++k)
-#pragma unroll
-          for (int t = 0; t < 4; ++t) O[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(sa[k], qb[t][k], O[t], 0, 0, 0);
-#pragma unroll
-        for (int t = 0; t < 4; ++t) O[t] *= gam[t];
-      }
+      for (int d = 0; d < 8; ++d) store4h(St + (16 * v + lc) * LD128 + dk_of(d, 4 * lq), S[d][0], S[d][1], S[d][2], S[d][3]);
+      lds_barrier();
     }
-    lds_barrier();
-
-    // ---------------- phase 3: O^T += delta^T Aqk^T -> output (waves 0..3);
-    // S = gamma_C S + K^T (D delta) (every wave, dk tile = wave)
-    if (wave < 4) {
-      const int td = wave;
+    if (p.state_out != nullptr) {
+      const int lane = tid & 63, lq = lane >> 4, lc = lane & 15;
+      float* s_out = p.state_out + ((b * p.Hv + j) * DK) * DV + half_id * DVS;
+#pragma unroll
+      for (int d = 0; d < 8; ++d)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) s_out[static_cast<int64_t>(dk_of(d, 4 * lq + r)) * DV + 16 * v + lc] = S[d][r];
+    }
+  } else {
+    cfloat4 O[4];  // O^T tiles (dv tile v, token tile t) of the newest chunk, C layout
+    // ---------------- phase 3 (query wave) of chunk c, run after the staging barrier of chunk
+    // c + 1 (or after the loop): O^T += delta^T Aqk^T -> output.  Dt and Aqk are next written
+    // in phase 2, and the output stores then have a whole chunk to complete before the next
+    // wait on the vector-memory counter (at staging).
+    auto finish_chunk = [&](int64_t c, int lq, int lc) {
+      const int64_t tc0 = c * CH;
       f16x8_v da[CH / 32];
 #pragma unroll
-      for (int k = 0; k < CH / 32; ++k) da[k] = *reinterpret_cast<const f16x8_v*>(Dt + (16 * td + lc) * LD64 + 32 * k + 8 * lq);
+      for (int k = 0; k < CH / 32; ++k) da[k] = *reinterpret_cast<const f16x8_v*>(Dt + (16 * v + lc) * LD64 + 32 * k + 8 * lq);
 #pragma unroll
       for (int tt = 0; tt < 4; ++tt) {
         f16x8_v ab2[CH / 32];
@@ -796,9 +779,9 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(2, 2))) void
 #pragma unroll
         for (int k = 0; k < CH / 32; ++k) O[tt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(da[k], ab2[k], O[tt], 0, 0, 0);
         const int tok = 16 * tt + lc;
-        const int64_t tg = t0 + tok;
+        const int64_t tg = tc0 + tok;
         if (tg < p.T) {
-          const int64_t base = b * p.out_sb + tg * p.out_st + static_cast<int64_t>(j) * DV + half_id * DVS + 16 * td + 4 * lq;
+          const int64_t base = b * p.out_sb + tg * p.out_st + static_cast<int64_t>(j) * DV + half_id * DVS + 16 * v + 4 * lq;
           if (p.out_dtype == QA_BF16) {
             bf16_t* o = reinterpret_cast<bf16_t*>(p.out) + base;
             uint2 packed;
@@ -810,35 +793,105 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(2, 2))) void
           }
         }
       }
-    }
-    const float gamC = s_gam[CH - 1];
-    {
-      f16x8_v kt[CH / 32], bd[4][CH / 32];  // K^T rows 16 wave.. (dk) as A operand, k = token
+    };
+    for (int64_t ci = 0; ci < p.nch; ++ci) {
+      int lane = tid & 63;
+      asm volatile("" : "+v"(lane));
+      const int lq = lane >> 4;
+      const int lc = lane & 15;
+      stage_chunk(p, smem, nx, b, j, qh, half_id, ci, tid);
+      if (ci > 0) finish_chunk(ci - 1, lq, lc);
+
+      // ---------------- phase 1 (query wave): the diagonal block A_vv and D_v = (I + A_vv)^-1
+      // (to Tb); then Q (all 64 tokens) into registers and gamma * (S0^T Q^T) for the output
+      // tiles of dv tile v, from the fp16 copy St of S0.
+      f16x8_v qr[4][DK / 32];  // Q rows 16 t + lc as 16x16x32 operands
+      f16x8_v kv[DK / 32];     // K rows 16 v + lc
+      // A_vv (K_v K_v^T, one operand read serving both sides), then D_v
 #pragma unroll
-      for (int k = 0; k < CH / 32; ++k) {
-        kt[k] = tr_operand32(Ks, LD128, 32 * k, 16 * wave, lane);
+      for (int k = 0; k < DK / 32; ++k) kv[k] = *reinterpret_cast<const f16x8_v*>(Ks + (16 * v + lc) * LD128 + 32 * k + 8 * lq);
+      {
+        const int i = 16 * v + lc;
+        const float bi = s_beta[i];
+        const float gi = s_G[i];
+        const cfloat4 gl = *reinterpret_cast<const cfloat4*>(s_G + 16 * v + 4 * lq);
+        cfloat4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int tv = 0; tv < 4; ++tv) bd[tv][k] = *reinterpret_cast<const f16x8_v*>(DDt + (16 * tv + lc) * LD64 + 32 * k + 8 * lq);
+        for (int k = 0; k < DK / 32; ++k) acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(kv[k], kv[k], acc, 0, 0, 0);
+        cfloat4 a;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const float e = bi * __expf(gi - gl[r]) * acc[r];
+          a[r] = 4 * lq + r < lc ? e : 0.f;
+        }
+        *reinterpret_cast<cfloat4*>(Adg + (16 * v + lc) * LDB + 4 * lq) = a;
       }
+      // The block was written by this wave just above, and one wave's LDS accesses are
+      // performed in order, so no barrier is needed.
+      solve_unit_lower16(Adg + (16 * v) * LDB, Tb + (16 * v) * LDB, lane);
+      // O^T tiles (dv tile v, token tiles t) = gamma * (S0^T Q^T), the S0 rows shared
+      f16x8_v sa[DK / 32];
 #pragma unroll
-      for (int tv = 0; tv < 4; ++tv) S[tv] *= gamC;
+      for (int k = 0; k < DK / 32; ++k) sa[k] = *reinterpret_cast<const f16x8_v*>(St + (16 * v + lc) * LD128 + 32 * k + 8 * lq);
+#pragma unroll
+      for (int t = 0; t < 4; ++t)
+#pragma unroll
+        for (int k = 0; k < DK / 32; ++k) qr[t][k] = *reinterpret_cast<const f16x8_v*>(Qs + (16 * t + lc) * LD128 + 32 * k + 8 * lq);
       __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-      for (int k = 0; k < CH / 32; ++k)
+      for (int t = 0; t < 4; ++t) O[t] = cfloat4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int tv = 0; tv < 4; ++tv) S[tv] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kt[k], bd[tv][k], S[tv], 0, 0, 0);
+      for (int k = 0; k < DK / 32; ++k)
 #pragma unroll
-      for (int tv = 0; tv < 4; ++tv) store4h(St + (16 * tv + lc) * LD128 + 16 * wave + 4 * lq, S[tv][0], S[tv][1], S[tv][2], S[tv][3]);
-    }
-    lds_barrier();
-  }
+        for (int t = 0; t < 4; ++t) O[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(sa[k], qr[t][k], O[t], 0, 0, 0);
+#pragma unroll
+      for (int t = 0; t < 4; ++t) O[t] *= s_gam[16 * t + lc];
+      lds_barrier();
 
-  if (p.state_out != nullptr) {
-    float* s_out = p.state_out + ((b * p.Hv + j) * DK) * DV + half_id * DVS;
+      // ---------------- phase 2 (query wave), alongside the chains: the lower tiles (i, v),
+      // v <= i <= v + 2, and for v = 3 also (3, 0), of Aqk[i][l] = exp(G_i - G_l) (q_i . k_l),
+      // l <= i, from this wave's Q and K_v registers.
+      cfloat4 acc[4];  // tile (i, v) in acc[i]: indices known at compile time keep them in registers
 #pragma unroll
-    for (int tv = 0; tv < 4; ++tv)
+      for (int i = 0; i < 4; ++i) {
+        if (i < v || i > v + 2) continue;
+        acc[i] = cfloat4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int r = 0; r < 4; ++r) s_out[static_cast<int64_t>(16 * wave + 4 * lq + r) * DV + 16 * tv + lc] = S[tv][r];
+        for (int k = 0; k < DK / 32; ++k) acc[i] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kv[k], qr[i][k], acc[i], 0, 0, 0);
+      }
+      cfloat4 acc30 = {0.f, 0.f, 0.f, 0.f};
+      if (v == 3) {
+        f16x8_v k0[DK / 32];
+#pragma unroll
+        for (int k = 0; k < DK / 32; ++k) k0[k] = *reinterpret_cast<const f16x8_v*>(Ks + lc * LD128 + 32 * k + 8 * lq);
+#pragma unroll
+        for (int k = 0; k < DK / 32; ++k) acc30 = __builtin_amdgcn_mfma_f32_16x16x32_f16(k0[k], qr[3][k], acc30, 0, 0, 0);
+      }
+      auto aqk_store = [&](int ti, int tl, const cfloat4& x) {
+        const int i = 16 * ti + lc;
+        const float gi = s_G[i];
+        const cfloat4 gl = *reinterpret_cast<const cfloat4*>(s_G + 16 * tl + 4 * lq);
+        float e[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const float y = __expf(gi - gl[r]) * x[r];
+          e[r] = 16 * tl + 4 * lq + r <= i ? y : 0.f;
+        }
+        store4h(Aqk + i * LD64 + 16 * tl + 4 * lq, e[0], e[1], e[2], e[3]);
+      };
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        if (i < v || i > v + 2) continue;
+        aqk_store(i, v, acc[i]);
+      }
+      if (v == 3) aqk_store(3, 0, acc30);
+      lds_barrier();
+
+    }
+    {
+      const int lane = tid & 63;
+      finish_chunk(p.nch - 1, lane >> 4, lane & 15);
+    }
   }
 }
 
