@@ -86,21 +86,26 @@ inline Workspace workspace_layout(int64_t batch, int64_t seq, int64_t hk, int64_
   return w;
 }
 
-// ---- LDS layout of chunk_kernel (bytes).  Per chunk: Qs, Ks, Vs and the scalars are
-// staged first; phase 1 reads them and St and writes Adg, Tb and Ahl; phase 2 reads Tb,
-// Ahl, Qs, Ks and the scalars and writes Dt, Aqk and St; phase 3 reads Dt and Aqk.
-// No two regions alias.
+// ---- LDS layout of chunk_kernel (bytes).  Per chunk c: Qs, Ks, Vs and the scalars are
+// staged first.  Phase 1 reads them; the key waves write Ahl, the query waves Adg, Tb and
+// Aqk[c % 2].  Phase 2: the key waves read Tb and Ahl and write Dt[c % 2] and St[(c + 1) % 2];
+// the query waves read Dt[(c - 1) % 2] and Aqk[(c - 1) % 2] (the output of chunk c - 1) and
+// St[c % 2].  No two regions alias; the double buffers let phase 2 read one chunk's tiles
+// while the other role writes the next chunk's.
 constexpr int LDB = 20;                            // row stride (floats) of the 16x16 fp32 diagonal blocks
+constexpr int ST_BYTES = DVS * LD128 * 2;          // one St [dv][dk] (fp16 copy of the state)
+constexpr int AQK_BYTES = CH * LD64 * 2;           // one Aqk [i][l]
+constexpr int DT_BYTES = DVS * LD64 * 2;           // one delta^T [dv][tok]
 constexpr int OFF_QS = 0;                          // Qs [tok][dk]
 constexpr int OFF_KS = OFF_QS + CH * LD128 * 2;    // Ks [tok][dk]
 constexpr int OFF_VS = OFF_KS + CH * LD128 * 2;    // Vs [tok][dv] (this workgroup's half)
-constexpr int OFF_ST = OFF_VS + CH * LD64 * 2;     // St [dv][dk] (fp16 copy of the state)
-constexpr int OFF_AQK = OFF_ST + DVS * LD128 * 2;  // Aqk [i][l]
-constexpr int OFF_ADG = OFF_AQK + CH * LD64 * 2;   // diagonal 16x16 blocks of A, fp32 [block][row][LDB]
+constexpr int OFF_ST = OFF_VS + CH * LD64 * 2;     // St x 2
+constexpr int OFF_AQK = OFF_ST + 2 * ST_BYTES;     // Aqk x 2
+constexpr int OFF_ADG = OFF_AQK + 2 * AQK_BYTES;   // diagonal 16x16 blocks of A, fp32 [block][row][LDB]
 constexpr int OFF_TB = OFF_ADG + 4 * 16 * LDB * 4; // D_p = (I + A_pp)^-1, fp32 [block][row][LDB]
 constexpr int OFF_AHL = OFF_TB + 4 * 16 * LDB * 4; // 6 off-diagonal blocks of A as fp16 hi | lo, one 16-byte A operand per lane
-constexpr int OFF_DT = OFF_AHL + 6 * 64 * 16;      // delta^T [dv][tok]
-constexpr int OFF_SC = OFF_DT + DVS * LD64 * 2;    // beta, G, gamma per token
+constexpr int OFF_DT = OFF_AHL + 6 * 64 * 16;      // delta^T x 2
+constexpr int OFF_SC = OFF_DT + 2 * DT_BYTES;      // beta, G, gamma per token
 constexpr int LDS_BYTES = OFF_SC + 3 * CH * 4;
 
 static_assert(OFF_ADG % 16 == 0 && OFF_DT % 16 == 0 && OFF_SC % 16 == 0, "16-byte aligned regions");
@@ -502,11 +507,16 @@ __device__ __forceinline__ void lower_block(int n, int& ti, int& tl) {
   ti = n < 1 ? 1 : n < 3 ? 2 : 3;
   tl = n - ti * (ti - 1) / 2;
 }
-// Row m of state tile d held by a key wave is dk_of(d, m): tiles 2 s and 2 s + 1 share
-// dk 32 s .. 32 s + 31, lane quad lq holding dk 32 s + 8 lq + 0..3 in tile 2 s and + 4..7 in
-// tile 2 s + 1, so that the eight values a lane holds for k-step s of K S0 are the eight
-// consecutive dk of a 16-byte K operand read.
-__device__ __forceinline__ constexpr int dk_of(int d, int m) { return 32 * (d >> 1) + 8 * (m >> 2) + 4 * (d & 1) + (m & 3); }
+// Row m = 4 q + r of state tile d = 2 s + h held by a key wave is
+//   dk_of(d, m) = 8 kblk(s, q) + 4 h + r,   kblk(s, q) = 2 s + (q & 1) + 8 (q >> 1),
+// so tiles 2 s and 2 s + 1 hold, in lane quad q, the eight consecutive dk of 8-half block
+// kblk(s, q): the eight values a lane holds for k-step s of K S0 match a 16-byte K operand
+// read at that block.  The blocks {2 s, 2 s + 1, 2 s + 8, 2 s + 9} of one k-step lie 0, 4, 32
+// and 36 dwords apart, which with rows 8 dwords apart (mod 64) keeps the 16 lanes of a
+// transposed K^T read (ktr_operand) on distinct banks.
+__device__ __forceinline__ constexpr int kblk(int s, int q) { return 2 * s + (q & 1) + 8 * (q >> 1); }
+__device__ __forceinline__ constexpr int dk_of(int d, int m) { return 8 * kblk(d >> 1, m >> 2) + 4 * (d & 1) + (m & 3); }
+static_assert(LD128 % 128 == 16, "the K^T reads rely on rows 8 dwords apart mod 64");
 
 // fp16 (a0..a3, b0..b3) as one 16x16x32 operand
 __device__ __forceinline__ f16x8_v pack8h(const cfloat4& a, const cfloat4& b) {
@@ -593,13 +603,14 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(2, 2))) void
   const int64_t b = (blockIdx.x >> 1) / p.Hv;  // batch row
   const int qh = j / (p.Hv / p.Hk);            // key head of this value head
 
-  // Aqk tiles above the diagonal are zero for every chunk
+  // Aqk tiles above the diagonal are zero for every chunk (both buffers)
   if (tid < 6 * 64) {
     const int lane = tid & 63, lq = lane >> 4, lc = lane & 15;
     const int n = tid >> 6;  // (ti, tl) = (0,1) (0,2) (0,3) (1,2) (1,3) (2,3)
     const int ti = n < 3 ? 0 : n < 5 ? 1 : 2;
     const int tl = ti + 1 + (n < 3 ? n : n < 5 ? n - 3 : 0);
-    store4h(Aqk + (16 * ti + lc) * LD64 + 16 * tl + 4 * lq, 0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+    for (int u = 0; u < 2; ++u) store4h(Aqk + u * (AQK_BYTES / 2) + (16 * ti + lc) * LD64 + 16 * tl + 4 * lq, 0.f, 0.f, 0.f, 0.f);
   }
   ChunkRegs nx = load_chunk(p, b, j, qh, half_id, 0, tid);
 
@@ -637,9 +648,10 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(2, 2))) void
 #pragma unroll
       for (int t = 0; t < 4; ++t)
 #pragma unroll
-        for (int k = 0; k < DK / 32; ++k) kr[t][k] = *reinterpret_cast<const f16x8_v*>(Ks + (16 * t + lc) * LD128 + 32 * k + 8 * lq);
-      // S0 as the B operand of K S0: slot e of lane (lq, lc) in k-step k is dk 32 k + 8 lq + e,
-      // which tile 2k (e < 4) or 2k + 1 (e >= 4) holds in register e % 4.
+        for (int k = 0; k < DK / 32; ++k) kr[t][k] = *reinterpret_cast<const f16x8_v*>(Ks + (16 * t + lc) * LD128 + 8 * kblk(k, lq));
+      // S0 as the B operand of K S0: slot e of lane (lq, lc) in k-step k is dk 8 kblk(k, lq) + e,
+      // which tile 2k (e < 4) or 2k + 1 (e >= 4) holds in register e % 4.  (The off-diagonal A
+      // blocks below use the same K registers for both operands, so the dk order is immaterial.)
       f16x8_v sb[DK / 32];
 #pragma unroll
       for (int k = 0; k < DK / 32; ++k) sb[k] = pack8h(S[2 * k], S[2 * k + 1]);
@@ -725,7 +737,7 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(2, 2))) void
         const cfloat4 zero = {0.f, 0.f, 0.f, 0.f};
         const cfloat4 d = mma3(dh[pb], dl[pb], rh, rl, zero);
         split4(d, xh[pb], xl[pb]);
-        store4h(Dt + (16 * v + lc) * LD64 + i0, d[0], d[1], d[2], d[3]);
+        store4h(Dt + (ci & 1) * (DT_BYTES / 2) + (16 * v + lc) * LD64 + i0, d[0], d[1], d[2], d[3]);
 #pragma unroll
         for (int r = 0; r < 4; ++r) dd[pb][r] = __expf(gC - gi[r]) * d[r];
       }
@@ -748,7 +760,8 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(2, 2))) void
         for (int s = 0; s < 2; ++s) S[d] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ka[s], bd[s], S[d], 0, 0, 0);
       }
 #pragma unroll
-      for (int d = 0; d < 8; ++d) store4h(St + (16 * v + lc) * LD128 + dk_of(d, 4 * lq), S[d][0], S[d][1], S[d][2], S[d][3]);
+      for (int d = 0; d < 8; ++d)
+        store4h(St + ((ci + 1) & 1) * (ST_BYTES / 2) + (16 * v + lc) * LD128 + dk_of(d, 4 * lq), S[d][0], S[d][1], S[d][2], S[d][3]);
       lds_barrier();
     }
     if (p.state_out != nullptr) {
@@ -761,23 +774,23 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(2, 2))) void
     }
   } else {
     cfloat4 O[4];  // O^T tiles (dv tile v, token tile t) of the newest chunk, C layout
-    // ---------------- phase 3 (query wave) of chunk c, run after the staging barrier of chunk
-    // c + 1 (or after the loop): O^T += delta^T Aqk^T -> output.  Dt and Aqk are next written
-    // in phase 2, and the output stores then have a whole chunk to complete before the next
-    // wait on the vector-memory counter (at staging).
+    // Output of chunk c, in phase 2 of chunk c + 1 (or after the loop): O^T += delta^T Aqk^T.
     auto finish_chunk = [&](int64_t c, int lq, int lc) {
       const int64_t tc0 = c * CH;
-      f16x8_v da[CH / 32];
+      f16x8_v da[CH / 32], ab2[4][CH / 32];
 #pragma unroll
-      for (int k = 0; k < CH / 32; ++k) da[k] = *reinterpret_cast<const f16x8_v*>(Dt + (16 * v + lc) * LD64 + 32 * k + 8 * lq);
+      for (int k = 0; k < CH / 32; ++k) {
+        da[k] = *reinterpret_cast<const f16x8_v*>(Dt + (c & 1) * (DT_BYTES / 2) + (16 * v + lc) * LD64 + 32 * k + 8 * lq);
+#pragma unroll
+        for (int tt = 0; tt < 4; ++tt) ab2[tt][k] = *reinterpret_cast<const f16x8_v*>(Aqk + (c & 1) * (AQK_BYTES / 2) + (16 * tt + lc) * LD64 + 32 * k + 8 * lq);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int k = 0; k < CH / 32; ++k)
+#pragma unroll
+        for (int tt = 0; tt < 4; ++tt) O[tt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(da[k], ab2[tt][k], O[tt], 0, 0, 0);
 #pragma unroll
       for (int tt = 0; tt < 4; ++tt) {
-        f16x8_v ab2[CH / 32];
-#pragma unroll
-        for (int k = 0; k < CH / 32; ++k) ab2[k] = *reinterpret_cast<const f16x8_v*>(Aqk + (16 * tt + lc) * LD64 + 32 * k + 8 * lq);
-        __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-        for (int k = 0; k < CH / 32; ++k) O[tt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(da[k], ab2[k], O[tt], 0, 0, 0);
         const int tok = 16 * tt + lc;
         const int64_t tg = tc0 + tok;
         if (tg < p.T) {
@@ -800,13 +813,13 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(2, 2))) void
       const int lq = lane >> 4;
       const int lc = lane & 15;
       stage_chunk(p, smem, nx, b, j, qh, half_id, ci, tid);
-      if (ci > 0) finish_chunk(ci - 1, lq, lc);
 
       // ---------------- phase 1 (query wave): the diagonal block A_vv and D_v = (I + A_vv)^-1
-      // (to Tb); then Q (all 64 tokens) into registers and gamma * (S0^T Q^T) for the output
-      // tiles of dv tile v, from the fp16 copy St of S0.
+      // (to Tb); Q (all 64 tokens) into registers and gamma * (S0^T Q^T) for the output tiles
+      // of chunk c (dv tile v) from St[c % 2].
       f16x8_v qr[4][DK / 32];  // Q rows 16 t + lc as 16x16x32 operands
       f16x8_v kv[DK / 32];     // K rows 16 v + lc
+      cfloat4 On[4];           // gamma * (S0^T Q^T) of chunk c, until the output of chunk c - 1 is done
       // A_vv (K_v K_v^T, one operand read serving both sides), then D_v
 #pragma unroll
       for (int k = 0; k < DK / 32; ++k) kv[k] = *reinterpret_cast<const f16x8_v*>(Ks + (16 * v + lc) * LD128 + 32 * k + 8 * lq);
@@ -829,28 +842,32 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(2, 2))) void
       // The block was written by this wave just above, and one wave's LDS accesses are
       // performed in order, so no barrier is needed.
       solve_unit_lower16(Adg + (16 * v) * LDB, Tb + (16 * v) * LDB, lane);
-      // O^T tiles (dv tile v, token tiles t) = gamma * (S0^T Q^T), the S0 rows shared
-      f16x8_v sa[DK / 32];
-#pragma unroll
-      for (int k = 0; k < DK / 32; ++k) sa[k] = *reinterpret_cast<const f16x8_v*>(St + (16 * v + lc) * LD128 + 32 * k + 8 * lq);
 #pragma unroll
       for (int t = 0; t < 4; ++t)
 #pragma unroll
         for (int k = 0; k < DK / 32; ++k) qr[t][k] = *reinterpret_cast<const f16x8_v*>(Qs + (16 * t + lc) * LD128 + 32 * k + 8 * lq);
+      // O^T tiles (dv tile v, token tiles t) = gamma * (S0^T Q^T), the S0 rows shared
+      f16x8_v sa[DK / 32];
+#pragma unroll
+      for (int k = 0; k < DK / 32; ++k) sa[k] = *reinterpret_cast<const f16x8_v*>(St + (ci & 1) * (ST_BYTES / 2) + (16 * v + lc) * LD128 + 32 * k + 8 * lq);
       __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-      for (int t = 0; t < 4; ++t) O[t] = cfloat4{0.f, 0.f, 0.f, 0.f};
+      for (int t = 0; t < 4; ++t) On[t] = cfloat4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int k = 0; k < DK / 32; ++k)
 #pragma unroll
-        for (int t = 0; t < 4; ++t) O[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(sa[k], qr[t][k], O[t], 0, 0, 0);
+        for (int t = 0; t < 4; ++t) On[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(sa[k], qr[t][k], On[t], 0, 0, 0);
 #pragma unroll
-      for (int t = 0; t < 4; ++t) O[t] *= s_gam[16 * t + lc];
+      for (int t = 0; t < 4; ++t) On[t] *= s_gam[16 * t + lc];
       lds_barrier();
 
-      // ---------------- phase 2 (query wave), alongside the chains: the lower tiles (i, v),
-      // v <= i <= v + 2, and for v = 3 also (3, 0), of Aqk[i][l] = exp(G_i - G_l) (q_i . k_l),
-      // l <= i, from this wave's Q and K_v registers.
+      // ---------------- phase 2 (query wave), alongside the chains: the output of chunk c - 1,
+      // then the lower tiles (i, v), v <= i <= v + 2, and for v = 3 also (3, 0), of
+      // Aqk[i][l] = exp(G_i - G_l) (q_i . k_l), l <= i, from the Q and K_v registers (to
+      // Aqk[c % 2]).
+      if (ci > 0) finish_chunk(ci - 1, lq, lc);
+#pragma unroll
+      for (int t = 0; t < 4; ++t) O[t] = On[t];
       cfloat4 acc[4];  // tile (i, v) in acc[i]: indices known at compile time keep them in registers
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
@@ -877,7 +894,7 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(2, 2))) void
           const float y = __expf(gi - gl[r]) * x[r];
           e[r] = 16 * tl + 4 * lq + r <= i ? y : 0.f;
         }
-        store4h(Aqk + i * LD64 + 16 * tl + 4 * lq, e[0], e[1], e[2], e[3]);
+        store4h(Aqk + (ci & 1) * (AQK_BYTES / 2) + i * LD64 + 16 * tl + 4 * lq, e[0], e[1], e[2], e[3]);
       };
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
@@ -886,7 +903,6 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(2, 2))) void
       }
       if (v == 3) aqk_store(3, 0, acc30);
       lds_barrier();
-
     }
     {
       const int lane = tid & 63;
