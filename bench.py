@@ -38,9 +38,10 @@ HBM_PEAK_GBS = 8000.0  # MI355X HBM3E, GB/s
 # profiles/paged_prefill_config3.md): FETCH_SIZE scaled by 2.0 and WRITE_SIZE by 1.0, the factors
 # a plain 1 GiB device copy reads back in the same runs. Counters need rocprofv3, so the figures
 # are the committed profile's, not measured live.
-TRAFFIC_DECODE = 1959219777
-TRAFFIC_DELTA = 1635882244
-TRAFFIC_PREFILL = 889788105  # average over the eight per-chunk launches
+TRAFFIC_DECODE = 1959222089
+TRAFFIC_DELTA = 1636013431
+TRAFFIC_PREFILL = 890087159  # average over the eight per-chunk launches
+SECONDARY_WARM_MS = 100.0  # wall time of untimed steps before each secondary (config 3, 4, 5) measurement
 MFMA_BF16_PEAK_TFLOPS = 2500.0  # MI355X dense bf16/fp16 MFMA, TFLOP/s
 
 
@@ -116,13 +117,24 @@ def time_decode(w, steps: int, warmup: int):
     return _timed(step, steps, warmup, ("decode_partial_mfma", "decode_combine"))
 
 
-def _timed(step, steps: int, warmup: int, labels: tuple[str, ...]):
-    """(ms per step over ``steps`` timed steps, per-kernel averages from a separate instrumented pass)."""
+def _timed(step, steps: int, warmup: int, labels: tuple[str, ...], warm_ms: float = 0.0):
+    """(ms per step over ``steps`` timed steps, per-kernel averages from a separate instrumented pass).
+
+    ``warmup`` untimed steps run first, and more until ``warm_ms`` of wall time has passed: after
+    the memory-bound decode measurement the GPU takes some tens of milliseconds of compute-heavy
+    work to reach its steady clock, and a sub-millisecond step timed before that reads up to 15%
+    slow."""
+    import time
+
     import torch
 
     for _ in range(warmup):
         step()
     torch.cuda.synchronize()
+    t_start = time.perf_counter()
+    while (time.perf_counter() - t_start) * 1e3 < warm_ms:
+        step()
+        torch.cuda.synchronize()
     stream = torch.cuda.current_stream()
     start = torch.cuda.Event(enable_timing=True)
     end = torch.cuda.Event(enable_timing=True)
@@ -227,7 +239,7 @@ def time_delta(w, steps: int, warmup: int) -> float:
         return hip_ops.chunk_gated_delta_rule(w["mixed"], w["a"], w["b"], w["a_log"], w["dt_bias"], w["conv_w"], key_heads=w["key_heads"],
                                               value_heads=w["value_heads"], keep_conv_state=False)
 
-    return _timed(step, steps, warmup, ("chunk_prep", "chunk_gate", "chunk_gated_delta"))
+    return _timed(step, steps, warmup, ("chunk_prep", "chunk_gate", "chunk_gated_delta"), warm_ms=SECONDARY_WARM_MS)
 
 
 # ----------------------------------------------------------------------------- config 3
@@ -282,7 +294,7 @@ def time_prefill(w, steps: int, warmup: int) -> float:
                                     starts, w["bs"])
             hip_ops.paged_attention_prefill(q, cu, starts, w["key_pool"], w["value_pool"], w["tables"], w["bs"], max_new=n, gate=gate)
 
-    return _timed(step, steps, warmup, ("paged_prefill",))
+    return _timed(step, steps, warmup, ("paged_prefill",), warm_ms=SECONDARY_WARM_MS)
 
 
 # ----------------------------------------------------------------------------- config 5
@@ -355,7 +367,7 @@ def time_hybrid(w, steps: int, warmup: int) -> float:
             hip_ops.paged_kv_append(x["new_k"], x["new_v"], full["key_pool"], full["value_pool"], full["tables"], x["positions"], w["bs"])
             hip_ops.paged_attention_decode_batched(x["query"], full["tables"], full["key_pool"], full["value_pool"], x["lens"], w["bs"])
 
-    return _timed(step, steps, warmup, ("decode_partial_mfma", "decode_combine", "gated_delta_step", "causal_conv1d"))
+    return _timed(step, steps, warmup, ("decode_partial_mfma", "decode_combine", "gated_delta_step", "causal_conv1d"), warm_ms=SECONDARY_WARM_MS)
 
 
 # ----------------------------------------------------------------------------- main
@@ -444,7 +456,7 @@ def main() -> int:
     if not args.no_delta:
         _log("bench: building config-4 workload (gated delta-rule chunked prefill)")
         dw = delta_workload(device)
-        dms, dkern = time_delta(dw, max(2, args.steps // 2), max(1, args.warmup // 2))
+        dms, dkern = time_delta(dw, max(20, args.steps), max(1, args.warmup))
         tflops = dw["flops"] / (dkern["chunk_gated_delta"]["avg_ms"] * 1e-3) / 1e12
         tok_s = dw["batch"] * dw["seq"] / (dms * 1e-3)
         _log(f"bench: delta prefill {dms:.3f} ms, {tok_s:,.0f} tokens/s, {tflops:.1f} TFLOP/s ({tflops / MFMA_BF16_PEAK_TFLOPS:.1%} of MFMA peak)")
@@ -465,7 +477,7 @@ def main() -> int:
     if not args.no_prefill:
         _log("bench: building config-3 workload (chunked paged prefill with gate)")
         pw = prefill_workload(device)
-        pms, pkern = time_prefill(pw, max(2, args.steps // 4), 1)
+        pms, pkern = time_prefill(pw, max(4, args.steps // 2), 1)
         ptf = pw["flops"] / (pkern["paged_prefill"]["total_ms_per_step"] * 1e-3) / 1e12
         _log(f"bench: paged prefill {pms:.3f} ms, {ptf:.1f} TFLOP/s ({ptf / MFMA_BF16_PEAK_TFLOPS:.1%} of MFMA peak)")
         record["secondary_prefill"] = {

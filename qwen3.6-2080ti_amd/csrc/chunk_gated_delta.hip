@@ -15,30 +15,28 @@
 //     Delta Networks" (ICLR 2025).  Per sequence and value head, chunk of
 //     C tokens, initial state S0, gamma = exp(G):
 //       A[i][l]  = beta_i exp(G_i - G_l) (k_i . k_l)         l < i
-//       T        = (I + A)^-1                                 (unit lower triangular)
-//       W        = T diag(beta gamma) K,  U = T diag(beta) V
-//       delta    = U - W S0
+//       (I + A) delta = R,  R = diag(beta) (V - diag(gamma) K S0)
 //       O        = gamma * (Q S0) + Aqk delta,  Aqk[i][l] = exp(G_i - G_l) (q_i . k_l), l <= i
 //       S_end    = gamma_C S0 + K^T (exp(G_C - G) * delta)
-//     which equals the per-token recurrence of src/reference_ops.py:310-318.
+//     which equals the per-token recurrence of src/reference_ops.py:310-318
+//     (delta = U - W S0 of the WY form; T, W and U themselves are never formed).
 //
 // chunk_kernel mapping: one workgroup (8 waves) per (batch row, value head,
-// half of dv); chunks run in order, the fp32 state slice S[dk][dv/2] stays in
-// registers (and as an fp16 copy in LDS for the products).  Matrix products use
-// v_mfma_f32_16x16x32_f16 on 16x16 output tiles with fp16 operands in LDS (fp32
-// accumulation).  Every LDS operand is stored with the reduction axis
-// contiguous; an output is written in whichever orientation its consumer needs
-// by choosing C or C^T (swapped operands).  W and U are never formed through
-// T: with 16-token blocks, (I + A) W = X gives W_p = D_p (X_p - sum_{k<p} A_pk
-// W_k), D_p = (I + A_pp)^-1 (a register forward substitution in fp32); each
-// wave runs this block recurrence for its own column tiles of X = [beta gamma K
-// | beta V] with fp16 hi + lo operand pairs (mma3 below), keeping the state
-// update within fp32-state tolerance.  The 16x16 accumulator layout equals the
-// B-operand layout of the 16-deep product, so every W_k feeds the next block
-// from registers.  The next chunk's tiles are loaded into registers while the
-// current one is computed; barriers order LDS only, so those loads stay in
-// flight across them.  Operands that reduce over tokens are read from the
-// token-major K and V tiles with ds_read_b64_tr_b16 (tr_operand below).
+// half of dv); chunks run in order.  The delta system is solved by blocked
+// forward substitution over 16-token blocks, delta_p = D_p (R_p - sum_{k<p}
+// A_pk delta_k) with D_p = (I + A_pp)^-1, on fp16 hi + lo operand pairs (mma3
+// below), which keeps the state within fp32-state tolerance.  Key waves 0..3
+// own a 16-column dv tile each: all of K and the fp32 state columns in
+// registers, R, the off-diagonal A blocks, the substitution chain and the state
+// update.  Query waves 4..7 own the same dv tiles for the output: the diagonal
+// inverses D_p, all of Q in registers, gamma * (Q S0), Aqk and the output.
+// Matrix products use v_mfma_f32_16x16x32_f16 (fp32 accumulation); the 16x16
+// accumulator layout equals the B-operand layout of the 16-deep product, so
+// delta feeds the next block and the state update from registers.  The next
+// chunk's tiles are loaded into registers while the current one is computed;
+// barriers order LDS only, so those loads stay in flight across them.
+// Operands that reduce over tokens are read from the token-major K and V tiles
+// with ds_read_b64_tr_b16.
 #include "qa_common.h"
 
 namespace qa {
@@ -318,47 +316,6 @@ __global__ __launch_bounds__(256) void gate_kernel(GateParams p) {
 // ---------------------------------------------------------------------------
 // 3. the chunked recurrence.
 
-// C(16x16) += A(16 x K) * B(K x 16); A stored [m][k] (lda), B stored [n][k] (ldb), fp16.
-// Lane l gets C[4(l/16) + r][l % 16].
-// All operand reads are issued before the first product (the scheduler would
-// otherwise pair each read with its product and serialise the LDS latency).
-template <int K>
-__device__ __forceinline__ cfloat4 mma(const half_t* A, int lda, const half_t* B, int ldb, cfloat4 acc, int lane) {
-  const int row = lane & 15;
-  const int kq = lane >> 4;
-  f16x8_v av[K / 32], bv[K / 32];
-#pragma unroll
-  for (int k = 0; k < K / 32; ++k) {
-    av[k] = *reinterpret_cast<const f16x8_v*>(A + row * lda + 32 * k + 8 * kq);
-    bv[k] = *reinterpret_cast<const f16x8_v*>(B + row * ldb + 32 * k + 8 * kq);
-  }
-  __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-  for (int k = 0; k < K / 32; ++k) acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(av[k], bv[k], acc, 0, 0, 0);
-  return acc;
-}
-
-// Two tiles that share the A rows: C0 += A B0, C1 += A B1 (B0, B1 stored [n][k]).
-template <int K>
-__device__ __forceinline__ void mma2(const half_t* A, int lda, const half_t* B0, const half_t* B1, int ldb, cfloat4& c0, cfloat4& c1,
-                                     int lane) {
-  const int row = lane & 15;
-  const int kq = lane >> 4;
-  f16x8_v av[K / 32], b0[K / 32], b1[K / 32];
-#pragma unroll
-  for (int k = 0; k < K / 32; ++k) {
-    av[k] = *reinterpret_cast<const f16x8_v*>(A + row * lda + 32 * k + 8 * kq);
-    b0[k] = *reinterpret_cast<const f16x8_v*>(B0 + row * ldb + 32 * k + 8 * kq);
-    b1[k] = *reinterpret_cast<const f16x8_v*>(B1 + row * ldb + 32 * k + 8 * kq);
-  }
-  __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-  for (int k = 0; k < K / 32; ++k) {
-    c0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(av[k], b0[k], c0, 0, 0, 0);
-    c1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(av[k], b1[k], c1, 0, 0, 0);
-  }
-}
-
 // Four fp16 of a column of a row-major LDS tile X, for each lane, by
 // ds_read_b64_tr_b16: lane i of 16-lane group g reads the 8 bytes at
 // X[row_g + i / 4][c0 + 4 (i % 4)], and the instruction returns to lane j of
@@ -371,14 +328,6 @@ __device__ __forceinline__ h4_v tr_read(const half_t* tile, int ld, int row_g, i
   typedef __attribute__((address_space(3))) s4_v lds_s4;
   const int i = lane & 15;
   return __builtin_bit_cast(h4_v, __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s4*)(tile + (row_g + (i >> 2)) * ld + c0 + 4 * (i & 3))));
-}
-
-// The 16x16x32 A operand of X^T for the row-major tile X: lane (g, j) gets
-// X[k0 + 8g + e][c0 + j], e = 0..7.
-__device__ __forceinline__ f16x8_v tr_operand32(const half_t* tile, int ld, int k0, int c0, int lane) {
-  const int g8 = 8 * (lane >> 4);
-  return __builtin_bit_cast(f16x8_v, __builtin_shufflevector(tr_read(tile, ld, k0 + g8, c0, lane), tr_read(tile, ld, k0 + g8 + 4, c0, lane),
-                                                             0, 1, 2, 3, 4, 5, 6, 7));
 }
 
 // v = hi + lo with hi = fp16(v) and lo = fp16(v - hi) (v - hi is exact in fp32).
@@ -435,29 +384,6 @@ __device__ __forceinline__ cfloat4 mma3(const h4_v& ah, const h4_v& al, const h4
   acc = __builtin_amdgcn_mfma_f32_16x16x16f16(ah, bh, acc, 0, 0, 0);
   acc = __builtin_amdgcn_mfma_f32_16x16x16f16(ah, bl, acc, 0, 0, 0);
   return __builtin_amdgcn_mfma_f32_16x16x16f16(al, bh, acc, 0, 0, 0);
-}
-
-// Two 16x16 tiles of X K^T over dk: lane (lq, lc) gets X[16 ti + lc] . K[16 tl + 4 lq + r]
-// (the row-i A-operand layout of the 16x16x16 products that consume A).  The operands of
-// both tiles are read before the first product, for latency overlap.
-__device__ __forceinline__ void tile_pair(const half_t* Ks, const half_t* X0, int ti0, int tl0, const half_t* X1, int ti1, int tl1,
-                                          cfloat4& a0, cfloat4& a1, int lq, int lc) {
-  f16x8_v k0[DK / 32], x0[DK / 32], k1[DK / 32], x1[DK / 32];
-#pragma unroll
-  for (int k = 0; k < DK / 32; ++k) {
-    k0[k] = *reinterpret_cast<const f16x8_v*>(Ks + (16 * tl0 + lc) * LD128 + 32 * k + 8 * lq);
-    x0[k] = *reinterpret_cast<const f16x8_v*>(X0 + (16 * ti0 + lc) * LD128 + 32 * k + 8 * lq);
-    k1[k] = *reinterpret_cast<const f16x8_v*>(Ks + (16 * tl1 + lc) * LD128 + 32 * k + 8 * lq);
-    x1[k] = *reinterpret_cast<const f16x8_v*>(X1 + (16 * ti1 + lc) * LD128 + 32 * k + 8 * lq);
-  }
-  __builtin_amdgcn_sched_barrier(0);
-  a0 = cfloat4{0.f, 0.f, 0.f, 0.f};
-  a1 = cfloat4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-  for (int k = 0; k < DK / 32; ++k) {
-    a0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(k0[k], x0[k], a0, 0, 0, 0);
-    a1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(k1[k], x1[k], a1, 0, 0, 0);
-  }
 }
 
 // v of lane S of each group of four lanes, to all four (DPP quad_perm [S, S, S, S])
