@@ -60,8 +60,8 @@ constexpr int NT = NW * 64;
 constexpr int KCONV = 4;
 constexpr int LD128 = 144;  // padded leading dims (halfs) of 128- and 64-wide fp16 tiles: strides of 8 (mod 16)
 constexpr int LD64 = 80;   // dwords measured to give the fewest LDS bank conflicts (136 / 72 had twice as many)
-constexpr int RUN = 128;    // tokens one prep wave walks
-constexpr int PU = 8;       // tokens per prep step
+constexpr int PU = 3;       // tokens per prep step (the conv history length)
+constexpr int RUN = 11 * PU;  // tokens one prep wave walks (swept: 33 beats 21, 63, 66 and 129)
 
 // ---- workspace (fp16 tensors, padded to whole chunks; tokens >= T are zero)
 struct Workspace {
@@ -166,122 +166,135 @@ __device__ __forceinline__ void store4h(half_t* dst, float a, float b, float c, 
 }
 
 // ---------------------------------------------------------------------------
-// 1. conv1d + SiLU (+ L2 norm) of one head of 128 channels over a run of tokens.
-// Wave = (row b, head, run of RUN tokens); lane l holds channels 2l, 2l+1 of
-// the head (one bf16 pair per token, so a wave reads 256 contiguous bytes per
-// token).  Heads are numbered in channel order: q heads, k heads, v heads.
+// 1. conv1d + SiLU (+ L2 norm) over a run of tokens.  Wave = (row b, group of
+// four consecutive heads in channel order, run of RUN tokens); the 16 lanes of
+// row r of the wave hold head 4 group + r, lane l its channels 8 (l % 16) .. + 7,
+// so one token of the group is one 1 KB read (rows of a group may be of
+// different kinds: q, k or v).  The L2 norm of a q or k head is a 16-lane row
+// reduction.  Tokens are taken three at a time, so the three-token conv history
+// rotates through registers without copies.  VEC16 loads a token's 8 channels
+// as one 16-byte read (rows 16-byte aligned), otherwise as four 4-byte reads.
+template <bool VEC16>
 __global__ __launch_bounds__(256) void prep_kernel(PrepParams p) {
   const int lane = threadIdx.x & 63;
   const int NH = 2 * p.Hk + p.Hv;
+  const int ngroups = (NH + 3) / 4;
   const int64_t nruns = (p.tp + RUN - 1) / RUN;
   // the work item is wave-uniform, so its address arithmetic runs on the scalar unit
   const int64_t item = static_cast<int64_t>(blockIdx.x) * 4 + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  if (item >= static_cast<int64_t>(p.B) * NH * nruns) return;
+  if (item >= static_cast<int64_t>(p.B) * ngroups * nruns) return;
   const int64_t run = item % nruns;
-  const int head = static_cast<int>((item / nruns) % NH);
-  const int64_t b = item / nruns / NH;
+  const int grp = static_cast<int>((item / nruns) % ngroups);
+  const int64_t b = item / nruns / ngroups;
+  const int head = 4 * grp + (lane >> 4);
+  const bool active = head < NH;  // the rows past the last head of a partial group idle
   const int kind = head < p.Hk ? 0 : head < 2 * p.Hk ? 1 : 2;  // q, k, v
-  const int ch = head * 128 + 2 * lane;
-  const float4 w0 = *reinterpret_cast<const float4*>(p.conv_w + static_cast<int64_t>(ch) * KCONV);
-  const float4 w1 = *reinterpret_cast<const float4*>(p.conv_w + static_cast<int64_t>(ch + 1) * KCONV);
+  const int ch = (active ? head : 0) * 128 + 8 * (lane & 15);
+  float w[8][KCONV];
+#pragma unroll
+  for (int c = 0; c < 8; ++c) {
+    const float4 wc = *reinterpret_cast<const float4*>(p.conv_w + static_cast<int64_t>(ch + c) * KCONV);
+    w[c][0] = wc.x;
+    w[c][1] = wc.y;
+    w[c][2] = wc.z;
+    w[c][3] = wc.w;
+  }
   const int64_t t0 = run * RUN;
   const int64_t t1 = min(t0 + RUN, p.tp);
   const bf16_t* xrow = p.x + b * p.x_sb + ch;
+  auto raw_at = [&](int64_t t) -> u32x4 {
+    u32x4 r = {0u, 0u, 0u, 0u};
+    if (active && t >= 0 && t < p.T) {
+      const bf16_t* src = xrow + t * p.x_st;
+      if constexpr (VEC16) {
+        r = *reinterpret_cast<const u32x4*>(src);
+      } else {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) r[e] = reinterpret_cast<const uint32_t*>(src)[e];
+      }
+    }
+    return r;
+  };
+  // raw input of channel c of a token: bf16 pairs (c even: low half)
+  auto chan = [](const u32x4& r, int c) -> float {
+    const uint32_t u = r[c >> 1];
+    return __uint_as_float((c & 1) ? (u & 0xffff0000u) : (u << 16));
+  };
 
-  // raw inputs of the three tokens before t0 (oldest first)
-  float hx[3], hy[3];
+  // history slot s holds the token t0 - 3 + s (slot (t - t0 + 3) % 3 in general)
+  float h[3][8];
 #pragma unroll
   for (int s = 0; s < 3; ++s) {
     const int64_t t = t0 - 3 + s;
-    float vx = 0.f, vy = 0.f;
-    if (t >= 0) {
-      if (t < p.T) {
-        const uint32_t u = *reinterpret_cast<const uint32_t*>(xrow + t * p.x_st);
-        vx = __uint_as_float(u << 16);
-        vy = __uint_as_float(u & 0xffff0000u);
-      }
-    } else if (p.conv_in != nullptr) {
-      vx = p.conv_in[(b * p.C + ch) * (KCONV - 1) + (KCONV - 1) + t];
-      vy = p.conv_in[(b * p.C + ch + 1) * (KCONV - 1) + (KCONV - 1) + t];
+    const u32x4 r = raw_at(t);
+#pragma unroll
+    for (int c = 0; c < 8; ++c) {
+      float val = chan(r, c);
+      if (t < 0 && p.conv_in != nullptr && active) val = p.conv_in[(b * p.C + ch + c) * (KCONV - 1) + (KCONV - 1) + t];
+      h[s][c] = val;
     }
-    hx[s] = vx;
-    hy[s] = vy;
   }
   const float qscale = kind == 0 ? rsqrtf(static_cast<float>(DK)) : 1.f;
-  const int hk = kind == 1 ? head - p.Hk : head;
-  const int hv = head - 2 * p.Hk;
+  const bool norm = kind < 2;
+  half_t* dst = kind == 0 ? p.qn + ((b * p.tp) * p.Hk + head) * DK
+              : kind == 1 ? p.kn + ((b * p.tp) * p.Hk + head - p.Hk) * DK
+                          : p.vn + ((b * p.tp) * p.Hv + head - 2 * p.Hk) * DV;
+  dst += 8 * (lane & 15);
+  const int64_t tstride = static_cast<int64_t>(kind == 2 ? p.Hv : p.Hk) * DK;
 
-  // raw inputs of the next two PU-token groups are in flight while a group is computed
-  uint32_t raw[PU], raw2[PU];
+  // raw inputs of the next two 3-token steps are in flight while a step is computed
+  u32x4 cur[PU], nxt[PU];
 #pragma unroll
   for (int jj = 0; jj < PU; ++jj) {
-    raw[jj] = t0 + jj < p.T ? *reinterpret_cast<const uint32_t*>(xrow + (t0 + jj) * p.x_st) : 0u;
-    raw2[jj] = t0 + PU + jj < p.T ? *reinterpret_cast<const uint32_t*>(xrow + (t0 + PU + jj) * p.x_st) : 0u;
+    cur[jj] = t0 + jj < t1 ? raw_at(t0 + jj) : u32x4{0u, 0u, 0u, 0u};
+    nxt[jj] = t0 + PU + jj < t1 ? raw_at(t0 + PU + jj) : u32x4{0u, 0u, 0u, 0u};
   }
   for (int64_t t = t0; t < t1; t += PU) {
-    uint32_t cur[PU];
+    u32x4 x[PU];
 #pragma unroll
     for (int jj = 0; jj < PU; ++jj) {
-      cur[jj] = raw[jj];
-      raw[jj] = raw2[jj];
+      x[jj] = cur[jj];
+      cur[jj] = nxt[jj];
       const int64_t tn = t + 2 * PU + jj;
-      raw2[jj] = tn < p.T && tn < t1 ? *reinterpret_cast<const uint32_t*>(xrow + tn * p.x_st) : 0u;
+      nxt[jj] = tn < t1 ? raw_at(tn) : u32x4{0u, 0u, 0u, 0u};
     }
-    float y0[PU], y1[PU], ss[PU];
 #pragma unroll
     for (int jj = 0; jj < PU; ++jj) {
-      const float x0 = __uint_as_float(cur[jj] << 16);
-      const float x1 = __uint_as_float(cur[jj] & 0xffff0000u);
-      const float a0 = w0.x * hx[0] + w0.y * hx[1] + w0.z * hx[2] + w0.w * x0;
-      const float a1 = w1.x * hy[0] + w1.y * hy[1] + w1.z * hy[2] + w1.w * x1;
-      hx[0] = hx[1];
-      hx[1] = hx[2];
-      hx[2] = x0;
-      hy[0] = hy[1];
-      hy[1] = hy[2];
-      hy[2] = x1;
+      // token t + jj: history slots jj, jj + 1, jj + 2 (mod 3) hold tokens t + jj - 3 .. - 1
+      float y[8];
+      float ss = 0.f;
       const bool live = t + jj < p.T;
-      y0[jj] = live ? silu_ref(a0) : 0.f;
-      y1[jj] = live ? silu_ref(a1) : 0.f;
-      ss[jj] = y0[jj] * y0[jj] + y1[jj] * y1[jj];
-    }
-    if (kind < 2) {
 #pragma unroll
-      for (int jj = 0; jj < PU; ++jj) {
-        const float r = rsqrtf(wave_sum_dpp(ss[jj]) + 1e-6f) * qscale;
-        y0[jj] *= r;
-        y1[jj] *= r;
+      for (int c = 0; c < 8; ++c) {
+        const float xc = chan(x[jj], c);
+        const float a = w[c][0] * h[jj % 3][c] + w[c][1] * h[(jj + 1) % 3][c] + w[c][2] * h[(jj + 2) % 3][c] + w[c][3] * xc;
+        h[jj % 3][c] = xc;
+        y[c] = live ? silu_ref(a) : 0.f;
+        ss += y[c] * y[c];
       }
-    }
-    half_t* dst = kind == 0 ? p.qn + ((b * p.tp + t) * p.Hk + hk) * DK
-                : kind == 1 ? p.kn + ((b * p.tp + t) * p.Hk + hk) * DK
-                            : p.vn + ((b * p.tp + t) * p.Hv + hv) * DV;
-    const int64_t tstride = static_cast<int64_t>(kind == 2 ? p.Hv : p.Hk) * DK;
+      const float tot = row16_sum(ss);
+      const float r = norm ? rsqrtf(tot + 1e-6f) * qscale : 1.f;
+      if (active && t + jj < t1) {
+        f16x8_v o;
 #pragma unroll
-    for (int jj = 0; jj < PU; ++jj) {
-      f16x2_v pr;
-      pr[0] = static_cast<half_t>(y0[jj]);
-      pr[1] = static_cast<half_t>(y1[jj]);
-      *reinterpret_cast<f16x2_v*>(dst + jj * tstride + 2 * lane) = pr;
+        for (int c = 0; c < 8; ++c) o[c] = static_cast<half_t>(y[c] * r);
+        *reinterpret_cast<f16x8_v*>(dst + (t + jj) * tstride) = o;
+      }
     }
   }
 
   // conv state: the raw inputs of the last K-1 tokens, written by the run holding token T-1
-  if (p.conv_out != nullptr && t0 <= p.T - 1 && p.T - 1 < t1) {
+  if (p.conv_out != nullptr && active && t0 <= p.T - 1 && p.T - 1 < t1) {
 #pragma unroll
     for (int s = 0; s < 3; ++s) {
       const int64_t t = p.T - 3 + s;
-      float vx = 0.f, vy = 0.f;
-      if (t >= 0) {
-        const uint32_t u = *reinterpret_cast<const uint32_t*>(xrow + t * p.x_st);
-        vx = __uint_as_float(u << 16);
-        vy = __uint_as_float(u & 0xffff0000u);
-      } else if (p.conv_in != nullptr) {
-        vx = p.conv_in[(b * p.C + ch) * (KCONV - 1) + (KCONV - 1) + t];
-        vy = p.conv_in[(b * p.C + ch + 1) * (KCONV - 1) + (KCONV - 1) + t];
+      const u32x4 r = raw_at(t);
+#pragma unroll
+      for (int c = 0; c < 8; ++c) {
+        float val = chan(r, c);
+        if (t < 0) val = p.conv_in != nullptr ? p.conv_in[(b * p.C + ch + c) * (KCONV - 1) + (KCONV - 1) + t] : 0.f;
+        p.conv_out[(b * p.C + ch + c) * (KCONV - 1) + s] = val;
       }
-      p.conv_out[(b * p.C + ch) * (KCONV - 1) + s] = vx;
-      p.conv_out[(b * p.C + ch + 1) * (KCONV - 1) + s] = vy;
     }
   }
 }
@@ -894,10 +907,16 @@ extern "C" int qa_chunk_gated_delta_rule(const void* mixed_qkv, int32_t x_dtype,
   pp.Hk = key_heads;
   pp.Hv = value_heads;
   pp.C = C;
-  const int64_t prep_waves = batch * (2 * key_heads + value_heads) * ((ws.tp + RUN - 1) / RUN);
+  const int64_t prep_waves = batch * ((2 * key_heads + value_heads + 3) / 4) * ((ws.tp + RUN - 1) / RUN);
+  QA_REQUIRE(prep_waves <= 4 * static_cast<int64_t>(0x7fffffff), "chunk_gated_delta_rule: too many prep waves");
+  const bool vec16 = x_stride_t % 8 == 0 && x_stride_b % 8 == 0 && (reinterpret_cast<uintptr_t>(mixed_qkv) & 15u) == 0;
   {
     KernelTimer timer_("chunk_prep", stream);
-    hipLaunchKernelGGL(prep_kernel, dim3(static_cast<unsigned>((prep_waves + 3) / 4)), dim3(256), 0, stream, pp);
+    const dim3 grid(static_cast<unsigned>((prep_waves + 3) / 4));
+    if (vec16)
+      hipLaunchKernelGGL(prep_kernel<true>, grid, dim3(256), 0, stream, pp);
+    else
+      hipLaunchKernelGGL(prep_kernel<false>, grid, dim3(256), 0, stream, pp);
   }
   if (int rc = check_launch("chunk_gated_delta_rule prep")) return rc;
 
