@@ -41,6 +41,7 @@ HBM_PEAK_GBS = 8000.0  # MI355X HBM3E, GB/s
 TRAFFIC_DECODE = 1959222089
 TRAFFIC_DELTA = 1636013431
 TRAFFIC_PREFILL = 890087159  # average over the eight per-chunk launches
+TRAFFIC_PROLOGUE = None  # not yet profiled
 SECONDARY_WARM_MS = 100.0  # wall time of untimed steps before each secondary (config 3, 4, 5) measurement
 MFMA_BF16_PEAK_TFLOPS = 2500.0  # MI355X dense bf16/fp16 MFMA, TFLOP/s
 
@@ -297,6 +298,40 @@ def time_prefill(w, steps: int, warmup: int) -> float:
     return _timed(step, steps, warmup, ("paged_prefill",), warm_ms=SECONDARY_WARM_MS)
 
 
+def prologue_workload(pw: dict, device: str, *, seed: int = 1) -> dict:
+    """The full-attention prologue (q/k RMSNorm + partial rotary + K/V append) over all of
+    config 3's new tokens in one launch: q_proj (tokens, H, 2D), k/v_proj (tokens, H_kv, D)
+    bf16, appended at positions prefix_b + n into config 3's pool and tables."""
+    import torch
+
+    batch, new, heads, dim = pw["batch"], pw["new"], pw["q"].shape[1], pw["q"].shape[2]
+    kv_heads = pw["key_pool"].shape[1]
+    tokens = batch * new
+    dgen = torch.Generator(device=device).manual_seed(seed)
+    q_proj = torch.randn((tokens, heads, 2 * dim), generator=dgen, device=device, dtype=torch.bfloat16)
+    k_proj = torch.randn((tokens, kv_heads, dim), generator=dgen, device=device, dtype=torch.bfloat16)
+    v_proj = torch.randn((tokens, kv_heads, dim), generator=dgen, device=device, dtype=torch.bfloat16)
+    qw = (torch.randn((dim,), generator=dgen, device=device) * 0.1).to(torch.bfloat16)
+    kw = (torch.randn((dim,), generator=dgen, device=device) * 0.1).to(torch.bfloat16)
+    cu = torch.arange(0, batch + 1, device=device, dtype=torch.int32) * new
+    starts = pw["prefixes"].to(device=device, dtype=torch.int32)
+    # bytes: the q half of q_proj, k and v read; q, k and v written (2 bytes each)
+    algo = 2 * tokens * dim * (heads + 2 * kv_heads) * 2
+    return {"q_proj": q_proj, "k_proj": k_proj, "v_proj": v_proj, "qw": qw, "kw": kw, "cu": cu, "starts": starts, "new": new,
+            "algo_bytes": algo, "tokens": tokens}
+
+
+def time_prologue(w: dict, pw: dict, steps: int, warmup: int):
+    import hip_ops
+
+    def step():
+        hip_ops.qk_norm_rope_kv_append(w["q_proj"], w["k_proj"], w["v_proj"], w["qw"], w["kw"], pw["key_pool"], pw["value_pool"], pw["tables"],
+                                       w["cu"], w["starts"], pw["bs"], max_new=w["new"], eps=1e-6, rope_theta=10_000_000.0,
+                                       partial_rotary_factor=0.25)
+
+    return _timed(step, steps, warmup, ("qk_norm_rope",), warm_ms=SECONDARY_WARM_MS)
+
+
 # ----------------------------------------------------------------------------- config 5
 
 
@@ -382,6 +417,7 @@ def main() -> int:
     parser.add_argument("--no-delta", action="store_true", help="skip the config-4 secondary measurement")
     parser.add_argument("--no-prefill", action="store_true", help="skip the config-3 secondary measurement")
     parser.add_argument("--no-hybrid", action="store_true", help="skip the config-5 secondary measurement")
+    parser.add_argument("--no-prologue", action="store_true", help="skip the full-attention prologue measurement (config 3 shapes)")
     parser.add_argument("--copy-probe-mib", type=int, default=0,
                         help="first run one plain device copy of this many MiB (reference point for HBM byte counters)")
     parser.add_argument("--cpu-budget", type=float, default=12.0)
@@ -492,6 +528,24 @@ def main() -> int:
                          "kernel": "qa::pfx::prefill_kernel<256>, one launch per 512-token query chunk (kv_append between)",
                          "kernel_ms_per_step": round(pkern["paged_prefill"]["total_ms_per_step"], 4), "kernels": pkern},
         }
+        if not args.no_prologue:
+            ow = prologue_workload(pw, device)
+            oms, okern = time_prologue(ow, pw, max(10, args.steps), max(1, args.warmup))
+            k_ms = okern["qk_norm_rope"]["avg_ms"]
+            ogbs = ow["algo_bytes"] / (k_ms * 1e-3) / 1e9
+            _log(f"bench: attention prologue {oms * 1e3:.1f} us for {ow['tokens']} tokens, {ogbs:.1f} GB/s ({ogbs / HBM_PEAK_GBS:.1%} of HBM peak)")
+            record["secondary_prologue"] = {
+                "metric": "full-attention prologue (q/k RMSNorm + partial RoPE + paged K/V append) HBM GB/s",
+                "value": round(ogbs, 2),
+                "unit": "GB/s",
+                "ms_per_step": round(oms, 4),
+                "config": {"workload": "config 3's 32768 new tokens (8 x 4096, prefix U[0, 8192] seed 0) in one launch", "q_heads": 16,
+                           "kv_heads": 2, "head_dim": 256, "rotary_dim": 64, "rope_theta": 1e7, "block_size": 16},
+                "roofline": {"bound": "hbm", "achieved": round(ogbs, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(ogbs / HBM_PEAK_GBS, 4),
+                             "traffic": TRAFFIC_PROLOGUE, "algo_bytes_per_launch": ow["algo_bytes"], "kernel": "qa::qkr::qk_norm_rope_kernel<4>",
+                             "kernel_avg_us": round(k_ms * 1e3, 2), "kernels": okern},
+            }
+            del ow
         del pw
         torch.cuda.empty_cache()
     if not args.no_hybrid:

@@ -146,7 +146,8 @@ int qa_paged_kv_gather(const qa_paged_kv* kv, int32_t head_dim, int64_t batch,
  * with element strides (q_stride_t, q_stride_h); cu_seqlens (batch+1) and
  * prefix_lens (batch) device index arrays (int32/int64); new token n of
  * sequence b sits at position prefix_lens[b] + n.  Optional gate
- * (total_new, heads*head_dim) bf16 logits: out *= sigmoid(gate).  Writes
+ * bf16 logits, element (n, h, d) at gate[n*gate_stride_t + h*gate_stride_h + d]
+ * (gate_stride_h 0 means head_dim): out *= sigmoid(gate).  Writes
  * output (total_new, heads, head_dim) bf16 contiguous.  bf16 MFMA, head_dim
  * 128 or 256, block size 16, GQA group <= 8, one shared pool.  Replaces the
  * reference's dense multi-token fallback (src/tp_runtime.py:551-610 ->
@@ -156,7 +157,35 @@ int qa_paged_attention_prefill(const void* query, int32_t q_dtype, int64_t q_str
                                int64_t batch, int64_t max_new, int32_t heads, int32_t head_dim,
                                const qa_paged_kv* kv, const void* block_tables, int32_t table_dtype,
                                int64_t table_stride, int64_t max_blocks, int32_t block_size, float scale,
-                               const void* gate, int64_t gate_stride_t, void* output, hipStream_t stream);
+                               const void* gate, int64_t gate_stride_t, int64_t gate_stride_h, void* output,
+                               hipStream_t stream);
+
+/* ---- full-attention prologue: q/k RMSNorm + partial RoPE + K/V append ---- */
+/* For new token n of row b (n in [cu_seqlens[b], cu_seqlens[b+1]), position
+ * starts[b] + n - cu_seqlens[b]): q = q_proj[n, h, 0:head_dim] (element strides
+ * q_stride_t, q_stride_h; the gate half of each q_proj head is left in place for
+ * qa_paged_attention_prefill), k = k_proj[n, g, :], v = v_proj[n, g, :], bf16.
+ * q and k get the reference's RMSNorm with the (1 + w) weight (q_norm_weight,
+ * k_norm_weight: head_dim, bf16 or fp32; eps) and the rotary embedding of their
+ * first rotary_dim elements at the token's position, rounding to bf16 where the
+ * reference's bf16 tensors do.  The bf16 cos/sin come from cos_sin_table
+ * (table_positions, 2, rotary_dim/2) for positions it covers and are computed
+ * from inv_freq (rotary_dim/2 fp32, device) otherwise.  q
+ * goes to q_out (tokens, heads, head_dim) bf16 contiguous; k and v (copied
+ * bit-exactly) go to slot (block_tables[b][pos/bs], pos%bs) of the shared pool
+ * (table entries outside the pool are skipped).  head_dim 64, 128 or 256.
+ * Replaces src/reference_ops.py:343-352 (rms_norm :166-169, rotary_embeddings
+ * :203-213, apply_rotary_pos_emb :216-224), src/tp_runtime.py:511-525 and the
+ * append of src/decode_state.py:271-293 for one layer's new tokens.          */
+int qa_qk_norm_rope_append(const void* q_proj, int64_t q_stride_t, int64_t q_stride_h, const void* k_proj,
+                           int64_t k_stride_t, int64_t k_stride_h, const void* v_proj, int64_t v_stride_t,
+                           int64_t v_stride_h, int32_t act_dtype, const void* q_norm_weight, const void* k_norm_weight,
+                           int32_t weight_dtype, float eps, const float* inv_freq, const void* cos_sin_table,
+                           int64_t table_positions, int32_t rotary_dim,
+                           const void* cu_seqlens, const void* starts, int32_t idx_dtype, int64_t batch, int64_t max_new,
+                           int32_t heads, int32_t head_dim, const qa_paged_kv* kv, const void* block_tables,
+                           int32_t table_dtype, int64_t table_stride, int64_t max_blocks, int32_t block_size, void* q_out,
+                           hipStream_t stream);
 
 /* ---- gated delta-rule linear attention --------------------------------- */
 /* Depthwise causal conv1d over `seq` tokens (+ optional SiLU), fp32 math.

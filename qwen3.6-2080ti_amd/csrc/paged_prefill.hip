@@ -55,7 +55,7 @@ struct Params {
   int table_i64;
   int64_t table_stride, max_blocks;
   const bf16_t* gate;          // (token, H*D) or null
-  int64_t gate_st;
+  int64_t gate_st, gate_sh;
   bf16_t* out;                 // (token, H, D) contiguous
   int64_t B;
   int H, Hkv, G, D;
@@ -372,7 +372,7 @@ __global__ __launch_bounds__(NT) void prefill_kernel(Params p) {
   const float inv = l_part > 0.f ? 1.f / l_part : 0.f;
   const int64_t tok = tok0 + n0 + col;
   bf16_t* orow = p.out + (tok * p.H + h) * static_cast<int64_t>(D);
-  const bf16_t* grow = p.gate != nullptr ? p.gate + tok * p.gate_st + static_cast<int64_t>(h) * D : nullptr;
+  const bf16_t* grow = p.gate != nullptr ? p.gate + tok * p.gate_st + static_cast<int64_t>(h) * p.gate_sh : nullptr;
 #pragma unroll
   for (int t = 0; t < MT; ++t) {
     const int d0 = 16 * t + 4 * quad;
@@ -397,7 +397,8 @@ extern "C" int qa_paged_attention_prefill(const void* query, int32_t q_dtype, in
                                           int64_t batch, int64_t max_new, int32_t heads, int32_t head_dim,
                                           const qa_paged_kv* kv, const void* block_tables, int32_t table_dtype,
                                           int64_t table_stride, int64_t max_blocks, int32_t block_size, float scale,
-                                          const void* gate, int64_t gate_stride_t, void* output, hipStream_t stream) {
+                                          const void* gate, int64_t gate_stride_t, int64_t gate_stride_h, void* output,
+                                          hipStream_t stream) {
   using namespace qa;
   using namespace qa::pfx;
   QA_REQUIRE(kv != nullptr && query && cu_seqlens && prefix_lens && block_tables && output, "paged prefill: pointers must be non-null");
@@ -434,6 +435,7 @@ extern "C" int qa_paged_attention_prefill(const void* query, int32_t q_dtype, in
   p.max_blocks = max_blocks;
   p.gate = reinterpret_cast<const bf16_t*>(gate);
   p.gate_st = gate_stride_t;
+  p.gate_sh = gate_stride_h != 0 ? gate_stride_h : head_dim;
   p.out = reinterpret_cast<bf16_t*>(output);
   p.B = batch;
   p.H = heads;

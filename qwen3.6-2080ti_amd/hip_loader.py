@@ -73,6 +73,12 @@ SIGNATURES: dict[str, tuple[Any, list[Any]]] = {
         [c_void_p, c_void_p, c_int32, c_int64, c_int64, c_int64, c_int64, c_int32, c_int64, c_int32, ctypes.POINTER(PagedKV),
          c_void_p, c_int32, c_int64, c_int64, c_void_p, c_int32, c_int64, c_void_p, c_int32, c_int32, c_void_p],
     ),
+    "qa_qk_norm_rope_append": (
+        c_int32,
+        [c_void_p, c_int64, c_int64, c_void_p, c_int64, c_int64, c_void_p, c_int64, c_int64, c_int32, c_void_p, c_void_p, c_int32,
+         c_float, c_void_p, c_void_p, c_int64, c_int32, c_void_p, c_void_p, c_int32, c_int64, c_int64, c_int32, c_int32, ctypes.POINTER(PagedKV),
+         c_void_p, c_int32, c_int64, c_int64, c_int32, c_void_p, c_void_p],
+    ),
     "qa_paged_kv_gather": (
         c_int32,
         [ctypes.POINTER(PagedKV), c_int32, c_int64, c_void_p, c_int32, c_int64, c_int64, c_int64, c_int32, c_void_p, c_void_p,
@@ -109,7 +115,7 @@ SIGNATURES: dict[str, tuple[Any, list[Any]]] = {
     "qa_paged_attention_prefill": (
         c_int32,
         [c_void_p, c_int32, c_int64, c_int64, c_void_p, c_void_p, c_int32, c_int64, c_int64, c_int32, c_int32, ctypes.POINTER(PagedKV),
-         c_void_p, c_int32, c_int64, c_int64, c_int32, c_float, c_void_p, c_int64, c_void_p, c_void_p],
+         c_void_p, c_int32, c_int64, c_int64, c_int32, c_float, c_void_p, c_int64, c_int64, c_void_p, c_void_p],
     ),
 }
 

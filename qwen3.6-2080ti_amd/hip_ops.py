@@ -611,8 +611,10 @@ def paged_attention_prefill(
     ``query`` ``(total_new, H, D)`` bf16; ``cu_seqlens`` ``(B+1,)`` and
     ``prefix_lens`` ``(B,)`` device index arrays; the new tokens' K/V must
     already be appended to ``key_pool``/``value_pool`` ``(P, H_kv, bs, D)`` at
-    positions ``prefix_b + n``.  ``gate`` ``(total_new, H*D)`` bf16 logits give
-    ``out * sigmoid(gate)`` (``src/reference_ops.py:338-340,360``).  Returns
+    positions ``prefix_b + n``.  ``gate`` ``(total_new, H*D)`` bf16 logits, or a
+    ``(total_new, H, D)`` view with a contiguous last dimension (such as the second half of
+    each ``q_proj`` head, read in place), give ``out * sigmoid(gate)``
+    (``src/reference_ops.py:338-340,360``).  Returns
     ``(total_new, H, D)`` bf16.
     """
     lib = L.load_library()
@@ -629,17 +631,136 @@ def paged_attention_prefill(
     _require(cu_seqlens.shape[0] == batch + 1, "cu_seqlens must have batch + 1 entries")
     tokens, heads, head_dim = query.shape
     gate_c = None
+    gate_sh = 0
     if gate is not None:
         _require_cuda(gate, "gate", device)
-        _require(gate.dtype == torch.bfloat16 and gate.shape == (tokens, heads * head_dim), "gate must be (tokens, heads*head_dim) bfloat16")
-        gate_c = gate.contiguous()
+        _require(gate.dtype == torch.bfloat16, "gate must be bfloat16")
+        if gate.dim() == 3:  # (tokens, heads, head_dim) view, e.g. the second half of each q_proj head
+            _require(gate.shape == (tokens, heads, head_dim), "gate must be (tokens, heads*head_dim) or (tokens, heads, head_dim)")
+            gate_c = gate if gate.stride(-1) == 1 else gate.contiguous()
+            gate_sh = gate_c.stride(1)
+        else:
+            _require(gate.shape == (tokens, heads * head_dim), "gate must be (tokens, heads*head_dim) or (tokens, heads, head_dim)")
+            gate_c = gate.contiguous()
     tables = block_tables.contiguous()
     out = torch.empty((tokens, heads, head_dim), dtype=torch.bfloat16, device=device)
     status = lib.qa_paged_attention_prefill(
         _ptr(query), _code(query), query.stride(0), query.stride(1), _ptr(cu_seqlens.contiguous()), _ptr(prefix_lens.contiguous()),
         _code(cu_seqlens), batch, int(max_new), heads, head_dim, ctypes.byref(desc), _ptr(tables), _code(tables), tables.stride(0),
-        tables.shape[1], int(block_size), float(scale or 0.0), _ptr(gate_c), 0 if gate_c is None else gate_c.stride(0), _ptr(out),
+        tables.shape[1], int(block_size), float(scale or 0.0), _ptr(gate_c), 0 if gate_c is None else gate_c.stride(0), gate_sh, _ptr(out),
         _stream(device),
     )
     L.check(lib, status, "paged_attention_prefill")
     return out
+
+
+_INV_FREQ: dict[tuple[int, float, str], torch.Tensor] = {}
+
+
+def rope_inv_freq(rotary_dim: int, rope_theta: float, device: torch.device) -> torch.Tensor:
+    """``inv_freq`` of ``rotary_embeddings`` (``src/reference_ops.py:203-213``), computed as the
+    reference computes it (fp32 torch on the CPU), moved to ``device`` once per
+    (rotary_dim, theta, device)."""
+    key = (int(rotary_dim), float(rope_theta), str(device))
+    cached = _INV_FREQ.get(key)
+    if cached is None:
+        inv = 1.0 / (float(rope_theta) ** (torch.arange(0, rotary_dim, 2, dtype=torch.float32) / rotary_dim))
+        cached = inv.to(device)
+        _INV_FREQ[key] = cached
+    return cached
+
+
+_COS_SIN: dict[tuple[int, float, str], torch.Tensor] = {}
+
+
+def rope_cos_sin_table(rotary_dim: int, rope_theta: float, positions: int, device: torch.device) -> torch.Tensor:
+    """bf16 ``(positions, 2, rotary_dim/2)`` cos and sin of ``pos * inv_freq``, computed with the
+    torch CPU operations of ``rotary_embeddings`` (``src/reference_ops.py:203-213``: fp32 angles,
+    fp32 cos/sin, cast to bf16) so the values are the reference's bit for bit; cached per
+    (rotary_dim, theta, device) and regrown when more positions are asked for."""
+    key = (int(rotary_dim), float(rope_theta), str(device))
+    cached = _COS_SIN.get(key)
+    if cached is None or cached.shape[0] < positions:
+        freqs = torch.outer(torch.arange(positions, dtype=torch.float32), rope_inv_freq(rotary_dim, rope_theta, torch.device("cpu")))
+        table = torch.stack((freqs.cos(), freqs.sin()), dim=1).to(torch.bfloat16).contiguous()
+        cached = table.to(device)
+        _COS_SIN[key] = cached
+    return cached
+
+
+def qk_norm_rope_kv_append(
+    q_proj: torch.Tensor,
+    k_proj: torch.Tensor,
+    v_proj: torch.Tensor,
+    q_norm_weight: torch.Tensor,
+    k_norm_weight: torch.Tensor,
+    key_pool: torch.Tensor,
+    value_pool: torch.Tensor,
+    block_tables: torch.Tensor,
+    cu_seqlens: torch.Tensor,
+    starts: torch.Tensor,
+    block_size: int,
+    *,
+    max_new: int,
+    eps: float,
+    rope_theta: float,
+    partial_rotary_factor: float,
+    table_positions: int = 131072,
+) -> tuple[torch.Tensor, torch.Tensor]:
+    """Prologue of a full-attention layer over packed new tokens, in one launch.
+
+    ``q_proj`` ``(tokens, H, 2D)`` (or ``(tokens, H*2D)``), ``k_proj``/``v_proj`` ``(tokens, H_kv, D)``
+    (or ``(tokens, H_kv*D)``), bf16, as the projections produce them; row ``b`` owns tokens
+    ``cu_seqlens[b]:cu_seqlens[b+1]`` at positions ``starts[b] + n``.  Applies the reference's
+    ``rms_norm`` with the ``(1 + w)`` weight and ``apply_rotary_pos_emb`` with
+    ``rotary_dim = int(D * partial_rotary_factor)`` (``src/reference_ops.py:343-347``,
+    ``src/tp_runtime.py:511-525``), appends k and v to the shared pool ``(P, H_kv, bs, D)`` at
+    those positions (the reference's ``cache.append``, ``src/decode_state.py:271-293``, without
+    repeating heads), and returns ``(query (tokens, H, D) bf16, gate (tokens, H, D) view of
+    q_proj)`` ready for :func:`paged_attention_prefill` or, for one token per row, decode.
+    The bf16 cos/sin of positions below ``table_positions`` come from :func:`rope_cos_sin_table`;
+    the kernel computes those of later positions itself.
+    """
+    lib = L.load_library()
+    _require_cuda(q_proj, "q_proj")
+    device = q_proj.device
+    for tensor, name in ((k_proj, "k_proj"), (v_proj, "v_proj"), (q_norm_weight, "q_norm_weight"), (k_norm_weight, "k_norm_weight"),
+                         (key_pool, "key_pool"), (value_pool, "value_pool"), (block_tables, "block_tables"), (cu_seqlens, "cu_seqlens"),
+                         (starts, "starts")):
+        _require_cuda(tensor, name, device)
+    _require(key_pool.dim() == 4, "qk_norm_rope_kv_append needs a shared pool (blocks, kv_heads, block_size, head_dim)")
+    _, kv_heads, _, head_dim = key_pool.shape
+    tokens = q_proj.shape[0]
+    q3 = q_proj.view(tokens, -1, 2 * head_dim) if q_proj.dim() == 2 else q_proj
+    k3 = k_proj.view(tokens, kv_heads, head_dim) if k_proj.dim() == 2 else k_proj
+    v3 = v_proj.view(tokens, kv_heads, head_dim) if v_proj.dim() == 2 else v_proj
+    heads = q3.shape[1]
+    _require(q3.dim() == 3 and q3.shape[2] == 2 * head_dim, "q_proj must be (tokens, heads, 2*head_dim)")
+    _require(k3.shape == (tokens, kv_heads, head_dim) and v3.shape == (tokens, kv_heads, head_dim), "k_proj/v_proj must be (tokens, kv_heads, head_dim)")
+    for tensor, name in ((q3, "q_proj"), (k3, "k_proj"), (v3, "v_proj"), (key_pool, "key_pool")):
+        _require(tensor.dtype == torch.bfloat16 and tensor.stride(-1) == 1, f"{name} must be bfloat16 with a contiguous last dimension")
+    _float_dtype(q_norm_weight, "q_norm_weight")
+    _require(q_norm_weight.dtype == k_norm_weight.dtype and q_norm_weight.shape == (head_dim,) and k_norm_weight.shape == (head_dim,),
+             "norm weights must be (head_dim,) of one dtype")
+    for tensor, name in ((cu_seqlens, "cu_seqlens"), (starts, "starts"), (block_tables, "block_tables")):
+        _index_dtype(tensor, name)
+    _require(cu_seqlens.dtype == starts.dtype, "cu_seqlens and starts must share a dtype")
+    batch = starts.shape[0]
+    _require(cu_seqlens.shape[0] == batch + 1, "cu_seqlens must have batch + 1 entries")
+    tables = block_tables.contiguous() if block_tables.dim() == 2 else block_tables.contiguous().view(1, -1).expand(batch, -1)
+    rotary_dim = int(head_dim * partial_rotary_factor)
+    inv_freq = rope_inv_freq(rotary_dim, rope_theta, device)
+    cos_sin = rope_cos_sin_table(rotary_dim, rope_theta, int(table_positions), device) if rotary_dim > 0 and table_positions > 0 else None
+    qw = q_norm_weight.contiguous()
+    kw = k_norm_weight.contiguous()
+    desc = _pool_descriptor(key_pool, value_pool, "shared")
+    query = torch.empty((tokens, heads, head_dim), dtype=torch.bfloat16, device=device)
+    status = lib.qa_qk_norm_rope_append(
+        _ptr(q3), q3.stride(0), q3.stride(1), _ptr(k3), k3.stride(0), k3.stride(1), _ptr(v3), v3.stride(0), v3.stride(1), _code(q3),
+        _ptr(qw), _ptr(kw), _code(qw), float(eps), _ptr(inv_freq), _ptr(cos_sin), 0 if cos_sin is None else cos_sin.shape[0], rotary_dim,
+        _ptr(cu_seqlens.contiguous()), _ptr(starts.contiguous()),
+        _code(cu_seqlens), batch, int(max_new), heads, head_dim, ctypes.byref(desc), _ptr(tables), _code(tables), tables.stride(0),
+        tables.shape[1], int(block_size), _ptr(query), _stream(device),
+    )
+    L.check(lib, status, "qk_norm_rope_kv_append")
+    return query, q3[..., head_dim:]

@@ -120,8 +120,10 @@ def recurrent_rule_case(ro, seed: int, batch: int, seq: int, heads: int, dk: int
     return case
 
 
-def full_attention_case(ro, seed: int, seq: int, heads: int, kv_heads: int, head_dim: int) -> dict:
-    """``full_attention`` (no cache, positions 0..seq-1) on seeded q/k/v/gate projections."""
+def full_attention_case(ro, seed: int, seq: int, heads: int, kv_heads: int, head_dim: int, position_offset: int = 0) -> dict:
+    """``full_attention`` (no cache, positions ``position_offset + 0..seq-1``) on seeded q/k/v/gate
+    projections; also records the projections, the norm weights and the rotary parameters, which
+    pin the q/k RMSNorm + rotary prologue."""
     g = torch.Generator().manual_seed(seed)
     batch = 1
     q_proj = torch.randn(batch, seq, heads * head_dim * 2, generator=g).to(torch.bfloat16)
@@ -146,7 +148,8 @@ def full_attention_case(ro, seed: int, seq: int, heads: int, kv_heads: int, head
 
     ro.apply_rotary_pos_emb = recording
     try:
-        out = ro.full_attention(torch.zeros(batch, seq, 8, dtype=torch.bfloat16), mapping, cfg, weights, cache=None, position_offset=0)
+        out = ro.full_attention(torch.zeros(batch, seq, 8, dtype=torch.bfloat16), mapping, cfg, weights, cache=None,
+                                position_offset=position_offset)
     finally:
         ro.apply_rotary_pos_emb = original
     gate = q_proj.view(batch, seq, heads, head_dim * 2)[..., head_dim:]
@@ -155,6 +158,9 @@ def full_attention_case(ro, seed: int, seq: int, heads: int, kv_heads: int, head
         "q_bf16": bits(seen["q"]), "k_bf16": bits(seen["k"]), "v_bf16": bits(v_proj.view(batch, seq, kv_heads, head_dim)),
         "gate_bf16": bits(gate), "out_bf16": bits(out.view(batch, seq, heads, head_dim)),
         "shape": np.array([batch, seq, heads, kv_heads, head_dim], dtype=np.int64),
+        "q_proj_bf16": bits(q_proj.view(batch, seq, heads, head_dim * 2)), "k_proj_bf16": bits(k_proj.view(batch, seq, kv_heads, head_dim)),
+        "q_norm_bf16": bits(q_norm), "k_norm_bf16": bits(k_norm),
+        "rope": np.array([cfg.rope_theta, cfg.partial_rotary_factor, cfg.rms_norm_eps, position_offset], dtype=np.float64),
     }
 
 
@@ -165,6 +171,7 @@ def main(reference_root: str) -> None:
     torch.set_num_threads(1)
     np.savez_compressed(HERE / "linear_attention_core.npz", **linear_attention_case(ro, 20240, 1, 40, 1, 2))
     np.savez_compressed(HERE / "full_attention_prefill.npz", **full_attention_case(ro, 20241, 20, 4, 2, 128))
+    np.savez_compressed(HERE / "full_attention_rope_d256.npz", **full_attention_case(ro, 20244, 12, 4, 2, 256, position_offset=3000))
     np.savez_compressed(HERE / "recurrent_rule_bf16.npz", **recurrent_rule_case(ro, 20242, 2, 7, 3, 16, 8, False))
     np.savez_compressed(HERE / "recurrent_rule_bf16_state.npz", **recurrent_rule_case(ro, 20243, 1, 5, 2, 16, 8, True))
     for f in sorted(HERE.glob("*.npz")):

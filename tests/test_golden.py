@@ -58,3 +58,26 @@ def test_full_attention_probs_cast_matches_reference() -> None:
     gate = bf16(v["gate_bf16"]).reshape(batch, seq, heads * dim)
     out = oa.dense_attention(q, k, val, position_offset=0, gate=gate)
     _ulp_close(out.transpose(1, 2), bf16(v["out_bf16"]))
+
+
+def _prologue_inputs(v: dict) -> tuple:
+    batch, seq, heads, kv_heads, head_dim = (int(x) for x in v["shape"])
+    theta, factor, eps, offset = (float(x) for x in v["rope"])
+    q_proj = bf16(v["q_proj_bf16"]).reshape(batch * seq, heads, 2 * head_dim)
+    k_proj = bf16(v["k_proj_bf16"]).reshape(batch * seq, kv_heads, head_dim)
+    positions = torch.arange(int(offset), int(offset) + seq).repeat(batch)
+    return q_proj, k_proj, bf16(v["q_norm_bf16"]), bf16(v["k_norm_bf16"]), positions, theta, factor, eps, (batch, seq, heads, kv_heads, head_dim)
+
+
+def test_qk_norm_rope_matches_reference_bit_for_bit() -> None:
+    from oracle import rope
+
+    for name in ("full_attention_prefill", "full_attention_rope_d256"):
+        v = load(name)
+        q_proj, k_proj, qw, kw, positions, theta, factor, eps, (batch, seq, heads, kv_heads, head_dim) = _prologue_inputs(v)
+        q, k = rope.qk_norm_rope(q_proj[..., :head_dim], k_proj, qw, kw, positions, eps=eps, rope_theta=theta, partial_rotary_factor=factor)
+        # the fixture holds the reference's (B, H, S, D) q and (B, H_kv, S, D) k after RMSNorm and rotation
+        q_ref = bf16(v["q_bf16"]).permute(0, 2, 1, 3).reshape(batch * seq, heads, head_dim)
+        k_ref = bf16(v["k_bf16"]).permute(0, 2, 1, 3).reshape(batch * seq, kv_heads, head_dim)
+        torch.testing.assert_close(q, q_ref, atol=0, rtol=0)
+        torch.testing.assert_close(k, k_ref, atol=0, rtol=0)
