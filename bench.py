@@ -38,10 +38,10 @@ HBM_PEAK_GBS = 8000.0  # MI355X HBM3E, GB/s
 # profiles/paged_prefill_config3.md): FETCH_SIZE scaled by 2.0 and WRITE_SIZE by 1.0, the factors
 # a plain 1 GiB device copy reads back in the same runs. Counters need rocprofv3, so the figures
 # are the committed profile's, not measured live.
-TRAFFIC_DECODE = 1959222089
-TRAFFIC_DELTA = 1636013431
-TRAFFIC_PREFILL = 890087159  # average over the eight per-chunk launches
-TRAFFIC_PROLOGUE = None  # not yet profiled
+TRAFFIC_DECODE = 1959210677
+TRAFFIC_DELTA = 1636029928
+TRAFFIC_PREFILL = 889734060  # average over the eight per-chunk launches
+TRAFFIC_PROLOGUE = 675541424
 SECONDARY_WARM_MS = 100.0  # wall time of untimed steps before each secondary (config 3, 4, 5) measurement
 MFMA_BF16_PEAK_TFLOPS = 2500.0  # MI355X dense bf16/fp16 MFMA, TFLOP/s
 
