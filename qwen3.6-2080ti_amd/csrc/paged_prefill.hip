@@ -14,17 +14,22 @@
 // transposing LDS read), so V is staged as loaded.  S^T in the MFMA accumulator
 // layout (lane: keys 4(l/16)+r, position l%16) is exactly the B-operand layout
 // of the PV product, so P stays in registers.  Online softmax per position
-// (column), fp32; P rounded to bf16 (the reference rounds probs to the query
-// dtype before PV, src/reference_ops.py:358).
+// (column), fp32, with a lazily moved reference max; P rounded to bf16 (the
+// reference rounds probs to the query dtype before PV, src/reference_ops.py:358).
 //
-// Pipeline: K and V tiles are double-buffered in LDS with K one tile ahead, so
-// iteration t issues the S products of tile t+1 next to the softmax of tile t
-// (MFMA and VALU work of one wave overlap), then the PV products of tile t,
-// with K of tile t+2 and V of tile t+1 staged from registers at the start of the
-// iteration and the loads of K(t+3) and V(t+2) issued during it; one barrier per
-// tile.  The row's block table is read into LDS once; global loads are
-// issued a tile ahead into registers and barriers order LDS only, so those
-// loads stay in flight across them.
+// Tiles reach LDS by global_load_lds_dwordx4 (global memory straight into LDS, no
+// registers, no LDS write instructions): rows of D bf16 back to back, 16-byte chunks
+// XOR-swizzled by row.  K and V are double-buffered with K one tile ahead: iteration t
+// starts the copies of K(t+2) and V(t+1), then (phase A) the S products of tile t+1
+// interleaved with the softmax of tile t, then (phase B) the PV products of tile t;
+// LDS operand reads run kAhead products ahead and a scheduling fence after each step
+// keeps that order.  Each wave waits for its own copies before the one barrier per
+// tile.  The row's block table is read into LDS once.  Workgroups are dispatched
+// longest row first (see the ranking at the top of the kernel).
+//
+// The kernel is written for HPW query heads per wave; one head per wave (two waves per
+// SIMD, 8 waves) measured faster than two (one wave per SIMD, where the accumulators of
+// both heads no longer fit the VGPRs and the compiler moves them to and from AGPRs).
 #include "qa_common.h"
 
 namespace qa {
@@ -35,12 +40,20 @@ typedef short short4_v __attribute__((ext_vector_type(4)));
 typedef float floatx4_v __attribute__((ext_vector_type(4)));
 typedef unsigned int u32x4_v __attribute__((ext_vector_type(4)));
 
-constexpr int NW = 8;          // waves
-constexpr int NT = NW * 64;
+constexpr int HMAX = 8;        // largest GQA group (query heads per KV head) a workgroup serves
 constexpr int POS = 16;        // new positions per workgroup
 constexpr int KT = 64;         // keys per tile
 constexpr int BS = 16;         // cache block size
 constexpr int MAXB = 4096;     // block-table entries of a row kept in LDS (65536 keys)
+constexpr int kRankRows = 64;  // batches up to this many rows are dispatched longest row first
+
+// HPW query heads per wave, so HMAX / HPW waves per workgroup.
+template <int D, int HPW>
+struct Cfg {
+  static constexpr int NW = HMAX / HPW;
+  static constexpr int NT = 64 * NW;
+  static constexpr int DC = D / 8;         // 16-byte chunks per K or V row
+};
 
 struct Params {
   const bf16_t* q;
@@ -62,25 +75,19 @@ struct Params {
   float scale;
 };
 
+// query heads per wave of the launched kernels
+constexpr int kHeadsPerWave = 1;
+// LDS operand reads issued ahead of the products that use them
+constexpr int kAhead = 4;
+
 template <int D>
 struct Smem {
-  // halfs per K and V row: a 32-byte pad (a row stride of 8 mod 16 dwords) measured fewest
-  // LDS bank conflicts for both the 16-row operand reads of K and the transposing reads of V
-  static constexpr int kLdK = D + 16;
-  static constexpr int kLdV = D + 16;
-  static constexpr int kKBytes = KT * kLdK * 2;
-  static constexpr int kVBytes = KT * kLdV * 2;
-  static constexpr int kBytes = 2 * kKBytes + 2 * kVBytes + MAXB * 4;  // two K and two V tiles + block table
+  // K and V tiles hold KT rows of D bf16 back to back; 16-byte chunk c of row r sits at
+  // chunk position c ^ 2 (r mod 8), which spreads the 16-row operand reads of K and the
+  // transposing reads of V over the LDS banks as a 32-byte row pad would
+  static constexpr int kTileBytes = KT * D * 2;
+  static constexpr int kBytes = 4 * kTileBytes + MAXB * 4;  // two K and two V tiles + block table
 };
-
-// Pieces of one tile's K (or V) in flight: thread c loads the 16-byte pieces
-// (key, chunk) c + j NT.
-template <int D>
-struct TileRegs {
-  static constexpr int KP = KT * (D / 8) / NT;  // pieces per thread
-  u32x4_v k[KP];
-};
-
 
 __device__ __forceinline__ int64_t rd_index(const void* base, int is64, int64_t i) {
   return is64 ? reinterpret_cast<const int64_t*>(base)[i] : reinterpret_cast<const int32_t*>(base)[i];
@@ -92,30 +99,6 @@ __device__ __forceinline__ int64_t block_of(const Params& p, int b, int64_t lb, 
   if (lb >= p.max_blocks) return -1;
   const int64_t e = rd_index(p.tables, p.table_i64, b * p.table_stride + lb);
   return e >= 0 && e < p.num_blocks ? e : -1;
-}
-
-// Per-thread element offsets inside a block: the key and chunk of each piece are
-// fixed by the thread index, only the block changes per tile.
-template <int D>
-struct TileLanes {
-  int kblk[TileRegs<D>::KP];   // which of the tile's blocks each piece lies in
-  int koff[TileRegs<D>::KP];   // element offset inside that block
-  int kkey[TileRegs<D>::KP];   // key index inside the tile
-};
-
-template <int D>
-__device__ __forceinline__ TileLanes<D> tile_lanes(const Params& p, int tid) {
-  constexpr int DC = D / 8;
-  TileLanes<D> ln;
-#pragma unroll
-  for (int j = 0; j < TileRegs<D>::KP; ++j) {
-    const int c = tid + j * NT;
-    const int key = c / DC;
-    ln.kkey[j] = key;
-    ln.kblk[j] = key / BS;
-    ln.koff[j] = static_cast<int>((key % BS) * p.sT) + 8 * (c % DC);
-  }
-  return ln;
 }
 
 __device__ __forceinline__ int pick(const int4& v, int i) { return i == 0 ? v.x : i == 1 ? v.y : i == 2 ? v.z : v.w; }
@@ -136,256 +119,446 @@ __device__ __forceinline__ int4 tile_phys(const Params& p, int b, int64_t key0, 
   return make_int4(blk(0), blk(1), blk(2), blk(3));
 }
 
-// Loads the pieces of one tile of the pool at base (K or V); keys past kv_len and absent blocks read as zero.
-template <int D>
-__device__ __forceinline__ void load_pieces(const Params& p, int64_t key0, int64_t kv_len, const bf16_t* base, const int4& phys,
-                                            const TileLanes<D>& ln, TileRegs<D>& r) {
-  // A tile whose keys all lie below kv_len in present blocks (all but the last tiles of a
-  // row): unpredicated loads from the block's address (scalar) plus the piece offset.
-  // (D = 256: piece j of every thread lies in block j of the tile)
-  if (D == 256 && key0 + KT <= kv_len && phys.x >= 0 && phys.y >= 0 && phys.z >= 0 && phys.w >= 0) {
-    static_assert(D != 256 || NT / (D / 8) == BS, "one step of pieces is one block");
+// One 16-byte copy from global memory into LDS per lane (global_load_lds_dwordx4): lane l's
+// 16 bytes land at LDS byte lds + 16 l (lds wave-uniform, through M0).  Issued as inline
+// assembly so that the compiler does not make every later LDS read wait for the copy (it
+// cannot tell which buffer a copy writes); the kernel waits for the copies itself
+// (s_waitcnt vmcnt(0)) before the barrier that hands a tile to the other waves.  M0 is
+// restored afterwards; one wait state separates the M0 write from the copy.
+__device__ __forceinline__ void lds_copy16(const void* src, uint32_t lds) {
+  uint32_t saved;
+  asm volatile(
+      "s_mov_b32 %0, m0\n\t"
+      "s_mov_b32 m0, %1\n\t"
+      "s_nop 0\n\t"
+      "global_load_lds_dwordx4 %2, off\n\t"
+      "s_mov_b32 m0, %0"
+      : "=&s"(saved)
+      : "s"(lds), "v"(src)
+      : "memory");
+}
+
+// s_waitcnt vmcnt(0) through the builtin, so that the compiler's own wait tracking knows every
+// vector-memory load has completed here (an inline-assembly wait would leave it assuming the
+// loads before the loop may still be in flight, and it would then wait for all vector-memory
+// operations, the tile copies included, at their first use inside the loop).
+__device__ __forceinline__ void wait_vm0() { __builtin_amdgcn_s_waitcnt(0x0F70); }
+
+// The lane's part of every copy of a tile.  A copy is one 1 KB region of the tile (64
+// chunks, RPR = 64 / DC whole rows); copy j of wave w covers region R = j NW + w, i.e. rows
+// R RPR + [0, RPR), and lane l the chunk position l of it: row R RPR + l / DC, position
+// l % DC, where it stores the logical chunk (l % DC) ^ 2 (row mod 8).  As NW RPR is a multiple
+// of 8, row mod 8 and so the chunk the lane fetches do not depend on j.
+template <class C>
+struct CopyLane {
+  static constexpr int RPR = 64 / C::DC;         // rows per region
+  static constexpr int STEP = RPR * C::NW;       // rows per copy step of the workgroup
+  static constexpr int NC = KT / STEP;           // copies per wave per tile
+  static constexpr bool kOneBlock = BS % STEP == 0;  // a step lies in one block, block j STEP / BS
+  static_assert(C::DC <= 64 && 64 % C::DC == 0 && BS % RPR == 0 && STEP % 8 == 0 && KT % STEP == 0,
+                "regions cover whole rows inside one block");
+  int lrow;  // row of the lane's chunk inside its region
+  int goff;  // element offset of that chunk from the region's first row: lrow sT + 8 c
+  int woff;  // kOneBlock: goff plus the wave's rows inside the step, (w RPR) sT
+};
+
+template <class C>
+__device__ __forceinline__ CopyLane<C> copy_lane(const Params& p, int wave, int lane) {
+  CopyLane<C> cl;
+  cl.lrow = lane / C::DC;
+  const int row = wave * CopyLane<C>::RPR + cl.lrow;  // its row in copy 0
+  const int c = (lane % C::DC) ^ (2 * (row & 7));
+  cl.goff = static_cast<int>(cl.lrow * p.sT) + 8 * c;
+  cl.woff = static_cast<int>(row * p.sT) + 8 * c;
+  return cl;
+}
+
+// Copies key tile key0 of the pool at base (K or V) into the tile at LDS byte dst (smem_lds
+// is the LDS address of smem).  Keys past kv_len and keys of absent blocks are written as
+// zeros by ds_write instead.
+template <class C>
+__device__ __forceinline__ void copy_tile(const Params& p, int64_t key0, int64_t kv_len, const bf16_t* base, const int4& phys,
+                                          const CopyLane<C>& cl, unsigned char* smem, uint32_t smem_lds, uint32_t dst, int wave,
+                                          int lane) {
+  using L = CopyLane<C>;
+  if (key0 + KT <= kv_len && phys.x >= 0 && phys.y >= 0 && phys.z >= 0 && phys.w >= 0) {
 #pragma unroll
-    for (int j = 0; j < TileRegs<D>::KP; ++j) {
-      const char* bp = reinterpret_cast<const char*>(base + static_cast<int64_t>(pick(phys, j)) * p.sP);
-      r.k[j] = *reinterpret_cast<const u32x4_v*>(bp + 2u * static_cast<uint32_t>(ln.koff[j]));
+    for (int j = 0; j < L::NC; ++j) {
+      const uint32_t lds = dst + 1024u * static_cast<uint32_t>(j * C::NW + wave);
+      if constexpr (L::kOneBlock) {
+        lds_copy16(base + static_cast<int64_t>(pick(phys, j * L::STEP / BS)) * p.sP + static_cast<int64_t>((j * L::STEP) % BS) * p.sT +
+                       cl.woff,
+                   lds);
+      } else {
+        const int row0 = (j * C::NW + wave) * L::RPR;
+        lds_copy16(base + static_cast<int64_t>(pick(phys, row0 / BS)) * p.sP + static_cast<int64_t>(row0 % BS) * p.sT + cl.goff, lds);
+      }
     }
     return;
   }
 #pragma unroll
-  for (int j = 0; j < TileRegs<D>::KP; ++j) {
-    const int blk = pick(phys, ln.kblk[j]);
-    r.k[j] = blk >= 0 && key0 + ln.kkey[j] < kv_len ? *reinterpret_cast<const u32x4_v*>(base + static_cast<int64_t>(blk) * p.sP + ln.koff[j])
-                                                   : u32x4_v{0u, 0u, 0u, 0u};
+  for (int j = 0; j < L::NC; ++j) {
+    const int row0 = (j * C::NW + wave) * L::RPR;
+    const uint32_t lds = dst + 1024u * static_cast<uint32_t>(j * C::NW + wave);
+    const int blk = pick(phys, row0 / BS);
+    if (blk >= 0 && key0 + row0 + cl.lrow < kv_len) {
+      lds_copy16(base + static_cast<int64_t>(blk) * p.sP + static_cast<int64_t>(row0 % BS) * p.sT + cl.goff, lds);
+    } else {
+      *reinterpret_cast<u32x4_v*>(smem + (lds - smem_lds) + 16 * lane) = u32x4_v{0u, 0u, 0u, 0u};
+    }
   }
 }
 
-template <int D, int LD>
-__device__ __forceinline__ void stage_pieces(bf16_t* dst, const TileRegs<D>& r, int tid) {
-  constexpr int DC = D / 8;
-#pragma unroll
-  for (int j = 0; j < TileRegs<D>::KP; ++j) {
-    const int c = tid + j * NT;
-    const int key = c / DC;
-    *reinterpret_cast<u32x4_v*>(dst + key * LD + 8 * (c - key * DC)) = r.k[j];
-  }
-}
-
-// Four bf16 of a column of a row-major LDS tile, for each lane, by
-// ds_read_b64_tr_b16: lane i of 16-lane group g reads the 8 bytes at
-// X[row_g + i / 4][c0 + 4 (i % 4)] and receives X[row_g + e][c0 + i], e = 0..3.
-__device__ __forceinline__ short4_v tr_read(const bf16_t* tile, int ld, int row_g, int c0, int lane) {
+// ds_read_b64_tr_b16 at LDS byte address addr: lane i of a 16-lane group reads 8 bytes
+// (four bf16 of one row) and receives element i of the four rows its group read.
+__device__ __forceinline__ short4_v tr_read_at(const unsigned char* addr) {
   typedef __attribute__((address_space(3))) short4_v lds_s4;
-  const int i = lane & 15;
-  return __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s4*)(tile + (row_g + (i >> 2)) * ld + c0 + 4 * (i & 3)));
+  return __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s4*)addr);
 }
 
-template <int D>
-__global__ __launch_bounds__(NT) void prefill_kernel(Params p) {
+template <int D, int HPW>
+__global__ __launch_bounds__(64 * (HMAX / HPW)) void prefill_kernel(Params p) {
+  using C = Cfg<D, HPW>;
   constexpr int KCH = D / 32;  // k-chunks of S^T
   constexpr int MT = D / 16;   // output dim tiles
-  constexpr int DC = D / 8;
+  constexpr int ST = KT / 16;  // 16-key sub-tiles of a tile
+  constexpr int TB = Smem<D>::kTileBytes;
   extern __shared__ __align__(16) unsigned char smem[];
-  auto Kbuf = [&](int i) { return reinterpret_cast<bf16_t*>(smem + i * Smem<D>::kKBytes); };
-  auto Vbuf = [&](int i) { return reinterpret_cast<bf16_t*>(smem + 2 * Smem<D>::kKBytes + i * Smem<D>::kVBytes); };
-  int* s_phys = reinterpret_cast<int*>(smem + 2 * Smem<D>::kKBytes + 2 * Smem<D>::kVBytes);
+  const uint32_t smem_lds = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(smem));
+  // tiles: K(0) K(1) V(0) V(1), then the block table
+  int* s_phys = reinterpret_cast<int*>(smem + 4 * TB);
 
-  const int pt = blockIdx.x;
-  const int bg = blockIdx.y;
-  const int b = bg / p.Hkv;
-  const int g = bg - b * p.Hkv;
+  const int tid = threadIdx.x;
+  // Dispatch order: workgroups start in blockIdx order (x fastest), and one workgroup's time
+  // is proportional to the keys its positions see, which differ by up to the longest prefix
+  // between rows.  So blockIdx.y walks the rows from the longest (prefix + new tokens) down
+  // (ranked here for up to kRankRows rows, else in index order) and blockIdx.x the position
+  // tiles from the last one down: longest first, which keeps the tail of the launch short.
+  const int rr = blockIdx.y / p.Hkv;
+  const int g = blockIdx.y - rr * p.Hkv;
+  const int pt = static_cast<int>(gridDim.x) - 1 - static_cast<int>(blockIdx.x);
+  int b = rr;
+  if (p.B <= kRankRows) {
+    int64_t* s_len = reinterpret_cast<int64_t*>(smem);             // row lengths
+    int* s_order = reinterpret_cast<int*>(smem + 8 * kRankRows);   // rows by rank
+    const int nb = static_cast<int>(p.B);
+    if (tid < nb)
+      s_len[tid] = rd_index(p.prefix, p.idx_i64, tid) + rd_index(p.cu, p.idx_i64, tid + 1) - rd_index(p.cu, p.idx_i64, tid);
+    lds_barrier();
+    if (tid < nb) {
+      const int64_t mine = s_len[tid];
+      int rank = 0;
+      for (int u = 0; u < nb; ++u) {
+        const int64_t other = s_len[u];
+        rank += other > mine || (other == mine && u < tid);
+      }
+      s_order[rank] = tid;
+    }
+    lds_barrier();
+    b = __builtin_amdgcn_readfirstlane(s_order[rr]);
+    lds_barrier();  // the tile buffers the ranking used are written next
+  }
   const int64_t tok0 = rd_index(p.cu, p.idx_i64, b);
   const int64_t n_new = rd_index(p.cu, p.idx_i64, b + 1) - tok0;
   const int64_t n0 = static_cast<int64_t>(pt) * POS;
   if (n0 >= n_new) return;
   const int64_t prefix = rd_index(p.prefix, p.idx_i64, b);
   const int64_t kv_len = prefix + min(n_new, n0 + POS);  // keys any of the 16 positions may see
-  const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int col = lane & 15;   // position within the tile (MFMA column)
   const int quad = lane >> 4;
-  const bool active = wave < p.G;
-  const int h = g * p.G + (active ? wave : 0);
+  const int hw0 = HPW * wave;  // the wave's first head within the GQA group
+  const bool active = hw0 < p.G;
   const int64_t my_pos = prefix + n0 + col;  // absolute position of this lane's column
   const bool row_live = n0 + col < n_new;
 
   // the row's block table, once (entries outside the pool become -1)
   const int64_t nlb = min64((kv_len + BS - 1) / BS, p.max_blocks);
-  for (int64_t lb = tid; lb < min64(nlb, MAXB); lb += NT) {
+  for (int64_t lb = tid; lb < min64(nlb, MAXB); lb += C::NT) {
     const int64_t e = rd_index(p.tables, p.table_i64, b * p.table_stride + lb);
     s_phys[lb] = e >= 0 && e < p.num_blocks ? static_cast<int>(e) : -1;
   }
 
-  // Q^T operand (B of S^T = K Q^T): lane holds position col, dims 32i + 8*quad + [0, 8)
-  bf16x8_v qreg[KCH];
-  {
+  const bf16_t* kb = p.kbase + static_cast<int64_t>(g) * p.sG;
+  const bf16_t* vb = p.vbase + static_cast<int64_t>(g) * p.sG;
+  const int64_t ntiles = (kv_len + KT - 1) / KT;
+  const CopyLane<C> cl = copy_lane<C>(p, wave, lane);
+  auto Kt = [&](int i) { return smem_lds + static_cast<uint32_t>(i * TB); };
+  auto Vt = [&](int i) { return smem_lds + static_cast<uint32_t>((2 + i) * TB); };
+  lds_barrier();  // s_phys
+  // Block ids of tiles kt .. kt+2 (wave-uniform), each looked up once
+  int4 phys_cur = tile_phys(p, b, 0, kv_len, s_phys, nlb);
+  int4 phys_n1 = tile_phys(p, b, KT, kv_len, s_phys, nlb);
+  int4 phys_n2 = tile_phys(p, b, 2 * KT, kv_len, s_phys, nlb);
+  copy_tile<C>(p, 0, kv_len, kb, phys_cur, cl, smem, smem_lds, Kt(0), wave, lane);
+  copy_tile<C>(p, 0, kv_len, vb, phys_cur, cl, smem, smem_lds, Vt(0), wave, lane);
+
+  // Q^T operands (B of S^T = K Q^T), one per head of the wave: lane holds position col,
+  // dims 32i + 8*quad + [0, 8); a head past the group reads as zeros and is never stored
+  bf16x8_v qreg[HPW][KCH];
+#pragma unroll
+  for (int hh = 0; hh < HPW; ++hh) {
+    const bool live = hw0 + hh < p.G;
+    const int h = g * p.G + (live ? hw0 + hh : 0);
     const bf16_t* qrow = p.q + (tok0 + n0 + col) * p.q_st + static_cast<int64_t>(h) * p.q_sh + 8 * quad;
 #pragma unroll
     for (int i = 0; i < KCH; ++i) {
       uint4 raw = make_uint4(0, 0, 0, 0);
-      if (active && row_live) raw = *reinterpret_cast<const uint4*>(qrow + 32 * i);
-      qreg[i] = __builtin_bit_cast(bf16x8_v, raw);
+      if (live && row_live) raw = *reinterpret_cast<const uint4*>(qrow + 32 * i);
+      qreg[hh][i] = __builtin_bit_cast(bf16x8_v, raw);
     }
   }
-  floatx4_v o[MT];
+  floatx4_v o[HPW][MT];
 #pragma unroll
-  for (int t = 0; t < MT; ++t) o[t] = floatx4_v{0.f, 0.f, 0.f, 0.f};
-  float m_run = -INFINITY;  // running max of the log2-domain scores
-  float l_part = 0.f;
+  for (int hh = 0; hh < HPW; ++hh)
+#pragma unroll
+    for (int t = 0; t < MT; ++t) o[hh][t] = floatx4_v{0.f, 0.f, 0.f, 0.f};
+  float m_run[HPW];  // running max of the log2-domain scores
+  float l_part[HPW];
+#pragma unroll
+  for (int hh = 0; hh < HPW; ++hh) {
+    m_run[hh] = -INFINITY;
+    l_part[hh] = 0.f;
+  }
   const float scale_l2 = p.scale * 1.4426950408889634f;
 
-  const bf16_t* kb = p.kbase + static_cast<int64_t>(g) * p.sG;
-  const bf16_t* vb = p.vbase + static_cast<int64_t>(g) * p.sG;
-  const int64_t ntiles = (kv_len + KT - 1) / KT;
-  lds_barrier();  // s_phys
-  const TileLanes<D> ln = tile_lanes<D>(p, tid);
+  // Operand addresses inside a tile (bytes).  K: row 16 st + col, chunk 4 i + quad, whose
+  // position is 16 (i >> 2) + 4 ((i & 3) ^ (r7 >> 1)) + (quad ^ 2 (r7 & 1)) with r7 = col & 7.
+  int koff[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) koff[i] = col * 2 * D + 64 * (i ^ ((col & 7) >> 1)) + 16 * (quad ^ (2 * (col & 1)));
+  // V, transposing reads: lane i of group quad reads row 4 quad + i / 4 (+ 32 jj, + 16), logical
+  // chunk 2 t + e with e = (i >> 1) & 1, bytes 8 (i & 1) of it; its position is 2 (t ^ r7) + e
+  // with r7 = (4 quad + i / 4) & 7
+  int voff[8];
+  {
+    const int li = lane & 15;
+    const int vr = 4 * quad + (li >> 2);
+#pragma unroll
+    for (int t = 0; t < 8; ++t) voff[t] = vr * 2 * D + 32 * (t ^ (vr & 7)) + 16 * ((li >> 1) & 1) + 8 * (li & 1);
+  }
 
-  // S^T of a tile from the K buffer kbuf (unscaled: nothing waits on the products here)
-  auto scores = [&](const bf16_t* kbuf, floatx4_v* s) {
+  // S^T of the tile in K buffer kbuf for every head of the wave (unscaled: nothing waits on
+  // the products here); each K operand read feeds HPW products
+  auto scores = [&](int kbuf, floatx4_v (&s)[HPW][ST]) {
+    const unsigned char* kt_lds = smem + kbuf * TB;
 #pragma unroll
-    for (int st = 0; st < KT / 16; ++st) {
-      floatx4_v acc = {0.f, 0.f, 0.f, 0.f};
-      const bf16_t* arow = kbuf + (16 * st + col) * Smem<D>::kLdK + 8 * quad;
+    for (int st = 0; st < ST; ++st) {
+      floatx4_v acc[HPW];
 #pragma unroll
-      for (int i = 0; i < KCH; ++i)
-        acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(*reinterpret_cast<const bf16x8_v*>(arow + 32 * i), qreg[i], acc, 0, 0, 0);
-      s[st] = acc;
+      for (int hh = 0; hh < HPW; ++hh) acc[hh] = floatx4_v{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int i = 0; i < KCH; ++i) {
+        const bf16x8_v a = *reinterpret_cast<const bf16x8_v*>(kt_lds + koff[i & 3] + 256 * (i >> 2) + st * 32 * D);
+#pragma unroll
+        for (int hh = 0; hh < HPW; ++hh) acc[hh] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, qreg[hh][i], acc[hh], 0, 0, 0);
+      }
+#pragma unroll
+      for (int hh = 0; hh < HPW; ++hh) s[hh][st] = acc[hh];
     }
   };
 
-  // Block ids of tiles kt .. kt+2 (wave-uniform), each looked up once and before any
-  // tile load of the iteration is issued: a table read that misses the LDS copy waits
-  // on global memory, and that wait would also wait for the tile loads in flight.
-  int4 phys_cur = tile_phys(p, b, 0, kv_len, s_phys, nlb);
-  int4 phys_n1 = tile_phys(p, b, KT, kv_len, s_phys, nlb);
-  int4 phys_n2 = tile_phys(p, b, 2 * KT, kv_len, s_phys, nlb);
-
-  // prologue: K and V of tile 0 and K of tile 1 staged; loads of K(2) and V(1) in flight
-  TileRegs<D> rk, rv;
-  load_pieces<D>(p, 0, kv_len, kb, phys_cur, ln, rk);
-  load_pieces<D>(p, 0, kv_len, vb, phys_cur, ln, rv);
-  stage_pieces<D, Smem<D>::kLdK>(Kbuf(0), rk, tid);
-  stage_pieces<D, Smem<D>::kLdV>(Vbuf(0), rv, tid);
-  if (ntiles > 1) {
-    load_pieces<D>(p, KT, kv_len, kb, phys_n1, ln, rk);
-    stage_pieces<D, Smem<D>::kLdK>(Kbuf(1), rk, tid);
-  }
+  // prologue: K(0) and V(0) landed, then K(1) copied while S(0) is computed
+  wait_vm0();
   lds_barrier();
-  load_pieces<D>(p, 2 * KT, kv_len, kb, phys_n2, ln, rk);
-  load_pieces<D>(p, KT, kv_len, vb, phys_n1, ln, rv);
-  floatx4_v s_cur[KT / 16];
-  if (active) scores(Kbuf(0), s_cur);
-  lds_barrier();  // every wave has read K(0) before iteration 0 stages K(2) over it
+  if (ntiles > 1) copy_tile<C>(p, KT, kv_len, kb, phys_n1, cl, smem, smem_lds, Kt(1), wave, lane);
+  floatx4_v s_cur[HPW][ST];
+  if (active) scores(0, s_cur);
+  wait_vm0();
+  lds_barrier();  // K(1) landed; every wave has read K(0)
 
+  // Iteration kt: copies of K(kt+2) (into the buffer of K(kt), whose products were taken in
+  // the previous iteration) and V(kt+1) (into the buffer of V(kt-1)) run while S of tile
+  // kt+1 (MFMA) goes next to the softmax of tile kt (VALU), then O += V(kt)^T P(kt); one
+  // barrier per tile, after this wave's copies have landed.
   for (int64_t kt = 0; kt < ntiles; ++kt) {
     const int64_t key0 = kt * KT;
     const int cb = static_cast<int>(kt & 1);
-    // ---- stage K of tile kt+2 and V of tile kt+1 (loaded during the previous iteration;
-    // their buffers were last read before the previous barrier).  Unconditional: past the
-    // last tile the pieces are zeros and those buffers are never read, and a conditional
-    // stage would leave a path on which the compiler makes later loads wait for earlier ones.
-    stage_pieces<D, Smem<D>::kLdK>(Kbuf(cb), rk, tid);
-    stage_pieces<D, Smem<D>::kLdV>(Vbuf(cb ^ 1), rv, tid);
     const int4 phys_n3 = tile_phys(p, b, key0 + 3 * KT, kv_len, s_phys, nlb);
-    // the loads of K(kt+3) go out now and those of V(kt+2) after the S products, so their
-    // issue overlaps this iteration's work
-    load_pieces<D>(p, key0 + 3 * KT, kv_len, kb, phys_n3, ln, rk);
-    floatx4_v s_nxt[KT / 16];
-    short4_v pb[KT / 16];  // this tile's probabilities, bf16, in the S^T accumulator layout
+    if (kt + 2 < ntiles) copy_tile<C>(p, key0 + 2 * KT, kv_len, kb, phys_n2, cl, smem, smem_lds, Kt(cb), wave, lane);
+    if (kt + 1 < ntiles) copy_tile<C>(p, key0 + KT, kv_len, vb, phys_n1, cl, smem, smem_lds, Vt(cb ^ 1), wave, lane);
+    floatx4_v s_nxt[HPW][ST];
     if (active) {
-      // ---- S of the next tile (MFMA) next to the softmax of this one (VALU)
-      if (kt + 1 < ntiles) scores(Kbuf(cb ^ 1), s_nxt);
-#pragma unroll
-      for (int st = 0; st < KT / 16; ++st) s_cur[st] *= scale_l2;
-      // only tiles that reach past the workgroup's first position, past the last
-      // visible key or over an absent block need a mask (wave-uniform test)
+      // only tiles that reach past the workgroup's first position, past the last visible
+      // key or over an absent block need a mask (wave-uniform test)
       if (!(key0 + KT - 1 <= prefix + n0 && key0 + KT <= kv_len && phys_cur.x >= 0 && phys_cur.y >= 0 && phys_cur.z >= 0 &&
             phys_cur.w >= 0)) {
         // last key offset of this tile the lane's column may see (-1: none)
         const int lim = static_cast<int>(max64(-1, min64(KT - 1, min(my_pos, kv_len - 1) - key0)));
 #pragma unroll
-        for (int st = 0; st < KT / 16; ++st)
+        for (int hh = 0; hh < HPW; ++hh)
 #pragma unroll
-          for (int r = 0; r < 4; ++r)
-            if (!(row_live && 16 * st + 4 * quad + r <= lim && pick(phys_cur, st) >= 0)) s_cur[st][r] = -INFINITY;
+          for (int st = 0; st < ST; ++st)
+#pragma unroll
+            for (int r = 0; r < 4; ++r)
+              if (!(row_live && 16 * st + 4 * quad + r <= lim && pick(phys_cur, st) >= 0)) s_cur[hh][st][r] = -INFINITY;
       }
-      float mx = -INFINITY;
+
+      // ---- softmax of this tile, cut into slices that phase A spreads between its products:
+      // slices 0 .. HPW*ST-1 scale one sub-tile and fold it into the lane's max; the next HPW
+      // finish one head's max over the four lanes of a column (permlane swaps) and its
+      // lazily rescaled running max; the next HPW*ST*2 turn two scores into probabilities
+      float mx[HPW], m_use[HPW], alpha[HPW], psum[HPW];
+      bool grow = false;  // some running max moved while the accumulators held something
+      short4_v pb[HPW][ST];  // probabilities, bf16, in the S^T accumulator layout
 #pragma unroll
-      for (int st = 0; st < KT / 16; ++st)
+      for (int hh = 0; hh < HPW; ++hh) {
+        mx[hh] = -INFINITY;
+        psum[hh] = 0.f;
+      }
+      constexpr int kSlices = HPW * ST + HPW + 2 * HPW * ST;
+      auto slice = [&](int k) {
+        if (k < HPW * ST) {
+          const int hh = k / ST, st = k % ST;
+          s_cur[hh][st] *= scale_l2;
+          mx[hh] = fmaxf(mx[hh], fmaxf(fmaxf(s_cur[hh][st][0], s_cur[hh][st][1]), fmaxf(s_cur[hh][st][2], s_cur[hh][st][3])));
+          asm volatile("" : "+v"(s_cur[hh][st]), "+v"(mx[hh]));
+        } else if (k < HPW * ST + HPW) {
+          const int hh = k - HPW * ST;
+          const auto r32 = __builtin_amdgcn_permlane32_swap(__float_as_uint(mx[hh]), __float_as_uint(mx[hh]), false, false);
+          const float m2 = fmaxf(__uint_as_float(r32[0]), __uint_as_float(r32[1]));
+          const auto r16 = __builtin_amdgcn_permlane16_swap(__float_as_uint(m2), __float_as_uint(m2), false, false);
+          const float m4 = fmaxf(__uint_as_float(r16[0]), __uint_as_float(r16[1]));
+          // lazy rescaling: the running max only moves when this tile's max exceeds it by
+          // more than 8 (log2 units), so probabilities stay below 2^8 and the accumulators are
+          // rarely rescaled; the result is the same softmax, as numerator and denominator
+          // share the reference point
+          const float m_old = m_run[hh];
+          const bool moves = m4 > m_old + 8.f;
+          alpha[hh] = moves ? __builtin_amdgcn_exp2f(m_old - m4) : 1.f;
+          grow = grow || (moves && m_old != -INFINITY);
+          m_run[hh] = moves ? m4 : m_old;
+          m_use[hh] = m_run[hh] == -INFINITY ? 0.f : m_run[hh];
+          asm volatile("" : "+v"(m_use[hh]), "+v"(alpha[hh]));
+        } else {
+          const int j = k - HPW * ST - HPW;
+          const int hh = j / (2 * ST), st = (j / 2) % ST, r0 = 2 * (j & 1);
 #pragma unroll
-        for (int r = 0; r < 4; ++r) mx = fmaxf(mx, s_cur[st][r]);
-      mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
-      mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-      const float m_new = fmaxf(m_run, mx);
-      const float m_use = m_new == -INFINITY ? 0.f : m_new;
-      const float alpha = __builtin_amdgcn_exp2f(m_run - m_use);
-      m_run = m_new;
-      float psum = 0.f;
-#pragma unroll
-      for (int st = 0; st < KT / 16; ++st)
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const float pr = __builtin_amdgcn_exp2f(s_cur[st][r] - m_use);
-          psum += pr;
-          pb[st][r] = static_cast<short>(f32_to_bf16(pr));
+          for (int r = r0; r < r0 + 2; ++r) {
+            const float pr = __builtin_amdgcn_exp2f(s_cur[hh][st][r] - m_use[hh]);
+            psum[hh] += pr;
+            pb[hh][st][r] = static_cast<short>(f32_to_bf16(pr));
+          }
+          // keep the slice in its step (the compiler would otherwise sink it to its first use)
+          asm volatile("" : "+v"(pb[hh][st]), "+v"(psum[hh]));
         }
-      l_part = l_part * alpha + psum;
-      // the accumulators only need rescaling when some position's running max moved
-      if (__ballot(alpha != 1.f) != 0) {
+      };
+
+      // ---- phase A: S of the next tile (past the last tile the products read a stale buffer
+      // and are never used).  Step s issues the K read of step s+kAhead, the products of step s
+      // (sub-tile s % ST, k-chunk s / ST: the ST * HPW accumulators rotate, so no product waits
+      // on the one before it) and softmax slice s; a fence after each step keeps that order.
+      {
+        constexpr int NS = ST * KCH;
+        const unsigned char* kt_lds = smem + (cb ^ 1) * TB;
+        auto kread = [&](int st_) {
+          const int st = st_ % ST, i = st_ / ST;
+          return *reinterpret_cast<const bf16x8_v*>(kt_lds + koff[i & 3] + 256 * (i >> 2) + st * 32 * D);
+        };
 #pragma unroll
-        for (int t = 0; t < MT; ++t) o[t] *= alpha;
+        for (int hh = 0; hh < HPW; ++hh)
+#pragma unroll
+          for (int st = 0; st < ST; ++st) s_nxt[hh][st] = floatx4_v{0.f, 0.f, 0.f, 0.f};
+        bf16x8_v kop[kAhead + 1];
+#pragma unroll
+        for (int st_ = 0; st_ < kAhead; ++st_) kop[st_] = kread(st_);
+#pragma unroll
+        for (int st_ = 0; st_ < NS; ++st_) {
+          if (st_ + kAhead < NS) kop[(st_ + kAhead) % (kAhead + 1)] = kread(st_ + kAhead);
+          const int st = st_ % ST, i = st_ / ST;
+#pragma unroll
+          for (int hh = 0; hh < HPW; ++hh)
+            s_nxt[hh][st] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kop[st_ % (kAhead + 1)], qreg[hh][i], s_nxt[hh][st], 0, 0, 0);
+          if (st_ < kSlices) slice(st_);
+          __builtin_amdgcn_sched_barrier(0);
+        }
+#pragma unroll
+        for (int k = NS; k < kSlices; ++k) slice(k);
+      }
+#pragma unroll
+      for (int hh = 0; hh < HPW; ++hh) l_part[hh] = l_part[hh] * alpha[hh] + psum[hh];
+      if (__ballot(grow) != 0) {
+#pragma unroll
+        for (int hh = 0; hh < HPW; ++hh)
+#pragma unroll
+          for (int t = 0; t < MT; ++t) o[hh][t] *= alpha[hh];
+      }
+
+      // ---- phase B: O^T += V^T P, 32 keys per v_mfma_f32_16x16x32_bf16: the reduction index
+      // k = 8 (l/16) + e of lane l stands for key 4 (l/16) + e of sub-tile 2j (e < 4) and of
+      // sub-tile 2j + 1 (e >= 4), so the B operand is the lane's own P of the two sub-tiles and
+      // the A operand two transposing reads of V rows, shared by the wave's heads.  Step u
+      // issues the reads of step u+kAhead and the products of step u (dim tile u % MT).
+      {
+        constexpr int NU = (KT / 32) * MT;
+        const unsigned char* vt_lds = smem + (2 + cb) * TB;
+        bf16x8_v bop[HPW][KT / 32];
+#pragma unroll
+        for (int hh = 0; hh < HPW; ++hh)
+#pragma unroll
+          for (int jj = 0; jj < KT / 32; ++jj)
+            bop[hh][jj] = __builtin_bit_cast(bf16x8_v, __builtin_shufflevector(pb[hh][2 * jj], pb[hh][2 * jj + 1], 0, 1, 2, 3, 4, 5, 6, 7));
+        auto vread = [&](int u) {
+          const int jj = u / MT, t = u % MT;
+          const unsigned char* va = vt_lds + voff[t & 7] + 256 * (t >> 3) + 32 * jj * 2 * D;
+          const short4_v a0 = tr_read_at(va);
+          const short4_v a1 = tr_read_at(va + 16 * 2 * D);
+          return __builtin_bit_cast(bf16x8_v, __builtin_shufflevector(a0, a1, 0, 1, 2, 3, 4, 5, 6, 7));
+        };
+        bf16x8_v vop[kAhead + 1];
+#pragma unroll
+        for (int u = 0; u < kAhead; ++u) vop[u] = vread(u);
+#pragma unroll
+        for (int u = 0; u < NU; ++u) {
+          if (u + kAhead < NU) vop[(u + kAhead) % (kAhead + 1)] = vread(u + kAhead);
+          const int jj = u / MT, t = u % MT;
+#pragma unroll
+          for (int hh = 0; hh < HPW; ++hh) o[hh][t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vop[u % (kAhead + 1)], bop[hh][jj], o[hh][t], 0, 0, 0);
+          __builtin_amdgcn_sched_barrier(0);
+        }
       }
     }
-    load_pieces<D>(p, key0 + 2 * KT, kv_len, vb, phys_n2, ln, rv);
-    if (active) {
-      // ---- O^T += V^T P, 32 keys per v_mfma_f32_16x16x32_bf16: the reduction index
-      // k = 8 (l/16) + e of lane l stands for key 4 (l/16) + e of sub-tile 2j (e < 4)
-      // and of sub-tile 2j + 1 (e >= 4), so the B operand is the lane's own P of the
-      // two sub-tiles and the A operand two transposing reads of V rows
-      const bf16_t* vt = Vbuf(cb);
-#pragma unroll
-      for (int jj = 0; jj < KT / 32; ++jj) {
-        const bf16x8_v bop = __builtin_bit_cast(bf16x8_v, __builtin_shufflevector(pb[2 * jj], pb[2 * jj + 1], 0, 1, 2, 3, 4, 5, 6, 7));
-#pragma unroll
-        for (int t = 0; t < MT; ++t) {
-          const short4_v a0 = tr_read(vt, Smem<D>::kLdV, 32 * jj + 4 * quad, 16 * t, lane);
-          const short4_v a1 = tr_read(vt, Smem<D>::kLdV, 32 * jj + 16 + 4 * quad, 16 * t, lane);
-          const bf16x8_v av = __builtin_bit_cast(bf16x8_v, __builtin_shufflevector(a0, a1, 0, 1, 2, 3, 4, 5, 6, 7));
-          o[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, bop, o[t], 0, 0, 0);
-          if ((t & 3) == 3) __builtin_amdgcn_sched_barrier(0);  // bound the operand loads in flight
-        }
-      }
-    }
+    wait_vm0();  // this wave's copies have landed
     lds_barrier();
 #pragma unroll
-    for (int st = 0; st < KT / 16; ++st) s_cur[st] = s_nxt[st];
+    for (int hh = 0; hh < HPW; ++hh)
+#pragma unroll
+      for (int st = 0; st < ST; ++st) s_cur[hh][st] = s_nxt[hh][st];
     phys_cur = phys_n1;
     phys_n1 = phys_n2;
     phys_n2 = phys_n3;
   }
 
   if (!active) return;
-  l_part += __shfl_xor(l_part, 16, 64);
-  l_part += __shfl_xor(l_part, 32, 64);
+#pragma unroll
+  for (int hh = 0; hh < HPW; ++hh) {
+    l_part[hh] += __shfl_xor(l_part[hh], 16, 64);
+    l_part[hh] += __shfl_xor(l_part[hh], 32, 64);
+  }
   if (!row_live) return;
-  const float inv = l_part > 0.f ? 1.f / l_part : 0.f;
   const int64_t tok = tok0 + n0 + col;
-  bf16_t* orow = p.out + (tok * p.H + h) * static_cast<int64_t>(D);
-  const bf16_t* grow = p.gate != nullptr ? p.gate + tok * p.gate_st + static_cast<int64_t>(h) * p.gate_sh : nullptr;
 #pragma unroll
-  for (int t = 0; t < MT; ++t) {
-    const int d0 = 16 * t + 4 * quad;
-    float v[4];
+  for (int hh = 0; hh < HPW; ++hh) {
+    if (hw0 + hh >= p.G) break;
+    const int h = g * p.G + hw0 + hh;
+    const float inv = l_part[hh] > 0.f ? 1.f / l_part[hh] : 0.f;
+    bf16_t* orow = p.out + (tok * p.H + h) * static_cast<int64_t>(D);
+    const bf16_t* grow = p.gate != nullptr ? p.gate + tok * p.gate_st + static_cast<int64_t>(h) * p.gate_sh : nullptr;
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      v[r] = o[t][r] * inv;
-      if (grow != nullptr) v[r] *= 1.f / (1.f + __expf(-bf16_to_f32(grow[d0 + r])));
+    for (int t = 0; t < MT; ++t) {
+      const int d0 = 16 * t + 4 * quad;
+      float v[4];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        v[r] = o[hh][t][r] * inv;
+        if (grow != nullptr) v[r] *= 1.f / (1.f + __expf(-bf16_to_f32(grow[d0 + r])));
+      }
+      uint2 packed;
+      packed.x = static_cast<uint32_t>(f32_to_bf16(v[0])) | (static_cast<uint32_t>(f32_to_bf16(v[1])) << 16);
+      packed.y = static_cast<uint32_t>(f32_to_bf16(v[2])) | (static_cast<uint32_t>(f32_to_bf16(v[3])) << 16);
+      *reinterpret_cast<uint2*>(orow + d0) = packed;
     }
-    uint2 packed;
-    packed.x = static_cast<uint32_t>(f32_to_bf16(v[0])) | (static_cast<uint32_t>(f32_to_bf16(v[1])) << 16);
-    packed.y = static_cast<uint32_t>(f32_to_bf16(v[2])) | (static_cast<uint32_t>(f32_to_bf16(v[3])) << 16);
-    *reinterpret_cast<uint2*>(orow + d0) = packed;
   }
 }
 
@@ -407,7 +580,7 @@ extern "C" int qa_paged_attention_prefill(const void* query, int32_t q_dtype, in
   QA_REQUIRE(head_dim == 128 || head_dim == 256, "paged prefill: head_dim must be 128 or 256");
   QA_REQUIRE(block_size == BS, "paged prefill: block_size must be 16");
   QA_REQUIRE(kv->kv_heads > 0 && heads % kv->kv_heads == 0, "paged prefill: query heads must be a multiple of KV heads");
-  QA_REQUIRE(heads / kv->kv_heads <= NW, "paged prefill: GQA group larger than %d", NW);
+  QA_REQUIRE(heads / kv->kv_heads <= HMAX, "paged prefill: GQA group larger than %d", HMAX);
   QA_REQUIRE(kv->row_key_ptrs == nullptr && kv->key && kv->value, "paged prefill: needs one shared pool");
   QA_REQUIRE(kv->stride_token % 8 == 0 && kv->stride_block % 8 == 0 && kv->stride_head % 8 == 0 &&
                  ((reinterpret_cast<uintptr_t>(kv->key) | reinterpret_cast<uintptr_t>(kv->value)) & 15u) == 0,
@@ -444,22 +617,24 @@ extern "C" int qa_paged_attention_prefill(const void* query, int32_t q_dtype, in
   p.D = head_dim;
   p.scale = scale > 0.f ? scale : 1.0f / sqrtf(static_cast<float>(head_dim));
   dim3 grid(static_cast<unsigned>(ceil_div(max_new, POS)), static_cast<unsigned>(batch * kv->kv_heads));
+  using C256 = Cfg<256, kHeadsPerWave>;
+  using C128 = Cfg<128, kHeadsPerWave>;
   static bool attr_set = false;
   if (!attr_set) {
-    hipError_t err = hipFuncSetAttribute(reinterpret_cast<const void*>(&prefill_kernel<256>), hipFuncAttributeMaxDynamicSharedMemorySize,
-                                         Smem<256>::kBytes);
+    hipError_t err = hipFuncSetAttribute(reinterpret_cast<const void*>(&prefill_kernel<256, kHeadsPerWave>),
+                                         hipFuncAttributeMaxDynamicSharedMemorySize, Smem<256>::kBytes);
     if (err == hipSuccess)
-      err = hipFuncSetAttribute(reinterpret_cast<const void*>(&prefill_kernel<128>), hipFuncAttributeMaxDynamicSharedMemorySize,
-                                Smem<128>::kBytes);
+      err = hipFuncSetAttribute(reinterpret_cast<const void*>(&prefill_kernel<128, kHeadsPerWave>),
+                                hipFuncAttributeMaxDynamicSharedMemorySize, Smem<128>::kBytes);
     if (err != hipSuccess) return fail("paged prefill: cannot reserve %d bytes of LDS: %s", Smem<256>::kBytes, hipGetErrorString(err));
     attr_set = true;
   }
   {
     KernelTimer timer_("paged_prefill", stream);
     if (head_dim == 256) {
-      hipLaunchKernelGGL(prefill_kernel<256>, grid, dim3(NT), Smem<256>::kBytes, stream, p);
+      hipLaunchKernelGGL((prefill_kernel<256, kHeadsPerWave>), grid, dim3(C256::NT), Smem<256>::kBytes, stream, p);
     } else {
-      hipLaunchKernelGGL(prefill_kernel<128>, grid, dim3(NT), Smem<128>::kBytes, stream, p);
+      hipLaunchKernelGGL((prefill_kernel<128, kHeadsPerWave>), grid, dim3(C128::NT), Smem<128>::kBytes, stream, p);
     }
   }
   return check_launch("paged prefill");
