@@ -40,7 +40,7 @@ HBM_PEAK_GBS = 8000.0  # MI355X HBM3E, GB/s
 # are the committed profile's, not measured live.
 TRAFFIC_DECODE = 1959210677
 TRAFFIC_DELTA = 1636029928
-TRAFFIC_PREFILL = 889734060  # average over the eight per-chunk launches
+TRAFFIC_PREFILL = 888455186  # average over the eight per-chunk launches
 TRAFFIC_PROLOGUE = 675541424
 SECONDARY_WARM_MS = 100.0  # wall time of untimed steps before each secondary (config 3, 4, 5) measurement
 MFMA_BF16_PEAK_TFLOPS = 2500.0  # MI355X dense bf16/fp16 MFMA, TFLOP/s
@@ -525,7 +525,7 @@ def main() -> int:
                        "prefix": "U[0, 8192] seed 0", "q_heads": 16, "kv_heads": 2, "head_dim": 256, "block_size": 16, "query_chunk": 512},
             "roofline": {"bound": "mfma", "achieved": round(ptf, 2), "peak": MFMA_BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
                          "frac": round(ptf / MFMA_BF16_PEAK_TFLOPS, 4), "traffic": TRAFFIC_PREFILL, "algo_flop_per_launch": pw["flops"],
-                         "kernel": "qa::pfx::prefill_kernel<256>, one launch per 512-token query chunk (kv_append between)",
+                         "kernel": "qa::pfx::prefill_kernel<256, 1>, one launch per 512-token query chunk (kv_append between)",
                          "kernel_ms_per_step": round(pkern["paged_prefill"]["total_ms_per_step"], 4), "kernels": pkern},
         }
         if not args.no_prologue:
