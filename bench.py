@@ -34,7 +34,7 @@ for _p in (REPO_ROOT, PACKAGE_DIR):
 
 HBM_PEAK_GBS = 8000.0  # MI355X HBM3E, GB/s
 # HBM bytes per launch of the decode kernel from rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE
-# (profiles/decode_partial_mfma_config2.md, profiles/chunk_gated_delta_config4.md,
+# (profiles/decode_partial_mfma_config2.md, profiles/chunk_gated_delta_config4.md, profiles/gated_rms_norm_config4.md,
 # profiles/paged_prefill_config3.md): FETCH_SIZE scaled by 2.0 and WRITE_SIZE by 1.0, the factors
 # a plain 1 GiB device copy reads back in the same runs. Counters need rocprofv3, so the figures
 # are the committed profile's, not measured live.
@@ -42,6 +42,7 @@ TRAFFIC_DECODE = 1959210677
 TRAFFIC_DELTA = 1636029928
 TRAFFIC_PREFILL = 888455186  # average over the eight per-chunk launches
 TRAFFIC_PROLOGUE = 675541424
+TRAFFIC_OUTPUT_NORM = 805389585
 SECONDARY_WARM_MS = 100.0  # wall time of untimed steps before each secondary (config 3, 4, 5) measurement
 MFMA_BF16_PEAK_TFLOPS = 2500.0  # MI355X dense bf16/fp16 MFMA, TFLOP/s
 
@@ -118,7 +119,7 @@ def time_decode(w, steps: int, warmup: int):
     return _timed(step, steps, warmup, ("decode_partial_mfma", "decode_combine"))
 
 
-def _timed(step, steps: int, warmup: int, labels: tuple[str, ...], warm_ms: float = 0.0):
+def _timed(step, steps: int, warmup: int, labels: tuple[str, ...], warm_ms: float = 0.0, timing_repeats: int = 5):
     """(ms per step over ``steps`` timed steps, per-kernel averages from a separate instrumented pass).
 
     ``warmup`` untimed steps run first, and more until ``warm_ms`` of wall time has passed: after
@@ -145,7 +146,7 @@ def _timed(step, steps: int, warmup: int, labels: tuple[str, ...], warm_ms: floa
     end.record(stream)
     torch.cuda.synchronize()
     ms = start.elapsed_time(end) / steps
-    return ms, kernel_times(step, max(1, min(steps, 5)), labels)
+    return ms, kernel_times(step, max(1, min(steps, timing_repeats)), labels)
 
 
 def cpu_baseline_decode(w, budget_s: float = 12.0):
@@ -332,6 +333,30 @@ def time_prologue(w: dict, pw: dict, steps: int, warmup: int):
     return _timed(step, steps, warmup, ("qk_norm_rope",), warm_ms=SECONDARY_WARM_MS)
 
 
+def output_norm_workload(device: str, *, seed: int = 2, batch: int = 4, seq: int = 8192, value_heads: int = 32, dim: int = 128) -> dict:
+    """The linear-attention output stage (gated RMSNorm + SiLU(z)) over config 4's tokens: the bf16
+    core the chunked prefill writes, the bf16 in_proj_z output and a bf16 norm weight, bf16 out."""
+    import torch
+
+    gen = torch.Generator(device=device).manual_seed(seed)
+    core = torch.randn((batch, seq, value_heads, dim), generator=gen, device=device, dtype=torch.bfloat16)
+    z = torch.randn((batch, seq, value_heads * dim), generator=gen, device=device, dtype=torch.bfloat16)
+    w = (1.0 + 0.2 * torch.randn((dim,), generator=gen, device=device)).to(torch.bfloat16)
+    # bytes: core and z read, out written (2 bytes each)
+    algo = 3 * batch * seq * value_heads * dim * 2
+    return {"core": core, "z": z, "w": w, "algo_bytes": algo, "rows": batch * seq * value_heads}
+
+
+def time_output_norm(w: dict, steps: int, warmup: int):
+    import hip_ops
+
+    def step():
+        hip_ops.gated_rms_norm(w["core"], w["z"], w["w"], 1e-6)
+
+    # a 0.16 ms launch: average the per-kernel events over 20 launches rather than 5
+    return _timed(step, steps, warmup, ("gated_rms_norm",), warm_ms=SECONDARY_WARM_MS, timing_repeats=20)
+
+
 # ----------------------------------------------------------------------------- config 5
 
 
@@ -418,6 +443,7 @@ def main() -> int:
     parser.add_argument("--no-prefill", action="store_true", help="skip the config-3 secondary measurement")
     parser.add_argument("--no-hybrid", action="store_true", help="skip the config-5 secondary measurement")
     parser.add_argument("--no-prologue", action="store_true", help="skip the full-attention prologue measurement (config 3 shapes)")
+    parser.add_argument("--no-output-norm", action="store_true", help="skip the linear-attention output stage measurement (config 4 shapes)")
     parser.add_argument("--copy-probe-mib", type=int, default=0,
                         help="first run one plain device copy of this many MiB (reference point for HBM byte counters)")
     parser.add_argument("--cpu-budget", type=float, default=12.0)
@@ -510,6 +536,24 @@ def main() -> int:
         }
         del dw
         torch.cuda.empty_cache()
+        if not args.no_output_norm:
+            nw = output_norm_workload(device)
+            nms, nkern = time_output_norm(nw, max(20, args.steps), max(1, args.warmup))
+            n_ms = nkern["gated_rms_norm"]["avg_ms"]
+            ngbs = nw["algo_bytes"] / (n_ms * 1e-3) / 1e9
+            _log(f"bench: output norm {n_ms * 1e3:.1f} us for {nw['rows']} rows, {ngbs:.1f} GB/s ({ngbs / HBM_PEAK_GBS:.1%} of HBM peak)")
+            record["secondary_output_norm"] = {
+                "metric": "linear-attention output stage (gated RMSNorm + SiLU(z)) HBM GB/s",
+                "value": round(ngbs, 2),
+                "unit": "GB/s",
+                "ms_per_step": round(nms, 4),
+                "config": {"workload": "config 4's 4 x 8192 tokens x 32 value heads of 128 (bf16 core and z in, bf16 out)", "eps": 1e-6},
+                "roofline": {"bound": "hbm", "achieved": round(ngbs, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(ngbs / HBM_PEAK_GBS, 4),
+                             "traffic": TRAFFIC_OUTPUT_NORM, "algo_bytes_per_launch": nw["algo_bytes"],
+                             "kernel": "qa::gnorm::gated_rms_norm_kernel<128, true>", "kernel_avg_us": round(n_ms * 1e3, 2), "kernels": nkern},
+            }
+            del nw
+            torch.cuda.empty_cache()
     if not args.no_prefill:
         _log("bench: building config-3 workload (chunked paged prefill with gate)")
         pw = prefill_workload(device)

@@ -269,6 +269,24 @@ int64_t qa_chunk_gated_delta_workspace(int64_t batch, int64_t seq, int32_t key_h
 /* LDS bytes one chunked-prefill workgroup reserves (for capacity planning). */
 int64_t qa_chunk_gated_delta_lds_bytes(void);
 
+/* ---- linear-attention output stage: gated RMSNorm + SiLU(z) ---------------- */
+/* For token t and value head h, over the head's head_dim elements
+ * x = x[t*x_stride_t + h*x_stride_h + d] and z = gate[t*gate_stride_t +
+ * h*gate_stride_h + d]:  n = (x / sqrt(mean(x^2) + eps)) cast to x's dtype,
+ * out[t*out_stride_t + h*out_stride_h + d] = (weight[d] * n) * silu(z) in fp32,
+ * stored as out_dtype.  x, gate, weight, out: float32 or bfloat16 (weight
+ * head_dim elements); head_dim 64, 128 or 256; rows start on 16-byte
+ * boundaries.  Replaces gated_rms_norm (src/reference_ops.py:172-178) as the
+ * linear-attention layers apply it to the recurrence output
+ * (src/reference_ops.py:284-287, src/tp_runtime.py:853-857), where the core
+ * arrives in fp32 and the result stays fp32 until the output projection.    */
+int qa_gated_rms_norm(const void* x, int32_t x_dtype, int64_t x_stride_t, int64_t x_stride_h,
+                      const void* gate, int32_t gate_dtype, int64_t gate_stride_t, int64_t gate_stride_h,
+                      const void* weight, int32_t weight_dtype, float eps,
+                      int64_t tokens, int32_t heads, int32_t head_dim,
+                      void* out, int32_t out_dtype, int64_t out_stride_t, int64_t out_stride_h,
+                      hipStream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -593,6 +593,40 @@ def chunk_gated_delta_rule(
     return out, final, conv_out
 
 
+def gated_rms_norm(core: torch.Tensor, z: torch.Tensor, weight: torch.Tensor, eps: float, *, out_dtype: torch.dtype | None = None) -> torch.Tensor:
+    """The output stage of a linear-attention layer: gated RMSNorm + SiLU(z) per value head.
+
+    ``core`` ``(..., heads, head_dim)`` (the recurrence output, float32 or bfloat16; its
+    ``head_dim`` axis contiguous), ``z`` the ``in_proj_z`` output ``(..., heads * head_dim)`` or
+    ``(..., heads, head_dim)``, ``weight`` ``(head_dim,)``.  Returns ``(..., heads * head_dim)``
+    in ``out_dtype`` (default: ``core``'s dtype, as ``gated_rms_norm`` returns,
+    ``src/reference_ops.py:172-178,284-287``).
+    """
+    lib = L.load_library()
+    _require_cuda(core, "core")
+    device = core.device
+    _require_cuda(z, "z", device)
+    _float_dtype(core, "core")
+    _float_dtype(z, "z")
+    _require(core.dim() >= 2 and core.stride(-1) == 1, "core must be (..., heads, head_dim) with a contiguous head_dim axis")
+    heads, head_dim = core.shape[-2], core.shape[-1]
+    lead = core.shape[:-2]
+    x = core.reshape(-1, heads, head_dim)
+    gate = z.reshape(*lead, heads, head_dim).reshape(-1, heads, head_dim)
+    _require(gate.stride(-1) == 1, "z must have a contiguous head_dim axis")
+    w = weight.reshape(-1).to(device=device).contiguous()
+    _float_dtype(w, "weight")
+    _require(w.numel() == head_dim, "weight must have head_dim elements")
+    out = torch.empty((x.shape[0], heads, head_dim), dtype=out_dtype or core.dtype, device=device)
+    _float_dtype(out, "out")
+    status = lib.qa_gated_rms_norm(
+        _ptr(x), _code(x), x.stride(0), x.stride(1), _ptr(gate), _code(gate), gate.stride(0), gate.stride(1), _ptr(w), _code(w), float(eps),
+        x.shape[0], int(heads), int(head_dim), _ptr(out), _code(out), out.stride(0), out.stride(1), _stream(device),
+    )
+    L.check(lib, status, "gated_rms_norm")
+    return out.reshape(*lead, heads * head_dim)
+
+
 def paged_attention_prefill(
     query: torch.Tensor,
     cu_seqlens: torch.Tensor,

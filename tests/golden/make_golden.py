@@ -13,7 +13,10 @@ bf16 rounding of two cast points the reference leaves to torch's CPU kernels:
   is the identity; that layer path is recorded too, as the end-to-end vector of
   the conv + gating + recurrence core);
 * ``probs.to(query.dtype)`` before the value product of ``full_attention``
-  (``src/reference_ops.py:358-359``).
+  (``src/reference_ops.py:358-359``);
+* the dtypes at which ``linear_attention`` hands its core and ``z`` to ``gated_rms_norm``
+  (``src/reference_ops.py:172-178,284-287``): the recorded inputs and output of that call
+  fix which of its casts are identities in the layer (the core arrives in fp32).
 
 For those, this script calls the reference functions themselves on small seeded
 inputs and stores inputs and outputs as plain arrays (``.npz``, no pickles; bf16
@@ -103,6 +106,55 @@ def linear_attention_case(ro, seed: int, batch: int, seq: int, key_heads: int, v
     }
 
 
+def linear_attention_output_case(ro, seed: int, batch: int, seq: int, key_heads: int, value_heads: int) -> dict:
+    """``linear_attention`` (cache=None) with a non-zero ``in_proj_z`` output and norm weight;
+    records what its ``gated_rms_norm`` received and returned (the core reaches it in fp32)."""
+    g = torch.Generator().manual_seed(seed)
+    dk = dv = 128
+    kernel = 4
+    qkv_dim = 2 * key_heads * dk + value_heads * dv
+    mixed = torch.randn(batch, seq, qkv_dim, generator=g).to(torch.bfloat16)
+    a = torch.randn(batch, seq, value_heads, generator=g).to(torch.bfloat16)
+    b = torch.randn(batch, seq, value_heads, generator=g).to(torch.bfloat16)
+    z = (torch.randn(batch, seq, value_heads * dv, generator=g) * 2.0).to(torch.bfloat16)
+    norm = (1.0 + 0.2 * torch.randn(dv, generator=g)).to(torch.bfloat16)
+    a_log = (torch.rand(value_heads, generator=g) * 2.0 - 1.0).float()
+    dt_bias = (torch.randn(value_heads, generator=g) * 0.5).float()
+    conv_w = (torch.randn(qkv_dim, 1, kernel, generator=g) * 0.5).float()
+    cfg = SimpleNamespace(
+        linear_attention=SimpleNamespace(
+            key_heads=key_heads, value_heads=value_heads, key_head_dim=dk, value_head_dim=dv, conv_kernel_dim=kernel,
+            value_state_dim=value_heads * dv,
+        ),
+        rms_norm_eps=1e-6,
+    )
+    mapping = SimpleNamespace(in_proj_qkv="qkv", in_proj_z="z", out_proj="out", in_proj_a="a", in_proj_b="b",
+                              conv1d_weight="conv", a_log="a_log", dt_bias="dt_bias", norm="norm")
+    weights = _Weights(
+        {"qkv": lambda h: mixed, "a": lambda h: a, "b": lambda h: b, "z": lambda h: z, "out": lambda h: h},
+        {"conv": conv_w, "a_log": a_log, "dt_bias": dt_bias, "norm": norm},
+    )
+    seen = {}
+    original = ro.gated_rms_norm
+
+    def recording(hidden, weight, gate, eps):
+        out = original(hidden, weight, gate, eps)
+        seen["x"], seen["gate"], seen["out"], seen["eps"] = hidden, gate, out, eps
+        return out
+
+    ro.gated_rms_norm = recording
+    try:
+        layer_out = ro.linear_attention(torch.zeros(batch, seq, 8, dtype=torch.bfloat16), mapping, cfg, weights, cache=None)
+    finally:
+        ro.gated_rms_norm = original
+    assert seen["x"].dtype == torch.float32 and seen["out"].dtype == torch.float32
+    return {
+        "x": seen["x"].numpy(), "gate_bf16": bits(seen["gate"]), "norm_bf16": bits(norm), "out": seen["out"].numpy(),
+        "layer_out_bf16": bits(layer_out), "eps": np.array([seen["eps"]], dtype=np.float64),
+        "shape": np.array([batch, seq, key_heads, value_heads, dk, dv, kernel], dtype=np.int64),
+    }
+
+
 def recurrent_rule_case(ro, seed: int, batch: int, seq: int, heads: int, dk: int, dv: int, with_state: bool) -> dict:
     """``recurrent_gated_delta_rule`` on bf16 q/k/v (output cast back to bf16)."""
     g = torch.Generator().manual_seed(seed)
@@ -172,6 +224,7 @@ def main(reference_root: str) -> None:
     np.savez_compressed(HERE / "linear_attention_core.npz", **linear_attention_case(ro, 20240, 1, 40, 1, 2))
     np.savez_compressed(HERE / "full_attention_prefill.npz", **full_attention_case(ro, 20241, 20, 4, 2, 128))
     np.savez_compressed(HERE / "full_attention_rope_d256.npz", **full_attention_case(ro, 20244, 12, 4, 2, 256, position_offset=3000))
+    np.savez_compressed(HERE / "linear_attention_output.npz", **linear_attention_output_case(ro, 20245, 2, 9, 1, 2))
     np.savez_compressed(HERE / "recurrent_rule_bf16.npz", **recurrent_rule_case(ro, 20242, 2, 7, 3, 16, 8, False))
     np.savez_compressed(HERE / "recurrent_rule_bf16_state.npz", **recurrent_rule_case(ro, 20243, 1, 5, 2, 16, 8, True))
     for f in sorted(HERE.glob("*.npz")):

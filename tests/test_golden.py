@@ -19,6 +19,7 @@ import torch
 from golden_io import bf16, f32, load
 from oracle import attention as oa
 from oracle import gated_delta as gd
+from oracle import gated_norm as gn
 
 
 def _ulp_close(out: torch.Tensor, ref: torch.Tensor) -> None:
@@ -81,3 +82,17 @@ def test_qk_norm_rope_matches_reference_bit_for_bit() -> None:
         k_ref = bf16(v["k_bf16"]).permute(0, 2, 1, 3).reshape(batch * seq, kv_heads, head_dim)
         torch.testing.assert_close(q, q_ref, atol=0, rtol=0)
         torch.testing.assert_close(k, k_ref, atol=0, rtol=0)
+
+
+def test_gated_rms_norm_matches_reference_layer_call() -> None:
+    """``gated_rms_norm`` as ``linear_attention`` calls it: an fp32 core (its mid cast is the
+    identity), bf16 ``z`` and weight; same torch CPU operations, so bit for bit in fp32, and the
+    layer's bf16 output (identity ``out_proj``) is that result cast to bf16."""
+    v = load("linear_attention_output")
+    x, gate, norm = f32(v["x"]), bf16(v["gate_bf16"]), bf16(v["norm_bf16"])
+    out = gn.gated_rms_norm(x, norm, gate, float(v["eps"][0]))
+    assert out.dtype == torch.float32
+    assert torch.equal(out, f32(v["out"]))
+    batch, seq, _kh, value_heads, _dk, dv, _k = (int(t) for t in v["shape"])
+    layer = bf16(v["layer_out_bf16"])
+    assert torch.equal(layer, out.reshape(batch, seq, value_heads * dv).to(torch.bfloat16))
