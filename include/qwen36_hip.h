@@ -239,6 +239,25 @@ int qa_gated_delta_step(const float* qkv, int64_t qkv_stride_b,
                         int64_t batch, int32_t key_heads, int32_t value_heads,
                         int32_t key_dim, int32_t value_dim, hipStream_t stream);
 
+/* qa_gated_delta_step followed, in the same kernel, by the layer's output
+ * stage: out[b, h, :] = (w * o / sqrt(mean(o^2) + eps)) * silu(z[b, h, :])
+ * on the step's fp32 output o of value head h, with z (B, Hv*dv) rows of
+ * z_stride_b elements (the in_proj_z output) and norm_weight (dv), both
+ * float32 or bfloat16.  The head's 128 outputs never leave the workgroup.
+ * Replaces gated_rms_norm (src/reference_ops.py:172-178) applied to the
+ * decode token's core (src/reference_ops.py:284-287, src/tp_runtime.py:
+ * 853-857), where the core is fp32 and its cast of the normalised value is
+ * the identity.                                                           */
+int qa_gated_delta_step_norm(const float* qkv, int64_t qkv_stride_b,
+                             const void* a, const void* b, int32_t ab_dtype, int64_t ab_stride_b,
+                             const float* a_log, const float* dt_bias,
+                             float* state, int64_t state_stride_slot, const void* slots, int32_t slots_dtype,
+                             const void* z, int32_t z_dtype, int64_t z_stride_b,
+                             const void* norm_weight, int32_t norm_dtype, float eps,
+                             void* out, int32_t out_dtype, int64_t out_stride_b,
+                             int64_t batch, int32_t key_heads, int32_t value_heads,
+                             int32_t key_dim, int32_t value_dim, hipStream_t stream);
+
 /* Chunked gated delta-rule prefill of one linear-attention layer, from the
  * raw in_proj outputs.  mixed_qkv (B, T, 2*Hqk*dk + Hv*dv) bfloat16,
  * a, b (B, T, Hv), a_log/dt_bias (Hv) fp32, conv_weight (C, 4) fp32,

@@ -340,14 +340,17 @@ def recurrent_gated_delta_rule(query: Any, key: Any, value: Any, g: Any, beta: A
 
 
 def linear_attention_decode_batch(
-    mixed_qkv: Any, a: Any, b: Any, a_log: Any, dt_bias: Any, conv_weight: Any, pool: LinearStatePool, slots: Any, config: AttentionConfig, *, out_dtype: Any = None
+    mixed_qkv: Any, a: Any, b: Any, a_log: Any, dt_bias: Any, conv_weight: Any, pool: LinearStatePool, slots: Any, config: AttentionConfig, *,
+    out_dtype: Any = None, z: Any = None, norm_weight: Any = None, eps: float = 1e-6
 ) -> Any:
     """One decode token of a linear-attention layer for a batch of requests.
 
     ``mixed_qkv`` ``(B, qkv_dim)``, ``a``/``b`` ``(B, Hv)`` are the
     ``in_proj_*`` outputs of the step; request ``r`` keeps its conv and
     recurrent state in row ``slots[r]`` of ``pool`` (updated in place).
-    Returns the core output ``(B, Hv, dv)`` before the gated RMSNorm.  This
+    Returns the core output ``(B, Hv, dv)`` before the gated RMSNorm, or, given
+    ``z`` (the ``in_proj_z`` output ``(B, Hv*dv)``) and ``norm_weight``, after it
+    (``src/reference_ops.py:284-287``), fused into the same kernel.  This
     replaces the stack / run / scatter of ``src/tp_runtime.py:2613-2717``.
     """
     import torch
@@ -357,7 +360,7 @@ def linear_attention_decode_batch(
     lin = config.linear_attention
     act = hip_ops.causal_conv1d_update(mixed_qkv, pool.conv, conv_weight, slots)
     return hip_ops.gated_delta_step(act, a, b, a_log, dt_bias, pool.state, key_heads=lin.key_heads, slots=slots,
-                                    out_dtype=torch.bfloat16 if out_dtype is None else out_dtype)
+                                    out_dtype=torch.bfloat16 if out_dtype is None else out_dtype, z=z, norm_weight=norm_weight, eps=eps)
 
 
 def linear_attention_prefill(mixed_qkv: Any, a: Any, b: Any, a_log: Any, dt_bias: Any, conv_weight: Any, config: AttentionConfig, *, conv_state: Any = None, initial_state: Any = None) -> tuple[Any, Any, Any]:

@@ -127,6 +127,13 @@ struct DeltaParams {
   void* out;
   int out_dtype;
   int64_t out_sb;  // fused: per batch row
+  // fused output stage (gated RMSNorm + SiLU(z)), NORM only
+  const void* z;
+  int z_dtype;
+  int64_t z_sb;
+  const void* norm_w;
+  int norm_dtype;
+  float norm_eps;
   int64_t B, S;
   int H, Hqk, dk, dv;
 };
@@ -166,7 +173,7 @@ __global__ __launch_bounds__(128) void delta_recurrent_generic(DeltaParams p) {
 }
 
 // dk = dv = 128: register-resident state, see the file header for the layout.
-template <bool FUSED>
+template <bool FUSED, bool NORM = false>
 __global__ __launch_bounds__(256) void delta_recurrent_128(DeltaParams p) {
   constexpr int DK = 128, DV = 128;
   __shared__ float red[2][4][DV];
@@ -306,13 +313,32 @@ __global__ __launch_bounds__(256) void delta_recurrent_128(DeltaParams p) {
     }
     __syncthreads();
     if (w == 0 && rg == 0) {
+      // lanes 0-15 of wave 0 (one DPP row) hold the head's 128 outputs, 8 each
+      float o[8];
+#pragma unroll
+      for (int c = 0; c < 8; ++c) o[c] = (red[1][0][col0 + c] + red[1][1][col0 + c]) + (red[1][2][col0 + c] + red[1][3][col0 + c]);
+      if (NORM) {
+        // the layer's output stage on the fp32 core (src/reference_ops.py:172-178,284-287: the
+        // core reaches gated_rms_norm in fp32, so its cast of the normalised value is the
+        // identity): (w * o / sqrt(mean(o^2) + eps)) * silu(z)
+        float ss = 0.f;
+#pragma unroll
+        for (int c = 0; c < 8; ++c) ss += o[c] * o[c];
+        ss = row16_sum(ss);
+        const float r = 1.0f / sqrtf(ss / static_cast<float>(DV) + p.norm_eps);
+#pragma unroll
+        for (int c = 0; c < 8; ++c) {
+          const float zv = load_any(p.z, p.z_dtype, b * p.z_sb + static_cast<int64_t>(h) * DV + col0 + c);
+          const float wv = load_any(p.norm_w, p.norm_dtype, col0 + c);
+          o[c] = (wv * (o[c] * r)) * __fdividef(zv, 1.0f + __expf(-zv));
+        }
+      }
 #pragma unroll
       for (int c = 0; c < 8; ++c) {
-        const float o = (red[1][0][col0 + c] + red[1][1][col0 + c]) + (red[1][2][col0 + c] + red[1][3][col0 + c]);
         if (FUSED)
-          store_any(p.out, p.out_dtype, b * p.out_sb + static_cast<int64_t>(h) * DV + col0 + c, o);
+          store_any(p.out, p.out_dtype, b * p.out_sb + static_cast<int64_t>(h) * DV + col0 + c, o[c]);
         else
-          reinterpret_cast<float*>(p.out)[((b * p.H + h) * p.S + t) * DV + col0 + c] = o;
+          reinterpret_cast<float*>(p.out)[((b * p.H + h) * p.S + t) * DV + col0 + c] = o[c];
       }
     }
   }
@@ -417,11 +443,12 @@ extern "C" int qa_linear_attention_recurrent_core(const float* query, const floa
   return check_launch("delta_recurrent_generic");
 }
 
-extern "C" int qa_gated_delta_step(const float* qkv, int64_t qkv_stride_b, const void* a, const void* b, int32_t ab_dtype,
-                                   int64_t ab_stride_b, const float* a_log, const float* dt_bias, float* state,
-                                   int64_t state_stride_slot, const void* slots, int32_t slots_dtype, void* out,
-                                   int32_t out_dtype, int64_t out_stride_b, int64_t batch, int32_t key_heads,
-                                   int32_t value_heads, int32_t key_dim, int32_t value_dim, hipStream_t stream) {
+static int gated_delta_step_impl(const float* qkv, int64_t qkv_stride_b, const void* a, const void* b, int32_t ab_dtype,
+                                 int64_t ab_stride_b, const float* a_log, const float* dt_bias, float* state,
+                                 int64_t state_stride_slot, const void* slots, int32_t slots_dtype, const void* z, int32_t z_dtype,
+                                 int64_t z_stride_b, const void* norm_weight, int32_t norm_dtype, float eps, void* out,
+                                 int32_t out_dtype, int64_t out_stride_b, int64_t batch, int32_t key_heads,
+                                 int32_t value_heads, int32_t key_dim, int32_t value_dim, hipStream_t stream) {
   using namespace qa;
   QA_REQUIRE(qkv && a && b && a_log && dt_bias && state && out, "gated_delta_step: pointers must be non-null");
   QA_REQUIRE(key_dim == 128 && value_dim == 128, "gated_delta_step: only key_dim = value_dim = 128 is built");
@@ -432,6 +459,10 @@ extern "C" int qa_gated_delta_step(const float* qkv, int64_t qkv_stride_b, const
   QA_REQUIRE(batch > 0 && batch * value_heads <= 0x7fffffff, "gated_delta_step: bad batch");
   QA_REQUIRE(aligned16(state) && state_stride_slot % 4 == 0 && qkv_stride_b >= 2 * key_heads * key_dim + value_heads * value_dim,
              "gated_delta_step: state must be 16-byte aligned and qkv rows complete");
+  const bool norm = z != nullptr;
+  QA_REQUIRE(!norm || (norm_weight != nullptr && is_float_dtype(z_dtype) && is_float_dtype(norm_dtype) && eps >= 0.f &&
+                       z_stride_b >= static_cast<int64_t>(value_heads) * value_dim),
+             "gated_delta_step: the output stage needs z (B, Hv*dv) and a norm weight (dv), float32/bfloat16, eps >= 0");
   DeltaParams p{};
   p.qkv = qkv;
   p.qkv_sb = qkv_stride_b;
@@ -449,6 +480,12 @@ extern "C" int qa_gated_delta_step(const float* qkv, int64_t qkv_stride_b, const
   p.out = out;
   p.out_dtype = out_dtype;
   p.out_sb = out_stride_b;
+  p.z = z;
+  p.z_dtype = z_dtype;
+  p.z_sb = z_stride_b;
+  p.norm_w = norm_weight;
+  p.norm_dtype = norm_dtype;
+  p.norm_eps = eps;
   p.B = batch;
   p.S = 1;
   p.H = value_heads;
@@ -457,7 +494,32 @@ extern "C" int qa_gated_delta_step(const float* qkv, int64_t qkv_stride_b, const
   p.dv = value_dim;
   {
     KernelTimer timer_("gated_delta_step", stream);
-    hipLaunchKernelGGL(delta_recurrent_128<true>, dim3(static_cast<unsigned>(batch * value_heads)), dim3(256), 0, stream, p);
+    if (norm)
+      hipLaunchKernelGGL((delta_recurrent_128<true, true>), dim3(static_cast<unsigned>(batch * value_heads)), dim3(256), 0, stream, p);
+    else
+      hipLaunchKernelGGL((delta_recurrent_128<true, false>), dim3(static_cast<unsigned>(batch * value_heads)), dim3(256), 0, stream, p);
   }
   return check_launch("delta_recurrent_128(fused step)");
+}
+
+extern "C" int qa_gated_delta_step(const float* qkv, int64_t qkv_stride_b, const void* a, const void* b, int32_t ab_dtype,
+                                   int64_t ab_stride_b, const float* a_log, const float* dt_bias, float* state,
+                                   int64_t state_stride_slot, const void* slots, int32_t slots_dtype, void* out,
+                                   int32_t out_dtype, int64_t out_stride_b, int64_t batch, int32_t key_heads,
+                                   int32_t value_heads, int32_t key_dim, int32_t value_dim, hipStream_t stream) {
+  return gated_delta_step_impl(qkv, qkv_stride_b, a, b, ab_dtype, ab_stride_b, a_log, dt_bias, state, state_stride_slot, slots,
+                               slots_dtype, nullptr, QA_F32, 0, nullptr, QA_F32, 0.f, out, out_dtype, out_stride_b, batch,
+                               key_heads, value_heads, key_dim, value_dim, stream);
+}
+
+extern "C" int qa_gated_delta_step_norm(const float* qkv, int64_t qkv_stride_b, const void* a, const void* b, int32_t ab_dtype,
+                                        int64_t ab_stride_b, const float* a_log, const float* dt_bias, float* state,
+                                        int64_t state_stride_slot, const void* slots, int32_t slots_dtype, const void* z,
+                                        int32_t z_dtype, int64_t z_stride_b, const void* norm_weight, int32_t norm_dtype, float eps,
+                                        void* out, int32_t out_dtype, int64_t out_stride_b, int64_t batch, int32_t key_heads,
+                                        int32_t value_heads, int32_t key_dim, int32_t value_dim, hipStream_t stream) {
+  if (z == nullptr) return qa::fail("gated_delta_step_norm: z must be non-null");
+  return gated_delta_step_impl(qkv, qkv_stride_b, a, b, ab_dtype, ab_stride_b, a_log, dt_bias, state, state_stride_slot, slots,
+                               slots_dtype, z, z_dtype, z_stride_b, norm_weight, norm_dtype, eps, out, out_dtype, out_stride_b, batch,
+                               key_heads, value_heads, key_dim, value_dim, stream);
 }

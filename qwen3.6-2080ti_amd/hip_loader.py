@@ -104,6 +104,11 @@ SIGNATURES: dict[str, tuple[Any, list[Any]]] = {
         [c_void_p, c_int64, c_void_p, c_void_p, c_int32, c_int64, c_void_p, c_void_p, c_void_p, c_int64, c_void_p, c_int32, c_void_p,
          c_int32, c_int64, c_int64, c_int32, c_int32, c_int32, c_int32, c_void_p],
     ),
+    "qa_gated_delta_step_norm": (
+        c_int32,
+        [c_void_p, c_int64, c_void_p, c_void_p, c_int32, c_int64, c_void_p, c_void_p, c_void_p, c_int64, c_void_p, c_int32, c_void_p,
+         c_int32, c_int64, c_void_p, c_int32, c_float, c_void_p, c_int32, c_int64, c_int64, c_int32, c_int32, c_int32, c_int32, c_void_p],
+    ),
     "qa_gated_rms_norm": (
         c_int32,
         [c_void_p, c_int32, c_int64, c_int64, c_void_p, c_int32, c_int64, c_int64, c_void_p, c_int32, c_float, c_int64, c_int32, c_int32,

@@ -495,6 +495,9 @@ def gated_delta_step(
     key_heads: int,
     slots: torch.Tensor | None = None,
     out_dtype: torch.dtype = torch.bfloat16,
+    z: torch.Tensor | None = None,
+    norm_weight: torch.Tensor | None = None,
+    eps: float = 1e-6,
 ) -> torch.Tensor:
     """Fused single-token recurrence of a linear-attention layer.
 
@@ -502,7 +505,10 @@ def gated_delta_step(
     ``(B, Hv)`` the raw ``in_proj_a``/``in_proj_b`` outputs; ``state``
     ``(slots, Hv, dk, dv)`` fp32 is updated in place at ``slots[b]`` (or ``b``).
     Returns ``(B, Hv, dv)`` in ``out_dtype``.  Follows
-    ``src/reference_ops.py:271-283,291-322`` for one token.
+    ``src/reference_ops.py:271-283,291-322`` for one token.  With ``z`` (the
+    ``in_proj_z`` output ``(B, Hv*dv)``) and ``norm_weight`` ``(dv,)`` the same
+    kernel also applies the layer's output stage, ``gated_rms_norm`` on the fp32
+    core (``src/reference_ops.py:172-178,284-287``).
     """
     lib = L.load_library()
     _require_cuda(qkv, "qkv")
@@ -524,10 +530,26 @@ def gated_delta_step(
         slots = slots.contiguous()
         slot_ptr, slot_code = _ptr(slots), _code(slots)
     out = torch.empty((batch, value_heads, value_dim), dtype=out_dtype, device=device)
-    status = lib.qa_gated_delta_step(
-        _ptr(qkv), qkv.stride(0), _ptr(a_c), _ptr(b_c), _code(a_c), a_c.stride(0), _ptr(alog), _ptr(dtb), _ptr(state), state.stride(0),
-        slot_ptr, slot_code, _ptr(out), _code(out), out.stride(0), batch, int(key_heads), value_heads, key_dim, value_dim, _stream(device),
-    )
+    if z is None:
+        _require(norm_weight is None, "norm_weight needs z")
+        status = lib.qa_gated_delta_step(
+            _ptr(qkv), qkv.stride(0), _ptr(a_c), _ptr(b_c), _code(a_c), a_c.stride(0), _ptr(alog), _ptr(dtb), _ptr(state), state.stride(0),
+            slot_ptr, slot_code, _ptr(out), _code(out), out.stride(0), batch, int(key_heads), value_heads, key_dim, value_dim, _stream(device),
+        )
+    else:
+        _require_cuda(z, "z", device)
+        _float_dtype(z, "z")
+        _require(norm_weight is not None, "the output stage needs norm_weight")
+        zz = z.reshape(batch, value_heads * value_dim)
+        _require(zz.stride(-1) == 1, "z rows must be contiguous")
+        w = norm_weight.reshape(-1).to(device=device).contiguous()
+        _float_dtype(w, "norm_weight")
+        _require(w.numel() == value_dim, "norm_weight must have value_dim elements")
+        status = lib.qa_gated_delta_step_norm(
+            _ptr(qkv), qkv.stride(0), _ptr(a_c), _ptr(b_c), _code(a_c), a_c.stride(0), _ptr(alog), _ptr(dtb), _ptr(state), state.stride(0),
+            slot_ptr, slot_code, _ptr(zz), _code(zz), zz.stride(0), _ptr(w), _code(w), float(eps), _ptr(out), _code(out), out.stride(0), batch,
+            int(key_heads), value_heads, key_dim, value_dim, _stream(device),
+        )
     L.check(lib, status, "gated_delta_step")
     return out
 

@@ -120,3 +120,70 @@ def test_rejects_unsupported_shapes() -> None:
     wide = torch.zeros(4, 2, 132, device=DEV, dtype=torch.bfloat16)
     with pytest.raises(RuntimeError, match="16-byte"):
         hip_ops.gated_rms_norm(wide[:, :, 2:130], torch.zeros(4, 256, device=DEV, dtype=torch.bfloat16), torch.ones(128, device=DEV), EPS)
+
+
+def _decode_inputs(seed: int, batch: int, key_heads: int, value_heads: int):
+    gen = torch.Generator().manual_seed(seed)
+    channels = 2 * key_heads * 128 + value_heads * 128
+    act = torch.randn(batch, channels, generator=gen)  # the conv + SiLU output of the step
+    a = torch.randn(batch, value_heads, generator=gen)
+    b = torch.randn(batch, value_heads, generator=gen)
+    a_log = torch.rand(value_heads, generator=gen) * 2.0 - 1.0
+    dt_bias = torch.randn(value_heads, generator=gen) * 0.5
+    state = torch.randn(batch, value_heads, 128, 128, generator=gen) * 0.05
+    z = (torch.randn(batch, value_heads * 128, generator=gen) * 2.0).to(torch.bfloat16)
+    norm = (1.0 + 0.2 * torch.randn(128, generator=gen)).to(torch.bfloat16)
+    return act, a, b, a_log, dt_bias, state, z, norm
+
+
+@pytest.mark.parametrize("out_dtype", [torch.float32, torch.bfloat16])
+def test_decode_step_with_fused_output_stage(out_dtype: torch.dtype) -> None:
+    """qa_gated_delta_step_norm = the plain step's fp32 core through the oracle's output stage
+    (the core is fp32, as in the reference's layers); the state update is the plain step's."""
+    import hip_ops
+
+    act, a, b, a_log, dt_bias, state0, z, norm = _decode_inputs(21, 3, 2, 4)
+    args = (act.to(DEV), a.to(DEV), b.to(DEV), a_log.to(DEV), dt_bias.to(DEV))
+    s_plain = state0.to(DEV).clone()
+    core = hip_ops.gated_delta_step(*args, s_plain, key_heads=2, out_dtype=torch.float32)
+    s_fused = state0.to(DEV).clone()
+    out = hip_ops.gated_delta_step(*args, s_fused, key_heads=2, out_dtype=out_dtype, z=z.to(DEV), norm_weight=norm.to(DEV), eps=EPS)
+    assert torch.equal(s_fused, s_plain)
+    ref = gn.gated_rms_norm(core.cpu().reshape(-1, 128), norm, z.reshape(-1, 128), EPS).reshape(3, 4, 128)
+    if out_dtype == torch.float32:
+        _fp32_close(out, ref)
+    else:
+        _mostly_bit_exact(out, ref.to(torch.bfloat16))
+
+
+def test_runtime_decode_batch_output_stage_on_slots() -> None:
+    """attention_runtime.linear_attention_decode_batch with z: slot-indexed states, fused stage."""
+    import attention_runtime as rt
+    from decode_state import LinearStatePool
+
+    from oracle import gated_delta as gd
+
+    shape = gd.LinearShape(key_heads=2, value_heads=4, key_head_dim=128, value_head_dim=128, conv_kernel_dim=4)
+    gen = torch.Generator().manual_seed(23)
+    batch = 3
+    mixed = torch.randn(batch, shape.qkv_dim, generator=gen)
+    a = torch.randn(batch, 4, generator=gen)
+    b = torch.randn(batch, 4, generator=gen)
+    a_log = torch.rand(4, generator=gen) * 2.0 - 1.0
+    dt_bias = torch.randn(4, generator=gen) * 0.5
+    conv_w = torch.randn(shape.qkv_dim, 4, generator=gen) * 0.5
+    z = (torch.randn(batch, 4 * 128, generator=gen) * 2.0).to(torch.bfloat16)
+    norm = (1.0 + 0.2 * torch.randn(128, generator=gen)).to(torch.bfloat16)
+    cfg = rt.parse_attention_config({"text_config": {
+        "linear_num_key_heads": 2, "linear_num_value_heads": 4, "linear_key_head_dim": 128, "linear_value_head_dim": 128,
+        "linear_conv_kernel_dim": 4, "num_attention_heads": 2, "num_key_value_heads": 2, "head_dim": 4, "attn_output_gate": True}})
+    slots = torch.tensor([2, 0, 3], device=DEV)
+    pool_a = LinearStatePool(4, 4, 128, 128, shape.qkv_dim, 4, device=DEV)
+    pool_b = LinearStatePool(4, 4, 128, 128, shape.qkv_dim, 4, device=DEV)
+    core = rt.linear_attention_decode_batch(mixed.to(DEV), a.to(DEV), b.to(DEV), a_log.to(DEV), dt_bias.to(DEV), conv_w.to(DEV), pool_a, slots, cfg,
+                                            out_dtype=torch.float32)
+    out = rt.linear_attention_decode_batch(mixed.to(DEV), a.to(DEV), b.to(DEV), a_log.to(DEV), dt_bias.to(DEV), conv_w.to(DEV), pool_b, slots, cfg,
+                                           out_dtype=torch.float32, z=z.to(DEV), norm_weight=norm.to(DEV), eps=EPS)
+    assert torch.equal(pool_a.state, pool_b.state) and torch.equal(pool_a.conv, pool_b.conv)
+    ref = gn.gated_rms_norm(core.cpu().reshape(-1, 128), norm, z.reshape(-1, 128), EPS).reshape(batch, 4, 128)
+    _fp32_close(out, ref)
