@@ -140,6 +140,27 @@ int qa_paged_kv_gather(const qa_paged_kv* kv, int32_t head_dim, int64_t batch,
                        int64_t max_blocks, int64_t valid, int32_t block_size,
                        void* key_out, void* value_out, hipStream_t stream);
 
+/* Device-side block reservation for a batched step (one kernel, no host
+ * round trip, so a decode step can be captured in a HIP graph).  Row b grows
+ * from lengths[b] to lengths[b] + n_b tokens (n_b = counts[b], or count_scalar
+ * when counts == NULL); the logical blocks ceil(len/bs) .. ceil((len+n)/bs)-1
+ * of its table get ids from the front of the free list, rows in order: the
+ * lowest-free-id policy of PagedKVBlockPool.allocate (src/decode_state.py:72-78)
+ * and of FullAttentionCache._grow_to's allocate calls (:365-374).  free_list
+ * holds ascending ids; free_state (device int32[2]) = {head, count} marks
+ * free_list[head .. head+count) as free and is advanced.  positions (may be
+ * NULL) receives the old lengths (the append positions); lengths are advanced
+ * in place.  All-or-nothing: status (device int32) = 0 on success, 1 not
+ * enough free blocks, 2 a row would pass max_blocks, 3 corrupt free_state,
+ * 4 negative or overflowing length/count -- then nothing else is written.
+ * Replaces the host-side allocate + page_table_tensor rebuild of
+ * src/decode_state.py:72-78,305-328 for the shared pool.                  */
+int qa_paged_kv_reserve(void* block_tables, int32_t table_dtype, int64_t table_stride, int64_t max_blocks,
+                        void* lengths, int32_t lengths_dtype, void* positions, int32_t positions_dtype,
+                        const void* counts, int32_t counts_dtype, int64_t count_scalar, int64_t batch,
+                        int32_t block_size, const int32_t* free_list, int64_t free_capacity,
+                        int32_t* free_state, int32_t* status, hipStream_t stream);
+
 /* ---- paged prefill ------------------------------------------------------ */
 /* Causal attention of packed new tokens over their paged KV (prefix + the
  * new tokens, already appended): query (total_new, heads, head_dim) bf16

@@ -188,3 +188,38 @@ def slot_mapping(tables: np.ndarray, starts: np.ndarray, counts: np.ndarray, blo
             physical, offset = slot_of(tables[row], pos, block_size)
             slots.append(physical * block_size + offset)
     return np.asarray(slots, dtype=np.int64)
+
+
+def reserve_step(
+    tables: np.ndarray, lengths: np.ndarray, counts: np.ndarray, free: list[int], block_size: int
+) -> tuple[int, np.ndarray, np.ndarray, np.ndarray, list[int]]:
+    """One batched step's block reservation over a fixed-capacity shared pool.
+
+    Each row ``b`` in order grows from ``lengths[b]`` to ``lengths[b] + counts[b]``
+    tokens; its new logical blocks ``ceil(len/bs) .. ceil((len+n)/bs) - 1`` take
+    ids from the head of the free list, as ``PagedKVBlockPool.allocate`` does
+    (``src/decode_state.py:72-78``) when ``FullAttentionCache._grow_to`` calls it
+    once per request (``src/decode_state.py:365-374``) -- except that a shared
+    pool does not grow: when the rows need more blocks than are free (status 1)
+    or a row would pass the table's width (status 2), or a length/count is
+    negative (status 4), nothing changes.  Returns ``(status, tables, positions,
+    lengths, free)`` with ``positions`` the lengths before the step.
+    """
+    tables = tables.copy()
+    lengths = lengths.astype(np.int64)
+    counts = np.broadcast_to(np.asarray(counts, dtype=np.int64), lengths.shape)
+    max_blocks = tables.shape[1]
+    if (lengths < 0).any() or (counts < 0).any():
+        return 4, tables, lengths.copy(), lengths.copy(), list(free)
+    have = [ceil_div(int(n), block_size) for n in lengths]
+    want = [ceil_div(int(n + c), block_size) for n, c in zip(lengths, counts)]
+    if any(w > max_blocks for w in want):
+        return 2, tables, lengths.copy(), lengths.copy(), list(free)
+    if sum(w - h for w, h in zip(want, have)) > len(free):
+        return 1, tables, lengths.copy(), lengths.copy(), list(free)
+    free = list(free)
+    for b in range(lengths.shape[0]):
+        k = want[b] - have[b]
+        taken, free = free[:k], free[k:]
+        tables[b, have[b] : want[b]] = taken
+    return 0, tables, lengths.copy(), lengths + counts, free

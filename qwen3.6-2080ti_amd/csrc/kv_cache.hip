@@ -257,3 +257,178 @@ extern "C" int qa_paged_kv_gather(const qa_paged_kv* kv, int32_t head_dim, int64
     hipLaunchKernelGGL(kv_gather_kernel<2>, grid, dim3(256), 0, stream, p, ko, vo);
   return check_launch("kv_gather_kernel");
 }
+
+// ---------------------------------------------------------------------------
+// Device-side block reservation for a batched step.  The free list is an ascending
+// int32 array of block ids with a device cursor state = {head, count}: the free ids are
+// free_list[head .. head + count).  Rows take new blocks from the front in row order, which
+// is the reference's allocation policy (lowest free id first, src/decode_state.py:72-78)
+// applied to one request after the other.  One workgroup: a first pass sums the blocks
+// every row needs and checks the tables, a second writes them, scanning rows 1024 at a
+// time, so the result is all-or-nothing and no host round trip is needed.
+namespace qa {
+
+struct ReserveParams {
+  void* tables;
+  int64_t table_stride, max_blocks;
+  void* lengths;  // in: current length; out: length + count
+  void* positions;  // out (may be null): the length before the step
+  const void* counts;
+  int64_t count_scalar;
+  const int32_t* free_list;
+  int32_t* free_state;  // {head, count}
+  int32_t* status;
+  int64_t batch, capacity;
+  int bs;
+  int table_i64, lengths_i64, positions_i64, counts_i64;
+};
+
+constexpr int RESERVE_THREADS = 1024;
+
+__device__ __forceinline__ void write_index(void* base, int is64, int64_t i, int64_t v) {
+  if (is64)
+    reinterpret_cast<int64_t*>(base)[i] = v;
+  else
+    reinterpret_cast<int32_t*>(base)[i] = static_cast<int32_t>(v);
+}
+
+__device__ __forceinline__ int64_t ceil_div64(int64_t a, int64_t b) { return (a + b - 1) / b; }
+
+__global__ __launch_bounds__(RESERVE_THREADS) void kv_reserve_kernel(ReserveParams p) {
+  __shared__ int64_t s_need[RESERVE_THREADS / 64];
+  __shared__ int s_bad[RESERVE_THREADS / 64];
+  __shared__ int s_scan[RESERVE_THREADS / 64];
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int64_t head = p.free_state[0];
+  const int64_t avail = p.free_state[1];
+  const int64_t len_max = p.lengths_i64 ? INT64_MAX / 2 : 0x7fffffff;
+
+  // pass 1: blocks needed and table / length checks
+  int64_t need = 0;
+  int bad = 0;
+  for (int64_t b = tid; b < p.batch; b += RESERVE_THREADS) {
+    const int64_t len = read_index(p.lengths, p.lengths_i64, b);
+    const int64_t n = p.counts != nullptr ? read_index(p.counts, p.counts_i64, b) : p.count_scalar;
+    if (len < 0 || n < 0 || len > len_max - n) {
+      bad |= 4;
+      continue;
+    }
+    const int64_t have = ceil_div64(len, p.bs);
+    const int64_t want = ceil_div64(len + n, p.bs);
+    if (want > p.max_blocks) bad |= 2;
+    need += want - have;
+  }
+  for (int off = 32; off > 0; off >>= 1) {
+    need += __shfl_xor(need, off, 64);
+    bad |= __shfl_xor(bad, off, 64);
+  }
+  if (lane == 0) {
+    s_need[wave] = need;
+    s_bad[wave] = bad;
+  }
+  __syncthreads();
+  int64_t total = 0;
+  bad = 0;
+#pragma unroll
+  for (int w = 0; w < RESERVE_THREADS / 64; ++w) {
+    total += s_need[w];
+    bad |= s_bad[w];
+  }
+  int code = 0;
+  if (head < 0 || avail < 0 || head + avail > p.capacity) code = 3;  // corrupt cursor
+  else if (bad & 4) code = 4;                                         // negative length/count or overflow
+  else if (bad & 2) code = 2;                                         // a table is too short
+  else if (total > avail) code = 1;                                   // not enough free blocks
+  if (code != 0) {
+    if (tid == 0) p.status[0] = code;
+    return;
+  }
+
+  // pass 2: exclusive scan of the per-row block counts, 1024 rows at a time
+  int64_t base = head;
+  for (int64_t r0 = 0; r0 < p.batch; r0 += RESERVE_THREADS) {
+    const int64_t b = r0 + tid;
+    int64_t len = 0, n = 0, have = 0;
+    int k = 0;
+    if (b < p.batch) {
+      len = read_index(p.lengths, p.lengths_i64, b);
+      n = p.counts != nullptr ? read_index(p.counts, p.counts_i64, b) : p.count_scalar;
+      have = ceil_div64(len, p.bs);
+      k = static_cast<int>(ceil_div64(len + n, p.bs) - have);
+    }
+    int incl = k;
+    for (int off = 1; off < 64; off <<= 1) {
+      const int up = __shfl_up(incl, off, 64);
+      if (lane >= off) incl += up;
+    }
+    if (lane == 63) s_scan[wave] = incl;
+    __syncthreads();
+    int before = 0, tile = 0;
+#pragma unroll
+    for (int w = 0; w < RESERVE_THREADS / 64; ++w) {
+      const int s = s_scan[w];
+      before += w < wave ? s : 0;
+      tile += s;
+    }
+    const int64_t first = base + before + incl - k;
+    for (int i = 0; i < k; ++i)
+      write_index(p.tables, p.table_i64, b * p.table_stride + have + i, p.free_list[first + i]);
+    if (b < p.batch) {
+      if (p.positions != nullptr) write_index(p.positions, p.positions_i64, b, len);
+      write_index(p.lengths, p.lengths_i64, b, len + n);
+    }
+    base += tile;
+    __syncthreads();  // s_scan is reused by the next group of rows
+  }
+  if (tid == 0) {
+    p.free_state[0] = static_cast<int32_t>(head + total);
+    p.free_state[1] = static_cast<int32_t>(avail - total);
+    p.status[0] = 0;
+  }
+}
+
+}  // namespace qa
+
+extern "C" int qa_paged_kv_reserve(void* block_tables, int32_t table_dtype, int64_t table_stride, int64_t max_blocks,
+                                   void* lengths, int32_t lengths_dtype, void* positions, int32_t positions_dtype,
+                                   const void* counts, int32_t counts_dtype, int64_t count_scalar, int64_t batch,
+                                   int32_t block_size, const int32_t* free_list, int64_t free_capacity, int32_t* free_state,
+                                   int32_t* status, hipStream_t stream) {
+  using namespace qa;
+  QA_REQUIRE(block_tables != nullptr && is_index_dtype(table_dtype), "block table must be an int32/int64 device array");
+  QA_REQUIRE(lengths != nullptr && is_index_dtype(lengths_dtype), "lengths must be an int32/int64 device array");
+  QA_REQUIRE(positions == nullptr || is_index_dtype(positions_dtype), "positions must be an int32/int64 device array");
+  QA_REQUIRE(counts == nullptr || is_index_dtype(counts_dtype), "counts must be an int32/int64 device array");
+  QA_REQUIRE(counts != nullptr || count_scalar >= 0, "count must be non-negative");
+  QA_REQUIRE(free_list != nullptr && free_state != nullptr && status != nullptr, "free list, free state and status must be non-null");
+  QA_REQUIRE(free_capacity > 0 && free_capacity <= 0x7fffffff, "free list capacity must be in [1, 2^31)");
+  QA_REQUIRE(batch >= 0, "batch must be non-negative");
+  QA_REQUIRE(block_size > 0 && max_blocks > 0, "block_size and max_blocks must be positive");
+  QA_REQUIRE(table_stride >= max_blocks || batch <= 1, "table rows overlap: stride %lld < max_blocks %lld",
+             static_cast<long long>(table_stride), static_cast<long long>(max_blocks));
+  ReserveParams p{};
+  p.tables = block_tables;
+  p.table_stride = table_stride;
+  p.max_blocks = max_blocks;
+  p.lengths = lengths;
+  p.positions = positions;
+  p.counts = counts;
+  p.count_scalar = count_scalar;
+  p.free_list = free_list;
+  p.free_state = free_state;
+  p.status = status;
+  p.batch = batch;
+  p.capacity = free_capacity;
+  p.bs = block_size;
+  p.table_i64 = table_dtype == QA_I64;
+  p.lengths_i64 = lengths_dtype == QA_I64;
+  p.positions_i64 = positions_dtype == QA_I64;
+  p.counts_i64 = counts_dtype == QA_I64;
+  {
+    KernelTimer timer_("kv_reserve", stream);
+    hipLaunchKernelGGL(kv_reserve_kernel, dim3(1), dim3(RESERVE_THREADS), 0, stream, p);
+  }
+  return check_launch("paged_kv_reserve");
+}

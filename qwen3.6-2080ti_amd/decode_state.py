@@ -151,6 +151,86 @@ class SharedKVBlockPool:
         if blocks:
             self.free_blocks = sorted(self.free_blocks + list(blocks))
 
+    def device_allocator(self) -> "DeviceBlockAllocator":
+        """Hand this pool's free list to a ``DeviceBlockAllocator``.
+
+        From then on blocks are reserved on the device; the host list is emptied
+        so a host ``allocate`` cannot hand out an id the device also owns.
+        """
+        allocator = DeviceBlockAllocator(self.block_count, device=self.key_blocks.device, free_blocks=self.free_blocks)
+        self.free_blocks = []
+        return allocator
+
+
+class DeviceBlockAllocator:
+    """Device-resident free list of a shared KV pool.
+
+    A batched step reserves the blocks its rows need with one kernel
+    (``hip_ops.paged_kv_reserve``): the ids come from the head of an ascending
+    int32 list, rows in order -- the reference's lowest-free-id policy
+    (``src/decode_state.py:72-78``) -- and the block tables and lengths are
+    updated on the device.  A decode step of reserve, K/V append and attention
+    therefore never waits for the host and can be captured in a HIP graph; the
+    host reads ``status`` only when it chooses to (``check``).  ``release``
+    (request completion) merges ids back and re-sorts on the host, as the
+    reference's ``release`` does (``src/decode_state.py:80-84``).
+    """
+
+    def __init__(self, num_blocks: int, *, device: Any, free_blocks: Sequence[int] | None = None) -> None:
+        import torch
+
+        if num_blocks <= 0:
+            raise ValueError("num_blocks must be positive")
+        ids = list(range(num_blocks)) if free_blocks is None else sorted(int(i) for i in free_blocks)
+        if ids and (ids[0] < 0 or ids[-1] >= num_blocks or len(set(ids)) != len(ids)):
+            raise ValueError("free block ids must be distinct and in [0, num_blocks)")
+        self.capacity = num_blocks
+        self.device = torch.device(device)
+        self.free_list = torch.full((num_blocks,), -1, dtype=torch.int32, device=self.device)
+        if ids:
+            self.free_list[: len(ids)] = torch.tensor(ids, dtype=torch.int32, device=self.device)
+        self.free_state = torch.tensor([0, len(ids)], dtype=torch.int32, device=self.device)
+        self.status = torch.zeros(1, dtype=torch.int32, device=self.device)
+
+    _STATUS = {
+        1: "shared KV pool exhausted",
+        2: "block table too short for the reserved blocks",
+        3: "device free list state is corrupt",
+        4: "negative or overflowing length/count",
+    }
+
+    def reserve(self, block_tables: Any, lengths: Any, block_size: int, *, counts: Any = 1, positions: Any = None) -> None:
+        """Reserve blocks for ``counts`` new tokens per row; advances ``lengths`` in place."""
+        import hip_ops
+
+        hip_ops.paged_kv_reserve(block_tables, lengths, self.free_list, self.free_state, self.status, block_size, counts=counts, positions=positions)
+
+    def check(self) -> None:
+        """Raise ``RuntimeError`` if the last reservation failed (reads the status: a sync)."""
+        code = int(self.status.item())
+        if code != 0:
+            raise RuntimeError(f"paged_kv_reserve failed: {self._STATUS.get(code, f'status {code}')}")
+
+    def free_blocks(self) -> list[int]:
+        head, count = (int(v) for v in self.free_state.tolist())
+        return [int(v) for v in self.free_list[head : head + count].tolist()]
+
+    @property
+    def free_count(self) -> int:
+        return int(self.free_state[1].item())
+
+    def release(self, blocks: Sequence[int]) -> None:
+        import torch
+
+        blocks = [int(b) for b in blocks]
+        if not blocks:
+            return
+        merged = sorted(self.free_blocks() + blocks)
+        if merged[0] < 0 or merged[-1] >= self.capacity or len(set(merged)) != len(merged):
+            raise ValueError("released block ids must be in range and not already free")
+        self.free_list[: len(merged)] = torch.tensor(merged, dtype=torch.int32, device=self.device)
+        self.free_state.copy_(torch.tensor([0, len(merged)], dtype=torch.int32))
+
 
 # --------------------------------------------------------------------------- records
 

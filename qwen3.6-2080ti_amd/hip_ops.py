@@ -338,6 +338,64 @@ def paged_kv_append(
     L.check(lib, status, "paged_kv_append")
 
 
+def paged_kv_reserve(
+    block_tables: torch.Tensor,
+    lengths: torch.Tensor,
+    free_list: torch.Tensor,
+    free_state: torch.Tensor,
+    status: torch.Tensor,
+    block_size: int,
+    *,
+    counts: torch.Tensor | int = 1,
+    positions: torch.Tensor | None = None,
+) -> None:
+    """Reserve the blocks a batched step needs, on the device (no host round trip).
+
+    Row ``b`` grows from ``lengths[b]`` to ``lengths[b] + counts_b`` tokens: its new
+    logical blocks get ids from the head of the ascending ``free_list`` (int32),
+    rows in order -- the reference's lowest-free-id policy
+    (``src/decode_state.py:72-78``).  ``free_state`` (int32 ``[head, count]``) is
+    advanced, ``lengths`` are advanced in place, ``positions`` (if given) receives
+    the old lengths.  ``status`` (int32 ``[1]``) becomes 0, or 1 (pool exhausted),
+    2 (a table row too short), 3 (corrupt free state), 4 (negative or overflowing
+    length or count), in which case nothing else is written.  Every argument is a
+    device tensor and nothing is read back, so the call can be captured in a HIP graph.
+    """
+    lib = L.load_library()
+    _require_cuda(block_tables, "block_tables")
+    device = block_tables.device
+    for tensor, name in ((lengths, "lengths"), (free_list, "free_list"), (free_state, "free_state"), (status, "status")):
+        _require_cuda(tensor, name, device)
+    _index_dtype(block_tables, "block_tables")
+    _index_dtype(lengths, "lengths")
+    _require(block_tables.dim() == 2 and block_tables.stride(1) == 1, "block_tables must have shape [batch, max_blocks] with contiguous rows")
+    _require(lengths.dim() == 1 and lengths.is_contiguous() and lengths.shape[0] == block_tables.shape[0], "lengths must be a contiguous [batch] tensor")
+    _require(free_list.dtype == torch.int32 and free_list.dim() == 1 and free_list.is_contiguous(), "free_list must be a contiguous int32 vector")
+    _require(free_state.dtype == torch.int32 and free_state.numel() == 2 and free_state.is_contiguous(), "free_state must be int32 [head, count]")
+    _require(status.dtype == torch.int32 and status.numel() >= 1, "status must be an int32 tensor")
+    count_ptr, count_code, count_scalar = ctypes.c_void_p(0), L.QA_I64, 0
+    if isinstance(counts, torch.Tensor):
+        _require_cuda(counts, "counts", device)
+        _index_dtype(counts, "counts")
+        _require(counts.dim() == 1 and counts.is_contiguous() and counts.shape[0] == lengths.shape[0], "counts must be a contiguous [batch] tensor")
+        count_ptr, count_code = _ptr(counts), _code(counts)
+    else:
+        count_scalar = int(counts)
+        _require(count_scalar >= 0, "counts must be non-negative")
+    pos_ptr, pos_code = ctypes.c_void_p(0), L.QA_I64
+    if positions is not None:
+        _require_cuda(positions, "positions", device)
+        _index_dtype(positions, "positions")
+        _require(positions.dim() == 1 and positions.is_contiguous() and positions.shape[0] == lengths.shape[0], "positions must be a contiguous [batch] tensor")
+        pos_ptr, pos_code = _ptr(positions), _code(positions)
+    status_code = lib.qa_paged_kv_reserve(
+        _ptr(block_tables), _code(block_tables), block_tables.stride(0), block_tables.shape[1], _ptr(lengths), _code(lengths),
+        pos_ptr, pos_code, count_ptr, count_code, count_scalar, lengths.shape[0], int(block_size), _ptr(free_list),
+        free_list.numel(), _ptr(free_state), _ptr(status), _stream(device),
+    )
+    L.check(lib, status_code, "paged_kv_reserve")
+
+
 def paged_kv_gather(key_pool: torch.Tensor, value_pool: torch.Tensor, block_tables: torch.Tensor, valid: int, block_size: int) -> tuple[torch.Tensor, torch.Tensor]:
     """Dense ``(B, H_kv, valid, D)`` logical-order K/V (``src/decode_state.py:295-303,395-404``)."""
     lib = L.load_library()

@@ -112,3 +112,162 @@ def test_append_then_decode_equals_dense_reference() -> None:
     for b in range(2):
         ref = attention.dense_attention(q[b : b + 1], dense_k[b : b + 1, :, : lens[b]], dense_v[b : b + 1, :, : lens[b]], position_offset=lens[b] - 1)
         torch.testing.assert_close(out[b : b + 1].cpu().float(), ref.float(), atol=2e-2, rtol=2e-2)
+
+
+@pytest.mark.parametrize("table_dtype,batch", [(torch.int32, 5), (torch.int64, 3000)])
+def test_device_reserve_matches_oracle_bit_exact(table_dtype, batch) -> None:
+    import hip_ops
+
+    rng = np.random.default_rng(31 + batch)
+    bs, max_blocks, capacity = 16, 24, 40000
+    lengths = rng.integers(0, 300, batch)
+    counts = rng.integers(0, 60, batch)
+    counts[::7] = 0
+    free = sorted(rng.permutation(capacity)[: capacity - 1000].tolist())
+    tables = np.full((batch, max_blocks), -1, dtype=np.int64)
+    status, want_t, want_pos, want_len, want_free = paged_kv.reserve_step(tables, lengths, counts, free, bs)
+    assert status == 0
+    print(f"device reserve: batch {batch}, table {table_dtype}, {len(free) - len(want_free)} blocks", flush=True)
+    free_list = torch.full((capacity,), -1, dtype=torch.int32, device=DEV)
+    free_list[: len(free)] = torch.tensor(free, dtype=torch.int32, device=DEV)
+    free_state = torch.tensor([0, len(free)], dtype=torch.int32, device=DEV)
+    st = torch.full((1,), 99, dtype=torch.int32, device=DEV)
+    t = torch.from_numpy(tables).to(DEV, table_dtype)
+    lens = torch.from_numpy(lengths).to(DEV, torch.int32)
+    pos = torch.full((batch,), -5, dtype=torch.int64, device=DEV)
+    hip_ops.paged_kv_reserve(t, lens, free_list, free_state, st, bs, counts=torch.from_numpy(counts).to(DEV), positions=pos)
+    assert int(st.item()) == 0
+    np.testing.assert_array_equal(t.cpu().numpy().astype(np.int64), want_t)
+    np.testing.assert_array_equal(pos.cpu().numpy(), want_pos)
+    np.testing.assert_array_equal(lens.cpu().numpy(), want_len)
+    head, count = free_state.tolist()
+    assert free_list[head : head + count].tolist() == want_free
+
+
+def test_device_reserve_failure_writes_nothing() -> None:
+    import hip_ops
+
+    bs = 16
+    free_list = torch.arange(3, dtype=torch.int32, device=DEV)
+    free_state = torch.tensor([0, 3], dtype=torch.int32, device=DEV)
+    st = torch.zeros(1, dtype=torch.int32, device=DEV)
+    tables = torch.full((2, 4), -1, dtype=torch.int32, device=DEV)
+    lens = torch.tensor([0, 0], dtype=torch.int64, device=DEV)
+    # 40 + 20 tokens need 3 + 2 blocks, 3 are free
+    hip_ops.paged_kv_reserve(tables, lens, free_list, free_state, st, bs, counts=torch.tensor([40, 20], device=DEV))
+    assert int(st.item()) == 1
+    # 70 tokens need 5 blocks of a 4-wide row
+    hip_ops.paged_kv_reserve(tables, lens, free_list, free_state, st, bs, counts=torch.tensor([70, 0], device=DEV))
+    assert int(st.item()) == 2
+    assert (tables == -1).all().item() and lens.tolist() == [0, 0] and free_state.tolist() == [0, 3]
+    # then a fitting request succeeds from the untouched state
+    hip_ops.paged_kv_reserve(tables, lens, free_list, free_state, st, bs, counts=torch.tensor([17, 16], device=DEV))
+    assert int(st.item()) == 0 and tables.tolist() == [[0, 1, -1, -1], [2, -1, -1, -1]] and free_state.tolist() == [3, 0]
+
+
+def test_device_allocator_release_resorts_and_reuses() -> None:
+    from decode_state import DeviceBlockAllocator
+
+    alloc = DeviceBlockAllocator(8, device=DEV)
+    tables = torch.full((2, 4), -1, dtype=torch.int32, device=DEV)
+    lens = torch.tensor([0, 0], dtype=torch.int32, device=DEV)
+    alloc.reserve(tables, lens, 4, counts=torch.tensor([9, 6], dtype=torch.int32, device=DEV))
+    alloc.check()
+    assert tables.tolist() == [[0, 1, 2, -1], [3, 4, -1, -1]] and alloc.free_blocks() == [5, 6, 7]
+    alloc.release([3, 1])
+    assert alloc.free_blocks() == [1, 3, 5, 6, 7] and alloc.free_count == 5
+    tables2 = torch.full((1, 4), -1, dtype=torch.int32, device=DEV)
+    alloc.reserve(tables2, torch.zeros(1, dtype=torch.int32, device=DEV), 4, counts=5)
+    alloc.check()
+    assert tables2.tolist() == [[1, 3, -1, -1]]
+    alloc.reserve(tables2, torch.zeros(1, dtype=torch.int32, device=DEV), 4, counts=16)  # 4 blocks, 3 free
+    with pytest.raises(RuntimeError, match="exhausted"):
+        alloc.check()
+    alloc.reserve(tables2, torch.zeros(1, dtype=torch.int32, device=DEV), 4, counts=17)  # 5 blocks of a 4-wide row
+    with pytest.raises(RuntimeError, match="table too short"):
+        alloc.check()
+    assert tables2.tolist() == [[1, 3, -1, -1]] and alloc.free_blocks() == [5, 6, 7]
+
+
+def test_graph_captured_decode_step_matches_eager_and_oracle() -> None:
+    """reserve -> K/V append -> batched decode captured once and replayed step after
+    step; every replay equals the same step run eagerly on a twin state, and the last
+    one matches the oracle's attention over the gathered cache."""
+    import hip_ops
+    from decode_state import DeviceBlockAllocator
+    from oracle import attention as oracle_attn
+
+    gen = torch.Generator().manual_seed(41)
+    batch, heads, kv_heads, dim, bs, pool_blocks, max_blocks, steps = 6, 16, 2, 256, 16, 96, 12, 5
+    init = torch.tensor([1, 15, 16, 33, 0, 47], dtype=torch.int32)
+
+    def make_state():
+        pool_k = torch.zeros(pool_blocks, kv_heads, bs, dim, dtype=torch.bfloat16, device=DEV)
+        pool_v = torch.zeros_like(pool_k)
+        alloc = DeviceBlockAllocator(pool_blocks, device=DEV)
+        tables = torch.full((batch, max_blocks), -1, dtype=torch.int32, device=DEV)
+        lens = torch.zeros(batch, dtype=torch.int32, device=DEV)
+        pos = torch.zeros(batch, dtype=torch.int64, device=DEV)
+        return dict(pool_k=pool_k, pool_v=pool_v, alloc=alloc, tables=tables, lens=lens, pos=pos)
+
+    prefill_k = torch.randn(batch, kv_heads, 64, dim, generator=gen).to(torch.bfloat16).to(DEV)
+    prefill_v = torch.randn(batch, kv_heads, 64, dim, generator=gen).to(torch.bfloat16).to(DEV)
+
+    def prefill(s):
+        s["alloc"].reserve(s["tables"], s["lens"], bs, counts=init.to(DEV), positions=s["pos"])
+        hip_ops.paged_kv_append(prefill_k, prefill_v, s["pool_k"], s["pool_v"], s["tables"], s["pos"], bs, counts=init.to(DEV))
+
+    def step(s, q, k, v):
+        s["alloc"].reserve(s["tables"], s["lens"], bs, counts=1, positions=s["pos"])
+        hip_ops.paged_kv_append(k, v, s["pool_k"], s["pool_v"], s["tables"], s["pos"], bs)
+        return hip_ops.paged_attention_decode_batched(q, s["tables"], s["pool_k"], s["pool_v"], s["lens"], bs)
+
+    eager, graphed, scratch = make_state(), make_state(), make_state()
+    for s in (eager, graphed, scratch):
+        prefill(s)
+    q_static = torch.zeros(batch, heads, 1, dim, dtype=torch.bfloat16, device=DEV)
+    k_static = torch.zeros(batch, kv_heads, 1, dim, dtype=torch.bfloat16, device=DEV)
+    v_static = torch.zeros_like(k_static)
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        step(scratch, q_static, k_static, v_static)  # first-call set-up outside the capture
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        out_static = step(graphed, q_static, k_static, v_static)
+    print("graph captured", flush=True)
+    for i in range(steps):
+        q = torch.randn(batch, heads, 1, dim, generator=gen).to(torch.bfloat16).to(DEV)
+        k = torch.randn(batch, kv_heads, 1, dim, generator=gen).to(torch.bfloat16).to(DEV)
+        v = torch.randn(batch, kv_heads, 1, dim, generator=gen).to(torch.bfloat16).to(DEV)
+        q_static.copy_(q)
+        k_static.copy_(k)
+        v_static.copy_(v)
+        graph.replay()
+        out_eager = step(eager, q, k, v)
+        torch.cuda.synchronize()
+        eager["alloc"].check()
+        graphed["alloc"].check()
+        assert torch.equal(out_static, out_eager), f"replay {i}"
+        for name in ("tables", "lens", "pos", "pool_k", "pool_v"):
+            assert torch.equal(graphed[name], eager[name]), f"replay {i}: {name}"
+        assert torch.equal(graphed["alloc"].free_state, eager["alloc"].free_state)
+    lens = eager["lens"].tolist()
+    assert lens == [int(n) + steps for n in init]
+    tables = eager["tables"].cpu().tolist()
+    ref = oracle_attn.paged_decode(
+        q.cpu(), [eager["pool_k"].cpu()] * batch, [eager["pool_v"].cpu()] * batch, tables, lens, block_size=bs, pool_layout="phbd"
+    )
+    torch.testing.assert_close(out_static.cpu().float(), ref.float(), atol=2e-2, rtol=2e-2)
+    # ids were handed out lowest first in row order: the prefill's blocks, then one per
+    # row whose next token opens a block
+    status, want_t, _p, want_len, _f = paged_kv.reserve_step(
+        np.full((batch, max_blocks), -1, dtype=np.int64), np.zeros(batch, dtype=np.int64), init.numpy(), list(range(pool_blocks)), bs
+    )
+    cur = want_len
+    for _ in range(steps):
+        status, want_t, _p, cur, _f = paged_kv.reserve_step(want_t, cur, 1, sorted(set(range(pool_blocks)) - set(want_t[want_t >= 0].tolist())), bs)
+        assert status == 0
+    np.testing.assert_array_equal(np.asarray(tables, dtype=np.int64), want_t)

@@ -99,3 +99,61 @@ def test_slot_mapping_closed_form() -> None:
     # row 0: pos 3 -> block 1 off 1 -> 3; pos 4 -> block 5 off 0 -> 10
     # row 1: pos 0..4 -> 0, 1, 4, 5, 8
     assert slots.tolist() == [3, 10, 0, 1, 4, 5, 8]
+
+
+def _reserve_token_by_token(tables, lengths, counts, free, bs):
+    """Brute force: each row appends its tokens one at a time and takes one block
+    from the head of the free list whenever a token starts a new block."""
+    tables = tables.copy()
+    free = list(free)
+    for b in range(len(lengths)):
+        for pos in range(int(lengths[b]), int(lengths[b] + counts[b])):
+            if pos % bs == 0:
+                tables[b, pos // bs] = free.pop(0)
+    return tables, free
+
+
+def test_reserve_step_matches_token_by_token_growth() -> None:
+    rng = np.random.default_rng(5)
+    bs, batch, max_blocks = 16, 37, 12
+    lengths = rng.integers(0, 100, batch)
+    counts = rng.integers(0, 40, batch)
+    counts[::5] = 0
+    free = sorted(rng.permutation(400)[:300].tolist())
+    tables = np.full((batch, max_blocks), -1, dtype=np.int64)
+    status, got, pos, new_len, rest = paged_kv.reserve_step(tables, lengths, counts, free, bs)
+    assert status == 0
+    want, want_rest = _reserve_token_by_token(tables, lengths, counts, free, bs)
+    np.testing.assert_array_equal(got, want)
+    assert rest == want_rest
+    np.testing.assert_array_equal(pos, lengths)
+    np.testing.assert_array_equal(new_len, lengths + counts)
+
+
+def test_reserve_step_is_free_list_allocate_per_row() -> None:
+    # the reference's pool hands out the head of its sorted free list per request
+    # (src/decode_state.py:72-78): rows of 0, 17 and 32 tokens, one new token each,
+    # need 1, 0 and 1 new blocks, taken as ids 0 then 1.
+    free = paged_kv.FreeList()
+    free.grow(6)
+    tables = np.full((3, 4), -1, dtype=np.int64)
+    tables[1, :2] = [4, 5]
+    tables[2, :2] = [2, 3]
+    status, got, _pos, new_len, rest = paged_kv.reserve_step(tables, np.array([0, 17, 32]), 1, [0, 1], 16)
+    assert status == 0
+    assert got[0].tolist() == [0, -1, -1, -1] and got[2].tolist() == [2, 3, 1, -1] and got[1].tolist() == [4, 5, -1, -1]
+    assert free.allocate(1) == [0] and free.allocate(1) == [1]
+    assert rest == [] and new_len.tolist() == [1, 18, 33]
+
+
+def test_reserve_step_all_or_nothing() -> None:
+    tables = np.full((2, 2), -1, dtype=np.int64)
+    lengths = np.array([0, 0])
+    # exhausted: needs 2 + 1 blocks, 2 free
+    status, got, _p, new_len, rest = paged_kv.reserve_step(tables, lengths, np.array([20, 5]), [7, 9], 16)
+    assert status == 1 and (got == -1).all() and new_len.tolist() == [0, 0] and rest == [7, 9]
+    # table too short: 40 tokens need 3 blocks of a 2-wide row
+    status, got, *_ = paged_kv.reserve_step(tables, lengths, np.array([40, 0]), list(range(10)), 16)
+    assert status == 2 and (got == -1).all()
+    status, *_ = paged_kv.reserve_step(tables, np.array([-1, 0]), 1, list(range(10)), 16)
+    assert status == 4
