@@ -140,6 +140,24 @@ int qa_paged_kv_gather(const qa_paged_kv* kv, int32_t head_dim, int64_t batch,
                        int64_t max_blocks, int64_t valid, int32_t block_size,
                        void* key_out, void* value_out, hipStream_t stream);
 
+/* ---- fp8 E4M3 block-scaled linear ------------------------------------- */
+/* y (rows, out_features) = x (rows, in_features) . W^T, W[n][k] =
+ * E4M3(weight[n][k]) * scale[n/128][k/128]: weight (out, in) fp8 E4M3 (fn)
+ * codes, row-major; scale (out/128, in/128) bf16; x float32 or bfloat16 rows
+ * (x_stride elements apart, 16-byte aligned); y float32 or bfloat16.  Both
+ * feature counts must be multiples of 128.  Weight values are converted
+ * exactly, scales applied per 128-deep block in fp32, fp32 x as a bf16
+ * hi + lo pair.  workspace: qa_fp8_linear_workspace(rows, out, in) bytes
+ * (0 when no K split is used; then it may be NULL).  Replaces
+ * fp8_e4m3_bf16_linear (src/fp8_cuda.py:16-17 -> src/csrc/fp8_linear.h,
+ * src/csrc/fp8_linear_cuda.cu:1368-1466) and the dequantised F.linear of
+ * src/reference_ops.py:436-506.                                            */
+int64_t qa_fp8_linear_workspace(int64_t rows, int64_t out_features, int64_t in_features);
+int qa_fp8_linear(const void* x, int32_t x_dtype, int64_t x_stride, int64_t rows,
+                  const void* weight, const void* scale, int64_t out_features, int64_t in_features,
+                  void* y, int32_t y_dtype, int64_t y_stride, void* workspace, int64_t workspace_bytes,
+                  hipStream_t stream);
+
 /* Device-side block reservation for a batched step (one kernel, no host
  * round trip, so a decode step can be captured in a HIP graph).  Row b grows
  * from lengths[b] to lengths[b] + n_b tokens (n_b = counts[b], or count_scalar

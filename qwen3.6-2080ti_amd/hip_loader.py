@@ -79,6 +79,12 @@ SIGNATURES: dict[str, tuple[Any, list[Any]]] = {
          c_float, c_void_p, c_void_p, c_int64, c_int32, c_void_p, c_void_p, c_int32, c_int64, c_int64, c_int32, c_int32, ctypes.POINTER(PagedKV),
          c_void_p, c_int32, c_int64, c_int64, c_int32, c_void_p, c_void_p],
     ),
+    "qa_fp8_linear_workspace": (c_int64, [c_int64, c_int64, c_int64]),
+    "qa_fp8_linear": (
+        c_int32,
+        [c_void_p, c_int32, c_int64, c_int64, c_void_p, c_void_p, c_int64, c_int64, c_void_p, c_int32, c_int64, c_void_p, c_int64,
+         c_void_p],
+    ),
     "qa_paged_kv_reserve": (
         c_int32,
         [c_void_p, c_int32, c_int64, c_int64, c_void_p, c_int32, c_void_p, c_int32, c_void_p, c_int32, c_int64, c_int64, c_int32,

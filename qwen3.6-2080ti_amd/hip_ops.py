@@ -396,6 +396,46 @@ def paged_kv_reserve(
     L.check(lib, status_code, "paged_kv_reserve")
 
 
+def fp8_e4m3_bf16_linear(input: torch.Tensor, weight: torch.Tensor, scale: torch.Tensor, *, out_dtype: torch.dtype = torch.float32) -> torch.Tensor:
+    """``y = input @ (E4M3(weight) * block scale)^T`` with 128 x 128 bf16 scale blocks.
+
+    Same name, arguments and result as the reference's ``fp8_cuda.fp8_e4m3_bf16_linear``
+    (``src/fp8_cuda.py:16-17`` -> ``src/csrc/fp8_linear_cuda.cu:1368-1466``): ``weight``
+    ``(N, K)`` ``torch.float8_e4m3fn`` (or its uint8 codes), ``scale`` ``(N/128, K/128)``
+    bf16, ``input`` ``(..., K)`` float32 (bf16 also accepted); returns ``(..., N)`` float32
+    (or ``out_dtype`` bf16).  N and K must be multiples of 128, as in the reference's op.
+    """
+    lib = L.load_library()
+    _require_cuda(input, "input")
+    device = input.device
+    _require_cuda(weight, "weight", device)
+    _require_cuda(scale, "scale", device)
+    _require(input.dtype in (torch.float32, torch.bfloat16), "input must be float32 or bfloat16")
+    _require(weight.dtype in (torch.float8_e4m3fn, torch.uint8), "weight must be torch.float8_e4m3fn")
+    _require(scale.dtype == torch.bfloat16, "scale must be bfloat16")
+    _require(weight.dim() == 2, "weight must be rank-2")
+    _require(scale.dim() == 2, "scale must be rank-2")
+    _require(input.dim() >= 2, "input must be at least rank-2")
+    _require(out_dtype in (torch.float32, torch.bfloat16), "out_dtype must be float32 or bfloat16")
+    rows, cols = weight.shape
+    _require(input.shape[-1] == cols, "input last dim must match weight cols")
+    _require(rows % 128 == 0, "weight rows must be divisible by 128 for the FP8 op")
+    _require(cols % 128 == 0, "weight cols must be divisible by 128 for the FP8 op")
+    _require(tuple(scale.shape) == (rows // 128, cols // 128), "scale blocks mismatch")
+    x = input.contiguous().view(-1, cols)
+    w = weight.contiguous()
+    s = scale.contiguous()
+    out = torch.empty((x.shape[0], rows), dtype=out_dtype, device=device)
+    nbytes = int(lib.qa_fp8_linear_workspace(x.shape[0], rows, cols))
+    ws = torch.empty(max(nbytes, 4), dtype=torch.uint8, device=device)
+    status = lib.qa_fp8_linear(
+        _ptr(x), _code(x), x.stride(0), x.shape[0], _ptr(w), _ptr(s), rows, cols, _ptr(out), _code(out), out.stride(0), _ptr(ws),
+        ws.numel(), _stream(device),
+    )
+    L.check(lib, status, "fp8_e4m3_bf16_linear")
+    return out.view(*input.shape[:-1], rows)
+
+
 def paged_kv_gather(key_pool: torch.Tensor, value_pool: torch.Tensor, block_tables: torch.Tensor, valid: int, block_size: int) -> tuple[torch.Tensor, torch.Tensor]:
     """Dense ``(B, H_kv, valid, D)`` logical-order K/V (``src/decode_state.py:295-303,395-404``)."""
     lib = L.load_library()
