@@ -43,6 +43,7 @@ TRAFFIC_DELTA = 1636029928
 TRAFFIC_PREFILL = 888455186  # average over the eight per-chunk launches
 TRAFFIC_PROLOGUE = 675541424
 TRAFFIC_OUTPUT_NORM = 805389585
+TRAFFIC_FP8_LINEAR = None  # set from the rocprofv3 --pmc runs of profiles/fp8_linear_config5_batch.md
 SECONDARY_WARM_MS = 100.0  # wall time of untimed steps before each secondary (config 3, 4, 5) measurement
 MFMA_BF16_PEAK_TFLOPS = 2500.0  # MI355X dense bf16/fp16 MFMA, TFLOP/s
 
@@ -357,6 +358,35 @@ def time_output_norm(w: dict, steps: int, warmup: int):
     return _timed(step, steps, warmup, ("gated_rms_norm",), warm_ms=SECONDARY_WARM_MS, timing_repeats=20)
 
 
+def fp8_linear_workload(device: str, *, seed: int = 3, rows: int = 128, out_features: int = 8192, in_features: int = 2048) -> dict:
+    """An fp8 E4M3 block-scaled projection at config 5's decode batch: rows = 128 tokens, out =
+    16 heads x 2 x 256 (q_proj with its gate half), in = a 2048 hidden size; fp32 input as the
+    reference passes it (``hidden_states.float()``), fp32 output; the weight is packed once by
+    ``fp8_pack_weight`` as a serving stack would at load time."""
+    import torch
+
+    import hip_ops
+
+    gen = torch.Generator(device=device).manual_seed(seed)
+    w = (0.5 * torch.randn((out_features, in_features), generator=gen, device=device)).to(torch.float8_e4m3fn)
+    s = (0.05 + torch.rand((out_features // 128, in_features // 128), generator=gen, device=device)).to(torch.bfloat16)
+    x = torch.randn((rows, in_features), generator=gen, device=device)
+    # bytes: weight codes + scales + x read, y written
+    algo = out_features * in_features + s.numel() * 2 + rows * in_features * 4 + rows * out_features * 4
+    w = hip_ops.fp8_pack_weight(w)  # once, as at weight-load time
+    return {"w": w, "s": s, "x": x, "algo_bytes": algo, "flops": 2.0 * rows * out_features * in_features,
+            "rows": rows, "out": out_features, "in": in_features}
+
+
+def time_fp8_linear(w: dict, steps: int, warmup: int):
+    import hip_ops
+
+    def step():
+        hip_ops.fp8_e4m3_bf16_linear(w["x"], w["w"], w["s"])
+
+    return _timed(step, steps, warmup, ("fp8_linear", "fp8_linear_reduce"), warm_ms=SECONDARY_WARM_MS, timing_repeats=20)
+
+
 # ----------------------------------------------------------------------------- config 5
 
 
@@ -444,6 +474,7 @@ def main() -> int:
     parser.add_argument("--no-hybrid", action="store_true", help="skip the config-5 secondary measurement")
     parser.add_argument("--no-prologue", action="store_true", help="skip the full-attention prologue measurement (config 3 shapes)")
     parser.add_argument("--no-output-norm", action="store_true", help="skip the linear-attention output stage measurement (config 4 shapes)")
+    parser.add_argument("--no-fp8-linear", action="store_true", help="skip the fp8 block-scaled projection measurement (config 5 batch)")
     parser.add_argument("--copy-probe-mib", type=int, default=0,
                         help="first run one plain device copy of this many MiB (reference point for HBM byte counters)")
     parser.add_argument("--cpu-budget", type=float, default=12.0)
@@ -610,6 +641,26 @@ def main() -> int:
                          "kernels": hkern},
         }
         del hw
+        torch.cuda.empty_cache()
+    if not args.no_fp8_linear:
+        fw = fp8_linear_workload(device)
+        fms, fkern = time_fp8_linear(fw, max(20, args.steps), max(1, args.warmup))
+        f_ms = fkern["fp8_linear"]["avg_ms"] + fkern.get("fp8_linear_reduce", {}).get("avg_ms", 0.0)
+        fgbs = fw["algo_bytes"] / (f_ms * 1e-3) / 1e9
+        _log(f"bench: fp8 linear {f_ms * 1e3:.2f} us ({fw['rows']} x {fw['out']} x {fw['in']}), {fgbs:.1f} GB/s ({fgbs / HBM_PEAK_GBS:.1%} of HBM peak)")
+        record["secondary_fp8_linear"] = {
+            "metric": "fp8 E4M3 block-scaled projection HBM GB/s",
+            "value": round(fgbs, 2),
+            "unit": "GB/s",
+            "ms_per_step": round(fms, 4),
+            "config": {"workload": "128 tokens (config 5's decode batch) x q_proj-shaped fp8 weight (8192 x 2048, 128x128 bf16 scales, packed once), fp32 in/out",
+                       "rows": fw["rows"], "out_features": fw["out"], "in_features": fw["in"]},
+            "roofline": {"bound": "hbm", "achieved": round(fgbs, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(fgbs / HBM_PEAK_GBS, 4),
+                         "traffic": TRAFFIC_FP8_LINEAR, "algo_bytes_per_launch": fw["algo_bytes"], "algo_flop_per_launch": fw["flops"],
+                         "kernel": "qa::f8l::fp8_linear_kernel<4, X_F16> (packed weight, K split 2) + qa::f8l::fp8_linear_reduce",
+                         "kernel_avg_us": round(f_ms * 1e3, 2), "kernels": fkern},
+        }
+        del fw
         torch.cuda.empty_cache()
     if not args.no_cpu_baseline:
         _log("bench: CPU baseline (reference path restatement)")

@@ -146,15 +146,25 @@ int qa_paged_kv_gather(const qa_paged_kv* kv, int32_t head_dim, int64_t batch,
  * codes, row-major; scale (out/128, in/128) bf16; x float32 or bfloat16 rows
  * (x_stride elements apart, 16-byte aligned); y float32 or bfloat16.  Both
  * feature counts must be multiples of 128.  Weight values are converted
- * exactly, scales applied per 128-deep block in fp32, fp32 x as a bf16
- * hi + lo pair.  workspace: qa_fp8_linear_workspace(rows, out, in) bytes
+ * exactly, scales applied per 128-deep block in fp32.  fp32 x of at most 16
+ * rows enters as a bf16 hi + lo pair (the reference's fp32 matvec regime),
+ * of more rows rounded to fp16 (its fp16 GEMM regime, .cu:1411-1460); bf16
+ * x as itself.  weight_packed = 1: weight is in qa_fp8_pack_weight's
+ * order (same bytes, streamed contiguously).  workspace: qa_fp8_linear_workspace(rows, out, in) bytes
  * (0 when no K split is used; then it may be NULL).  Replaces
  * fp8_e4m3_bf16_linear (src/fp8_cuda.py:16-17 -> src/csrc/fp8_linear.h,
  * src/csrc/fp8_linear_cuda.cu:1368-1466) and the dequantised F.linear of
  * src/reference_ops.py:436-506.                                            */
 int64_t qa_fp8_linear_workspace(int64_t rows, int64_t out_features, int64_t in_features);
+/* Weight re-laid once (at load time) for streaming: 16-row x 128-column
+ * tiles of 2 KB, consecutive along K, bytes in the order the products read
+ * them; pass weight_packed = 1 with the result.  No counterpart in the
+ * reference (its weights stay row-major).                                  */
+int qa_fp8_pack_weight(const void* weight, void* packed, int64_t out_features, int64_t in_features,
+                       hipStream_t stream);
 int qa_fp8_linear(const void* x, int32_t x_dtype, int64_t x_stride, int64_t rows,
-                  const void* weight, const void* scale, int64_t out_features, int64_t in_features,
+                  const void* weight, int32_t weight_packed, const void* scale,
+                  int64_t out_features, int64_t in_features,
                   void* y, int32_t y_dtype, int64_t y_stride, void* workspace, int64_t workspace_bytes,
                   hipStream_t stream);
 

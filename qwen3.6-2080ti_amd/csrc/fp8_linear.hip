@@ -5,21 +5,27 @@
 // dequantize_fp8_weight(w, scale_inv))) and its native op
 // (src/csrc/fp8_linear_cuda.cu:98-127, 1368-1466).
 //
-// The weight bytes are converted to bf16 exactly (every E4M3 value is a bf16
-// value) by v_cvt_pk_f32_fp8; the block scale multiplies each 128-deep partial
-// product in fp32, so the only roundings are those of x and of the fp32 sums.
-// An fp32 x enters as a bf16 hi + lo pair (x = hi + lo to 2^-17 relative), a
-// bf16 x as itself.  Products run on v_mfma_f32_16x16x32_bf16 with the weight
-// tile as the A operand, so a lane's accumulator holds four consecutive outputs
-// of one x row (16-byte stores).
+// The weight bytes are converted exactly (every E4M3 value is a bf16 and an
+// fp16 value) by v_cvt_pk_f32_fp8; the block scale multiplies each 128-deep
+// partial product in fp32, so the only roundings are those of x and of the fp32
+// sums.  x enters, like the reference's two regimes (fp32 matvec below 16 rows,
+// fp16 GEMM from 16 rows, src/csrc/fp8_linear_cuda.cu:1411-1460):
+//   * fp32 x, at most 16 rows: a bf16 hi + lo pair (x = hi + lo to 2^-17);
+//   * fp32 x, more rows: rounded to fp16, products on fp16 operands;
+//   * bf16 x: as itself (exact).
+// Products run on v_mfma_f32_16x16x32_{bf16,f16} with the weight tile as the A
+// operand, so a lane's accumulator holds four consecutive outputs of one x row
+// (16-byte stores).
 //
 // Work item: a workgroup of 4 waves owns one 128-row block of W (one scale row)
 // for 16 * MS rows of x and a range of 128-deep K blocks.  Per K block the x
 // tile goes to LDS (double-buffered, one barrier per block); each wave streams
-// its 32 weight rows straight from global memory into registers one block
+// its 32 weight rows straight from global memory into registers two blocks
 // ahead.  When the grid is small, K is split over workgroups that write fp32
 // partials, summed in a fixed order by a second kernel.
 #include "qa_common.h"
+
+#include <type_traits>
 
 namespace qa {
 namespace f8l {
@@ -28,9 +34,14 @@ constexpr int KB = 128;       // scale block, rows and columns
 constexpr int NT = 256;       // threads per workgroup
 constexpr int WROWS = 32;     // weight rows per wave (two 16-row MFMA tiles)
 constexpr int NTILE = 4 * WROWS;
-constexpr int LDX = KB + 8;   // bf16 row stride of the x tile in LDS
+constexpr int LDX = KB + 8;   // 16-bit row stride of the x tile in LDS
+constexpr int MAX_KB = 1024;  // K blocks per row (in_features <= 131072)
+
+// How x enters the products.
+enum Mode { X_BF16 = 0, X_SPLIT = 1, X_F16 = 2 };
 
 typedef __bf16 bf16x8_v __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x8_v __attribute__((ext_vector_type(8)));
 typedef float f32x4_v __attribute__((ext_vector_type(4)));
 typedef float f32x2_v __attribute__((ext_vector_type(2)));
 typedef unsigned int u32x4_v __attribute__((ext_vector_type(4)));
@@ -48,91 +59,124 @@ struct Params {
   int blocks_per_split;
   int ksplit;
   int y_f32;
+  int packed;  // weight in the tile order of qa_fp8_pack_weight
 };
 
-// Eight fp8 E4M3 codes (two dwords) as a bf16x8 operand, exactly.
-__device__ __forceinline__ bf16x8_v fp8x8_to_bf16(unsigned lo, unsigned hi) {
+// Eight fp8 E4M3 codes (two dwords) as an 8-element bf16 or fp16 operand, exactly.
+template <typename V>
+__device__ __forceinline__ V fp8x8_operand(unsigned lo, unsigned hi) {
+  typedef decltype(V{}[0]) elem_ref;
+  typedef typename std::remove_reference<elem_ref>::type E;
   const f32x2_v a = __builtin_amdgcn_cvt_pk_f32_fp8(lo, false);
   const f32x2_v b = __builtin_amdgcn_cvt_pk_f32_fp8(lo, true);
   const f32x2_v c = __builtin_amdgcn_cvt_pk_f32_fp8(hi, false);
   const f32x2_v d = __builtin_amdgcn_cvt_pk_f32_fp8(hi, true);
-  bf16x8_v r;
-  r[0] = static_cast<__bf16>(a[0]);
-  r[1] = static_cast<__bf16>(a[1]);
-  r[2] = static_cast<__bf16>(b[0]);
-  r[3] = static_cast<__bf16>(b[1]);
-  r[4] = static_cast<__bf16>(c[0]);
-  r[5] = static_cast<__bf16>(c[1]);
-  r[6] = static_cast<__bf16>(d[0]);
-  r[7] = static_cast<__bf16>(d[1]);
+  V r;
+  r[0] = static_cast<E>(a[0]);
+  r[1] = static_cast<E>(a[1]);
+  r[2] = static_cast<E>(b[0]);
+  r[3] = static_cast<E>(b[1]);
+  r[4] = static_cast<E>(c[0]);
+  r[5] = static_cast<E>(c[1]);
+  r[6] = static_cast<E>(d[0]);
+  r[7] = static_cast<E>(d[1]);
   return r;
 }
 
-// The x tile of one K block in registers: item i = (row, 32-column quarter) of
-// the 16 MS x 128 tile, items t, t + 256, ... per thread.
-template <int MS, bool XF32>
-struct XRegs {
-  static constexpr int ITEMS = (16 * MS * 4 + NT - 1) / NT;
-  u32x4_v v[ITEMS][XF32 ? 8 : 4];
+template <int MODE>
+struct ModeTraits;
+template <>
+struct ModeTraits<X_BF16> {
+  typedef bf16x8_v V;
+  static constexpr bool XF32 = false, LO = false;
+};
+template <>
+struct ModeTraits<X_SPLIT> {
+  typedef bf16x8_v V;
+  static constexpr bool XF32 = true, LO = true;
+};
+template <>
+struct ModeTraits<X_F16> {
+  typedef f16x8_v V;
+  static constexpr bool XF32 = true, LO = false;
 };
 
-template <int MS, bool XF32>
-__device__ __forceinline__ void load_x(const Params& p, int64_t m0, int64_t kb, int tid, XRegs<MS, XF32>& r) {
-#pragma unroll
-  for (int it = 0; it < XRegs<MS, XF32>::ITEMS; ++it) {
-    const int item = tid + it * NT;
-    const int row = item >> 2;
-    const int64_t m = m0 + row;
-    const bool live = row < 16 * MS && m < p.M;
-    const int64_t k = kb * KB + 32 * (item & 3);
-    constexpr int PIECES = XF32 ? 8 : 4;
-#pragma unroll
-    for (int q = 0; q < PIECES; ++q) {
-      if (live) {
-        const char* src = static_cast<const char*>(p.x) + (m * p.x_stride + k) * (XF32 ? 4 : 2) + 16 * q;
-        r.v[it][q] = *reinterpret_cast<const u32x4_v*>(src);
-      } else {
-        r.v[it][q] = u32x4_v{0u, 0u, 0u, 0u};
-      }
-    }
-  }
+__device__ __forceinline__ f32x4_v mfma(const bf16x8_v& a, const bf16x8_v& b, const f32x4_v& c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+}
+__device__ __forceinline__ f32x4_v mfma(const f16x8_v& a, const f16x8_v& b, const f32x4_v& c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
 }
 
-// bf16 hi (and for fp32 x the lo remainder) of the staged x tile into LDS.
+// The x tile of one K block (16 MS rows x 128 columns) spread evenly over the 256
+// threads: thread t holds 8 MS consecutive columns, from 8 MS (t % (16 / MS)), of row
+// t / (16 / MS), as raw fp32 or bf16 pieces of 16 bytes.
 template <int MS, bool XF32>
-__device__ __forceinline__ void store_x(const XRegs<MS, XF32>& r, __bf16* xh, __bf16* xl, int tid) {
+struct XRegs {
+  static constexpr int PIECES = XF32 ? 2 * MS : MS;
+  u32x4_v v[PIECES];
+};
+
+template <int MS>
+__device__ __forceinline__ int x_row(int tid) { return tid / (16 / MS); }
+template <int MS>
+__device__ __forceinline__ int x_col(int tid) { return 8 * MS * (tid % (16 / MS)); }
+
+// Loads are unconditional (rows clamped to valid ones, zeroed when stored) so that the
+// compiler's wait counts stay exact across the unrolled loop: a load under a branch makes
+// every later wait drain all loads in flight.
+template <int MS, bool XF32>
+__device__ __forceinline__ void load_x(const Params& p, int64_t m0, int64_t kb, int tid, XRegs<MS, XF32>& r) {
+  const int64_t m = min64(m0 + x_row<MS>(tid), p.M - 1);
+  const char* src = static_cast<const char*>(p.x) + (m * p.x_stride + kb * KB + x_col<MS>(tid)) * (XF32 ? 4 : 2);
 #pragma unroll
-  for (int it = 0; it < XRegs<MS, XF32>::ITEMS; ++it) {
-    const int item = tid + it * NT;
-    const int row = item >> 2;
-    if (row >= 16 * MS) continue;
-    const int off = row * LDX + 32 * (item & 3);
-    if constexpr (XF32) {
+  for (int q = 0; q < XRegs<MS, XF32>::PIECES; ++q) r.v[q] = *reinterpret_cast<const u32x4_v*>(src + 16 * q);
+}
+
+// The staged x tile into LDS as the products' operand type (for X_SPLIT also the
+// bf16 lo remainder, v - hi, exact in fp32); rows past M are stored as zeros.
+template <int MS, int MODE>
+__device__ __forceinline__ void store_x(const XRegs<MS, ModeTraits<MODE>::XF32>& r, unsigned short* xh, unsigned short* xl, int tid,
+                                        int64_t rows_left) {
+  typedef typename ModeTraits<MODE>::V V;
+  const int row = x_row<MS>(tid);
+  const bool live = row < rows_left;
+  const int off = row * LDX + x_col<MS>(tid);
+  if constexpr (ModeTraits<MODE>::XF32) {
 #pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        bf16x8_v h, l;
+    for (int g = 0; g < MS; ++g) {
+      V h;
+      bf16x8_v l;
 #pragma unroll
-        for (int e = 0; e < 8; ++e) {
-          const float v = __uint_as_float(r.v[it][2 * q + e / 4][e % 4]);
+      for (int e = 0; e < 8; ++e) {
+        const float v = live ? __uint_as_float(r.v[2 * g + e / 4][e % 4]) : 0.f;
+        if constexpr (MODE == X_F16) {
+          h[e] = static_cast<_Float16>(v);
+        } else {
           h[e] = static_cast<__bf16>(v);
           l[e] = static_cast<__bf16>(v - static_cast<float>(h[e]));
         }
-        *reinterpret_cast<bf16x8_v*>(xh + off + 8 * q) = h;
-        *reinterpret_cast<bf16x8_v*>(xl + off + 8 * q) = l;
       }
-    } else {
-#pragma unroll
-      for (int q = 0; q < 4; ++q) *reinterpret_cast<u32x4_v*>(xh + off + 8 * q) = r.v[it][q];
+      *reinterpret_cast<V*>(xh + off + 8 * g) = h;
+      if constexpr (ModeTraits<MODE>::LO) *reinterpret_cast<bf16x8_v*>(xl + off + 8 * g) = l;
     }
+  } else {
+#pragma unroll
+    for (int q = 0; q < MS; ++q) *reinterpret_cast<u32x4_v*>(xh + off + 8 * q) = live ? r.v[q] : u32x4_v{0u, 0u, 0u, 0u};
   }
 }
 
 // Workgroup (n tile, m tile, k split).  Lane l of a wave supplies, for k-step s of a
 // 128-deep block, the columns k = 32 (l / 16) + 8 s .. + 7 of row l % 16 of both operands
 // (the same k for A and B, so the products sum every k of the block once).
-template <int MS, bool XF32>
+template <int MS, int MODE>
 __global__ __launch_bounds__(NT) void fp8_linear_kernel(Params p) {
-  __shared__ __align__(16) __bf16 xs[2][XF32 ? 2 : 1][16 * MS * LDX];
+  typedef ModeTraits<MODE> T;
+  typedef typename T::V V;
+  __shared__ __align__(16) unsigned short xs[2][T::LO ? 2 : 1][16 * MS * LDX];
+  // the block scales of this workgroup's K range, read once: a per-block scalar load would
+  // be waited for by every barrier (s_waitcnt lgkmcnt covers scalar loads)
+  __shared__ float s_scale[MAX_KB];
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
@@ -143,8 +187,14 @@ __global__ __launch_bounds__(NT) void fp8_linear_kernel(Params p) {
   const int64_t kb0 = static_cast<int64_t>(blockIdx.z) * p.blocks_per_split;
   const int64_t kb1 = min64(kb0 + p.blocks_per_split, p.K / KB);
   const int64_t n_wave = ntile * NTILE + wave * WROWS;
-  const uint8_t* wrow0 = p.w + (n_wave + lr) * p.K + 32 * lg;
-  const uint8_t* wrow1 = wrow0 + 16 * p.K;
+  // Row-major weight: lane (lg, lr) reads 32 bytes of row n + lr per block.  Packed weight:
+  // the same 32 bytes sit at 16 lane + 1024 h of the 16-row tile's 2 KB chunk for the block,
+  // and a tile's chunks follow each other along K, so a wave streams contiguous memory.
+  const int64_t nkb = p.K / KB;
+  const int64_t skb = p.packed ? 2048 : KB;
+  const int64_t sh = p.packed ? 1024 : 16;
+  const uint8_t* wrow0 = p.packed ? p.w + (n_wave / 16) * nkb * 2048 + 16 * lane : p.w + (n_wave + lr) * p.K + 32 * lg;
+  const uint8_t* wrow1 = p.packed ? wrow0 + nkb * 2048 : wrow0 + 16 * p.K;
   const bf16_t* srow = p.scale + ntile * p.scale_cols;
 
   f32x4_v acc[MS][2];
@@ -153,32 +203,29 @@ __global__ __launch_bounds__(NT) void fp8_linear_kernel(Params p) {
 #pragma unroll
     for (int j = 0; j < 2; ++j) acc[i][j] = f32x4_v{0.f, 0.f, 0.f, 0.f};
 
-  XRegs<MS, XF32> xr;
-  u32x4_v wcur[2][2], wnext[2][2];
-  load_x<MS, XF32>(p, m0, kb0, tid, xr);
-  if (kb0 < kb1) {
+  // Three-deep rings of x and weight registers: block kb + 2 is loaded while block kb is
+  // computed (indices fixed at compile time by the three-way unrolled loop, so no copies).
+  XRegs<MS, T::XF32> xr[3];
+  u32x4_v wr[3][2][2];
+  auto load_w = [&](int64_t kb, u32x4_v (&w)[2][2]) {
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
-      wcur[0][h] = *reinterpret_cast<const u32x4_v*>(wrow0 + kb0 * KB + 16 * h);
-      wcur[1][h] = *reinterpret_cast<const u32x4_v*>(wrow1 + kb0 * KB + 16 * h);
+      w[0][h] = *reinterpret_cast<const u32x4_v*>(wrow0 + kb * skb + h * sh);
+      w[1][h] = *reinterpret_cast<const u32x4_v*>(wrow1 + kb * skb + h * sh);
     }
-  }
-  for (int64_t kb = kb0; kb < kb1; ++kb) {
+  };
+  // Block kb of the unrolled loop; kb may run up to two past the range (padding steps,
+  // whose loads re-read the last block and whose products are not accumulated).
+  auto step = [&](int64_t kb, XRegs<MS, T::XF32>& x, u32x4_v (&w)[2][2], XRegs<MS, T::XF32>& x_next2, u32x4_v (&w_next2)[2][2]) {
     const int buf = static_cast<int>(kb - kb0) & 1;
-    __bf16* xh = xs[buf][0];
-    __bf16* xl = xs[buf][XF32 ? 1 : 0];
-    store_x<MS, XF32>(xr, xh, xl, tid);
-    const float sc = bf16_to_f32(srow[kb]);
-    const bool more = kb + 1 < kb1;
-    if (more) {
-      load_x<MS, XF32>(p, m0, kb + 1, tid, xr);
-#pragma unroll
-      for (int h = 0; h < 2; ++h) {
-        wnext[0][h] = *reinterpret_cast<const u32x4_v*>(wrow0 + (kb + 1) * KB + 16 * h);
-        wnext[1][h] = *reinterpret_cast<const u32x4_v*>(wrow1 + (kb + 1) * KB + 16 * h);
-      }
-    }
+    unsigned short* xh = xs[buf][0];
+    unsigned short* xl = xs[buf][T::LO ? 1 : 0];
+    store_x<MS, MODE>(x, xh, xl, tid, p.M - m0);
+    const int64_t kn = min64(kb + 2, kb1 - 1);
+    load_x<MS, T::XF32>(p, m0, kn, tid, x_next2);
+    load_w(kn, w_next2);
     lds_barrier();
+    const float sc = kb < kb1 ? s_scale[kb - kb0] : 0.f;
     f32x4_v blk[MS][2];
 #pragma unroll
     for (int i = 0; i < MS; ++i)
@@ -186,32 +233,39 @@ __global__ __launch_bounds__(NT) void fp8_linear_kernel(Params p) {
       for (int j = 0; j < 2; ++j) blk[i][j] = f32x4_v{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int s = 0; s < 4; ++s) {
-      bf16x8_v a[2];
+      V a[2];
 #pragma unroll
-      for (int j = 0; j < 2; ++j) a[j] = fp8x8_to_bf16(wcur[j][s >> 1][2 * (s & 1)], wcur[j][s >> 1][2 * (s & 1) + 1]);
+      for (int j = 0; j < 2; ++j) a[j] = fp8x8_operand<V>(w[j][s >> 1][2 * (s & 1)], w[j][s >> 1][2 * (s & 1) + 1]);
 #pragma unroll
       for (int i = 0; i < MS; ++i) {
         const int off = (16 * i + lr) * LDX + 32 * lg + 8 * s;
-        const bf16x8_v bh = *reinterpret_cast<const bf16x8_v*>(xh + off);
+        const V bh = *reinterpret_cast<const V*>(xh + off);
 #pragma unroll
-        for (int j = 0; j < 2; ++j) blk[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[j], bh, blk[i][j], 0, 0, 0);
-        if constexpr (XF32) {
-          const bf16x8_v bl = *reinterpret_cast<const bf16x8_v*>(xl + off);
+        for (int j = 0; j < 2; ++j) blk[i][j] = mfma(a[j], bh, blk[i][j]);
+        if constexpr (T::LO) {
+          const V bl = *reinterpret_cast<const V*>(xl + off);
 #pragma unroll
-          for (int j = 0; j < 2; ++j) blk[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[j], bl, blk[i][j], 0, 0, 0);
+          for (int j = 0; j < 2; ++j) blk[i][j] = mfma(a[j], bl, blk[i][j]);
         }
       }
     }
+    if (kb < kb1) {  // a padding step's products (possibly NaN x 0) are dropped, not scaled by 0
 #pragma unroll
-    for (int i = 0; i < MS; ++i)
+      for (int i = 0; i < MS; ++i)
 #pragma unroll
-      for (int j = 0; j < 2; ++j) acc[i][j] += sc * blk[i][j];
-    if (more) {
-#pragma unroll
-      for (int j = 0; j < 2; ++j)
-#pragma unroll
-        for (int h = 0; h < 2; ++h) wcur[j][h] = wnext[j][h];
+        for (int j = 0; j < 2; ++j) acc[i][j] += sc * blk[i][j];
     }
+  };
+  load_x<MS, T::XF32>(p, m0, kb0, tid, xr[0]);
+  load_w(kb0, wr[0]);
+  load_x<MS, T::XF32>(p, m0, min64(kb0 + 1, kb1 - 1), tid, xr[1]);
+  load_w(min64(kb0 + 1, kb1 - 1), wr[1]);
+  // after the first blocks' loads, so its latency overlaps theirs
+  for (int64_t t = tid; t < kb1 - kb0; t += NT) s_scale[t] = bf16_to_f32(srow[kb0 + t]);
+  for (int64_t kb = kb0; kb < kb1; kb += 3) {
+    step(kb, xr[0], wr[0], xr[2], wr[2]);
+    step(kb + 1, xr[1], wr[1], xr[0], wr[0]);
+    step(kb + 2, xr[2], wr[2], xr[1], wr[1]);
   }
 
   // C = W X^T: lane (lg, lr) of tile (i, j) holds y[m0 + 16 i + lr][n_wave + 16 j + 4 lg + r]
@@ -255,6 +309,24 @@ __global__ __launch_bounds__(256) void fp8_linear_reduce(Params p) {
   }
 }
 
+// Packed weight: chunk (t, kb) of 2048 bytes for rows 16 t .. 16 t + 15 and K block kb, at
+// (t * K/128 + kb) * 2048; byte 1024 h + 16 l + e of the chunk is
+// w[16 t + l % 16][128 kb + 32 (l / 16) + 16 h + e].  One thread per 16-byte piece.
+__global__ __launch_bounds__(256) void fp8_pack_kernel(const uint8_t* __restrict__ src, uint8_t* __restrict__ dst, int64_t N, int64_t K) {
+  const int64_t piece = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+  if (piece >= N * K / 16) return;
+  const int64_t nkb = K / KB;
+  const int64_t chunk = piece >> 7;  // 128 pieces per chunk
+  const int within = static_cast<int>(piece & 127);
+  const int h = within >> 6;
+  const int l = within & 63;
+  const int64_t t = chunk / nkb;
+  const int64_t kb = chunk - t * nkb;
+  const int64_t row = 16 * t + (l & 15);
+  const int64_t col = KB * kb + 32 * (l >> 4) + 16 * h;
+  *reinterpret_cast<u32x4_v*>(dst + 16 * piece) = *reinterpret_cast<const u32x4_v*>(src + row * K + col);
+}
+
 struct Plan {
   int ms;
   int64_t mtiles, ntiles;
@@ -263,7 +335,8 @@ struct Plan {
 };
 
 // Rows per workgroup and the K split, from the shape alone (so the workspace query and
-// the launch agree): about 512 workgroups, at least two K blocks per split.
+// the launch agree): K is split only when there are fewer than 256 tiles, to about 256
+// workgroups with at least four K blocks each.
 inline Plan make_plan(int64_t M, int64_t N, int64_t K) {
   Plan pl{};
   pl.ms = M <= 16 ? 1 : M <= 32 ? 2 : 4;
@@ -271,8 +344,8 @@ inline Plan make_plan(int64_t M, int64_t N, int64_t K) {
   pl.ntiles = N / NTILE;
   const int64_t kblocks = K / KB;
   const int64_t tiles = pl.mtiles * pl.ntiles;
-  int64_t split = (512 + tiles - 1) / tiles;
-  split = split < kblocks / 2 ? split : kblocks / 2;
+  int64_t split = tiles >= 256 ? 1 : (256 + tiles - 1) / tiles;
+  split = split < kblocks / 4 ? split : kblocks / 4;
   if (split < 1) split = 1;
   pl.blocks_per_split = static_cast<int>((kblocks + split - 1) / split);
   pl.ksplit = static_cast<int>((kblocks + pl.blocks_per_split - 1) / pl.blocks_per_split);
@@ -281,12 +354,14 @@ inline Plan make_plan(int64_t M, int64_t N, int64_t K) {
 }
 
 template <int MS>
-void launch(const Plan& pl, const Params& p, bool xf32, hipStream_t stream) {
+void launch(const Plan& pl, const Params& p, int mode, hipStream_t stream) {
   const dim3 grid(static_cast<unsigned>(pl.ntiles), static_cast<unsigned>(pl.mtiles), static_cast<unsigned>(pl.ksplit));
-  if (xf32)
-    hipLaunchKernelGGL((fp8_linear_kernel<MS, true>), grid, dim3(NT), 0, stream, p);
+  if (mode == X_SPLIT)
+    hipLaunchKernelGGL((fp8_linear_kernel<MS, X_SPLIT>), grid, dim3(NT), 0, stream, p);
+  else if (mode == X_F16)
+    hipLaunchKernelGGL((fp8_linear_kernel<MS, X_F16>), grid, dim3(NT), 0, stream, p);
   else
-    hipLaunchKernelGGL((fp8_linear_kernel<MS, false>), grid, dim3(NT), 0, stream, p);
+    hipLaunchKernelGGL((fp8_linear_kernel<MS, X_BF16>), grid, dim3(NT), 0, stream, p);
 }
 
 }  // namespace f8l
@@ -297,9 +372,24 @@ extern "C" int64_t qa_fp8_linear_workspace(int64_t rows, int64_t out_features, i
   return qa::f8l::make_plan(rows, out_features, in_features).workspace;
 }
 
+extern "C" int qa_fp8_pack_weight(const void* weight, void* packed, int64_t out_features, int64_t in_features, hipStream_t stream) {
+  using namespace qa;
+  using namespace qa::f8l;
+  QA_REQUIRE(weight && packed && weight != packed, "fp8_pack_weight: distinct non-null pointers required");
+  QA_REQUIRE(out_features > 0 && in_features > 0 && out_features % 128 == 0 && in_features % 128 == 0,
+             "fp8_pack_weight: both dimensions must be positive multiples of 128");
+  QA_REQUIRE((reinterpret_cast<uintptr_t>(weight) & 15u) == 0 && (reinterpret_cast<uintptr_t>(packed) & 15u) == 0,
+             "fp8_pack_weight: pointers must be 16-byte aligned");
+  const int64_t pieces = out_features * in_features / 16;
+  QA_REQUIRE((pieces + 255) / 256 <= 0x7fffffff, "fp8_pack_weight: weight too large");
+  hipLaunchKernelGGL(fp8_pack_kernel, dim3(static_cast<unsigned>((pieces + 255) / 256)), dim3(256), 0, stream,
+                     static_cast<const uint8_t*>(weight), static_cast<uint8_t*>(packed), out_features, in_features);
+  return check_launch("fp8_pack_weight");
+}
+
 extern "C" int qa_fp8_linear(const void* x, int32_t x_dtype, int64_t x_stride, int64_t rows, const void* weight,
-                             const void* scale, int64_t out_features, int64_t in_features, void* y, int32_t y_dtype,
-                             int64_t y_stride, void* workspace, int64_t workspace_bytes, hipStream_t stream) {
+                             int32_t weight_packed, const void* scale, int64_t out_features, int64_t in_features, void* y,
+                             int32_t y_dtype, int64_t y_stride, void* workspace, int64_t workspace_bytes, hipStream_t stream) {
   using namespace qa;
   using namespace qa::f8l;
   QA_REQUIRE(x && weight && scale && y, "fp8_linear: pointers must be non-null");
@@ -309,6 +399,7 @@ extern "C" int qa_fp8_linear(const void* x, int32_t x_dtype, int64_t x_stride, i
   QA_REQUIRE(out_features % 128 == 0, "weight rows must be divisible by 128 for the FP8 op");
   QA_REQUIRE(in_features % 128 == 0, "weight cols must be divisible by 128 for the FP8 op");
   QA_REQUIRE(x_stride >= in_features && y_stride >= out_features, "row strides must cover a row");
+  QA_REQUIRE(in_features <= 128LL * MAX_KB, "fp8_linear: in_features above %d", 128 * MAX_KB);
   const int xsize = x_dtype == QA_F32 ? 4 : 2;
   QA_REQUIRE((reinterpret_cast<uintptr_t>(x) & 15u) == 0 && (x_stride * xsize) % 16 == 0, "input rows must be 16-byte aligned");
   QA_REQUIRE((reinterpret_cast<uintptr_t>(weight) & 15u) == 0, "weight must be 16-byte aligned");
@@ -334,15 +425,17 @@ extern "C" int qa_fp8_linear(const void* x, int32_t x_dtype, int64_t x_stride, i
   p.blocks_per_split = pl.blocks_per_split;
   p.ksplit = pl.ksplit;
   p.y_f32 = y_dtype == QA_F32;
-  const bool xf32 = x_dtype == QA_F32;
+  p.packed = weight_packed != 0;
+  // fp32 x: exact-ish hi + lo up to 16 rows, fp16 beyond (the reference's matvec / fp16 GEMM split)
+  const int mode = x_dtype == QA_BF16 ? X_BF16 : rows <= 16 ? X_SPLIT : X_F16;
   {
     KernelTimer timer_("fp8_linear", stream);
     if (pl.ms == 1)
-      launch<1>(pl, p, xf32, stream);
+      launch<1>(pl, p, mode, stream);
     else if (pl.ms == 2)
-      launch<2>(pl, p, xf32, stream);
+      launch<2>(pl, p, mode, stream);
     else
-      launch<4>(pl, p, xf32, stream);
+      launch<4>(pl, p, mode, stream);
   }
   if (int rc = check_launch("fp8_linear")) return rc;
   if (pl.ksplit > 1) {

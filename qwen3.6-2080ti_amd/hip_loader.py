@@ -80,10 +80,11 @@ SIGNATURES: dict[str, tuple[Any, list[Any]]] = {
          c_void_p, c_int32, c_int64, c_int64, c_int32, c_void_p, c_void_p],
     ),
     "qa_fp8_linear_workspace": (c_int64, [c_int64, c_int64, c_int64]),
+    "qa_fp8_pack_weight": (c_int32, [c_void_p, c_void_p, c_int64, c_int64, c_void_p]),
     "qa_fp8_linear": (
         c_int32,
-        [c_void_p, c_int32, c_int64, c_int64, c_void_p, c_void_p, c_int64, c_int64, c_void_p, c_int32, c_int64, c_void_p, c_int64,
-         c_void_p],
+        [c_void_p, c_int32, c_int64, c_int64, c_void_p, c_int32, c_void_p, c_int64, c_int64, c_void_p, c_int32, c_int64, c_void_p,
+         c_int64, c_void_p],
     ),
     "qa_paged_kv_reserve": (
         c_int32,

@@ -396,7 +396,31 @@ def paged_kv_reserve(
     L.check(lib, status_code, "paged_kv_reserve")
 
 
-def fp8_e4m3_bf16_linear(input: torch.Tensor, weight: torch.Tensor, scale: torch.Tensor, *, out_dtype: torch.dtype = torch.float32) -> torch.Tensor:
+class PackedFp8Weight:
+    """An fp8 E4M3 weight re-laid by ``fp8_pack_weight`` (same bytes, streaming order)."""
+
+    def __init__(self, data: torch.Tensor, out_features: int, in_features: int) -> None:
+        self.data = data
+        self.shape = (out_features, in_features)
+        self.device = data.device
+
+
+def fp8_pack_weight(weight: torch.Tensor) -> PackedFp8Weight:
+    """Re-lay an ``(N, K)`` fp8 weight once (at load time) into 16 x 128 tiles of 2 KB, consecutive
+    along K, in the order the linear kernel reads them: each wave then streams contiguous memory.
+    No counterpart in the reference, whose weights stay row-major."""
+    lib = L.load_library()
+    _require_cuda(weight, "weight")
+    _require(weight.dtype in (torch.float8_e4m3fn, torch.uint8) and weight.dim() == 2, "weight must be a rank-2 torch.float8_e4m3fn tensor")
+    rows, cols = weight.shape
+    _require(rows % 128 == 0 and cols % 128 == 0, "weight rows and cols must be divisible by 128 for the FP8 op")
+    src = weight.contiguous()
+    dst = torch.empty((rows * cols,), dtype=torch.uint8, device=weight.device)
+    L.check(lib, lib.qa_fp8_pack_weight(_ptr(src), _ptr(dst), rows, cols, _stream(weight.device)), "fp8_pack_weight")
+    return PackedFp8Weight(dst, rows, cols)
+
+
+def fp8_e4m3_bf16_linear(input: torch.Tensor, weight: torch.Tensor | PackedFp8Weight, scale: torch.Tensor, *, out_dtype: torch.dtype = torch.float32) -> torch.Tensor:
     """``y = input @ (E4M3(weight) * block scale)^T`` with 128 x 128 bf16 scale blocks.
 
     Same name, arguments and result as the reference's ``fp8_cuda.fp8_e4m3_bf16_linear``
@@ -404,16 +428,18 @@ def fp8_e4m3_bf16_linear(input: torch.Tensor, weight: torch.Tensor, scale: torch
     ``(N, K)`` ``torch.float8_e4m3fn`` (or its uint8 codes), ``scale`` ``(N/128, K/128)``
     bf16, ``input`` ``(..., K)`` float32 (bf16 also accepted); returns ``(..., N)`` float32
     (or ``out_dtype`` bf16).  N and K must be multiples of 128, as in the reference's op.
+    ``weight`` may also be the ``fp8_pack_weight`` form of the same weight (faster streaming).
     """
     lib = L.load_library()
     _require_cuda(input, "input")
     device = input.device
-    _require_cuda(weight, "weight", device)
+    _require_cuda(weight.data if isinstance(weight, PackedFp8Weight) else weight, "weight", device)
     _require_cuda(scale, "scale", device)
     _require(input.dtype in (torch.float32, torch.bfloat16), "input must be float32 or bfloat16")
-    _require(weight.dtype in (torch.float8_e4m3fn, torch.uint8), "weight must be torch.float8_e4m3fn")
+    packed = isinstance(weight, PackedFp8Weight)
+    _require(packed or weight.dtype in (torch.float8_e4m3fn, torch.uint8), "weight must be torch.float8_e4m3fn")
     _require(scale.dtype == torch.bfloat16, "scale must be bfloat16")
-    _require(weight.dim() == 2, "weight must be rank-2")
+    _require(packed or weight.dim() == 2, "weight must be rank-2")
     _require(scale.dim() == 2, "scale must be rank-2")
     _require(input.dim() >= 2, "input must be at least rank-2")
     _require(out_dtype in (torch.float32, torch.bfloat16), "out_dtype must be float32 or bfloat16")
@@ -423,13 +449,13 @@ def fp8_e4m3_bf16_linear(input: torch.Tensor, weight: torch.Tensor, scale: torch
     _require(cols % 128 == 0, "weight cols must be divisible by 128 for the FP8 op")
     _require(tuple(scale.shape) == (rows // 128, cols // 128), "scale blocks mismatch")
     x = input.contiguous().view(-1, cols)
-    w = weight.contiguous()
+    w = weight.data if packed else weight.contiguous()
     s = scale.contiguous()
     out = torch.empty((x.shape[0], rows), dtype=out_dtype, device=device)
     nbytes = int(lib.qa_fp8_linear_workspace(x.shape[0], rows, cols))
     ws = torch.empty(max(nbytes, 4), dtype=torch.uint8, device=device)
     status = lib.qa_fp8_linear(
-        _ptr(x), _code(x), x.stride(0), x.shape[0], _ptr(w), _ptr(s), rows, cols, _ptr(out), _code(out), out.stride(0), _ptr(ws),
+        _ptr(x), _code(x), x.stride(0), x.shape[0], _ptr(w), int(packed), _ptr(s), rows, cols, _ptr(out), _code(out), out.stride(0), _ptr(ws),
         ws.numel(), _stream(device),
     )
     L.check(lib, status, "fp8_e4m3_bf16_linear")
