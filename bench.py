@@ -43,7 +43,7 @@ TRAFFIC_DELTA = 1636029928
 TRAFFIC_PREFILL = 888455186  # average over the eight per-chunk launches
 TRAFFIC_PROLOGUE = 675541424
 TRAFFIC_OUTPUT_NORM = 805389585
-TRAFFIC_FP8_LINEAR = None  # set from the rocprofv3 --pmc runs of profiles/fp8_linear_config5_batch.md
+TRAFFIC_FP8_LINEAR = 46357504  # main kernel + split-K reduce, from profiles/fp8_linear_config5_batch.md
 SECONDARY_WARM_MS = 100.0  # wall time of untimed steps before each secondary (config 3, 4, 5) measurement
 MFMA_BF16_PEAK_TFLOPS = 2500.0  # MI355X dense bf16/fp16 MFMA, TFLOP/s
 

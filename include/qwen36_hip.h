@@ -72,7 +72,8 @@ const char* qa_arch(void);
  * by the benchmark for per-kernel roofline figures).  Enabling or disabling
  * clears the totals.  Labels: decode_partial_mfma, decode_partial_generic,
  * decode_combine, paged_prefill, chunk_gated_delta, gated_delta_step,
- * causal_conv1d.  qa_read_kernel_timing waits for the recorded events.      */
+ * causal_conv1d, fp8_linear, fp8_linear_reduce, kv_reserve (and others).
+ * qa_read_kernel_timing waits for the recorded events.                   */
 void qa_set_kernel_timing(int32_t enabled);
 int qa_read_kernel_timing(const char* label, double* total_ms, int64_t* launches);
 
