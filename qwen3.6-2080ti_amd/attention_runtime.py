@@ -372,3 +372,99 @@ def linear_attention_prefill(mixed_qkv: Any, a: Any, b: Any, a_log: Any, dt_bias
         mixed_qkv, a, b, a_log, dt_bias, conv_weight, key_heads=lin.key_heads, value_heads=lin.value_heads, conv_state=conv_state,
         initial_state=initial_state,
     )
+
+
+# --------------------------------------------------------------------------- fp8 projections
+
+
+@dataclass
+class LinearDispatchStats:
+    """Counters of ``reference_ops.LinearDispatchStats`` (``src/reference_ops.py:29-51``).
+
+    The ``moe_*`` fields are kept so code reading them still works; this build has no MoE path,
+    so they stay 0.
+    """
+
+    calls: int = 0
+    fp8_weight_calls: int = 0
+    eligible_cuda_calls: int = 0
+    cuda_kernel_hits: int = 0
+    fallback_calls: int = 0
+    fallback_disabled_cuda_kernel: int = 0
+    fallback_missing_scale: int = 0
+    fallback_hidden_not_cuda: int = 0
+    fallback_weight_not_cuda: int = 0
+    fallback_scale_not_cuda: int = 0
+    fallback_weight_dtype: int = 0
+    fallback_scale_dtype: int = 0
+    fallback_hidden_alignment: int = 0
+    fallback_weight_alignment: int = 0
+    moe_calls: int = 0
+    moe_packed_calls: int = 0
+    moe_loop_calls: int = 0
+    moe_single_token_dispatch_calls: int = 0
+    moe_single_token_dispatch_hits: int = 0
+    moe_single_token_local_assignments: int = 0
+    moe_assignments: int = 0
+    moe_local_assignments: int = 0
+
+    def to_dict(self) -> dict[str, int]:
+        return dict(vars(self))
+
+
+def linear_native(hidden_states: Any, weight: Any, scale_inv: Any | None = None, *, use_cuda_kernel: bool = True,
+                  stats: LinearDispatchStats | None = None) -> Any | None:
+    """The native branch of the reference's ``linear`` (``src/reference_ops.py:436-495``).
+
+    Same eligibility test and counters: an fp8 E4M3 weight (row-major, or packed by
+    ``hip_ops.fp8_pack_weight``) with a bf16 ``scale_inv``, all on the GPU, the hidden size and the
+    weight rows multiples of 128.  Eligible calls return ``hip_ops.fp8_e4m3_bf16_linear`` of
+    ``hidden_states.float()`` (fp32); others return ``None`` and the caller keeps its own
+    dequantise-and-``F.linear`` path, as the reference does (``:496-497``).
+    """
+    import torch
+
+    import hip_ops
+
+    packed = isinstance(weight, hip_ops.PackedFp8Weight)
+    weight_tensor = weight.data if packed else weight
+    has_scale = scale_inv is not None
+    hidden_is_cuda = bool(getattr(hidden_states, "is_cuda", False))
+    weight_is_cuda = bool(getattr(weight_tensor, "is_cuda", False))
+    scale_is_cuda = bool(has_scale and getattr(scale_inv, "is_cuda", False))
+    weight_is_fp8 = packed or weight.dtype == torch.float8_e4m3fn
+    scale_is_bf16 = bool(has_scale and scale_inv.dtype == torch.bfloat16)
+    hidden_aligned = hidden_states.shape[-1] % 128 == 0
+    weight_aligned = weight.shape[0] % 128 == 0
+    eligible = (use_cuda_kernel and has_scale and hidden_is_cuda and weight_is_cuda and scale_is_cuda and weight_is_fp8
+                and scale_is_bf16 and hidden_aligned and weight_aligned)
+    if stats is not None:
+        stats.calls += 1
+        if weight_is_fp8:
+            stats.fp8_weight_calls += 1
+        if eligible:
+            stats.eligible_cuda_calls += 1
+            stats.cuda_kernel_hits += 1
+        else:
+            stats.fallback_calls += 1
+            if not use_cuda_kernel:
+                stats.fallback_disabled_cuda_kernel += 1
+            if weight_is_fp8 and not has_scale:
+                stats.fallback_missing_scale += 1
+            if weight_is_fp8 and not hidden_is_cuda:
+                stats.fallback_hidden_not_cuda += 1
+            if weight_is_fp8 and not weight_is_cuda:
+                stats.fallback_weight_not_cuda += 1
+            if weight_is_fp8 and has_scale and not scale_is_cuda:
+                stats.fallback_scale_not_cuda += 1
+            if not weight_is_fp8:
+                stats.fallback_weight_dtype += 1
+            if weight_is_fp8 and has_scale and not scale_is_bf16:
+                stats.fallback_scale_dtype += 1
+            if weight_is_fp8 and not hidden_aligned:
+                stats.fallback_hidden_alignment += 1
+            if weight_is_fp8 and not weight_aligned:
+                stats.fallback_weight_alignment += 1
+    if not eligible:
+        return None
+    return hip_ops.fp8_e4m3_bf16_linear(hidden_states.float(), weight, scale_inv)

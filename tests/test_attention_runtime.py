@@ -141,3 +141,24 @@ def test_missing_native_library_is_raised_not_a_dense_fallback(monkeypatch) -> N
     monkeypatch.setattr(hip_ops, "paged_attention_decode", rejected)
     assert ar.full_attention_paged(torch.zeros(1, 2, 1, 4), None, cache, _enabled(), runtime) is None
     assert runtime.paged_attention_stats.fallback_no_kernel == 1
+
+
+def test_linear_native_ladder_counts_like_the_reference_on_cpu_tensors() -> None:
+    # src/reference_ops.py:444-494: CPU tensors and non-fp8 weights fall back with the same counters
+    import torch
+
+    from attention_runtime import LinearDispatchStats, linear_native
+
+    stats = LinearDispatchStats()
+    w8 = torch.zeros((256, 128)).to(torch.float8_e4m3fn)
+    scale = torch.ones((2, 1), dtype=torch.bfloat16)
+    x = torch.zeros((3, 128))
+    assert linear_native(x, w8, scale, stats=stats) is None
+    assert linear_native(x, torch.zeros((256, 128)), None, stats=stats) is None
+    assert linear_native(x, w8, None, use_cuda_kernel=False, stats=stats) is None
+    assert linear_native(torch.zeros((3, 100)), torch.zeros((200, 100)).to(torch.float8_e4m3fn), scale.float(), stats=stats) is None
+    d = stats.to_dict()
+    assert d["calls"] == 4 and d["fallback_calls"] == 4 and d["cuda_kernel_hits"] == 0 and d["fp8_weight_calls"] == 3
+    assert d["fallback_hidden_not_cuda"] == 3 and d["fallback_weight_not_cuda"] == 3 and d["fallback_scale_not_cuda"] == 2
+    assert d["fallback_weight_dtype"] == 1 and d["fallback_missing_scale"] == 1 and d["fallback_disabled_cuda_kernel"] == 1
+    assert d["fallback_scale_dtype"] == 1 and d["fallback_hidden_alignment"] == 1 and d["fallback_weight_alignment"] == 1

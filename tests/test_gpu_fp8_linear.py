@@ -142,3 +142,19 @@ def test_packed_weight_layout_and_identical_results(rows, n, k, xdt) -> None:
     a = ops.fp8_e4m3_bf16_linear(x, packed, s.to(DEV))
     b = ops.fp8_e4m3_bf16_linear(x, w.to(DEV), s.to(DEV))
     assert torch.equal(a, b)
+
+
+def test_runtime_linear_native_hits_the_kernel() -> None:
+    from attention_runtime import LinearDispatchStats, linear_native
+
+    ops = _ops()
+    gen = torch.Generator().manual_seed(17)
+    w, s = _weights(gen, 256, 384)
+    x = torch.randn((2, 5, 384), generator=gen).to(torch.bfloat16)
+    stats = LinearDispatchStats()
+    out = linear_native(x.to(DEV), w.to(DEV), s.to(DEV), stats=stats)
+    out_packed = linear_native(x.to(DEV), ops.fp8_pack_weight(w.to(DEV)), s.to(DEV), stats=stats)
+    assert stats.cuda_kernel_hits == 2 and stats.fallback_calls == 0
+    assert out.shape == (2, 5, 256) and out.dtype == torch.float32 and torch.equal(out, out_packed)
+    ref = oracle.linear(x.float().view(-1, 384), w.view(torch.uint8).numpy(), s).view(2, 5, 256)
+    torch.testing.assert_close(out.cpu(), ref, atol=2e-3, rtol=2e-3)
