@@ -96,9 +96,9 @@ struct ModeTraits<X_SPLIT> {
   static constexpr bool XF32 = true, LO = true;
 };
 template <>
-struct ModeTraits<X_F16> {
+struct ModeTraits<X_F16> {  // x cast to fp16 once by fp8_cast_x_kernel, then staged as 16-bit data
   typedef f16x8_v V;
-  static constexpr bool XF32 = true, LO = false;
+  static constexpr bool XF32 = false, LO = false;
 };
 
 __device__ __forceinline__ f32x4_v mfma(const bf16x8_v& a, const bf16x8_v& b, const f32x4_v& c) {
@@ -327,11 +327,35 @@ __global__ __launch_bounds__(256) void fp8_pack_kernel(const uint8_t* __restrict
   *reinterpret_cast<u32x4_v*>(dst + 16 * piece) = *reinterpret_cast<const u32x4_v*>(src + row * K + col);
 }
 
+// fp32 x (rows > 16) to fp16 once per call, round to nearest even (the reference's
+// float_rows_to_half_kernel, src/csrc/fp8_linear_cuda.cu:146-150): staging 16-bit x keeps the
+// main kernel's register ring small enough for its LDS operand reads to overlap.
+__global__ __launch_bounds__(256) void fp8_cast_x_kernel(const float* __restrict__ x, int64_t x_stride, _Float16* __restrict__ out,
+                                                          int64_t M, int64_t K) {
+  const int64_t g = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;  // group of 8 elements
+  if (g >= M * K / 8) return;
+  const int64_t m = (8 * g) / K;
+  const int64_t k = 8 * g - m * K;
+  const float4 a = *reinterpret_cast<const float4*>(x + m * x_stride + k);
+  const float4 b = *reinterpret_cast<const float4*>(x + m * x_stride + k + 4);
+  f16x8_v r;
+  r[0] = static_cast<_Float16>(a.x);
+  r[1] = static_cast<_Float16>(a.y);
+  r[2] = static_cast<_Float16>(a.z);
+  r[3] = static_cast<_Float16>(a.w);
+  r[4] = static_cast<_Float16>(b.x);
+  r[5] = static_cast<_Float16>(b.y);
+  r[6] = static_cast<_Float16>(b.z);
+  r[7] = static_cast<_Float16>(b.w);
+  *reinterpret_cast<f16x8_v*>(out + m * K + k) = r;
+}
+
 struct Plan {
   int ms;
   int64_t mtiles, ntiles;
   int ksplit, blocks_per_split;
-  int64_t workspace;
+  int64_t partial_bytes;  // fp32 partials of the K split
+  int64_t workspace;      // partials, then (rows > 16) the fp16 copy of an fp32 x
 };
 
 // Rows per workgroup and the K split, from the shape alone (so the workspace query and
@@ -349,7 +373,8 @@ inline Plan make_plan(int64_t M, int64_t N, int64_t K) {
   if (split < 1) split = 1;
   pl.blocks_per_split = static_cast<int>((kblocks + split - 1) / split);
   pl.ksplit = static_cast<int>((kblocks + pl.blocks_per_split - 1) / pl.blocks_per_split);
-  pl.workspace = pl.ksplit > 1 ? static_cast<int64_t>(pl.ksplit) * M * N * 4 : 0;
+  pl.partial_bytes = pl.ksplit > 1 ? (static_cast<int64_t>(pl.ksplit) * M * N * 4 + 255) / 256 * 256 : 0;
+  pl.workspace = pl.partial_bytes + (M > 16 ? M * K * 2 : 0);
   return pl;
 }
 
@@ -419,6 +444,21 @@ extern "C" int qa_fp8_linear(const void* x, int32_t x_dtype, int64_t x_stride, i
   p.y = y;
   p.y_stride = y_stride;
   p.partial = pl.ksplit > 1 ? static_cast<float*>(workspace) : nullptr;
+  // fp32 x: exact-ish hi + lo up to 16 rows, fp16 beyond (the reference's matvec / fp16 GEMM split)
+  const int mode = x_dtype == QA_BF16 ? X_BF16 : rows <= 16 ? X_SPLIT : X_F16;
+  if (mode == X_F16) {
+    _Float16* x16 = reinterpret_cast<_Float16*>(static_cast<char*>(workspace) + pl.partial_bytes);
+    const int64_t groups = rows * in_features / 8;
+    QA_REQUIRE((groups + 255) / 256 <= 0x7fffffff, "fp8_linear: input too large");
+    {
+      KernelTimer timer_("fp8_linear_cast", stream);
+      hipLaunchKernelGGL(fp8_cast_x_kernel, dim3(static_cast<unsigned>((groups + 255) / 256)), dim3(256), 0, stream,
+                         static_cast<const float*>(x), x_stride, x16, rows, in_features);
+    }
+    if (int rc = check_launch("fp8_linear cast")) return rc;
+    p.x = x16;
+    p.x_stride = in_features;
+  }
   p.M = rows;
   p.N = out_features;
   p.K = in_features;
@@ -426,8 +466,6 @@ extern "C" int qa_fp8_linear(const void* x, int32_t x_dtype, int64_t x_stride, i
   p.ksplit = pl.ksplit;
   p.y_f32 = y_dtype == QA_F32;
   p.packed = weight_packed != 0;
-  // fp32 x: exact-ish hi + lo up to 16 rows, fp16 beyond (the reference's matvec / fp16 GEMM split)
-  const int mode = x_dtype == QA_BF16 ? X_BF16 : rows <= 16 ? X_SPLIT : X_F16;
   {
     KernelTimer timer_("fp8_linear", stream);
     if (pl.ms == 1)
