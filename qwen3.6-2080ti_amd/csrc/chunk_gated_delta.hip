@@ -1,14 +1,14 @@
 // Chunked gated delta-rule prefill for gfx950 (dk = dv = 128, conv kernel 4,
 // chunk 64), from the raw in_proj outputs of a linear-attention layer.
 //
-// Three launches on the caller's stream:
+// Two launches on the caller's stream (steps 1 and 2 share one grid):
 //  1. prep_kernel -- causal conv1d + SiLU of every q/k/v channel and the L2
 //     norm of q and k per (token, head), q also scaled by dk^-0.5
 //     (src/reference_ops.py:181-183, 240-258, 297-304).  Each (row, head,
 //     token run) is done once, by one wave walking its tokens with the conv
 //     window in registers, and written token-major as fp16 to a workspace.
 //     It also writes the conv state.
-//  2. gate_kernel -- g = -exp(A_log) softplus(a + dt_bias), beta = sigmoid(b)
+//  2. gate_item -- g = -exp(A_log) softplus(a + dt_bias), beta = sigmoid(b)
 //     (src/reference_ops.py:271-275) and G, the inclusive sum of g inside each
 //     chunk.
 //  3. chunk_kernel -- the recurrence in the WY/UT form of Yang et al., "Gated
@@ -174,15 +174,23 @@ __device__ __forceinline__ void store4h(half_t* dst, float a, float b, float c, 
 // reduction.  Tokens are taken three at a time, so the three-token conv history
 // rotates through registers without copies.  VEC16 loads a token's 8 channels
 // as one 16-byte read (rows 16-byte aligned), otherwise as four 4-byte reads.
+__device__ __forceinline__ void gate_item(const GateParams& p, int64_t item, int lane);
+
 template <bool VEC16>
-__global__ __launch_bounds__(256) void prep_kernel(PrepParams p) {
+__global__ __launch_bounds__(256) void prep_kernel(PrepParams p, GateParams gp) {
   const int lane = threadIdx.x & 63;
   const int NH = 2 * p.Hk + p.Hv;
   const int ngroups = (NH + 3) / 4;
   const int64_t nruns = (p.tp + RUN - 1) / RUN;
   // the work item is wave-uniform, so its address arithmetic runs on the scalar unit
   const int64_t item = static_cast<int64_t>(blockIdx.x) * 4 + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  if (item >= static_cast<int64_t>(p.B) * ngroups * nruns) return;
+  const int64_t prep_items = static_cast<int64_t>(p.B) * ngroups * nruns;
+  if (item >= prep_items) {
+    // the gating waves follow the conv waves in the same grid (one launch fewer; they run in
+    // the conv waves' tail)
+    if (item - prep_items < static_cast<int64_t>(gp.B) * gp.Hv * gp.nch) gate_item(gp, item - prep_items, lane);
+    return;
+  }
   const int64_t run = item % nruns;
   const int grp = static_cast<int>((item / nruns) % ngroups);
   const int64_t b = item / nruns / ngroups;
@@ -301,10 +309,7 @@ __global__ __launch_bounds__(256) void prep_kernel(PrepParams p) {
 
 // ---------------------------------------------------------------------------
 // 2. gating: wave = (row b, value head, chunk), lane = token of the chunk.
-__global__ __launch_bounds__(256) void gate_kernel(GateParams p) {
-  const int lane = threadIdx.x & 63;
-  const int64_t item = static_cast<int64_t>(blockIdx.x) * 4 + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  if (item >= static_cast<int64_t>(p.B) * p.Hv * p.nch) return;
+__device__ __forceinline__ void gate_item(const GateParams& p, int64_t item, int lane) {
   const int64_t c = item % p.nch;
   const int hv = static_cast<int>((item / p.nch) % p.Hv);
   const int64_t b = item / p.nch / p.Hv;
@@ -908,18 +913,6 @@ extern "C" int qa_chunk_gated_delta_rule(const void* mixed_qkv, int32_t x_dtype,
   pp.Hv = value_heads;
   pp.C = C;
   const int64_t prep_waves = batch * ((2 * key_heads + value_heads + 3) / 4) * ((ws.tp + RUN - 1) / RUN);
-  QA_REQUIRE(prep_waves <= 4 * static_cast<int64_t>(0x7fffffff), "chunk_gated_delta_rule: too many prep waves");
-  const bool vec16 = x_stride_t % 8 == 0 && x_stride_b % 8 == 0 && (reinterpret_cast<uintptr_t>(mixed_qkv) & 15u) == 0;
-  {
-    KernelTimer timer_("chunk_prep", stream);
-    const dim3 grid(static_cast<unsigned>((prep_waves + 3) / 4));
-    if (vec16)
-      hipLaunchKernelGGL(prep_kernel<true>, grid, dim3(256), 0, stream, pp);
-    else
-      hipLaunchKernelGGL(prep_kernel<false>, grid, dim3(256), 0, stream, pp);
-  }
-  if (int rc = check_launch("chunk_gated_delta_rule prep")) return rc;
-
   GateParams gp{};
   gp.a = a;
   gp.bb = b;
@@ -935,11 +928,18 @@ extern "C" int qa_chunk_gated_delta_rule(const void* mixed_qkv, int32_t x_dtype,
   gp.B = static_cast<int>(batch);
   gp.Hv = value_heads;
   const int64_t gate_waves = batch * value_heads * ws.nch;
+  QA_REQUIRE(prep_waves + gate_waves <= 4 * static_cast<int64_t>(0x7fffffff), "chunk_gated_delta_rule: too many prep waves");
+  const bool vec16 = x_stride_t % 8 == 0 && x_stride_b % 8 == 0 && (reinterpret_cast<uintptr_t>(mixed_qkv) & 15u) == 0;
   {
-    KernelTimer timer_("chunk_gate", stream);
-    hipLaunchKernelGGL(gate_kernel, dim3(static_cast<unsigned>((gate_waves + 3) / 4)), dim3(256), 0, stream, gp);
+    // conv + SiLU + norms, with the gating (g, beta and the in-chunk cumulative G) as extra waves
+    KernelTimer timer_("chunk_prep", stream);
+    const dim3 grid(static_cast<unsigned>((prep_waves + gate_waves + 3) / 4));
+    if (vec16)
+      hipLaunchKernelGGL(prep_kernel<true>, grid, dim3(256), 0, stream, pp, gp);
+    else
+      hipLaunchKernelGGL(prep_kernel<false>, grid, dim3(256), 0, stream, pp, gp);
   }
-  if (int rc = check_launch("chunk_gated_delta_rule gate")) return rc;
+  if (int rc = check_launch("chunk_gated_delta_rule prep")) return rc;
 
   ChunkParams p{};
   p.qn = pp.qn;
