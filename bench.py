@@ -257,6 +257,78 @@ def cpu_baseline_decode(w, budget_s: float = 12.0):
     }
 
 
+def cpu_baseline_config1(device: str) -> dict:
+    """BASELINE config 1 in full on the host: batch 4, 16 q heads, 2 KV heads, D 256, 512 cached
+    tokens per row, block size 16, table = seeded permutation of 128 blocks (32 per row), bf16
+    N(0, 1) Q/K/V, seed 0 -- through the reference's CPU decode as the engine runs it (fp32,
+    repeated heads, ``index_select`` gather, dense softmax; ``oracle.attention.reference_layout_decode_cpu``).
+    Reports the algorithmic GB/s of the config-2 formula (bf16 K/V bytes)."""
+    import torch
+
+    from oracle import attention
+
+    batch, heads, kv_heads, dim, ctx, bs = 4, 16, 2, 256, 512, 16
+    gen = torch.Generator().manual_seed(0)
+    perm = torch.randperm(128, generator=gen)
+    tables = [perm[32 * b : 32 * (b + 1)].tolist() for b in range(batch)]
+    q = torch.randn((batch, heads, 1, dim), generator=gen).to(torch.bfloat16).float()
+    pools_k, pools_v = [], []
+    for b in range(batch):
+        # the reference's per-request pool (heads after _repeat_kv, P, bs, D) in fp32 (src/decode_state.py:37-44,
+        # src/tp_runtime.py:518-525)
+        k = torch.randn((kv_heads, 128, bs, dim), generator=gen).to(torch.bfloat16).float()
+        v = torch.randn((kv_heads, 128, bs, dim), generator=gen).to(torch.bfloat16).float()
+        pools_k.append(k.repeat_interleave(heads // kv_heads, dim=0).contiguous())
+        pools_v.append(v.repeat_interleave(heads // kv_heads, dim=0).contiguous())
+    attention.reference_layout_decode_cpu(q, pools_k, pools_v, tables, [ctx] * batch, block_size=bs)  # warm
+    reps = 0
+    t0 = time.perf_counter()
+    while True:
+        attention.reference_layout_decode_cpu(q, pools_k, pools_v, tables, [ctx] * batch, block_size=bs)
+        reps += 1
+        elapsed = time.perf_counter() - t0
+        if elapsed >= 2.0:
+            break
+    algo = batch * ctx * kv_heads * dim * 2 * 2 + 2 * batch * heads * dim * 2 + batch * (ctx // bs) * 4
+    return {"value": round(algo * reps / elapsed / 1e9, 4), "unit": "GB/s", "cores": torch.get_num_threads(), "kind": "port",
+            "ms_per_step": round(elapsed / reps * 1e3, 3),
+            "sample": f"config 1 in full (4 rows x 512 tokens, 128 shuffled blocks, seed 0), {reps} steps; reference fp32 repeated-head "
+                      f"layout, index_select gather + dense fp32 softmax; torch CPU threads={torch.get_num_threads()}"}
+
+
+def cpu_baseline_delta(dw: dict, budget_s: float = 30.0, piece: int = 256) -> dict:
+    """BASELINE config 4 on the host through the reference's CPU layer core
+    (``oracle.gated_delta.linear_attention_core``: fp32 conv1d + SiLU, gating, L2 norm, and the
+    per-token ``recurrent_gated_delta_rule`` loop of ``src/reference_ops.py:291-322``) on the same
+    seeded inputs as the GPU run, streamed ``piece`` tokens at a time with the conv tail and state
+    carried (identical results to one call); stops at ``budget_s`` and reports tokens/s over the
+    tokens done (all 4 x 8192 when the budget allows)."""
+    import torch
+
+    from oracle import gated_delta as gd
+
+    shape = gd.LinearShape(dw["key_heads"], dw["value_heads"], 128, 128, 4)
+    batch, seq = dw["batch"], dw["seq"]
+    a_log, dt_bias = dw["a_log"].cpu(), dw["dt_bias"].cpu()
+    conv_w = dw["conv_w"].cpu()
+    tail = state = None
+    done = 0
+    elapsed = 0.0
+    while done < seq and elapsed < budget_s:
+        n = min(piece, seq - done)
+        mixed = dw["mixed"][:, done : done + n].float().cpu()
+        a = dw["a"][:, done : done + n].float().cpu()
+        b = dw["b"][:, done : done + n].float().cpu()
+        t0 = time.perf_counter()
+        _core, state, tail = gd.linear_attention_core(mixed, a, b, a_log, dt_bias, conv_w, shape, conv_tail=tail, initial_state=state)
+        elapsed += time.perf_counter() - t0
+        done += n
+    return {"value": round(batch * done / elapsed, 1), "unit": "tokens/s", "cores": torch.get_num_threads(), "kind": "port",
+            "sample": f"config 4, {done} of {seq} tokens of all {batch} rows x {dw['value_heads']} value heads (same seeded inputs as the GPU "
+                      f"run), reference layer core with the per-token recurrence loop, fp32; torch CPU threads={torch.get_num_threads()}, "
+                      f"os.cpu_count()={os.cpu_count()}"}
+
+
 # ----------------------------------------------------------------------------- config 4
 
 
@@ -532,6 +604,7 @@ def main() -> int:
     parser.add_argument("--copy-probe-mib", type=int, default=0,
                         help="first run one plain device copy of this many MiB (reference point for HBM byte counters)")
     parser.add_argument("--cpu-budget", type=float, default=12.0)
+    parser.add_argument("--cpu-budget-delta", type=float, default=30.0)
     args = parser.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (got --gpus {args.gpus}); the hot path is not sharded in this build", file=sys.stderr)
@@ -620,10 +693,14 @@ def main() -> int:
         }
     del w
     torch.cuda.empty_cache()
+    cpu_delta = None
     if not args.no_delta:
         _log("bench: building config-4 workload (gated delta-rule chunked prefill)")
         dw = delta_workload(device)
         dms, dkern = time_delta(dw, max(20, args.steps), max(1, args.warmup))
+        if not args.no_cpu_baseline:
+            _log("bench: CPU baseline of config 4 (reference layer core, per-token loop)")
+            cpu_delta = cpu_baseline_delta(dw, args.cpu_budget_delta)
         tflops = dw["flops"] / (dkern["chunk_gated_delta"]["avg_ms"] * 1e-3) / 1e12
         tok_s = dw["batch"] * dw["seq"] / (dms * 1e-3)
         _log(f"bench: delta prefill {dms:.3f} ms, {tok_s:,.0f} tokens/s, {tflops:.1f} TFLOP/s ({tflops / MFMA_BF16_PEAK_TFLOPS:.1%} of MFMA peak)")
@@ -739,6 +816,9 @@ def main() -> int:
     if not args.no_cpu_baseline:
         _log("bench: CPU baseline (reference path restatement)")
         record["cpu_baseline"] = cpu_baseline_decode(wc, args.cpu_budget)
+        record["cpu_baseline"]["config1"] = cpu_baseline_config1(device)
+        if cpu_delta is not None:
+            record["cpu_baseline"]["delta"] = cpu_delta
     print(json.dumps(record), flush=True)
     return 0
 

@@ -147,9 +147,9 @@ int qa_paged_kv_gather(const qa_paged_kv* kv, int32_t head_dim, int64_t batch,
  * codes, row-major; scale (out/128, in/128) bf16; x float32 or bfloat16 rows
  * (x_stride elements apart, 16-byte aligned); y float32 or bfloat16.  Both
  * feature counts must be multiples of 128.  Weight values are converted
- * exactly, scales applied per 128-deep block in fp32.  fp32 x of at most 16
+ * exactly, scales applied per 128-deep block in fp32.  fp32 x of fewer than 16
  * rows enters as a bf16 hi + lo pair (the reference's fp32 matvec regime),
- * of more rows rounded to fp16 (its fp16 GEMM regime, .cu:1411-1460); bf16
+ * of 16 rows or more rounded to fp16 (its fp16 GEMM regime, .cu:1411-1460); bf16
  * x as itself.  weight_packed = 1: weight is in qa_fp8_pack_weight's
  * order (same bytes, streamed contiguously).  workspace: qa_fp8_linear_workspace(rows, out, in) bytes
  * (0 when no K split is used; then it may be NULL).  Replaces
@@ -241,22 +241,25 @@ int qa_qk_norm_rope_append(const void* q_proj, int64_t q_stride_t, int64_t q_str
 /* Depthwise causal conv1d over `seq` tokens (+ optional SiLU), fp32 math.
  * x: (batch, seq, channels) with element strides (x_stride_b, x_stride_t),
  * channels contiguous, float32 or bfloat16.  initial_state/final_state:
- * (rows, channels, kernel-1) fp32 (row = slots[b] when slots != NULL, else
- * b); a NULL initial_state means zeros.  weight: (channels, kernel) fp32.
+ * (state_rows, channels, kernel-1) fp32 (row = slots[b] when slots != NULL,
+ * else b); a NULL initial_state means zeros.  A row whose state row lies
+ * outside [0, state_rows) (e.g. a -1 pad) touches no state and outputs zeros.
+ * weight: (channels, kernel) fp32.
  * out: (batch, seq, channels) float32 or bfloat16.  Replaces the conv of
  * linear_attention (src/reference_ops.py:240-258, src/tp_runtime.py:2635-2659). */
 int qa_causal_conv1d_prefill(const void* x, int32_t x_dtype, int64_t x_stride_b, int64_t x_stride_t,
                              const float* initial_state, float* final_state, int64_t state_stride_b,
-                             const void* slots, int32_t slots_dtype,
+                             const void* slots, int32_t slots_dtype, int64_t state_rows,
                              const float* weight, int64_t batch, int64_t seq, int32_t channels, int32_t kernel,
                              void* out, int32_t out_dtype, int64_t out_stride_b, int64_t out_stride_t,
                              int32_t apply_silu, hipStream_t stream);
 
-/* Single-token conv update with the (rows, channels, kernel-1) conv state
- * updated in place (the cache's conv_tail, src/reference_ops.py:253-257).   */
+/* Single-token conv update with the (state_rows, channels, kernel-1) conv
+ * state updated in place (the cache's conv_tail, src/reference_ops.py:253-257);
+ * rows whose slot is outside [0, state_rows) output zeros.                  */
 int qa_causal_conv1d_update(const void* x, int32_t x_dtype, int64_t x_stride_b,
                             float* conv_state, int64_t state_stride_b, const void* slots, int32_t slots_dtype,
-                            const float* weight, int64_t batch, int32_t channels, int32_t kernel,
+                            int64_t state_rows, const float* weight, int64_t batch, int32_t channels, int32_t kernel,
                             void* out, int32_t out_dtype, int64_t out_stride_b, int32_t apply_silu,
                             hipStream_t stream);
 
@@ -277,15 +280,17 @@ int qa_linear_attention_recurrent_core(const float* query, const float* key, con
  * projection outputs; a_log, dt_bias (Hv) fp32.  Computes
  * beta = sigmoid(b), g = -exp(a_log) softplus(a + dt_bias), L2-normalised
  * q*dk^-0.5 and k (value head j reads key head j / (Hv/Hqk)), one recurrence
- * step on state[slot(b)] (slots, Hv, dk, dv) fp32 in place, and writes
- * out (B, Hv, dv).  dk = dv = 128.  Replaces the per-request state stacking
+ * step on state[slot(b)] (state_rows, Hv, dk, dv) fp32 in place, and writes
+ * out (B, Hv, dv).  A row whose slot lies outside [0, state_rows) (a -1 pad, a
+ * stale id) reads and writes no state and gets zero outputs.
+ * dk = dv = 128.  Replaces the per-request state stacking
  * and recurrence of src/tp_runtime.py:2613-2717 with a slot-indexed pool
  * (src/reference_ops.py:271-283, :291-322).                               */
 int qa_gated_delta_step(const float* qkv, int64_t qkv_stride_b,
                         const void* a, const void* b, int32_t ab_dtype, int64_t ab_stride_b,
                         const float* a_log, const float* dt_bias,
                         float* state, int64_t state_stride_slot, const void* slots, int32_t slots_dtype,
-                        void* out, int32_t out_dtype, int64_t out_stride_b,
+                        int64_t state_rows, void* out, int32_t out_dtype, int64_t out_stride_b,
                         int64_t batch, int32_t key_heads, int32_t value_heads,
                         int32_t key_dim, int32_t value_dim, hipStream_t stream);
 
@@ -302,7 +307,7 @@ int qa_gated_delta_step_norm(const float* qkv, int64_t qkv_stride_b,
                              const void* a, const void* b, int32_t ab_dtype, int64_t ab_stride_b,
                              const float* a_log, const float* dt_bias,
                              float* state, int64_t state_stride_slot, const void* slots, int32_t slots_dtype,
-                             const void* z, int32_t z_dtype, int64_t z_stride_b,
+                             int64_t state_rows, const void* z, int32_t z_dtype, int64_t z_stride_b,
                              const void* norm_weight, int32_t norm_dtype, float eps,
                              void* out, int32_t out_dtype, int64_t out_stride_b,
                              int64_t batch, int32_t key_heads, int32_t value_heads,

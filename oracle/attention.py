@@ -24,6 +24,12 @@ wrong index or a transposed operand would break: output invariance under
 physical-block permutation, GQA == MHA on explicitly repeated KV, causality
 (changing a future token leaves earlier rows unchanged), decode of the last
 position == last row of prefill, and uniform attention for a zero query.
+:func:`paged_prefill` is checked against the same fp64 loop with query
+positions ``prefix + n`` over a shuffled pool whose unwritten slots hold
+garbage (ragged prefixes including 0, lengths that are not block multiples,
+GQA 16/2, a gate); :func:`reference_layout_decode_cpu` (and the ``"hpbd"``
+branch of :func:`gather_dense`) against the fp64 loop and against
+:func:`paged_decode` on a shared GQA pool holding the same tokens.
 """
 
 from __future__ import annotations

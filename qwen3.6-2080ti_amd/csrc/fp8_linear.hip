@@ -327,7 +327,7 @@ __global__ __launch_bounds__(256) void fp8_pack_kernel(const uint8_t* __restrict
   *reinterpret_cast<u32x4_v*>(dst + 16 * piece) = *reinterpret_cast<const u32x4_v*>(src + row * K + col);
 }
 
-// fp32 x (rows > 16) to fp16 once per call, round to nearest even (the reference's
+// fp32 x (16 rows or more) to fp16 once per call, round to nearest even (the reference's
 // float_rows_to_half_kernel, src/csrc/fp8_linear_cuda.cu:146-150): staging 16-bit x keeps the
 // main kernel's register ring small enough for its LDS operand reads to overlap.
 __global__ __launch_bounds__(256) void fp8_cast_x_kernel(const float* __restrict__ x, int64_t x_stride, _Float16* __restrict__ out,
@@ -355,7 +355,7 @@ struct Plan {
   int64_t mtiles, ntiles;
   int ksplit, blocks_per_split;
   int64_t partial_bytes;  // fp32 partials of the K split
-  int64_t workspace;      // partials, then (rows > 16) the fp16 copy of an fp32 x
+  int64_t workspace;      // partials, then (rows >= 16) the fp16 copy of an fp32 x
 };
 
 // Rows per workgroup and the K split, from the shape alone (so the workspace query and
@@ -374,7 +374,7 @@ inline Plan make_plan(int64_t M, int64_t N, int64_t K) {
   pl.blocks_per_split = static_cast<int>((kblocks + split - 1) / split);
   pl.ksplit = static_cast<int>((kblocks + pl.blocks_per_split - 1) / pl.blocks_per_split);
   pl.partial_bytes = pl.ksplit > 1 ? (static_cast<int64_t>(pl.ksplit) * M * N * 4 + 255) / 256 * 256 : 0;
-  pl.workspace = pl.partial_bytes + (M > 16 ? M * K * 2 : 0);
+  pl.workspace = pl.partial_bytes + (M >= 16 ? M * K * 2 : 0);
   return pl;
 }
 
@@ -444,8 +444,9 @@ extern "C" int qa_fp8_linear(const void* x, int32_t x_dtype, int64_t x_stride, i
   p.y = y;
   p.y_stride = y_stride;
   p.partial = pl.ksplit > 1 ? static_cast<float*>(workspace) : nullptr;
-  // fp32 x: exact-ish hi + lo up to 16 rows, fp16 beyond (the reference's matvec / fp16 GEMM split)
-  const int mode = x_dtype == QA_BF16 ? X_BF16 : rows <= 16 ? X_SPLIT : X_F16;
+  // fp32 x: exact-ish hi + lo below 16 rows, fp16 from 16 rows on (the reference's fp32 matvec for
+  // batch < kDefaultCublasBatchThreshold = 16, its fp16 GEMM otherwise, src/csrc/fp8_linear_cuda.cu:1411-1460)
+  const int mode = x_dtype == QA_BF16 ? X_BF16 : rows < 16 ? X_SPLIT : X_F16;
   if (mode == X_F16) {
     _Float16* x16 = reinterpret_cast<_Float16*>(static_cast<char*>(workspace) + pl.partial_bytes);
     const int64_t groups = rows * in_features / 8;

@@ -39,6 +39,10 @@ __device__ __forceinline__ int64_t slot_of(const void* slots, int is64, int64_t 
   return is64 ? reinterpret_cast<const int64_t*>(slots)[b] : reinterpret_cast<const int32_t*>(slots)[b];
 }
 
+// A row whose state slot lies outside [0, rows) (a -1 pad, a stale or foreign id) reads and
+// writes no state and produces zeros, as the paged-KV kernels do for invalid block ids.
+__device__ __forceinline__ bool slot_valid(int64_t slot, int64_t rows) { return slot >= 0 && slot < rows; }
+
 // ---------------------------------------------------------------------------
 // causal depthwise conv1d (src/reference_ops.py:245-258)
 
@@ -49,6 +53,7 @@ struct ConvParams {
   const float* state_in;  // (rows, C, K-1) or null (zeros)
   float* state_out;       // (rows, C, K-1) or null
   int64_t state_sb;
+  int64_t state_rows;     // rows of the state buffers (checked when either is given)
   const void* slots;
   int slots_i64;
   const float* weight;  // (C, K)
@@ -68,6 +73,10 @@ __global__ __launch_bounds__(256) void conv1d_kernel(ConvParams p) {
   const int64_t b = blockIdx.y;
   if (c >= p.C) return;
   const int64_t row = slot_of(p.slots, p.slots_i64, b);
+  if ((p.state_in != nullptr || p.state_out != nullptr) && !slot_valid(row, p.state_rows)) {
+    for (int64_t t = 0; t < p.seq; ++t) store_any(p.out, p.out_dtype, b * p.out_sb + t * p.out_st + c, 0.f);
+    return;
+  }
   float win[kConvMaxK];
   float w[kConvMaxK];
 #pragma unroll
@@ -121,6 +130,7 @@ struct DeltaParams {
   const float* state_in;
   float* state_out;
   int64_t state_sb;  // per batch row / slot (elements)
+  int64_t state_rows;  // slots of the state pool (fused step)
   const void* slots;
   int slots_i64;
   // output
@@ -191,6 +201,14 @@ __global__ __launch_bounds__(256) void delta_recurrent_128(DeltaParams p) {
   float* s_out;
   if (FUSED) {
     const int64_t slot = slot_of(p.slots, p.slots_i64, b);
+    if (!slot_valid(slot, p.state_rows)) {
+      // the whole workgroup takes this branch (one row per workgroup); its 128 outputs are zeros
+      if (w == 0 && rg == 0) {
+#pragma unroll
+        for (int c = 0; c < 8; ++c) store_any(p.out, p.out_dtype, b * p.out_sb + static_cast<int64_t>(h) * DV + col0 + c, 0.f);
+      }
+      return;
+    }
     s_in = p.state_in + slot * p.state_sb + static_cast<int64_t>(h) * DK * DV;
     s_out = p.state_out + slot * p.state_sb + static_cast<int64_t>(h) * DK * DV;
   } else {
@@ -359,7 +377,7 @@ static bool aligned16(const void* ptr) { return (reinterpret_cast<uintptr_t>(ptr
 
 extern "C" int qa_causal_conv1d_prefill(const void* x, int32_t x_dtype, int64_t x_stride_b, int64_t x_stride_t,
                                         const float* initial_state, float* final_state, int64_t state_stride_b,
-                                        const void* slots, int32_t slots_dtype, const float* weight, int64_t batch,
+                                        const void* slots, int32_t slots_dtype, int64_t state_rows, const float* weight, int64_t batch,
                                         int64_t seq, int32_t channels, int32_t kernel, void* out, int32_t out_dtype,
                                         int64_t out_stride_b, int64_t out_stride_t, int32_t apply_silu, hipStream_t stream) {
   using namespace qa;
@@ -370,6 +388,7 @@ extern "C" int qa_causal_conv1d_prefill(const void* x, int32_t x_dtype, int64_t 
   QA_REQUIRE(channels > 0 && batch > 0 && batch <= 65535, "conv1d: bad batch/channels");
   QA_REQUIRE(seq >= 0, "conv1d: seq must be non-negative");
   QA_REQUIRE(slots == nullptr || is_index_dtype(slots_dtype), "conv1d: slots must be int32/int64");
+  QA_REQUIRE((initial_state == nullptr && final_state == nullptr) || state_rows > 0, "conv1d: state_rows must be positive");
   ConvParams p{};
   p.x = x;
   p.x_dtype = x_dtype;
@@ -378,6 +397,7 @@ extern "C" int qa_causal_conv1d_prefill(const void* x, int32_t x_dtype, int64_t 
   p.state_in = initial_state;
   p.state_out = final_state;
   p.state_sb = state_stride_b;
+  p.state_rows = state_rows;
   p.slots = slots;
   p.slots_i64 = slots_dtype == QA_I64;
   p.weight = weight;
@@ -399,12 +419,13 @@ extern "C" int qa_causal_conv1d_prefill(const void* x, int32_t x_dtype, int64_t 
 }
 
 extern "C" int qa_causal_conv1d_update(const void* x, int32_t x_dtype, int64_t x_stride_b, float* conv_state,
-                                       int64_t state_stride_b, const void* slots, int32_t slots_dtype, const float* weight,
+                                       int64_t state_stride_b, const void* slots, int32_t slots_dtype, int64_t state_rows,
+                                       const float* weight,
                                        int64_t batch, int32_t channels, int32_t kernel, void* out, int32_t out_dtype,
                                        int64_t out_stride_b, int32_t apply_silu, hipStream_t stream) {
   QA_REQUIRE(conv_state != nullptr, "conv1d update: conv_state must be non-null");
   return qa_causal_conv1d_prefill(x, x_dtype, x_stride_b, 0, conv_state, conv_state, state_stride_b, slots, slots_dtype,
-                                  weight, batch, 1, channels, kernel, out, out_dtype, out_stride_b, 0, apply_silu, stream);
+                                  state_rows, weight, batch, 1, channels, kernel, out, out_dtype, out_stride_b, 0, apply_silu, stream);
 }
 
 extern "C" int qa_linear_attention_recurrent_core(const float* query, const float* key, const float* value, const float* g,
@@ -445,7 +466,8 @@ extern "C" int qa_linear_attention_recurrent_core(const float* query, const floa
 
 static int gated_delta_step_impl(const float* qkv, int64_t qkv_stride_b, const void* a, const void* b, int32_t ab_dtype,
                                  int64_t ab_stride_b, const float* a_log, const float* dt_bias, float* state,
-                                 int64_t state_stride_slot, const void* slots, int32_t slots_dtype, const void* z, int32_t z_dtype,
+                                 int64_t state_stride_slot, const void* slots, int32_t slots_dtype, int64_t state_rows,
+                                 const void* z, int32_t z_dtype,
                                  int64_t z_stride_b, const void* norm_weight, int32_t norm_dtype, float eps, void* out,
                                  int32_t out_dtype, int64_t out_stride_b, int64_t batch, int32_t key_heads,
                                  int32_t value_heads, int32_t key_dim, int32_t value_dim, hipStream_t stream) {
@@ -457,6 +479,7 @@ static int gated_delta_step_impl(const float* qkv, int64_t qkv_stride_b, const v
   QA_REQUIRE(out_dtype == QA_F32 || out_dtype == QA_BF16, "gated_delta_step: out must be float32 or bfloat16");
   QA_REQUIRE(slots == nullptr || is_index_dtype(slots_dtype), "gated_delta_step: slots must be int32/int64");
   QA_REQUIRE(batch > 0 && batch * value_heads <= 0x7fffffff, "gated_delta_step: bad batch");
+  QA_REQUIRE(state_rows > 0, "gated_delta_step: state_rows must be positive");
   QA_REQUIRE(aligned16(state) && state_stride_slot % 4 == 0 && qkv_stride_b >= 2 * key_heads * key_dim + value_heads * value_dim,
              "gated_delta_step: state must be 16-byte aligned and qkv rows complete");
   const bool norm = z != nullptr;
@@ -475,6 +498,7 @@ static int gated_delta_step_impl(const float* qkv, int64_t qkv_stride_b, const v
   p.state_in = state;
   p.state_out = state;
   p.state_sb = state_stride_slot;
+  p.state_rows = state_rows;
   p.slots = slots;
   p.slots_i64 = slots_dtype == QA_I64;
   p.out = out;
@@ -504,22 +528,23 @@ static int gated_delta_step_impl(const float* qkv, int64_t qkv_stride_b, const v
 
 extern "C" int qa_gated_delta_step(const float* qkv, int64_t qkv_stride_b, const void* a, const void* b, int32_t ab_dtype,
                                    int64_t ab_stride_b, const float* a_log, const float* dt_bias, float* state,
-                                   int64_t state_stride_slot, const void* slots, int32_t slots_dtype, void* out,
-                                   int32_t out_dtype, int64_t out_stride_b, int64_t batch, int32_t key_heads,
+                                   int64_t state_stride_slot, const void* slots, int32_t slots_dtype, int64_t state_rows,
+                                   void* out, int32_t out_dtype, int64_t out_stride_b, int64_t batch, int32_t key_heads,
                                    int32_t value_heads, int32_t key_dim, int32_t value_dim, hipStream_t stream) {
   return gated_delta_step_impl(qkv, qkv_stride_b, a, b, ab_dtype, ab_stride_b, a_log, dt_bias, state, state_stride_slot, slots,
-                               slots_dtype, nullptr, QA_F32, 0, nullptr, QA_F32, 0.f, out, out_dtype, out_stride_b, batch,
+                               slots_dtype, state_rows, nullptr, QA_F32, 0, nullptr, QA_F32, 0.f, out, out_dtype, out_stride_b, batch,
                                key_heads, value_heads, key_dim, value_dim, stream);
 }
 
 extern "C" int qa_gated_delta_step_norm(const float* qkv, int64_t qkv_stride_b, const void* a, const void* b, int32_t ab_dtype,
                                         int64_t ab_stride_b, const float* a_log, const float* dt_bias, float* state,
-                                        int64_t state_stride_slot, const void* slots, int32_t slots_dtype, const void* z,
-                                        int32_t z_dtype, int64_t z_stride_b, const void* norm_weight, int32_t norm_dtype, float eps,
+                                        int64_t state_stride_slot, const void* slots, int32_t slots_dtype, int64_t state_rows,
+                                        const void* z, int32_t z_dtype, int64_t z_stride_b, const void* norm_weight, int32_t norm_dtype,
+                                        float eps,
                                         void* out, int32_t out_dtype, int64_t out_stride_b, int64_t batch, int32_t key_heads,
                                         int32_t value_heads, int32_t key_dim, int32_t value_dim, hipStream_t stream) {
   if (z == nullptr) return qa::fail("gated_delta_step_norm: z must be non-null");
   return gated_delta_step_impl(qkv, qkv_stride_b, a, b, ab_dtype, ab_stride_b, a_log, dt_bias, state, state_stride_slot, slots,
-                               slots_dtype, z, z_dtype, z_stride_b, norm_weight, norm_dtype, eps, out, out_dtype, out_stride_b, batch,
+                               slots_dtype, state_rows, z, z_dtype, z_stride_b, norm_weight, norm_dtype, eps, out, out_dtype, out_stride_b, batch,
                                key_heads, value_heads, key_dim, value_dim, stream);
 }

@@ -827,12 +827,16 @@ static int run_decode(const DecodeHostArgs& a, hipStream_t stream) {
   p.split_tokens = choose_split_tokens(a.max_tokens, a.block_size);
   p.n_splits = static_cast<int>(std::max<int64_t>(1, ceil_div(std::max<int64_t>(a.max_tokens, 1), p.split_tokens)));
   QA_REQUIRE(p.n_splits <= kCombineMaxSplits, "paged decode: %lld tokens need more than %d splits", static_cast<long long>(a.max_tokens), kCombineMaxSplits);
-  const int64_t need = decode_workspace_bytes(a.batch, a.heads, a.head_dim, a.max_tokens, a.block_size);
-  QA_REQUIRE(a.workspace != nullptr && a.workspace_bytes >= need, "paged decode workspace too small: need %lld bytes", static_cast<long long>(need));
   p.n_waves = static_cast<int>(balanced_waves(static_cast<int64_t>(p.B) * p.Hkv, a.max_tokens));
+  const bool mfma = a.q_dtype == QA_BF16 && kv.dtype == QA_BF16 && mfma_eligible(p, a, kv);
+  // bytes of the path taken (qa_paged_attention_decode_workspace returns the larger of the two)
+  const int64_t slots = static_cast<int64_t>(p.n_waves) + static_cast<int64_t>(p.B) * p.Hkv;
+  const int64_t need = mfma ? (slots * p.G * (p.D + 2) + 2 * static_cast<int64_t>(p.B) * p.Hkv) * 4
+                            : static_cast<int64_t>(p.B) * p.H * p.n_splits * (p.D + 2) * 4;
+  QA_REQUIRE(a.workspace != nullptr && a.workspace_bytes >= need, "paged decode workspace too small: need %lld bytes, have %lld",
+             static_cast<long long>(need), static_cast<long long>(a.workspace_bytes));
   p.part_o = reinterpret_cast<float*>(a.workspace);
-  if (a.q_dtype == QA_BF16 && kv.dtype == QA_BF16 && mfma_eligible(p, a, kv)) {
-    const int64_t slots = static_cast<int64_t>(p.n_waves) + static_cast<int64_t>(p.B) * p.Hkv;
+  if (mfma) {
     p.part_ml = p.part_o + slots * p.G * p.D;
     p.rg_waves = reinterpret_cast<int32_t*>(p.part_ml + slots * p.G * 2);
     return launch_mfma(p, stream);

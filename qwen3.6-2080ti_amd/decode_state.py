@@ -135,6 +135,7 @@ class SharedKVBlockPool:
         self.key_blocks = torch.zeros((num_blocks, kv_heads, block_size, head_dim), dtype=dtype, device=device)
         self.value_blocks = torch.zeros_like(self.key_blocks)
         self.free_blocks: list[int] = list(range(num_blocks))
+        self.allocator: DeviceBlockAllocator | None = None
 
     @property
     def block_count(self) -> int:
@@ -142,24 +143,33 @@ class SharedKVBlockPool:
 
     def allocate(self, count: int, key: Any = None, value: Any = None) -> list[int]:
         del key, value
+        if self.allocator is not None:
+            raise RuntimeError("shared KV pool: the free list belongs to its DeviceBlockAllocator; reserve blocks on the device")
         if count > len(self.free_blocks):
             raise RuntimeError(f"shared KV pool exhausted: need {count} blocks, {len(self.free_blocks)} free")
         taken, self.free_blocks = self.free_blocks[:count], self.free_blocks[count:]
         return taken
 
     def release(self, blocks: list[int]) -> None:
-        if blocks:
-            self.free_blocks = sorted(self.free_blocks + list(blocks))
+        """Return blocks to the free list: the host list, or the device one after ``device_allocator``."""
+        if not blocks:
+            return
+        if self.allocator is not None:
+            self.allocator.release(blocks)
+            return
+        self.free_blocks = sorted(self.free_blocks + list(blocks))
 
     def device_allocator(self) -> "DeviceBlockAllocator":
-        """Hand this pool's free list to a ``DeviceBlockAllocator``.
+        """Hand this pool's free list to a ``DeviceBlockAllocator`` (once).
 
-        From then on blocks are reserved on the device; the host list is emptied
-        so a host ``allocate`` cannot hand out an id the device also owns.
+        From then on blocks are reserved on the device: the host list is emptied, host
+        ``allocate`` raises, and ``release`` (e.g. ``FullAttentionCache.release`` at request
+        completion) merges ids into the device list, so freed blocks stay reservable.
         """
-        allocator = DeviceBlockAllocator(self.block_count, device=self.key_blocks.device, free_blocks=self.free_blocks)
-        self.free_blocks = []
-        return allocator
+        if self.allocator is None:
+            self.allocator = DeviceBlockAllocator(self.block_count, device=self.key_blocks.device, free_blocks=self.free_blocks)
+            self.free_blocks = []
+        return self.allocator
 
 
 class DeviceBlockAllocator:

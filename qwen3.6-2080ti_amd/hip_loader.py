@@ -98,13 +98,13 @@ SIGNATURES: dict[str, tuple[Any, list[Any]]] = {
     ),
     "qa_causal_conv1d_prefill": (
         c_int32,
-        [c_void_p, c_int32, c_int64, c_int64, c_void_p, c_void_p, c_int64, c_void_p, c_int32, c_void_p, c_int64, c_int64, c_int32,
-         c_int32, c_void_p, c_int32, c_int64, c_int64, c_int32, c_void_p],
+        [c_void_p, c_int32, c_int64, c_int64, c_void_p, c_void_p, c_int64, c_void_p, c_int32, c_int64, c_void_p, c_int64, c_int64,
+         c_int32, c_int32, c_void_p, c_int32, c_int64, c_int64, c_int32, c_void_p],
     ),
     "qa_causal_conv1d_update": (
         c_int32,
-        [c_void_p, c_int32, c_int64, c_void_p, c_int64, c_void_p, c_int32, c_void_p, c_int64, c_int32, c_int32, c_void_p, c_int32,
-         c_int64, c_int32, c_void_p],
+        [c_void_p, c_int32, c_int64, c_void_p, c_int64, c_void_p, c_int32, c_int64, c_void_p, c_int64, c_int32, c_int32, c_void_p,
+         c_int32, c_int64, c_int32, c_void_p],
     ),
     "qa_linear_attention_recurrent_core": (
         c_int32,
@@ -113,13 +113,14 @@ SIGNATURES: dict[str, tuple[Any, list[Any]]] = {
     ),
     "qa_gated_delta_step": (
         c_int32,
-        [c_void_p, c_int64, c_void_p, c_void_p, c_int32, c_int64, c_void_p, c_void_p, c_void_p, c_int64, c_void_p, c_int32, c_void_p,
-         c_int32, c_int64, c_int64, c_int32, c_int32, c_int32, c_int32, c_void_p],
+        [c_void_p, c_int64, c_void_p, c_void_p, c_int32, c_int64, c_void_p, c_void_p, c_void_p, c_int64, c_void_p, c_int32, c_int64,
+         c_void_p, c_int32, c_int64, c_int64, c_int32, c_int32, c_int32, c_int32, c_void_p],
     ),
     "qa_gated_delta_step_norm": (
         c_int32,
-        [c_void_p, c_int64, c_void_p, c_void_p, c_int32, c_int64, c_void_p, c_void_p, c_void_p, c_int64, c_void_p, c_int32, c_void_p,
-         c_int32, c_int64, c_void_p, c_int32, c_float, c_void_p, c_int32, c_int64, c_int64, c_int32, c_int32, c_int32, c_int32, c_void_p],
+        [c_void_p, c_int64, c_void_p, c_void_p, c_int32, c_int64, c_void_p, c_void_p, c_void_p, c_int64, c_void_p, c_int32, c_int64,
+         c_void_p, c_int32, c_int64, c_void_p, c_int32, c_float, c_void_p, c_int32, c_int64, c_int64, c_int32, c_int32, c_int32, c_int32,
+         c_void_p],
     ),
     "qa_gated_rms_norm": (
         c_int32,

@@ -571,7 +571,7 @@ def causal_conv1d_prefill(
     out = torch.empty((batch, seq, channels), dtype=out_dtype, device=device)
     status = lib.qa_causal_conv1d_prefill(
         _ptr(x), _code(x), x.stride(0), x.stride(1), _ptr(state_in), _ptr(new_state), channels * (kernel - 1), ctypes.c_void_p(0), L.QA_I32,
-        _ptr(w), batch, seq, channels, kernel, _ptr(out), _code(out), out.stride(0), out.stride(1), int(apply_silu), _stream(device),
+        batch, _ptr(w), batch, seq, channels, kernel, _ptr(out), _code(out), out.stride(0), out.stride(1), int(apply_silu), _stream(device),
     )
     L.check(lib, status, "causal_conv1d_prefill")
     return out, new_state
@@ -601,7 +601,8 @@ def causal_conv1d_update(x: torch.Tensor, conv_state: torch.Tensor, weight: torc
         slot_ptr, slot_code = _ptr(slots), _code(slots)
     out = torch.empty((batch, channels), dtype=torch.float32, device=device)
     status = lib.qa_causal_conv1d_update(
-        _ptr(x), _code(x), x.stride(0), _ptr(conv_state), channels * (kernel - 1), slot_ptr, slot_code, _ptr(w), batch, channels, kernel,
+        _ptr(x), _code(x), x.stride(0), _ptr(conv_state), channels * (kernel - 1), slot_ptr, slot_code, conv_state.shape[0], _ptr(w), batch,
+        channels, kernel,
         _ptr(out), L.QA_F32, out.stride(0), int(apply_silu), _stream(device),
     )
     L.check(lib, status, "causal_conv1d_update")
@@ -658,7 +659,7 @@ def gated_delta_step(
         _require(norm_weight is None, "norm_weight needs z")
         status = lib.qa_gated_delta_step(
             _ptr(qkv), qkv.stride(0), _ptr(a_c), _ptr(b_c), _code(a_c), a_c.stride(0), _ptr(alog), _ptr(dtb), _ptr(state), state.stride(0),
-            slot_ptr, slot_code, _ptr(out), _code(out), out.stride(0), batch, int(key_heads), value_heads, key_dim, value_dim, _stream(device),
+            slot_ptr, slot_code, state.shape[0], _ptr(out), _code(out), out.stride(0), batch, int(key_heads), value_heads, key_dim, value_dim, _stream(device),
         )
     else:
         _require_cuda(z, "z", device)
@@ -671,7 +672,7 @@ def gated_delta_step(
         _require(w.numel() == value_dim, "norm_weight must have value_dim elements")
         status = lib.qa_gated_delta_step_norm(
             _ptr(qkv), qkv.stride(0), _ptr(a_c), _ptr(b_c), _code(a_c), a_c.stride(0), _ptr(alog), _ptr(dtb), _ptr(state), state.stride(0),
-            slot_ptr, slot_code, _ptr(zz), _code(zz), zz.stride(0), _ptr(w), _code(w), float(eps), _ptr(out), _code(out), out.stride(0), batch,
+            slot_ptr, slot_code, state.shape[0], _ptr(zz), _code(zz), zz.stride(0), _ptr(w), _code(w), float(eps), _ptr(out), _code(out), out.stride(0), batch,
             int(key_heads), value_heads, key_dim, value_dim, _stream(device),
         )
     L.check(lib, status, "gated_delta_step")

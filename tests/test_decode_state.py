@@ -24,16 +24,18 @@ from decode_state import (
 
 
 def _kv(step: int, *, batch: int = 1, heads: int = 2, seq: int = 1, head_dim: int = 4):
-    # arange-based K/V as tests/unit/test_decode_state.py:18-24
-    base = float(step * 1000)
-    count = batch * heads * seq * head_dim
-    key = (base + torch.arange(count, dtype=torch.float32)).reshape(batch, heads, seq, head_dim)
-    value = (base + 0.5 + torch.arange(count, dtype=torch.float32)).reshape(batch, heads, seq, head_dim)
-    return key, value
+    """Token tensors tagged with their step: element i of step s is s * 4096 + i (keys) and its
+    negation (values), so a token written to the wrong slot or returned in the wrong order
+    changes the compared tensors."""
+    shape = (batch, heads, seq, head_dim)
+    tagged = torch.arange(batch * heads * seq * head_dim, dtype=torch.float32).reshape(shape) + float(4096 * step)
+    return tagged, -tagged - 1.0
 
 
 def _mapping(layer_types):
-    return SimpleNamespace(layers=tuple(SimpleNamespace(index=i, layer_type=t) for i, t in enumerate(layer_types)))
+    """A model-layer mapping with only the fields ``DecodeState.empty`` reads (index, layer_type)."""
+    layers = [SimpleNamespace(index=i, layer_type=kind) for i, kind in enumerate(layer_types)]
+    return SimpleNamespace(layers=tuple(layers))
 
 
 def test_append_returns_views_equal_to_manual_concat() -> None:  # :33-44
@@ -248,6 +250,28 @@ def test_shared_pool_caches_share_storage_and_gather_in_order() -> None:
     assert pool.free_blocks == [0, 1, 5, 6, 7]
     with pytest.raises(RuntimeError, match="exhausted"):
         FullAttentionCache(block_size=2, shared_pool=pool).append_blocks(*_kv(3, seq=20))
+
+
+def test_shared_pool_release_after_device_hand_off_goes_to_the_device_list() -> None:
+    """After ``device_allocator()`` the host list is empty, host ``allocate`` refuses, and a cache's
+    ``release`` merges its blocks into the allocator's sorted free list (they stay reservable)."""
+    pool = SharedKVBlockPool(8, kv_heads=2, head_dim=4, block_size=2, dtype=torch.float32)
+    a = FullAttentionCache(block_size=2, shared_pool=pool)
+    b = FullAttentionCache(block_size=2, shared_pool=pool)
+    a.append_blocks(*_kv(1, seq=3))
+    b.append_blocks(*_kv(2, seq=2))
+    assert a.block_table == [0, 1] and b.block_table == [2]
+    alloc = pool.device_allocator()
+    assert pool.device_allocator() is alloc
+    assert pool.free_blocks == [] and alloc.free_blocks() == [3, 4, 5, 6, 7] and alloc.free_count == 5
+    with pytest.raises(RuntimeError, match="DeviceBlockAllocator"):
+        FullAttentionCache(block_size=2, shared_pool=pool).append_blocks(*_kv(3, seq=1))
+    a.release()
+    assert alloc.free_blocks() == [0, 1, 3, 4, 5, 6, 7] and pool.free_blocks == []
+    b.release()
+    assert alloc.free_blocks() == list(range(8))
+    with pytest.raises(ValueError, match="already free"):
+        pool.release([4])
 
 
 def test_page_table_tensor_is_reused_until_the_table_changes() -> None:

@@ -1,8 +1,8 @@
 """fp8 E4M3 block-scaled linear (``hip_ops.fp8_e4m3_bf16_linear``) against the oracle.
 
 Tolerances: weight decoding bit-exact; fp32 output within 1e-5 x max|y| absolute
-and 1e-3 relative of the float64 sum for bf16 inputs and for fp32 inputs of at
-most 16 rows (fp32 summation of up to 4096 terms); fp32 inputs of more rows are
+and 1e-3 relative of the float64 sum for bf16 inputs and for fp32 inputs of
+fewer than 16 rows (fp32 summation of up to 4096 terms); fp32 inputs of 16 rows or more are
 rounded to fp16 as the reference's own GEMM path does
 (``src/csrc/fp8_linear_cuda.cu:1411-1460``): within 1e-3 x max|y| and 1e-3
 relative; everything within the reference's own 2e-3 of its fp32 restatement
@@ -76,7 +76,7 @@ def test_matches_reference_test_case() -> None:
         out = ops.fp8_e4m3_bf16_linear(x.to(DEV), weight.to(DEV), scale.to(DEV))
         assert out.dtype == torch.float32 and out.shape == (batch, 384)
         torch.testing.assert_close(out.cpu(), oracle.linear(x, codes, scale), atol=2e-3, rtol=2e-3)
-        _close_to_fp64(out, oracle.linear_fp64(x, codes, scale), fp16_input=batch > 16)
+        _close_to_fp64(out, oracle.linear_fp64(x, codes, scale), fp16_input=batch >= 16)
 
 
 @pytest.mark.parametrize("rows,n,k", [(1, 256, 512), (37, 384, 1024), (128, 1024, 4096), (200, 512, 768), (4096, 256, 256)])
@@ -88,7 +88,27 @@ def test_fp32_input_matches_fp64(rows, n, k) -> None:
     print(f"fp8 linear fp32: rows {rows}, out {n}, in {k}, workspace {ops.L.load_library().qa_fp8_linear_workspace(rows, n, k)}", flush=True)
     out = ops.fp8_e4m3_bf16_linear(x.to(DEV), w.to(DEV), s.to(DEV))
     ref = oracle.linear_fp64(x, w.view(torch.uint8).numpy(), s)
-    _close_to_fp64(out, ref, fp16_input=rows > 16)
+    _close_to_fp64(out, ref, fp16_input=rows >= 16)
+
+
+@pytest.mark.parametrize("rows", [15, 16])
+def test_regime_boundary_at_16_rows(rows) -> None:
+    """Below 16 rows fp32 x enters exactly; from 16 rows on it is rounded to fp16 first, as the
+    reference's ``batch < kDefaultCublasBatchThreshold`` (16) split does
+    (``src/csrc/fp8_linear_cuda.cu:1411-1460``).  Each side matches its own fp64 form at 1e-5 and
+    not the other one's."""
+    ops = _ops()
+    gen = torch.Generator().manual_seed(160 + rows)
+    w, s = _weights(gen, 256, 1024)
+    x = torch.randn((rows, 1024), generator=gen) * 3.0
+    codes = w.view(torch.uint8).numpy()
+    out = ops.fp8_e4m3_bf16_linear(x.to(DEV), w.to(DEV), s.to(DEV)).cpu().double()
+    exact = oracle.linear_fp64(x, codes, s)
+    rounded = oracle.linear_fp64(x.half().float(), codes, s)
+    want, other = (rounded, exact) if rows >= 16 else (exact, rounded)
+    scale = want.abs().max().item()
+    torch.testing.assert_close(out, want, atol=1e-5 * scale, rtol=1e-4)
+    assert (out - other).abs().max().item() > 1e-4 * scale
 
 
 def test_bf16_input_and_output_and_leading_dims() -> None:

@@ -159,3 +159,42 @@ def test_fused_step_bf16_output_and_bf16_gates() -> None:
     assert out.dtype == torch.bfloat16
     torch.testing.assert_close(out.cpu().float(), ref_core[:, 0].float(), atol=2e-2, rtol=2e-2)
     assert _rel(state, ref_state) < 1e-3
+
+
+@pytest.mark.parametrize("slot_dtype", [torch.int32, torch.int64])
+def test_invalid_slots_give_zeros_and_leave_the_pools_untouched(slot_dtype) -> None:
+    """A -1 pad or an id past the pool in ``slots``: that row's conv and step outputs are zeros,
+    no state row changes, and the valid rows match a run without the invalid rows."""
+    ops = _ops()
+    shape = gd.LinearShape(key_heads=2, value_heads=4, key_head_dim=128, value_head_dim=128, conv_kernel_dim=4)
+    mixed, a, b, a_log, dt_bias, w = _layer_inputs(37, 4, 1, shape)
+    gen = torch.Generator().manual_seed(38)
+    rows = 3
+    state0 = (torch.randn(rows, shape.value_heads, 128, 128, generator=gen) * 0.05).to(DEV)
+    conv0 = torch.randn(rows, shape.qkv_dim, 3, generator=gen).to(DEV)
+    slots = torch.tensor([2, -1, 0, rows], device=DEV, dtype=slot_dtype)
+    state_pool, conv_pool = state0.clone(), conv0.clone()
+    x, av, bv = mixed[:, 0].contiguous().to(DEV), a[:, 0].contiguous().to(DEV), b[:, 0].contiguous().to(DEV)
+    act = ops.causal_conv1d_update(x, conv_pool, w.to(DEV), slots)
+    out = ops.gated_delta_step(act, av, bv, a_log.to(DEV), dt_bias.to(DEV), state_pool, key_heads=shape.key_heads, slots=slots,
+                               out_dtype=torch.float32)
+    z = torch.randn(4, shape.value_heads * 128, generator=gen).to(DEV)
+    nw = torch.ones(128, device=DEV)
+    state_norm = state0.clone()
+    out_norm = ops.gated_delta_step(act, av, bv, a_log.to(DEV), dt_bias.to(DEV), state_norm, key_heads=shape.key_heads, slots=slots,
+                                    out_dtype=torch.float32, z=z, norm_weight=nw)
+    for bad in (1, 3):
+        assert torch.count_nonzero(act[bad]) == 0
+        assert torch.count_nonzero(out[bad]) == 0
+        assert torch.count_nonzero(out_norm[bad]) == 0
+    # slot 1 is no valid row's slot: untouched bit for bit
+    assert torch.equal(state_pool[1], state0[1]) and torch.equal(conv_pool[1], conv0[1]) and torch.equal(state_norm[1], state0[1])
+    # the valid rows equal the same step with only those rows
+    good = torch.tensor([0, 2], device=DEV)
+    ref_state, ref_conv = state0.clone(), conv0.clone()
+    ref_slots = slots[good].contiguous()
+    ref_act = ops.causal_conv1d_update(x[good].contiguous(), ref_conv, w.to(DEV), ref_slots)
+    ref_out = ops.gated_delta_step(ref_act, av[good].contiguous(), bv[good].contiguous(), a_log.to(DEV), dt_bias.to(DEV), ref_state,
+                                   key_heads=shape.key_heads, slots=ref_slots, out_dtype=torch.float32)
+    assert torch.equal(act[good], ref_act) and torch.equal(out[good], ref_out)
+    assert torch.equal(state_pool, ref_state) and torch.equal(conv_pool, ref_conv)

@@ -189,6 +189,27 @@ def test_device_allocator_release_resorts_and_reuses() -> None:
     assert tables2.tolist() == [[1, 3, -1, -1]] and alloc.free_blocks() == [5, 6, 7]
 
 
+def test_reserve_after_shared_pool_hand_off_reuses_released_cache_blocks() -> None:
+    """A cache on a shared pool releases its blocks after the pool's free list went to the device:
+    the next device reservation takes those ids first (lowest free id)."""
+    from decode_state import FullAttentionCache, SharedKVBlockPool
+
+    pool = SharedKVBlockPool(6, kv_heads=1, head_dim=8, block_size=4, dtype=torch.bfloat16, device=DEV)
+    cache = FullAttentionCache(block_size=4, shared_pool=pool)
+    cache.append_blocks(torch.ones(1, 1, 7, 8, dtype=torch.bfloat16, device=DEV), torch.ones(1, 1, 7, 8, dtype=torch.bfloat16, device=DEV))
+    assert cache.block_table == [0, 1]
+    alloc = pool.device_allocator()
+    tables = torch.full((1, 4), -1, dtype=torch.int32, device=DEV)
+    lens = torch.zeros(1, dtype=torch.int32, device=DEV)
+    alloc.reserve(tables, lens, 4, counts=4)
+    alloc.check()
+    assert tables.tolist() == [[2, -1, -1, -1]]
+    cache.release()
+    alloc.reserve(tables, lens, 4, counts=8)
+    alloc.check()
+    assert tables.tolist() == [[2, 0, 1, -1]] and lens.tolist() == [12] and alloc.free_blocks() == [3, 4, 5]
+
+
 def test_graph_captured_decode_step_matches_eager_and_oracle() -> None:
     """reserve -> K/V append -> batched decode captured once and replayed step after
     step; every replay equals the same step run eagerly on a twin state, and the last

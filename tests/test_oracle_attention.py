@@ -112,3 +112,112 @@ def test_gate_applies_sigmoid_per_head_channel() -> None:
     gated = attention.dense_attention(q, k, v, position_offset=2, cast_probs=False, gate=gate)
     expected = plain * torch.sigmoid(gate.reshape(1, 1, 2, 4).transpose(1, 2))
     torch.testing.assert_close(gated, expected, rtol=0, atol=0)
+
+
+def _scatter_into_pool(dense: torch.Tensor, table: list[int], pool: torch.Tensor, bs: int, layout: str) -> None:
+    """Write dense ``(H_kv, T, D)`` tokens into their slots ``(table[t // bs], t % bs)``."""
+    for t in range(dense.shape[1]):
+        if layout == "phbd":
+            pool[table[t // bs], :, t % bs] = dense[:, t]
+        else:  # "hpbd": the reference's per-request (heads, P, bs, D) pool
+            pool[:, table[t // bs], t % bs] = dense[:, t]
+
+
+def test_paged_prefill_matches_textbook_fp64_on_ragged_prefixes_gqa_and_gate() -> None:
+    """``paged_prefill`` (prefix offsets, per-row query slicing, gate reshape) against an independent
+    fp64 loop: a shuffled shared pool whose unused slots hold garbage, prefixes 0 / 5 / 21 (not
+    multiples of the block size), new lengths 7 / 16 / 3, GQA 16 query heads on 2 KV heads."""
+    bs, heads, kv_heads, dim = 4, 16, 2, 8
+    prefixes, news = [0, 5, 21], [7, 16, 3]
+    totals = [p + n for p, n in zip(prefixes, news)]
+    need = [(t + bs - 1) // bs for t in totals]
+    pool_blocks = sum(need) + 5
+    rng = np.random.default_rng(40)
+    perm = [int(x) for x in rng.permutation(pool_blocks)]
+    tables, cursor = [], 0
+    for n in need:
+        tables.append(perm[cursor : cursor + n])
+        cursor += n
+    pool_k = torch.full((pool_blocks, kv_heads, bs, dim), 1e4)  # garbage everywhere a token is not written
+    pool_v = torch.full((pool_blocks, kv_heads, bs, dim), -1e4)
+    dense_k = [_rand(kv_heads, t, dim, seed=41 + b) for b, t in enumerate(totals)]
+    dense_v = [_rand(kv_heads, t, dim, seed=51 + b) for b, t in enumerate(totals)]
+    for b in range(3):
+        _scatter_into_pool(dense_k[b], tables[b], pool_k, bs, "phbd")
+        _scatter_into_pool(dense_v[b], tables[b], pool_v, bs, "phbd")
+    query = _rand(sum(news), heads, dim, seed=61)
+    gate = _rand(sum(news), heads * dim, seed=62)
+    outs = attention.paged_prefill(query, pool_k, pool_v, tables, prefixes, news, block_size=bs, gate=gate)
+    offset = 0
+    for b in range(3):
+        q = query[offset : offset + news[b]].transpose(0, 1).numpy()  # (H, new, D)
+        ref = attention.textbook_attention_fp64(
+            q, dense_k[b].numpy(), dense_v[b].numpy(), query_positions=np.arange(prefixes[b], totals[b]),
+            valid=np.ones(totals[b], bool), scale=dim**-0.5,
+        )
+        g = gate[offset : offset + news[b]].double().reshape(news[b], heads, dim).transpose(0, 1).numpy()
+        ref = ref * (1.0 / (1.0 + np.exp(-g)))
+        assert outs[b].shape == (news[b], heads, dim)
+        np.testing.assert_allclose(outs[b].transpose(0, 1).numpy(), ref, rtol=2e-6, atol=2e-6)
+        offset += news[b]
+
+
+def test_paged_prefill_mistakes_are_caught_by_the_textbook_check() -> None:
+    """The checks above can fail: a query offset by one position or a gate on the wrong head axis differs."""
+    heads, kv_heads, dim, total, new = 4, 2, 8, 9, 4
+    k = _rand(kv_heads, total, dim, seed=70)
+    v = _rand(kv_heads, total, dim, seed=71)
+    q = _rand(heads, new, dim, seed=72)
+    right = attention.textbook_attention_fp64(q.numpy(), k.numpy(), v.numpy(), query_positions=np.arange(5, 9), valid=np.ones(total, bool),
+                                              scale=dim**-0.5)
+    off_by_one = attention.textbook_attention_fp64(q.numpy(), k.numpy(), v.numpy(), query_positions=np.arange(4, 8),
+                                                   valid=np.ones(total, bool), scale=dim**-0.5)
+    assert np.abs(right - off_by_one).max() > 1e-3
+    gate = _rand(new, heads * dim, seed=73)
+    good = gate.reshape(new, heads, dim).transpose(0, 1)
+    bad = gate.reshape(new, dim, heads).permute(2, 0, 1)
+    assert (torch.sigmoid(good) - torch.sigmoid(bad)).abs().max() > 1e-2
+
+
+def test_reference_layout_decode_equals_shared_pool_decode_and_textbook() -> None:
+    """``reference_layout_decode_cpu`` (repeated heads, per-request ``(H, P, bs, D)`` pools, the
+    ``"hpbd"`` branch of ``gather_dense``) == ``paged_decode`` on a shared GQA ``(P, H_kv, bs, D)``
+    pool holding the same tokens == the fp64 textbook."""
+    bs, heads, kv_heads, dim = 4, 8, 2, 8
+    lens = [13, 1, 8]
+    query = _rand(3, heads, 1, dim, seed=80)
+    rng = np.random.default_rng(81)
+    shared_blocks = sum((n + bs - 1) // bs for n in lens) + 3
+    shared_perm = [int(x) for x in rng.permutation(shared_blocks)]
+    shared_k = torch.full((shared_blocks, kv_heads, bs, dim), 7e3)
+    shared_v = torch.full((shared_blocks, kv_heads, bs, dim), -7e3)
+    ref_k, ref_v, ref_tables, shared_tables, cursor = [], [], [], [], 0
+    for b, n in enumerate(lens):
+        nb = (n + bs - 1) // bs
+        dk = _rand(kv_heads, n, dim, seed=82 + b)
+        dv = _rand(kv_heads, n, dim, seed=92 + b)
+        shared_tables.append(shared_perm[cursor : cursor + nb])
+        cursor += nb
+        _scatter_into_pool(dk, shared_tables[b], shared_k, bs, "phbd")
+        _scatter_into_pool(dv, shared_tables[b], shared_v, bs, "phbd")
+        # the reference's per-request pool: post-repeat heads (h reads kv head h // G), own shuffled table
+        table = [int(x) for x in rng.permutation(nb + 2)[:nb]]
+        pk = torch.full((heads, nb + 2, bs, dim), 5e3)
+        pv = torch.full((heads, nb + 2, bs, dim), -5e3)
+        rep = heads // kv_heads
+        _scatter_into_pool(dk.repeat_interleave(rep, dim=0), table, pk, bs, "hpbd")
+        _scatter_into_pool(dv.repeat_interleave(rep, dim=0), table, pv, bs, "hpbd")
+        ref_k.append(pk)
+        ref_v.append(pv)
+        ref_tables.append(table)
+        want = attention.textbook_attention_fp64(query[b].numpy(), dk.numpy(), dv.numpy(), query_positions=np.array([n - 1]),
+                                                 valid=np.ones(n, bool), scale=dim**-0.5)
+        got = attention.reference_layout_decode_cpu(query[b : b + 1], [pk], [pv], [table], [n], block_size=bs)
+        np.testing.assert_allclose(got[0].numpy(), want, rtol=2e-6, atol=2e-6)
+    ref_out = attention.reference_layout_decode_cpu(query, ref_k, ref_v, ref_tables, lens, block_size=bs)
+    shared_out = attention.paged_decode(query, [shared_k] * 3, [shared_v] * 3, shared_tables, lens, block_size=bs, pool_layout="phbd")
+    torch.testing.assert_close(ref_out, shared_out, rtol=1e-6, atol=1e-6)
+    # gather_dense("hpbd") returns the tokens in logical order
+    dense = attention.gather_dense(ref_k[0], ref_tables[0], lens[0], block_size=bs, pool_layout="hpbd")
+    assert dense.shape == (heads, lens[0], dim)
+    torch.testing.assert_close(dense[:: heads // kv_heads], _rand(kv_heads, lens[0], dim, seed=82), rtol=0, atol=0)
