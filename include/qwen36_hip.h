@@ -112,6 +112,26 @@ int qa_paged_attention_decode_batched(const void* query, int32_t q_dtype, int64_
                                       void* output, void* workspace, int64_t workspace_bytes,
                                       hipStream_t stream);
 
+/* qa_paged_attention_decode_batched without a workspace argument: the split-K
+ * partials live in a static device array of this library (32 MiB, one copy per
+ * device, held until the process ends), so the call allocates nothing and
+ * needs no caller memory beyond inputs and outputs.  No counterpart in the
+ * reference: it is for callers that cannot allocate (code under HIP graph
+ * capture, tight serving loops, harnesses that forbid hipMalloc).  Sizes whose
+ * partials exceed 32 MiB are rejected (status 1, message names the bytes
+ * needed); at D = 256 and 8 query heads per KV head the MFMA path fits about
+ * 1,900 (row, KV head) groups.  Every call on a device shares that device's
+ * array, and nothing in it needs to start at zero: calls that overlap on one
+ * device (e.g. on two streams) race and must be serialised by the caller.   */
+int qa_paged_attention_decode_batched_noalloc(const void* query, int32_t q_dtype, int64_t q_stride_b, int64_t q_stride_h,
+                                              int64_t batch, int32_t heads, int32_t head_dim,
+                                              const qa_paged_kv* kv,
+                                              const void* block_tables, int32_t table_dtype, int64_t table_stride,
+                                              int64_t max_blocks,
+                                              const void* sequence_lengths, int32_t lengths_dtype,
+                                              int32_t block_size, float scale, void* output,
+                                              hipStream_t stream);
+
 /* ---- paged KV cache --------------------------------------------------- */
 /* Write `new_tokens` tokens of each row into its slots
  * (table[pos/bs], pos%bs) for pos = start_b .. start_b + count_b - 1.

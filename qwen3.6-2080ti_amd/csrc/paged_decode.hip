@@ -12,6 +12,15 @@
 
 #include <algorithm>
 #include <cstdlib>
+#include <mutex>
+
+// Static scratch of qa_paged_attention_decode_batched_noalloc: the split-K partials and
+// row-group records that the other decode entry points keep in the caller's workspace.
+// Every device the library runs on holds its own copy until the process ends.  Host code
+// never uses this name as an address: decode_scratch() looks up each device's copy with
+// hipGetSymbolAddress once and hands that pointer to the kernels.
+constexpr int64_t kDecodeScratchBytes = int64_t{32} << 20;
+static __device__ __align__(256) unsigned char scratch[kDecodeScratchBytes];
 
 namespace qa {
 
@@ -757,6 +766,7 @@ struct DecodeHostArgs {
   void* output;
   void* workspace;
   int64_t workspace_bytes;
+  bool static_scratch;  // workspace is this device's copy of `scratch`
 };
 
 // The MFMA path needs 16-token blocks, D in {128, 256}, G <= 16 and 16-byte
@@ -833,8 +843,8 @@ static int run_decode(const DecodeHostArgs& a, hipStream_t stream) {
   const int64_t slots = static_cast<int64_t>(p.n_waves) + static_cast<int64_t>(p.B) * p.Hkv;
   const int64_t need = mfma ? (slots * p.G * (p.D + 2) + 2 * static_cast<int64_t>(p.B) * p.Hkv) * 4
                             : static_cast<int64_t>(p.B) * p.H * p.n_splits * (p.D + 2) * 4;
-  QA_REQUIRE(a.workspace != nullptr && a.workspace_bytes >= need, "paged decode workspace too small: need %lld bytes, have %lld",
-             static_cast<long long>(need), static_cast<long long>(a.workspace_bytes));
+  QA_REQUIRE(a.workspace != nullptr && a.workspace_bytes >= need, "paged decode %s too small: need %lld bytes, have %lld",
+             a.static_scratch ? "static scratch" : "workspace", static_cast<long long>(need), static_cast<long long>(a.workspace_bytes));
   p.part_o = reinterpret_cast<float*>(a.workspace);
   if (mfma) {
     p.part_ml = p.part_o + slots * p.G * p.D;
@@ -847,6 +857,28 @@ static int run_decode(const DecodeHostArgs& a, hipStream_t stream) {
   if (a.q_dtype == QA_BF16 && kv.dtype == QA_BF16) return dispatch_generic<bf16_t, bf16_t>(p, stream);
   if (a.q_dtype == QA_F32 && kv.dtype == QA_BF16) return dispatch_generic<float, bf16_t>(p, stream);
   return dispatch_generic<bf16_t, float>(p, stream);
+}
+
+// This device's address of `scratch`, looked up once per device (with that device current)
+// and kept; the kernels receive this pointer, never the host-side name.
+static int decode_scratch(void** out) {
+  constexpr int kMaxDevices = 64;
+  static std::mutex mu;
+  static void* addr[kMaxDevices] = {};
+  int dev = -1;
+  hipError_t err = hipGetDevice(&dev);
+  if (err != hipSuccess) return fail("paged decode (no-alloc): hipGetDevice failed: %s", hipGetErrorString(err));
+  if (dev < 0 || dev >= kMaxDevices) return fail("paged decode (no-alloc): device %d out of range", dev);
+  std::lock_guard<std::mutex> lock(mu);
+  if (addr[dev] == nullptr) {
+    void* ptr = nullptr;
+    err = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (err != hipSuccess || ptr == nullptr)
+      return fail("paged decode (no-alloc): hipGetSymbolAddress(scratch) failed on device %d: %s", dev, hipGetErrorString(err));
+    addr[dev] = ptr;
+  }
+  *out = addr[dev];
+  return 0;
 }
 
 }  // namespace qa
@@ -916,5 +948,39 @@ extern "C" int qa_paged_attention_decode_batched(const void* query, int32_t q_dt
   a.output = output;
   a.workspace = workspace;
   a.workspace_bytes = workspace_bytes;
+  return qa::run_decode(a, stream);
+}
+
+extern "C" int qa_paged_attention_decode_batched_noalloc(const void* query, int32_t q_dtype, int64_t q_stride_b, int64_t q_stride_h,
+                                                         int64_t batch, int32_t heads, int32_t head_dim, const qa_paged_kv* kv,
+                                                         const void* block_tables, int32_t table_dtype, int64_t table_stride,
+                                                         int64_t max_blocks, const void* sequence_lengths, int32_t lengths_dtype,
+                                                         int32_t block_size, float scale, void* output, hipStream_t stream) {
+  QA_REQUIRE(sequence_lengths != nullptr, "sequence_lengths must be a device array");
+  void* ws = nullptr;
+  if (int rc = qa::decode_scratch(&ws)) return rc;
+  qa::DecodeHostArgs a{};
+  a.query = query;
+  a.q_dtype = q_dtype;
+  a.q_sb = q_stride_b;
+  a.q_sh = q_stride_h;
+  a.batch = batch;
+  a.heads = heads;
+  a.head_dim = head_dim;
+  a.kv = kv;
+  a.tables = block_tables;
+  a.table_dtype = table_dtype;
+  a.table_stride = table_stride;
+  a.max_blocks = max_blocks;
+  a.lens = sequence_lengths;
+  a.lens_dtype = lengths_dtype;
+  a.len_scalar = 0;
+  a.max_tokens = max_blocks * static_cast<int64_t>(block_size);
+  a.block_size = block_size;
+  a.scale = scale;
+  a.output = output;
+  a.workspace = ws;
+  a.workspace_bytes = kDecodeScratchBytes;
+  a.static_scratch = true;
   return qa::run_decode(a, stream);
 }

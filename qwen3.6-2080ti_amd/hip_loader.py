@@ -68,6 +68,11 @@ SIGNATURES: dict[str, tuple[Any, list[Any]]] = {
         [c_void_p, c_int32, c_int64, c_int64, c_int64, c_int32, c_int32, ctypes.POINTER(PagedKV), c_void_p, c_int32, c_int64,
          c_int64, c_void_p, c_int32, c_int32, c_float, c_void_p, c_void_p, c_int64, c_void_p],
     ),
+    "qa_paged_attention_decode_batched_noalloc": (
+        c_int32,
+        [c_void_p, c_int32, c_int64, c_int64, c_int64, c_int32, c_int32, ctypes.POINTER(PagedKV), c_void_p, c_int32, c_int64,
+         c_int64, c_void_p, c_int32, c_int32, c_float, c_void_p, c_void_p],
+    ),
     "qa_paged_kv_append": (
         c_int32,
         [c_void_p, c_void_p, c_int32, c_int64, c_int64, c_int64, c_int64, c_int32, c_int64, c_int32, ctypes.POINTER(PagedKV),
