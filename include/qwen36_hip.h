@@ -343,7 +343,8 @@ int qa_gated_delta_step_norm(const float* qkv, int64_t qkv_stride_b,
  * :291-322 in 64-token chunks (WY/UT form) on fp16 MFMA with fp32
  * accumulation and an fp32 state.  dk = dv = 128, conv kernel 4.  The
  * workspace (256-byte aligned, qa_chunk_gated_delta_workspace bytes) holds the
- * normalised fp16 q/k/v and the gates between the launches.  The reference
+ * normalised fp16 q/k and the gates between the launches (the v channels are
+ * convolved inside the second launch).  The reference
  * has no chunked kernel: its prefill runs the token-serial recurrence
  * (src/tp_runtime.py:2744-2787).                                          */
 int qa_chunk_gated_delta_rule(const void* mixed_qkv, int32_t x_dtype, int64_t x_stride_b, int64_t x_stride_t,

@@ -2,12 +2,15 @@
 // chunk 64), from the raw in_proj outputs of a linear-attention layer.
 //
 // Two launches on the caller's stream (steps 1 and 2 share one grid):
-//  1. prep_kernel -- causal conv1d + SiLU of every q/k/v channel and the L2
+//  1. prep_kernel -- causal conv1d + SiLU of every q/k channel and the L2
 //     norm of q and k per (token, head), q also scaled by dk^-0.5
 //     (src/reference_ops.py:181-183, 240-258, 297-304).  Each (row, head,
 //     token run) is done once, by one wave walking its tokens with the conv
 //     window in registers, and written token-major as fp16 to a workspace.
-//     It also writes the conv state.
+//     It also writes the q/k conv state.  (The v channels are convolved by
+//     chunk_kernel itself as it stages them: each v channel is read by one
+//     workgroup only, so the fp16 round trip through the workspace would only
+//     add HBM traffic.)
 //  2. gate_item -- g = -exp(A_log) softplus(a + dt_bias), beta = sigmoid(b)
 //     (src/reference_ops.py:271-275) and G, the inclusive sum of g inside each
 //     chunk.
@@ -22,7 +25,9 @@
 //     (delta = U - W S0 of the WY form; T, W and U themselves are never formed).
 //
 // chunk_kernel mapping: one workgroup (8 waves) per (batch row, value head,
-// half of dv); chunks run in order.  The delta system is solved by blocked
+// half of dv), the workgroups of one key head on one XCD; chunks run in order,
+// chunk c + 1 staged to LDS during phase 2 of chunk c (its v channels convolved
+// on the way, one token per lane).  The delta system is solved by blocked
 // forward substitution over 16-token blocks, delta_p = D_p (R_p - sum_{k<p}
 // A_pk delta_k) with D_p = (I + A_pp)^-1, on fp16 hi + lo operand pairs (mma3
 // below), which keeps the state within fp32-state tolerance.  Key waves 0..3
@@ -66,7 +71,7 @@ constexpr int RUN = 11 * PU;  // tokens one prep wave walks (swept: 33 beats 21,
 // ---- workspace (fp16 tensors, padded to whole chunks; tokens >= T are zero)
 struct Workspace {
   int64_t tp, nch;
-  int64_t off_qn, off_kn, off_vn, off_gb, bytes;
+  int64_t off_qn, off_kn, off_gb, bytes;
 };
 
 inline int64_t align256(int64_t v) { return (v + 255) & ~int64_t{255}; }
@@ -78,36 +83,41 @@ inline Workspace workspace_layout(int64_t batch, int64_t seq, int64_t hk, int64_
   const int64_t qk = batch * w.tp * hk * DK * 2;  // qn, kn: (B, Tp, Hk, 128)
   w.off_qn = 0;
   w.off_kn = align256(w.off_qn + qk);
-  w.off_vn = align256(w.off_kn + qk);                             // vn: (B, Tp, Hv, 128)
-  w.off_gb = align256(w.off_vn + batch * w.tp * hv * DV * 2);     // gb: (B, Hv, Tp, 2) fp32 (G, beta)
+  w.off_gb = align256(w.off_kn + qk);  // gb: (B, Hv, Tp, 2) fp32 (G, beta)
   w.bytes = align256(w.off_gb + batch * hv * w.tp * 2 * 4);
   return w;
 }
 
-// ---- LDS layout of chunk_kernel (bytes).  Per chunk c: Qs, Ks, Vs and the scalars are
-// staged first.  Phase 1 reads them; the key waves write Ahl, the query waves Adg, Tb and
-// Aqk[c % 2].  Phase 2: the key waves read Tb and Ahl and write Dt[c % 2] and St[(c + 1) % 2];
+// ---- LDS layout of chunk_kernel (bytes).  Phase 1 of chunk c reads Qs, Vs, Ks[c % 2] and
+// the scalars [c % 2]; the key waves write Ahl, the query waves Adg, Tb and Aqk[c % 2].
+// Phase 2: the key waves read Tb, Ahl and Ks[c % 2] and write Dt[c % 2] and St[(c + 1) % 2];
 // the query waves read Dt[(c - 1) % 2] and Aqk[(c - 1) % 2] (the output of chunk c - 1) and
-// St[c % 2].  No two regions alias; the double buffers let phase 2 read one chunk's tiles
-// while the other role writes the next chunk's.
+// St[c % 2].  Chunk c + 1 is staged at the start of phase 2: Qs and Vs are read in phase 1
+// only (the waves keep their operands in registers), so one copy of each suffices; Ks and
+// the scalars, still read in phase 2, take the other half of their double buffers.  No two
+// regions alias; the double buffers let phase 2 read one chunk's tiles while the other role
+// writes the next chunk's.
 constexpr int LDB = 20;                            // row stride (floats) of the 16x16 fp32 diagonal blocks
 constexpr int ST_BYTES = DVS * LD128 * 2;          // one St [dv][dk] (fp16 copy of the state)
 constexpr int AQK_BYTES = CH * LD64 * 2;           // one Aqk [i][l]
 constexpr int DT_BYTES = DVS * LD64 * 2;           // one delta^T [dv][tok]
+constexpr int KS_BYTES = CH * LD128 * 2;           // one Q or K tile
+constexpr int SC_BYTES = 3 * CH * 4;               // beta, G, gamma per token
 constexpr int OFF_QS = 0;                          // Qs [tok][dk]
-constexpr int OFF_KS = OFF_QS + CH * LD128 * 2;    // Ks [tok][dk]
-constexpr int OFF_VS = OFF_KS + CH * LD128 * 2;    // Vs [tok][dv] (this workgroup's half)
+constexpr int OFF_KS = OFF_QS + KS_BYTES;          // Ks [tok][dk] x 2
+constexpr int OFF_VS = OFF_KS + 2 * KS_BYTES;      // Vs [tok][dv] (this workgroup's half)
 constexpr int OFF_ST = OFF_VS + CH * LD64 * 2;     // St x 2
 constexpr int OFF_AQK = OFF_ST + 2 * ST_BYTES;     // Aqk x 2
 constexpr int OFF_ADG = OFF_AQK + 2 * AQK_BYTES;   // diagonal 16x16 blocks of A, fp32 [block][row][LDB]
 constexpr int OFF_TB = OFF_ADG + 4 * 16 * LDB * 4; // D_p = (I + A_pp)^-1, fp32 [block][row][LDB]
 constexpr int OFF_AHL = OFF_TB + 4 * 16 * LDB * 4; // 6 off-diagonal blocks of A as fp16 hi | lo, one 16-byte A operand per lane
 constexpr int OFF_DT = OFF_AHL + 6 * 64 * 16;      // delta^T x 2
-constexpr int OFF_SC = OFF_DT + 2 * DT_BYTES;      // beta, G, gamma per token
-constexpr int LDS_BYTES = OFF_SC + 3 * CH * 4;
+constexpr int OFF_SC = OFF_DT + 2 * DT_BYTES;      // scalars x 2
+constexpr int LDS_BYTES = OFF_SC + 2 * SC_BYTES;
 
 static_assert(OFF_ADG % 16 == 0 && OFF_DT % 16 == 0 && OFF_SC % 16 == 0, "16-byte aligned regions");
 static_assert(LDS_BYTES <= 160 * 1024, "LDS budget");
+static_assert(KS_BYTES % 16 == 0 && SC_BYTES % 16 == 0, "16-byte aligned buffers");
 
 struct PrepParams {
   const bf16_t* x;
@@ -117,7 +127,6 @@ struct PrepParams {
   float* conv_out;        // (B, C, 3) or null
   half_t* qn;
   half_t* kn;
-  half_t* vn;
   int64_t T, tp, nch;
   int B, Hk, Hv, C;
 };
@@ -137,7 +146,12 @@ struct GateParams {
 struct ChunkParams {
   const half_t* qn;
   const half_t* kn;
-  const half_t* vn;
+  const bf16_t* x;        // mixed_qkv: the v channels are convolved here
+  int64_t x_sb, x_st;
+  const float* conv_w;    // (C, 4)
+  const float* conv_in;   // (B, C, 3) or null
+  float* conv_out;        // (B, C, 3) or null
+  int C;
   const float* gb;
   const float* state_in;  // (B, Hv, dk, dv) or null
   float* state_out;       // (B, Hv, dk, dv) or null
@@ -166,11 +180,11 @@ __device__ __forceinline__ void store4h(half_t* dst, float a, float b, float c, 
 }
 
 // ---------------------------------------------------------------------------
-// 1. conv1d + SiLU (+ L2 norm) over a run of tokens.  Wave = (row b, group of
-// four consecutive heads in channel order, run of RUN tokens); the 16 lanes of
-// row r of the wave hold head 4 group + r, lane l its channels 8 (l % 16) .. + 7,
-// so one token of the group is one 1 KB read (rows of a group may be of
-// different kinds: q, k or v).  The L2 norm of a q or k head is a 16-lane row
+// 1. conv1d + SiLU + L2 norm of the q and k heads over a run of tokens.  Wave =
+// (row b, group of four consecutive heads in channel order, run of RUN tokens);
+// the 16 lanes of row r of the wave hold head 4 group + r, lane l its channels
+// 8 (l % 16) .. + 7, so one token of the group is one 1 KB read (rows of a group
+// may be q or k heads).  The L2 norm of a q or k head is a 16-lane row
 // reduction.  Tokens are taken three at a time, so the three-token conv history
 // rotates through registers without copies.  VEC16 loads a token's 8 channels
 // as one 16-byte read (rows 16-byte aligned), otherwise as four 4-byte reads.
@@ -179,7 +193,7 @@ __device__ __forceinline__ void gate_item(const GateParams& p, int64_t item, int
 template <bool VEC16>
 __global__ __launch_bounds__(256) void prep_kernel(PrepParams p, GateParams gp) {
   const int lane = threadIdx.x & 63;
-  const int NH = 2 * p.Hk + p.Hv;
+  const int NH = 2 * p.Hk;  // q and k heads (the v channels are convolved in chunk_kernel)
   const int ngroups = (NH + 3) / 4;
   const int64_t nruns = (p.tp + RUN - 1) / RUN;
   // the work item is wave-uniform, so its address arithmetic runs on the scalar unit
@@ -196,7 +210,7 @@ __global__ __launch_bounds__(256) void prep_kernel(PrepParams p, GateParams gp) 
   const int64_t b = item / nruns / ngroups;
   const int head = 4 * grp + (lane >> 4);
   const bool active = head < NH;  // the rows past the last head of a partial group idle
-  const int kind = head < p.Hk ? 0 : head < 2 * p.Hk ? 1 : 2;  // q, k, v
+  const int kind = head < p.Hk ? 0 : 1;  // q, k
   const int ch = (active ? head : 0) * 128 + 8 * (lane & 15);
   float w[8][KCONV];
 #pragma unroll
@@ -243,12 +257,9 @@ __global__ __launch_bounds__(256) void prep_kernel(PrepParams p, GateParams gp) 
     }
   }
   const float qscale = kind == 0 ? rsqrtf(static_cast<float>(DK)) : 1.f;
-  const bool norm = kind < 2;
-  half_t* dst = kind == 0 ? p.qn + ((b * p.tp) * p.Hk + head) * DK
-              : kind == 1 ? p.kn + ((b * p.tp) * p.Hk + head - p.Hk) * DK
-                          : p.vn + ((b * p.tp) * p.Hv + head - 2 * p.Hk) * DV;
+  half_t* dst = kind == 0 ? p.qn + ((b * p.tp) * p.Hk + head) * DK : p.kn + ((b * p.tp) * p.Hk + head - p.Hk) * DK;
   dst += 8 * (lane & 15);
-  const int64_t tstride = static_cast<int64_t>(kind == 2 ? p.Hv : p.Hk) * DK;
+  const int64_t tstride = static_cast<int64_t>(p.Hk) * DK;
 
   // raw inputs of the next two 3-token steps are in flight while a step is computed
   u32x4 cur[PU], nxt[PU];
@@ -281,7 +292,7 @@ __global__ __launch_bounds__(256) void prep_kernel(PrepParams p, GateParams gp) 
         ss += y[c] * y[c];
       }
       const float tot = row16_sum(ss);
-      const float r = norm ? rsqrtf(tot + 1e-6f) * qscale : 1.f;
+      const float r = rsqrtf(tot + 1e-6f) * qscale;
       if (active && t + jj < t1) {
         f16x8_v o;
 #pragma unroll
@@ -371,14 +382,15 @@ __device__ __forceinline__ void split4(const cfloat4& v, h4_v& hi, h4_v& lo) {
 }
 
 // One chunk's inputs, staged in registers while the previous chunk is computed:
-// 16-byte pieces of q and k rows, of this workgroup's half of the v rows, and
-// of (G, beta) (used by threads < 32).
+// 16-byte pieces of the fp16 q and k rows, the raw bf16 v of token (tid % 64) in this wave's
+// eight channels of the workgroup's v half, and (G, beta) (used by threads < 32).
 struct ChunkRegs {
   u32x4 q0, q1, k0, k1, v;
   cfloat4 gb;
 };
 
-__device__ __forceinline__ ChunkRegs load_chunk(const ChunkParams& p, int64_t b, int j, int qh, int half_id, int64_t ci, int tid) {
+template <bool VEC16>
+__device__ __forceinline__ ChunkRegs load_chunk(const ChunkParams& p, int64_t b, int j, int qh, int64_t vch, int64_t ci, int tid) {
   ChunkRegs r;
   const int64_t t0 = ci * CH;
   // 1024 pieces of 16 bytes per q/k tile: thread tid takes pieces tid and tid + 512
@@ -388,10 +400,29 @@ __device__ __forceinline__ ChunkRegs load_chunk(const ChunkParams& p, int64_t b,
   r.q1 = *reinterpret_cast<const u32x4*>(p.qn + row_off2);
   r.k0 = *reinterpret_cast<const u32x4*>(p.kn + row_off);
   r.k1 = *reinterpret_cast<const u32x4*>(p.kn + row_off2);
-  // 512 pieces per v half tile: token tid / 8, columns 8 (tid % 8) of this half
-  r.v = *reinterpret_cast<const u32x4*>(p.vn + ((b * p.tp + t0 + (tid >> 3)) * p.Hv + j) * DV + half_id * DVS + 8 * (tid & 7));
+  // tokens past the sequence read the last token instead (no branch); their v is masked to 0
+  // when staged and they only feed later masked tokens
+  const int64_t t = min64(t0 + (tid & 63), p.T - 1);
+  const bf16_t* src = p.x + b * p.x_sb + t * p.x_st + vch;
+  if constexpr (VEC16) {
+    r.v = *reinterpret_cast<const u32x4*>(src);
+  } else {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) r.v[e] = reinterpret_cast<const uint32_t*>(src)[e];
+  }
   r.gb = *reinterpret_cast<const cfloat4*>(p.gb + ((b * p.Hv + j) * p.tp + t0) * 2 + 4 * (tid & (CH / 2 - 1)));
   return r;
+}
+
+// channel c of the raw bf16 pairs of a token (c even: low half)
+__device__ __forceinline__ float raw_chan(const u32x4& r, int c) {
+  const uint32_t u = r[c >> 1];
+  return __uint_as_float((c & 1) ? (u & 0xffff0000u) : (u << 16));
+}
+
+// x of lane l - 1 to lane l, and `first` (wave-uniform) to lane 0 (DPP wave_shr:1)
+__device__ __forceinline__ float from_prev_lane(float x, float first) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(__builtin_bit_cast(int, first), __builtin_bit_cast(int, x), 0x138, 0xf, 0xf, false));
 }
 
 // acc += ah bh + ah bl + al bh for 16x16 blocks held as fp16 hi + lo pairs in the
@@ -488,14 +519,18 @@ __device__ __forceinline__ f16x8_v ktr_operand(const half_t* Ks, int row_g, int 
   return __builtin_bit_cast(f16x8_v, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
 }
 
-// One chunk's tiles from the registers they were loaded into to LDS, and the next chunk's
-// loads issued; ends with the barrier after which the tiles may be read.
-__device__ __forceinline__ void stage_chunk(const ChunkParams& p, unsigned char* smem, ChunkRegs& nx, int64_t b, int j, int qh,
-                                            int half_id, int64_t ci, int tid) {
+// Chunk ci from the registers it was loaded into to LDS: the q and k tiles (Ks and the scalars
+// into their ci % 2 copies), and this wave's eight v channels convolved (conv1d + SiLU,
+// src/reference_ops.py:245-258) with one token per lane -- the three earlier tokens of a lane
+// come from the lanes below it, for lanes 0..2 from `hist` (the raw inputs of the previous
+// chunk's last three tokens, or the initial conv state), which is then advanced.  Tokens past
+// the sequence get zero v.
+__device__ __forceinline__ void stage_chunk(const ChunkParams& p, unsigned char* smem, const ChunkRegs& nx, int64_t ci, int tid, int wave,
+                                            const float* cw, float (&hist)[3][8]) {
   half_t* Qs = reinterpret_cast<half_t*>(smem + OFF_QS);
-  half_t* Ks = reinterpret_cast<half_t*>(smem + OFF_KS);
+  half_t* Ks = reinterpret_cast<half_t*>(smem + OFF_KS + (ci & 1) * KS_BYTES);
   half_t* Vs = reinterpret_cast<half_t*>(smem + OFF_VS);
-  float* s_beta = reinterpret_cast<float*>(smem + OFF_SC);
+  float* s_beta = reinterpret_cast<float*>(smem + OFF_SC + (ci & 1) * SC_BYTES);
   float* s_G = s_beta + CH;
   float* s_gam = s_G + CH;
   const int c0 = tid, c1 = tid + NT;
@@ -503,7 +538,6 @@ __device__ __forceinline__ void stage_chunk(const ChunkParams& p, unsigned char*
   *reinterpret_cast<u32x4*>(Qs + (c1 >> 4) * LD128 + 8 * (c1 & 15)) = nx.q1;
   *reinterpret_cast<u32x4*>(Ks + (c0 >> 4) * LD128 + 8 * (c0 & 15)) = nx.k0;
   *reinterpret_cast<u32x4*>(Ks + (c1 >> 4) * LD128 + 8 * (c1 & 15)) = nx.k1;
-  *reinterpret_cast<u32x4*>(Vs + (tid >> 3) * LD64 + 8 * (tid & 7)) = nx.v;
   if (tid < CH / 2) {
     s_G[2 * tid] = nx.gb.x;
     s_beta[2 * tid] = nx.gb.y;
@@ -512,9 +546,48 @@ __device__ __forceinline__ void stage_chunk(const ChunkParams& p, unsigned char*
     s_gam[2 * tid] = __expf(nx.gb.x);
     s_gam[2 * tid + 1] = __expf(nx.gb.z);
   }
-  // (the last chunk reloads itself rather than branching, so nx stays in registers)
-  nx = load_chunk(p, b, j, qh, half_id, min(ci + 1, p.nch - 1), tid);
-  lds_barrier();
+  const int lane = tid & 63;
+  // tokens past the sequence: v = 0 (a multiply, not a branch, so no wait sits inside a branch)
+  const float live = ci * CH + lane < p.T ? 1.f : 0.f;
+  float4 w4[8];  // the taps of the eight channels (wave-uniform: scalar loads, one wait)
+#pragma unroll
+  for (int c = 0; c < 8; ++c) w4[c] = *reinterpret_cast<const float4*>(cw + 4 * c);
+  f16x8_v o;
+#pragma unroll
+  for (int c = 0; c < 8; ++c) {
+    const float x0 = raw_chan(nx.v, c);
+    const float x1 = from_prev_lane(x0, hist[2][c]);
+    const float x2 = from_prev_lane(x1, hist[1][c]);
+    const float x3 = from_prev_lane(x2, hist[0][c]);
+    const float a = w4[c].x * x3 + w4[c].y * x2 + w4[c].z * x1 + w4[c].w * x0;
+    o[c] = static_cast<half_t>(silu_ref(a) * live);
+#pragma unroll
+    for (int s = 0; s < 3; ++s) hist[s][c] = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, x0), CH - 3 + s));
+  }
+  *reinterpret_cast<f16x8_v*>(Vs + lane * LD64 + 8 * wave) = o;
+}
+
+// Workgroup -> (batch row, value head, dv half).  The 2 Hv / Hk workgroups that read one key
+// head's q and k tiles get block indices equal mod 8, so they run on one XCD and share its L2
+// (workgroups are dispatched to the XCDs round robin), when the key-head count allows it.
+__device__ __forceinline__ void chunk_item(const ChunkParams& p, int& b, int& j, int& qh, int& half_id) {
+  const int per = p.Hv / p.Hk;
+  const int members = 2 * per;
+  const int groups = static_cast<int>(gridDim.x) / members;
+  const int bid = static_cast<int>(blockIdx.x);
+  int g, r;
+  if (groups % 8 == 0) {
+    const int s = bid >> 3;
+    g = (bid & 7) + 8 * (s / members);
+    r = s % members;
+  } else {
+    g = bid / members;
+    r = bid % members;
+  }
+  b = g / p.Hk;
+  qh = g % p.Hk;
+  j = qh * per + (r >> 1);
+  half_id = r & 1;
 }
 
 // The workgroup's waves take two roles, each running its own chunk loop with the same
@@ -523,29 +596,37 @@ __device__ __forceinline__ void stage_chunk(const ChunkParams& p, unsigned char*
 //    substitution chain for dv tile v, the off-diagonal blocks of A, the state update;
 //  query waves 4..7 (v = wave - 4): the diagonal block A_vv and its inverse, all of Q,
 //    gamma Q S0, Aqk, and the output tiles of dv tile v.
+template <bool VEC16>
 __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(2, 2))) void chunk_kernel(ChunkParams p) {
   extern __shared__ __align__(16) unsigned char smem[];
-  half_t* Qs = reinterpret_cast<half_t*>(smem + OFF_QS);
-  half_t* Ks = reinterpret_cast<half_t*>(smem + OFF_KS);
+  const half_t* Qs = reinterpret_cast<const half_t*>(smem + OFF_QS);
   float* Adg = reinterpret_cast<float*>(smem + OFF_ADG);
   float* Tb = reinterpret_cast<float*>(smem + OFF_TB);
   unsigned char* Ahl = smem + OFF_AHL;
   half_t* Dt = reinterpret_cast<half_t*>(smem + OFF_DT);
-  half_t* Vs = reinterpret_cast<half_t*>(smem + OFF_VS);
+  const half_t* Vs = reinterpret_cast<const half_t*>(smem + OFF_VS);
   half_t* St = reinterpret_cast<half_t*>(smem + OFF_ST);
   half_t* Aqk = reinterpret_cast<half_t*>(smem + OFF_AQK);
-  float* s_beta = reinterpret_cast<float*>(smem + OFF_SC);
-  float* s_G = s_beta + CH;
-  float* s_gam = s_G + CH;
+  // K tile and per-token scalars of chunk ci (double-buffered: phase 2 of chunk ci stages ci + 1)
+  auto ks_of = [&](int64_t ci) { return reinterpret_cast<const half_t*>(smem + OFF_KS + (ci & 1) * KS_BYTES); };
+  auto sc_of = [&](int64_t ci) { return reinterpret_cast<const float*>(smem + OFF_SC + (ci & 1) * SC_BYTES); };
 
   const int tid = threadIdx.x;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const bool kwave = wave < 4;
   const int v = wave & 3;  // the dv tile (16 columns) a wave of either role owns
-  const int half_id = blockIdx.x & 1;
-  const int j = (blockIdx.x >> 1) % p.Hv;      // value head
-  const int64_t b = (blockIdx.x >> 1) / p.Hv;  // batch row
-  const int qh = j / (p.Hv / p.Hk);            // key head of this value head
+  int bi, j, qh, half_id;
+  chunk_item(p, bi, j, qh, half_id);
+  const int64_t b = bi;
+  // this wave's eight v channels (of the workgroup's 64) in mixed_qkv, their conv weights and the
+  // raw inputs of the three tokens before the chunk being staged
+  const int64_t vch = 2 * static_cast<int64_t>(p.Hk) * DK + static_cast<int64_t>(j) * DV + half_id * DVS + 8 * wave;
+  const float* cw = p.conv_w + vch * KCONV;
+  float hist[3][8];
+#pragma unroll
+  for (int s3 = 0; s3 < 3; ++s3)
+#pragma unroll
+    for (int c = 0; c < 8; ++c) hist[s3][c] = p.conv_in == nullptr ? 0.f : p.conv_in[(b * p.C + vch + c) * (KCONV - 1) + s3];
 
   // Aqk tiles above the diagonal are zero for every chunk (both buffers)
   if (tid < 6 * 64) {
@@ -556,7 +637,20 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(2, 2))) void
 #pragma unroll
     for (int u = 0; u < 2; ++u) store4h(Aqk + u * (AQK_BYTES / 2) + (16 * ti + lc) * LD64 + 16 * tl + 4 * lq, 0.f, 0.f, 0.f, 0.f);
   }
-  ChunkRegs nx = load_chunk(p, b, j, qh, half_id, 0, tid);
+  ChunkRegs nx = load_chunk<VEC16>(p, b, j, qh, vch, 0, tid);
+  stage_chunk(p, smem, nx, 0, tid, wave, cw, hist);
+  nx = load_chunk<VEC16>(p, b, j, qh, vch, min64(1, p.nch - 1), tid);
+  // (each role passes one barrier after its own set-up: the key waves' first St copy must be
+  // visible to the query waves' phase 1 of chunk 0, as the staged chunk 0 must be to both)
+  // chunk ci + 1 is staged in phase 2 of chunk ci (the query waves at its start, the key waves
+  // at its end, so the two waves of a SIMD do not run the VALU-heavy v conv at the same time);
+  // the loads of ci + 2 follow.
+  auto stage_next = [&](int64_t ci) {
+    if (ci + 1 < p.nch) {
+      stage_chunk(p, smem, nx, ci + 1, tid, wave, cw, hist);
+      nx = load_chunk<VEC16>(p, b, j, qh, vch, min64(ci + 2, p.nch - 1), tid);
+    }
+  };
 
   if (kwave) {
     // state columns dv = 16 v + lc as eight 16x16 tiles: S[d][r] = S[dk_of(d, 4 lq + r)][16 v + lc]
@@ -571,6 +665,7 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(2, 2))) void
         store4h(St + (16 * v + lc) * LD128 + dk_of(d, 4 * lq), S[d][0], S[d][1], S[d][2], S[d][3]);
       }
     }
+    lds_barrier();
     for (int64_t ci = 0; ci < p.nch; ++ci) {
       // The lane index is re-derived opaquely each chunk, so the per-lane LDS addresses of the
       // loop body are recomputed in it rather than hoisted out and held in VGPRs across it.
@@ -578,7 +673,10 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(2, 2))) void
       asm volatile("" : "+v"(lane));
       const int lq = lane >> 4;
       const int lc = lane & 15;
-      stage_chunk(p, smem, nx, b, j, qh, half_id, ci, tid);
+      const half_t* Ks = ks_of(ci);
+      const float* s_beta = sc_of(ci);
+      const float* s_G = s_beta + CH;
+      const float* s_gam = s_G + CH;
 
       // ---------------- phase 1 (key wave): K (all 64 tokens) into registers; R = diag(beta)
       // (V - diag(gamma) K S0) for dv tile v, with S0 from this wave's registers, kept for its
@@ -706,6 +804,7 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(2, 2))) void
 #pragma unroll
       for (int d = 0; d < 8; ++d)
         store4h(St + ((ci + 1) & 1) * (ST_BYTES / 2) + (16 * v + lc) * LD128 + dk_of(d, 4 * lq), S[d][0], S[d][1], S[d][2], S[d][3]);
+      stage_next(ci);
       lds_barrier();
     }
     if (p.state_out != nullptr) {
@@ -751,12 +850,16 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(2, 2))) void
         }
       }
     };
+    lds_barrier();
     for (int64_t ci = 0; ci < p.nch; ++ci) {
       int lane = tid & 63;
       asm volatile("" : "+v"(lane));
       const int lq = lane >> 4;
       const int lc = lane & 15;
-      stage_chunk(p, smem, nx, b, j, qh, half_id, ci, tid);
+      const half_t* Ks = ks_of(ci);
+      const float* s_beta = sc_of(ci);
+      const float* s_G = s_beta + CH;
+      const float* s_gam = s_G + CH;
 
       // ---------------- phase 1 (query wave): the diagonal block A_vv and D_v = (I + A_vv)^-1
       // (to Tb); Q (all 64 tokens) into registers and gamma * (S0^T Q^T) for the output tiles
@@ -804,6 +907,7 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(2, 2))) void
 #pragma unroll
       for (int t = 0; t < 4; ++t) On[t] *= s_gam[16 * t + lc];
       lds_barrier();
+      stage_next(ci);
 
       // ---------------- phase 2 (query wave), alongside the chains: the output of chunk c - 1,
       // then the lower tiles (i, v), v <= i <= v + 2, and for v = 3 also (3, 0), of
@@ -851,6 +955,22 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(2, 2))) void
     {
       const int lane = tid & 63;
       finish_chunk(p.nch - 1, lane >> 4, lane & 15);
+    }
+  }
+  // the conv state of this wave's v channels: the raw inputs of the last K - 1 tokens
+  if (p.conv_out != nullptr) {
+    const int lane = tid & 63;
+    if (lane < KCONV - 1) {
+      const int64_t t = p.T - (KCONV - 1) + lane;
+#pragma unroll
+      for (int c = 0; c < 8; ++c) {
+        float val = 0.f;
+        if (t >= 0)
+          val = bf16_to_f32(p.x[b * p.x_sb + t * p.x_st + vch + c]);
+        else if (p.conv_in != nullptr)
+          val = p.conv_in[(b * p.C + vch + c) * (KCONV - 1) + (KCONV - 1) + t];
+        p.conv_out[(b * p.C + vch + c) * (KCONV - 1) + lane] = val;
+      }
     }
   }
 }
@@ -904,7 +1024,6 @@ extern "C" int qa_chunk_gated_delta_rule(const void* mixed_qkv, int32_t x_dtype,
   pp.conv_out = conv_state_out;
   pp.qn = reinterpret_cast<half_t*>(wsb + ws.off_qn);
   pp.kn = reinterpret_cast<half_t*>(wsb + ws.off_kn);
-  pp.vn = reinterpret_cast<half_t*>(wsb + ws.off_vn);
   pp.T = seq;
   pp.tp = ws.tp;
   pp.nch = ws.nch;
@@ -912,7 +1031,7 @@ extern "C" int qa_chunk_gated_delta_rule(const void* mixed_qkv, int32_t x_dtype,
   pp.Hk = key_heads;
   pp.Hv = value_heads;
   pp.C = C;
-  const int64_t prep_waves = batch * ((2 * key_heads + value_heads + 3) / 4) * ((ws.tp + RUN - 1) / RUN);
+  const int64_t prep_waves = batch * ((2 * key_heads + 3) / 4) * ((ws.tp + RUN - 1) / RUN);
   GateParams gp{};
   gp.a = a;
   gp.bb = b;
@@ -944,7 +1063,13 @@ extern "C" int qa_chunk_gated_delta_rule(const void* mixed_qkv, int32_t x_dtype,
   ChunkParams p{};
   p.qn = pp.qn;
   p.kn = pp.kn;
-  p.vn = pp.vn;
+  p.x = pp.x;
+  p.x_sb = x_stride_b;
+  p.x_st = x_stride_t;
+  p.conv_w = conv_weight;
+  p.conv_in = conv_state_in;
+  p.conv_out = conv_state_out;
+  p.C = C;
   p.gb = gp.gb;
   p.state_in = initial_state;
   p.state_out = final_state;
@@ -959,13 +1084,19 @@ extern "C" int qa_chunk_gated_delta_rule(const void* mixed_qkv, int32_t x_dtype,
   p.Hv = value_heads;
   static bool attr_set = false;
   if (!attr_set) {
-    hipError_t err = hipFuncSetAttribute(reinterpret_cast<const void*>(&chunk_kernel), hipFuncAttributeMaxDynamicSharedMemorySize, LDS_BYTES);
+    hipError_t err = hipFuncSetAttribute(reinterpret_cast<const void*>(&chunk_kernel<true>), hipFuncAttributeMaxDynamicSharedMemorySize, LDS_BYTES);
+    if (err == hipSuccess)
+      err = hipFuncSetAttribute(reinterpret_cast<const void*>(&chunk_kernel<false>), hipFuncAttributeMaxDynamicSharedMemorySize, LDS_BYTES);
     if (err != hipSuccess) return fail("chunk_gated_delta_rule: cannot reserve %d bytes of LDS: %s", LDS_BYTES, hipGetErrorString(err));
     attr_set = true;
   }
   {
     KernelTimer timer_("chunk_gated_delta", stream);
-    hipLaunchKernelGGL(chunk_kernel, dim3(static_cast<unsigned>(batch * value_heads * 2)), dim3(NT), LDS_BYTES, stream, p);
+    const dim3 grid(static_cast<unsigned>(batch * value_heads * 2));
+    if (vec16)
+      hipLaunchKernelGGL(chunk_kernel<true>, grid, dim3(NT), LDS_BYTES, stream, p);
+    else
+      hipLaunchKernelGGL(chunk_kernel<false>, grid, dim3(NT), LDS_BYTES, stream, p);
   }
   return check_launch("chunk_gated_delta_rule");
 }
