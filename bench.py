@@ -121,32 +121,37 @@ def time_decode(w, steps: int, warmup: int):
 
 
 def time_serving_step(w, steps: int, warmup: int) -> dict:
-    """Config 2 as a serving decode step: device block reservation (one new token per row), the
-    new token's K/V appended, then the batched attention -- eager, and replayed from one captured
-    HIP graph.  Appends land past the cached lengths (and in free blocks), so the primary
-    measurement's cache is not disturbed.  Returns ms per step for both and per-kernel times."""
+    """Config 2 as a serving decode step through the runtime's device-table path
+    (``attention_runtime.full_attention_decode_device`` on ``decode_state.DeviceBatchPageTables``):
+    one block reservation for the step (one new token per row), the new token's K/V appended,
+    then the batched attention -- eager, and replayed from one captured HIP graph.  Appends land
+    past the cached lengths (and in free blocks), so the primary measurement's cache is not
+    disturbed.  Returns ms per step for both and per-kernel times."""
     import torch
 
-    import hip_ops
-    from decode_state import DeviceBlockAllocator
+    import attention_runtime as ar
+    from decode_state import DeviceBatchPageTables, SharedKVBlockPool
 
     batch, bs = w["tables"].shape[0], w["bs"]
     extra = 16  # table columns for up to 256 new tokens per row
-    tables = torch.full((batch, w["tables"].shape[1] + extra), -1, dtype=torch.int32, device=w["tables"].device)
-    tables[:, : w["tables"].shape[1]] = w["tables"]
-    used = set(int(v) for v in w["tables_cpu"][w["tables_cpu"] >= 0].tolist())
-    alloc = DeviceBlockAllocator(w["pool_blocks"], device=tables.device, free_blocks=[b for b in range(w["pool_blocks"]) if b not in used])
-    lens = w["lens"].clone()
-    pos = torch.zeros(batch, dtype=torch.int64, device=tables.device)
-    gen = torch.Generator(device=tables.device).manual_seed(5)
     kv_heads, dim = w["key_pool"].shape[1], w["key_pool"].shape[3]
-    k_new = torch.randn((batch, kv_heads, 1, dim), generator=gen, device=tables.device, dtype=torch.bfloat16)
-    v_new = torch.randn((batch, kv_heads, 1, dim), generator=gen, device=tables.device, dtype=torch.bfloat16)
+    heads = w["query"].shape[1]
+    used = set(int(v) for v in w["tables_cpu"][w["tables_cpu"] >= 0].tolist())
+    pool = SharedKVBlockPool.from_tensors(w["key_pool"], w["value_pool"], free_blocks=[b for b in range(w["pool_blocks"]) if b not in used])
+    tables = DeviceBatchPageTables(pool, rows=batch, max_blocks=w["tables"].shape[1] + extra)
+    tables.adopt_rows(w["tables"], w["lens"])
+    config = ar.parse_attention_config({"text_config": {
+        "num_attention_heads": heads, "num_key_value_heads": kv_heads, "head_dim": dim, "attn_output_gate": False,
+        "native_paged_attention": True, "linear_num_key_heads": 16, "linear_num_value_heads": 32, "linear_key_head_dim": 128,
+        "linear_value_head_dim": 128, "linear_conv_kernel_dim": 4}})
+    runtime = ar.HotPathRuntime()
+    gen = torch.Generator(device=w["tables"].device).manual_seed(5)
+    k_new = torch.randn((batch, kv_heads, 1, dim), generator=gen, device=w["tables"].device, dtype=torch.bfloat16)
+    v_new = torch.randn((batch, kv_heads, 1, dim), generator=gen, device=w["tables"].device, dtype=torch.bfloat16)
 
     def step():
-        alloc.reserve(tables, lens, bs, counts=1, positions=pos)
-        hip_ops.paged_kv_append(k_new, v_new, w["key_pool"], w["value_pool"], tables, pos, bs)
-        return hip_ops.paged_attention_decode_batched(w["query"], tables, w["key_pool"], w["value_pool"], lens, bs)
+        tables.reserve_step()
+        return ar.full_attention_decode_device(w["query"], None, k_new, v_new, pool.key_blocks, pool.value_blocks, tables, config, runtime)
 
     eager_ms, kern = _timed(step, steps, warmup, ("kv_reserve", "decode_partial_mfma", "decode_combine"), timing_repeats=3)
     side = torch.cuda.Stream()
@@ -167,10 +172,46 @@ def time_serving_step(w, steps: int, warmup: int) -> dict:
         graph.replay()
     end.record()
     torch.cuda.synchronize()
-    alloc.check()
+    tables.check()
+    if runtime.paged_attention_stats.native_hits == 0:
+        raise RuntimeError("serving step: the device decode path did not run")
     graph_ms = start.elapsed_time(end) / steps
-    tokens_added = int((lens - w["lens"]).max().item())
+    tokens_added = int((tables.sequence_lengths - w["lens"]).max().item())
     return {"eager_ms": eager_ms, "graph_ms": graph_ms, "kernels": kern, "tokens_added": tokens_added}
+
+
+def reference_layout_workload(w: dict, device: str, *, seed: int = 11) -> dict:
+    """Config 2's contexts in the reference engine's own cache layout: one pool per request,
+    ``(1, heads, P_b, bs, D)`` fp32 with the KV heads repeated to the 16 query heads
+    (``src/decode_state.py:37-44``, ``src/tp_runtime.py:518-525``), blocks shuffled inside each
+    pool, handed to ``paged_attention_decode_batched`` as the reference's list of pools
+    (``src/tp_runtime.py:626-643``).  ~31 GB of fp32 K/V."""
+    import torch
+
+    gen = torch.Generator().manual_seed(seed)
+    dgen = torch.Generator(device=device).manual_seed(seed)
+    heads, dim, bs = w["query"].shape[1], w["query"].shape[3], w["bs"]
+    ctx = [int(c) for c in w["ctx"]]
+    need = [(c + bs - 1) // bs for c in ctx]
+    tables = torch.full((len(ctx), max(need)), -1, dtype=torch.int64)
+    keys, values = [], []
+    for b, n in enumerate(need):
+        tables[b, :n] = torch.randperm(n, generator=gen)
+        keys.append(torch.randn((1, heads, n, bs, dim), generator=dgen, device=device))
+        values.append(torch.randn((1, heads, n, bs, dim), generator=dgen, device=device))
+    query = w["query"].float()
+    layout_bytes = sum(ctx) * heads * dim * 4 * 2 + 2 * len(ctx) * heads * dim * 4 + sum(need) * 8
+    return {"query": query, "tables": tables.to(device), "keys": keys, "values": values, "lens": w["lens"].long(), "bs": bs,
+            "layout_bytes": layout_bytes, "gqa_bytes": w["algo_bytes"]}
+
+
+def time_reference_layout(rw: dict, steps: int, warmup: int):
+    import hip_ops
+
+    def step():
+        return hip_ops.paged_attention_decode_batched(rw["query"], rw["tables"], rw["keys"], rw["values"], rw["lens"], rw["bs"])
+
+    return _timed(step, steps, warmup, ("decode_partial_generic", "decode_combine"))
 
 
 def _timed(step, steps: int, warmup: int, labels: tuple[str, ...], warm_ms: float = 0.0, timing_repeats: int = 5):
@@ -601,6 +642,7 @@ def main() -> int:
     parser.add_argument("--no-output-norm", action="store_true", help="skip the linear-attention output stage measurement (config 4 shapes)")
     parser.add_argument("--no-fp8-linear", action="store_true", help="skip the fp8 block-scaled projection measurement (config 5 batch)")
     parser.add_argument("--no-serving", action="store_true", help="skip the graph-replayed serving decode step (config 2)")
+    parser.add_argument("--no-reference-layout", action="store_true", help="skip the decode over the reference's per-request fp32 pools")
     parser.add_argument("--copy-probe-mib", type=int, default=0,
                         help="first run one plain device copy of this many MiB (reference point for HBM byte counters)")
     parser.add_argument("--cpu-budget", type=float, default=12.0)
@@ -680,7 +722,7 @@ def main() -> int:
         _log(f"bench: serving decode step (reserve + append + attention) eager {sv['eager_ms']:.4f} ms, graph replay {sv['graph_ms']:.4f} ms = "
              f"{sv_gbs:.1f} GB/s ({sv_gbs / HBM_PEAK_GBS:.1%} of HBM peak)")
         record["secondary_serving_step"] = {
-            "metric": "graph-replayed decode step (device block reservation + K/V append + paged attention) HBM GB/s",
+            "metric": "graph-replayed decode step through the runtime's device page tables (block reservation + K/V append + paged attention) HBM GB/s",
             "value": round(sv_gbs, 2),
             "unit": "GB/s",
             "ms_per_step": round(sv["graph_ms"], 5),
@@ -691,6 +733,28 @@ def main() -> int:
                          "traffic": None, "algo_bytes_per_step": sv_bytes, "kernel": "kv_reserve_kernel + kv_append_kernel + decode_partial_mfma + decode_combine",
                          "kernels": sv["kernels"]},
         }
+    if not args.no_reference_layout:
+        _log("bench: building the reference-layout workload (per-request fp32 pools, repeated heads)")
+        rw = reference_layout_workload(w, device)
+        rms, rkern = time_reference_layout(rw, max(3, args.steps // 4), 1)
+        r_gbs = rw["layout_bytes"] / (rms * 1e-3) / 1e9
+        r_eq = rw["gqa_bytes"] / (rms * 1e-3) / 1e9
+        _log(f"bench: reference layout decode {rms:.3f} ms/step, {r_gbs:.1f} GB/s of its own fp32 bytes ({r_gbs / HBM_PEAK_GBS:.1%} of HBM peak); "
+             f"{r_eq:.1f} GB/s GQA-bf16 equivalent")
+        record["secondary_reference_layout"] = {
+            "metric": "paged decode over the reference's per-request fp32 repeated-head pools, HBM GB/s of that layout",
+            "value": round(r_gbs, 2),
+            "unit": "GB/s",
+            "ms_per_step": round(rms, 4),
+            "gqa_bf16_equivalent_gbs": round(r_eq, 2),
+            "config": {"workload": "config 2 contexts (64 rows, U[1024, 32768] seed 0) in the reference engine's layout: one (1, 16, P_b, 16, 256) fp32 "
+                                   "pool per request, KV heads repeated 8x, shuffled blocks, list of pools", "layout_bytes": rw["layout_bytes"]},
+            "roofline": {"bound": "hbm", "achieved": round(r_gbs, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(r_gbs / HBM_PEAK_GBS, 4),
+                         "traffic": None, "algo_bytes_per_step": rw["layout_bytes"], "kernel": "qa::decode_partial_generic<float, float, 1, 4> + decode_combine",
+                         "kernels": rkern},
+        }
+        del rw
+        torch.cuda.empty_cache()
     del w
     torch.cuda.empty_cache()
     cpu_delta = None

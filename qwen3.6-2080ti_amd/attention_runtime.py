@@ -34,7 +34,7 @@ import contextlib
 from dataclasses import dataclass, field
 from typing import Any, Iterator, Sequence
 
-from decode_state import FullAttentionCache, LinearStatePool, batch_page_tables
+from decode_state import DeviceBatchPageTables, FullAttentionCache, LinearStatePool, batch_page_tables
 
 # --------------------------------------------------------------------------- config
 
@@ -292,6 +292,46 @@ def full_attention_paged_batch(query: Any, gate: Any | None, caches: Sequence[Fu
     except RuntimeError:
         # a kernel-side rejection (shape, dtype, workspace): the caller's dense path runs,
         # as src/tp_runtime.py:591 and :2537 do
+        record_native_paged_dispatch(runtime, "no_kernel", native=False)
+        return None
+    record_native_paged_dispatch(runtime, reason, native=True)
+    return heads if gate is None else _gate_heads(heads, gate)
+
+
+def full_attention_decode_device(
+    query: Any, gate: Any | None, key: Any, value: Any, key_blocks: Any, value_blocks: Any, tables: DeviceBatchPageTables,
+    config: AttentionConfig, runtime: HotPathRuntime, *, no_alloc: bool = False,
+) -> Any | None:
+    """One decode token of a full-attention layer for every row of a running batch, on
+    device-resident page tables: the batched native branch of
+    ``_tp_full_attention_batch_paged_or_dense`` (``src/tp_runtime.py:2498-2555``) without its
+    per-step host work (the table rebuild and copy of ``batch_page_tables``,
+    ``src/decode_state.py:545-603``).
+
+    ``tables.reserve_step()`` must have run for this step (once for all layers sharing the
+    tables).  ``key``/``value`` ``(rows, H_kv, 1, D)`` are the step's post-rotary K/V; they go
+    to the reserved slots of this layer's shared pool ``key_blocks``/``value_blocks``
+    ``(P, H_kv, bs, D)``, then ``query`` ``(rows, H, 1, D)`` attends over each row's cache.
+    Rows without a request give zeros.  Same dispatch ladder and counters as the cache form;
+    ``None`` means the caller runs its dense path.  With ``no_alloc`` the attention runs on the
+    library's static scratch (``qa_paged_attention_decode_batched_noalloc``) instead of a
+    workspace.  Nothing here reads back to the host or copies host to device.
+    """
+    reason = paged_attention_fallback_reason(config, query, key_blocks, value_blocks, seq_len=int(query.shape[2]), batched=False)
+    if reason != "no_kernel":
+        record_native_paged_dispatch(runtime, reason, native=False)
+        return None
+    import hip_loader
+    import hip_ops
+
+    try:
+        with runtime.profile_scope("batch.full_attention.native_paged_device"):
+            tables.append(key, value, key_blocks, value_blocks)
+            decode = hip_ops.paged_attention_decode_batched_noalloc if no_alloc else hip_ops.paged_attention_decode_batched
+            heads = decode(query, tables.block_tables, key_blocks, value_blocks, tables.sequence_lengths, tables.block_size)
+    except hip_loader.NativeLibraryMissing:
+        raise
+    except RuntimeError:
         record_native_paged_dispatch(runtime, "no_kernel", native=False)
         return None
     record_native_paged_dispatch(runtime, reason, native=True)

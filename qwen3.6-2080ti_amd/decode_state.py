@@ -137,6 +137,22 @@ class SharedKVBlockPool:
         self.free_blocks: list[int] = list(range(num_blocks))
         self.allocator: DeviceBlockAllocator | None = None
 
+    @classmethod
+    def from_tensors(cls, key_blocks: Any, value_blocks: Any, *, free_blocks: Sequence[int] | None = None) -> "SharedKVBlockPool":
+        """A pool over existing ``(P, H_kv, bs, D)`` tensors (e.g. a cache restored from elsewhere);
+        ``free_blocks`` lists the ids not in use (all when omitted)."""
+        if key_blocks.dim() != 4 or value_blocks.shape != key_blocks.shape:
+            raise ValueError("pool tensors must be (num_blocks, kv_heads, block_size, head_dim) and alike")
+        pool = cls.__new__(cls)
+        pool.block_size = int(key_blocks.shape[2])
+        pool.kv_heads = int(key_blocks.shape[1])
+        pool.head_dim = int(key_blocks.shape[3])
+        pool.key_blocks = key_blocks
+        pool.value_blocks = value_blocks
+        pool.free_blocks = list(range(int(key_blocks.shape[0]))) if free_blocks is None else sorted(int(b) for b in free_blocks)
+        pool.allocator = None
+        return pool
+
     @property
     def block_count(self) -> int:
         return int(self.key_blocks.shape[0])
@@ -240,6 +256,110 @@ class DeviceBlockAllocator:
             raise ValueError("released block ids must be in range and not already free")
         self.free_list[: len(merged)] = torch.tensor(merged, dtype=torch.int32, device=self.device)
         self.free_state.copy_(torch.tensor([0, len(merged)], dtype=torch.int32))
+
+
+class DeviceBatchPageTables:
+    """Block tables and lengths of the rows of a running decode batch, kept on the device.
+
+    The reference rebuilds ``-1``-padded ``(B, max_blocks)`` tables on the host for every
+    full-attention layer of every step and copies them to the device (``batch_page_tables``,
+    ``src/decode_state.py:545-603``; its engine probe counts those rebuilds,
+    ``src/engine.py:489-516``).  Here a running batch keeps one ``(rows, max_blocks)`` int32
+    table, ``(rows,)`` int32 lengths and per-row step token counts on the device:
+    ``reserve_step`` grows every active row by its step count with one kernel (ids from the
+    pool's device free list, lowest first, rows in order: ``PagedKVBlockPool.allocate``'s
+    policy, ``:72-78``) and leaves the append positions in ``positions``; ``append`` writes a
+    layer's step K/V there.  The full-attention layers of a model grow their caches identically
+    (every layer appends the same tokens), so layers whose pools have the same block count share
+    one table and a step reserves once for all of them.  ``reserve_step``, ``append`` and the
+    decode neither read back to the host nor copy host to device, so a whole decode step can be
+    captured in a HIP graph; the host touches the tables only when a request joins
+    (``add_request``) or finishes (``release_request``).
+    """
+
+    def __init__(self, pool: SharedKVBlockPool, rows: int, max_blocks: int) -> None:
+        import torch
+
+        if rows <= 0 or max_blocks <= 0:
+            raise ValueError("rows and max_blocks must be positive")
+        self.pool = pool
+        self.block_size = pool.block_size
+        self.num_blocks = pool.block_count
+        self.allocator = pool.device_allocator()
+        device = pool.key_blocks.device
+        self.block_tables = torch.full((rows, max_blocks), -1, dtype=torch.int32, device=device)
+        self.sequence_lengths = torch.zeros(rows, dtype=torch.int32, device=device)
+        self.positions = torch.zeros(rows, dtype=torch.int32, device=device)
+        self.step_counts = torch.zeros(rows, dtype=torch.int32, device=device)
+        self.active = [False] * rows
+
+    @property
+    def rows(self) -> int:
+        return len(self.active)
+
+    def add_request(self, prompt_tokens: int = 0) -> int:
+        """Take the lowest free row for a new request; reserve its prompt's blocks (positions of
+        the row then hold 0, the first append position).  The row joins later steps with one
+        token each."""
+        import torch
+
+        if prompt_tokens < 0:
+            raise ValueError("prompt_tokens must be non-negative")
+        try:
+            row = self.active.index(False)
+        except ValueError:
+            raise RuntimeError("device page tables: every row holds a request") from None
+        self.active[row] = True
+        if prompt_tokens:
+            counts = torch.zeros_like(self.step_counts)
+            counts[row] = prompt_tokens
+            self.allocator.reserve(self.block_tables, self.sequence_lengths, self.block_size, counts=counts, positions=self.positions)
+            self.allocator.check()
+        self.step_counts[row] = 1
+        return row
+
+    def adopt_rows(self, block_tables: Any, lengths: Any) -> None:
+        """Take over requests whose blocks are already written: row ``r`` gets ``block_tables[r]``
+        (``-1`` padded) and ``lengths[r]`` tokens.  Their ids must not be in the pool's free list
+        (``SharedKVBlockPool.from_tensors(..., free_blocks=...)``)."""
+        import torch
+
+        rows, width = block_tables.shape
+        if rows > self.rows or width > self.block_tables.shape[1]:
+            raise ValueError("adopted tables do not fit the device tables")
+        self.block_tables[:rows].fill_(-1)
+        self.block_tables[:rows, :width] = block_tables.to(device=self.block_tables.device, dtype=torch.int32)
+        self.sequence_lengths[:rows] = lengths.to(device=self.block_tables.device, dtype=torch.int32)
+        self.step_counts[:rows] = 1
+        for r in range(rows):
+            self.active[r] = True
+
+    def reserve_step(self) -> None:
+        """Blocks for one step of every active row (device only; ``check`` reads the status)."""
+        self.allocator.reserve(self.block_tables, self.sequence_lengths, self.block_size, counts=self.step_counts, positions=self.positions)
+
+    def append(self, key: Any, value: Any, key_blocks: Any, value_blocks: Any, *, counts: Any = None) -> None:
+        """Write a layer's new K/V ``(rows, H_kv, S, D)`` at the reserved positions of its pool."""
+        import hip_ops
+
+        hip_ops.paged_kv_append(key, value, key_blocks, value_blocks, self.block_tables, self.positions, self.block_size,
+                                counts=self.step_counts if counts is None else counts)
+
+    def check(self) -> None:
+        self.allocator.check()
+
+    def release_request(self, row: int) -> list[int]:
+        """The request in ``row`` finished: its blocks return to the device free list (one read of
+        the row) and the row is emptied.  Returns the released block ids."""
+        if not self.active[row]:
+            raise ValueError(f"row {row} holds no request")
+        ids = [int(b) for b in self.block_tables[row].tolist() if b >= 0]
+        self.allocator.release(ids)
+        self.block_tables[row].fill_(-1)
+        self.sequence_lengths[row] = 0
+        self.step_counts[row] = 0
+        self.active[row] = False
+        return ids
 
 
 # --------------------------------------------------------------------------- records

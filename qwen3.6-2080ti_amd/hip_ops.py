@@ -251,6 +251,50 @@ def paged_attention_decode_batched(
     return out
 
 
+def paged_attention_decode_batched_noalloc(
+    query: torch.Tensor,
+    block_tables: torch.Tensor,
+    key_blocks: torch.Tensor,
+    value_blocks: torch.Tensor,
+    sequence_lengths: torch.Tensor,
+    block_size: int,
+    *,
+    scale: float | None = None,
+) -> torch.Tensor:
+    """``paged_attention_decode_batched`` on one shared ``(P, H_kv, bs, D)`` pool with the split-K
+    partials in the library's static per-device scratch (``qa_paged_attention_decode_batched_noalloc``):
+    the library allocates nothing; only the output is a new tensor.  Sizes whose partials exceed the
+    scratch raise ``RuntimeError``; calls that overlap on one device race."""
+    lib = L.load_library()
+    _require_cuda(query, "query")
+    device = query.device
+    for tensor, name in ((block_tables, "block_tables"), (sequence_lengths, "sequence_lengths"), (key_blocks, "key_blocks"),
+                         (value_blocks, "value_blocks")):
+        _require_cuda(tensor, name, device)
+    _float_dtype(query, "query")
+    _float_dtype(key_blocks, "key_blocks")
+    _index_dtype(block_tables, "block_tables")
+    _index_dtype(sequence_lengths, "sequence_lengths")
+    _require(query.dim() == 4 and query.shape[2] == 1, "query must have shape [batch, heads, 1, head_dim]")
+    _require(key_blocks.dim() == 4 and value_blocks.shape == key_blocks.shape, "shared pools must have shape [blocks, kv_heads, block_size, head_dim]")
+    batch, heads, _, head_dim = query.shape
+    _require(block_tables.dim() == 2 and block_tables.shape[0] == batch and block_tables.shape[1] > 0, "block_tables must have shape [batch, max_blocks]")
+    _require(sequence_lengths.dim() == 1 and sequence_lengths.shape[0] == batch, "sequence_lengths batch must match query")
+    _require(key_blocks.shape[2] == block_size, "KV block_size mismatch")
+    desc = _pool_descriptor(key_blocks, value_blocks, "shared")
+    _require(heads % desc.kv_heads == 0, "KV heads must divide query heads")
+    q = query.contiguous()
+    tables = block_tables.contiguous()
+    lens = sequence_lengths.contiguous()
+    out = torch.empty_like(q)
+    status = lib.qa_paged_attention_decode_batched_noalloc(
+        _ptr(q), _code(q), q.stride(0), q.stride(1), batch, heads, head_dim, ctypes.byref(desc), _ptr(tables), _code(tables),
+        tables.stride(0), tables.shape[1], _ptr(lens), _code(lens), int(block_size), float(scale or 0.0), _ptr(out), _stream(device),
+    )
+    L.check(lib, status, "paged_attention_decode_batched_noalloc")
+    return out
+
+
 def _per_request_descriptor(key_list: list[torch.Tensor], value_list: list[torch.Tensor], device: torch.device, keepalive: list[torch.Tensor]) -> L.PagedKV:
     """Pointer-array descriptor for contiguous per-request pools ``(1, heads, P_b, bs, D)``.
 

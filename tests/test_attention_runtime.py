@@ -162,3 +162,30 @@ def test_linear_native_ladder_counts_like_the_reference_on_cpu_tensors() -> None
     assert d["fallback_hidden_not_cuda"] == 3 and d["fallback_weight_not_cuda"] == 3 and d["fallback_scale_not_cuda"] == 2
     assert d["fallback_weight_dtype"] == 1 and d["fallback_missing_scale"] == 1 and d["fallback_disabled_cuda_kernel"] == 1
     assert d["fallback_scale_dtype"] == 1 and d["fallback_hidden_alignment"] == 1 and d["fallback_weight_alignment"] == 1
+
+
+def test_device_page_tables_row_bookkeeping_and_cpu_dispatch_reason() -> None:
+    """Rows of a DeviceBatchPageTables are taken lowest first and reused after release; on CPU
+    tensors the device decode entry reports reason "cpu" and returns None (the caller's dense path)."""
+    import torch
+
+    from decode_state import DeviceBatchPageTables, SharedKVBlockPool
+
+    pool = SharedKVBlockPool(8, kv_heads=2, head_dim=4, block_size=2, dtype=torch.float32)
+    tables = DeviceBatchPageTables(pool, rows=3, max_blocks=4)
+    assert pool.free_blocks == [] and tables.allocator.free_blocks() == list(range(8))
+    assert [tables.add_request(), tables.add_request()] == [0, 1]
+    assert tables.step_counts.tolist() == [1, 1, 0] and tables.active == [True, True, False]
+    assert tables.release_request(0) == []
+    assert tables.step_counts.tolist() == [0, 1, 0] and tables.add_request() == 0
+    with pytest.raises(ValueError, match="holds no request"):
+        tables.release_request(2)
+    config = ar.parse_attention_config({"text_config": {
+        "linear_num_key_heads": 1, "linear_num_value_heads": 1, "linear_key_head_dim": 4, "linear_value_head_dim": 4,
+        "linear_conv_kernel_dim": 4, "num_attention_heads": 2, "num_key_value_heads": 2, "head_dim": 4, "attn_output_gate": False,
+        "native_paged_attention": True}})
+    runtime = ar.HotPathRuntime()
+    q = torch.zeros(3, 2, 1, 4)
+    kv = torch.zeros(3, 2, 1, 4)
+    assert ar.full_attention_decode_device(q, None, kv, kv, pool.key_blocks, pool.value_blocks, tables, config, runtime) is None
+    assert runtime.paged_attention_stats.fallback_cpu == 1 and runtime.paged_attention_stats.native_hits == 0

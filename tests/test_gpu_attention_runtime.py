@@ -119,3 +119,117 @@ def test_recurrent_wrapper_matches_oracle_and_keeps_dtype() -> None:
     assert out.dtype == q.dtype and out.shape == (2, 6, 3, 8) and state.dtype == torch.float32
     torch.testing.assert_close(out.cpu(), ref_out, atol=2e-5, rtol=2e-5)
     torch.testing.assert_close(state.cpu(), ref_state, atol=2e-5, rtol=2e-5)
+
+
+def test_device_page_tables_running_batch_two_layers_matches_oracle_and_replays_as_a_graph() -> None:
+    """A running batch on device-resident page tables shared by two full-attention layers: prompts
+    admitted, decode steps (one reservation per step for both layers, the step's K/V appended, then
+    attention), a request released and a new one reusing its blocks and row, then the whole step
+    captured in a HIP graph (no-alloc attention) and replayed three times -- every step and every
+    replay against the oracle's dense attention over the tokens written so far (bf16, 2e-2)."""
+    import hip_ops
+    from decode_state import DeviceBatchPageTables
+
+    gen = torch.Generator().manual_seed(64)
+    heads, kv_heads, dim, bs, layers = 16, 2, 256, 16, 2
+    config = _enabled(heads, kv_heads, dim)
+    pools = [SharedKVBlockPool(40, kv_heads, dim, block_size=bs, device=DEV) for _ in range(layers)]
+    tables = DeviceBatchPageTables(pools[0], rows=4, max_blocks=12)
+    runtime = ar.HotPathRuntime()
+    total = 160
+    # dense K/V of every (layer, request) the test may write, in token order
+    dense = {}
+
+    def tokens(layer, req):
+        if (layer, req) not in dense:
+            dense[(layer, req)] = (torch.randn(1, kv_heads, total, dim, generator=gen).to(torch.bfloat16),
+                                   torch.randn(1, kv_heads, total, dim, generator=gen).to(torch.bfloat16))
+        return dense[(layer, req)]
+
+    length = {}
+    row_of = {}
+
+    def admit(req, prompt):
+        row = tables.add_request(prompt)
+        row_of[req] = row
+        length[req] = prompt
+        for layer, pool in enumerate(pools):
+            k, v = tokens(layer, req)
+            hip_ops.paged_kv_append(k[:, :, :prompt].to(DEV), v[:, :, :prompt].to(DEV), pool.key_blocks, pool.value_blocks,
+                                    tables.block_tables[row : row + 1], tables.positions[row : row + 1], bs)
+
+    def step_inputs(layer):
+        k_new = torch.zeros(tables.rows, kv_heads, 1, dim, dtype=torch.bfloat16)
+        v_new = torch.zeros_like(k_new)
+        for req, row in row_of.items():
+            k, v = tokens(layer, req)
+            k_new[row] = k[0, :, length[req] : length[req] + 1]
+            v_new[row] = v[0, :, length[req] : length[req] + 1]
+        return k_new.to(DEV), v_new.to(DEV)
+
+    def check(outs, q, gate, written):
+        for layer in range(layers):
+            for req, row in row_of.items():
+                k, v = tokens(layer, req)
+                n = written[req]
+                ref = oracle_attn.dense_attention(q[row : row + 1].cpu(), k[:, :, :n], v[:, :, :n], position_offset=n - 1, gate=gate[row : row + 1].cpu())
+                got = outs[layer][row : row + 1].cpu().float()
+                torch.testing.assert_close(got, ref.transpose(1, 2).reshape(1, 1, heads * dim).float(), atol=2e-2, rtol=2e-2)
+            free_rows = [r for r in range(tables.rows) if not tables.active[r]]
+            for r in free_rows:
+                assert torch.count_nonzero(outs[layer][r]) == 0
+
+    for req, prompt in enumerate([37, 5, 80]):
+        admit(req, prompt)
+    for step in range(3):
+        q = torch.randn(tables.rows, heads, 1, dim, generator=gen).to(torch.bfloat16).to(DEV)
+        gate = torch.randn(tables.rows, 1, heads * dim, generator=gen).to(torch.bfloat16).to(DEV)
+        tables.reserve_step()
+        outs = []
+        for layer, pool in enumerate(pools):
+            k_new, v_new = step_inputs(layer)
+            outs.append(ar.full_attention_decode_device(q, gate, k_new, v_new, pool.key_blocks, pool.value_blocks, tables, config, runtime))
+        tables.check()
+        for req in row_of:
+            length[req] += 1
+        check(outs, q, gate, length)
+        if step == 1:
+            released = tables.release_request(row_of.pop(1))
+            assert len(released) == 1
+            admit(3, 20)  # the freed row and the lowest free block ids
+            assert row_of[3] == 1 and int(tables.block_tables[1, 0]) == min(released + tables.allocator.free_blocks() + [int(tables.block_tables[1, 0])])
+    assert runtime.paged_attention_stats.native_hits == 3 * layers
+    # the whole step in a HIP graph: fixed inputs, each replay appends them at the next position
+    q = torch.randn(tables.rows, heads, 1, dim, generator=gen).to(torch.bfloat16).to(DEV)
+    gate = torch.randn(tables.rows, 1, heads * dim, generator=gen).to(torch.bfloat16).to(DEV)
+    fixed = [step_inputs(layer) for layer in range(layers)]
+    for layer in range(layers):  # the reference tokens of the replays: the same K/V at every new position
+        for req in row_of:
+            k, v = tokens(layer, req)
+            for r in range(3):
+                k[0, :, length[req] + r] = fixed[layer][0][row_of[req], :, 0].cpu()
+                v[0, :, length[req] + r] = fixed[layer][1][row_of[req], :, 0].cpu()
+
+    def step():
+        tables.reserve_step()
+        return [ar.full_attention_decode_device(q, gate, fixed[layer][0], fixed[layer][1], pool.key_blocks, pool.value_blocks, tables, config,
+                                                runtime, no_alloc=True) for layer, pool in enumerate(pools)]
+
+    # first-call set-up of the no-alloc path (its scratch address) outside the capture: a read-only call
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        hip_ops.paged_attention_decode_batched_noalloc(q, tables.block_tables, pools[0].key_blocks, pools[0].value_blocks, tables.sequence_lengths, bs)
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        graph_outs = step()
+    print("graph captured", flush=True)
+    for r in range(3):
+        graph.replay()
+        torch.cuda.synchronize()
+        tables.check()
+        for req in row_of:
+            length[req] += 1
+        check(graph_outs, q, gate, length)
