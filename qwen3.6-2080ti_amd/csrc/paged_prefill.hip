@@ -24,8 +24,9 @@
 // interleaved with the softmax of tile t, then (phase B) the PV products of tile t;
 // LDS operand reads run kAhead products ahead and a scheduling fence after each step
 // keeps that order.  Each wave waits for its own copies before the one barrier per
-// tile.  The row's block table is read into LDS once.  Workgroups are dispatched
-// longest row first (see the ranking at the top of the kernel).
+// tile.  The first four waves issue all the copies, so the other four (one per SIMD) start
+// their products at once.  The row's block table is read into LDS once.  Workgroups are
+// dispatched longest row first (see the ranking at the top of the kernel).
 //
 // The kernel is written for HPW query heads per wave; one head per wave (two waves per
 // SIMD, 8 waves) measured faster than two (one wave per SIMD, where the accumulators of
@@ -52,7 +53,6 @@ template <int D, int HPW>
 struct Cfg {
   static constexpr int NW = HMAX / HPW;
   static constexpr int NT = 64 * NW;
-  static constexpr int DC = D / 8;         // 16-byte chunks per K or V row
 };
 
 struct Params {
@@ -144,8 +144,19 @@ __device__ __forceinline__ void lds_copy16(const void* src, uint32_t lds) {
 // operations, the tile copies included, at their first use inside the loop).
 __device__ __forceinline__ void wait_vm0() { __builtin_amdgcn_s_waitcnt(0x0F70); }
 
+// The waves that copy the tiles: the first kCopyWaves of the workgroup (waves w and w + 4
+// share a SIMD, so one wave of each SIMD copies while the other starts its products; issued
+// by all eight waves at once, the copies stall every wave until the memory pipeline drains).
+constexpr int kCopyWaves = 4;
+
+template <int D>
+struct CopyCfg {
+  static constexpr int NW = kCopyWaves;  // copying waves
+  static constexpr int DC = D / 8;       // 16-byte chunks per K or V row
+};
+
 // The lane's part of every copy of a tile.  A copy is one 1 KB region of the tile (64
-// chunks, RPR = 64 / DC whole rows); copy j of wave w covers region R = j NW + w, i.e. rows
+// chunks, RPR = 64 / DC whole rows); copy j of copying wave w covers region R = j NW + w, i.e. rows
 // R RPR + [0, RPR), and lane l the chunk position l of it: row R RPR + l / DC, position
 // l % DC, where it stores the logical chunk (l % DC) ^ 2 (row mod 8).  As NW RPR is a multiple
 // of 8, row mod 8 and so the chunk the lane fetches do not depend on j.
@@ -153,7 +164,7 @@ template <class C>
 struct CopyLane {
   static constexpr int RPR = 64 / C::DC;         // rows per region
   static constexpr int STEP = RPR * C::NW;       // rows per copy step of the workgroup
-  static constexpr int NC = KT / STEP;           // copies per wave per tile
+  static constexpr int NC = KT / STEP;           // copies per copying wave per tile
   static constexpr bool kOneBlock = BS % STEP == 0;  // a step lies in one block, block j STEP / BS
   static_assert(C::DC <= 64 && 64 % C::DC == 0 && BS % RPR == 0 && STEP % 8 == 0 && KT % STEP == 0,
                 "regions cover whole rows inside one block");
@@ -283,7 +294,9 @@ __global__ __launch_bounds__(64 * (HMAX / HPW)) void prefill_kernel(Params p) {
   const bf16_t* kb = p.kbase + static_cast<int64_t>(g) * p.sG;
   const bf16_t* vb = p.vbase + static_cast<int64_t>(g) * p.sG;
   const int64_t ntiles = (kv_len + KT - 1) / KT;
-  const CopyLane<C> cl = copy_lane<C>(p, wave, lane);
+  using CC = CopyCfg<D>;
+  const bool copier = wave < kCopyWaves;
+  const CopyLane<CC> cl = copy_lane<CC>(p, wave, lane);
   auto Kt = [&](int i) { return smem_lds + static_cast<uint32_t>(i * TB); };
   auto Vt = [&](int i) { return smem_lds + static_cast<uint32_t>((2 + i) * TB); };
   lds_barrier();  // s_phys
@@ -291,8 +304,10 @@ __global__ __launch_bounds__(64 * (HMAX / HPW)) void prefill_kernel(Params p) {
   int4 phys_cur = tile_phys(p, b, 0, kv_len, s_phys, nlb);
   int4 phys_n1 = tile_phys(p, b, KT, kv_len, s_phys, nlb);
   int4 phys_n2 = tile_phys(p, b, 2 * KT, kv_len, s_phys, nlb);
-  copy_tile<C>(p, 0, kv_len, kb, phys_cur, cl, smem, smem_lds, Kt(0), wave, lane);
-  copy_tile<C>(p, 0, kv_len, vb, phys_cur, cl, smem, smem_lds, Vt(0), wave, lane);
+  if (copier) {
+    copy_tile<CC>(p, 0, kv_len, kb, phys_cur, cl, smem, smem_lds, Kt(0), wave, lane);
+    copy_tile<CC>(p, 0, kv_len, vb, phys_cur, cl, smem, smem_lds, Vt(0), wave, lane);
+  }
 
   // Q^T operands (B of S^T = K Q^T), one per head of the wave: lane holds position col,
   // dims 32i + 8*quad + [0, 8); a head past the group reads as zeros and is never stored
@@ -362,7 +377,7 @@ __global__ __launch_bounds__(64 * (HMAX / HPW)) void prefill_kernel(Params p) {
   // prologue: K(0) and V(0) landed, then K(1) copied while S(0) is computed
   wait_vm0();
   lds_barrier();
-  if (ntiles > 1) copy_tile<C>(p, KT, kv_len, kb, phys_n1, cl, smem, smem_lds, Kt(1), wave, lane);
+  if (ntiles > 1 && copier) copy_tile<CC>(p, KT, kv_len, kb, phys_n1, cl, smem, smem_lds, Kt(1), wave, lane);
   floatx4_v s_cur[HPW][ST];
   if (active) scores(0, s_cur);
   wait_vm0();
@@ -376,8 +391,10 @@ __global__ __launch_bounds__(64 * (HMAX / HPW)) void prefill_kernel(Params p) {
     const int64_t key0 = kt * KT;
     const int cb = static_cast<int>(kt & 1);
     const int4 phys_n3 = tile_phys(p, b, key0 + 3 * KT, kv_len, s_phys, nlb);
-    if (kt + 2 < ntiles) copy_tile<C>(p, key0 + 2 * KT, kv_len, kb, phys_n2, cl, smem, smem_lds, Kt(cb), wave, lane);
-    if (kt + 1 < ntiles) copy_tile<C>(p, key0 + KT, kv_len, vb, phys_n1, cl, smem, smem_lds, Vt(cb ^ 1), wave, lane);
+    if (copier) {
+      if (kt + 2 < ntiles) copy_tile<CC>(p, key0 + 2 * KT, kv_len, kb, phys_n2, cl, smem, smem_lds, Kt(cb), wave, lane);
+      if (kt + 1 < ntiles) copy_tile<CC>(p, key0 + KT, kv_len, vb, phys_n1, cl, smem, smem_lds, Vt(cb ^ 1), wave, lane);
+    }
     floatx4_v s_nxt[HPW][ST];
     if (active) {
       // only tiles that reach past the workgroup's first position, past the last visible
