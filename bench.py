@@ -35,13 +35,13 @@ for _p in (REPO_ROOT, PACKAGE_DIR):
 HBM_PEAK_GBS = 8000.0  # MI355X HBM3E, GB/s
 # HBM bytes per launch of the decode kernel from rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE
 # (profiles/decode_partial_mfma_config2.md, profiles/chunk_gated_delta_config4.md, profiles/gated_rms_norm_config4.md,
-# profiles/paged_prefill_config3.md): FETCH_SIZE scaled by 2.0 and WRITE_SIZE by 1.0, the factors
+# profiles/paged_prefill_config3.md, profiles/qk_norm_rope_config3.md): FETCH_SIZE scaled by 2.0 and WRITE_SIZE by 1.0, the factors
 # a plain 1 GiB device copy reads back in the same runs. Counters need rocprofv3, so the figures
 # are the committed profile's, not measured live.
 TRAFFIC_DECODE = 1959210677
-TRAFFIC_DELTA = 1636029928
-TRAFFIC_PREFILL = 888455186  # average over the eight per-chunk launches
-TRAFFIC_PROLOGUE = 675541424
+TRAFFIC_DELTA = 822636636  # chunk_kernel alone; the step (with prep_kernel) moves 1,399,985,329
+TRAFFIC_PREFILL = 888510552  # average over the eight per-chunk launches
+TRAFFIC_PROLOGUE = 675674420
 TRAFFIC_OUTPUT_NORM = 805389585
 TRAFFIC_FP8_LINEAR = 43744256  # cast + main kernel + split-K reduce, from profiles/fp8_linear_config5_batch.md
 SECONDARY_WARM_MS = 100.0  # wall time of untimed steps before each secondary (config 3, 4, 5) measurement
@@ -832,7 +832,7 @@ def main() -> int:
                 "config": {"workload": "config 3's 32768 new tokens (8 x 4096, prefix U[0, 8192] seed 0) in one launch", "q_heads": 16,
                            "kv_heads": 2, "head_dim": 256, "rotary_dim": 64, "rope_theta": 1e7, "block_size": 16},
                 "roofline": {"bound": "hbm", "achieved": round(ogbs, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(ogbs / HBM_PEAK_GBS, 4),
-                             "traffic": TRAFFIC_PROLOGUE, "algo_bytes_per_launch": ow["algo_bytes"], "kernel": "qa::qkr::qk_norm_rope_kernel<4>",
+                             "traffic": TRAFFIC_PROLOGUE, "algo_bytes_per_launch": ow["algo_bytes"], "kernel": "qa::qkr::qk_norm_rope_kernel<4, 1>",
                              "kernel_avg_us": round(k_ms * 1e3, 2), "kernels": okern},
             }
             del ow

@@ -15,7 +15,9 @@
 // is go to slot (table[b][pos / bs], pos % bs) of the pool (bit-exact copy for v).
 //
 // Mapping: one 256-thread workgroup per (new token of row b, row b); its four
-// waves walk the H query heads, the H_kv key heads and the H_kv value heads.
+// waves walk the H query heads, the H_kv key heads and the H_kv value heads, each
+// wave loading the rows of all its heads before it reduces any of them (with one
+// head's load in flight at a time the kernel is bound by memory latency).
 // Lane l of a wave holds elements E l .. E l + E - 1 of a head (D = 64 E); the
 // mean is a wave reduction and the rotary partner of an element comes from the
 // lane rd / (2 E) away (rd / 2 a multiple of E).
@@ -57,6 +59,13 @@ __device__ __forceinline__ int64_t read_index(const void* base, int is64, int64_
 
 __device__ __forceinline__ float round_bf16(float f) { return bf16_to_f32(f32_to_bf16(f)); }
 
+// head tasks whose loads a wave issues before reducing any of them (20 tasks of 4 waves at
+// H = 16, H_kv = 2 fit one pass)
+constexpr int kTasksInFlight = 8;
+// new tokens of one row per workgroup (measured at config 3: two per workgroup no faster,
+// four slower)
+constexpr int kTokensPerGroup = 1;
+
 template <int E>
 __device__ __forceinline__ void load_e(const bf16_t* src, float (&x)[E]) {
   if constexpr (E == 4) {
@@ -90,94 +99,149 @@ __device__ __forceinline__ void store_e(bf16_t* dst, const float (&y)[E]) {
   }
 }
 
+// Per-token values of the kernel: the packed row, the pool slot (-1: outside the table or the
+// pool, skipped) and the bf16 rotary factors of this lane's elements (the reference's cos/sin
+// tensors: from the table when it covers the position, else computed here).
 template <int E>
-__global__ __launch_bounds__(256) void qk_norm_rope_kernel(Params p) {
-  const int b = blockIdx.y;
-  const int64_t r0 = read_index(p.cu, p.idx_i64, b);
-  const int64_t n = r0 + blockIdx.x;
-  if (n >= read_index(p.cu, p.idx_i64, b + 1)) return;
-  const int64_t pos = read_index(p.starts, p.idx_i64, b) + blockIdx.x;
-  const int lane = threadIdx.x & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int j0 = E * lane;  // first element of this lane
-
-  // the pool slot of this token (-1: outside the table or the pool, skipped)
-  int64_t slot = -1;
-  if (pos >= 0 && pos / p.bs < p.max_blocks) {
-    const int64_t phys = read_index(p.tables, p.table_i64, static_cast<int64_t>(b) * p.table_stride + pos / p.bs);
-    if (phys >= 0 && phys < p.num_blocks) slot = phys * p.sP + (pos % p.bs) * p.sT;
-  }
-  // rotary factors of this lane's elements (bf16 values, as the reference's cos/sin tensors):
-  // from the table when it covers the position, else computed here
-  const int half = p.rd / 2;
-  const bool rot = j0 < p.rd;
+struct TokenCtx {
+  int64_t n;
+  int64_t slot;
+  bool live;
   float c[E], s[E];
+};
+
+template <int E>
+__device__ __forceinline__ TokenCtx<E> token_ctx(const Params& p, int b, int64_t r0, int64_t r1, int64_t start, int64_t x, int j0) {
+  TokenCtx<E> t;
+  t.live = r0 + x < r1;
+  const int64_t xx = t.live ? x : r1 - 1 - r0;  // a token past the row reads the row's last one again
+  t.n = r0 + xx;
+  const int64_t pos = start + xx;
+  t.slot = -1;
+  if (t.live && pos >= 0 && pos / p.bs < p.max_blocks) {
+    const int64_t phys = read_index(p.tables, p.table_i64, static_cast<int64_t>(b) * p.table_stride + pos / p.bs);
+    if (phys >= 0 && phys < p.num_blocks) t.slot = phys * p.sP + (pos % p.bs) * p.sT;
+  }
+  const int half = p.rd / 2;
 #pragma unroll
   for (int e = 0; e < E; ++e) {
-    c[e] = 1.f;
-    s[e] = 0.f;
+    t.c[e] = 1.f;
+    t.s[e] = 0.f;
   }
-  if (rot) {
+  if (j0 < p.rd) {
     const int jh = j0 % (half > 0 ? half : 1);  // E consecutive frequencies (half is a multiple of E)
     if (pos >= 0 && pos < p.cs_len) {
       const bf16_t* row = p.cs_table + pos * 2 * half;
-      load_e<E>(row + jh, c);
-      load_e<E>(row + half + jh, s);
+      load_e<E>(row + jh, t.c);
+      load_e<E>(row + half + jh, t.s);
     } else {
 #pragma unroll
       for (int e = 0; e < E; ++e) {
         const float ang = static_cast<float>(pos) * p.inv_freq[jh + e];
-        c[e] = round_bf16(cosf(ang));
-        s[e] = round_bf16(sinf(ang));
+        t.c[e] = round_bf16(cosf(ang));
+        t.s[e] = round_bf16(sinf(ang));
       }
     }
   }
+  return t;
+}
+
+template <int E, int TPW>
+__global__ __launch_bounds__(256) void qk_norm_rope_kernel(Params p) {
+  const int b = blockIdx.y;
+  const int64_t r0 = read_index(p.cu, p.idx_i64, b);
+  const int64_t r1 = read_index(p.cu, p.idx_i64, b + 1);
+  const int64_t x0 = static_cast<int64_t>(blockIdx.x) * TPW;
+  if (r0 + x0 >= r1) return;
+  const int64_t start = read_index(p.starts, p.idx_i64, b);
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int j0 = E * lane;  // first element of this lane
+
+  TokenCtx<E> tk[TPW];
+#pragma unroll
+  for (int u = 0; u < TPW; ++u) tk[u] = token_ctx<E>(p, b, r0, r1, start, x0 + u, j0);
+  const int half = p.rd / 2;
+  const bool rot = j0 < p.rd;
   const int partner = j0 < half ? lane + half / E : lane - half / E;  // lane holding element j +- rd/2
   const bool ror8 = half / E == 8;  // partner 8 lanes away in the same 16-lane row: a DPP rotate
   const float sign = j0 < half ? -1.f : 1.f;
   const float inv_d = 1.f / static_cast<float>(p.D);
   // this lane's (1 + w) factors of the q and k norms, read once
   float wq[E], wk[E];
+  if (p.w_f32) {
+#pragma unroll
+    for (int e = 0; e < E; ++e) {
+      wq[e] = reinterpret_cast<const float*>(p.qw)[j0 + e];
+      wk[e] = reinterpret_cast<const float*>(p.kw)[j0 + e];
+    }
+  } else {
+    load_e<E>(reinterpret_cast<const bf16_t*>(p.qw) + j0, wq);
+    load_e<E>(reinterpret_cast<const bf16_t*>(p.kw) + j0, wk);
+  }
 #pragma unroll
   for (int e = 0; e < E; ++e) {
-    wq[e] = 1.f + (p.w_f32 ? reinterpret_cast<const float*>(p.qw)[j0 + e] : bf16_to_f32(reinterpret_cast<const bf16_t*>(p.qw)[j0 + e]));
-    wk[e] = 1.f + (p.w_f32 ? reinterpret_cast<const float*>(p.kw)[j0 + e] : bf16_to_f32(reinterpret_cast<const bf16_t*>(p.kw)[j0 + e]));
+    wq[e] += 1.f;
+    wk[e] += 1.f;
   }
 
-  // Task t of the workgroup: query head t (t < H), key head t - H (t < H + H_kv), value head
-  // t - H - H_kv; wave w takes tasks w, w + 4, ....
+  // Task t of a token: query head t (t < H), key head t - H (t < H + H_kv), value head
+  // t - H - H_kv; wave w takes tasks w, w + 4, ... of each of the workgroup's TPW tokens.  The
+  // loads of up to kTasksInFlight tasks of every token are issued before any of them is
+  // reduced, so a wave waits for memory once per pass rather than once per head (one load in
+  // flight per wave leaves the kernel latency-bound).
   const int ntask = p.H + 2 * p.Hkv;
-  for (int task = wave; task < ntask; task += 4) {
-    if (task < p.H + p.Hkv) {
-      const bool isq = task < p.H;
-      const int h = isq ? task : task - p.H;
-      const bf16_t* src = isq ? p.q + n * p.q_st + static_cast<int64_t>(h) * p.q_sh : p.k + n * p.k_st + static_cast<int64_t>(h) * p.k_sh;
-      float x[E];
-      load_e<E>(src + j0, x);
-      float ss = 0.f;
+  auto task_src = [&](int64_t n, int task) -> const bf16_t* {
+    if (task < p.H) return p.q + n * p.q_st + static_cast<int64_t>(task) * p.q_sh;
+    if (task < p.H + p.Hkv) return p.k + n * p.k_st + static_cast<int64_t>(task - p.H) * p.k_sh;
+    return p.v + n * p.v_st + static_cast<int64_t>(task - p.H - p.Hkv) * p.v_sh;
+  };
+  for (int pass = wave; pass < ntask; pass += 4 * kTasksInFlight) {
+    float xin[TPW][kTasksInFlight][E];
 #pragma unroll
-      for (int e = 0; e < E; ++e) ss += x[e] * x[e];
-      const float rs = rsqrtf(wave_sum_dpp(ss) * inv_d + p.eps);
-      float y[E];
+    for (int u = 0; u < TPW; ++u)
 #pragma unroll
-      for (int e = 0; e < E; ++e) y[e] = round_bf16((x[e] * rs) * (isq ? wq[e] : wk[e]));
-      float o[E];
-#pragma unroll
-      for (int e = 0; e < E; ++e) {
-        const float yp = ror8 ? __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(y[e]), 0x128, 0xF, 0xF, false))  // row_ror:8
-                              : __shfl(y[e], partner, 64);
-        o[e] = rot ? round_bf16(round_bf16(y[e] * c[e]) + round_bf16(sign * yp * s[e])) : y[e];
+      for (int i = 0; i < kTasksInFlight; ++i) {
+        // tasks past the end load the last task's row again (no branch, so the loads issue
+        // back to back) and are never used
+        load_e<E>(task_src(tk[u].n, min(pass + 4 * i, ntask - 1)) + j0, xin[u][i]);
       }
-      if (isq) {
-        store_e<E>(p.q_out + (n * p.H + h) * static_cast<int64_t>(p.D) + j0, o);
-      } else if (slot >= 0) {
-        store_e<E>(p.kpool + slot + static_cast<int64_t>(h) * p.sG + j0, o);
+#pragma unroll
+    for (int u = 0; u < TPW; ++u) {
+      if (!tk[u].live) break;
+      const int64_t n = tk[u].n;
+      const int64_t slot = tk[u].slot;
+#pragma unroll
+      for (int i = 0; i < kTasksInFlight; ++i) {
+        const int task = pass + 4 * i;
+        if (task >= ntask) break;
+        if (task < p.H + p.Hkv) {
+          const bool isq = task < p.H;
+          const int h = isq ? task : task - p.H;
+          float ss = 0.f;
+#pragma unroll
+          for (int e = 0; e < E; ++e) ss += xin[u][i][e] * xin[u][i][e];
+          const float rs = rsqrtf(wave_sum_dpp(ss) * inv_d + p.eps);
+          float y[E];
+#pragma unroll
+          for (int e = 0; e < E; ++e) y[e] = round_bf16((xin[u][i][e] * rs) * (isq ? wq[e] : wk[e]));
+          float o[E];
+#pragma unroll
+          for (int e = 0; e < E; ++e) {
+            const float yp = ror8 ? __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(y[e]), 0x128, 0xF, 0xF, false))  // row_ror:8
+                                  : __shfl(y[e], partner, 64);
+            o[e] = rot ? round_bf16(round_bf16(y[e] * tk[u].c[e]) + round_bf16(sign * yp * tk[u].s[e])) : y[e];
+          }
+          if (isq) {
+            store_e<E>(p.q_out + (n * p.H + h) * static_cast<int64_t>(p.D) + j0, o);
+          } else if (slot >= 0) {
+            store_e<E>(p.kpool + slot + static_cast<int64_t>(h) * p.sG + j0, o);
+          }
+        } else if (slot >= 0) {
+          const int h = task - p.H - p.Hkv;
+          store_e<E>(p.vpool + slot + static_cast<int64_t>(h) * p.sG + j0, xin[u][i]);
+        }
       }
-    } else if (slot >= 0) {
-      const int h = task - p.H - p.Hkv;
-      float x[E];
-      load_e<E>(p.v + n * p.v_st + static_cast<int64_t>(h) * p.v_sh + j0, x);
-      store_e<E>(p.vpool + slot + static_cast<int64_t>(h) * p.sG + j0, x);
     }
   }
 }
@@ -258,15 +322,15 @@ extern "C" int qa_qk_norm_rope_append(const void* q_proj, int64_t q_stride_t, in
   p.rd = rotary_dim;
   p.bs = block_size;
   p.q_out = reinterpret_cast<bf16_t*>(q_out);
-  const dim3 grid(static_cast<unsigned>(max_new), static_cast<unsigned>(batch));
+  const dim3 grid(static_cast<unsigned>(ceil_div(max_new, kTokensPerGroup)), static_cast<unsigned>(batch));
   {
     KernelTimer timer_("qk_norm_rope", stream);
     if (E == 4)
-      hipLaunchKernelGGL(qk_norm_rope_kernel<4>, grid, dim3(256), 0, stream, p);
+      hipLaunchKernelGGL((qk_norm_rope_kernel<4, kTokensPerGroup>), grid, dim3(256), 0, stream, p);
     else if (E == 2)
-      hipLaunchKernelGGL(qk_norm_rope_kernel<2>, grid, dim3(256), 0, stream, p);
+      hipLaunchKernelGGL((qk_norm_rope_kernel<2, kTokensPerGroup>), grid, dim3(256), 0, stream, p);
     else
-      hipLaunchKernelGGL(qk_norm_rope_kernel<1>, grid, dim3(256), 0, stream, p);
+      hipLaunchKernelGGL((qk_norm_rope_kernel<1, kTokensPerGroup>), grid, dim3(256), 0, stream, p);
   }
   return check_launch("qk_norm_rope_append");
 }
