@@ -17,12 +17,14 @@
 // operand, so a lane's accumulator holds four consecutive outputs of one x row
 // (16-byte stores).
 //
-// Work item: a workgroup of 4 waves owns one 128-row block of W (one scale row)
-// for 16 * MS rows of x and a range of 128-deep K blocks.  Per K block the x
-// tile goes to LDS (double-buffered, one barrier per block); each wave streams
-// its 32 weight rows straight from global memory into registers two blocks
-// ahead.  When the grid is small, K is split over workgroups that write fp32
-// partials, summed in a fixed order by a second kernel.
+// Tiled path (at most 16 rows, or more than 256): a workgroup of 4 waves owns one
+// 128-row block of W (one scale row) for 16 * MS rows of x and a range of 128-deep
+// K blocks.  Per K block the x tile goes to LDS (double-buffered, one barrier per
+// block); each wave streams its 32 weight rows straight from global memory into
+// registers two blocks ahead.  When the grid is small, K is split over workgroups
+// that write fp32 partials, summed in a fixed order by a second kernel.  Wide path
+// (17 to 256 rows of 16-bit x): see fp8_linear_wide_kernel below, one pass over K
+// per output tile with no K split.
 #include "qa_common.h"
 
 #include <type_traits>
@@ -327,6 +329,145 @@ __global__ __launch_bounds__(256) void fp8_pack_kernel(const uint8_t* __restrict
   *reinterpret_cast<u32x4_v*>(dst + 16 * piece) = *reinterpret_cast<const u32x4_v*>(src + row * K + col);
 }
 
+// ---- Wide path (16-bit x of more than 16 rows): one pass over K per output tile.
+//
+// Work item: 64 weight rows x 16 XT rows of x x all of K, 8 waves: wave w multiplies weight tile
+// w % 4 (16 rows) with x tiles [XT/2 (w / 4), XT/2 (w / 4 + 1)), so the two waves of a SIMD (w and
+// w + 4) hide each other's waits.  Per 128-deep K block the workgroup copies the x tile and the four
+// 2 KB weight tiles from global memory straight into LDS (global_load_lds_dwordx4, no registers),
+// kDepth blocks ahead of the block it multiplies, into a ring of kDepth + 1 block buffers; one
+// barrier per block.  Both weight layouts land in the same LDS order (the packed chunk's), so they
+// give identical results.  The x tile's 16-byte chunks are XOR-swizzled by row (chunk c of row r at
+// position c ^ (r mod 16)), which puts the 16 rows of an operand read on distinct banks.  No K
+// split: each weight tile is read once whatever the row count (when the count of weight tiles is a
+// multiple of 8, the m tiles of one weight tile share block indices mod 8, so one XCD and its L2),
+// and no partial sums leave the workgroup.
+constexpr int WN = 64;                 // weight rows per workgroup of the wide path
+constexpr int WNT = 512;               // threads per workgroup of the wide path
+constexpr int kDepth = 3;              // K blocks in flight ahead of the one multiplied
+constexpr int kRing = kDepth + 1;
+
+template <int XT>
+struct WideSmem {
+  static_assert(XT % 2 == 0, "two x halves");
+  static constexpr int kXBytes = 16 * XT * KB * 2;  // x tile of one block, 16-bit
+  static constexpr int kWBytes = WN * KB;           // the four weight tiles of one block, fp8
+  static constexpr int kBlockBytes = kXBytes + kWBytes;
+  static constexpr int kBytes = kRing * kBlockBytes + MAX_KB * 4;  // + the block scales (fp32)
+  static constexpr int kCopies = XT / 2 + 1;        // 1 KB copies per wave per block
+};
+
+template <int MODE, int XT>
+__global__ __launch_bounds__(WNT) void fp8_linear_wide_kernel(Params p) {
+  static_assert(MODE == X_BF16 || MODE == X_F16, "16-bit x only");
+  typedef typename ModeTraits<MODE>::V V;
+  using S = WideSmem<XT>;
+  constexpr int XH = XT / 2;  // x tiles per wave
+  extern __shared__ __align__(16) unsigned char smem[];
+  const uint32_t smem_lds = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(smem));
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wt = wave & 3;   // weight tile
+  const int xh = wave >> 2;  // x half
+  const int lr = lane & 15;
+  const int lg = lane >> 4;
+  const int64_t m0 = static_cast<int64_t>(blockIdx.y) * 16 * XT;
+  const int64_t nkb = p.K / KB;
+  const int64_t n_blk = static_cast<int64_t>(blockIdx.x) * WN;
+
+  // Copy sources.  Weight: wave w copies half h = w / 4 of tile w % 4 of a block: lane l's 16 bytes
+  // to LDS byte 2048 (w % 4) + 1024 h + 16 l of the block's weight region (packed: contiguous;
+  // row-major: row 16 (w % 4) + l % 16, columns 32 (l / 16) + 16 h).  x: copy j of wave w covers
+  // rows 4 (w + 8 j) + l / 16 of the tile, chunk position l % 16 holding logical chunk
+  // (l % 16) ^ (row mod 16); the row mod 16 is (4 w + l / 16) mod 16 for every j.
+  const int64_t n_t = n_blk + 16 * wt;
+  const uint8_t* wsrc = (p.packed ? p.w + (n_t / 16) * nkb * 2048 + 16 * lane : p.w + (n_t + lr) * p.K + 32 * lg) + xh * (p.packed ? 1024 : 16);
+  const int64_t wstep = p.packed ? 2048 : KB;  // per block
+  const int xchunk = (lane & 15) ^ ((4 * wave + lg) & 15);
+  const char* xsrc[XH];
+#pragma unroll
+  for (int j = 0; j < XH; ++j) {
+    const int64_t m = min64(m0 + 4 * (wave + 8 * j) + lg, p.M - 1);  // rows past M read row M - 1, never stored
+    xsrc[j] = static_cast<const char*>(p.x) + (m * p.x_stride + 8 * xchunk) * 2;
+  }
+  auto xbuf = [&](int64_t kb) { return static_cast<uint32_t>((kb % kRing) * S::kBlockBytes); };
+  auto issue = [&](int64_t kb) {
+    const uint32_t base = smem_lds + xbuf(kb);
+#pragma unroll
+    for (int j = 0; j < XH; ++j) lds_copy16(xsrc[j] + kb * KB * 2, base + 1024u * static_cast<uint32_t>(wave + 8 * j));
+    lds_copy16(wsrc + kb * wstep, base + S::kXBytes + 2048u * wt + 1024u * xh);
+  };
+
+#pragma unroll
+  for (int d = 0; d < kDepth; ++d)
+    if (d < nkb) issue(d);
+  // the block scales of the workgroup's weight rows (one 128-row scale row), into LDS once; their
+  // loads follow the first blocks' copies, so waiting for them overlaps those copies (the first
+  // barrier of the loop makes them visible)
+  float* s_scale = reinterpret_cast<float*>(smem + kRing * S::kBlockBytes);
+  const bf16_t* srow = p.scale + (n_blk / KB) * p.scale_cols;
+  for (int64_t t = tid; t < nkb; t += WNT) s_scale[t] = bf16_to_f32(srow[t]);
+
+  f32x4_v acc[XH];
+#pragma unroll
+  for (int i = 0; i < XH; ++i) acc[i] = f32x4_v{0.f, 0.f, 0.f, 0.f};
+  for (int64_t kb = 0; kb < nkb; ++kb) {
+    // this wave's copies of block kb have landed (those of the blocks after it may be in flight),
+    // then the barrier makes every wave's copies visible and frees the buffer of block kb - 1
+    if (kb + kDepth - 1 < nkb)
+      asm volatile("s_waitcnt vmcnt(%0)" ::"n"(S::kCopies * (kDepth - 1)) : "memory");
+    else
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    lds_barrier();
+    // every operand read of the block first, then the products, then the copies of block
+    // kb + kDepth (into the buffer of block kb - 1, free since the barrier): the copies' issue
+    // stall then overlaps the products instead of delaying the reads
+    const unsigned char* xb = smem + xbuf(kb);
+    const unsigned char* wb = xb + S::kXBytes + 2048 * wt + 16 * lane;
+    const u32x4_v w0 = *reinterpret_cast<const u32x4_v*>(wb);
+    const u32x4_v w1 = *reinterpret_cast<const u32x4_v*>(wb + 1024);
+    V bx[4][XH];
+#pragma unroll
+    for (int s = 0; s < 4; ++s)
+#pragma unroll
+      for (int i = 0; i < XH; ++i)
+        bx[s][i] = *reinterpret_cast<const V*>(xb + (16 * (XH * xh + i) + lr) * (KB * 2) + 16 * ((4 * lg + s) ^ lr));
+    __builtin_amdgcn_sched_barrier(0);
+    f32x4_v blk[XH];
+#pragma unroll
+    for (int i = 0; i < XH; ++i) blk[i] = f32x4_v{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+      const u32x4_v& w = s < 2 ? w0 : w1;
+      const V a = fp8x8_operand<V>(w[2 * (s & 1)], w[2 * (s & 1) + 1]);
+#pragma unroll
+      for (int i = 0; i < XH; ++i) blk[i] = mfma(a, bx[s][i], blk[i]);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    if (kb + kDepth < nkb) issue(kb + kDepth);
+    const float sc = s_scale[kb];
+#pragma unroll
+    for (int i = 0; i < XH; ++i) acc[i] += sc * blk[i];
+  }
+
+  // C = W X^T: lane (lg, lr) of tile i holds y[m0 + 16 (XH xh + i) + lr][n_t + 4 lg + r]
+#pragma unroll
+  for (int i = 0; i < XH; ++i) {
+    const int64_t m = m0 + 16 * (XH * xh + i) + lr;
+    if (m >= p.M) continue;
+    const int64_t n = n_t + 4 * lg;
+    if (p.y_f32) {
+      *reinterpret_cast<f32x4_v*>(static_cast<float*>(p.y) + m * p.y_stride + n) = acc[i];
+    } else {
+      uint2 packed;
+      packed.x = static_cast<uint32_t>(f32_to_bf16(acc[i][0])) | (static_cast<uint32_t>(f32_to_bf16(acc[i][1])) << 16);
+      packed.y = static_cast<uint32_t>(f32_to_bf16(acc[i][2])) | (static_cast<uint32_t>(f32_to_bf16(acc[i][3])) << 16);
+      *reinterpret_cast<uint2*>(static_cast<bf16_t*>(p.y) + m * p.y_stride + n) = packed;
+    }
+  }
+}
+
 // fp32 x (16 rows or more) to fp16 once per call, round to nearest even (the reference's
 // float_rows_to_half_kernel, src/csrc/fp8_linear_cuda.cu:146-150): staging 16-bit x keeps the
 // main kernel's register ring small enough for its LDS operand reads to overlap.
@@ -351,6 +492,8 @@ __global__ __launch_bounds__(256) void fp8_cast_x_kernel(const float* __restrict
 }
 
 struct Plan {
+  int wide;  // 16-bit x of 17..256 rows: the wide kernel (no K split), xt tiles of 16 rows
+  int xt;
   int ms;
   int64_t mtiles, ntiles;
   int ksplit, blocks_per_split;
@@ -363,6 +506,17 @@ struct Plan {
 // workgroups with at least four K blocks each.
 inline Plan make_plan(int64_t M, int64_t N, int64_t K) {
   Plan pl{};
+  if (M > 16 && M <= 256) {
+    // x is 16-bit here in both input dtypes (fp32 x of 16 rows or more is cast to fp16 first)
+    pl.wide = 1;
+    pl.xt = M <= 32 ? 2 : 4;
+    pl.mtiles = (M + 16 * pl.xt - 1) / (16 * pl.xt);
+    pl.ntiles = N / WN;
+    pl.ksplit = 1;
+    pl.blocks_per_split = static_cast<int>(K / KB);
+    pl.workspace = M * K * 2;  // the fp16 copy of an fp32 x
+    return pl;
+  }
   pl.ms = M <= 16 ? 1 : M <= 32 ? 2 : 4;
   pl.mtiles = (M + 16 * pl.ms - 1) / (16 * pl.ms);
   pl.ntiles = N / NTILE;
@@ -376,6 +530,20 @@ inline Plan make_plan(int64_t M, int64_t N, int64_t K) {
   pl.partial_bytes = pl.ksplit > 1 ? (static_cast<int64_t>(pl.ksplit) * M * N * 4 + 255) / 256 * 256 : 0;
   pl.workspace = pl.partial_bytes + (M >= 16 ? M * K * 2 : 0);
   return pl;
+}
+
+template <int MODE, int XT>
+int launch_wide(const Plan& pl, const Params& p, hipStream_t stream) {
+  static bool attr_set = false;  // the dynamic LDS of the ring is above the 64 KB default for XT = 4
+  if (!attr_set) {
+    const hipError_t err = hipFuncSetAttribute(reinterpret_cast<const void*>(&fp8_linear_wide_kernel<MODE, XT>),
+                                               hipFuncAttributeMaxDynamicSharedMemorySize, WideSmem<XT>::kBytes);
+    if (err != hipSuccess) return fail("fp8_linear: cannot reserve %d bytes of LDS: %s", WideSmem<XT>::kBytes, hipGetErrorString(err));
+    attr_set = true;
+  }
+  const dim3 grid(static_cast<unsigned>(pl.ntiles), static_cast<unsigned>(pl.mtiles));
+  hipLaunchKernelGGL((fp8_linear_wide_kernel<MODE, XT>), grid, dim3(WNT), WideSmem<XT>::kBytes, stream, p);
+  return 0;
 }
 
 template <int MS>
@@ -467,6 +635,18 @@ extern "C" int qa_fp8_linear(const void* x, int32_t x_dtype, int64_t x_stride, i
   p.ksplit = pl.ksplit;
   p.y_f32 = y_dtype == QA_F32;
   p.packed = weight_packed != 0;
+  if (pl.wide) {
+    int rc = 0;
+    {
+      KernelTimer timer_("fp8_linear", stream);
+      if (mode == X_F16)
+        rc = pl.xt == 2 ? launch_wide<X_F16, 2>(pl, p, stream) : launch_wide<X_F16, 4>(pl, p, stream);
+      else
+        rc = pl.xt == 2 ? launch_wide<X_BF16, 2>(pl, p, stream) : launch_wide<X_BF16, 4>(pl, p, stream);
+    }
+    if (rc) return rc;
+    return check_launch("fp8_linear");
+  }
   {
     KernelTimer timer_("fp8_linear", stream);
     if (pl.ms == 1)

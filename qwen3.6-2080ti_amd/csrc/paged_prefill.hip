@@ -119,25 +119,6 @@ __device__ __forceinline__ int4 tile_phys(const Params& p, int b, int64_t key0, 
   return make_int4(blk(0), blk(1), blk(2), blk(3));
 }
 
-// One 16-byte copy from global memory into LDS per lane (global_load_lds_dwordx4): lane l's
-// 16 bytes land at LDS byte lds + 16 l (lds wave-uniform, through M0).  Issued as inline
-// assembly so that the compiler does not make every later LDS read wait for the copy (it
-// cannot tell which buffer a copy writes); the kernel waits for the copies itself
-// (s_waitcnt vmcnt(0)) before the barrier that hands a tile to the other waves.  M0 is
-// restored afterwards; one wait state separates the M0 write from the copy.
-__device__ __forceinline__ void lds_copy16(const void* src, uint32_t lds) {
-  uint32_t saved;
-  asm volatile(
-      "s_mov_b32 %0, m0\n\t"
-      "s_mov_b32 m0, %1\n\t"
-      "s_nop 0\n\t"
-      "global_load_lds_dwordx4 %2, off\n\t"
-      "s_mov_b32 m0, %0"
-      : "=&s"(saved)
-      : "s"(lds), "v"(src)
-      : "memory");
-}
-
 // s_waitcnt vmcnt(0) through the builtin, so that the compiler's own wait tracking knows every
 // vector-memory load has completed here (an inline-assembly wait would leave it assuming the
 // loads before the loop may still be in flight, and it would then wait for all vector-memory

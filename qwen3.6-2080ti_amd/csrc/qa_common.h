@@ -79,6 +79,25 @@ __device__ __forceinline__ int64_t load_index(const IT* p) {
 // prefetches issued before it; cross-wave data here always goes through LDS.
 __device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
 
+// One 16-byte copy from global memory into LDS per lane (global_load_lds_dwordx4): lane l's
+// 16 bytes land at LDS byte lds + 16 l (lds wave-uniform, through M0).  Issued as inline
+// assembly so that the compiler does not make every later LDS read wait for the copy (it
+// cannot tell which buffer a copy writes); the kernel waits for the copies itself
+// (s_waitcnt vmcnt(0)) before the barrier that hands a tile to the other waves.  M0 is
+// restored afterwards; one wait state separates the M0 write from the copy.
+__device__ __forceinline__ void lds_copy16(const void* src, uint32_t lds) {
+  uint32_t saved;
+  asm volatile(
+      "s_mov_b32 %0, m0\n\t"
+      "s_mov_b32 m0, %1\n\t"
+      "s_nop 0\n\t"
+      "global_load_lds_dwordx4 %2, off\n\t"
+      "s_mov_b32 m0, %0"
+      : "=&s"(saved)
+      : "s"(lds), "v"(src)
+      : "memory");
+}
+
 __device__ __forceinline__ float wave_sum(float v) {
 #pragma unroll
   for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
