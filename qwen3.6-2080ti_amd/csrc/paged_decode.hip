@@ -527,77 +527,85 @@ __global__ __launch_bounds__(256, QA_DECODE_WAVES_PER_SIMD) void decode_partial_
 // Merge the partials of one (row, head) of the balanced schedule.  The partial
 // kernel records, per row group, the first and the last wave that covered it;
 // those waves wrote slots first + rg .. last + rg.  m is in the log2 domain.
-// The first kCombinePrefetch partial rows are loaded before the weights are
-// known so their latency overlaps the reductions.  Rows without a visible
-// tile get 0 (their row-group record is stale and not read).
+// One wave per (row, head), four per workgroup, no LDS and no barrier: lane l
+// owns columns [CPL l, CPL (l + 1)) of every partial row (one 8- or 16-byte
+// load per row), and lane s holds (m, l) of partial s for the reductions; the
+// weight of partial s reaches the other lanes with v_readlane.  The first
+// kCombinePrefetch partial rows are loaded before the weights are known so
+// their latency overlaps the reductions.  Rows without a visible tile get 0
+// (their row-group record is stale and not read).
 constexpr int kCombinePrefetch = 8;
+constexpr int kCombineWaves = 4;
 
-template <typename QT>
-__global__ __launch_bounds__(256) void decode_combine_balanced(DecodeParams p) {
-  __shared__ float weight[kMaxDecodeWaves];
-  __shared__ float redf[4];
-  const int bh = blockIdx.x;
+template <typename QT, int D>
+__global__ __launch_bounds__(64 * kCombineWaves) void decode_combine_balanced(DecodeParams p) {
+  constexpr int CPL = D / 64;
+  typedef float vec_t __attribute__((ext_vector_type(CPL)));
+  const int lane = threadIdx.x & 63;
+  const int bh = blockIdx.x * kCombineWaves + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  if (bh >= p.B * p.H) return;
   const int b = bh / p.H;
   const int h = bh - b * p.H;
   const int g = h / p.G;
   const int hh = h - g * p.G;
-  const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
-  QT* out = reinterpret_cast<QT*>(p.out) + static_cast<int64_t>(bh) * p.D;
+  QT* out = reinterpret_cast<QT*>(p.out) + static_cast<int64_t>(bh) * D + CPL * lane;
 
   const int64_t rg = static_cast<int64_t>(b) * p.Hkv + g;
   const int32_t w_first = p.rg_waves[2 * rg];
   const int32_t w_last = p.rg_waves[2 * rg + 1];
   if (row_tiles(p, b) == 0) {
-    for (int d = threadIdx.x; d < p.D; d += blockDim.x) Elem<QT>::store(out + d, 0.f);
+#pragma unroll
+    for (int i = 0; i < CPL; ++i) Elem<QT>::store(out + i, 0.f);
     return;
   }
   const int n = w_last - w_first + 1;
   const int64_t slot0 = w_first + rg;
   const float* ml = p.part_ml + (slot0 * p.G + hh) * 2;
-  const float* po = p.part_o + (slot0 * p.G + hh) * p.D;
+  const float* po = p.part_o + (slot0 * p.G + hh) * D + CPL * lane;
   const int64_t sml = 2 * static_cast<int64_t>(p.G);
-  const int64_t so = static_cast<int64_t>(p.G) * p.D;
-  const int d0 = threadIdx.x;  // D <= 256: one column per thread
-  float pre[kCombinePrefetch];
-#pragma unroll
-  for (int s = 0; s < kCombinePrefetch; ++s) pre[s] = (s < n && d0 < p.D) ? po[s * so + d0] : 0.f;
+  const int64_t so = static_cast<int64_t>(p.G) * D;
+  auto row = [&](int s) { return *reinterpret_cast<const vec_t*>(po + s * so); };
 
-  float big = -INFINITY;
-  for (int s = threadIdx.x; s < n; s += blockDim.x) big = fmaxf(big, ml[s * sml]);
+  vec_t pre[kCombinePrefetch];
+#pragma unroll
+  for (int s = 0; s < kCombinePrefetch; ++s) pre[s] = s < n ? row(s) : vec_t(0.f);
+  // (m, l) of partials 0..63 stay in registers; later ones are read again.
+  float2 ml0 = lane < n ? *reinterpret_cast<const float2*>(ml + lane * sml) : make_float2(-INFINITY, 0.f);
+  float big = ml0.x;
+  for (int c = 64; c < n; c += 64) big = fmaxf(big, c + lane < n ? ml[(c + lane) * sml] : -INFINITY);
   big = wave_max(big);
-  if (lane == 0) redf[wave] = big;
-  __syncthreads();
-  big = fmaxf(fmaxf(redf[0], redf[1]), fmaxf(redf[2], redf[3]));
-  __syncthreads();
   const float use = big == -INFINITY ? 0.f : big;
+
+  vec_t acc0 = vec_t(0.f), acc1 = vec_t(0.f);
   float den = 0.f;
-  for (int s = threadIdx.x; s < n; s += blockDim.x) {
-    const float f = exp2f(ml[s * sml] - use);
-    weight[s] = f;
-    den += f * ml[s * sml + 1];
+  for (int c = 0; c < n; c += 64) {
+    const float2 e = c == 0 ? ml0 : (c + lane < n ? *reinterpret_cast<const float2*>(ml + (c + lane) * sml) : make_float2(-INFINITY, 0.f));
+    const float f = c + lane < n ? exp2f(e.x - use) : 0.f;
+    den += f * e.y;
+    const int cnt = min(64, n - c);
+    int j = 0;
+    if (c == 0) {
+#pragma unroll
+      for (int s = 0; s < kCombinePrefetch; s += 2) {
+        if (s < cnt) acc0 += __int_as_float(__builtin_amdgcn_readlane(__float_as_int(f), s)) * pre[s];
+        if (s + 1 < cnt) acc1 += __int_as_float(__builtin_amdgcn_readlane(__float_as_int(f), s + 1)) * pre[s + 1];
+      }
+      j = kCombinePrefetch;
+    }
+    for (; j + 4 <= cnt; j += 4) {
+      const vec_t v0 = row(c + j), v1 = row(c + j + 1), v2 = row(c + j + 2), v3 = row(c + j + 3);
+      acc0 += __int_as_float(__builtin_amdgcn_readlane(__float_as_int(f), j)) * v0;
+      acc1 += __int_as_float(__builtin_amdgcn_readlane(__float_as_int(f), j + 1)) * v1;
+      acc0 += __int_as_float(__builtin_amdgcn_readlane(__float_as_int(f), j + 2)) * v2;
+      acc1 += __int_as_float(__builtin_amdgcn_readlane(__float_as_int(f), j + 3)) * v3;
+    }
+    for (; j < cnt; ++j) acc0 += __int_as_float(__builtin_amdgcn_readlane(__float_as_int(f), j)) * row(c + j);
   }
   den = wave_sum(den);
-  if (lane == 0) redf[wave] = den;
-  __syncthreads();
-  den = redf[0] + redf[1] + redf[2] + redf[3];
   const float inv = den > 0.f ? 1.f / den : 0.f;
-  if (d0 < p.D) {
-    float acc0 = 0.f, acc1 = 0.f;
+  const vec_t o = (acc0 + acc1) * inv;
 #pragma unroll
-    for (int s = 0; s < kCombinePrefetch; s += 2) {
-      if (s < n) acc0 += weight[s] * pre[s];
-      if (s + 1 < n) acc1 += weight[s + 1] * pre[s + 1];
-    }
-    float acc2 = 0.f, acc3 = 0.f;
-    int s = kCombinePrefetch;
-    for (; s + 2 <= n; s += 2) {
-      acc2 += weight[s] * po[s * so + d0];
-      acc3 += weight[s + 1] * po[(s + 1) * so + d0];
-    }
-    if (s < n) acc2 += weight[s] * po[s * so + d0];
-    Elem<QT>::store(out + d0, ((acc0 + acc1) + (acc2 + acc3)) * inv);
-  }
+  for (int i = 0; i < CPL; ++i) Elem<QT>::store(out + i, o[i]);
 }
 
 // Merge the splits of one (row, head): O = sum_s e^{m_s-M} o_s / sum_s e^{m_s-M} l_s.
@@ -734,7 +742,7 @@ static int launch_mfma_d(DecodeParams& p, hipStream_t stream) {
   if (int rc = check_launch("decode_partial_mfma")) return rc;
   {
     KernelTimer timer_("decode_combine", stream);
-    hipLaunchKernelGGL((decode_combine_balanced<bf16_t>), dim3(p.B * p.H), dim3(256), 0, stream, p);
+    hipLaunchKernelGGL((decode_combine_balanced<bf16_t, D>), dim3(ceil_div(p.B * p.H, kCombineWaves)), dim3(64 * kCombineWaves), 0, stream, p);
   }
   return check_launch("decode_combine");
 }
