@@ -64,24 +64,28 @@ struct Params {
   int packed;  // weight in the tile order of qa_fp8_pack_weight
 };
 
-// Eight fp8 E4M3 codes (two dwords) as an 8-element bf16 or fp16 operand, exactly.
+// Eight fp8 E4M3 codes (two dwords) as an 8-element bf16 or fp16 operand, exactly: every E4M3
+// value is representable in both.  v_cvt_scalef32_pk_{f16,bf16}_fp8 turns two codes (one 16-bit
+// word of the dword) into two 16-bit values in one instruction; the scale 1.0 leaves them as they
+// are.  Element e is byte e of (lo, hi), the order v_cvt_pk_f32_fp8 gives as well.
+typedef _Float16 f16x2_v __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x2_v __attribute__((ext_vector_type(2)));
 template <typename V>
 __device__ __forceinline__ V fp8x8_operand(unsigned lo, unsigned hi) {
-  typedef decltype(V{}[0]) elem_ref;
-  typedef typename std::remove_reference<elem_ref>::type E;
-  const f32x2_v a = __builtin_amdgcn_cvt_pk_f32_fp8(lo, false);
-  const f32x2_v b = __builtin_amdgcn_cvt_pk_f32_fp8(lo, true);
-  const f32x2_v c = __builtin_amdgcn_cvt_pk_f32_fp8(hi, false);
-  const f32x2_v d = __builtin_amdgcn_cvt_pk_f32_fp8(hi, true);
   V r;
-  r[0] = static_cast<E>(a[0]);
-  r[1] = static_cast<E>(a[1]);
-  r[2] = static_cast<E>(b[0]);
-  r[3] = static_cast<E>(b[1]);
-  r[4] = static_cast<E>(c[0]);
-  r[5] = static_cast<E>(c[1]);
-  r[6] = static_cast<E>(d[0]);
-  r[7] = static_cast<E>(d[1]);
+  if constexpr (std::is_same<V, f16x8_v>::value) {
+    const f16x2_v a = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(lo, 1.0f, false);
+    const f16x2_v b = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(lo, 1.0f, true);
+    const f16x2_v c = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(hi, 1.0f, false);
+    const f16x2_v d = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(hi, 1.0f, true);
+    r = __builtin_shufflevector(__builtin_shufflevector(a, b, 0, 1, 2, 3), __builtin_shufflevector(c, d, 0, 1, 2, 3), 0, 1, 2, 3, 4, 5, 6, 7);
+  } else {
+    const bf16x2_v a = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(lo, 1.0f, false);
+    const bf16x2_v b = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(lo, 1.0f, true);
+    const bf16x2_v c = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(hi, 1.0f, false);
+    const bf16x2_v d = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(hi, 1.0f, true);
+    r = __builtin_shufflevector(__builtin_shufflevector(a, b, 0, 1, 2, 3), __builtin_shufflevector(c, d, 0, 1, 2, 3), 0, 1, 2, 3, 4, 5, 6, 7);
+  }
   return r;
 }
 
@@ -468,6 +472,135 @@ __global__ __launch_bounds__(WNT) void fp8_linear_wide_kernel(Params p) {
   }
 }
 
+// ---- x-resident path (17-256 rows of 16-bit x, in_features <= XR_KMAX): no barrier in the K loop.
+//
+// Work item: 128 weight rows (one row of 128 x 128 scale blocks) x 32 rows of x x all of K, 8 waves:
+// wave w multiplies weight tile w (16 rows) with both 16-row x tiles.  The workgroup's x (32 rows x
+// K, 16-bit, at most 128 KB) is copied into LDS once, before the K loop (global_load_lds_dwordx4,
+// 16-byte chunks XOR-swizzled by row as in the wide path, so the 16 rows of an operand read fall on
+// distinct banks), and stays there; each wave loads its own weight tile straight into registers,
+// all of K at once (32 bytes per lane and block, already in operand order for both weight
+// layouts).  With no barrier and no copies inside the loop, the operand reads of one block are
+// issued before the products of the one before.  The workgroups of one weight group differ in blockIdx.y only,
+// so when the group count is a multiple of 8 they share an XCD and its L2 for the weight.
+constexpr int XR_ROWS = 32;      // x rows per workgroup (two 16-row tiles)
+constexpr int XR_WN = 128;       // weight rows per workgroup (a wave per 16-row tile)
+constexpr int XR_KMAX = 2048;    // in_features the x tile can hold
+constexpr int kXresXBytes = XR_ROWS * XR_KMAX * 2;
+constexpr int kXresBytes = kXresXBytes + (XR_KMAX / KB) * 4;  // + the block scales (fp32)
+
+template <int MODE>
+__global__ __launch_bounds__(WNT) void fp8_linear_xres_kernel(Params p) {
+  static_assert(MODE == X_BF16 || MODE == X_F16, "16-bit x only");
+  typedef typename ModeTraits<MODE>::V V;
+  extern __shared__ __align__(16) unsigned char smem[];
+  const uint32_t smem_lds = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(smem));
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int lr = lane & 15;
+  const int lg = lane >> 4;
+  const int64_t m0 = static_cast<int64_t>(blockIdx.y) * XR_ROWS;
+  const int64_t nkb = p.K / KB;
+  const int64_t n_blk = static_cast<int64_t>(blockIdx.x) * XR_WN;
+  const int64_t n_t = n_blk + 16 * wave;
+  const int64_t row_bytes = p.K * 2;  // one x row in LDS
+
+  // the block scales of the workgroup's weight rows (loaded first: the waits below count on it)
+  float* s_scale = reinterpret_cast<float*>(smem + kXresXBytes);
+  const float sc_in = tid < nkb ? bf16_to_f32(p.scale[(n_blk / KB) * p.scale_cols + tid]) : 0.f;
+  // x into LDS: copy j fills LDS bytes [1 KB j, 1 KB (j + 1)); lane l's 16 bytes there are row r,
+  // position c of it, and hold logical chunk c ^ (r mod 16).  Rows past M read row M - 1 (their
+  // outputs are never stored).
+  const uint32_t row_chunks = static_cast<uint32_t>(p.K / 8);  // 16-byte chunks per row
+  const int copies = static_cast<int>(XR_ROWS * row_chunks / 64);
+  const char* xbase = static_cast<const char*>(p.x);
+  for (int j = wave; j < copies; j += WNT / 64) {
+    const uint32_t q = 64u * static_cast<uint32_t>(j) + static_cast<uint32_t>(lane);  // chunk index in the tile
+    const uint32_t r = q / row_chunks;
+    const uint32_t c = q - r * row_chunks;
+    const int64_t m = min64(m0 + r, p.M - 1);
+    lds_copy16(xbase + m * p.x_stride * 2 + 16 * (c ^ (r & 15)), smem_lds + 1024u * static_cast<uint32_t>(j));
+  }
+  // this wave's weight tile, all of it into registers at once (at most XR_KMAX / KB blocks of 32
+  // bytes per lane; block kb at wsrc + kb * wstep, the lane's two 16-byte pieces woff1 apart;
+  // blocks past the last read the last one again and are not used)
+  constexpr int NB = XR_KMAX / KB;
+  const uint8_t* wsrc = p.packed ? p.w + (n_t / 16) * nkb * 2048 + 16 * lane : p.w + (n_t + lr) * p.K + 32 * lg;
+  const int64_t wstep = p.packed ? 2048 : KB;
+  const int64_t woff1 = p.packed ? 1024 : 16;
+  u32x4_v w0[NB], w1[NB];
+#pragma unroll
+  for (int d = 0; d < NB; ++d) {
+    const uint8_t* src = wsrc + min64(d, nkb - 1) * wstep;
+    w0[d] = *reinterpret_cast<const u32x4_v*>(src);
+    w1[d] = *reinterpret_cast<const u32x4_v*>(src + woff1);
+  }
+  // The scale and the x copies have landed once at most the 2 NB weight loads issued after them
+  // are in flight (the copies are invisible to the compiler, so it cannot place this wait; its
+  // own waits for the weight blocks, all younger than the copies, stay exact).  The weights keep
+  // streaming into the loop.
+  static_assert(2 * NB < 64, "vmcnt immediate");
+  __builtin_amdgcn_s_waitcnt((0x0F70 & ~0xC00F) | ((2 * NB) & 15) | (((2 * NB) >> 4) << 14));
+  if (tid < nkb) s_scale[tid] = sc_in;
+  lds_barrier();
+
+  // the x operands of block kb: tile i, k-step s (row 16 i + lr, chunk 16 kb + 4 lg + s, swizzled)
+  auto read_x = [&](int64_t kb, V (&bx)[4][2]) {
+#pragma unroll
+    for (int s = 0; s < 4; ++s)
+#pragma unroll
+      for (int i = 0; i < 2; ++i)
+        bx[s][i] = *reinterpret_cast<const V*>(smem + (16 * i + lr) * row_bytes + 16 * ((kb * 16 + 4 * lg + s) ^ lr));
+  };
+  f32x4_v acc[2];
+#pragma unroll
+  for (int i = 0; i < 2; ++i) acc[i] = f32x4_v{0.f, 0.f, 0.f, 0.f};
+  // the operand reads of block kb + 1 are issued before the products of block kb
+  V bxn[4][2];
+  read_x(0, bxn);
+#pragma unroll
+  for (int kb = 0; kb < NB; ++kb) {
+    V bx[4][2];
+#pragma unroll
+    for (int s = 0; s < 4; ++s)
+#pragma unroll
+      for (int i = 0; i < 2; ++i) bx[s][i] = bxn[s][i];
+    if (kb + 1 < NB) read_x(min64(kb + 1, nkb - 1), bxn);
+    if (kb < nkb) {
+      f32x4_v blk[2];
+#pragma unroll
+      for (int i = 0; i < 2; ++i) blk[i] = f32x4_v{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int s = 0; s < 4; ++s) {
+        const u32x4_v& w = s < 2 ? w0[kb] : w1[kb];
+        const V a = fp8x8_operand<V>(w[2 * (s & 1)], w[2 * (s & 1) + 1]);
+#pragma unroll
+        for (int i = 0; i < 2; ++i) blk[i] = mfma(a, bx[s][i], blk[i]);
+      }
+      const float sc = s_scale[kb];
+#pragma unroll
+      for (int i = 0; i < 2; ++i) acc[i] += sc * blk[i];
+    }
+  }
+
+  // C = W X^T: lane (lg, lr) of tile i holds y[m0 + 16 i + lr][n_t + 4 lg + r]
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    const int64_t m = m0 + 16 * i + lr;
+    if (m >= p.M) continue;
+    const int64_t n = n_t + 4 * lg;
+    if (p.y_f32) {
+      *reinterpret_cast<f32x4_v*>(static_cast<float*>(p.y) + m * p.y_stride + n) = acc[i];
+    } else {
+      uint2 packed;
+      packed.x = static_cast<uint32_t>(f32_to_bf16(acc[i][0])) | (static_cast<uint32_t>(f32_to_bf16(acc[i][1])) << 16);
+      packed.y = static_cast<uint32_t>(f32_to_bf16(acc[i][2])) | (static_cast<uint32_t>(f32_to_bf16(acc[i][3])) << 16);
+      *reinterpret_cast<uint2*>(static_cast<bf16_t*>(p.y) + m * p.y_stride + n) = packed;
+    }
+  }
+}
+
 // fp32 x (16 rows or more) to fp16 once per call, round to nearest even (the reference's
 // float_rows_to_half_kernel, src/csrc/fp8_linear_cuda.cu:146-150): staging 16-bit x keeps the
 // main kernel's register ring small enough for its LDS operand reads to overlap.
@@ -492,6 +625,7 @@ __global__ __launch_bounds__(256) void fp8_cast_x_kernel(const float* __restrict
 }
 
 struct Plan {
+  int xres;  // 16-bit x of 17..256 rows, in_features <= XR_KMAX: the x-resident kernel
   int wide;  // 16-bit x of 17..256 rows: the wide kernel (no K split), xt tiles of 16 rows
   int xt;
   int ms;
@@ -506,8 +640,17 @@ struct Plan {
 // workgroups with at least four K blocks each.
 inline Plan make_plan(int64_t M, int64_t N, int64_t K) {
   Plan pl{};
-  if (M > 16 && M <= 256) {
+  if (M > 16 && M <= 256 && K <= XR_KMAX) {
     // x is 16-bit here in both input dtypes (fp32 x of 16 rows or more is cast to fp16 first)
+    pl.xres = 1;
+    pl.mtiles = (M + XR_ROWS - 1) / XR_ROWS;
+    pl.ntiles = N / XR_WN;
+    pl.ksplit = 1;
+    pl.blocks_per_split = static_cast<int>(K / KB);
+    pl.workspace = M * K * 2;  // the fp16 copy of an fp32 x
+    return pl;
+  }
+  if (M > 16 && M <= 256) {
     pl.wide = 1;
     pl.xt = M <= 32 ? 2 : 4;
     pl.mtiles = (M + 16 * pl.xt - 1) / (16 * pl.xt);
@@ -543,6 +686,20 @@ int launch_wide(const Plan& pl, const Params& p, hipStream_t stream) {
   }
   const dim3 grid(static_cast<unsigned>(pl.ntiles), static_cast<unsigned>(pl.mtiles));
   hipLaunchKernelGGL((fp8_linear_wide_kernel<MODE, XT>), grid, dim3(WNT), WideSmem<XT>::kBytes, stream, p);
+  return 0;
+}
+
+template <int MODE>
+int launch_xres(const Plan& pl, const Params& p, hipStream_t stream) {
+  static bool attr_set = false;  // the x tile is above the 64 KB default of dynamic LDS
+  if (!attr_set) {
+    const hipError_t err = hipFuncSetAttribute(reinterpret_cast<const void*>(&fp8_linear_xres_kernel<MODE>),
+                                               hipFuncAttributeMaxDynamicSharedMemorySize, kXresBytes);
+    if (err != hipSuccess) return fail("fp8_linear: cannot reserve %d bytes of LDS: %s", kXresBytes, hipGetErrorString(err));
+    attr_set = true;
+  }
+  const dim3 grid(static_cast<unsigned>(pl.ntiles), static_cast<unsigned>(pl.mtiles));
+  hipLaunchKernelGGL((fp8_linear_xres_kernel<MODE>), grid, dim3(WNT), kXresBytes, stream, p);
   return 0;
 }
 
@@ -635,6 +792,15 @@ extern "C" int qa_fp8_linear(const void* x, int32_t x_dtype, int64_t x_stride, i
   p.ksplit = pl.ksplit;
   p.y_f32 = y_dtype == QA_F32;
   p.packed = weight_packed != 0;
+  if (pl.xres) {
+    int rc = 0;
+    {
+      KernelTimer timer_("fp8_linear", stream);
+      rc = mode == X_F16 ? launch_xres<X_F16>(pl, p, stream) : launch_xres<X_BF16>(pl, p, stream);
+    }
+    if (rc) return rc;
+    return check_launch("fp8_linear");
+  }
   if (pl.wide) {
     int rc = 0;
     {

@@ -54,12 +54,13 @@ def test_every_finite_e4m3_code_decodes_exactly() -> None:
     assert sorted(set(codes.ravel().tolist())) == [c for c in range(256) if (c & 0x7F) != 0x7F]
 
 
-def test_nan_code_gives_nan_like_the_reference_cpu_path() -> None:
+@pytest.mark.parametrize("rows", [2, 32])
+def test_nan_code_gives_nan_like_the_reference_cpu_path(rows) -> None:
     ops = _ops()
     codes = torch.zeros((128, 128), dtype=torch.uint8)
     codes[5, 3] = 0x7F
-    out = ops.fp8_e4m3_bf16_linear(torch.ones((2, 128), device=DEV), codes.to(DEV), torch.ones((1, 1), dtype=torch.bfloat16, device=DEV))
-    ref = oracle.linear(torch.ones((2, 128)), codes.numpy(), torch.ones((1, 1), dtype=torch.bfloat16))
+    out = ops.fp8_e4m3_bf16_linear(torch.ones((rows, 128), device=DEV), codes.to(DEV), torch.ones((1, 1), dtype=torch.bfloat16, device=DEV))
+    ref = oracle.linear(torch.ones((rows, 128)), codes.numpy(), torch.ones((1, 1), dtype=torch.bfloat16))
     assert torch.isnan(out[:, 5]).all().item() and torch.isnan(ref[:, 5]).all().item()
     assert (out.cpu()[:, torch.arange(128) != 5] == 0).all().item()
 
@@ -79,7 +80,7 @@ def test_matches_reference_test_case() -> None:
         _close_to_fp64(out, oracle.linear_fp64(x, codes, scale), fp16_input=batch >= 16)
 
 
-@pytest.mark.parametrize("rows,n,k", [(1, 256, 512), (37, 384, 1024), (128, 1024, 4096), (200, 512, 768), (4096, 256, 256)])
+@pytest.mark.parametrize("rows,n,k", [(1, 256, 512), (37, 384, 1024), (128, 1024, 2048), (128, 1024, 4096), (200, 512, 768), (256, 256, 2048), (4096, 256, 256)])
 def test_fp32_input_matches_fp64(rows, n, k) -> None:
     ops = _ops()
     gen = torch.Generator().manual_seed(rows + n + k)
@@ -148,7 +149,7 @@ def test_rejects_shapes_the_reference_rejects() -> None:
         ops.fp8_e4m3_bf16_linear(x, torch.zeros((128, 256), dtype=torch.uint8, device=DEV), torch.ones((1, 2), device=DEV))
 
 
-@pytest.mark.parametrize("rows,n,k,xdt", [(1, 256, 512, torch.float32), (37, 384, 1024, torch.float32), (128, 1024, 4096, torch.bfloat16)])
+@pytest.mark.parametrize("rows,n,k,xdt", [(1, 256, 512, torch.float32), (37, 384, 1024, torch.float32), (128, 1024, 2048, torch.bfloat16), (128, 1024, 4096, torch.bfloat16)])
 def test_packed_weight_layout_and_identical_results(rows, n, k, xdt) -> None:
     ops = _ops()
     gen = torch.Generator().manual_seed(rows * 7 + k)
