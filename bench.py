@@ -43,7 +43,7 @@ TRAFFIC_DELTA = 822636636  # chunk_kernel alone; the step (with prep_kernel) mov
 TRAFFIC_PREFILL = 888510552  # average over the eight per-chunk launches
 TRAFFIC_PROLOGUE = 675674420
 TRAFFIC_OUTPUT_NORM = 805389585
-TRAFFIC_FP8_LINEAR = 26850307  # cast + wide kernel, from profiles/fp8_linear_config5_batch.md
+TRAFFIC_FP8_LINEAR = 29648896  # x-resident kernel (one launch), from profiles/fp8_linear_config5_batch.md
 SECONDARY_WARM_MS = 100.0  # wall time of untimed steps before each secondary (config 3, 4, 5) measurement
 MFMA_BF16_PEAK_TFLOPS = 2500.0  # MI355X dense bf16/fp16 MFMA, TFLOP/s
 
@@ -872,7 +872,7 @@ def main() -> int:
                        "rows": fw["rows"], "out_features": fw["out"], "in_features": fw["in"]},
             "roofline": {"bound": "hbm", "achieved": round(fgbs, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(fgbs / HBM_PEAK_GBS, 4),
                          "traffic": TRAFFIC_FP8_LINEAR, "algo_bytes_per_launch": fw["algo_bytes"], "algo_flop_per_launch": fw["flops"],
-                         "kernel": "qa::f8l::fp8_cast_x_kernel + fp8_linear_wide_kernel<X_F16, 4> (packed weight, one pass over K)",
+                         "kernel": "qa::f8l::fp8_linear_xres_kernel<X_F16, true> (fp32 x rounded to fp16 as it is staged, x resident in LDS, packed weight streamed into registers, one launch)",
                          "kernel_avg_us": round(f_ms * 1e3, 2), "kernels": fkern},
         }
         del fw

@@ -489,9 +489,13 @@ constexpr int XR_KMAX = 2048;    // in_features the x tile can hold
 constexpr int kXresXBytes = XR_ROWS * XR_KMAX * 2;
 constexpr int kXresBytes = kXresXBytes + (XR_KMAX / KB) * 4;  // + the block scales (fp32)
 
-template <int MODE>
+// XCAST: x is fp32 and is rounded to fp16 (to nearest even, as fp8_cast_x_kernel does) while it is
+// staged, in two rounds of eight 16-byte chunks per thread through registers; otherwise x is 16-bit
+// and goes to LDS by copies.
+template <int MODE, bool XCAST>
 __global__ __launch_bounds__(WNT) void fp8_linear_xres_kernel(Params p) {
-  static_assert(MODE == X_BF16 || MODE == X_F16, "16-bit x only");
+  static_assert(MODE == X_BF16 || MODE == X_F16, "16-bit x operands only");
+  static_assert(!XCAST || MODE == X_F16, "fp32 x is rounded to fp16");
   typedef typename ModeTraits<MODE>::V V;
   extern __shared__ __align__(16) unsigned char smem[];
   const uint32_t smem_lds = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(smem));
@@ -509,40 +513,89 @@ __global__ __launch_bounds__(WNT) void fp8_linear_xres_kernel(Params p) {
   // the block scales of the workgroup's weight rows (loaded first: the waits below count on it)
   float* s_scale = reinterpret_cast<float*>(smem + kXresXBytes);
   const float sc_in = tid < nkb ? bf16_to_f32(p.scale[(n_blk / KB) * p.scale_cols + tid]) : 0.f;
-  // x into LDS: copy j fills LDS bytes [1 KB j, 1 KB (j + 1)); lane l's 16 bytes there are row r,
-  // position c of it, and hold logical chunk c ^ (r mod 16).  Rows past M read row M - 1 (their
-  // outputs are never stored).
-  const uint32_t row_chunks = static_cast<uint32_t>(p.K / 8);  // 16-byte chunks per row
-  const int copies = static_cast<int>(XR_ROWS * row_chunks / 64);
-  const char* xbase = static_cast<const char*>(p.x);
-  for (int j = wave; j < copies; j += WNT / 64) {
-    const uint32_t q = 64u * static_cast<uint32_t>(j) + static_cast<uint32_t>(lane);  // chunk index in the tile
-    const uint32_t r = q / row_chunks;
-    const uint32_t c = q - r * row_chunks;
-    const int64_t m = min64(m0 + r, p.M - 1);
-    lds_copy16(xbase + m * p.x_stride * 2 + 16 * (c ^ (r & 15)), smem_lds + 1024u * static_cast<uint32_t>(j));
-  }
-  // this wave's weight tile, all of it into registers at once (at most XR_KMAX / KB blocks of 32
-  // bytes per lane; block kb at wsrc + kb * wstep, the lane's two 16-byte pieces woff1 apart;
-  // blocks past the last read the last one again and are not used)
+  const uint32_t row_chunks = static_cast<uint32_t>(p.K / 8);  // 16-byte fp16 chunks per x row
+  // this wave's weight tile, all of it into registers (at most XR_KMAX / KB blocks of 32 bytes per
+  // lane; block kb at wsrc + kb * wstep, the lane's two 16-byte pieces woff1 apart; blocks past the
+  // last read the last one again and are not used), in halves of NB / 2 blocks
   constexpr int NB = XR_KMAX / KB;
   const uint8_t* wsrc = p.packed ? p.w + (n_t / 16) * nkb * 2048 + 16 * lane : p.w + (n_t + lr) * p.K + 32 * lg;
   const int64_t wstep = p.packed ? 2048 : KB;
   const int64_t woff1 = p.packed ? 1024 : 16;
   u32x4_v w0[NB], w1[NB];
+  auto wload = [&](int h) {
 #pragma unroll
-  for (int d = 0; d < NB; ++d) {
-    const uint8_t* src = wsrc + min64(d, nkb - 1) * wstep;
-    w0[d] = *reinterpret_cast<const u32x4_v*>(src);
-    w1[d] = *reinterpret_cast<const u32x4_v*>(src + woff1);
+    for (int d = h * NB / 2; d < (h + 1) * NB / 2; ++d) {
+      const uint8_t* src = wsrc + min64(d, nkb - 1) * wstep;
+      w0[d] = *reinterpret_cast<const u32x4_v*>(src);
+      w1[d] = *reinterpret_cast<const u32x4_v*>(src + woff1);
+    }
+  };
+  if constexpr (XCAST) {
+    // Thread t stages the fp16 chunks q = t + WNT i (i < nkb: row q / row_chunks, chunk c = q mod
+    // row_chunks, 8 fp32 values each) at row r, position c ^ (r mod 16); rows past M read row M - 1.
+    // Round h converts i in [8 h, 8 h + 8): its loads, then half h of the weight loads, then the
+    // conversion, so the compiler's waits for the x loads leave the weight loads in flight.
+    static_assert(NB == 16, "two rounds of eight chunks");
+    const float* xf = static_cast<const float*>(p.x);
+    float4 xa[8][2];
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {
+        const int i = 8 * h + u;
+        if (i < nkb) {
+          const uint32_t q = static_cast<uint32_t>(tid) + WNT * static_cast<uint32_t>(i);
+          const uint32_t r = q / row_chunks;
+          const float* src = xf + min64(m0 + r, p.M - 1) * p.x_stride + 8 * (q - r * row_chunks);
+          xa[u][0] = *reinterpret_cast<const float4*>(src);
+          xa[u][1] = *reinterpret_cast<const float4*>(src + 4);
+        }
+      }
+      wload(h);
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {
+        const int i = 8 * h + u;
+        if (i < nkb) {
+          const uint32_t q = static_cast<uint32_t>(tid) + WNT * static_cast<uint32_t>(i);
+          const uint32_t r = q / row_chunks;
+          const uint32_t c = q - r * row_chunks;
+          f16x8_v v;
+          v[0] = static_cast<_Float16>(xa[u][0].x);
+          v[1] = static_cast<_Float16>(xa[u][0].y);
+          v[2] = static_cast<_Float16>(xa[u][0].z);
+          v[3] = static_cast<_Float16>(xa[u][0].w);
+          v[4] = static_cast<_Float16>(xa[u][1].x);
+          v[5] = static_cast<_Float16>(xa[u][1].y);
+          v[6] = static_cast<_Float16>(xa[u][1].z);
+          v[7] = static_cast<_Float16>(xa[u][1].w);
+          *reinterpret_cast<f16x8_v*>(smem + r * row_bytes + 16 * (c ^ (r & 15))) = v;
+        }
+      }
+    }
+    if (tid < nkb) s_scale[tid] = sc_in;
+  } else {
+    // x into LDS: copy j fills LDS bytes [1 KB j, 1 KB (j + 1)); lane l's 16 bytes there are row r,
+    // position c of it, and hold logical chunk c ^ (r mod 16).  Rows past M read row M - 1 (their
+    // outputs are never stored).
+    const int copies = static_cast<int>(XR_ROWS * row_chunks / 64);
+    const char* xbase = static_cast<const char*>(p.x);
+    for (int j = wave; j < copies; j += WNT / 64) {
+      const uint32_t q = 64u * static_cast<uint32_t>(j) + static_cast<uint32_t>(lane);  // chunk index in the tile
+      const uint32_t r = q / row_chunks;
+      const uint32_t c = q - r * row_chunks;
+      const int64_t m = min64(m0 + r, p.M - 1);
+      lds_copy16(xbase + m * p.x_stride * 2 + 16 * (c ^ (r & 15)), smem_lds + 1024u * static_cast<uint32_t>(j));
+    }
+    wload(0);
+    wload(1);
+    // The scale and the x copies have landed once at most the 2 NB weight loads issued after them
+    // are in flight (the copies are invisible to the compiler, so it cannot place this wait; its
+    // own waits for the weight blocks, all younger than the copies, stay exact).  The weights keep
+    // streaming into the loop.
+    static_assert(2 * NB < 64, "vmcnt immediate");
+    __builtin_amdgcn_s_waitcnt((0x0F70 & ~0xC00F) | ((2 * NB) & 15) | (((2 * NB) >> 4) << 14));
+    if (tid < nkb) s_scale[tid] = sc_in;
   }
-  // The scale and the x copies have landed once at most the 2 NB weight loads issued after them
-  // are in flight (the copies are invisible to the compiler, so it cannot place this wait; its
-  // own waits for the weight blocks, all younger than the copies, stay exact).  The weights keep
-  // streaming into the loop.
-  static_assert(2 * NB < 64, "vmcnt immediate");
-  __builtin_amdgcn_s_waitcnt((0x0F70 & ~0xC00F) | ((2 * NB) & 15) | (((2 * NB) >> 4) << 14));
-  if (tid < nkb) s_scale[tid] = sc_in;
   lds_barrier();
 
   // the x operands of block kb: tile i, k-step s (row 16 i + lr, chunk 16 kb + 4 lg + s, swizzled)
@@ -689,17 +742,17 @@ int launch_wide(const Plan& pl, const Params& p, hipStream_t stream) {
   return 0;
 }
 
-template <int MODE>
+template <int MODE, bool XCAST>
 int launch_xres(const Plan& pl, const Params& p, hipStream_t stream) {
   static bool attr_set = false;  // the x tile is above the 64 KB default of dynamic LDS
   if (!attr_set) {
-    const hipError_t err = hipFuncSetAttribute(reinterpret_cast<const void*>(&fp8_linear_xres_kernel<MODE>),
+    const hipError_t err = hipFuncSetAttribute(reinterpret_cast<const void*>(&fp8_linear_xres_kernel<MODE, XCAST>),
                                                hipFuncAttributeMaxDynamicSharedMemorySize, kXresBytes);
     if (err != hipSuccess) return fail("fp8_linear: cannot reserve %d bytes of LDS: %s", kXresBytes, hipGetErrorString(err));
     attr_set = true;
   }
   const dim3 grid(static_cast<unsigned>(pl.ntiles), static_cast<unsigned>(pl.mtiles));
-  hipLaunchKernelGGL((fp8_linear_xres_kernel<MODE>), grid, dim3(WNT), kXresBytes, stream, p);
+  hipLaunchKernelGGL((fp8_linear_xres_kernel<MODE, XCAST>), grid, dim3(WNT), kXresBytes, stream, p);
   return 0;
 }
 
@@ -772,7 +825,9 @@ extern "C" int qa_fp8_linear(const void* x, int32_t x_dtype, int64_t x_stride, i
   // fp32 x: exact-ish hi + lo below 16 rows, fp16 from 16 rows on (the reference's fp32 matvec for
   // batch < kDefaultCublasBatchThreshold = 16, its fp16 GEMM otherwise, src/csrc/fp8_linear_cuda.cu:1411-1460)
   const int mode = x_dtype == QA_BF16 ? X_BF16 : rows < 16 ? X_SPLIT : X_F16;
-  if (mode == X_F16) {
+  // the x-resident kernel rounds fp32 x to fp16 itself while staging it
+  const bool xcast = pl.xres && mode == X_F16;
+  if (mode == X_F16 && !xcast) {
     _Float16* x16 = reinterpret_cast<_Float16*>(static_cast<char*>(workspace) + pl.partial_bytes);
     const int64_t groups = rows * in_features / 8;
     QA_REQUIRE((groups + 255) / 256 <= 0x7fffffff, "fp8_linear: input too large");
@@ -796,7 +851,7 @@ extern "C" int qa_fp8_linear(const void* x, int32_t x_dtype, int64_t x_stride, i
     int rc = 0;
     {
       KernelTimer timer_("fp8_linear", stream);
-      rc = mode == X_F16 ? launch_xres<X_F16>(pl, p, stream) : launch_xres<X_BF16>(pl, p, stream);
+      rc = xcast ? launch_xres<X_F16, true>(pl, p, stream) : launch_xres<X_BF16, false>(pl, p, stream);
     }
     if (rc) return rc;
     return check_launch("fp8_linear");
