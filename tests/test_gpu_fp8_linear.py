@@ -80,7 +80,7 @@ def test_matches_reference_test_case() -> None:
         _close_to_fp64(out, oracle.linear_fp64(x, codes, scale), fp16_input=batch >= 16)
 
 
-@pytest.mark.parametrize("rows,n,k", [(1, 256, 512), (37, 384, 1024), (128, 1024, 2048), (128, 1024, 4096), (200, 512, 768), (256, 256, 2048), (4096, 256, 256)])
+@pytest.mark.parametrize("rows,n,k", [(1, 256, 512), (37, 384, 1024), (48, 256, 640), (128, 1024, 2048), (128, 1024, 4096), (200, 512, 768), (256, 256, 2048), (4096, 256, 256)])
 def test_fp32_input_matches_fp64(rows, n, k) -> None:
     ops = _ops()
     gen = torch.Generator().manual_seed(rows + n + k)
