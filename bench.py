@@ -607,7 +607,7 @@ def hybrid_workload(device: str, *, seed: int = 0, batch: int = 128, groups: int
 
 
 def time_hybrid(w, steps: int, warmup: int) -> float:
-    """One step = every layer's attention for one decode token of all sequences (KV append + paged decode, or conv update + fused delta step)."""
+    """One step = every layer's attention for one decode token of all sequences (KV append + paged decode, or the delta step with its conv update fused in)."""
     import torch
 
     import hip_ops
@@ -617,8 +617,8 @@ def time_hybrid(w, steps: int, warmup: int) -> float:
     def step():
         for g in range(w["groups"]):
             for lin in w["linear"][3 * g : 3 * g + 3]:
-                act = hip_ops.causal_conv1d_update(x["mixed"], lin["conv"], lin["conv_w"])
-                hip_ops.gated_delta_step(act, x["a"], x["b"], lin["a_log"], lin["dt_bias"], lin["state"], key_heads=w["key_heads"])
+                hip_ops.gated_delta_step_conv(x["mixed"], lin["conv"], lin["conv_w"], x["a"], x["b"], lin["a_log"], lin["dt_bias"], lin["state"],
+                                              key_heads=w["key_heads"])
             full = w["full"][g]
             hip_ops.paged_kv_append(x["new_k"], x["new_v"], full["key_pool"], full["value_pool"], full["tables"], x["positions"], w["bs"])
             hip_ops.paged_attention_decode_batched(x["query"], full["tables"], full["key_pool"], full["value_pool"], x["lens"], w["bs"])

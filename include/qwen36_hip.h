@@ -333,6 +333,30 @@ int qa_gated_delta_step_norm(const float* qkv, int64_t qkv_stride_b,
                              int64_t batch, int32_t key_heads, int32_t value_heads,
                              int32_t key_dim, int32_t value_dim, hipStream_t stream);
 
+/* qa_causal_conv1d_update and qa_gated_delta_step(_norm) in one kernel:
+ * x (B, 2*Hqk*dk + Hv*dv) is the token's raw in_proj_qkv row (float32 or
+ * bfloat16, rows of x_stride_b elements); conv_state (state_rows, C, K-1)
+ * fp32 (rows of conv_state_stride_b elements) and state are both updated in
+ * place at slot(b); conv_weight (C, K) fp32, 2 <= K <= 8.  z == NULL runs
+ * no output stage (then norm_weight is ignored).  A workgroup per (row, key
+ * head) owns the key head's q/k channels and its value heads' v channels,
+ * so every conv state entry has one writer; Hv / Hqk must be 1, 2 or 4.
+ * The activations are those of qa_causal_conv1d_update, so the outputs and
+ * states equal the two calls'.  Replaces, per decode token, the conv1d with
+ * cache of src/reference_ops.py:252-258 followed by the steps of
+ * :271-322 (src/tp_runtime.py:2613-2717), in one launch.                  */
+int qa_gated_delta_step_conv(const void* x, int32_t x_dtype, int64_t x_stride_b,
+                             float* conv_state, int64_t conv_state_stride_b,
+                             const float* conv_weight, int32_t conv_kernel,
+                             const void* a, const void* b, int32_t ab_dtype, int64_t ab_stride_b,
+                             const float* a_log, const float* dt_bias,
+                             float* state, int64_t state_stride_slot, const void* slots, int32_t slots_dtype,
+                             int64_t state_rows, const void* z, int32_t z_dtype, int64_t z_stride_b,
+                             const void* norm_weight, int32_t norm_dtype, float eps,
+                             void* out, int32_t out_dtype, int64_t out_stride_b,
+                             int64_t batch, int32_t key_heads, int32_t value_heads,
+                             int32_t key_dim, int32_t value_dim, hipStream_t stream);
+
 /* Chunked gated delta-rule prefill of one linear-attention layer, from the
  * raw in_proj outputs.  mixed_qkv (B, T, 2*Hqk*dk + Hv*dv) bfloat16,
  * a, b (B, T, Hv), a_log/dt_bias (Hv) fp32, conv_weight (C, 4) fp32,

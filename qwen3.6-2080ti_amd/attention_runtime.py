@@ -392,15 +392,22 @@ def linear_attention_decode_batch(
     ``z`` (the ``in_proj_z`` output ``(B, Hv*dv)``) and ``norm_weight``, after it
     (``src/reference_ops.py:284-287``), fused into the same kernel.  This
     replaces the stack / run / scatter of ``src/tp_runtime.py:2613-2717``.
+    With 1, 2 or 4 value heads per key head the conv update runs inside the
+    step's kernel (one launch, no activation round trip through HBM);
+    otherwise it is a launch of its own before the step.
     """
     import torch
 
     import hip_ops
 
     lin = config.linear_attention
+    odt = torch.bfloat16 if out_dtype is None else out_dtype
+    if lin.value_heads // lin.key_heads in (1, 2, 4):
+        return hip_ops.gated_delta_step_conv(mixed_qkv, pool.conv, conv_weight, a, b, a_log, dt_bias, pool.state, key_heads=lin.key_heads,
+                                             slots=slots, out_dtype=odt, z=z, norm_weight=norm_weight, eps=eps)
     act = hip_ops.causal_conv1d_update(mixed_qkv, pool.conv, conv_weight, slots)
     return hip_ops.gated_delta_step(act, a, b, a_log, dt_bias, pool.state, key_heads=lin.key_heads, slots=slots,
-                                    out_dtype=torch.bfloat16 if out_dtype is None else out_dtype, z=z, norm_weight=norm_weight, eps=eps)
+                                    out_dtype=odt, z=z, norm_weight=norm_weight, eps=eps)
 
 
 def linear_attention_prefill(mixed_qkv: Any, a: Any, b: Any, a_log: Any, dt_bias: Any, conv_weight: Any, config: AttentionConfig, *, conv_state: Any = None, initial_state: Any = None) -> tuple[Any, Any, Any]:

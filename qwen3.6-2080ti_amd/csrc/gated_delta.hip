@@ -27,6 +27,19 @@ __device__ __forceinline__ float load_any(const void* base, int dtype, int64_t i
   return dtype == QA_BF16 ? bf16_to_f32(reinterpret_cast<const bf16_t*>(base)[i]) : reinterpret_cast<const float*>(base)[i];
 }
 
+// A float32 or bfloat16 element as raw bits, converted later by bits_to_f32: a conversion inside
+// the dtype branch makes the compiler wait there for every load issued before it.
+__device__ __forceinline__ uint32_t load_bits(const void* base, bool bf16, int64_t i) {
+  uint32_t v;
+  if (bf16)
+    v = reinterpret_cast<const uint16_t*>(base)[i];
+  else
+    v = reinterpret_cast<const uint32_t*>(base)[i];
+  return v;
+}
+
+__device__ __forceinline__ float bits_to_f32(uint32_t v, bool bf16) { return __uint_as_float(bf16 ? v << 16 : v); }
+
 __device__ __forceinline__ void store_any(void* base, int dtype, int64_t i, float v) {
   if (dtype == QA_BF16)
     reinterpret_cast<bf16_t*>(base)[i] = f32_to_bf16(v);
@@ -182,12 +195,70 @@ __global__ __launch_bounds__(128) void delta_recurrent_generic(DeltaParams p) {
   }
 }
 
+// One token of the recurrence on the register-resident 128x128 state of 256 threads (thread
+// (w, rg, cg) owns rows 32 w + 8 rg + [0, 8) and columns 8 cg + [0, 8)): S *= decay,
+// delta = (v - S^T k) beta, S += k delta^T, o = S^T q (src/reference_ops.py:310-318).  The two
+// reductions over dk are shuffles inside each wave plus a 4-way sum across waves through red;
+// o[c] (column 8 cg + c) is complete in wave 0's row group 0.
+__device__ __forceinline__ void recurrence_token_128(float (&S)[8][8], const float (&kr)[8], const float (&qr)[8], const float (&vc)[8], float decay,
+                                                     float beta, float (&red)[2][4][128], int w, int rg, int cg, float (&o)[8]) {
+  const int col0 = 8 * cg;
+  float part[8];
+#pragma unroll
+  for (int c = 0; c < 8; ++c) {
+    float acc = 0.f;
+#pragma unroll
+    for (int r = 0; r < 8; ++r) {
+      S[r][c] *= decay;
+      acc += S[r][c] * kr[r];
+    }
+    part[c] = acc;
+  }
+#pragma unroll
+  for (int c = 0; c < 8; ++c) {
+    part[c] += __shfl_xor(part[c], 16, 64);
+    part[c] += __shfl_xor(part[c], 32, 64);
+  }
+  if (rg == 0) {
+#pragma unroll
+    for (int c = 0; c < 8; ++c) red[0][w][col0 + c] = part[c];
+  }
+  __syncthreads();
+  float delta[8];
+#pragma unroll
+  for (int c = 0; c < 8; ++c) {
+    const float kv = (red[0][0][col0 + c] + red[0][1][col0 + c]) + (red[0][2][col0 + c] + red[0][3][col0 + c]);
+    delta[c] = (vc[c] - kv) * beta;
+  }
+#pragma unroll
+  for (int c = 0; c < 8; ++c) {
+    float acc = 0.f;
+#pragma unroll
+    for (int r = 0; r < 8; ++r) {
+      S[r][c] += kr[r] * delta[c];
+      acc += S[r][c] * qr[r];
+    }
+    part[c] = acc;
+  }
+#pragma unroll
+  for (int c = 0; c < 8; ++c) {
+    part[c] += __shfl_xor(part[c], 16, 64);
+    part[c] += __shfl_xor(part[c], 32, 64);
+  }
+  if (rg == 0) {
+#pragma unroll
+    for (int c = 0; c < 8; ++c) red[1][w][col0 + c] = part[c];
+  }
+  __syncthreads();
+#pragma unroll
+  for (int c = 0; c < 8; ++c) o[c] = (red[1][0][col0 + c] + red[1][1][col0 + c]) + (red[1][2][col0 + c] + red[1][3][col0 + c]);
+}
+
 // dk = dv = 128: register-resident state, see the file header for the layout.
-template <bool FUSED, bool NORM = false>
+// Reference-compatible core over S tokens of prepared (B, H, S, d) inputs.
 __global__ __launch_bounds__(256) void delta_recurrent_128(DeltaParams p) {
   constexpr int DK = 128, DV = 128;
   __shared__ float red[2][4][DV];
-  __shared__ float nrm[2][4];
   const int64_t b = blockIdx.x / p.H;
   const int h = blockIdx.x - static_cast<int>(b) * p.H;
   const int w = threadIdx.x >> 6;
@@ -196,25 +267,8 @@ __global__ __launch_bounds__(256) void delta_recurrent_128(DeltaParams p) {
   const int cg = lane & 15;
   const int row0 = 32 * w + 8 * rg;
   const int col0 = 8 * cg;
-
-  const float* s_in;
-  float* s_out;
-  if (FUSED) {
-    const int64_t slot = slot_of(p.slots, p.slots_i64, b);
-    if (!slot_valid(slot, p.state_rows)) {
-      // the whole workgroup takes this branch (one row per workgroup); its 128 outputs are zeros
-      if (w == 0 && rg == 0) {
-#pragma unroll
-        for (int c = 0; c < 8; ++c) store_any(p.out, p.out_dtype, b * p.out_sb + static_cast<int64_t>(h) * DV + col0 + c, 0.f);
-      }
-      return;
-    }
-    s_in = p.state_in + slot * p.state_sb + static_cast<int64_t>(h) * DK * DV;
-    s_out = p.state_out + slot * p.state_sb + static_cast<int64_t>(h) * DK * DV;
-  } else {
-    s_in = p.state_in + (b * p.H + h) * DK * DV;
-    s_out = p.state_out + (b * p.H + h) * DK * DV;
-  }
+  const float* s_in = p.state_in + (b * p.H + h) * DK * DV;
+  float* s_out = p.state_out + (b * p.H + h) * DK * DV;
   float S[8][8];
 #pragma unroll
   for (int r = 0; r < 8; ++r) {
@@ -223,149 +277,247 @@ __global__ __launch_bounds__(256) void delta_recurrent_128(DeltaParams p) {
     S[r][0] = lo.x; S[r][1] = lo.y; S[r][2] = lo.z; S[r][3] = lo.w;
     S[r][4] = hi.x; S[r][5] = hi.y; S[r][6] = hi.z; S[r][7] = hi.w;
   }
-
-  const int T = FUSED ? 1 : static_cast<int>(p.S);
-  for (int t = 0; t < T; ++t) {
+  for (int64_t t = 0; t < p.S; ++t) {
+    const int64_t tok = (b * p.H + h) * p.S + t;
     float kr[8], qr[8], vc[8];
-    float decay, beta;
-    if (FUSED) {
-      const int qh = h / (p.H / p.Hqk);
-      const float* base = p.qkv + b * p.qkv_sb;
-      const float* qv = base + qh * DK;
-      const float* kvv = base + p.Hqk * DK + qh * DK;
-      const float* vv = base + 2 * p.Hqk * DK + h * DV;
-      float sq = 0.f, sk = 0.f;
 #pragma unroll
-      for (int r = 0; r < 8; ++r) {
-        qr[r] = qv[row0 + r];
-        kr[r] = kvv[row0 + r];
-        sq += qr[r] * qr[r];
-        sk += kr[r] * kr[r];
-      }
-#pragma unroll
-      for (int c = 0; c < 8; ++c) vc[c] = vv[col0 + c];
-      // sum over the 4 row groups of this wave (lanes xor 16, 32), then the 4 waves
-      sq += __shfl_xor(sq, 16, 64);
-      sq += __shfl_xor(sq, 32, 64);
-      sk += __shfl_xor(sk, 16, 64);
-      sk += __shfl_xor(sk, 32, 64);
-      if (lane == 0) {
-        nrm[0][w] = sq;
-        nrm[1][w] = sk;
-      }
-      __syncthreads();
-      sq = (nrm[0][0] + nrm[0][1]) + (nrm[0][2] + nrm[0][3]);
-      sk = (nrm[1][0] + nrm[1][1]) + (nrm[1][2] + nrm[1][3]);
-      // l2_norm (src/reference_ops.py:181-183) and q * dk^-0.5 (:304)
-      const float rq = rsqrtf(sq + 1e-6f) * rsqrtf(static_cast<float>(DK));
-      const float rk = rsqrtf(sk + 1e-6f);
-#pragma unroll
-      for (int r = 0; r < 8; ++r) {
-        qr[r] *= rq;
-        kr[r] *= rk;
-      }
-      // gating (src/reference_ops.py:271-275)
-      const float av = load_any(p.a, p.ab_dtype, b * p.ab_sb + h);
-      const float bv = load_any(p.bb, p.ab_dtype, b * p.ab_sb + h);
-      const float gval = -__expf(p.a_log[h]) * softplus_ref(av + p.dt_bias[h]);
-      decay = __expf(gval);
-      beta = sigmoid_ref(bv);
-    } else {
-      const int64_t tok = (b * p.H + h) * p.S + t;
-#pragma unroll
-      for (int r = 0; r < 8; ++r) {
-        qr[r] = p.q[tok * DK + row0 + r];
-        kr[r] = p.k[tok * DK + row0 + r];
-      }
-#pragma unroll
-      for (int c = 0; c < 8; ++c) vc[c] = p.v[tok * DV + col0 + c];
-      decay = __expf(p.g[tok]);
-      beta = p.beta[tok];
-    }
-
-    float part[8];
-#pragma unroll
-    for (int c = 0; c < 8; ++c) {
-      float acc = 0.f;
-#pragma unroll
-      for (int r = 0; r < 8; ++r) {
-        S[r][c] *= decay;
-        acc += S[r][c] * kr[r];
-      }
-      part[c] = acc;
+    for (int r = 0; r < 8; ++r) {
+      qr[r] = p.q[tok * DK + row0 + r];
+      kr[r] = p.k[tok * DK + row0 + r];
     }
 #pragma unroll
-    for (int c = 0; c < 8; ++c) {
-      part[c] += __shfl_xor(part[c], 16, 64);
-      part[c] += __shfl_xor(part[c], 32, 64);
-    }
-    if (rg == 0) {
-#pragma unroll
-      for (int c = 0; c < 8; ++c) red[0][w][col0 + c] = part[c];
-    }
-    __syncthreads();
-    float delta[8];
-#pragma unroll
-    for (int c = 0; c < 8; ++c) {
-      const float kv = (red[0][0][col0 + c] + red[0][1][col0 + c]) + (red[0][2][col0 + c] + red[0][3][col0 + c]);
-      delta[c] = (vc[c] - kv) * beta;
-    }
-#pragma unroll
-    for (int c = 0; c < 8; ++c) {
-      float acc = 0.f;
-#pragma unroll
-      for (int r = 0; r < 8; ++r) {
-        S[r][c] += kr[r] * delta[c];
-        acc += S[r][c] * qr[r];
-      }
-      part[c] = acc;
-    }
-#pragma unroll
-    for (int c = 0; c < 8; ++c) {
-      part[c] += __shfl_xor(part[c], 16, 64);
-      part[c] += __shfl_xor(part[c], 32, 64);
-    }
-    if (rg == 0) {
-#pragma unroll
-      for (int c = 0; c < 8; ++c) red[1][w][col0 + c] = part[c];
-    }
-    __syncthreads();
+    for (int c = 0; c < 8; ++c) vc[c] = p.v[tok * DV + col0 + c];
+    const float decay = __expf(p.g[tok]);
+    const float beta = p.beta[tok];
+    float o[8];
+    recurrence_token_128(S, kr, qr, vc, decay, beta, red, w, rg, cg, o);
     if (w == 0 && rg == 0) {
-      // lanes 0-15 of wave 0 (one DPP row) hold the head's 128 outputs, 8 each
-      float o[8];
 #pragma unroll
-      for (int c = 0; c < 8; ++c) o[c] = (red[1][0][col0 + c] + red[1][1][col0 + c]) + (red[1][2][col0 + c] + red[1][3][col0 + c]);
-      if (NORM) {
-        // the layer's output stage on the fp32 core (src/reference_ops.py:172-178,284-287: the
-        // core reaches gated_rms_norm in fp32, so its cast of the normalised value is the
-        // identity): (w * o / sqrt(mean(o^2) + eps)) * silu(z)
-        float ss = 0.f;
-#pragma unroll
-        for (int c = 0; c < 8; ++c) ss += o[c] * o[c];
-        ss = row16_sum(ss);
-        const float r = 1.0f / sqrtf(ss / static_cast<float>(DV) + p.norm_eps);
-#pragma unroll
-        for (int c = 0; c < 8; ++c) {
-          const float zv = load_any(p.z, p.z_dtype, b * p.z_sb + static_cast<int64_t>(h) * DV + col0 + c);
-          const float wv = load_any(p.norm_w, p.norm_dtype, col0 + c);
-          o[c] = (wv * (o[c] * r)) * __fdividef(zv, 1.0f + __expf(-zv));
-        }
-      }
-#pragma unroll
-      for (int c = 0; c < 8; ++c) {
-        if (FUSED)
-          store_any(p.out, p.out_dtype, b * p.out_sb + static_cast<int64_t>(h) * DV + col0 + c, o[c]);
-        else
-          reinterpret_cast<float*>(p.out)[((b * p.H + h) * p.S + t) * DV + col0 + c] = o[c];
-      }
+      for (int c = 0; c < 8; ++c) reinterpret_cast<float*>(p.out)[tok * DV + col0 + c] = o[c];
     }
   }
-
 #pragma unroll
   for (int r = 0; r < 8; ++r) {
     *reinterpret_cast<float4*>(s_out + (row0 + r) * DV + col0) = make_float4(S[r][0], S[r][1], S[r][2], S[r][3]);
     *reinterpret_cast<float4*>(s_out + (row0 + r) * DV + col0 + 4) = make_float4(S[r][4], S[r][5], S[r][6], S[r][7]);
   }
+}
+
+// The 128 outputs of value head h of row b as zeros (a row whose state slot is invalid).
+__device__ __forceinline__ void step_zero_outputs(const DeltaParams& p, int64_t b, int h, int tid) {
+  if (tid < 16) {
+#pragma unroll
+    for (int c = 0; c < 8; ++c) store_any(p.out, p.out_dtype, b * p.out_sb + static_cast<int64_t>(h) * 128 + 8 * tid + c, 0.f);
+  }
+}
+
+// Thread tid of a head's 256 holds the 8 x 8 block of the head's state at rows 32 w + 8 rg, columns
+// 8 cg (w = tid / 64, rg = lane / 16, cg = lane % 16).
+__device__ __forceinline__ void load_state_128(const float* s, int tid, float (&S)[8][8]) {
+  constexpr int DV = 128;
+  const int lane = tid & 63;
+  const int row0 = 32 * (tid >> 6) + 8 * (lane >> 4);
+  const int col0 = 8 * (lane & 15);
+#pragma unroll
+  for (int r = 0; r < 8; ++r) {
+    const float4 lo = *reinterpret_cast<const float4*>(s + (row0 + r) * DV + col0);
+    const float4 hi = *reinterpret_cast<const float4*>(s + (row0 + r) * DV + col0 + 4);
+    S[r][0] = lo.x; S[r][1] = lo.y; S[r][2] = lo.z; S[r][3] = lo.w;
+    S[r][4] = hi.x; S[r][5] = hi.y; S[r][6] = hi.z; S[r][7] = hi.w;
+  }
+}
+
+// One fused decode step of value head h of row b on 256 threads (tid = 0..255) from its state
+// block S (load_state_128 of s): qv / kvv are the post-conv q and k rows of its key head and vv
+// its v row (global memory or LDS), s its state (written back in place).  l2_norm of q and k
+// (src/reference_ops.py:181-183, q * dk^-0.5 :304), the gating (:271-275), one recurrence step,
+// and with NORM the layer's output stage on the fp32 core.
+template <bool NORM>
+__device__ __forceinline__ void step_128(const DeltaParams& p, int64_t b, int h, float* s, float (&S)[8][8], uint32_t a_bits, uint32_t b_bits,
+                                         const float* qv, const float* kvv, const float* vv, float (&red)[2][4][128], float (&nrm)[2][4],
+                                         int tid) {
+  constexpr int DK = 128, DV = 128;
+  const int w = tid >> 6;
+  const int lane = tid & 63;
+  const int rg = lane >> 4;
+  const int cg = lane & 15;
+  const int row0 = 32 * w + 8 * rg;
+  const int col0 = 8 * cg;
+  float kr[8], qr[8], vc[8];
+  float sq = 0.f, sk = 0.f;
+#pragma unroll
+  for (int r = 0; r < 8; ++r) {
+    qr[r] = qv[row0 + r];
+    kr[r] = kvv[row0 + r];
+    sq += qr[r] * qr[r];
+    sk += kr[r] * kr[r];
+  }
+#pragma unroll
+  for (int c = 0; c < 8; ++c) vc[c] = vv[col0 + c];
+  // sum over the 4 row groups of this wave (lanes xor 16, 32), then the 4 waves
+  sq += __shfl_xor(sq, 16, 64);
+  sq += __shfl_xor(sq, 32, 64);
+  sk += __shfl_xor(sk, 16, 64);
+  sk += __shfl_xor(sk, 32, 64);
+  if (lane == 0) {
+    nrm[0][w] = sq;
+    nrm[1][w] = sk;
+  }
+  __syncthreads();
+  sq = (nrm[0][0] + nrm[0][1]) + (nrm[0][2] + nrm[0][3]);
+  sk = (nrm[1][0] + nrm[1][1]) + (nrm[1][2] + nrm[1][3]);
+  const float rq = rsqrtf(sq + 1e-6f) * rsqrtf(static_cast<float>(DK));
+  const float rk = rsqrtf(sk + 1e-6f);
+#pragma unroll
+  for (int r = 0; r < 8; ++r) {
+    qr[r] *= rq;
+    kr[r] *= rk;
+  }
+  const float av = bits_to_f32(a_bits, p.ab_dtype == QA_BF16);
+  const float bv = bits_to_f32(b_bits, p.ab_dtype == QA_BF16);
+  const float gval = -__expf(p.a_log[h]) * softplus_ref(av + p.dt_bias[h]);
+  const float decay = __expf(gval);
+  const float beta = sigmoid_ref(bv);
+  float o[8];
+  recurrence_token_128(S, kr, qr, vc, decay, beta, red, w, rg, cg, o);
+  if (w == 0 && rg == 0) {
+    // lanes 0-15 of wave 0 (one DPP row) hold the head's 128 outputs, 8 each
+    if (NORM) {
+      // the layer's output stage on the fp32 core (src/reference_ops.py:172-178,284-287: the
+      // core reaches gated_rms_norm in fp32, so its cast of the normalised value is the
+      // identity): (w * o / sqrt(mean(o^2) + eps)) * silu(z)
+      float ss = 0.f;
+#pragma unroll
+      for (int c = 0; c < 8; ++c) ss += o[c] * o[c];
+      ss = row16_sum(ss);
+      const float r = 1.0f / sqrtf(ss / static_cast<float>(DV) + p.norm_eps);
+#pragma unroll
+      for (int c = 0; c < 8; ++c) {
+        const float zv = load_any(p.z, p.z_dtype, b * p.z_sb + static_cast<int64_t>(h) * DV + col0 + c);
+        const float wv = load_any(p.norm_w, p.norm_dtype, col0 + c);
+        o[c] = (wv * (o[c] * r)) * __fdividef(zv, 1.0f + __expf(-zv));
+      }
+    }
+#pragma unroll
+    for (int c = 0; c < 8; ++c) store_any(p.out, p.out_dtype, b * p.out_sb + static_cast<int64_t>(h) * DV + col0 + c, o[c]);
+  }
+#pragma unroll
+  for (int r = 0; r < 8; ++r) {
+    *reinterpret_cast<float4*>(s + (row0 + r) * DV + col0) = make_float4(S[r][0], S[r][1], S[r][2], S[r][3]);
+    *reinterpret_cast<float4*>(s + (row0 + r) * DV + col0 + 4) = make_float4(S[r][4], S[r][5], S[r][6], S[r][7]);
+  }
+}
+
+// Fused decode step on the post-conv row qkv (B, C) in global memory: a workgroup per (row, value
+// head).
+template <bool NORM>
+__global__ __launch_bounds__(256) void delta_step_128(DeltaParams p) {
+  constexpr int DK = 128, DV = 128;
+  __shared__ float red[2][4][DV];
+  __shared__ float nrm[2][4];
+  const int64_t b = blockIdx.x / p.H;
+  const int h = blockIdx.x - static_cast<int>(b) * p.H;
+  const int64_t slot = slot_of(p.slots, p.slots_i64, b);
+  if (!slot_valid(slot, p.state_rows)) {
+    // the whole workgroup takes this branch (one row per workgroup)
+    step_zero_outputs(p, b, h, threadIdx.x);
+    return;
+  }
+  const int qh = h / (p.H / p.Hqk);
+  const float* base = p.qkv + b * p.qkv_sb;
+  float* s = p.state_out + slot * p.state_sb + static_cast<int64_t>(h) * DK * DV;
+  const uint32_t a_bits = load_bits(p.a, p.ab_dtype == QA_BF16, b * p.ab_sb + h);
+  const uint32_t b_bits = load_bits(p.bb, p.ab_dtype == QA_BF16, b * p.ab_sb + h);
+  float S[8][8];
+  load_state_128(s, threadIdx.x, S);
+  step_128<NORM>(p, b, h, s, S, a_bits, b_bits, base + qh * DK, base + p.Hqk * DK + qh * DK, base + 2 * p.Hqk * DK + h * DV, red, nrm,
+                 threadIdx.x);
+}
+
+// The conv update of the token feeding the fused step (src/reference_ops.py:245-258 for one
+// token): raw mixed q|k|v row x (B, C), conv state (rows, C, K-1) fp32 by slot, in place, taps
+// (C, K) fp32.
+struct ConvStep {
+  const void* x;
+  int x_dtype;
+  int64_t x_sb;
+  float* state;
+  int64_t state_sb;
+  const float* w;
+  int K;
+};
+
+// Conv update + fused decode step: a workgroup per (row, key head) with R = H / Hqk groups of 256
+// threads, one per value head of the key head.  The workgroup first convolves the channels it
+// owns (the key head's q and k rows and its value heads' v rows; every channel belongs to one
+// workgroup, so each conv state entry has one reader and one writer) into LDS, then each group
+// runs step_128 from there.  The conv arithmetic is conv1d_kernel's, so the activations are the
+// same values qa_causal_conv1d_update produces.
+template <bool NORM, int R>
+__global__ __launch_bounds__(256 * R) void delta_step_conv_128(DeltaParams p, ConvStep cs) {
+  constexpr int DK = 128, DV = 128, NCH = 2 * DK + R * DV;
+  // channels per thread: 384 over 256 threads (R = 1), one for R = 2 and 4
+  constexpr int ITER = (NCH + 256 * R - 1) / (256 * R);
+  __shared__ float act[NCH];
+  __shared__ float red[R][2][4][DV];
+  __shared__ float nrm[R][2][4];
+  const int64_t b = blockIdx.x / p.Hqk;
+  const int qh = blockIdx.x - static_cast<int>(b) * p.Hqk;
+  const int g = threadIdx.x >> 8;
+  const int h = qh * R + g;
+  const int tid = threadIdx.x & 255;
+  const int64_t slot = slot_of(p.slots, p.slots_i64, b);
+  if (!slot_valid(slot, p.state_rows)) {
+    step_zero_outputs(p, b, h, tid);
+    return;
+  }
+  // The conv inputs are loaded first and the head's state block right after, so the state is in
+  // flight while the conv is computed and exchanged through LDS.
+  float win[ITER][kConvMaxK];
+  float wt[ITER][kConvMaxK];
+  float* st[ITER];
+  uint32_t xbits[ITER];
+  const bool xbf16 = cs.x_dtype == QA_BF16;
+#pragma unroll
+  for (int it = 0; it < ITER; ++it) {
+    const int c = threadIdx.x + it * 256 * R;
+    const int cc = c < NCH ? c : 0;
+    const int64_t ch = cc < DK ? static_cast<int64_t>(qh) * DK + cc
+                               : cc < 2 * DK ? static_cast<int64_t>(p.Hqk + qh) * DK + (cc - DK)
+                                             : 2 * static_cast<int64_t>(p.Hqk) * DK + static_cast<int64_t>(qh) * R * DV + (cc - 2 * DK);
+    st[it] = cs.state + slot * cs.state_sb + ch * (cs.K - 1);
+#pragma unroll
+    for (int i = 0; i < kConvMaxK; ++i) {
+      wt[it][i] = (c < NCH && i < cs.K) ? cs.w[ch * cs.K + i] : 0.f;
+      win[it][i] = (c < NCH && i < cs.K - 1) ? st[it][i] : 0.f;
+    }
+    xbits[it] = c < NCH ? load_bits(cs.x, xbf16, b * cs.x_sb + ch) : 0u;
+  }
+  float* s = p.state_out + slot * p.state_sb + static_cast<int64_t>(h) * DK * DV;
+  const uint32_t a_bits = load_bits(p.a, p.ab_dtype == QA_BF16, b * p.ab_sb + h);
+  const uint32_t b_bits = load_bits(p.bb, p.ab_dtype == QA_BF16, b * p.ab_sb + h);
+  float S[8][8];
+  load_state_128(s, tid, S);
+#pragma unroll
+  for (int it = 0; it < ITER; ++it) {
+    const int c = threadIdx.x + it * 256 * R;
+    if (c < NCH) {
+      const float x = bits_to_f32(xbits[it], xbf16);
+#pragma unroll
+      for (int i = 0; i < kConvMaxK; ++i)
+        if (i == cs.K - 1) win[it][i] = x;
+      float acc = 0.f;
+#pragma unroll
+      for (int i = 0; i < kConvMaxK; ++i)
+        if (i < cs.K) acc += wt[it][i] * win[it][i];
+      act[c] = silu_ref(acc);
+#pragma unroll
+      for (int i = 0; i < kConvMaxK - 1; ++i)
+        if (i < cs.K - 1) st[it][i] = win[it][i + 1];
+    }
+  }
+  __syncthreads();
+  step_128<NORM>(p, b, h, s, S, a_bits, b_bits, act, act + DK, act + 2 * DK + g * DV, red[g], nrm[g], tid);
 }
 
 static bool aligned16(const void* ptr) { return (reinterpret_cast<uintptr_t>(ptr) & 15u) == 0; }
@@ -456,7 +608,7 @@ extern "C" int qa_linear_attention_recurrent_core(const float* query, const floa
   p.dv = value_dim;
   const bool fast = key_dim == 128 && value_dim == 128 && aligned16(initial_state) && aligned16(final_state);
   if (fast) {
-    hipLaunchKernelGGL(delta_recurrent_128<false>, dim3(static_cast<unsigned>(batch * heads)), dim3(256), 0, stream, p);
+    hipLaunchKernelGGL(delta_recurrent_128, dim3(static_cast<unsigned>(batch * heads)), dim3(256), 0, stream, p);
     return check_launch("delta_recurrent_128");
   }
   dim3 grid(static_cast<unsigned>(batch * heads), static_cast<unsigned>(ceil_div(value_dim, 128)));
@@ -464,7 +616,7 @@ extern "C" int qa_linear_attention_recurrent_core(const float* query, const floa
   return check_launch("delta_recurrent_generic");
 }
 
-static int gated_delta_step_impl(const float* qkv, int64_t qkv_stride_b, const void* a, const void* b, int32_t ab_dtype,
+static int gated_delta_step_impl(const float* qkv, int64_t qkv_stride_b, const qa::ConvStep* conv, const void* a, const void* b, int32_t ab_dtype,
                                  int64_t ab_stride_b, const float* a_log, const float* dt_bias, float* state,
                                  int64_t state_stride_slot, const void* slots, int32_t slots_dtype, int64_t state_rows,
                                  const void* z, int32_t z_dtype,
@@ -472,7 +624,7 @@ static int gated_delta_step_impl(const float* qkv, int64_t qkv_stride_b, const v
                                  int32_t out_dtype, int64_t out_stride_b, int64_t batch, int32_t key_heads,
                                  int32_t value_heads, int32_t key_dim, int32_t value_dim, hipStream_t stream) {
   using namespace qa;
-  QA_REQUIRE(qkv && a && b && a_log && dt_bias && state && out, "gated_delta_step: pointers must be non-null");
+  QA_REQUIRE((qkv || conv) && a && b && a_log && dt_bias && state && out, "gated_delta_step: pointers must be non-null");
   QA_REQUIRE(key_dim == 128 && value_dim == 128, "gated_delta_step: only key_dim = value_dim = 128 is built");
   QA_REQUIRE(key_heads > 0 && value_heads % key_heads == 0, "gated_delta_step: value heads must be a multiple of key heads");
   QA_REQUIRE(ab_dtype == QA_F32 || ab_dtype == QA_BF16, "gated_delta_step: a/b must be float32 or bfloat16");
@@ -480,7 +632,8 @@ static int gated_delta_step_impl(const float* qkv, int64_t qkv_stride_b, const v
   QA_REQUIRE(slots == nullptr || is_index_dtype(slots_dtype), "gated_delta_step: slots must be int32/int64");
   QA_REQUIRE(batch > 0 && batch * value_heads <= 0x7fffffff, "gated_delta_step: bad batch");
   QA_REQUIRE(state_rows > 0, "gated_delta_step: state_rows must be positive");
-  QA_REQUIRE(aligned16(state) && state_stride_slot % 4 == 0 && qkv_stride_b >= 2 * key_heads * key_dim + value_heads * value_dim,
+  const int64_t channels = 2 * static_cast<int64_t>(key_heads) * key_dim + static_cast<int64_t>(value_heads) * value_dim;
+  QA_REQUIRE(aligned16(state) && state_stride_slot % 4 == 0 && (conv != nullptr || qkv_stride_b >= channels),
              "gated_delta_step: state must be 16-byte aligned and qkv rows complete");
   const bool norm = z != nullptr;
   QA_REQUIRE(!norm || (norm_weight != nullptr && is_float_dtype(z_dtype) && is_float_dtype(norm_dtype) && eps >= 0.f &&
@@ -516,14 +669,29 @@ static int gated_delta_step_impl(const float* qkv, int64_t qkv_stride_b, const v
   p.Hqk = key_heads;
   p.dk = key_dim;
   p.dv = value_dim;
+  if (conv != nullptr) {
+    const int groups = value_heads / key_heads;
+    QA_REQUIRE(groups == 1 || groups == 2 || groups == 4, "gated_delta_step_conv: value heads per key head must be 1, 2 or 4");
+    QA_REQUIRE(batch * key_heads <= 0x7fffffff, "gated_delta_step_conv: bad batch");
+    const dim3 grid(static_cast<unsigned>(batch * key_heads));
+    KernelTimer timer_("gated_delta_step", stream);
+#define QA_CONV_STEP(NORM_, R_) hipLaunchKernelGGL((delta_step_conv_128<NORM_, R_>), grid, dim3(256 * R_), 0, stream, p, *conv)
+    if (norm) {
+      if (groups == 1) QA_CONV_STEP(true, 1); else if (groups == 2) QA_CONV_STEP(true, 2); else QA_CONV_STEP(true, 4);
+    } else {
+      if (groups == 1) QA_CONV_STEP(false, 1); else if (groups == 2) QA_CONV_STEP(false, 2); else QA_CONV_STEP(false, 4);
+    }
+#undef QA_CONV_STEP
+    return check_launch("delta_step_conv_128");
+  }
   {
     KernelTimer timer_("gated_delta_step", stream);
     if (norm)
-      hipLaunchKernelGGL((delta_recurrent_128<true, true>), dim3(static_cast<unsigned>(batch * value_heads)), dim3(256), 0, stream, p);
+      hipLaunchKernelGGL((delta_step_128<true>), dim3(static_cast<unsigned>(batch * value_heads)), dim3(256), 0, stream, p);
     else
-      hipLaunchKernelGGL((delta_recurrent_128<true, false>), dim3(static_cast<unsigned>(batch * value_heads)), dim3(256), 0, stream, p);
+      hipLaunchKernelGGL((delta_step_128<false>), dim3(static_cast<unsigned>(batch * value_heads)), dim3(256), 0, stream, p);
   }
-  return check_launch("delta_recurrent_128(fused step)");
+  return check_launch("delta_step_128");
 }
 
 extern "C" int qa_gated_delta_step(const float* qkv, int64_t qkv_stride_b, const void* a, const void* b, int32_t ab_dtype,
@@ -531,7 +699,7 @@ extern "C" int qa_gated_delta_step(const float* qkv, int64_t qkv_stride_b, const
                                    int64_t state_stride_slot, const void* slots, int32_t slots_dtype, int64_t state_rows,
                                    void* out, int32_t out_dtype, int64_t out_stride_b, int64_t batch, int32_t key_heads,
                                    int32_t value_heads, int32_t key_dim, int32_t value_dim, hipStream_t stream) {
-  return gated_delta_step_impl(qkv, qkv_stride_b, a, b, ab_dtype, ab_stride_b, a_log, dt_bias, state, state_stride_slot, slots,
+  return gated_delta_step_impl(qkv, qkv_stride_b, nullptr, a, b, ab_dtype, ab_stride_b, a_log, dt_bias, state, state_stride_slot, slots,
                                slots_dtype, state_rows, nullptr, QA_F32, 0, nullptr, QA_F32, 0.f, out, out_dtype, out_stride_b, batch,
                                key_heads, value_heads, key_dim, value_dim, stream);
 }
@@ -544,7 +712,36 @@ extern "C" int qa_gated_delta_step_norm(const float* qkv, int64_t qkv_stride_b, 
                                         void* out, int32_t out_dtype, int64_t out_stride_b, int64_t batch, int32_t key_heads,
                                         int32_t value_heads, int32_t key_dim, int32_t value_dim, hipStream_t stream) {
   if (z == nullptr) return qa::fail("gated_delta_step_norm: z must be non-null");
-  return gated_delta_step_impl(qkv, qkv_stride_b, a, b, ab_dtype, ab_stride_b, a_log, dt_bias, state, state_stride_slot, slots,
+  return gated_delta_step_impl(qkv, qkv_stride_b, nullptr, a, b, ab_dtype, ab_stride_b, a_log, dt_bias, state, state_stride_slot, slots,
                                slots_dtype, state_rows, z, z_dtype, z_stride_b, norm_weight, norm_dtype, eps, out, out_dtype, out_stride_b, batch,
                                key_heads, value_heads, key_dim, value_dim, stream);
+}
+
+extern "C" int qa_gated_delta_step_conv(const void* x, int32_t x_dtype, int64_t x_stride_b, float* conv_state, int64_t conv_state_stride_b,
+                                        const float* conv_weight, int32_t conv_kernel, const void* a, const void* b, int32_t ab_dtype,
+                                        int64_t ab_stride_b, const float* a_log, const float* dt_bias, float* state,
+                                        int64_t state_stride_slot, const void* slots, int32_t slots_dtype, int64_t state_rows,
+                                        const void* z, int32_t z_dtype, int64_t z_stride_b, const void* norm_weight, int32_t norm_dtype,
+                                        float eps, void* out, int32_t out_dtype, int64_t out_stride_b, int64_t batch, int32_t key_heads,
+                                        int32_t value_heads, int32_t key_dim, int32_t value_dim, hipStream_t stream) {
+  using namespace qa;
+  QA_REQUIRE(x && conv_state && conv_weight, "gated_delta_step_conv: x, conv_state and conv_weight must be non-null");
+  QA_REQUIRE(x_dtype == QA_F32 || x_dtype == QA_BF16, "gated_delta_step_conv: x must be float32 or bfloat16");
+  QA_REQUIRE(conv_kernel >= 2 && conv_kernel <= kConvMaxK, "gated_delta_step_conv: conv kernel size must be in [2, %d]", kConvMaxK);
+  QA_REQUIRE(key_heads > 0 && value_heads > 0 && key_dim > 0 && value_dim > 0, "gated_delta_step_conv: head counts and dims must be positive");
+  const int64_t channels = 2 * static_cast<int64_t>(key_heads) * key_dim + static_cast<int64_t>(value_heads) * value_dim;
+  QA_REQUIRE(x_stride_b >= channels && conv_state_stride_b >= channels * (conv_kernel - 1),
+             "gated_delta_step_conv: x rows and conv state rows must hold every channel");
+  QA_REQUIRE(z == nullptr || norm_weight != nullptr, "gated_delta_step_conv: the output stage needs norm_weight");
+  ConvStep cs{};
+  cs.x = x;
+  cs.x_dtype = x_dtype;
+  cs.x_sb = x_stride_b;
+  cs.state = conv_state;
+  cs.state_sb = conv_state_stride_b;
+  cs.w = conv_weight;
+  cs.K = conv_kernel;
+  return gated_delta_step_impl(nullptr, 0, &cs, a, b, ab_dtype, ab_stride_b, a_log, dt_bias, state, state_stride_slot, slots, slots_dtype,
+                               state_rows, z, z_dtype, z_stride_b, norm_weight, norm_dtype, eps, out, out_dtype, out_stride_b, batch, key_heads,
+                               value_heads, key_dim, value_dim, stream);
 }

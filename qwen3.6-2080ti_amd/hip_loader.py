@@ -127,6 +127,12 @@ SIGNATURES: dict[str, tuple[Any, list[Any]]] = {
          c_void_p, c_int32, c_int64, c_void_p, c_int32, c_float, c_void_p, c_int32, c_int64, c_int64, c_int32, c_int32, c_int32, c_int32,
          c_void_p],
     ),
+    "qa_gated_delta_step_conv": (
+        c_int32,
+        [c_void_p, c_int32, c_int64, c_void_p, c_int64, c_void_p, c_int32, c_void_p, c_void_p, c_int32, c_int64, c_void_p, c_void_p,
+         c_void_p, c_int64, c_void_p, c_int32, c_int64, c_void_p, c_int32, c_int64, c_void_p, c_int32, c_float, c_void_p, c_int32, c_int64,
+         c_int64, c_int32, c_int32, c_int32, c_int32, c_void_p],
+    ),
     "qa_gated_rms_norm": (
         c_int32,
         [c_void_p, c_int32, c_int64, c_int64, c_void_p, c_int32, c_int64, c_int64, c_void_p, c_int32, c_float, c_int64, c_int32, c_int32,

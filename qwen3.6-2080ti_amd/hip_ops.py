@@ -723,6 +723,81 @@ def gated_delta_step(
     return out
 
 
+def gated_delta_step_conv(
+    x: torch.Tensor,
+    conv_state: torch.Tensor,
+    conv_weight: torch.Tensor,
+    a: torch.Tensor,
+    b: torch.Tensor,
+    a_log: torch.Tensor,
+    dt_bias: torch.Tensor,
+    state: torch.Tensor,
+    *,
+    key_heads: int,
+    slots: torch.Tensor | None = None,
+    out_dtype: torch.dtype = torch.bfloat16,
+    z: torch.Tensor | None = None,
+    norm_weight: torch.Tensor | None = None,
+    eps: float = 1e-6,
+) -> torch.Tensor:
+    """``causal_conv1d_update`` followed by ``gated_delta_step`` in one kernel.
+
+    ``x`` ``(B, C)`` is the token's raw ``in_proj_qkv`` row (float32 or bfloat16),
+    ``conv_state`` ``(rows, C, K-1)`` fp32 and ``state`` ``(rows, Hv, dk, dv)`` fp32 are
+    both updated in place at row ``slots[b]`` (or ``b``); the other arguments and the
+    result are ``gated_delta_step``'s.  The activations and outputs equal those of the
+    two calls.
+    """
+    lib = L.load_library()
+    _require_cuda(x, "x")
+    device = x.device
+    _require(x.dim() == 2 and x.stride(-1) == 1, "x must be (batch, channels)")
+    _float_dtype(x, "x")
+    batch, channels = x.shape
+    w = _conv_weight(conv_weight, channels, device)
+    kernel = w.shape[1]
+    _require_cuda(conv_state, "conv_state", device)
+    _require(conv_state.dtype == torch.float32 and conv_state.is_contiguous(), "conv_state must be contiguous float32")
+    _require(tuple(conv_state.shape[1:]) == (channels, kernel - 1), "conv_state must be (rows, channels, kernel-1)")
+    _require_cuda(state, "state", device)
+    _require(state.dtype == torch.float32 and state.dim() == 4 and state.is_contiguous(), "state must be contiguous (slots, Hv, dk, dv) float32")
+    _require(conv_state.shape[0] == state.shape[0], "conv_state and state must have the same rows")
+    _, value_heads, key_dim, value_dim = state.shape
+    _require(channels == 2 * int(key_heads) * key_dim + value_heads * value_dim, "x must hold the q, k and v channels")
+    _require(a.shape == (batch, value_heads) and b.shape == (batch, value_heads), "a/b must be (batch, value_heads)")
+    _require(a.dtype == b.dtype and a.dtype in (torch.float32, torch.bfloat16), "a/b must share a float32/bfloat16 dtype")
+    a_c, b_c = a.contiguous(), b.contiguous()
+    alog = _f32_contig(a_log.reshape(-1), "a_log", device)
+    dtb = _f32_contig(dt_bias.reshape(-1), "dt_bias", device)
+    slot_ptr, slot_code = ctypes.c_void_p(0), L.QA_I32
+    if slots is not None:
+        _require_cuda(slots, "slots", device)
+        _index_dtype(slots, "slots")
+        slots = slots.contiguous()
+        slot_ptr, slot_code = _ptr(slots), _code(slots)
+    z_ptr, z_code, z_sb, w_ptr, w_code = ctypes.c_void_p(0), L.QA_F32, 0, ctypes.c_void_p(0), L.QA_F32
+    if z is not None:
+        _require_cuda(z, "z", device)
+        _float_dtype(z, "z")
+        _require(norm_weight is not None, "the output stage needs norm_weight")
+        zz = z.reshape(batch, value_heads * value_dim)
+        _require(zz.stride(-1) == 1, "z rows must be contiguous")
+        nw = norm_weight.reshape(-1).to(device=device).contiguous()
+        _float_dtype(nw, "norm_weight")
+        _require(nw.numel() == value_dim, "norm_weight must have value_dim elements")
+        z_ptr, z_code, z_sb, w_ptr, w_code = _ptr(zz), _code(zz), zz.stride(0), _ptr(nw), _code(nw)
+    else:
+        _require(norm_weight is None, "norm_weight needs z")
+    out = torch.empty((batch, value_heads, value_dim), dtype=out_dtype, device=device)
+    status = lib.qa_gated_delta_step_conv(
+        _ptr(x), _code(x), x.stride(0), _ptr(conv_state), channels * (kernel - 1), _ptr(w), kernel, _ptr(a_c), _ptr(b_c), _code(a_c),
+        a_c.stride(0), _ptr(alog), _ptr(dtb), _ptr(state), state.stride(0), slot_ptr, slot_code, state.shape[0], z_ptr, z_code, z_sb, w_ptr,
+        w_code, float(eps), _ptr(out), _code(out), out.stride(0), batch, int(key_heads), value_heads, key_dim, value_dim, _stream(device),
+    )
+    L.check(lib, status, "gated_delta_step_conv")
+    return out
+
+
 def chunk_gated_delta_rule(
     mixed_qkv: torch.Tensor,
     a: torch.Tensor,

@@ -235,8 +235,8 @@ def test_config5_hybrid_step_sampled_rows_match_oracle() -> None:
         for j in range(3):
             i = 3 * g + j
             lin = w["linear"][i]
-            act = hip_ops.causal_conv1d_update(x["mixed"], lin["conv"], lin["conv_w"])
-            o = hip_ops.gated_delta_step(act, x["a"], x["b"], lin["a_log"], lin["dt_bias"], lin["state"], key_heads=w["key_heads"])
+            o = hip_ops.gated_delta_step_conv(x["mixed"], lin["conv"], lin["conv_w"], x["a"], x["b"], lin["a_log"], lin["dt_bias"], lin["state"],
+                                              key_heads=w["key_heads"])
             if i in lin_check:
                 lin_check[i] = o
         full = w["full"][g]

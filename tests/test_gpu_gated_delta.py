@@ -198,3 +198,50 @@ def test_invalid_slots_give_zeros_and_leave_the_pools_untouched(slot_dtype) -> N
                                    key_heads=shape.key_heads, slots=ref_slots, out_dtype=torch.float32)
     assert torch.equal(act[good], ref_act) and torch.equal(out[good], ref_out)
     assert torch.equal(state_pool, ref_state) and torch.equal(conv_pool, ref_conv)
+
+
+@pytest.mark.parametrize("key_heads,value_heads", [(2, 2), (2, 4), (1, 4)])
+@pytest.mark.parametrize("x_dtype", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("norm", [False, True])
+def test_conv_fused_step_equals_conv_update_then_step(key_heads, value_heads, x_dtype, norm) -> None:
+    """qa_gated_delta_step_conv == qa_causal_conv1d_update followed by qa_gated_delta_step(_norm),
+    bit for bit (outputs, recurrent states, conv states), over two tokens, with a -1 pad and an id
+    past the pool among the slots."""
+    ops = _ops()
+    shape = gd.LinearShape(key_heads=key_heads, value_heads=value_heads, key_head_dim=128, value_head_dim=128, conv_kernel_dim=4)
+    batch, rows = 5, 6
+    mixed, a, b, a_log, dt_bias, w = _layer_inputs(41 + value_heads, batch, 2, shape)
+    gen = torch.Generator().manual_seed(42)
+    state0 = (torch.randn(rows, value_heads, 128, 128, generator=gen) * 0.05).to(DEV)
+    conv0 = torch.randn(rows, shape.qkv_dim, 3, generator=gen).to(DEV)
+    slots = torch.tensor([3, -1, 0, rows, 5], device=DEV, dtype=torch.int32)
+    z = torch.randn(2, batch, value_heads * 128, generator=gen).to(torch.bfloat16).to(DEV)
+    nw = (1 + 0.1 * torch.randn(128, generator=gen)).to(DEV)
+    s_ref, c_ref = state0.clone(), conv0.clone()
+    s_fused, c_fused = state0.clone(), conv0.clone()
+    for step in range(2):
+        x = mixed[:, step].to(x_dtype).contiguous().to(DEV)
+        av, bv = a[:, step].contiguous().to(DEV), b[:, step].contiguous().to(DEV)
+        kw = dict(key_heads=key_heads, slots=slots, out_dtype=torch.float32)
+        if norm:
+            kw.update(z=z[step], norm_weight=nw)
+        act = ops.causal_conv1d_update(x, c_ref, w.to(DEV), slots)
+        ref = ops.gated_delta_step(act, av, bv, a_log.to(DEV), dt_bias.to(DEV), s_ref, **kw)
+        out = ops.gated_delta_step_conv(x, c_fused, w.to(DEV), av, bv, a_log.to(DEV), dt_bias.to(DEV), s_fused, **kw)
+        assert torch.equal(out, ref), f"step {step}: max diff {(out - ref).abs().max().item()}"
+        assert torch.equal(s_fused, s_ref) and torch.equal(c_fused, c_ref)
+        for bad in (1, 3):
+            assert torch.count_nonzero(out[bad]) == 0
+    # rows 1, 2 and 4 are no valid request's slot: untouched
+    for r in (1, 2, 4):
+        assert torch.equal(s_fused[r], state0[r]) and torch.equal(c_fused[r], conv0[r])
+
+
+def test_conv_fused_step_rejects_unsupported_head_ratio() -> None:
+    ops = _ops()
+    shape = gd.LinearShape(key_heads=1, value_heads=3, key_head_dim=128, value_head_dim=128, conv_kernel_dim=4)
+    x = torch.zeros(1, shape.qkv_dim, device=DEV)
+    ab = torch.zeros(1, 3, device=DEV)
+    with pytest.raises(RuntimeError, match="1, 2 or 4"):
+        ops.gated_delta_step_conv(x, torch.zeros(1, shape.qkv_dim, 3, device=DEV), torch.zeros(shape.qkv_dim, 4, device=DEV), ab, ab,
+                                  torch.zeros(3, device=DEV), torch.zeros(3, device=DEV), torch.zeros(1, 3, 128, 128, device=DEV), key_heads=1)
