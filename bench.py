@@ -852,7 +852,7 @@ def main() -> int:
             "config": {"workload": "48-layer hybrid decode step, attention only (BASELINE config 5)", "batch": 128, "layers": "12 x (3 linear + 1 full)",
                        "context": "U[256, 65536] seed 0", "sum_context": hw["sum_ctx"], "pool_blocks_per_layer": hw["pool_blocks"]},
             "roofline": {"bound": "hbm", "achieved": round(hgbs, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(hgbs / HBM_PEAK_GBS, 4),
-                         "traffic": None, "algo_bytes_per_step": hw["algo_bytes"], "kernel": "whole step (12 paged-decode + 36 conv/delta-step layers)",
+                         "traffic": None, "algo_bytes_per_step": hw["algo_bytes"], "kernel": "whole step (12 paged-decode + 36 delta-step layers with the conv update fused in)",
                          "kernels": hkern},
         }
         del hw
