@@ -60,6 +60,10 @@ def kernel_times(step, repeats: int, labels: tuple[str, ...]) -> dict[str, dict[
     import hip_loader
 
     torch.cuda.synchronize()
+    # two untimed steps keep the GPU busy up to the first timed launch: started from an idle
+    # GPU, the first launch reads several percent slow and skews a short average
+    for _ in range(2):
+        step()
     with hip_loader.KernelTiming() as timing:
         for _ in range(repeats):
             step()
