@@ -245,3 +245,27 @@ def test_conv_fused_step_rejects_unsupported_head_ratio() -> None:
     with pytest.raises(RuntimeError, match="1, 2 or 4"):
         ops.gated_delta_step_conv(x, torch.zeros(1, shape.qkv_dim, 3, device=DEV), torch.zeros(shape.qkv_dim, 4, device=DEV), ab, ab,
                                   torch.zeros(3, device=DEV), torch.zeros(3, device=DEV), torch.zeros(1, 3, 128, 128, device=DEV), key_heads=1)
+
+
+@pytest.mark.parametrize("conv_kernel", [2, 3, 8])
+def test_conv_fused_step_other_conv_kernels_and_strided_rows(conv_kernel) -> None:
+    """Conv kernel sizes other than the model's 4, and x rows that are a slice of a wider
+    projection output: still equal to qa_causal_conv1d_update + qa_gated_delta_step bit for bit."""
+    ops = _ops()
+    shape = gd.LinearShape(key_heads=2, value_heads=4, key_head_dim=128, value_head_dim=128, conv_kernel_dim=conv_kernel)
+    batch, rows = 3, 4
+    mixed, a, b, a_log, dt_bias, w = _layer_inputs(60 + conv_kernel, batch, 1, shape)
+    gen = torch.Generator().manual_seed(61)
+    state0 = (torch.randn(rows, 4, 128, 128, generator=gen) * 0.05).to(DEV)
+    conv0 = torch.randn(rows, shape.qkv_dim, conv_kernel - 1, generator=gen).to(DEV)
+    slots = torch.tensor([2, 0, 3], device=DEV, dtype=torch.int64)
+    wide = torch.randn(batch, shape.qkv_dim + 96, generator=gen).to(torch.bfloat16).to(DEV)
+    wide[:, 32 : 32 + shape.qkv_dim] = mixed[:, 0].to(DEV)
+    x = wide[:, 32 : 32 + shape.qkv_dim]  # row stride qkv_dim + 96
+    av, bv = a[:, 0].contiguous().to(DEV), b[:, 0].contiguous().to(DEV)
+    s_ref, c_ref, s_fused, c_fused = state0.clone(), conv0.clone(), state0.clone(), conv0.clone()
+    act = ops.causal_conv1d_update(x.contiguous(), c_ref, w.to(DEV), slots)
+    ref = ops.gated_delta_step(act, av, bv, a_log.to(DEV), dt_bias.to(DEV), s_ref, key_heads=2, slots=slots)
+    out = ops.gated_delta_step_conv(x, c_fused, w.to(DEV), av, bv, a_log.to(DEV), dt_bias.to(DEV), s_fused, key_heads=2, slots=slots)
+    assert torch.equal(out, ref)
+    assert torch.equal(s_fused, s_ref) and torch.equal(c_fused, c_ref)
