@@ -203,7 +203,8 @@ def test_invalid_slots_give_zeros_and_leave_the_pools_untouched(slot_dtype) -> N
 @pytest.mark.parametrize("key_heads,value_heads", [(2, 2), (2, 4), (1, 4)])
 @pytest.mark.parametrize("x_dtype", [torch.bfloat16, torch.float32])
 @pytest.mark.parametrize("norm", [False, True])
-def test_conv_fused_step_equals_conv_update_then_step(key_heads, value_heads, x_dtype, norm) -> None:
+@pytest.mark.parametrize("out_dtype", [torch.float32, torch.bfloat16])
+def test_conv_fused_step_equals_conv_update_then_step(key_heads, value_heads, x_dtype, norm, out_dtype) -> None:
     """qa_gated_delta_step_conv == qa_causal_conv1d_update followed by qa_gated_delta_step(_norm),
     bit for bit (outputs, recurrent states, conv states), over two tokens, with a -1 pad and an id
     past the pool among the slots."""
@@ -222,13 +223,13 @@ def test_conv_fused_step_equals_conv_update_then_step(key_heads, value_heads, x_
     for step in range(2):
         x = mixed[:, step].to(x_dtype).contiguous().to(DEV)
         av, bv = a[:, step].contiguous().to(DEV), b[:, step].contiguous().to(DEV)
-        kw = dict(key_heads=key_heads, slots=slots, out_dtype=torch.float32)
+        kw = dict(key_heads=key_heads, slots=slots, out_dtype=out_dtype)
         if norm:
             kw.update(z=z[step], norm_weight=nw)
         act = ops.causal_conv1d_update(x, c_ref, w.to(DEV), slots)
         ref = ops.gated_delta_step(act, av, bv, a_log.to(DEV), dt_bias.to(DEV), s_ref, **kw)
         out = ops.gated_delta_step_conv(x, c_fused, w.to(DEV), av, bv, a_log.to(DEV), dt_bias.to(DEV), s_fused, **kw)
-        assert torch.equal(out, ref), f"step {step}: max diff {(out - ref).abs().max().item()}"
+        assert out.dtype == out_dtype and torch.equal(out, ref), f"step {step}: max diff {(out.float() - ref.float()).abs().max().item()}"
         assert torch.equal(s_fused, s_ref) and torch.equal(c_fused, c_ref)
         for bad in (1, 3):
             assert torch.count_nonzero(out[bad]) == 0
