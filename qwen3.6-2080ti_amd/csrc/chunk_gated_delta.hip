@@ -832,6 +832,33 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(2, 2))) void
       for (int k = 0; k < CH / 32; ++k)
 #pragma unroll
         for (int tt = 0; tt < 4; ++tt) O[tt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(da[k], ab2[tt][k], O[tt], 0, 0, 0);
+      if (p.out_dtype == QA_BF16 && p.out_st % 8 == 0 && p.out_sb % 8 == 0) {
+        // 16-byte stores: lanes 16 apart (rows lq, lq ^ 1) hold the adjacent dv quads of one
+        // token, so one row swap per element gives the even row both quads of token tile 2m and
+        // the odd row both quads of tile 2m + 1 (v_permlane16_swap of O[2m] and O[2m + 1]).
+        const int odd = lq & 1;
+#pragma unroll
+        for (int m = 0; m < 2; ++m) {
+          float lo[4], hi[4];
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const auto sw = __builtin_amdgcn_permlane16_swap(__float_as_uint(O[2 * m][r]), __float_as_uint(O[2 * m + 1][r]), false, false);
+            lo[r] = __uint_as_float(sw[0]);
+            hi[r] = __uint_as_float(sw[1]);
+          }
+          const int64_t tg = tc0 + 16 * (2 * m + odd) + lc;
+          if (tg < p.T) {
+            const int64_t base = b * p.out_sb + tg * p.out_st + static_cast<int64_t>(j) * DV + half_id * DVS + 16 * v + 4 * (lq - odd);
+            uint4 packed;
+            packed.x = static_cast<uint32_t>(f32_to_bf16(lo[0])) | (static_cast<uint32_t>(f32_to_bf16(lo[1])) << 16);
+            packed.y = static_cast<uint32_t>(f32_to_bf16(lo[2])) | (static_cast<uint32_t>(f32_to_bf16(lo[3])) << 16);
+            packed.z = static_cast<uint32_t>(f32_to_bf16(hi[0])) | (static_cast<uint32_t>(f32_to_bf16(hi[1])) << 16);
+            packed.w = static_cast<uint32_t>(f32_to_bf16(hi[2])) | (static_cast<uint32_t>(f32_to_bf16(hi[3])) << 16);
+            *reinterpret_cast<uint4*>(reinterpret_cast<bf16_t*>(p.out) + base) = packed;
+          }
+        }
+        return;
+      }
 #pragma unroll
       for (int tt = 0; tt < 4; ++tt) {
         const int tok = 16 * tt + lc;
