@@ -42,7 +42,7 @@ TRAFFIC_DECODE = 1959210677
 TRAFFIC_DELTA = 822685286  # chunk_kernel alone; the step (with prep_kernel) moves 1,400,024,473
 TRAFFIC_PREFILL = 888510552  # average over the eight per-chunk launches
 TRAFFIC_PROLOGUE = 675674420
-TRAFFIC_OUTPUT_NORM = 805389585
+TRAFFIC_OUTPUT_NORM = 805417779
 TRAFFIC_FP8_LINEAR = 29648896  # x-resident kernel (one launch), from profiles/fp8_linear_config5_batch.md
 SECONDARY_WARM_MS = 100.0  # wall time of untimed steps before each secondary (config 3, 4, 5) measurement
 MFMA_BF16_PEAK_TFLOPS = 2500.0  # MI355X dense bf16/fp16 MFMA, TFLOP/s

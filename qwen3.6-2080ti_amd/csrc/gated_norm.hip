@@ -76,6 +76,45 @@ __device__ __forceinline__ void load_row(const void* p, bool bf16, float* v) {
   }
 }
 
+// E consecutive elements at p (16-byte aligned) as raw bits: the loads only, the conversion is
+// raw_to_f32's.  A conversion inside the dtype branch makes the compiler wait there for every load
+// issued before it, so the loads of all rows are issued first and converted afterwards.
+template <int E>
+struct RawRow {
+  u32x4_v u[E / 4];  // fp32: E / 4 units; bf16: E / 8 (or, for E = 4, the low half of one)
+};
+
+template <int E>
+__device__ __forceinline__ void load_raw(const void* p, bool bf16, RawRow<E>& r) {
+  if (bf16) {
+    if constexpr (E % 8 == 0) {
+#pragma unroll
+      for (int c = 0; c < E / 8; ++c) r.u[c] = *reinterpret_cast<const u32x4_v*>(reinterpret_cast<const bf16_t*>(p) + 8 * c);
+    } else {
+      const uint2 u = *reinterpret_cast<const uint2*>(p);
+      r.u[0] = u32x4_v{u.x, u.y, 0u, 0u};
+    }
+  } else {
+#pragma unroll
+    for (int c = 0; c < E / 4; ++c) r.u[c] = *reinterpret_cast<const u32x4_v*>(reinterpret_cast<const float*>(p) + 4 * c);
+  }
+}
+
+template <int E>
+__device__ __forceinline__ void raw_to_f32(const RawRow<E>& r, bool bf16, float* v) {
+  if (bf16) {
+#pragma unroll
+    for (int e = 0; e < E; e += 2) {
+      const uint32_t u = r.u[e / 8][(e % 8) / 2];
+      v[e] = __uint_as_float(u << 16);
+      v[e + 1] = __uint_as_float(u & 0xFFFF0000u);
+    }
+  } else {
+#pragma unroll
+    for (int e = 0; e < E; ++e) v[e] = __uint_as_float(r.u[e / 4][e % 4]);
+  }
+}
+
 template <int E>
 __device__ __forceinline__ void store_row(void* p, bool bf16, const float* v) {
   if (bf16) {
@@ -107,32 +146,34 @@ __global__ __launch_bounds__(256) void gated_rms_norm_kernel(Params p) {
   constexpr int E = D / 16;
   const int l = threadIdx.x & 15;
   const int64_t d0 = static_cast<int64_t>(E) * l;
-  // RPG rows per 16-lane group, all of whose loads are issued before any arithmetic
+  // RPG rows per 16-lane group, all of whose loads are issued before any arithmetic: a row past
+  // the end loads the last row again (no branch around a load) and is not stored
   float x[RPG][E], z[RPG][E], w[E];
+  RawRow<E> zr[RPG], wr;
   bool live[RPG];
   int64_t t[RPG], h[RPG];
+  load_raw<E>(reinterpret_cast<const char*>(p.w) + d0 * (p.w_bf16 ? sizeof(bf16_t) : sizeof(float)), p.w_bf16, wr);
 #pragma unroll
   for (int k = 0; k < RPG; ++k) {
-    const int64_t row = (static_cast<int64_t>(blockIdx.x) * 16 + (threadIdx.x >> 4)) * RPG + k;
-    live[k] = row < p.rows;
-    t[k] = live[k] ? row / p.heads : 0;
-    h[k] = live[k] ? row - t[k] * p.heads : 0;
-#pragma unroll
-    for (int e = 0; e < E; ++e) x[k][e] = z[k][e] = 0.f;
-    if (live[k]) {
-      constexpr size_t xs = XBF16 ? sizeof(bf16_t) : sizeof(float);
-      load_row<E>(reinterpret_cast<const char*>(p.x) + (t[k] * p.x_st + h[k] * p.x_sh + d0) * xs, XBF16, x[k]);
-      load_row<E>(reinterpret_cast<const char*>(p.g) + (t[k] * p.g_st + h[k] * p.g_sh + d0) * (p.g_bf16 ? sizeof(bf16_t) : sizeof(float)),
-                  p.g_bf16, z[k]);
-    }
+    const int64_t row0 = (static_cast<int64_t>(blockIdx.x) * 16 + (threadIdx.x >> 4)) * RPG + k;
+    live[k] = row0 < p.rows;
+    const int64_t row = live[k] ? row0 : p.rows - 1;
+    t[k] = row / p.heads;
+    h[k] = row - t[k] * p.heads;
+    constexpr size_t xs = XBF16 ? sizeof(bf16_t) : sizeof(float);
+    load_row<E>(reinterpret_cast<const char*>(p.x) + (t[k] * p.x_st + h[k] * p.x_sh + d0) * xs, XBF16, x[k]);
+    load_raw<E>(reinterpret_cast<const char*>(p.g) + (t[k] * p.g_st + h[k] * p.g_sh + d0) * (p.g_bf16 ? sizeof(bf16_t) : sizeof(float)),
+                p.g_bf16, zr[k]);
   }
-  load_row<E>(reinterpret_cast<const char*>(p.w) + d0 * (p.w_bf16 ? sizeof(bf16_t) : sizeof(float)), p.w_bf16, w);
+  raw_to_f32<E>(wr, p.w_bf16, w);
+#pragma unroll
+  for (int k = 0; k < RPG; ++k) raw_to_f32<E>(zr[k], p.g_bf16, z[k]);
 #pragma unroll
   for (int k = 0; k < RPG; ++k) {
     float ss = 0.f;
 #pragma unroll
     for (int e = 0; e < E; ++e) ss += x[k][e] * x[k][e];
-    ss = row16_sum(ss);  // every lane of the row takes part (dead rows hold zeros)
+    ss = row16_sum(ss);  // every lane of the row takes part (a dead row holds a copy of the last row)
     const float r = 1.0f / sqrtf(ss / static_cast<float>(D) + p.eps);
     float y[E];
 #pragma unroll
