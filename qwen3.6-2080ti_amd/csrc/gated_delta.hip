@@ -157,6 +157,9 @@ struct DeltaParams {
   const void* norm_w;
   int norm_dtype;
   float norm_eps;
+  // the decode steps' vector paths: z and the norm weight read as 16-byte vectors, the 8 outputs
+  // of a lane written as 16-byte vectors (set by the host when pointers and strides allow)
+  int norm_vec, out_vec;
   int64_t B, S;
   int H, Hqk, dk, dv;
 };
@@ -311,6 +314,48 @@ __device__ __forceinline__ void step_zero_outputs(const DeltaParams& p, int64_t 
   }
 }
 
+// The output stage's z and norm weight for the 8 outputs a lane of wave 0 holds (columns 8 (tid % 16)
+// .. + 7), as raw bits: one 16-byte vector for bf16, two for fp32, all issued before any is used
+// (element loads through the dtype branch each waited for the one before).
+struct NormIn {
+  uint4 z[2];
+  uint4 w[2];
+};
+
+template <bool NORM>
+__device__ __forceinline__ void load_norm_in(const DeltaParams& p, int64_t b, int h, int tid, NormIn& n) {
+  if constexpr (NORM) {
+    if (p.norm_vec && tid < 64) {
+      const int col0 = 8 * (tid & 15);
+      const int64_t zi = b * p.z_sb + static_cast<int64_t>(h) * 128 + col0;
+      if (p.z_dtype == QA_BF16) {
+        n.z[0] = *reinterpret_cast<const uint4*>(reinterpret_cast<const bf16_t*>(p.z) + zi);
+      } else {
+        n.z[0] = *reinterpret_cast<const uint4*>(reinterpret_cast<const float*>(p.z) + zi);
+        n.z[1] = *reinterpret_cast<const uint4*>(reinterpret_cast<const float*>(p.z) + zi + 4);
+      }
+      if (p.norm_dtype == QA_BF16) {
+        n.w[0] = *reinterpret_cast<const uint4*>(reinterpret_cast<const bf16_t*>(p.norm_w) + col0);
+      } else {
+        n.w[0] = *reinterpret_cast<const uint4*>(reinterpret_cast<const float*>(p.norm_w) + col0);
+        n.w[1] = *reinterpret_cast<const uint4*>(reinterpret_cast<const float*>(p.norm_w) + col0 + 4);
+      }
+    }
+  }
+}
+
+// element c (0..7) of a NormIn vector pair
+__device__ __forceinline__ float norm_elem(const uint4 (&v)[2], bool bf16, int c) {
+  if (bf16) {
+    const uint4 u = v[0];
+    const uint32_t word = (c >> 1) == 0 ? u.x : (c >> 1) == 1 ? u.y : (c >> 1) == 2 ? u.z : u.w;
+    return __uint_as_float((c & 1) ? (word & 0xffff0000u) : (word << 16));
+  }
+  const uint4 u = v[c >> 2];
+  const uint32_t word = (c & 3) == 0 ? u.x : (c & 3) == 1 ? u.y : (c & 3) == 2 ? u.z : u.w;
+  return __uint_as_float(word);
+}
+
 // Thread tid of a head's 256 holds the 8 x 8 block of the head's state at rows 32 w + 8 rg, columns
 // 8 cg (w = tid / 64, rg = lane / 16, cg = lane % 16).
 __device__ __forceinline__ void load_state_128(const float* s, int tid, float (&S)[8][8]) {
@@ -383,6 +428,8 @@ __device__ __forceinline__ void step_128(const DeltaParams& p, int64_t b, int h,
   if (w == 0 && rg == 0) {
     // lanes 0-15 of wave 0 (one DPP row) hold the head's 128 outputs, 8 each
     if (NORM) {
+      NormIn nin;
+      load_norm_in<NORM>(p, b, h, tid, nin);  // in flight while the sum of squares is taken
       // the layer's output stage on the fp32 core (src/reference_ops.py:172-178,284-287: the
       // core reaches gated_rms_norm in fp32, so its cast of the normalised value is the
       // identity): (w * o / sqrt(mean(o^2) + eps)) * silu(z)
@@ -391,15 +438,40 @@ __device__ __forceinline__ void step_128(const DeltaParams& p, int64_t b, int h,
       for (int c = 0; c < 8; ++c) ss += o[c] * o[c];
       ss = row16_sum(ss);
       const float r = 1.0f / sqrtf(ss / static_cast<float>(DV) + p.norm_eps);
+      if (p.norm_vec) {
 #pragma unroll
-      for (int c = 0; c < 8; ++c) {
-        const float zv = load_any(p.z, p.z_dtype, b * p.z_sb + static_cast<int64_t>(h) * DV + col0 + c);
-        const float wv = load_any(p.norm_w, p.norm_dtype, col0 + c);
-        o[c] = (wv * (o[c] * r)) * __fdividef(zv, 1.0f + __expf(-zv));
+        for (int c = 0; c < 8; ++c) {
+          const float zv = norm_elem(nin.z, p.z_dtype == QA_BF16, c);
+          const float wv = norm_elem(nin.w, p.norm_dtype == QA_BF16, c);
+          o[c] = (wv * (o[c] * r)) * __fdividef(zv, 1.0f + __expf(-zv));
+        }
+      } else {
+#pragma unroll
+        for (int c = 0; c < 8; ++c) {
+          const float zv = load_any(p.z, p.z_dtype, b * p.z_sb + static_cast<int64_t>(h) * DV + col0 + c);
+          const float wv = load_any(p.norm_w, p.norm_dtype, col0 + c);
+          o[c] = (wv * (o[c] * r)) * __fdividef(zv, 1.0f + __expf(-zv));
+        }
       }
     }
+    const int64_t oi = b * p.out_sb + static_cast<int64_t>(h) * DV + col0;
+    if (p.out_vec) {
+      if (p.out_dtype == QA_BF16) {
+        uint4 u;
+        u.x = static_cast<uint32_t>(f32_to_bf16(o[0])) | (static_cast<uint32_t>(f32_to_bf16(o[1])) << 16);
+        u.y = static_cast<uint32_t>(f32_to_bf16(o[2])) | (static_cast<uint32_t>(f32_to_bf16(o[3])) << 16);
+        u.z = static_cast<uint32_t>(f32_to_bf16(o[4])) | (static_cast<uint32_t>(f32_to_bf16(o[5])) << 16);
+        u.w = static_cast<uint32_t>(f32_to_bf16(o[6])) | (static_cast<uint32_t>(f32_to_bf16(o[7])) << 16);
+        *reinterpret_cast<uint4*>(reinterpret_cast<bf16_t*>(p.out) + oi) = u;
+      } else {
+        float* op = reinterpret_cast<float*>(p.out) + oi;
+        *reinterpret_cast<float4*>(op) = make_float4(o[0], o[1], o[2], o[3]);
+        *reinterpret_cast<float4*>(op + 4) = make_float4(o[4], o[5], o[6], o[7]);
+      }
+    } else {
 #pragma unroll
-    for (int c = 0; c < 8; ++c) store_any(p.out, p.out_dtype, b * p.out_sb + static_cast<int64_t>(h) * DV + col0 + c, o[c]);
+      for (int c = 0; c < 8; ++c) store_any(p.out, p.out_dtype, oi + c, o[c]);
+    }
   }
 #pragma unroll
   for (int r = 0; r < 8; ++r) {
@@ -663,6 +735,11 @@ static int gated_delta_step_impl(const float* qkv, int64_t qkv_stride_b, const q
   p.norm_w = norm_weight;
   p.norm_dtype = norm_dtype;
   p.norm_eps = eps;
+  {
+    const int zs = z_dtype == QA_BF16 ? 2 : 4, ws = norm_dtype == QA_BF16 ? 2 : 4, os = out_dtype == QA_BF16 ? 2 : 4;
+    p.norm_vec = norm && aligned16(z) && aligned16(norm_weight) && (z_stride_b * zs) % 16 == 0;
+    p.out_vec = aligned16(out) && (out_stride_b * os) % 16 == 0;
+  }
   p.B = batch;
   p.S = 1;
   p.H = value_heads;
