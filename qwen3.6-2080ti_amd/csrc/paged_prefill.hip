@@ -89,15 +89,24 @@ struct Smem {
   static constexpr int kBytes = 4 * kTileBytes + MAXB * 4;  // two K and two V tiles + block table
 };
 
-__device__ __forceinline__ int64_t rd_index(const void* base, int is64, int64_t i) {
-  return is64 ? reinterpret_cast<const int64_t*>(base)[i] : reinterpret_cast<const int32_t*>(base)[i];
+// Index arrays are read with their dtype known at compile time (the kernel is instantiated per
+// index and table dtype): a load whose conversion sits inside a run-time dtype branch makes the
+// compiler wait there for every load issued before it, which had serialised the index reads of
+// every workgroup's start-up.
+template <bool I64>
+__device__ __forceinline__ int64_t rd_index(const void* base, int64_t i) {
+  if constexpr (I64)
+    return reinterpret_cast<const int64_t*>(base)[i];
+  else
+    return reinterpret_cast<const int32_t*>(base)[i];
 }
 
 // Physical block of logical block lb of row b (-1 if absent or outside the pool).
+template <bool T64>
 __device__ __forceinline__ int64_t block_of(const Params& p, int b, int64_t lb, const int* s_phys, int64_t nlb) {
   if (lb < nlb && lb < MAXB) return s_phys[lb];
   if (lb >= p.max_blocks) return -1;
-  const int64_t e = rd_index(p.tables, p.table_i64, b * p.table_stride + lb);
+  const int64_t e = rd_index<T64>(p.tables, b * p.table_stride + lb);
   return e >= 0 && e < p.num_blocks ? e : -1;
 }
 
@@ -105,6 +114,7 @@ __device__ __forceinline__ int pick(const int4& v, int i) { return i == 0 ? v.x 
 
 // Physical blocks of the four 16-key blocks of the tile at key0 (wave-uniform; -1 = absent):
 // one 16-byte LDS read when the whole tile lies in the cached part of the block table.
+template <bool T64>
 __device__ __forceinline__ int4 tile_phys(const Params& p, int b, int64_t key0, int64_t kv_len, const int* s_phys, int64_t nlb) {
   const int64_t lb0 = key0 / BS;
   if (lb0 + 4 <= min64(nlb, MAXB)) {
@@ -114,7 +124,7 @@ __device__ __forceinline__ int4 tile_phys(const Params& p, int b, int64_t key0, 
   }
   auto blk = [&](int q) {
     const int64_t t = key0 + BS * q;
-    return __builtin_amdgcn_readfirstlane(t < kv_len ? static_cast<int>(block_of(p, b, t / BS, s_phys, nlb)) : -1);
+    return __builtin_amdgcn_readfirstlane(t < kv_len ? static_cast<int>(block_of<T64>(p, b, t / BS, s_phys, nlb)) : -1);
   };
   return make_int4(blk(0), blk(1), blk(2), blk(3));
 }
@@ -208,7 +218,7 @@ __device__ __forceinline__ short4_v tr_read_at(const unsigned char* addr) {
   return __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s4*)addr);
 }
 
-template <int D, int HPW>
+template <int D, int HPW, bool I64, bool T64>
 __global__ __launch_bounds__(64 * (HMAX / HPW)) void prefill_kernel(Params p) {
   using C = Cfg<D, HPW>;
   constexpr int KCH = D / 32;  // k-chunks of S^T
@@ -235,7 +245,7 @@ __global__ __launch_bounds__(64 * (HMAX / HPW)) void prefill_kernel(Params p) {
     int* s_order = reinterpret_cast<int*>(smem + 8 * kRankRows);   // rows by rank
     const int nb = static_cast<int>(p.B);
     if (tid < nb)
-      s_len[tid] = rd_index(p.prefix, p.idx_i64, tid) + rd_index(p.cu, p.idx_i64, tid + 1) - rd_index(p.cu, p.idx_i64, tid);
+      s_len[tid] = rd_index<I64>(p.prefix, tid) + rd_index<I64>(p.cu, tid + 1) - rd_index<I64>(p.cu, tid);
     lds_barrier();
     if (tid < nb) {
       const int64_t mine = s_len[tid];
@@ -250,11 +260,11 @@ __global__ __launch_bounds__(64 * (HMAX / HPW)) void prefill_kernel(Params p) {
     b = __builtin_amdgcn_readfirstlane(s_order[rr]);
     lds_barrier();  // the tile buffers the ranking used are written next
   }
-  const int64_t tok0 = rd_index(p.cu, p.idx_i64, b);
-  const int64_t n_new = rd_index(p.cu, p.idx_i64, b + 1) - tok0;
+  const int64_t tok0 = rd_index<I64>(p.cu, b);
+  const int64_t n_new = rd_index<I64>(p.cu, b + 1) - tok0;
   const int64_t n0 = static_cast<int64_t>(pt) * POS;
   if (n0 >= n_new) return;
-  const int64_t prefix = rd_index(p.prefix, p.idx_i64, b);
+  const int64_t prefix = rd_index<I64>(p.prefix, b);
   const int64_t kv_len = prefix + min(n_new, n0 + POS);  // keys any of the 16 positions may see
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -267,9 +277,17 @@ __global__ __launch_bounds__(64 * (HMAX / HPW)) void prefill_kernel(Params p) {
 
   // the row's block table, once (entries outside the pool become -1)
   const int64_t nlb = min64((kv_len + BS - 1) / BS, p.max_blocks);
-  for (int64_t lb = tid; lb < min64(nlb, MAXB); lb += C::NT) {
-    const int64_t e = rd_index(p.tables, p.table_i64, b * p.table_stride + lb);
-    s_phys[lb] = e >= 0 && e < p.num_blocks ? static_cast<int>(e) : -1;
+  {
+    // two entries per thread per step, both loads issued before either is used (the second at a
+    // clamped index when it lies past the row)
+    const int64_t lim = min64(nlb, MAXB);
+    for (int64_t lb = tid; lb < lim; lb += 2 * C::NT) {
+      const int64_t lb2 = lb + C::NT;
+      const int64_t e0 = rd_index<T64>(p.tables, b * p.table_stride + lb);
+      const int64_t e1 = rd_index<T64>(p.tables, b * p.table_stride + min64(lb2, lim - 1));
+      s_phys[lb] = e0 >= 0 && e0 < p.num_blocks ? static_cast<int>(e0) : -1;
+      if (lb2 < lim) s_phys[lb2] = e1 >= 0 && e1 < p.num_blocks ? static_cast<int>(e1) : -1;
+    }
   }
 
   const bf16_t* kb = p.kbase + static_cast<int64_t>(g) * p.sG;
@@ -282,9 +300,9 @@ __global__ __launch_bounds__(64 * (HMAX / HPW)) void prefill_kernel(Params p) {
   auto Vt = [&](int i) { return smem_lds + static_cast<uint32_t>((2 + i) * TB); };
   lds_barrier();  // s_phys
   // Block ids of tiles kt .. kt+2 (wave-uniform), each looked up once
-  int4 phys_cur = tile_phys(p, b, 0, kv_len, s_phys, nlb);
-  int4 phys_n1 = tile_phys(p, b, KT, kv_len, s_phys, nlb);
-  int4 phys_n2 = tile_phys(p, b, 2 * KT, kv_len, s_phys, nlb);
+  int4 phys_cur = tile_phys<T64>(p, b, 0, kv_len, s_phys, nlb);
+  int4 phys_n1 = tile_phys<T64>(p, b, KT, kv_len, s_phys, nlb);
+  int4 phys_n2 = tile_phys<T64>(p, b, 2 * KT, kv_len, s_phys, nlb);
   if (copier) {
     copy_tile<CC>(p, 0, kv_len, kb, phys_cur, cl, smem, smem_lds, Kt(0), wave, lane);
     copy_tile<CC>(p, 0, kv_len, vb, phys_cur, cl, smem, smem_lds, Vt(0), wave, lane);
@@ -371,7 +389,7 @@ __global__ __launch_bounds__(64 * (HMAX / HPW)) void prefill_kernel(Params p) {
   for (int64_t kt = 0; kt < ntiles; ++kt) {
     const int64_t key0 = kt * KT;
     const int cb = static_cast<int>(kt & 1);
-    const int4 phys_n3 = tile_phys(p, b, key0 + 3 * KT, kv_len, s_phys, nlb);
+    const int4 phys_n3 = tile_phys<T64>(p, b, key0 + 3 * KT, kv_len, s_phys, nlb);
     if (copier) {
       if (kt + 2 < ntiles) copy_tile<CC>(p, key0 + 2 * KT, kv_len, kb, phys_n2, cl, smem, smem_lds, Kt(cb), wave, lane);
       if (kt + 1 < ntiles) copy_tile<CC>(p, key0 + KT, kv_len, vb, phys_n1, cl, smem, smem_lds, Vt(cb ^ 1), wave, lane);
@@ -563,6 +581,32 @@ __global__ __launch_bounds__(64 * (HMAX / HPW)) void prefill_kernel(Params p) {
 }  // namespace pfx
 }  // namespace qa
 
+namespace qa {
+namespace pfx {
+
+template <int D, bool I64, bool T64>
+static int launch_one(const Params& p, dim3 grid, hipStream_t stream) {
+  static bool attr_set = false;  // per instantiation
+  if (!attr_set) {
+    const hipError_t err = hipFuncSetAttribute(reinterpret_cast<const void*>(&prefill_kernel<D, kHeadsPerWave, I64, T64>),
+                                               hipFuncAttributeMaxDynamicSharedMemorySize, Smem<D>::kBytes);
+    if (err != hipSuccess) return fail("paged prefill: cannot reserve %d bytes of LDS: %s", Smem<D>::kBytes, hipGetErrorString(err));
+    attr_set = true;
+  }
+  hipLaunchKernelGGL((prefill_kernel<D, kHeadsPerWave, I64, T64>), grid, dim3(Cfg<D, kHeadsPerWave>::NT), Smem<D>::kBytes, stream, p);
+  return 0;
+}
+
+template <int D>
+static int launch_prefill(const Params& p, dim3 grid, hipStream_t stream) {
+  if (p.idx_i64)
+    return p.table_i64 ? launch_one<D, true, true>(p, grid, stream) : launch_one<D, true, false>(p, grid, stream);
+  return p.table_i64 ? launch_one<D, false, true>(p, grid, stream) : launch_one<D, false, false>(p, grid, stream);
+}
+
+}  // namespace pfx
+}  // namespace qa
+
 extern "C" int qa_paged_attention_prefill(const void* query, int32_t q_dtype, int64_t q_stride_t, int64_t q_stride_h,
                                           const void* cu_seqlens, const void* prefix_lens, int32_t idx_dtype,
                                           int64_t batch, int64_t max_new, int32_t heads, int32_t head_dim,
@@ -615,25 +659,10 @@ extern "C" int qa_paged_attention_prefill(const void* query, int32_t q_dtype, in
   p.D = head_dim;
   p.scale = scale > 0.f ? scale : 1.0f / sqrtf(static_cast<float>(head_dim));
   dim3 grid(static_cast<unsigned>(ceil_div(max_new, POS)), static_cast<unsigned>(batch * kv->kv_heads));
-  using C256 = Cfg<256, kHeadsPerWave>;
-  using C128 = Cfg<128, kHeadsPerWave>;
-  static bool attr_set = false;
-  if (!attr_set) {
-    hipError_t err = hipFuncSetAttribute(reinterpret_cast<const void*>(&prefill_kernel<256, kHeadsPerWave>),
-                                         hipFuncAttributeMaxDynamicSharedMemorySize, Smem<256>::kBytes);
-    if (err == hipSuccess)
-      err = hipFuncSetAttribute(reinterpret_cast<const void*>(&prefill_kernel<128, kHeadsPerWave>),
-                                hipFuncAttributeMaxDynamicSharedMemorySize, Smem<128>::kBytes);
-    if (err != hipSuccess) return fail("paged prefill: cannot reserve %d bytes of LDS: %s", Smem<256>::kBytes, hipGetErrorString(err));
-    attr_set = true;
-  }
   {
     KernelTimer timer_("paged_prefill", stream);
-    if (head_dim == 256) {
-      hipLaunchKernelGGL((prefill_kernel<256, kHeadsPerWave>), grid, dim3(C256::NT), Smem<256>::kBytes, stream, p);
-    } else {
-      hipLaunchKernelGGL((prefill_kernel<128, kHeadsPerWave>), grid, dim3(C128::NT), Smem<128>::kBytes, stream, p);
-    }
+    const int rc = head_dim == 256 ? launch_prefill<256>(p, grid, stream) : launch_prefill<128>(p, grid, stream);
+    if (rc != 0) return rc;
   }
   return check_launch("paged prefill");
 }
