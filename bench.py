@@ -40,7 +40,7 @@ HBM_PEAK_GBS = 8000.0  # MI355X HBM3E, GB/s
 # are the committed profile's, not measured live.
 TRAFFIC_DECODE = 1959210677
 TRAFFIC_DELTA = 822685286  # chunk_kernel alone; the step (with prep_kernel) moves 1,400,024,473
-TRAFFIC_PREFILL = 888510552  # average over the eight per-chunk launches
+TRAFFIC_PREFILL = 888476672  # average over the eight per-chunk launches
 TRAFFIC_PROLOGUE = 675674420
 TRAFFIC_OUTPUT_NORM = 805417779
 TRAFFIC_FP8_LINEAR = 29648896  # x-resident kernel (one launch), from profiles/fp8_linear_config5_batch.md
