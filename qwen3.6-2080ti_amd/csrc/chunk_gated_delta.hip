@@ -83,8 +83,8 @@ inline Workspace workspace_layout(int64_t batch, int64_t seq, int64_t hk, int64_
   const int64_t qk = batch * w.tp * hk * DK * 2;  // qn, kn: (B, Tp, Hk, 128)
   w.off_qn = 0;
   w.off_kn = align256(w.off_qn + qk);
-  w.off_gb = align256(w.off_kn + qk);  // gb: (B, Hv, Tp, 2) fp32 (G, beta)
-  w.bytes = align256(w.off_gb + batch * hv * w.tp * 2 * 4);
+  w.off_gb = align256(w.off_kn + qk);  // gb: (B, Hv, Tp, 4) fp32 (G, beta, exp(G), exp(G_C - G))
+  w.bytes = align256(w.off_gb + batch * hv * w.tp * 4 * 4);
   return w;
 }
 
@@ -102,7 +102,7 @@ constexpr int ST_BYTES = DVS * LD128 * 2;          // one St [dv][dk] (fp16 copy
 constexpr int AQK_BYTES = CH * LD64 * 2;           // one Aqk [i][l]
 constexpr int DT_BYTES = DVS * LD64 * 2;           // one delta^T [dv][tok]
 constexpr int KS_BYTES = CH * LD128 * 2;           // one Q or K tile
-constexpr int SC_BYTES = 3 * CH * 4;               // beta, G, gamma per token
+constexpr int SC_BYTES = 4 * CH * 4;               // beta, G, gamma, exp(G_C - G) per token
 constexpr int OFF_QS = 0;                          // Qs [tok][dk]
 constexpr int OFF_KS = OFF_QS + KS_BYTES;          // Ks [tok][dk] x 2
 constexpr int OFF_VS = OFF_KS + 2 * KS_BYTES;      // Vs [tok][dv] (this workgroup's half)
@@ -338,8 +338,11 @@ __device__ __forceinline__ void gate_item(const GateParams& p, int64_t item, int
     const float up = __shfl_up(G, off, 64);
     if (lane >= off) G += up;
   }
-  float2* dst = reinterpret_cast<float2*>(p.gb) + (b * p.Hv + hv) * p.tp + t;
-  *dst = make_float2(G, beta);
+  // the decay factors the chunk kernel applies per token, exp(G) and exp(G_C - G) (G_C: the
+  // chunk's last token; tokens past the sequence add g = 0, so G_C is that of the last one)
+  const float gC = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, G), CH - 1));
+  float4* dst = reinterpret_cast<float4*>(p.gb) + (b * p.Hv + hv) * p.tp + t;
+  *dst = make_float4(G, beta, __expf(G), __expf(gC - G));
 }
 
 // ---------------------------------------------------------------------------
@@ -383,7 +386,8 @@ __device__ __forceinline__ void split4(const cfloat4& v, h4_v& hi, h4_v& lo) {
 
 // One chunk's inputs, staged in registers while the previous chunk is computed:
 // 16-byte pieces of the fp16 q and k rows, the raw bf16 v of token (tid % 64) in this wave's
-// eight channels of the workgroup's v half, and (G, beta) (used by threads < 32).
+// eight channels of the workgroup's v half, and (G, beta, exp(G), exp(G_C - G)) of token tid % 64
+// (used by wave 0).
 struct ChunkRegs {
   u32x4 q0, q1, k0, k1, v;
   cfloat4 gb;
@@ -410,7 +414,7 @@ __device__ __forceinline__ ChunkRegs load_chunk(const ChunkParams& p, int64_t b,
 #pragma unroll
     for (int e = 0; e < 4; ++e) r.v[e] = reinterpret_cast<const uint32_t*>(src)[e];
   }
-  r.gb = *reinterpret_cast<const cfloat4*>(p.gb + ((b * p.Hv + j) * p.tp + t0) * 2 + 4 * (tid & (CH / 2 - 1)));
+  r.gb = *reinterpret_cast<const cfloat4*>(p.gb + ((b * p.Hv + j) * p.tp + t0 + (tid & (CH - 1))) * 4);
   return r;
 }
 
@@ -533,18 +537,17 @@ __device__ __forceinline__ void stage_chunk(const ChunkParams& p, unsigned char*
   float* s_beta = reinterpret_cast<float*>(smem + OFF_SC + (ci & 1) * SC_BYTES);
   float* s_G = s_beta + CH;
   float* s_gam = s_G + CH;
+  float* s_dec = s_gam + CH;
   const int c0 = tid, c1 = tid + NT;
   *reinterpret_cast<u32x4*>(Qs + (c0 >> 4) * LD128 + 8 * (c0 & 15)) = nx.q0;
   *reinterpret_cast<u32x4*>(Qs + (c1 >> 4) * LD128 + 8 * (c1 & 15)) = nx.q1;
   *reinterpret_cast<u32x4*>(Ks + (c0 >> 4) * LD128 + 8 * (c0 & 15)) = nx.k0;
   *reinterpret_cast<u32x4*>(Ks + (c1 >> 4) * LD128 + 8 * (c1 & 15)) = nx.k1;
-  if (tid < CH / 2) {
-    s_G[2 * tid] = nx.gb.x;
-    s_beta[2 * tid] = nx.gb.y;
-    s_G[2 * tid + 1] = nx.gb.z;
-    s_beta[2 * tid + 1] = nx.gb.w;
-    s_gam[2 * tid] = __expf(nx.gb.x);
-    s_gam[2 * tid + 1] = __expf(nx.gb.z);
+  if (tid < CH) {
+    s_G[tid] = nx.gb.x;
+    s_beta[tid] = nx.gb.y;
+    s_gam[tid] = nx.gb.z;
+    s_dec[tid] = nx.gb.w;
   }
   const int lane = tid & 63;
   // tokens past the sequence: v = 0 (a multiply, not a branch, so no wait sits inside a branch)
@@ -761,7 +764,7 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(2, 2))) void
         ah[n] = src[0];
         al[n] = src[1];
       }
-      const float gC = s_G[CH - 1];
+      const float* s_dec = s_gam + CH;
       h4_v xh[4], xl[4];
       cfloat4 dd[4];  // exp(G_C - G) delta, C layout
 #pragma unroll
@@ -773,7 +776,7 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(2, 2))) void
           const int n = pb * (pb - 1) / 2 + k;
           acc = mma3(ah[n], al[n], xh[k], xl[k], acc);
         }
-        const cfloat4 gi = *reinterpret_cast<const cfloat4*>(s_G + i0);
+        const cfloat4 de = *reinterpret_cast<const cfloat4*>(s_dec + i0);
         h4_v rh, rl;
         split4(R[pb] - acc, rh, rl);
         const cfloat4 zero = {0.f, 0.f, 0.f, 0.f};
@@ -781,7 +784,7 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(2, 2))) void
         split4(d, xh[pb], xl[pb]);
         store4h(Dt + (ci & 1) * (DT_BYTES / 2) + (16 * v + lc) * LD64 + i0, d[0], d[1], d[2], d[3]);
 #pragma unroll
-        for (int r = 0; r < 4; ++r) dd[pb][r] = __expf(gC - gi[r]) * d[r];
+        for (int r = 0; r < 4; ++r) dd[pb][r] = de[r] * d[r];
       }
       // S update.  k-step s covers tokens 32 s .. 32 s + 31, slot e of lane (lq, lc) being
       // token 32 s + 4 lq + e (e < 4, block 2 s) or 32 s + 16 + 4 lq + e - 4 (block 2 s + 1):
