@@ -77,6 +77,21 @@ def test_chunked_prefill_weak_decay_long_memory_state_precision() -> None:
     assert _rel(out, ref_core) < 5e-3
 
 
+def test_chunked_prefill_strong_and_mixed_decay_matches_oracle() -> None:
+    # The chunk kernel forms the in-chunk decays exp(G_i - G_l) from one exponential per row
+    # when every 16-token block of a chunk decays by at most e^60, and from one per element
+    # otherwise.  Heads with A_log up to ~+4 (g down to ~-50 per token) and a run of tokens with
+    # large a put chunks of both kinds into one sequence and one launch.
+    mixed, a, b, a_log, dt_bias, w = _inputs(45, 2, 300, SHAPE, a_log_scale=2.0)
+    a[:, 100:140] += 8.0
+    a_log[0] = 3.5
+    ref_core, ref_state, _ = gd.linear_attention_core(mixed.float(), a, b, a_log, dt_bias, w, SHAPE)
+    out, state, _ = _run(mixed, a, b, a_log, dt_bias, w, SHAPE, out_dtype=torch.float32)
+    assert _rel(state, ref_state) < 1e-3
+    assert _rel(out, ref_core) < 5e-3
+    torch.testing.assert_close(out.cpu(), ref_core, atol=2e-2, rtol=2e-2)
+
+
 def test_prefill_then_decode_equals_longer_prefill() -> None:
     import hip_ops
 
