@@ -767,21 +767,26 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(2, 2))) void
       const float* s_dec = s_gam + CH;
       h4_v xh[4], xl[4];
       cfloat4 dd[4];  // exp(G_C - G) delta, C layout
+      // sum_{k<p} A_pk delta_k is accumulated as soon as each delta_k exists (pacc[p] takes the
+      // terms in the order k = 0, 1, ..), so only one product per block waits on the previous
+      // block's delta.
+      cfloat4 pacc[4];
+#pragma unroll
+      for (int pb = 0; pb < 4; ++pb) pacc[pb] = cfloat4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int pb = 0; pb < 4; ++pb) {
         const int i0 = 16 * pb + 4 * lq;
-        cfloat4 acc = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-        for (int k = 0; k < pb; ++k) {
-          const int n = pb * (pb - 1) / 2 + k;
-          acc = mma3(ah[n], al[n], xh[k], xl[k], acc);
-        }
         const cfloat4 de = *reinterpret_cast<const cfloat4*>(s_dec + i0);
         h4_v rh, rl;
-        split4(R[pb] - acc, rh, rl);
+        split4(R[pb] - pacc[pb], rh, rl);
         const cfloat4 zero = {0.f, 0.f, 0.f, 0.f};
         const cfloat4 d = mma3(dh[pb], dl[pb], rh, rl, zero);
         split4(d, xh[pb], xl[pb]);
+#pragma unroll
+        for (int q = pb + 1; q < 4; ++q) {
+          const int n = q * (q - 1) / 2 + pb;
+          pacc[q] = mma3(ah[n], al[n], xh[pb], xl[pb], pacc[q]);
+        }
         store4h(Dt + (ci & 1) * (DT_BYTES / 2) + (16 * v + lc) * LD64 + i0, d[0], d[1], d[2], d[3]);
 #pragma unroll
         for (int r = 0; r < 4; ++r) dd[pb][r] = de[r] * d[r];
