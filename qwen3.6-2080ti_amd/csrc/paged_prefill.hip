@@ -412,7 +412,8 @@ __global__ __launch_bounds__(64 * (HMAX / HPW)) void prefill_kernel(Params p) {
       }
 
       // ---- softmax of this tile, cut into slices that phase A spreads between its products:
-      // slices 0 .. HPW*ST-1 scale one sub-tile and fold it into the lane's max; the next HPW
+      // slices 0 .. HPW*ST-1 fold one sub-tile of raw scores into the lane's max (the scale is
+      // positive, so it is applied to the max and inside the exponent's FMA); the next HPW
       // finish one head's max over the four lanes of a column (permlane swaps) and its
       // lazily rescaled running max; the next HPW*ST*2 turn two scores into probabilities
       float mx[HPW], m_use[HPW], alpha[HPW], psum[HPW];
@@ -427,15 +428,14 @@ __global__ __launch_bounds__(64 * (HMAX / HPW)) void prefill_kernel(Params p) {
       auto slice = [&](int k) {
         if (k < HPW * ST) {
           const int hh = k / ST, st = k % ST;
-          s_cur[hh][st] *= scale_l2;
-          mx[hh] = fmaxf(mx[hh], fmaxf(fmaxf(s_cur[hh][st][0], s_cur[hh][st][1]), fmaxf(s_cur[hh][st][2], s_cur[hh][st][3])));
+          mx[hh] = fmaxf(fmaxf(mx[hh], s_cur[hh][st][0]), fmaxf(fmaxf(s_cur[hh][st][1], s_cur[hh][st][2]), s_cur[hh][st][3]));
           asm volatile("" : "+v"(s_cur[hh][st]), "+v"(mx[hh]));
         } else if (k < HPW * ST + HPW) {
           const int hh = k - HPW * ST;
           const auto r32 = __builtin_amdgcn_permlane32_swap(__float_as_uint(mx[hh]), __float_as_uint(mx[hh]), false, false);
           const float m2 = fmaxf(__uint_as_float(r32[0]), __uint_as_float(r32[1]));
           const auto r16 = __builtin_amdgcn_permlane16_swap(__float_as_uint(m2), __float_as_uint(m2), false, false);
-          const float m4 = fmaxf(__uint_as_float(r16[0]), __uint_as_float(r16[1]));
+          const float m4 = fmaxf(__uint_as_float(r16[0]), __uint_as_float(r16[1])) * scale_l2;
           // lazy rescaling: the running max only moves when this tile's max exceeds it by
           // more than 8 (log2 units), so probabilities stay below 2^8 and the accumulators are
           // rarely rescaled; the result is the same softmax, as numerator and denominator
@@ -452,7 +452,7 @@ __global__ __launch_bounds__(64 * (HMAX / HPW)) void prefill_kernel(Params p) {
           const int hh = j / (2 * ST), st = (j / 2) % ST, r0 = 2 * (j & 1);
 #pragma unroll
           for (int r = r0; r < r0 + 2; ++r) {
-            const float pr = __builtin_amdgcn_exp2f(s_cur[hh][st][r] - m_use[hh]);
+            const float pr = __builtin_amdgcn_exp2f(__builtin_fmaf(s_cur[hh][st][r], scale_l2, -m_use[hh]));
             psum[hh] += pr;
             pb[hh][st][r] = static_cast<short>(f32_to_bf16(pr));
           }
