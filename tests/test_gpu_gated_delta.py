@@ -238,6 +238,46 @@ def test_conv_fused_step_equals_conv_update_then_step(key_heads, value_heads, x_
         assert torch.equal(s_fused[r], state0[r]) and torch.equal(c_fused[r], conv0[r])
 
 
+@pytest.mark.parametrize("key_heads,value_heads", [(16, 32), (16, 16)])
+@pytest.mark.parametrize("norm", [False, True])
+def test_conv_fused_step_large_batch_equals_conv_update_then_step(key_heads, value_heads, norm) -> None:
+    """A config-5-sized batch (80 rows x 16 key heads, more workgroups than the GPU holds at once):
+    the fused step stays bit-equal to qa_causal_conv1d_update + qa_gated_delta_step(_norm) over two
+    tokens, with a -1 pad and an id past the pool among the slots, and leaves unused pool rows
+    untouched."""
+    ops = _ops()
+    shape = gd.LinearShape(key_heads=key_heads, value_heads=value_heads, key_head_dim=128, value_head_dim=128, conv_kernel_dim=4)
+    batch, rows = 80, 84
+    mixed, a, b, a_log, dt_bias, w = _layer_inputs(70 + value_heads, batch, 2, shape)
+    gen = torch.Generator(device=DEV).manual_seed(71)
+    state0 = torch.randn(rows, value_heads, 128, 128, generator=gen, device=DEV) * 0.05
+    conv0 = torch.randn(rows, shape.qkv_dim, 3, generator=gen, device=DEV)
+    slots = torch.randperm(rows, generator=torch.Generator().manual_seed(72))[:batch].to(torch.int64)
+    slots[5] = -1
+    slots[17] = rows
+    used = set(int(s) for s in slots.tolist() if 0 <= s < rows)
+    slots = slots.to(DEV)
+    z = torch.randn(2, batch, value_heads * 128, generator=gen, device=DEV).to(torch.bfloat16)
+    nw = 1 + 0.1 * torch.randn(128, generator=gen, device=DEV)
+    s_ref, c_ref = state0.clone(), conv0.clone()
+    s_fused, c_fused = state0.clone(), conv0.clone()
+    for step in range(2):
+        x = mixed[:, step].to(torch.bfloat16).contiguous().to(DEV)
+        av, bv = a[:, step].contiguous().to(DEV), b[:, step].contiguous().to(DEV)
+        kw = dict(key_heads=key_heads, slots=slots, out_dtype=torch.bfloat16)
+        if norm:
+            kw.update(z=z[step], norm_weight=nw)
+        act = ops.causal_conv1d_update(x, c_ref, w.to(DEV), slots)
+        ref = ops.gated_delta_step(act, av, bv, a_log.to(DEV), dt_bias.to(DEV), s_ref, **kw)
+        out = ops.gated_delta_step_conv(x, c_fused, w.to(DEV), av, bv, a_log.to(DEV), dt_bias.to(DEV), s_fused, **kw)
+        assert torch.equal(out, ref), f"step {step}: max diff {(out.float() - ref.float()).abs().max().item()}"
+        assert torch.equal(s_fused, s_ref) and torch.equal(c_fused, c_ref)
+        assert torch.count_nonzero(out[5]) == 0 and torch.count_nonzero(out[17]) == 0
+    for r in range(rows):
+        if r not in used:
+            assert torch.equal(s_fused[r], state0[r]) and torch.equal(c_fused[r], conv0[r])
+
+
 def test_conv_fused_step_rejects_unsupported_head_ratio() -> None:
     ops = _ops()
     shape = gd.LinearShape(key_heads=1, value_heads=3, key_head_dim=128, value_head_dim=128, conv_kernel_dim=4)
