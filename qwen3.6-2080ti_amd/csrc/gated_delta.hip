@@ -6,10 +6,12 @@
 // (src/reference_ops.py:310-318):
 //   S <- S * exp(g_t);  kv = S^T k_t;  delta = (v_t - kv) * beta_t;
 //   S <- S + k_t delta^T;  o_t = S^T q_t
-// The 128x128 fast path keeps S in registers: 256 threads, thread (wave w,
-// lane = 16*rg + cg) owns rows 32w + 8rg + [0,8) and columns 8cg + [0,8); the
-// two reductions over dk per token run as a 2-step shuffle inside each wave
-// plus a 4-way LDS sum across waves.
+// The 128x128 fast paths keep S in registers on 256 threads.  The multi-token
+// core (delta_recurrent_128): thread (wave w, lane = 16*rg + cg) owns rows
+// 32w + 8rg + [0,8) and columns 8cg + [0,8); the two reductions over dk per
+// token run as a 2-step shuffle inside each wave plus a 4-way LDS sum across
+// waves.  The single-token decode steps use the column layout described at
+// load_state_cols, whose reductions stay inside each wave.
 #include "qa_common.h"
 
 namespace qa {
@@ -480,13 +482,196 @@ __device__ __forceinline__ void step_128(const DeltaParams& p, int64_t b, int h,
   }
 }
 
+// ---------------------------------------------------------------------------
+// Column layout of a value head's 128x128 state for the single-token steps: thread tid of the
+// head's 256 (wave w = tid / 64, lane l) holds rows 8 (l / 4) + [0, 8) and columns
+// 32 w + 8 (l % 4) + [0, 8).  Each wave owns 32 whole columns, so the l2 norms of q and k and both
+// sums over dk of the recurrence stay inside the wave (a butterfly over the 16 lanes of equal
+// l % 4; xor partners add the same two values, so every lane gets the same sum), and a step needs
+// no LDS exchange or workgroup barrier except for the output stage's mean over the 128 columns.
+
+__device__ __forceinline__ void load_state_cols(const float* s, int tid, float (&S)[8][8]) {
+  constexpr int DV = 128;
+  const int lane = tid & 63;
+  const int row0 = 8 * (lane >> 2);
+  const int col0 = 32 * (tid >> 6) + 8 * (lane & 3);
+#pragma unroll
+  for (int r = 0; r < 8; ++r) {
+    const float4 lo = *reinterpret_cast<const float4*>(s + (row0 + r) * DV + col0);
+    const float4 hi = *reinterpret_cast<const float4*>(s + (row0 + r) * DV + col0 + 4);
+    S[r][0] = lo.x; S[r][1] = lo.y; S[r][2] = lo.z; S[r][3] = lo.w;
+    S[r][4] = hi.x; S[r][5] = hi.y; S[r][6] = hi.z; S[r][7] = hi.w;
+  }
+}
+
+// sum over the 16 lanes of the wave that share l % 4 (lanes l ^ 4, ^ 8, ^ 16, ^ 32)
+__device__ __forceinline__ float rows_sum(float v) {
+  v += __shfl_xor(v, 4, 64);
+  v += __shfl_xor(v, 8, 64);
+  v += __shfl_xor(v, 16, 64);
+  v += __shfl_xor(v, 32, 64);
+  return v;
+}
+
+// The output stage's z and norm weight of the 8 outputs a lane l < 4 of wave w holds (columns
+// 32 w + 8 l .. + 7), as raw bits, issued before they are needed (see NormIn).
+template <bool NORM>
+__device__ __forceinline__ void load_norm_in_cols(const DeltaParams& p, int64_t b, int h, int tid, NormIn& n) {
+  if constexpr (NORM) {
+    const int lane = tid & 63;
+    if (p.norm_vec && lane < 4) {
+      const int col0 = 32 * (tid >> 6) + 8 * lane;
+      const int64_t zi = b * p.z_sb + static_cast<int64_t>(h) * 128 + col0;
+      if (p.z_dtype == QA_BF16) {
+        n.z[0] = *reinterpret_cast<const uint4*>(reinterpret_cast<const bf16_t*>(p.z) + zi);
+      } else {
+        n.z[0] = *reinterpret_cast<const uint4*>(reinterpret_cast<const float*>(p.z) + zi);
+        n.z[1] = *reinterpret_cast<const uint4*>(reinterpret_cast<const float*>(p.z) + zi + 4);
+      }
+      if (p.norm_dtype == QA_BF16) {
+        n.w[0] = *reinterpret_cast<const uint4*>(reinterpret_cast<const bf16_t*>(p.norm_w) + col0);
+      } else {
+        n.w[0] = *reinterpret_cast<const uint4*>(reinterpret_cast<const float*>(p.norm_w) + col0);
+        n.w[1] = *reinterpret_cast<const uint4*>(reinterpret_cast<const float*>(p.norm_w) + col0 + 4);
+      }
+    }
+  }
+}
+
+// step_128 on the column layout (load_state_cols of s): the same arithmetic per element, l2 norms,
+// gating, one recurrence step, with NORM the output stage; nrm holds the four waves' partial sums
+// of squares of the outputs.
+template <bool NORM>
+__device__ __forceinline__ void step_cols(const DeltaParams& p, int64_t b, int h, float* s, float (&S)[8][8], uint32_t a_bits, uint32_t b_bits,
+                                          const float* qv, const float* kvv, const float* vv, float (&nrm)[4], int tid) {
+  constexpr int DK = 128, DV = 128;
+  const int w = tid >> 6;
+  const int lane = tid & 63;
+  const int row0 = 8 * (lane >> 2);
+  const int col0 = 32 * w + 8 * (lane & 3);
+  float kr[8], qr[8], vc[8];
+  float sq = 0.f, sk = 0.f;
+#pragma unroll
+  for (int r = 0; r < 8; ++r) {
+    qr[r] = qv[row0 + r];
+    kr[r] = kvv[row0 + r];
+    sq += qr[r] * qr[r];
+    sk += kr[r] * kr[r];
+  }
+#pragma unroll
+  for (int c = 0; c < 8; ++c) vc[c] = vv[col0 + c];
+  sq = rows_sum(sq);
+  sk = rows_sum(sk);
+  const float rq = rsqrtf(sq + 1e-6f) * rsqrtf(static_cast<float>(DK));
+  const float rk = rsqrtf(sk + 1e-6f);
+#pragma unroll
+  for (int r = 0; r < 8; ++r) {
+    qr[r] *= rq;
+    kr[r] *= rk;
+  }
+  const float av = bits_to_f32(a_bits, p.ab_dtype == QA_BF16);
+  const float bv = bits_to_f32(b_bits, p.ab_dtype == QA_BF16);
+  const float gval = -__expf(p.a_log[h]) * softplus_ref(av + p.dt_bias[h]);
+  const float decay = __expf(gval);
+  const float beta = sigmoid_ref(bv);
+  // S *= decay; delta = (v - S^T k) beta; S += k delta^T; o = S^T q  (src/reference_ops.py:310-318)
+  float part[8];
+#pragma unroll
+  for (int c = 0; c < 8; ++c) {
+    float acc = 0.f;
+#pragma unroll
+    for (int r = 0; r < 8; ++r) {
+      S[r][c] *= decay;
+      acc += S[r][c] * kr[r];
+    }
+    part[c] = acc;
+  }
+#pragma unroll
+  for (int c = 0; c < 8; ++c) part[c] = rows_sum(part[c]);
+  float delta[8];
+#pragma unroll
+  for (int c = 0; c < 8; ++c) delta[c] = (vc[c] - part[c]) * beta;
+#pragma unroll
+  for (int c = 0; c < 8; ++c) {
+    float acc = 0.f;
+#pragma unroll
+    for (int r = 0; r < 8; ++r) {
+      S[r][c] += kr[r] * delta[c];
+      acc += S[r][c] * qr[r];
+    }
+    part[c] = acc;
+  }
+  // the state goes back first (its stores need nothing that follows), then the output stage's
+  // inputs are loaded into the registers it held, in flight during the reductions
+#pragma unroll
+  for (int r = 0; r < 8; ++r) {
+    *reinterpret_cast<float4*>(s + (row0 + r) * DV + col0) = make_float4(S[r][0], S[r][1], S[r][2], S[r][3]);
+    *reinterpret_cast<float4*>(s + (row0 + r) * DV + col0 + 4) = make_float4(S[r][4], S[r][5], S[r][6], S[r][7]);
+  }
+  NormIn nin;
+  load_norm_in_cols<NORM>(p, b, h, tid, nin);
+  float o[8];
+#pragma unroll
+  for (int c = 0; c < 8; ++c) o[c] = rows_sum(part[c]);
+  if (NORM) {
+    // the layer's output stage on the fp32 core (src/reference_ops.py:172-178,284-287: the core
+    // reaches gated_rms_norm in fp32, so its cast of the normalised value is the identity):
+    // (w * o / sqrt(mean(o^2) + eps)) * silu(z); the mean spans the four waves' columns
+    float ss = 0.f;
+#pragma unroll
+    for (int c = 0; c < 8; ++c) ss += o[c] * o[c];
+    ss += __shfl_xor(ss, 1, 64);
+    ss += __shfl_xor(ss, 2, 64);
+    if (lane == 0) nrm[w] = ss;
+    __syncthreads();
+    const float tot = (nrm[0] + nrm[1]) + (nrm[2] + nrm[3]);
+    const float r = 1.0f / sqrtf(tot / static_cast<float>(DV) + p.norm_eps);
+    if (lane < 4) {
+      if (p.norm_vec) {
+#pragma unroll
+        for (int c = 0; c < 8; ++c) {
+          const float zv = norm_elem(nin.z, p.z_dtype == QA_BF16, c);
+          const float wv = norm_elem(nin.w, p.norm_dtype == QA_BF16, c);
+          o[c] = (wv * (o[c] * r)) * __fdividef(zv, 1.0f + __expf(-zv));
+        }
+      } else {
+#pragma unroll
+        for (int c = 0; c < 8; ++c) {
+          const float zv = load_any(p.z, p.z_dtype, b * p.z_sb + static_cast<int64_t>(h) * DV + col0 + c);
+          const float wv = load_any(p.norm_w, p.norm_dtype, col0 + c);
+          o[c] = (wv * (o[c] * r)) * __fdividef(zv, 1.0f + __expf(-zv));
+        }
+      }
+    }
+  }
+  if (lane < 4) {
+    const int64_t oi = b * p.out_sb + static_cast<int64_t>(h) * DV + col0;
+    if (p.out_vec) {
+      if (p.out_dtype == QA_BF16) {
+        uint4 u;
+        u.x = static_cast<uint32_t>(f32_to_bf16(o[0])) | (static_cast<uint32_t>(f32_to_bf16(o[1])) << 16);
+        u.y = static_cast<uint32_t>(f32_to_bf16(o[2])) | (static_cast<uint32_t>(f32_to_bf16(o[3])) << 16);
+        u.z = static_cast<uint32_t>(f32_to_bf16(o[4])) | (static_cast<uint32_t>(f32_to_bf16(o[5])) << 16);
+        u.w = static_cast<uint32_t>(f32_to_bf16(o[6])) | (static_cast<uint32_t>(f32_to_bf16(o[7])) << 16);
+        *reinterpret_cast<uint4*>(reinterpret_cast<bf16_t*>(p.out) + oi) = u;
+      } else {
+        float* op = reinterpret_cast<float*>(p.out) + oi;
+        *reinterpret_cast<float4*>(op) = make_float4(o[0], o[1], o[2], o[3]);
+        *reinterpret_cast<float4*>(op + 4) = make_float4(o[4], o[5], o[6], o[7]);
+      }
+    } else {
+#pragma unroll
+      for (int c = 0; c < 8; ++c) store_any(p.out, p.out_dtype, oi + c, o[c]);
+    }
+  }
+}
+
 // Fused decode step on the post-conv row qkv (B, C) in global memory: a workgroup per (row, value
 // head).
 template <bool NORM>
 __global__ __launch_bounds__(256) void delta_step_128(DeltaParams p) {
   constexpr int DK = 128, DV = 128;
-  __shared__ float red[2][4][DV];
-  __shared__ float nrm[2][4];
+  __shared__ float nrm[4];
   const int64_t b = blockIdx.x / p.H;
   const int h = blockIdx.x - static_cast<int>(b) * p.H;
   const int64_t slot = slot_of(p.slots, p.slots_i64, b);
@@ -501,9 +686,9 @@ __global__ __launch_bounds__(256) void delta_step_128(DeltaParams p) {
   const uint32_t a_bits = load_bits(p.a, p.ab_dtype == QA_BF16, b * p.ab_sb + h);
   const uint32_t b_bits = load_bits(p.bb, p.ab_dtype == QA_BF16, b * p.ab_sb + h);
   float S[8][8];
-  load_state_128(s, threadIdx.x, S);
-  step_128<NORM>(p, b, h, s, S, a_bits, b_bits, base + qh * DK, base + p.Hqk * DK + qh * DK, base + 2 * p.Hqk * DK + h * DV, red, nrm,
-                 threadIdx.x);
+  load_state_cols(s, threadIdx.x, S);
+  step_cols<NORM>(p, b, h, s, S, a_bits, b_bits, base + qh * DK, base + p.Hqk * DK + qh * DK, base + 2 * p.Hqk * DK + h * DV, nrm,
+                  threadIdx.x);
 }
 
 // The conv update of the token feeding the fused step (src/reference_ops.py:245-258 for one
@@ -531,8 +716,7 @@ __global__ __launch_bounds__(256 * R) void delta_step_conv_128(DeltaParams p, Co
   // channels per thread: 384 over 256 threads (R = 1), one for R = 2 and 4
   constexpr int ITER = (NCH + 256 * R - 1) / (256 * R);
   __shared__ float act[NCH];
-  __shared__ float red[R][2][4][DV];
-  __shared__ float nrm[R][2][4];
+  __shared__ float nrm[R][4];
   const int64_t b = blockIdx.x / p.Hqk;
   const int qh = blockIdx.x - static_cast<int>(b) * p.Hqk;
   const int g = threadIdx.x >> 8;
@@ -569,7 +753,7 @@ __global__ __launch_bounds__(256 * R) void delta_step_conv_128(DeltaParams p, Co
   const uint32_t a_bits = load_bits(p.a, p.ab_dtype == QA_BF16, b * p.ab_sb + h);
   const uint32_t b_bits = load_bits(p.bb, p.ab_dtype == QA_BF16, b * p.ab_sb + h);
   float S[8][8];
-  load_state_128(s, tid, S);
+  load_state_cols(s, tid, S);
 #pragma unroll
   for (int it = 0; it < ITER; ++it) {
     const int c = threadIdx.x + it * 256 * R;
@@ -589,7 +773,7 @@ __global__ __launch_bounds__(256 * R) void delta_step_conv_128(DeltaParams p, Co
     }
   }
   __syncthreads();
-  step_128<NORM>(p, b, h, s, S, a_bits, b_bits, act, act + DK, act + 2 * DK + g * DV, red[g], nrm[g], tid);
+  step_cols<NORM>(p, b, h, s, S, a_bits, b_bits, act, act + DK, act + 2 * DK + g * DV, nrm[g], tid);
 }
 
 static bool aligned16(const void* ptr) { return (reinterpret_cast<uintptr_t>(ptr) & 15u) == 0; }
