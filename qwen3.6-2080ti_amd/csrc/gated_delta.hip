@@ -316,35 +316,13 @@ __device__ __forceinline__ void step_zero_outputs(const DeltaParams& p, int64_t 
   }
 }
 
-// The output stage's z and norm weight for the 8 outputs a lane of wave 0 holds (columns 8 (tid % 16)
-// .. + 7), as raw bits: one 16-byte vector for bf16, two for fp32, all issued before any is used
-// (element loads through the dtype branch each waited for the one before).
+// The output stage's z and norm weight for the 8 outputs a lane holds, as raw bits: one 16-byte
+// vector for bf16, two for fp32, all issued before any is used (element loads through the dtype
+// branch each waited for the one before).
 struct NormIn {
   uint4 z[2];
   uint4 w[2];
 };
-
-template <bool NORM>
-__device__ __forceinline__ void load_norm_in(const DeltaParams& p, int64_t b, int h, int tid, NormIn& n) {
-  if constexpr (NORM) {
-    if (p.norm_vec && tid < 64) {
-      const int col0 = 8 * (tid & 15);
-      const int64_t zi = b * p.z_sb + static_cast<int64_t>(h) * 128 + col0;
-      if (p.z_dtype == QA_BF16) {
-        n.z[0] = *reinterpret_cast<const uint4*>(reinterpret_cast<const bf16_t*>(p.z) + zi);
-      } else {
-        n.z[0] = *reinterpret_cast<const uint4*>(reinterpret_cast<const float*>(p.z) + zi);
-        n.z[1] = *reinterpret_cast<const uint4*>(reinterpret_cast<const float*>(p.z) + zi + 4);
-      }
-      if (p.norm_dtype == QA_BF16) {
-        n.w[0] = *reinterpret_cast<const uint4*>(reinterpret_cast<const bf16_t*>(p.norm_w) + col0);
-      } else {
-        n.w[0] = *reinterpret_cast<const uint4*>(reinterpret_cast<const float*>(p.norm_w) + col0);
-        n.w[1] = *reinterpret_cast<const uint4*>(reinterpret_cast<const float*>(p.norm_w) + col0 + 4);
-      }
-    }
-  }
-}
 
 // element c (0..7) of a NormIn vector pair
 __device__ __forceinline__ float norm_elem(const uint4 (&v)[2], bool bf16, int c) {
@@ -356,130 +334,6 @@ __device__ __forceinline__ float norm_elem(const uint4 (&v)[2], bool bf16, int c
   const uint4 u = v[c >> 2];
   const uint32_t word = (c & 3) == 0 ? u.x : (c & 3) == 1 ? u.y : (c & 3) == 2 ? u.z : u.w;
   return __uint_as_float(word);
-}
-
-// Thread tid of a head's 256 holds the 8 x 8 block of the head's state at rows 32 w + 8 rg, columns
-// 8 cg (w = tid / 64, rg = lane / 16, cg = lane % 16).
-__device__ __forceinline__ void load_state_128(const float* s, int tid, float (&S)[8][8]) {
-  constexpr int DV = 128;
-  const int lane = tid & 63;
-  const int row0 = 32 * (tid >> 6) + 8 * (lane >> 4);
-  const int col0 = 8 * (lane & 15);
-#pragma unroll
-  for (int r = 0; r < 8; ++r) {
-    const float4 lo = *reinterpret_cast<const float4*>(s + (row0 + r) * DV + col0);
-    const float4 hi = *reinterpret_cast<const float4*>(s + (row0 + r) * DV + col0 + 4);
-    S[r][0] = lo.x; S[r][1] = lo.y; S[r][2] = lo.z; S[r][3] = lo.w;
-    S[r][4] = hi.x; S[r][5] = hi.y; S[r][6] = hi.z; S[r][7] = hi.w;
-  }
-}
-
-// One fused decode step of value head h of row b on 256 threads (tid = 0..255) from its state
-// block S (load_state_128 of s): qv / kvv are the post-conv q and k rows of its key head and vv
-// its v row (global memory or LDS), s its state (written back in place).  l2_norm of q and k
-// (src/reference_ops.py:181-183, q * dk^-0.5 :304), the gating (:271-275), one recurrence step,
-// and with NORM the layer's output stage on the fp32 core.
-template <bool NORM>
-__device__ __forceinline__ void step_128(const DeltaParams& p, int64_t b, int h, float* s, float (&S)[8][8], uint32_t a_bits, uint32_t b_bits,
-                                         const float* qv, const float* kvv, const float* vv, float (&red)[2][4][128], float (&nrm)[2][4],
-                                         int tid) {
-  constexpr int DK = 128, DV = 128;
-  const int w = tid >> 6;
-  const int lane = tid & 63;
-  const int rg = lane >> 4;
-  const int cg = lane & 15;
-  const int row0 = 32 * w + 8 * rg;
-  const int col0 = 8 * cg;
-  float kr[8], qr[8], vc[8];
-  float sq = 0.f, sk = 0.f;
-#pragma unroll
-  for (int r = 0; r < 8; ++r) {
-    qr[r] = qv[row0 + r];
-    kr[r] = kvv[row0 + r];
-    sq += qr[r] * qr[r];
-    sk += kr[r] * kr[r];
-  }
-#pragma unroll
-  for (int c = 0; c < 8; ++c) vc[c] = vv[col0 + c];
-  // sum over the 4 row groups of this wave (lanes xor 16, 32), then the 4 waves
-  sq += __shfl_xor(sq, 16, 64);
-  sq += __shfl_xor(sq, 32, 64);
-  sk += __shfl_xor(sk, 16, 64);
-  sk += __shfl_xor(sk, 32, 64);
-  if (lane == 0) {
-    nrm[0][w] = sq;
-    nrm[1][w] = sk;
-  }
-  __syncthreads();
-  sq = (nrm[0][0] + nrm[0][1]) + (nrm[0][2] + nrm[0][3]);
-  sk = (nrm[1][0] + nrm[1][1]) + (nrm[1][2] + nrm[1][3]);
-  const float rq = rsqrtf(sq + 1e-6f) * rsqrtf(static_cast<float>(DK));
-  const float rk = rsqrtf(sk + 1e-6f);
-#pragma unroll
-  for (int r = 0; r < 8; ++r) {
-    qr[r] *= rq;
-    kr[r] *= rk;
-  }
-  const float av = bits_to_f32(a_bits, p.ab_dtype == QA_BF16);
-  const float bv = bits_to_f32(b_bits, p.ab_dtype == QA_BF16);
-  const float gval = -__expf(p.a_log[h]) * softplus_ref(av + p.dt_bias[h]);
-  const float decay = __expf(gval);
-  const float beta = sigmoid_ref(bv);
-  float o[8];
-  recurrence_token_128(S, kr, qr, vc, decay, beta, red, w, rg, cg, o);
-  if (w == 0 && rg == 0) {
-    // lanes 0-15 of wave 0 (one DPP row) hold the head's 128 outputs, 8 each
-    if (NORM) {
-      NormIn nin;
-      load_norm_in<NORM>(p, b, h, tid, nin);  // in flight while the sum of squares is taken
-      // the layer's output stage on the fp32 core (src/reference_ops.py:172-178,284-287: the
-      // core reaches gated_rms_norm in fp32, so its cast of the normalised value is the
-      // identity): (w * o / sqrt(mean(o^2) + eps)) * silu(z)
-      float ss = 0.f;
-#pragma unroll
-      for (int c = 0; c < 8; ++c) ss += o[c] * o[c];
-      ss = row16_sum(ss);
-      const float r = 1.0f / sqrtf(ss / static_cast<float>(DV) + p.norm_eps);
-      if (p.norm_vec) {
-#pragma unroll
-        for (int c = 0; c < 8; ++c) {
-          const float zv = norm_elem(nin.z, p.z_dtype == QA_BF16, c);
-          const float wv = norm_elem(nin.w, p.norm_dtype == QA_BF16, c);
-          o[c] = (wv * (o[c] * r)) * __fdividef(zv, 1.0f + __expf(-zv));
-        }
-      } else {
-#pragma unroll
-        for (int c = 0; c < 8; ++c) {
-          const float zv = load_any(p.z, p.z_dtype, b * p.z_sb + static_cast<int64_t>(h) * DV + col0 + c);
-          const float wv = load_any(p.norm_w, p.norm_dtype, col0 + c);
-          o[c] = (wv * (o[c] * r)) * __fdividef(zv, 1.0f + __expf(-zv));
-        }
-      }
-    }
-    const int64_t oi = b * p.out_sb + static_cast<int64_t>(h) * DV + col0;
-    if (p.out_vec) {
-      if (p.out_dtype == QA_BF16) {
-        uint4 u;
-        u.x = static_cast<uint32_t>(f32_to_bf16(o[0])) | (static_cast<uint32_t>(f32_to_bf16(o[1])) << 16);
-        u.y = static_cast<uint32_t>(f32_to_bf16(o[2])) | (static_cast<uint32_t>(f32_to_bf16(o[3])) << 16);
-        u.z = static_cast<uint32_t>(f32_to_bf16(o[4])) | (static_cast<uint32_t>(f32_to_bf16(o[5])) << 16);
-        u.w = static_cast<uint32_t>(f32_to_bf16(o[6])) | (static_cast<uint32_t>(f32_to_bf16(o[7])) << 16);
-        *reinterpret_cast<uint4*>(reinterpret_cast<bf16_t*>(p.out) + oi) = u;
-      } else {
-        float* op = reinterpret_cast<float*>(p.out) + oi;
-        *reinterpret_cast<float4*>(op) = make_float4(o[0], o[1], o[2], o[3]);
-        *reinterpret_cast<float4*>(op + 4) = make_float4(o[4], o[5], o[6], o[7]);
-      }
-    } else {
-#pragma unroll
-      for (int c = 0; c < 8; ++c) store_any(p.out, p.out_dtype, oi + c, o[c]);
-    }
-  }
-#pragma unroll
-  for (int r = 0; r < 8; ++r) {
-    *reinterpret_cast<float4*>(s + (row0 + r) * DV + col0) = make_float4(S[r][0], S[r][1], S[r][2], S[r][3]);
-    *reinterpret_cast<float4*>(s + (row0 + r) * DV + col0 + 4) = make_float4(S[r][4], S[r][5], S[r][6], S[r][7]);
-  }
 }
 
 // ---------------------------------------------------------------------------
@@ -538,8 +392,11 @@ __device__ __forceinline__ void load_norm_in_cols(const DeltaParams& p, int64_t 
   }
 }
 
-// step_128 on the column layout (load_state_cols of s): the same arithmetic per element, l2 norms,
-// gating, one recurrence step, with NORM the output stage; nrm holds the four waves' partial sums
+// One fused decode step of value head h of row b on 256 threads (tid = 0..255) from its state
+// block S (load_state_cols of s): qv / kvv are the post-conv q and k rows of its key head and vv its
+// v row (global memory or LDS), s its state (written back in place).  l2_norm of q and k
+// (src/reference_ops.py:181-183, q * dk^-0.5 :304), the gating (:271-275), one recurrence step,
+// and with NORM the layer's output stage on the fp32 core; nrm holds the four waves' partial sums
 // of squares of the outputs.
 template <bool NORM>
 __device__ __forceinline__ void step_cols(const DeltaParams& p, int64_t b, int h, float* s, float (&S)[8][8], uint32_t a_bits, uint32_t b_bits,
@@ -708,7 +565,7 @@ struct ConvStep {
 // threads, one per value head of the key head.  The workgroup first convolves the channels it
 // owns (the key head's q and k rows and its value heads' v rows; every channel belongs to one
 // workgroup, so each conv state entry has one reader and one writer) into LDS, then each group
-// runs step_128 from there.  The conv arithmetic is conv1d_kernel's, so the activations are the
+// runs step_cols from there.  The conv arithmetic is conv1d_kernel's, so the activations are the
 // same values qa_causal_conv1d_update produces.
 template <bool NORM, int R>
 __global__ __launch_bounds__(256 * R) void delta_step_conv_128(DeltaParams p, ConvStep cs) {
