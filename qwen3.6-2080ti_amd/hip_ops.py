@@ -687,6 +687,8 @@ def gated_delta_step(
     _require(state.dtype == torch.float32 and state.dim() == 4 and state.is_contiguous(), "state must be contiguous (slots, Hv, dk, dv) float32")
     _, value_heads, key_dim, value_dim = state.shape
     batch = qkv.shape[0]
+    _require_cuda(a, "a", device)
+    _require_cuda(b, "b", device)
     _require(a.shape == (batch, value_heads) and b.shape == (batch, value_heads), "a/b must be (batch, value_heads)")
     _require(a.dtype == b.dtype and a.dtype in (torch.float32, torch.bfloat16), "a/b must share a float32/bfloat16 dtype")
     a_c, b_c = a.contiguous(), b.contiguous()
@@ -764,6 +766,8 @@ def gated_delta_step_conv(
     _require(conv_state.shape[0] == state.shape[0], "conv_state and state must have the same rows")
     _, value_heads, key_dim, value_dim = state.shape
     _require(channels == 2 * int(key_heads) * key_dim + value_heads * value_dim, "x must hold the q, k and v channels")
+    _require_cuda(a, "a", device)
+    _require_cuda(b, "b", device)
     _require(a.shape == (batch, value_heads) and b.shape == (batch, value_heads), "a/b must be (batch, value_heads)")
     _require(a.dtype == b.dtype and a.dtype in (torch.float32, torch.bfloat16), "a/b must share a float32/bfloat16 dtype")
     a_c, b_c = a.contiguous(), b.contiguous()
@@ -830,6 +834,8 @@ def chunk_gated_delta_rule(
     batch, seq, channels = mixed_qkv.shape
     dk = dv = 128
     _require(channels == 2 * key_heads * dk + value_heads * dv, "mixed_qkv channels must be 2*key_heads*128 + value_heads*128")
+    _require_cuda(a, "a", device)
+    _require_cuda(b, "b", device)
     _require(a.shape == (batch, seq, value_heads) and b.shape == a.shape, "a/b must be (batch, seq, value_heads)")
     _require(a.dtype == b.dtype and a.dtype in (torch.float32, torch.bfloat16), "a/b must share a float32/bfloat16 dtype")
     _require(a.stride() == b.stride() and a.stride(-1) == 1, "a/b must share strides with contiguous heads")

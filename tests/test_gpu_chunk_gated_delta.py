@@ -78,10 +78,9 @@ def test_chunked_prefill_weak_decay_long_memory_state_precision() -> None:
 
 
 def test_chunked_prefill_strong_and_mixed_decay_matches_oracle() -> None:
-    # The chunk kernel forms the in-chunk decays exp(G_i - G_l) from one exponential per row
-    # when every 16-token block of a chunk decays by at most e^60, and from one per element
-    # otherwise.  Heads with A_log up to ~+4 (g down to ~-50 per token) and a run of tokens with
-    # large a put chunks of both kinds into one sequence and one launch.
+    # Heads with A_log up to ~+4 (g down to ~-50 per token, so in-chunk decays exp(G_i - G_l)
+    # span far beyond the fp32 range of exp(-G_l) alone) beside weakly decaying heads, and a run
+    # of tokens with large a inside otherwise moderate chunks, in one sequence and one launch.
     mixed, a, b, a_log, dt_bias, w = _inputs(45, 2, 300, SHAPE, a_log_scale=2.0)
     a[:, 100:140] += 8.0
     a_log[0] = 3.5
@@ -129,3 +128,15 @@ def test_chunked_prefill_matches_recurrent_core_kernel() -> None:
     rec_out, rec_state = hip_ops.linear_attention_recurrent_core(*(x.to(DEV) for x in (pq, pk, pv, pg, pb, ps)))
     assert _rel(out.transpose(1, 2), rec_out) < 2e-3
     assert _rel(state, rec_state) < 1e-3
+
+
+def test_gate_inputs_on_the_host_are_rejected() -> None:
+    import hip_ops
+
+    mixed, a, b, a_log, dt_bias, w = _inputs(46, 1, 64, SHAPE)
+    with pytest.raises(RuntimeError, match="a must be CUDA"):
+        hip_ops.chunk_gated_delta_rule(mixed.to(DEV), a, b.to(DEV), a_log.to(DEV), dt_bias.to(DEV), w.to(DEV),
+                                       key_heads=SHAPE.key_heads, value_heads=SHAPE.value_heads)
+    with pytest.raises(RuntimeError, match="b must be CUDA"):
+        hip_ops.chunk_gated_delta_rule(mixed.to(DEV), a.to(DEV), b, a_log.to(DEV), dt_bias.to(DEV), w.to(DEV),
+                                       key_heads=SHAPE.key_heads, value_heads=SHAPE.value_heads)

@@ -310,3 +310,23 @@ def test_conv_fused_step_other_conv_kernels_and_strided_rows(conv_kernel) -> Non
     out = ops.gated_delta_step_conv(x, c_fused, w.to(DEV), av, bv, a_log.to(DEV), dt_bias.to(DEV), s_fused, key_heads=2, slots=slots)
     assert torch.equal(out, ref)
     assert torch.equal(s_fused, s_ref) and torch.equal(c_fused, c_ref)
+
+
+def test_gate_inputs_on_the_host_are_rejected() -> None:
+    """a / b given as host tensors raise the wrappers' error instead of reaching a kernel."""
+    ops = _ops()
+    shape = gd.LinearShape(key_heads=2, value_heads=4, key_head_dim=128, value_head_dim=128, conv_kernel_dim=4)
+    batch = 2
+    mixed, a, b, a_log, dt_bias, w = _layer_inputs(80, batch, 1, shape)
+    x = mixed[:, 0].contiguous().to(DEV)
+    state = torch.zeros(batch, 4, 128, 128, device=DEV)
+    conv = torch.zeros(batch, shape.qkv_dim, 3, device=DEV)
+    act = ops.causal_conv1d_update(x, conv.clone(), w.to(DEV))
+    a_host, b_dev = a[:, 0].contiguous(), b[:, 0].contiguous().to(DEV)
+    with pytest.raises(RuntimeError, match="a must be CUDA"):
+        ops.gated_delta_step(act, a_host, b_dev, a_log.to(DEV), dt_bias.to(DEV), state, key_heads=2)
+    with pytest.raises(RuntimeError, match="a must be CUDA"):
+        ops.gated_delta_step_conv(x, conv, w.to(DEV), a_host, b_dev, a_log.to(DEV), dt_bias.to(DEV), state, key_heads=2)
+    with pytest.raises(RuntimeError, match="b must be CUDA"):
+        ops.gated_delta_step(act, a_host.to(DEV), b[:, 0].contiguous(), a_log.to(DEV), dt_bias.to(DEV), state, key_heads=2)
+    assert torch.count_nonzero(state) == 0 and torch.count_nonzero(conv) == 0
