@@ -534,7 +534,7 @@ __global__ __launch_bounds__(256, QA_DECODE_WAVES_PER_SIMD) void decode_partial_
 // kCombinePrefetch partial rows are loaded before the weights are known so
 // their latency overlaps the reductions.  Rows without a visible tile get 0
 // (their row-group record is stale and not read).
-constexpr int kCombinePrefetch = 8;
+constexpr int kCombinePrefetch = 32;
 constexpr int kCombineWaves = 4;
 
 template <typename QT, int D>
