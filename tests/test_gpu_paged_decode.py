@@ -225,10 +225,11 @@ def test_gqa_pool_equals_repeated_reference_layout() -> None:
     torch.testing.assert_close(out_ref_layout, out_shared, atol=1e-5, rtol=1e-5)
 
 
-@pytest.mark.parametrize("ctx", [4000, 140_000])
+@pytest.mark.parametrize("ctx", [3700, 4000, 4200, 140_000])
 def test_long_context_split_merge(ctx) -> None:
-    """Long contexts split over many partial launches: 4000 tokens use a few splits, 140000 use hundreds,
-    all merged by the combine kernel; a repeated call must give the same result."""
+    """Long contexts split over many waves of the balanced schedule: 3700, 4000 and 4200 tokens give
+    30, 32 and 34 partials per row group (under, at and over the 32 rows the combine loads before its
+    merge weights), 140000 give hundreds; a repeated call must give the same result."""
     ops = _ops()
     gen = torch.Generator().manual_seed(13)
     heads, kv_heads, dim, bs = 16, 2, 256, 16
