@@ -302,29 +302,42 @@ def cpu_baseline_decode(w, budget_s: float = 12.0):
     }
 
 
+def config1_inputs() -> dict:
+    """BASELINE config 1's inputs, drawn once for every user (``cpu_baseline_config1`` and the GPU
+    parity test ``tests/test_gpu_paged_decode.py``): batch 4, 16 q heads, 2 KV heads, D 256, 512
+    cached tokens per row, block size 16, bf16 N(0, 1) Q/K/V, one ``torch.Generator`` seeded 0
+    drawing the block permutation, then q, then the K and V pools.  The pool holds 128 physical
+    blocks ``(128, H_kv, bs, D)``; row ``b``'s table is blocks ``perm[32 b : 32 b + 32]``."""
+    import torch
+
+    batch, heads, kv_heads, dim, ctx, bs, blocks = 4, 16, 2, 256, 512, 16, 128
+    gen = torch.Generator().manual_seed(0)
+    perm = torch.randperm(blocks, generator=gen)
+    q = torch.randn((batch, heads, 1, dim), generator=gen).to(torch.bfloat16)
+    key_pool = torch.randn((blocks, kv_heads, bs, dim), generator=gen).to(torch.bfloat16)
+    value_pool = torch.randn((blocks, kv_heads, bs, dim), generator=gen).to(torch.bfloat16)
+    return {"query": q, "key_pool": key_pool, "value_pool": value_pool, "tables": perm.reshape(batch, ctx // bs),
+            "lens": [ctx] * batch, "bs": bs, "heads": heads, "kv_heads": kv_heads, "dim": dim, "ctx": ctx, "batch": batch}
+
+
 def cpu_baseline_config1(device: str) -> dict:
-    """BASELINE config 1 in full on the host: batch 4, 16 q heads, 2 KV heads, D 256, 512 cached
-    tokens per row, block size 16, table = seeded permutation of 128 blocks (32 per row), bf16
-    N(0, 1) Q/K/V, seed 0 -- through the reference's CPU decode as the engine runs it (fp32,
-    repeated heads, ``index_select`` gather, dense softmax; ``oracle.attention.reference_layout_decode_cpu``).
+    """BASELINE config 1 in full on the host (``config1_inputs``: the GPU parity test's inputs)
+    through the reference's CPU decode as the engine runs it (fp32, repeated heads,
+    ``index_select`` gather, dense softmax; ``oracle.attention.reference_layout_decode_cpu``).
     Reports the algorithmic GB/s of the config-2 formula (bf16 K/V bytes)."""
     import torch
 
     from oracle import attention
 
-    batch, heads, kv_heads, dim, ctx, bs = 4, 16, 2, 256, 512, 16
-    gen = torch.Generator().manual_seed(0)
-    perm = torch.randperm(128, generator=gen)
-    tables = [perm[32 * b : 32 * (b + 1)].tolist() for b in range(batch)]
-    q = torch.randn((batch, heads, 1, dim), generator=gen).to(torch.bfloat16).float()
-    pools_k, pools_v = [], []
-    for b in range(batch):
-        # the reference's per-request pool (heads after _repeat_kv, P, bs, D) in fp32 (src/decode_state.py:37-44,
-        # src/tp_runtime.py:518-525)
-        k = torch.randn((kv_heads, 128, bs, dim), generator=gen).to(torch.bfloat16).float()
-        v = torch.randn((kv_heads, 128, bs, dim), generator=gen).to(torch.bfloat16).float()
-        pools_k.append(k.repeat_interleave(heads // kv_heads, dim=0).contiguous())
-        pools_v.append(v.repeat_interleave(heads // kv_heads, dim=0).contiguous())
+    c1 = config1_inputs()
+    batch, heads, kv_heads, dim, ctx, bs = c1["batch"], c1["heads"], c1["kv_heads"], c1["dim"], c1["ctx"], c1["bs"]
+    tables = c1["tables"].tolist()
+    q = c1["query"].float()
+    # each request's reference pool (heads after _repeat_kv, P, bs, D) in fp32 (src/decode_state.py:37-44,
+    # src/tp_runtime.py:518-525); every row's table indexes the one 128-block pool, so one tensor serves all rows
+    pool_k = c1["key_pool"].float().permute(1, 0, 2, 3).repeat_interleave(heads // kv_heads, dim=0).contiguous()
+    pool_v = c1["value_pool"].float().permute(1, 0, 2, 3).repeat_interleave(heads // kv_heads, dim=0).contiguous()
+    pools_k, pools_v = [pool_k] * batch, [pool_v] * batch
     attention.reference_layout_decode_cpu(q, pools_k, pools_v, tables, [ctx] * batch, block_size=bs)  # warm
     reps = 0
     t0 = time.perf_counter()

@@ -34,7 +34,7 @@ import contextlib
 from dataclasses import dataclass, field
 from typing import Any, Iterator, Sequence
 
-from decode_state import DeviceBatchPageTables, FullAttentionCache, LinearStatePool, batch_page_tables
+from decode_state import DeviceBatchPageTables, FullAttentionCache, LinearStatePool, PrefillStep, batch_page_tables
 
 # --------------------------------------------------------------------------- config
 
@@ -123,6 +123,11 @@ class PagedAttentionDispatchStats:
     fallback_cpu: int = 0
     fallback_per_request_pools: int = 0
     fallback_shape: int = 0
+    # multi-token steps served by the native chunked prefill (``full_attention_prefill_device``).
+    # The reference has no native prefill, so its ladder counts every such call in
+    # ``fallback_prefill_or_multitoken``; here they count as calls and native prefill hits only,
+    # which leaves the reference's fields meaning what they mean there.
+    native_prefill_hits: int = 0
 
     def snapshot(self) -> "PagedAttentionDispatchStats":
         return PagedAttentionDispatchStats(**vars(self))
@@ -317,25 +322,170 @@ def full_attention_decode_device(
     library's static scratch (``qa_paged_attention_decode_batched_noalloc``) instead of a
     workspace.  Nothing here reads back to the host or copies host to device.
     """
-    reason = paged_attention_fallback_reason(config, query, key_blocks, value_blocks, seq_len=int(query.shape[2]), batched=False)
+    reason = _device_pool_reason(config, query, key_blocks, value_blocks, tables)
     if reason != "no_kernel":
         record_native_paged_dispatch(runtime, reason, native=False)
         return None
-    import hip_loader
     import hip_ops
 
-    try:
-        with runtime.profile_scope("batch.full_attention.native_paged_device"):
-            tables.append(key, value, key_blocks, value_blocks)
-            decode = hip_ops.paged_attention_decode_batched_noalloc if no_alloc else hip_ops.paged_attention_decode_batched
-            heads = decode(query, tables.block_tables, key_blocks, value_blocks, tables.sequence_lengths, tables.block_size)
-    except hip_loader.NativeLibraryMissing:
-        raise
-    except RuntimeError:
-        record_native_paged_dispatch(runtime, "no_kernel", native=False)
-        return None
+    # Once the append has written this step's K/V into the pool the cache has advanced, so a
+    # later kernel error propagates: a dense fallback would attend over a cache that already
+    # holds the step (and under graph capture would record a step without attention).
+    with runtime.profile_scope("batch.full_attention.native_paged_device"):
+        tables.append(key, value, key_blocks, value_blocks)
+        decode = hip_ops.paged_attention_decode_batched_noalloc if no_alloc else hip_ops.paged_attention_decode_batched
+        heads = decode(query, tables.block_tables, key_blocks, value_blocks, tables.sequence_lengths, tables.block_size)
     record_native_paged_dispatch(runtime, reason, native=True)
     return heads if gate is None else _gate_heads(heads, gate)
+
+
+def _device_pool_reason(config: AttentionConfig, query: Any, key_blocks: Any, value_blocks: Any, tables: DeviceBatchPageTables) -> str:
+    """The dispatch ladder for a step on device page tables, checked before anything is written:
+    the reference's reasons (one token per row), then what the native kernels need of the pool
+    (a shared ``(P, H_kv, bs, D)`` bf16 pool with the tables' block size and block count)."""
+    reason = paged_attention_fallback_reason(config, query, key_blocks, value_blocks, seq_len=int(query.shape[2]), batched=False)
+    if reason != "no_kernel":
+        return reason
+    if key_blocks.dim() != 4 or tuple(value_blocks.shape) != tuple(key_blocks.shape):
+        return "shape"
+    if int(key_blocks.shape[2]) != tables.block_size or int(key_blocks.shape[0]) != tables.num_blocks:
+        return "shape"
+    return "no_kernel"
+
+
+def _qk_norm_rope(q_proj: Any, k_proj: Any, v_proj: Any, q_norm_weight: Any, k_norm_weight: Any, key_blocks: Any, value_blocks: Any,
+                  block_tables: Any, cu_seqlens: Any, starts: Any, block_size: int, max_new: int, rope: "RopeConfig") -> tuple[Any, Any]:
+    import hip_ops
+
+    return hip_ops.qk_norm_rope_kv_append(
+        q_proj, k_proj, v_proj, q_norm_weight, k_norm_weight, key_blocks, value_blocks, block_tables, cu_seqlens, starts, block_size,
+        max_new=max_new, eps=rope.rms_norm_eps, rope_theta=rope.rope_theta, partial_rotary_factor=rope.partial_rotary_factor,
+    )
+
+
+@dataclass(frozen=True)
+class RopeConfig:
+    """The fields of ``RuntimeConfig`` the full-attention prologue reads (``src/runtime_config.py:55-90``;
+    ``rms_norm``, ``rotary_embeddings`` and ``apply_rotary_pos_emb`` of ``src/reference_ops.py:166-224``)."""
+
+    rms_norm_eps: float = 1e-6
+    rope_theta: float = 10_000_000.0
+    partial_rotary_factor: float = 0.25
+
+
+def full_attention_decode_step_device(
+    q_proj: Any, k_proj: Any, v_proj: Any, q_norm_weight: Any, k_norm_weight: Any, key_blocks: Any, value_blocks: Any,
+    tables: DeviceBatchPageTables, config: AttentionConfig, runtime: HotPathRuntime, rope: RopeConfig = RopeConfig(), *,
+    no_alloc: bool = False,
+) -> Any | None:
+    """One decode token of a full-attention layer for every row of a running batch, from the
+    projection outputs: ``tp_full_attention``'s norm/RoPE/append (``src/tp_runtime.py:511-525``)
+    and paged decode with the output gate (``:551-610``, ``:673-695``), at TP = 1.
+
+    ``q_proj`` ``(rows, H*2D)`` (query and gate halves of each head, as the projection writes
+    them), ``k_proj``/``v_proj`` ``(rows, H_kv*D)``, bf16; ``tables.reserve_step()`` has run for
+    the step.  One launch applies the q/k RMSNorm with the ``(1 + w)`` weights and the partial
+    rotary embedding at each row's position and writes k and v to the reserved slots of this
+    layer's shared pool; the batched decode follows, and the gate (read in place from
+    ``q_proj``) multiplies its output.  Returns ``(rows, 1, H*D)`` in bf16 (rows without a
+    request give zeros), or ``None`` -- counted by the reference's ladder -- when the caller must
+    run its dense path; that is decided before anything is written.
+    """
+    rows = int(q_proj.shape[0])
+    full = config.full_attention
+    heads, head_dim, kv_heads = full.num_heads, full.head_dim, full.num_key_value_heads
+    probe = q_proj.view(rows, heads, 1, 2 * head_dim)[..., :head_dim]
+    reason = _device_pool_reason(config, probe, key_blocks, value_blocks, tables)
+    if reason == "no_kernel" and (rows != tables.rows or int(key_blocks.shape[1]) != kv_heads or int(key_blocks.shape[3]) != head_dim
+                                  or str(key_blocks.dtype) != "torch.bfloat16" or str(q_proj.dtype) != "torch.bfloat16"):
+        reason = "shape"
+    if reason != "no_kernel":
+        record_native_paged_dispatch(runtime, reason, native=False)
+        return None
+    import hip_ops
+
+    cu = _row_offsets(rows, q_proj.device)
+    with runtime.profile_scope("batch.full_attention.native_paged_device"):
+        query, gate = _qk_norm_rope(q_proj, k_proj, v_proj, q_norm_weight, k_norm_weight, key_blocks, value_blocks, tables.block_tables,
+                                    cu, tables.positions, tables.block_size, 1, rope)
+        decode = hip_ops.paged_attention_decode_batched_noalloc if no_alloc else hip_ops.paged_attention_decode_batched
+        heads_out = decode(query.view(rows, heads, 1, head_dim), tables.block_tables, key_blocks, value_blocks, tables.sequence_lengths,
+                           tables.block_size)
+    record_native_paged_dispatch(runtime, reason, native=True)
+    if not full.output_gate:
+        return heads_out.view(rows, 1, heads * head_dim)
+    return _gate_heads(heads_out, gate.reshape(rows, 1, heads * head_dim))
+
+
+_ROW_OFFSETS: dict[tuple[int, str], Any] = {}
+
+
+def _row_offsets(rows: int, device: Any) -> Any:
+    """``cu_seqlens`` of one token per row, ``[0, 1, .., rows]`` int32, cached per (rows, device)
+    so a captured decode step reads a tensor that outlives the capture."""
+    import torch
+
+    key = (rows, str(device))
+    cached = _ROW_OFFSETS.get(key)
+    if cached is None:
+        cached = torch.arange(rows + 1, dtype=torch.int32, device=device)
+        _ROW_OFFSETS[key] = cached
+    return cached
+
+
+def full_attention_prefill_device(
+    q_proj: Any, k_proj: Any, v_proj: Any, q_norm_weight: Any, k_norm_weight: Any, key_blocks: Any, value_blocks: Any,
+    step: PrefillStep, config: AttentionConfig, runtime: HotPathRuntime, rope: RopeConfig = RopeConfig(),
+) -> Any | None:
+    """A multi-token step (a prompt or one chunk of it) of a full-attention layer, from the
+    projection outputs, on the native chunked prefill: ``tp_full_attention``
+    (``src/tp_runtime.py:499-548``) at TP = 1 with the step's K/V appended to the layer's shared
+    pool and causal attention over each row's cache and new tokens
+    (``_tp_full_attention_paged_or_dense``, ``:551-610``, whose native branch is decode-only: the
+    reference runs every prefill through the dense gather + masked softmax of ``:698-730``).
+
+    ``q_proj`` ``(tokens, H*2D)``, ``k_proj``/``v_proj`` ``(tokens, H_kv*D)`` bf16, packed in the
+    row order of ``step`` (``DeviceBatchPageTables.reserve_prefill``, run once per step for all
+    layers); new token ``n`` of a row sits at position ``starts[row] + n``.  One launch applies
+    the q/k RMSNorm and partial RoPE and writes k and v to the reserved slots; the prefill kernel
+    then attends over the row's prefix and its new tokens causally and applies the output gate,
+    read in place from ``q_proj``.  Returns ``(tokens, H*D)`` bf16.
+
+    Ladder: the reference's reasons first (``"disabled"``, ``"cpu"``, ``"shape"``), then what the
+    native kernels need -- a shared ``(P, H_kv, bs, D)`` bf16 pool of the tables' geometry.  A
+    call that does not qualify returns ``None`` and counts as ``"prefill_or_multitoken"`` (the
+    reference's reason for every multi-token call) or ``"shape"``, so the caller's dense path
+    runs; nothing has been written by then.  Native calls count in ``native_prefill_hits``.
+    """
+    import torch
+
+    tokens = int(q_proj.shape[0])
+    full = config.full_attention
+    heads, head_dim, kv_heads = full.num_heads, full.head_dim, full.num_key_value_heads
+    probe = q_proj.view(tokens, heads, 1, 2 * head_dim)[:1, :, :, :head_dim]
+    reason = paged_attention_fallback_reason(config, probe, key_blocks, value_blocks, seq_len=1, batched=False)
+    if reason == "no_kernel":
+        if key_blocks.dim() != 4:
+            reason = "prefill_or_multitoken"  # per-request (reference-layout) pools: the dense path
+        elif (tuple(value_blocks.shape) != tuple(key_blocks.shape) or int(key_blocks.shape[2]) != step.block_size
+              or int(key_blocks.shape[1]) != kv_heads or int(key_blocks.shape[3]) != head_dim or tokens != step.total_tokens
+              or key_blocks.dtype != torch.bfloat16 or q_proj.dtype != torch.bfloat16):
+            reason = "shape"
+    if reason != "no_kernel":
+        record_native_paged_dispatch(runtime, reason, native=False)
+        return None
+    import hip_ops
+
+    with runtime.profile_scope("full_attention.native_paged_prefill"):
+        query, gate = _qk_norm_rope(q_proj, k_proj, v_proj, q_norm_weight, k_norm_weight, key_blocks, value_blocks, step.block_tables,
+                                    step.cu_seqlens, step.starts, step.block_size, step.max_new, rope)
+        out = hip_ops.paged_attention_prefill(query, step.cu_seqlens, step.starts, key_blocks, value_blocks, step.block_tables,
+                                              step.block_size, max_new=step.max_new, gate=gate if full.output_gate else None)
+    stats = runtime.paged_attention_stats
+    stats.calls += 1
+    stats.eligible += 1
+    stats.native_prefill_hits += 1
+    return out.view(tokens, heads * head_dim)
 
 
 # --------------------------------------------------------------------------- linear attention
@@ -410,15 +560,30 @@ def linear_attention_decode_batch(
                                     out_dtype=odt, z=z, norm_weight=norm_weight, eps=eps)
 
 
-def linear_attention_prefill(mixed_qkv: Any, a: Any, b: Any, a_log: Any, dt_bias: Any, conv_weight: Any, config: AttentionConfig, *, conv_state: Any = None, initial_state: Any = None) -> tuple[Any, Any, Any]:
-    """Prefill of a linear-attention layer on the chunked kernel (``src/reference_ops.py:240-283``)."""
+def linear_attention_prefill(mixed_qkv: Any, a: Any, b: Any, a_log: Any, dt_bias: Any, conv_weight: Any, config: AttentionConfig, *,
+                             conv_state: Any = None, initial_state: Any = None, z: Any = None, norm_weight: Any = None,
+                             eps: float = 1e-6) -> tuple[Any, Any, Any]:
+    """Prefill of a linear-attention layer on the chunked kernel (``src/reference_ops.py:240-287``).
+
+    ``mixed_qkv`` ``(B, S, qkv_dim)`` bf16 and ``a``/``b`` ``(B, S, Hv)`` are the ``in_proj_*``
+    outputs.  Returns ``(core, final_state, conv_state)``: ``core`` ``(B, S, Hv, dv)`` bf16 is the
+    recurrence output, or, given ``z`` (the ``in_proj_z`` output ``(B, S, Hv*dv)``) and
+    ``norm_weight`` ``(dv,)``, the layer's output stage applied to it -- the gated RMSNorm with
+    SiLU(z) of ``src/reference_ops.py:284-287`` (``src/tp_runtime.py:853-857``) -- as
+    ``(B, S, Hv*dv)`` bf16, ready for ``out_proj``.
+    """
     import hip_ops
 
     lin = config.linear_attention
-    return hip_ops.chunk_gated_delta_rule(
+    if (z is None) != (norm_weight is None):
+        raise ValueError("linear_attention_prefill: z and norm_weight go together")
+    core, state, conv = hip_ops.chunk_gated_delta_rule(
         mixed_qkv, a, b, a_log, dt_bias, conv_weight, key_heads=lin.key_heads, value_heads=lin.value_heads, conv_state=conv_state,
         initial_state=initial_state,
     )
+    if z is None:
+        return core, state, conv
+    return hip_ops.gated_rms_norm(core, z, norm_weight, eps), state, conv
 
 
 # --------------------------------------------------------------------------- fp8 projections

@@ -6,18 +6,19 @@
 // (src/csrc/fp8_linear_cuda.cu:98-127, 1368-1466).
 //
 // The weight bytes are converted exactly (every E4M3 value is a bf16 and an
-// fp16 value) by v_cvt_pk_f32_fp8; the block scale multiplies each 128-deep
-// partial product in fp32, so the only roundings are those of x and of the fp32
-// sums.  x enters, like the reference's two regimes (fp32 matvec below 16 rows,
-// fp16 GEMM from 16 rows, src/csrc/fp8_linear_cuda.cu:1411-1460):
-//   * fp32 x, at most 16 rows: a bf16 hi + lo pair (x = hi + lo to 2^-17);
-//   * fp32 x, more rows: rounded to fp16, products on fp16 operands;
+// fp16 value) by v_cvt_scalef32_pk_{f16,bf16}_fp8 (two codes per instruction,
+// scale 1); the block scale multiplies each 128-deep partial product in fp32, so
+// the only roundings are those of x and of the fp32 sums.  x enters, like the
+// reference's two regimes (fp32 matvec below 16 rows, fp16 GEMM from 16 rows,
+// src/csrc/fp8_linear_cuda.cu:1411-1460):
+//   * fp32 x, fewer than 16 rows: a bf16 hi + lo pair (x = hi + lo to 2^-17);
+//   * fp32 x, 16 rows or more: rounded to fp16, products on fp16 operands;
 //   * bf16 x: as itself (exact).
 // Products run on v_mfma_f32_16x16x32_{bf16,f16} with the weight tile as the A
 // operand, so a lane's accumulator holds four consecutive outputs of one x row
 // (16-byte stores).
 //
-// Tiled path (at most 16 rows, or more than 256): a workgroup of 4 waves owns one
+// Tiled path (16 rows or fewer, or more than 256): a workgroup of 4 waves owns one
 // 128-row block of W (one scale row) for 16 * MS rows of x and a range of 128-deep
 // K blocks.  Per K block the x tile goes to LDS (double-buffered, one barrier per
 // block); each wave streams its 32 weight rows straight from global memory into

@@ -290,6 +290,9 @@ class DeviceBatchPageTables:
         self.block_tables = torch.full((rows, max_blocks), -1, dtype=torch.int32, device=device)
         self.sequence_lengths = torch.zeros(rows, dtype=torch.int32, device=device)
         self.positions = torch.zeros(rows, dtype=torch.int32, device=device)
+        # the append positions of an admission reserve: kept apart from `positions`, so a request
+        # admitted between a step's reserve and its per-layer appends leaves that step's positions
+        self._admit_positions = torch.zeros(rows, dtype=torch.int32, device=device)
         self.step_counts = torch.zeros(rows, dtype=torch.int32, device=device)
         self.active = [False] * rows
 
@@ -298,9 +301,12 @@ class DeviceBatchPageTables:
         return len(self.active)
 
     def add_request(self, prompt_tokens: int = 0) -> int:
-        """Take the lowest free row for a new request; reserve its prompt's blocks (positions of
-        the row then hold 0, the first append position).  The row joins later steps with one
-        token each."""
+        """Take the lowest free row for a new request and reserve blocks for ``prompt_tokens``
+        tokens (whose K/V the caller then writes at positions 0 ..).  The row joins later steps
+        with one token each.  ``positions`` (the append positions of the current step) is left
+        as it is, so a request may be admitted between a step's ``reserve_step`` and its
+        appends.  A prompt that is to run through :func:`attention_runtime.full_attention_prefill_device`
+        is admitted with ``prompt_tokens=0`` and reserved by :meth:`reserve_prefill` instead."""
         import torch
 
         if prompt_tokens < 0:
@@ -313,10 +319,49 @@ class DeviceBatchPageTables:
         if prompt_tokens:
             counts = torch.zeros_like(self.step_counts)
             counts[row] = prompt_tokens
-            self.allocator.reserve(self.block_tables, self.sequence_lengths, self.block_size, counts=counts, positions=self.positions)
+            self.allocator.reserve(self.block_tables, self.sequence_lengths, self.block_size, counts=counts, positions=self._admit_positions)
             self.allocator.check()
         self.step_counts[row] = 1
         return row
+
+    def reserve_prefill(self, rows: Sequence[int], counts: Sequence[int]) -> "PrefillStep":
+        """Reserve blocks for a multi-token step (a prompt, or one chunk of it) of some rows.
+
+        Row ``rows[i]`` grows by ``counts[i]`` tokens; the step's tokens are packed in that
+        order (row ``rows[i]`` owns ``cu_seqlens[i]:cu_seqlens[i + 1]``).  Like ``reserve_step``
+        it runs once for all full-attention layers sharing these tables, and the returned record
+        feeds each layer's :func:`attention_runtime.full_attention_prefill_device`.  Other rows
+        keep their lengths and the step positions of ``reserve_step``.  Reads the reservation
+        status back (one sync), so a failed reservation raises here rather than in a layer."""
+        import torch
+
+        rows = [int(r) for r in rows]
+        counts = [int(c) for c in counts]
+        if not rows or len(rows) != len(counts):
+            raise ValueError("reserve_prefill needs one count per row")
+        if len(set(rows)) != len(rows) or min(rows) < 0 or max(rows) >= self.rows:
+            raise ValueError("reserve_prefill rows must be distinct table rows")
+        if min(counts) <= 0:
+            raise ValueError("reserve_prefill counts must be positive")
+        for r in rows:
+            if not self.active[r]:
+                raise ValueError(f"row {r} holds no request")
+        device = self.block_tables.device
+        index = torch.tensor(rows, dtype=torch.int64, device=device)
+        full = torch.zeros_like(self.step_counts)
+        full[index] = torch.tensor(counts, dtype=torch.int32, device=device)
+        self.allocator.reserve(self.block_tables, self.sequence_lengths, self.block_size, counts=full, positions=self._admit_positions)
+        self.allocator.check()
+        cu = [0]
+        for c in counts:
+            cu.append(cu[-1] + c)
+        return PrefillStep(
+            rows=tuple(rows), counts=tuple(counts), index=index,
+            cu_seqlens=torch.tensor(cu, dtype=torch.int32, device=device),
+            starts=self._admit_positions.index_select(0, index),
+            block_tables=self.block_tables.index_select(0, index),
+            max_new=max(counts), total_tokens=cu[-1], block_size=self.block_size,
+        )
 
     def adopt_rows(self, block_tables: Any, lengths: Any) -> None:
         """Take over requests whose blocks are already written: row ``r`` gets ``block_tables[r]``
@@ -360,6 +405,24 @@ class DeviceBatchPageTables:
         self.step_counts[row] = 0
         self.active[row] = False
         return ids
+
+
+@dataclass(frozen=True)
+class PrefillStep:
+    """The reservation of one multi-token step (``DeviceBatchPageTables.reserve_prefill``):
+    rows in packing order, their new token counts, ``cu_seqlens`` ``(n + 1,)`` and the first
+    new position ``starts`` ``(n,)`` of each row (its length before the step), and the rows'
+    block tables ``(n, max_blocks)`` after the reservation, all int32 on the device."""
+
+    rows: tuple[int, ...]
+    counts: tuple[int, ...]
+    index: Any
+    cu_seqlens: Any
+    starts: Any
+    block_tables: Any
+    max_new: int
+    total_tokens: int
+    block_size: int
 
 
 # --------------------------------------------------------------------------- records

@@ -189,3 +189,64 @@ def test_device_page_tables_row_bookkeeping_and_cpu_dispatch_reason() -> None:
     kv = torch.zeros(3, 2, 1, 4)
     assert ar.full_attention_decode_device(q, None, kv, kv, pool.key_blocks, pool.value_blocks, tables, config, runtime) is None
     assert runtime.paged_attention_stats.fallback_cpu == 1 and runtime.paged_attention_stats.native_hits == 0
+
+
+def _tables_on_cpu(rows=3):
+    from decode_state import DeviceBatchPageTables, SharedKVBlockPool
+
+    pool = SharedKVBlockPool(8, kv_heads=2, head_dim=4, block_size=2)
+    return pool, DeviceBatchPageTables(pool, rows=rows, max_blocks=4)
+
+
+def _small_enabled(**overrides) -> ar.AttentionConfig:
+    text = {"linear_num_key_heads": 1, "linear_num_value_heads": 1, "linear_key_head_dim": 4, "linear_value_head_dim": 4,
+            "linear_conv_kernel_dim": 4, "num_attention_heads": 2, "num_key_value_heads": 2, "head_dim": 4, "attn_output_gate": True,
+            "native_paged_attention": True}
+    cfg = ar.parse_attention_config({"text_config": text})
+    return replace(cfg, full_attention=replace(cfg.full_attention, **overrides)) if overrides else cfg
+
+
+def test_native_prefill_counter_is_reported_and_starts_at_zero() -> None:
+    stats = ar.HotPathRuntime().paged_attention_stats
+    assert stats.to_dict()["native_prefill_hits"] == 0
+    assert stats.snapshot().native_prefill_hits == 0
+
+
+@pytest.mark.parametrize("overrides,counter", [({"native_paged_attention": False}, "fallback_disabled"), ({}, "fallback_cpu")])
+def test_prefill_and_decode_step_entries_follow_the_ladder_on_cpu(overrides, counter) -> None:
+    """The projection-output entries return None before writing anything when the reference's
+    ladder says no (disabled, CPU tensors), and count the fallback as the reference does."""
+    from decode_state import PrefillStep
+
+    pool, tables = _tables_on_cpu()
+    config = _small_enabled(**overrides)
+    runtime = ar.HotPathRuntime()
+    q_proj = torch.zeros(3, 2 * 2 * 4, dtype=torch.bfloat16)
+    kv = torch.zeros(3, 2 * 4, dtype=torch.bfloat16)
+    w = torch.zeros(4, dtype=torch.bfloat16)
+    step = PrefillStep(rows=(0,), counts=(3,), index=torch.tensor([0]), cu_seqlens=torch.tensor([0, 3], dtype=torch.int32),
+                       starts=torch.zeros(1, dtype=torch.int32), block_tables=torch.full((1, 4), -1, dtype=torch.int32), max_new=3,
+                       total_tokens=3, block_size=2)
+    assert ar.full_attention_prefill_device(q_proj, kv, kv, w, w, pool.key_blocks, pool.value_blocks, step, config, runtime) is None
+    assert ar.full_attention_decode_step_device(q_proj, kv, kv, w, w, pool.key_blocks, pool.value_blocks, tables, config, runtime) is None
+    stats = runtime.paged_attention_stats.to_dict()
+    assert stats[counter] == 2 and stats["dense_fallbacks"] == 2 and stats["native_prefill_hits"] == 0 and stats["native_hits"] == 0
+    assert torch.count_nonzero(pool.key_blocks) == 0
+
+
+def test_reserve_prefill_rejects_bad_steps_before_touching_the_device() -> None:
+    _pool, tables = _tables_on_cpu()
+    tables.add_request()
+    with pytest.raises(ValueError, match="one count per row"):
+        tables.reserve_prefill([0], [1, 2])
+    with pytest.raises(ValueError, match="distinct"):
+        tables.reserve_prefill([0, 0], [1, 2])
+    with pytest.raises(ValueError, match="positive"):
+        tables.reserve_prefill([0], [0])
+    with pytest.raises(ValueError, match="holds no request"):
+        tables.reserve_prefill([1], [4])
+
+
+def test_linear_prefill_needs_z_and_norm_weight_together() -> None:
+    with pytest.raises(ValueError, match="go together"):
+        ar.linear_attention_prefill(None, None, None, None, None, None, _small_enabled(), z=torch.zeros(1))

@@ -156,7 +156,7 @@ def test_device_page_tables_running_batch_two_layers_matches_oracle_and_replays_
         for layer, pool in enumerate(pools):
             k, v = tokens(layer, req)
             hip_ops.paged_kv_append(k[:, :, :prompt].to(DEV), v[:, :, :prompt].to(DEV), pool.key_blocks, pool.value_blocks,
-                                    tables.block_tables[row : row + 1], tables.positions[row : row + 1], bs)
+                                    tables.block_tables[row : row + 1], torch.zeros(1, dtype=torch.int32, device=DEV), bs)
 
     def step_inputs(layer):
         k_new = torch.zeros(tables.rows, kv_heads, 1, dim, dtype=torch.bfloat16)
@@ -233,3 +233,142 @@ def test_device_page_tables_running_batch_two_layers_matches_oracle_and_replays_
         for req in row_of:
             length[req] += 1
         check(graph_outs, q, gate, length)
+
+
+THETA, FACTOR, EPS = 10_000_000.0, 0.25, 1e-6
+
+
+def test_prefill_and_decode_from_projection_outputs_match_oracle() -> None:
+    """The full-attention layer from its projection outputs through the runtime: two chunked
+    prefill steps of a ragged batch (prefixes 0 and not block multiples, rows out of order, a row
+    left empty), then decode steps from projection outputs -- q/k RMSNorm (1 + w) + partial RoPE +
+    append in one launch, attention over the cache, the output gate read in place from q_proj --
+    each against the oracle's norm/rope and dense causal attention over the tokens written so far
+    (bf16 outputs, 2e-2).  GQA 16/2, D = 256, block size 16."""
+    from decode_state import DeviceBatchPageTables
+    from oracle import rope
+
+    gen = torch.Generator().manual_seed(65)
+    heads, kv_heads, dim, bs = 16, 2, 256, 16
+    config = _enabled(heads, kv_heads, dim)
+    rope_cfg = ar.RopeConfig(rms_norm_eps=EPS, rope_theta=THETA, partial_rotary_factor=FACTOR)
+    pool = SharedKVBlockPool(48, kv_heads, dim, block_size=bs, device=DEV)
+    tables = DeviceBatchPageTables(pool, rows=4, max_blocks=12)
+    runtime = ar.HotPathRuntime()
+    qw = (torch.randn(dim, generator=gen) * 0.1).to(torch.bfloat16)
+    kw = (torch.randn(dim, generator=gen) * 0.1).to(torch.bfloat16)
+    hist_k = {r: torch.zeros(0, kv_heads, dim, dtype=torch.bfloat16) for r in range(3)}
+    hist_v = {r: torch.zeros(0, kv_heads, dim, dtype=torch.bfloat16) for r in range(3)}
+    for _ in range(3):
+        tables.add_request(0)
+
+    def projections(tokens):
+        q_proj = torch.randn(tokens, heads * 2 * dim, generator=gen).to(torch.bfloat16)
+        k_proj = torch.randn(tokens, kv_heads * dim, generator=gen).to(torch.bfloat16)
+        v_proj = torch.randn(tokens, kv_heads * dim, generator=gen).to(torch.bfloat16)
+        return q_proj, k_proj, v_proj
+
+    def expected(q_proj, k_proj, v_proj, rows, counts):
+        """Per row: the oracle's q/k after norm and rope at the row's positions, the K/V history
+        extended by the step, and dense causal attention with the gate."""
+        outs, off = [], 0
+        q3 = q_proj.view(-1, heads, 2 * dim)
+        for row, n in zip(rows, counts):
+            prefix = hist_k[row].shape[0]
+            positions = torch.arange(prefix, prefix + n)
+            q, k = rope.qk_norm_rope(q3[off : off + n, :, :dim], k_proj[off : off + n].view(n, kv_heads, dim), qw, kw, positions,
+                                     eps=EPS, rope_theta=THETA, partial_rotary_factor=FACTOR)
+            hist_k[row] = torch.cat([hist_k[row], k])
+            hist_v[row] = torch.cat([hist_v[row], v_proj[off : off + n].view(n, kv_heads, dim)])
+            gate = q3[off : off + n, :, dim:].reshape(1, n, heads * dim)
+            ref = oracle_attn.dense_attention(q.transpose(0, 1).unsqueeze(0), hist_k[row].transpose(0, 1).unsqueeze(0),
+                                              hist_v[row].transpose(0, 1).unsqueeze(0), position_offset=prefix, gate=gate)
+            outs.append(ref[0].transpose(0, 1).reshape(n, heads * dim))
+            off += n
+        return torch.cat(outs)
+
+    for rows, counts in (([0, 1, 2], [37, 5, 80]), ([2, 0], [19, 16])):
+        step = tables.reserve_prefill(rows, counts)
+        assert step.starts.cpu().tolist() == [hist_k[r].shape[0] for r in rows]
+        q_proj, k_proj, v_proj = projections(sum(counts))
+        out = ar.full_attention_prefill_device(q_proj.to(DEV), k_proj.to(DEV), v_proj.to(DEV), qw.to(DEV), kw.to(DEV), pool.key_blocks,
+                                               pool.value_blocks, step, config, runtime, rope_cfg)
+        assert out is not None and out.shape == (sum(counts), heads * dim)
+        ref = expected(q_proj, k_proj, v_proj, rows, counts)
+        torch.testing.assert_close(out.cpu().float(), ref.float(), atol=2e-2, rtol=2e-2)
+    assert tables.sequence_lengths.cpu().tolist() == [53, 5, 99, 0]
+    for _ in range(2):
+        tables.reserve_step()
+        q_proj, k_proj, v_proj = projections(tables.rows)
+        out = ar.full_attention_decode_step_device(q_proj.to(DEV), k_proj.to(DEV), v_proj.to(DEV), qw.to(DEV), kw.to(DEV), pool.key_blocks,
+                                                   pool.value_blocks, tables, config, runtime, rope_cfg)
+        tables.check()
+        assert out is not None and out.shape == (tables.rows, 1, heads * dim)
+        ref = expected(q_proj[:3], k_proj[:3], v_proj[:3], [0, 1, 2], [1, 1, 1])
+        torch.testing.assert_close(out[:3, 0].cpu().float(), ref.float(), atol=2e-2, rtol=2e-2)
+        assert torch.count_nonzero(out[3]) == 0  # the row without a request
+    stats = runtime.paged_attention_stats
+    assert (stats.native_prefill_hits, stats.native_hits, stats.dense_fallbacks, stats.calls) == (2, 2, 0, 4)
+
+
+def test_prefill_on_reference_layout_pools_keeps_the_dense_path() -> None:
+    """The native prefill needs the shared GQA pool: a per-request (reference-layout) pool is
+    counted as the reference's ``prefill_or_multitoken`` and nothing is written."""
+    from decode_state import DeviceBatchPageTables
+
+    heads, kv_heads, dim = 16, 2, 256
+    config = _enabled(heads, kv_heads, dim)
+    pool = SharedKVBlockPool(8, kv_heads, dim, block_size=16, device=DEV)
+    tables = DeviceBatchPageTables(pool, rows=1, max_blocks=4)
+    tables.add_request(0)
+    step = tables.reserve_prefill([0], [3])
+    ref_pool = torch.zeros(1, heads, 4, 16, dim, dtype=torch.bfloat16, device=DEV)
+    runtime = ar.HotPathRuntime()
+    q_proj = torch.randn(3, heads * 2 * dim, device=DEV).to(torch.bfloat16)
+    kv = torch.randn(3, kv_heads * dim, device=DEV).to(torch.bfloat16)
+    w = torch.zeros(dim, dtype=torch.bfloat16, device=DEV)
+    assert ar.full_attention_prefill_device(q_proj, kv, kv, w, w, ref_pool, ref_pool, step, config, runtime) is None
+    stats = runtime.paged_attention_stats
+    assert (stats.fallback_prefill_or_multitoken, stats.dense_fallbacks, stats.native_prefill_hits) == (1, 1, 0)
+    assert torch.count_nonzero(ref_pool) == 0
+
+
+def test_admission_between_reserve_and_append_keeps_step_positions() -> None:
+    from decode_state import DeviceBatchPageTables
+
+    pool = SharedKVBlockPool(16, 2, 256, block_size=16, device=DEV)
+    tables = DeviceBatchPageTables(pool, rows=3, max_blocks=4)
+    tables.add_request(20)
+    tables.reserve_step()
+    before = tables.positions.cpu().tolist()
+    tables.add_request(7)
+    assert tables.positions.cpu().tolist() == before
+    assert tables.sequence_lengths.cpu().tolist() == [21, 7, 0]
+
+
+def test_linear_prefill_with_output_stage_matches_oracle() -> None:
+    """``linear_attention_prefill`` with ``z`` and ``norm_weight`` applies the layer's gated
+    RMSNorm + SiLU(z) to the chunked core (bf16 output, 2e-2)."""
+    from oracle import gated_norm
+
+    config = _enabled()
+    lin = config.linear_attention
+    shape = gd.LinearShape(lin.key_heads, lin.value_heads, lin.key_head_dim, lin.value_head_dim, lin.conv_kernel_dim)
+    gen = torch.Generator().manual_seed(66)
+    batch, seq = 2, 150
+    mixed = torch.randn(batch, seq, shape.qkv_dim, generator=gen).to(torch.bfloat16)
+    a = torch.randn(batch, seq, shape.value_heads, generator=gen)
+    b = torch.randn(batch, seq, shape.value_heads, generator=gen)
+    a_log = torch.randn(shape.value_heads, generator=gen) * 0.3
+    dt_bias = torch.zeros(shape.value_heads)
+    w = torch.randn(shape.qkv_dim, 1, 4, generator=gen) * 0.5
+    z = torch.randn(batch, seq, shape.value_heads * 128, generator=gen).to(torch.bfloat16)
+    norm_w = (1.0 + 0.1 * torch.randn(128, generator=gen)).to(torch.bfloat16)
+    out, state, _ = ar.linear_attention_prefill(mixed.to(DEV), a.to(DEV), b.to(DEV), a_log.to(DEV), dt_bias.to(DEV), w.to(DEV), config,
+                                                z=z.to(DEV), norm_weight=norm_w.to(DEV), eps=EPS)
+    core, ref_state, _ = gd.linear_attention_core(mixed.float(), a, b, a_log, dt_bias, w, shape)
+    ref = gated_norm.linear_attention_output(core.to(torch.bfloat16), z, norm_w, EPS)
+    assert out.shape == (batch, seq, shape.value_heads * 128) and out.dtype == torch.bfloat16
+    torch.testing.assert_close(out.cpu().float(), ref.reshape(batch, seq, -1).float(), atol=2e-2, rtol=2e-2)
+    err = (state.cpu().double() - ref_state.double()).norm() / ref_state.double().norm()
+    assert float(err) < 1e-3

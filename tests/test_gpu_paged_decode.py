@@ -138,16 +138,11 @@ def test_batched_rejects_mismatched_pool_count() -> None:
 
 
 def _config1_inputs():
-    """seed 0, B=4, H=16, H_kv=2, D=256, ctx 512, bs 16, 128 shuffled blocks."""
-    torch.manual_seed(0)
-    batch, heads, kv_heads, dim, ctx, bs = 4, 16, 2, 256, 512, 16
-    blocks = 128
-    perm = torch.randperm(blocks)
-    tables = perm.reshape(batch, ctx // bs)
-    q = torch.randn(batch, heads, 1, dim).to(torch.bfloat16)
-    key_pool = torch.randn(blocks, kv_heads, bs, dim).to(torch.bfloat16)
-    value_pool = torch.randn(blocks, kv_heads, bs, dim).to(torch.bfloat16)
-    return q, key_pool, value_pool, tables, [ctx] * batch, bs
+    """BASELINE config 1 as the benchmark's CPU baseline draws it (``bench.config1_inputs``)."""
+    import bench
+
+    c1 = bench.config1_inputs()
+    return c1["query"], c1["key_pool"], c1["value_pool"], c1["tables"], c1["lens"], c1["bs"]
 
 
 def test_config1_bf16_shared_pool_matches_oracle() -> None:
@@ -226,13 +221,16 @@ def test_gqa_pool_equals_repeated_reference_layout() -> None:
 
 
 @pytest.mark.parametrize("ctx", [3700, 4000, 4200, 140_000])
-def test_long_context_split_merge(ctx) -> None:
+@pytest.mark.parametrize("heads,dim", [(16, 256), (8, 128)])
+def test_long_context_split_merge(ctx, heads, dim) -> None:
     """Long contexts split over many waves of the balanced schedule: 3700, 4000 and 4200 tokens give
     30, 32 and 34 partials per row group (under, at and over the 32 rows the combine loads before its
-    merge weights), 140000 give hundreds; a repeated call must give the same result."""
+    merge weights), 140000 give hundreds; a repeated call must give the same result.  Both head
+    dims: D = 256 (four columns per combine lane) and D = 128 (two per lane)."""
     ops = _ops()
     gen = torch.Generator().manual_seed(13)
-    heads, kv_heads, dim, bs = 16, 2, 256, 16
+    kv_heads, bs = 2, 16
+    print(f"long-context decode: ctx {ctx}, heads {heads}/{kv_heads}, D {dim}", flush=True)
     blocks = (ctx + bs - 1) // bs
     kp = torch.randn(blocks + 3, kv_heads, bs, dim, generator=gen).to(torch.bfloat16)
     vp = torch.randn(blocks + 3, kv_heads, bs, dim, generator=gen).to(torch.bfloat16)

@@ -84,3 +84,16 @@ def test_last_prefill_row_equals_decode_kernel() -> None:
         q[-1:].unsqueeze(2).to(DEV), table_t.to(DEV), kp.to(DEV), vp.to(DEV), torch.tensor([75], device=DEV), 16
     )
     torch.testing.assert_close(out[-1].float(), dec[0, :, 0].float(), atol=1e-2, rtol=1e-2)
+
+
+def test_prefill_past_the_lds_table_reads_the_table_from_global_memory() -> None:
+    """A row whose block table is longer than the 4,096 entries the kernel keeps in LDS (a
+    66,000-token prefix and 64 new tokens: 4,129 blocks) takes the kernel's global-memory table
+    path; a short row beside it keeps the LDS path.  Both against the oracle."""
+    prefixes, news = [66000, 10], [64, 17]
+    print("prefill: prefix 66000 + 64 new, prefix 10 + 17 new (GQA 16/2, D=256)", flush=True)
+    kp, vp, tables, table_t, q, gate = _setup(55, prefixes, news, heads=16, kv_heads=2, dim=256)
+    assert table_t.shape[1] > 4096
+    out = _run(q, [0, 64, 81], prefixes, kp, vp, table_t, max_new=64, gate=gate)
+    refs = oracle_attn.paged_prefill(q, kp, vp, tables, prefixes, news, block_size=16, gate=gate)
+    torch.testing.assert_close(out.cpu().float(), torch.cat(refs).float(), atol=2e-2, rtol=2e-2)
