@@ -24,24 +24,28 @@
 //     which equals the per-token recurrence of src/reference_ops.py:310-318
 //     (delta = U - W S0 of the WY form; T, W and U themselves are never formed).
 //
-// chunk_kernel mapping: one workgroup (8 waves) per (batch row, value head,
-// half of dv), the workgroups of one key head on one XCD; chunks run in order,
-// chunk c + 1 staged to LDS during phase 2 of chunk c (its v channels convolved
-// on the way, one token per lane).  The delta system is solved by blocked
-// forward substitution over 16-token blocks, delta_p = D_p (R_p - sum_{k<p}
-// A_pk delta_k) with D_p = (I + A_pp)^-1, on fp16 hi + lo operand pairs (mma3
-// below), which keeps the state within fp32-state tolerance.  Key waves 0..3
-// own a 16-column dv tile each: all of K and the fp32 state columns in
-// registers, R, the off-diagonal A blocks, the substitution chain and the state
-// update.  Query waves 4..7 own the same dv tiles for the output: the diagonal
-// inverses D_p, all of Q in registers, gamma * (Q S0), Aqk and the output.
-// Matrix products use v_mfma_f32_16x16x32_f16 (fp32 accumulation); the 16x16
-// accumulator layout equals the B-operand layout of the 16-deep product, so
-// delta feeds the next block and the state update from registers.  The next
-// chunk's tiles are loaded into registers while the current one is computed;
-// barriers order LDS only, so those loads stay in flight across them.
-// Operands that reduce over tokens are read from the token-major K and V tiles
-// with ds_read_b64_tr_b16.
+// chunk_kernel mapping: one workgroup per (batch row, value head, half of dv), the workgroups of
+// one key head on one XCD; chunks run in order.  Twelve waves (three per SIMD) in three roles,
+// each with its own chunk loop and the same two barriers per chunk, so the registers one role
+// holds are not reserved in the others:
+//  * key waves 0..3 own a 16-column dv tile each and run only work that depends on the state,
+//    chunk c in iteration c: K S0 and the output's S0^T Q^T from one fp16 copy of the fp32 state
+//    registers, R, the blocked forward substitution of the delta system over 16-token blocks,
+//    delta_p = D_p (R_p - sum_{k<p} A_pk delta_k), on fp16 hi + lo operand pairs (mma3 below,
+//    which keeps the state within fp32-state tolerance), the state update, and the output
+//    O^T = gamma (S0^T Q^T) + delta^T Aqk^T with its stores.  They write no LDS.
+//  * A waves 4..7 prepare chunk c + 1: each stages its own 16 k rows and gate scalars, then
+//    (from its own rows, no barrier) the diagonal block A_uu and D_u = (I + A_uu)^-1 as hi | lo
+//    operands; after the mid-chunk barrier, the off-diagonal A blocks (hi | lo) and eight of the
+//    64 v channels of chunk c + 1 (conv1d + SiLU).
+//  * V waves 8..11 stage chunk c + 1's q rows and convolve eight v channels each; after the
+//    mid-chunk barrier, its Aqk tiles.
+// Every buffer another role reads in the same phase is double-buffered by chunk parity.  Matrix
+// products use v_mfma_f32_16x16x32_f16 / 16x16x16 (fp32 accumulation); the 16x16 accumulator
+// layout equals the B-operand layout, so delta feeds the next block, the state update and the
+// output from registers.  The next chunk's tiles are loaded into registers one chunk ahead;
+// barriers order LDS only, so those loads stay in flight across them.  Operands that reduce over
+// tokens are read from the token-major K and V tiles with ds_read_b64_tr_b16.
 #include "qa_common.h"
 
 namespace qa {
@@ -60,8 +64,6 @@ constexpr int CH = 64;      // tokens per chunk
 constexpr int DK = 128;
 constexpr int DV = 128;
 constexpr int DVS = 64;     // dv columns per workgroup
-constexpr int NW = 8;       // waves per workgroup
-constexpr int NT = NW * 64;
 constexpr int KCONV = 4;
 constexpr int LD128 = 144;  // padded leading dims (halfs) of 128- and 64-wide fp16 tiles: strides of 8 (mod 16)
 constexpr int LD64 = 80;   // dwords measured to give the fewest LDS bank conflicts (136 / 72 had twice as many)
@@ -88,36 +90,11 @@ inline Workspace workspace_layout(int64_t batch, int64_t seq, int64_t hk, int64_
   return w;
 }
 
-// ---- LDS layout of chunk_kernel (bytes).  Phase 1 of chunk c reads Qs, Vs, Ks[c % 2] and
-// the scalars [c % 2]; the key waves write Ahl, the query waves Adg, Tb and Aqk[c % 2].
-// Phase 2: the key waves read Tb, Ahl and Ks[c % 2] and write Dt[c % 2] and St[(c + 1) % 2];
-// the query waves read Dt[(c - 1) % 2] and Aqk[(c - 1) % 2] (the output of chunk c - 1) and
-// St[c % 2].  Chunk c + 1 is staged at the start of phase 2: Qs and Vs are read in phase 1
-// only (the waves keep their operands in registers), so one copy of each suffices; Ks and
-// the scalars, still read in phase 2, take the other half of their double buffers.  No two
-// regions alias; the double buffers let phase 2 read one chunk's tiles while the other role
-// writes the next chunk's.
-constexpr int LDB = 20;                            // row stride (floats) of the 16x16 fp32 diagonal blocks
-constexpr int ST_BYTES = DVS * LD128 * 2;          // one St [dv][dk] (fp16 copy of the state)
-constexpr int AQK_BYTES = CH * LD64 * 2;           // one Aqk [i][l]
-constexpr int DT_BYTES = DVS * LD64 * 2;           // one delta^T [dv][tok]
-constexpr int KS_BYTES = CH * LD128 * 2;           // one Q or K tile
-constexpr int SC_BYTES = 4 * CH * 4;               // beta, G, gamma, exp(G_C - G) per token
-constexpr int OFF_QS = 0;                          // Qs [tok][dk]
-constexpr int OFF_KS = OFF_QS + KS_BYTES;          // Ks [tok][dk] x 2
-constexpr int OFF_VS = OFF_KS + 2 * KS_BYTES;      // Vs [tok][dv] (this workgroup's half)
-constexpr int OFF_ST = OFF_VS + CH * LD64 * 2;     // St x 2
-constexpr int OFF_AQK = OFF_ST + 2 * ST_BYTES;     // Aqk x 2
-constexpr int OFF_ADG = OFF_AQK + 2 * AQK_BYTES;   // diagonal 16x16 blocks of A, fp32 [block][row][LDB]
-constexpr int OFF_TB = OFF_ADG + 4 * 16 * LDB * 4; // D_p = (I + A_pp)^-1, fp32 [block][row][LDB]
-constexpr int OFF_AHL = OFF_TB + 4 * 16 * LDB * 4; // 6 off-diagonal blocks of A as fp16 hi | lo, one 16-byte A operand per lane
-constexpr int OFF_DT = OFF_AHL + 6 * 64 * 16;      // delta^T x 2
-constexpr int OFF_SC = OFF_DT + 2 * DT_BYTES;      // scalars x 2
-constexpr int LDS_BYTES = OFF_SC + 2 * SC_BYTES;
-
-static_assert(OFF_ADG % 16 == 0 && OFF_DT % 16 == 0 && OFF_SC % 16 == 0, "16-byte aligned regions");
-static_assert(LDS_BYTES <= 160 * 1024, "LDS budget");
-static_assert(KS_BYTES % 16 == 0 && SC_BYTES % 16 == 0, "16-byte aligned buffers");
+// ---- tile sizes of chunk_kernel (bytes; fp16 tiles in LDS with the padded leading dims above)
+constexpr int LDB = 20;                   // row stride (floats) of the 16x16 fp32 diagonal blocks
+constexpr int AQK_BYTES = CH * LD64 * 2;  // one Aqk [i][aqk_col(l)]
+constexpr int KS_BYTES = CH * LD128 * 2;  // one Q or K tile [tok][dk]
+static_assert(KS_BYTES % 16 == 0 && AQK_BYTES % 16 == 0, "16-byte aligned buffers");
 
 struct PrepParams {
   const bf16_t* x;
@@ -384,40 +361,6 @@ __device__ __forceinline__ void split4(const cfloat4& v, h4_v& hi, h4_v& lo) {
   lo = __builtin_bit_cast(h4_v, u32x2{l0, l1});
 }
 
-// One chunk's inputs, staged in registers while the previous chunk is computed:
-// 16-byte pieces of the fp16 q and k rows, the raw bf16 v of token (tid % 64) in this wave's
-// eight channels of the workgroup's v half, and (G, beta, exp(G), exp(G_C - G)) of token tid % 64
-// (used by wave 0).
-struct ChunkRegs {
-  u32x4 q0, q1, k0, k1, v;
-  cfloat4 gb;
-};
-
-template <bool VEC16>
-__device__ __forceinline__ ChunkRegs load_chunk(const ChunkParams& p, int64_t b, int j, int qh, int64_t vch, int64_t ci, int tid) {
-  ChunkRegs r;
-  const int64_t t0 = ci * CH;
-  // 1024 pieces of 16 bytes per q/k tile: thread tid takes pieces tid and tid + 512
-  const int64_t row_off = ((b * p.tp + t0 + (tid >> 4)) * p.Hk + qh) * DK + 8 * (tid & 15);
-  const int64_t row_off2 = row_off + static_cast<int64_t>(NT >> 4) * p.Hk * DK;
-  r.q0 = *reinterpret_cast<const u32x4*>(p.qn + row_off);
-  r.q1 = *reinterpret_cast<const u32x4*>(p.qn + row_off2);
-  r.k0 = *reinterpret_cast<const u32x4*>(p.kn + row_off);
-  r.k1 = *reinterpret_cast<const u32x4*>(p.kn + row_off2);
-  // tokens past the sequence read the last token instead (no branch); their v is masked to 0
-  // when staged and they only feed later masked tokens
-  const int64_t t = min64(t0 + (tid & 63), p.T - 1);
-  const bf16_t* src = p.x + b * p.x_sb + t * p.x_st + vch;
-  if constexpr (VEC16) {
-    r.v = *reinterpret_cast<const u32x4*>(src);
-  } else {
-#pragma unroll
-    for (int e = 0; e < 4; ++e) r.v[e] = reinterpret_cast<const uint32_t*>(src)[e];
-  }
-  r.gb = *reinterpret_cast<const cfloat4*>(p.gb + ((b * p.Hv + j) * p.tp + t0 + (tid & (CH - 1))) * 4);
-  return r;
-}
-
 // channel c of the raw bf16 pairs of a token (c even: low half)
 __device__ __forceinline__ float raw_chan(const u32x4& r, int c) {
   const uint32_t u = r[c >> 1];
@@ -523,53 +466,6 @@ __device__ __forceinline__ f16x8_v ktr_operand(const half_t* Ks, int row_g, int 
   return __builtin_bit_cast(f16x8_v, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
 }
 
-// Chunk ci from the registers it was loaded into to LDS: the q and k tiles (Ks and the scalars
-// into their ci % 2 copies), and this wave's eight v channels convolved (conv1d + SiLU,
-// src/reference_ops.py:245-258) with one token per lane -- the three earlier tokens of a lane
-// come from the lanes below it, for lanes 0..2 from `hist` (the raw inputs of the previous
-// chunk's last three tokens, or the initial conv state), which is then advanced.  Tokens past
-// the sequence get zero v.
-__device__ __forceinline__ void stage_chunk(const ChunkParams& p, unsigned char* smem, const ChunkRegs& nx, int64_t ci, int tid, int wave,
-                                            const float* cw, float (&hist)[3][8]) {
-  half_t* Qs = reinterpret_cast<half_t*>(smem + OFF_QS);
-  half_t* Ks = reinterpret_cast<half_t*>(smem + OFF_KS + (ci & 1) * KS_BYTES);
-  half_t* Vs = reinterpret_cast<half_t*>(smem + OFF_VS);
-  float* s_beta = reinterpret_cast<float*>(smem + OFF_SC + (ci & 1) * SC_BYTES);
-  float* s_G = s_beta + CH;
-  float* s_gam = s_G + CH;
-  float* s_dec = s_gam + CH;
-  const int c0 = tid, c1 = tid + NT;
-  *reinterpret_cast<u32x4*>(Qs + (c0 >> 4) * LD128 + 8 * (c0 & 15)) = nx.q0;
-  *reinterpret_cast<u32x4*>(Qs + (c1 >> 4) * LD128 + 8 * (c1 & 15)) = nx.q1;
-  *reinterpret_cast<u32x4*>(Ks + (c0 >> 4) * LD128 + 8 * (c0 & 15)) = nx.k0;
-  *reinterpret_cast<u32x4*>(Ks + (c1 >> 4) * LD128 + 8 * (c1 & 15)) = nx.k1;
-  if (tid < CH) {
-    s_G[tid] = nx.gb.x;
-    s_beta[tid] = nx.gb.y;
-    s_gam[tid] = nx.gb.z;
-    s_dec[tid] = nx.gb.w;
-  }
-  const int lane = tid & 63;
-  // tokens past the sequence: v = 0 (a multiply, not a branch, so no wait sits inside a branch)
-  const float live = ci * CH + lane < p.T ? 1.f : 0.f;
-  float4 w4[8];  // the taps of the eight channels (wave-uniform: scalar loads, one wait)
-#pragma unroll
-  for (int c = 0; c < 8; ++c) w4[c] = *reinterpret_cast<const float4*>(cw + 4 * c);
-  f16x8_v o;
-#pragma unroll
-  for (int c = 0; c < 8; ++c) {
-    const float x0 = raw_chan(nx.v, c);
-    const float x1 = from_prev_lane(x0, hist[2][c]);
-    const float x2 = from_prev_lane(x1, hist[1][c]);
-    const float x3 = from_prev_lane(x2, hist[0][c]);
-    const float a = w4[c].x * x3 + w4[c].y * x2 + w4[c].z * x1 + w4[c].w * x0;
-    o[c] = static_cast<half_t>(silu_ref(a) * live);
-#pragma unroll
-    for (int s = 0; s < 3; ++s) hist[s][c] = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, x0), CH - 3 + s));
-  }
-  *reinterpret_cast<f16x8_v*>(Vs + lane * LD64 + 8 * wave) = o;
-}
-
 // Workgroup -> (batch row, value head, dv half).  The 2 Hv / Hk workgroups that read one key
 // head's q and k tiles get block indices equal mod 8, so they run on one XCD and share its L2
 // (workgroups are dispatched to the XCDs round robin), when the key-head count allows it.
@@ -593,420 +489,636 @@ __device__ __forceinline__ void chunk_item(const ChunkParams& p, int& b, int& j,
   half_id = r & 1;
 }
 
-// The workgroup's waves take two roles, each running its own chunk loop with the same
-// barriers (three per chunk), so the registers of one role are not held by the other:
-//  key waves 0..3 (v = wave): the fp32 state columns dv = 16 v + lc, all of K, R and the
-//    substitution chain for dv tile v, the off-diagonal blocks of A, the state update;
-//  query waves 4..7 (v = wave - 4): the diagonal block A_vv and its inverse, all of Q,
-//    gamma Q S0, Aqk, and the output tiles of dv tile v.
-template <bool VEC16>
-__global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(2, 2))) void chunk_kernel(ChunkParams p) {
-  extern __shared__ __align__(16) unsigned char smem[];
-  const half_t* Qs = reinterpret_cast<const half_t*>(smem + OFF_QS);
+// ---------------------------------------------------------------------------
+// 3. the chunked recurrence, chunk_kernel (layout and roles in the file header).
+constexpr int VS_BYTES = CH * LD64 * 2;  // one V tile [tok][64 dv]
+// per-token scalars of a chunk: beta, G, gamma = exp(G), exp(G_C - G), and the factors of R for V
+// stored scaled by -log2(e) (see conv_v): beta' = -ln(2) beta, gamma' = log2(e) gamma
+constexpr int SC_BYTES = 6 * CH * 4;
+constexpr int HL_BLOCK = 1024;           // one 16x16 block as fp16 hi | lo A operands, 16 bytes per lane
+constexpr int OFF_QS = 0;                // Qs x 2
+constexpr int OFF_KS = OFF_QS + 2 * KS_BYTES;
+constexpr int OFF_VS = OFF_KS + 2 * KS_BYTES;
+constexpr int OFF_DHL = OFF_VS + 2 * VS_BYTES;           // D_p, p = 0..3, x 2
+constexpr int OFF_AHL = OFF_DHL + 2 * 4 * HL_BLOCK;      // A_pk (p > k) in lower_block order, x 2
+constexpr int OFF_AQK = OFF_AHL + 2 * 6 * HL_BLOCK;      // Aqk [tok][aqk_col(l)], x 2
+constexpr int OFF_SC = OFF_AQK + 2 * AQK_BYTES;          // the per-token scalars, x 2
+constexpr int OFF_ADG = OFF_SC + 2 * SC_BYTES;           // query scratch: A_pp, fp32 [block][row][LDB]
+constexpr int OFF_TB = OFF_ADG + 4 * 16 * LDB * 4;       // query scratch: D_p, fp32 [block][row][LDB]
+constexpr int OFF_TAPS = OFF_TB + 4 * 16 * LDB * 4;      // conv taps of the workgroup's 64 v channels, fp32 [ch][4]
+constexpr int LDS_BYTES = OFF_TAPS + DVS * KCONV * 4;
+static_assert(LDS_BYTES <= 160 * 1024, "LDS budget");
+static_assert(OFF_DHL % 16 == 0 && OFF_AHL % 16 == 0 && OFF_AQK % 16 == 0 && OFF_SC % 16 == 0 && OFF_ADG % 16 == 0, "16-byte regions");
+
+// Column position of key token l in an Aqk row: l = 32 s + 16 h + 4 q + r is kept at
+// 32 s + 8 q + 4 h + r, so the eight tokens of k-step s that lane quad q of a 16x16x32 operand
+// takes -- the token order of delta's packed operand (pack8h of two token tiles) -- are one
+// 16-byte read.
+__device__ __forceinline__ constexpr int aqk_col(int l) { return (l & ~31) + 8 * ((l >> 2) & 3) + 4 * ((l >> 4) & 1) + (l & 3); }
+
+// DPP wave_ror:1 -- lane l gets lane l - 1, lane 0 gets lane 63 (every source lane is valid, so no
+// old value is needed)
+__device__ __forceinline__ float rotate_in(float x) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, x), 0x13C, 0xf, 0xf, false));
+}
+
+// Chunk ci's v channels c0 .. c0 + 8 G - 1 of the workgroup's 64, convolved (conv1d + SiLU,
+// src/reference_ops.py:245-258) with one token per lane, into Vs.  prev[ch] holds the raw input of
+// channel ch at token ci * 64 - 64 + lane (the previous chunk; for chunk 0 lanes 61..63 hold the
+// initial conv state, tokens -3..-1); the three earlier tokens of lane l come from lanes l - 1 ..
+// l - 3 by DPP, and for the first lanes from prev rotated in.  The taps, read from LDS (one address
+// for the whole wave), are stored times -log2(e), so the tap sum is t = -log2(e) a and
+// silu(a) = a / (1 + 2^t); Vs receives t / (1 + 2^t) = -log2(e) silu(a), and R's factors carry the
+// constant back (beta' and gamma' of the scalars).  Tokens past the sequence get zero v.  prev is
+// advanced to this chunk.
+template <int G>
+__device__ __forceinline__ void conv_v(const ChunkParams& p, half_t* Vs, const u32x4 (&raw)[G], float (&prev)[8 * G],
+                                       const float* taps, int64_t ci, int lane, int c0) {
+  const bool ragged = (ci + 1) * CH > p.T;  // wave-uniform: only the last chunk can hold tokens past T
+  const float live = ci * CH + lane < p.T ? 1.f : 0.f;
+#pragma unroll
+  for (int g = 0; g < G; ++g) {
+    f16x8_v o;
+#pragma unroll
+    for (int c = 0; c < 8; ++c) {
+      const int ch = 8 * g + c;
+      const float x0 = raw_chan(raw[g], c);
+      const float r1 = rotate_in(prev[ch]);
+      const float x1 = from_prev_lane(x0, r1);
+      const float r2 = rotate_in(r1);
+      const float x2 = from_prev_lane(x1, r2);
+      const float r3 = rotate_in(r2);
+      const float x3 = from_prev_lane(x2, r3);
+      const float4 w = *reinterpret_cast<const float4*>(taps + KCONV * (c0 + ch));
+      const float t = w.x * x3 + w.y * x2 + w.z * x1 + w.w * x0;
+      float y = t * __builtin_amdgcn_rcpf(1.f + __builtin_amdgcn_exp2f(t));
+      if (ragged) y *= live;
+      o[c] = static_cast<half_t>(y);
+      prev[ch] = x0;
+    }
+    *reinterpret_cast<f16x8_v*>(Vs + lane * LD64 + c0 + 8 * g) = o;
+  }
+}
+
+// Raw bf16 v of token ci * 64 + lane in channels vch .. vch + 8 G - 1 (tokens past the sequence read
+// the last one; conv_v masks them).  The chunk's base is wave-uniform; lane_x = lane * x_st (32-bit).
+template <bool VEC16, int G>
+__device__ __forceinline__ void load_v(const ChunkParams& p, int64_t b, int64_t vch, int64_t ci, int lane, uint32_t lane_x, u32x4 (&r)[G]) {
+  const bf16_t* base = p.x + b * p.x_sb + ci * CH * p.x_st + vch;
+  const int64_t left = p.T - 1 - ci * CH;  // the last token's lane in this chunk
+  const uint32_t off = left >= CH - 1 ? lane_x : static_cast<uint32_t>(min(lane, static_cast<int>(left))) * static_cast<uint32_t>(p.x_st);
+#pragma unroll
+  for (int g = 0; g < G; ++g) {
+    const bf16_t* src = base + off + 8 * g;
+    if constexpr (VEC16) {
+      r[g] = *reinterpret_cast<const u32x4*>(src);
+    } else {
+#pragma unroll
+      for (int e = 0; e < 4; ++e) r[g][e] = reinterpret_cast<const uint32_t*>(src)[e];
+    }
+  }
+}
+
+// The v-conv state of one wave: the raw inputs of the chunk before the one to convolve, and the raw
+// inputs of the next chunk in flight.
+template <int G>
+struct ConvState {
+  float prev[8 * G];
+  u32x4 raw[G];
+  uint32_t lane_x;  // lane * x_st
+};
+
+// Also copies the channels' taps to LDS (taps: the workgroup's table, c0: the first channel's index
+// in it), read by this wave only.
+template <bool VEC16, int G>
+__device__ __forceinline__ void conv_init(const ChunkParams& p, int64_t b, int64_t vch, int lane, float* taps, int c0, ConvState<G>& cs) {
+  if (lane < 8 * G) {
+    constexpr float kNegLog2e = -1.4426950408889634f;
+    const float4 w = *reinterpret_cast<const float4*>(p.conv_w + (vch + lane) * KCONV);
+    *reinterpret_cast<float4*>(taps + KCONV * (c0 + lane)) = make_float4(kNegLog2e * w.x, kNegLog2e * w.y, kNegLog2e * w.z, kNegLog2e * w.w);
+  }
+#pragma unroll
+  for (int c = 0; c < 8 * G; ++c) {
+    float h = 0.f;
+    if (p.conv_in != nullptr && lane >= CH - (KCONV - 1)) h = p.conv_in[(b * p.C + vch + c) * (KCONV - 1) + lane - (CH - (KCONV - 1))];
+    cs.prev[c] = h;
+  }
+  cs.lane_x = static_cast<uint32_t>(lane) * static_cast<uint32_t>(p.x_st);
+  load_v<VEC16, G>(p, b, vch, 0, lane, cs.lane_x, cs.raw);
+}
+
+// Convolve chunk ci (its raw inputs are in cs.raw) into Vs and load chunk ci + 1's.
+template <bool VEC16, int G>
+__device__ __forceinline__ void conv_step(const ChunkParams& p, half_t* Vs, const float* taps, int64_t b, int64_t vch, int64_t ci, int lane,
+                                          int c0, ConvState<G>& cs) {
+  conv_v<G>(p, Vs, cs.raw, cs.prev, taps, ci, lane, c0);
+  load_v<VEC16, G>(p, b, vch, min64(ci + 1, p.nch - 1), lane, cs.lane_x, cs.raw);
+}
+
+// the conv state of channels vch .. vch + 8 G - 1: the raw inputs of the last K - 1 tokens
+template <int G>
+__device__ __forceinline__ void conv_tail(const ChunkParams& p, int64_t b, int64_t vch, int lane) {
+  if (p.conv_out == nullptr || lane >= KCONV - 1) return;
+  const int64_t t = p.T - (KCONV - 1) + lane;
+#pragma unroll
+  for (int c = 0; c < 8 * G; ++c) {
+    float val = 0.f;
+    if (t >= 0)
+      val = bf16_to_f32(p.x[b * p.x_sb + t * p.x_st + vch + c]);
+    else if (p.conv_in != nullptr)
+      val = p.conv_in[(b * p.C + vch + c) * (KCONV - 1) + (KCONV - 1) + t];
+    p.conv_out[(b * p.C + vch + c) * (KCONV - 1) + lane] = val;
+  }
+}
+
+// Rows 16 u .. 16 u + 15 of one chunk's q or k tile in wave u's registers: lane l holds the 16-byte
+// pieces 4 m + l % 4 (m = 0..3) of row 16 u + l / 4.
+struct RowRegs {
+  u32x4 x[4];
+};
+
+__device__ __forceinline__ RowRegs load_rows_g(const ChunkParams& p, const half_t* base_tensor, int64_t b, int qh, int64_t ci, int u,
+                                               uint32_t lane_off) {
+  RowRegs r;
+  const half_t* base = base_tensor + ((b * p.tp + ci * CH + 16 * u) * p.Hk + qh) * DK;  // wave-uniform
+#pragma unroll
+  for (int m = 0; m < 4; ++m) r.x[m] = *reinterpret_cast<const u32x4*>(base + lane_off + 32 * m);
+  return r;
+}
+
+// lane_off of load_rows_g: row lane / 4 of the 16, its 16-byte piece lane % 4
+__device__ __forceinline__ uint32_t rows_lane_offset(const ChunkParams& p, int lane) {
+  return static_cast<uint32_t>(lane >> 2) * static_cast<uint32_t>(p.Hk * DK) + 8 * (lane & 3);
+}
+
+__device__ __forceinline__ void store_rows(half_t* tile, const RowRegs& r, int u, int lane) {
+  const int o = (16 * u + (lane >> 2)) * LD128 + 8 * (lane & 3);
+#pragma unroll
+  for (int m = 0; m < 4; ++m) *reinterpret_cast<u32x4*>(tile + o + 32 * m) = r.x[m];
+}
+
+// (G, beta, exp(G), exp(G_C - G)) of token 16 u + l % 16 of one chunk
+__device__ __forceinline__ cfloat4 load_gate(const ChunkParams& p, int64_t b, int j, int64_t ci, int u, int lane) {
+  const float* base = p.gb + ((b * p.Hv + j) * p.tp + ci * CH + 16 * u) * 4;  // wave-uniform
+  return *reinterpret_cast<const cfloat4*>(base + 4 * (lane & 15));
+}
+
+__device__ __forceinline__ void store_gate(unsigned char* smem, const cfloat4& gb, int64_t ci, int u, int lane) {
+  if (lane < 16) {
+    float* sc = reinterpret_cast<float*>(smem + OFF_SC + (ci & 1) * SC_BYTES);
+    const int t = 16 * u + lane;
+    sc[t] = gb.y;           // beta
+    sc[CH + t] = gb.x;      // G
+    sc[2 * CH + t] = gb.z;  // gamma = exp(G)
+    sc[3 * CH + t] = gb.w;  // exp(G_C - G)
+    sc[4 * CH + t] = -0.69314718055994531f * gb.y;  // beta' = -ln(2) beta
+    sc[5 * CH + t] = 1.4426950408889634f * gb.z;    // gamma' = log2(e) gamma
+  }
+}
+
+// Epilogues of the state-independent blocks of chunk ci, from a product x = X_l X_i^T held as
+// lane (lq, lc) = [16 ti + lc][16 tl + 4 lq + r]:
+//  A[i][l] = beta_i exp(G_i - G_l) (k_i . k_l), l < i, as fp16 hi | lo A operands of the substitution;
+//  Aqk[i][l] = exp(G_i - G_l) (q_i . k_l), l <= i, in the output's column order.
+__device__ __forceinline__ void a_store(unsigned char* smem, int64_t ci, int ti, int tl, const cfloat4& x, int lane) {
+  const int lq = lane >> 4, lc = lane & 15;
+  const float* s_beta = reinterpret_cast<const float*>(smem + OFF_SC + (ci & 1) * SC_BYTES);
+  const float* s_G = s_beta + CH;
+  const int i = 16 * ti + lc;
+  const float gi = s_G[i];
+  const float bi = s_beta[i];
+  const cfloat4 gl = *reinterpret_cast<const cfloat4*>(s_G + 16 * tl + 4 * lq);
+  cfloat4 a;
+#pragma unroll
+  for (int r = 0; r < 4; ++r) a[r] = bi * __expf(gi - gl[r]) * x[r];
+  h4_v hi, lo;
+  split4(a, hi, lo);
+  const int n = ti * (ti - 1) / 2 + tl;  // lower_block order
+  h4_v* dst = reinterpret_cast<h4_v*>(smem + OFF_AHL + (ci & 1) * 6 * HL_BLOCK + n * HL_BLOCK + 16 * lane);
+  dst[0] = hi;
+  dst[1] = lo;
+}
+
+__device__ __forceinline__ void aqk_store(unsigned char* smem, int64_t ci, int ti, int tl, const cfloat4& x, int lane) {
+  const int lq = lane >> 4, lc = lane & 15;
+  const float* s_G = reinterpret_cast<const float*>(smem + OFF_SC + (ci & 1) * SC_BYTES) + CH;
+  half_t* Aqk = reinterpret_cast<half_t*>(smem + OFF_AQK + (ci & 1) * AQK_BYTES);
+  const int i = 16 * ti + lc;
+  const float gi = s_G[i];
+  const cfloat4 gl = *reinterpret_cast<const cfloat4*>(s_G + 16 * tl + 4 * lq);
+  float e[4];
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    const float y = __expf(gi - gl[r]) * x[r];
+    e[r] = 16 * tl + 4 * lq + r <= i ? y : 0.f;
+  }
+  store4h(Aqk + i * LD64 + aqk_col(16 * tl + 4 * lq), e[0], e[1], e[2], e[3]);
+}
+
+// Rows 16 t .. 16 t + 15 of a staged q or k tile as 16x16x32 operands (natural dk order).
+__device__ __forceinline__ void load_rows(const half_t* tile, int t, int lane, f16x8_v (&x)[DK / 32]) {
+  const int lq = lane >> 4, lc = lane & 15;
+#pragma unroll
+  for (int k = 0; k < DK / 32; ++k) x[k] = *reinterpret_cast<const f16x8_v*>(tile + (16 * t + lc) * LD128 + 32 * k + 8 * lq);
+}
+
+__device__ __forceinline__ cfloat4 rows_product(const f16x8_v (&x)[DK / 32], const f16x8_v (&y)[DK / 32]) {
+  cfloat4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int k = 0; k < DK / 32; ++k) acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(x[k], y[k], acc, 0, 0, 0);
+  return acc;
+}
+
+// A wave u, phase A, from the k rows and scalars it staged itself (its own LDS writes, so no
+// barrier): the diagonal block A_uu and D_u = (I + A_uu)^-1 as fp16 hi | lo operands.
+__device__ __forceinline__ void prepare_diagonal(unsigned char* smem, int64_t ci, int u, int lane) {
+  const int lq = lane >> 4, lc = lane & 15;
+  const half_t* Ks = reinterpret_cast<const half_t*>(smem + OFF_KS + (ci & 1) * KS_BYTES);
+  const float* s_beta = reinterpret_cast<const float*>(smem + OFF_SC + (ci & 1) * SC_BYTES);
+  const float* s_G = s_beta + CH;
   float* Adg = reinterpret_cast<float*>(smem + OFF_ADG);
   float* Tb = reinterpret_cast<float*>(smem + OFF_TB);
-  unsigned char* Ahl = smem + OFF_AHL;
-  half_t* Dt = reinterpret_cast<half_t*>(smem + OFF_DT);
-  const half_t* Vs = reinterpret_cast<const half_t*>(smem + OFF_VS);
-  half_t* St = reinterpret_cast<half_t*>(smem + OFF_ST);
-  half_t* Aqk = reinterpret_cast<half_t*>(smem + OFF_AQK);
-  // K tile and per-token scalars of chunk ci (double-buffered: phase 2 of chunk ci stages ci + 1)
-  auto ks_of = [&](int64_t ci) { return reinterpret_cast<const half_t*>(smem + OFF_KS + (ci & 1) * KS_BYTES); };
-  auto sc_of = [&](int64_t ci) { return reinterpret_cast<const float*>(smem + OFF_SC + (ci & 1) * SC_BYTES); };
+  unsigned char* Dhl = smem + OFF_DHL + (ci & 1) * 4 * HL_BLOCK;
+  f16x8_v kv[DK / 32];
+  load_rows(Ks, u, lane, kv);
+  // A_uu from the Gram block (symmetric: lane (lq, lc) holds k_{16u+4lq+r} . k_{16u+lc})
+  const cfloat4 gram = rows_product(kv, kv);
+  const int i = 16 * u + lc;
+  const float bi = s_beta[i];
+  const float gi = s_G[i];
+  const cfloat4 gl = *reinterpret_cast<const cfloat4*>(s_G + 16 * u + 4 * lq);
+  cfloat4 a;
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    const float e = bi * __expf(gi - gl[r]) * gram[r];
+    a[r] = 4 * lq + r < lc ? e : 0.f;
+  }
+  *reinterpret_cast<cfloat4*>(Adg + (16 * u + lc) * LDB + 4 * lq) = a;
+  // Adg was written by this wave just above; one wave's LDS accesses are performed in order
+  solve_unit_lower16(Adg + (16 * u) * LDB, Tb + (16 * u) * LDB, lane);
+  h4_v hi, lo;
+  split4(*reinterpret_cast<const cfloat4*>(Tb + (16 * u + lc) * LDB + 4 * lq), hi, lo);
+  h4_v* dst = reinterpret_cast<h4_v*>(Dhl + u * HL_BLOCK + 16 * lane);
+  dst[0] = hi;
+  dst[1] = lo;
+}
 
+// A wave u, phase B: the off-diagonal blocks n = u and u + 4 (< 6, lower_block order) of A.
+__device__ __forceinline__ void prepare_a_blocks(unsigned char* smem, int64_t ci, int u, int lane) {
+  const half_t* Ks = reinterpret_cast<const half_t*>(smem + OFF_KS + (ci & 1) * KS_BYTES);
+  int ti, tl;
+  lower_block(u, ti, tl);
+  f16x8_v kl[DK / 32], ki[DK / 32];
+  load_rows(Ks, tl, lane, kl);
+  load_rows(Ks, ti, lane, ki);
+  if (u < 2) {
+    int ti2, tl2;
+    lower_block(u + 4, ti2, tl2);
+    f16x8_v kl2[DK / 32], ki2[DK / 32];
+    load_rows(Ks, tl2, lane, kl2);
+    load_rows(Ks, ti2, lane, ki2);
+    const cfloat4 x = rows_product(kl, ki);
+    const cfloat4 x2 = rows_product(kl2, ki2);
+    a_store(smem, ci, ti, tl, x, lane);
+    a_store(smem, ci, ti2, tl2, x2, lane);
+  } else {
+    a_store(smem, ci, ti, tl, rows_product(kl, ki), lane);
+  }
+}
+
+// V wave u, phase B: the Aqk tiles (i, u), u <= i <= u + 2, and (3, 0) for u = 3.
+__device__ __forceinline__ void prepare_aqk(unsigned char* smem, int64_t ci, int u, int lane) {
+  const half_t* Ks = reinterpret_cast<const half_t*>(smem + OFF_KS + (ci & 1) * KS_BYTES);
+  const half_t* Qs = reinterpret_cast<const half_t*>(smem + OFF_QS + (ci & 1) * KS_BYTES);
+  f16x8_v kl[DK / 32];
+  load_rows(Ks, u, lane, kl);
+  if (u < 2) {
+    f16x8_v q0[DK / 32], q1[DK / 32], q2[DK / 32];
+    load_rows(Qs, u, lane, q0);
+    load_rows(Qs, u + 1, lane, q1);
+    load_rows(Qs, u + 2, lane, q2);
+    const cfloat4 x0 = rows_product(kl, q0);
+    const cfloat4 x1 = rows_product(kl, q1);
+    const cfloat4 x2 = rows_product(kl, q2);
+    aqk_store(smem, ci, u, u, x0, lane);
+    aqk_store(smem, ci, u + 1, u, x1, lane);
+    aqk_store(smem, ci, u + 2, u, x2, lane);
+  } else {
+    // u = 2: (2, 2), (3, 2); u = 3: (3, 3), (3, 0)
+    f16x8_v q0[DK / 32], q3[DK / 32], k0[DK / 32];
+    load_rows(Qs, u, lane, q0);
+    load_rows(Qs, 3, lane, q3);
+    if (u == 3) load_rows(Ks, 0, lane, k0);
+    const cfloat4 x0 = rows_product(kl, q0);
+    const cfloat4 x1 = u == 2 ? rows_product(kl, q3) : rows_product(k0, q3);
+    aqk_store(smem, ci, u, u, x0, lane);
+    if (u == 2)
+      aqk_store(smem, ci, 3, 2, x1, lane);
+    else
+      aqk_store(smem, ci, 3, 0, x1, lane);
+  }
+}
+
+// Key waves, chunk ci: phase A -- K S0, R, gamma (S0^T Q^T) -- and phase B -- the substitution,
+// the state update and the output stores.
+__device__ __forceinline__ void key_phase_a(const ChunkParams& p, unsigned char* smem, const cfloat4 (&S)[8], int64_t ci, int v, int tid,
+                                            cfloat4 (&R)[4], cfloat4 (&On)[4]) {
+  int lane = tid & 63;
+  asm volatile("" : "+v"(lane));
+  const int lq = lane >> 4, lc = lane & 15;
+  const half_t* Ks = reinterpret_cast<const half_t*>(smem + OFF_KS + (ci & 1) * KS_BYTES);
+  const half_t* Qs = reinterpret_cast<const half_t*>(smem + OFF_QS + (ci & 1) * KS_BYTES);
+  const half_t* Vs = reinterpret_cast<const half_t*>(smem + OFF_VS + (ci & 1) * VS_BYTES);
+  const float* s_beta = reinterpret_cast<const float*>(smem + OFF_SC + (ci & 1) * SC_BYTES);
+  const float* s_gam = s_beta + 2 * CH;
+  // S0 as the B operand of K S0 (and, as the A operand, of S0^T Q^T): slot e of lane (lq, lc) in
+  // k-step s is dk 8 kblk(s, lq) + e, held by tile 2 s (e < 4) or 2 s + 1 (e >= 4)
+  f16x8_v sb[DK / 32];
+#pragma unroll
+  for (int s = 0; s < DK / 32; ++s) sb[s] = pack8h(S[2 * s], S[2 * s + 1]);
+  cfloat4 acc[4];
+#pragma unroll
+  for (int t = 0; t < 4; ++t) {
+    f16x8_v kr[DK / 32], qr[DK / 32];
+#pragma unroll
+    for (int s = 0; s < DK / 32; ++s) {
+      kr[s] = *reinterpret_cast<const f16x8_v*>(Ks + (16 * t + lc) * LD128 + 8 * kblk(s, lq));
+      qr[s] = *reinterpret_cast<const f16x8_v*>(Qs + (16 * t + lc) * LD128 + 8 * kblk(s, lq));
+    }
+    acc[t] = cfloat4{0.f, 0.f, 0.f, 0.f};
+    On[t] = cfloat4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int s = 0; s < DK / 32; ++s) acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kr[s], sb[s], acc[t], 0, 0, 0);
+#pragma unroll
+    for (int s = 0; s < DK / 32; ++s) On[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(sb[s], qr[s], On[t], 0, 0, 0);
+  }
+#pragma unroll
+  for (int t = 0; t < 4; ++t) {
+    const h4_v v4 = tr_read(Vs, LD64, 16 * t + 4 * lq, 16 * v, lane);
+    // V is stored as -log2(e) v: R = beta (v - gamma K S0) = beta' (V + gamma' K S0)
+    const cfloat4 bt = *reinterpret_cast<const cfloat4*>(s_beta + 4 * CH + 16 * t + 4 * lq);
+    const cfloat4 gm = *reinterpret_cast<const cfloat4*>(s_beta + 5 * CH + 16 * t + 4 * lq);
+#pragma unroll
+    for (int r = 0; r < 4; ++r) R[t][r] = bt[r] * __builtin_fmaf(gm[r], acc[t][r], static_cast<float>(v4[r]));
+    On[t] *= s_gam[16 * t + lc];
+  }
+}
+
+__device__ __forceinline__ void key_phase_b(const ChunkParams& p, unsigned char* smem, cfloat4 (&S)[8], int64_t ci, int64_t b, int j,
+                                            int half_id, int v, int tid, const cfloat4 (&R)[4], cfloat4 (&On)[4], bool out16,
+                                            const uint32_t (&out_off)[2]) {
+  int lane = tid & 63;
+  asm volatile("" : "+v"(lane));
+  const int lq = lane >> 4, lc = lane & 15;
+  const half_t* Ks = reinterpret_cast<const half_t*>(smem + OFF_KS + (ci & 1) * KS_BYTES);
+  const float* s_beta = reinterpret_cast<const float*>(smem + OFF_SC + (ci & 1) * SC_BYTES);
+  const float* s_gam = s_beta + 2 * CH;
+  const float* s_dec = s_beta + 3 * CH;
+  const unsigned char* Dhl = smem + OFF_DHL + (ci & 1) * 4 * HL_BLOCK;
+  const unsigned char* Ahl = smem + OFF_AHL + (ci & 1) * 6 * HL_BLOCK;
+  const half_t* Aqk = reinterpret_cast<const half_t*>(smem + OFF_AQK + (ci & 1) * AQK_BYTES);
+  // (I + A) delta = R by blocked forward substitution over the 16-token blocks p,
+  // delta_p = D_p (R_p - sum_{k<p} A_pk delta_k), on hi + lo operand pairs; R and delta stay fp32
+  // in registers (the 16x16 accumulator layout is the B-operand layout)
+  h4_v dh[4], dl[4], ah[6], al[6];
+#pragma unroll
+  for (int pb = 0; pb < 4; ++pb) {
+    const h4_v* src = reinterpret_cast<const h4_v*>(Dhl + pb * HL_BLOCK + 16 * lane);
+    dh[pb] = src[0];
+    dl[pb] = src[1];
+  }
+#pragma unroll
+  for (int n = 0; n < 6; ++n) {
+    const h4_v* src = reinterpret_cast<const h4_v*>(Ahl + n * HL_BLOCK + 16 * lane);
+    ah[n] = src[0];
+    al[n] = src[1];
+  }
+  h4_v xh[4], xl[4];
+  cfloat4 dlt[4];  // delta, C layout
+  cfloat4 pacc[4];  // sum_{k<p} A_pk delta_k, accumulated as soon as each delta_k exists
+#pragma unroll
+  for (int pb = 0; pb < 4; ++pb) pacc[pb] = cfloat4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int pb = 0; pb < 4; ++pb) {
+    h4_v rh, rl;
+    split4(R[pb] - pacc[pb], rh, rl);
+    const cfloat4 zero = {0.f, 0.f, 0.f, 0.f};
+    dlt[pb] = mma3(dh[pb], dl[pb], rh, rl, zero);
+    split4(dlt[pb], xh[pb], xl[pb]);
+#pragma unroll
+    for (int q = pb + 1; q < 4; ++q) {
+      const int n = q * (q - 1) / 2 + pb;
+      pacc[q] = mma3(ah[n], al[n], xh[pb], xl[pb], pacc[q]);
+    }
+  }
+  // S = gamma_C S + K^T (exp(G_C - G) delta): k-step s covers tokens 32 s .. 32 s + 31 in the order of
+  // pack8h(tile 2 s, tile 2 s + 1); delta^T in the same order is the A operand of the output
+  f16x8_v bd[2], da[2];
+#pragma unroll
+  for (int s = 0; s < 2; ++s) {
+    const cfloat4 de0 = *reinterpret_cast<const cfloat4*>(s_dec + 32 * s + 4 * lq);
+    const cfloat4 de1 = *reinterpret_cast<const cfloat4*>(s_dec + 32 * s + 16 + 4 * lq);
+    bd[s] = pack8h(de0 * dlt[2 * s], de1 * dlt[2 * s + 1]);
+    da[s] = pack8h(dlt[2 * s], dlt[2 * s + 1]);
+  }
+  const float gamC = s_gam[CH - 1];
+#pragma unroll
+  for (int d = 0; d < 8; ++d) S[d] *= gamC;
+#pragma unroll
+  for (int d = 0; d < 8; ++d) {
+    f16x8_v ka[2];
+#pragma unroll
+    for (int s = 0; s < 2; ++s) ka[s] = ktr_operand(Ks, 32 * s + 4 * lq, d, lane);
+#pragma unroll
+    for (int s = 0; s < 2; ++s) S[d] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ka[s], bd[s], S[d], 0, 0, 0);
+  }
+  // output: O^T += delta^T Aqk^T (Aqk is zero above the diagonal, so k-step 1 only reaches token tiles 2, 3)
+#pragma unroll
+  for (int t = 0; t < 4; ++t) {
+#pragma unroll
+    for (int s = 0; s < 2; ++s) {
+      if (s == 1 && t < 2) continue;
+      const f16x8_v aq = *reinterpret_cast<const f16x8_v*>(Aqk + (16 * t + lc) * LD64 + 32 * s + 8 * lq);
+      On[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(da[s], aq, On[t], 0, 0, 0);
+    }
+  }
+  const int64_t tc0 = ci * CH;
+  const int ntok = static_cast<int>(min64(CH, p.T - tc0));  // tokens of this chunk inside the sequence
+  if (out16) {
+    // 16-byte stores: lanes 16 apart (rows lq, lq ^ 1) hold the adjacent dv quads of one token; one
+    // row swap (v_permlane16_swap of On[2m], On[2m + 1]) gives the even row both quads of token tile
+    // 2m and the odd row both quads of tile 2m + 1.  The chunk's base is wave-uniform; out_off[m]
+    // is this lane's offset from it.
+    const int odd = lq & 1;
+    bf16_t* obase = reinterpret_cast<bf16_t*>(p.out) + b * p.out_sb + tc0 * p.out_st + static_cast<int64_t>(j) * DV + half_id * DVS + 16 * v;
+#pragma unroll
+    for (int m = 0; m < 2; ++m) {
+      float lo[4], hi[4];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const auto sw = __builtin_amdgcn_permlane16_swap(__float_as_uint(On[2 * m][r]), __float_as_uint(On[2 * m + 1][r]), false, false);
+        lo[r] = __uint_as_float(sw[0]);
+        hi[r] = __uint_as_float(sw[1]);
+      }
+      if (ntok == CH || 16 * (2 * m + odd) + lc < ntok) {
+        uint4 packed;
+        packed.x = static_cast<uint32_t>(f32_to_bf16(lo[0])) | (static_cast<uint32_t>(f32_to_bf16(lo[1])) << 16);
+        packed.y = static_cast<uint32_t>(f32_to_bf16(lo[2])) | (static_cast<uint32_t>(f32_to_bf16(lo[3])) << 16);
+        packed.z = static_cast<uint32_t>(f32_to_bf16(hi[0])) | (static_cast<uint32_t>(f32_to_bf16(hi[1])) << 16);
+        packed.w = static_cast<uint32_t>(f32_to_bf16(hi[2])) | (static_cast<uint32_t>(f32_to_bf16(hi[3])) << 16);
+        *reinterpret_cast<uint4*>(obase + out_off[m]) = packed;
+      }
+    }
+    return;
+  }
+#pragma unroll
+  for (int t = 0; t < 4; ++t) {
+    const int64_t tg = tc0 + 16 * t + lc;
+    if (tg < p.T) {
+      const int64_t base = b * p.out_sb + tg * p.out_st + static_cast<int64_t>(j) * DV + half_id * DVS + 16 * v + 4 * lq;
+      if (p.out_dtype == QA_BF16) {
+        uint2 packed;
+        packed.x = static_cast<uint32_t>(f32_to_bf16(On[t][0])) | (static_cast<uint32_t>(f32_to_bf16(On[t][1])) << 16);
+        packed.y = static_cast<uint32_t>(f32_to_bf16(On[t][2])) | (static_cast<uint32_t>(f32_to_bf16(On[t][3])) << 16);
+        *reinterpret_cast<uint2*>(reinterpret_cast<bf16_t*>(p.out) + base) = packed;
+      } else {
+        *reinterpret_cast<float4*>(reinterpret_cast<float*>(p.out) + base) = make_float4(On[t][0], On[t][1], On[t][2], On[t][3]);
+      }
+    }
+  }
+}
+
+// The three roles run their own chunk loops with the same barriers (two per chunk, two before the
+// first), so the registers one role holds are not reserved in the others.  Twelve waves, three per
+// SIMD: key waves 0..3, A waves 4..7 (u = wave - 4) and V waves 8..11 (u = wave - 8).  Iteration ci:
+//   phase A: key -- K S0, Q S0, R of chunk ci; A wave u -- stage k rows 16 u .. and the gate scalars
+//            of chunk ci + 1, then A_uu and D_u; V wave u -- stage q rows 16 u .. of chunk ci + 1
+//            and convolve its v channels 16 u .. 16 u + 7;
+//   phase B: key -- substitution, state update, output of chunk ci; A waves -- chunk ci + 1's
+//            off-diagonal A blocks and v channels 16 u + 8 .. 16 u + 15; V waves -- its Aqk tiles.
+// Everything a role writes in a phase goes to buffers no other role reads in that phase (V, K, Q,
+// the scalars and the A / D / Aqk operands are double-buffered by chunk parity).
+constexpr int NT = 768;  // twelve waves, three per SIMD
+template <bool VEC16>
+__global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(3, 3))) void chunk_kernel(ChunkParams p) {
+  extern __shared__ __align__(16) unsigned char smem[];
   const int tid = threadIdx.x;
+  const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const bool kwave = wave < 4;
-  const int v = wave & 3;  // the dv tile (16 columns) a wave of either role owns
   int bi, j, qh, half_id;
   chunk_item(p, bi, j, qh, half_id);
   const int64_t b = bi;
-  // this wave's eight v channels (of the workgroup's 64) in mixed_qkv, their conv weights and the
-  // raw inputs of the three tokens before the chunk being staged
-  const int64_t vch = 2 * static_cast<int64_t>(p.Hk) * DK + static_cast<int64_t>(j) * DV + half_id * DVS + 8 * wave;
-  const float* cw = p.conv_w + vch * KCONV;
-  float hist[3][8];
-#pragma unroll
-  for (int s3 = 0; s3 < 3; ++s3)
-#pragma unroll
-    for (int c = 0; c < 8; ++c) hist[s3][c] = p.conv_in == nullptr ? 0.f : p.conv_in[(b * p.C + vch + c) * (KCONV - 1) + s3];
+  auto vs_of = [&](int64_t ci) { return reinterpret_cast<half_t*>(smem + OFF_VS + (ci & 1) * VS_BYTES); };
+  auto ks_of = [&](int64_t ci) { return reinterpret_cast<half_t*>(smem + OFF_KS + (ci & 1) * KS_BYTES); };
+  auto qs_of = [&](int64_t ci) { return reinterpret_cast<half_t*>(smem + OFF_QS + (ci & 1) * KS_BYTES); };
 
-  // Aqk tiles above the diagonal are zero for every chunk (both buffers)
-  if (tid < 6 * 64) {
-    const int lane = tid & 63, lq = lane >> 4, lc = lane & 15;
-    const int n = tid >> 6;  // (ti, tl) = (0,1) (0,2) (0,3) (1,2) (1,3) (2,3)
-    const int ti = n < 3 ? 0 : n < 5 ? 1 : 2;
-    const int tl = ti + 1 + (n < 3 ? n : n < 5 ? n - 3 : 0);
-#pragma unroll
-    for (int u = 0; u < 2; ++u) store4h(Aqk + u * (AQK_BYTES / 2) + (16 * ti + lc) * LD64 + 16 * tl + 4 * lq, 0.f, 0.f, 0.f, 0.f);
-  }
-  ChunkRegs nx = load_chunk<VEC16>(p, b, j, qh, vch, 0, tid);
-  stage_chunk(p, smem, nx, 0, tid, wave, cw, hist);
-  nx = load_chunk<VEC16>(p, b, j, qh, vch, min64(1, p.nch - 1), tid);
-  // (each role passes one barrier after its own set-up: the key waves' first St copy must be
-  // visible to the query waves' phase 1 of chunk 0, as the staged chunk 0 must be to both)
-  // chunk ci + 1 is staged in phase 2 of chunk ci (the query waves at its start, the key waves
-  // at its end, so the two waves of a SIMD do not run the VALU-heavy v conv at the same time);
-  // the loads of ci + 2 follow.
-  auto stage_next = [&](int64_t ci) {
-    if (ci + 1 < p.nch) {
-      stage_chunk(p, smem, nx, ci + 1, tid, wave, cw, hist);
-      nx = load_chunk<VEC16>(p, b, j, qh, vch, min64(ci + 2, p.nch - 1), tid);
-    }
-  };
-
-  if (kwave) {
+  if (wave < 4) {
+    const int v = wave;
     // state columns dv = 16 v + lc as eight 16x16 tiles: S[d][r] = S[dk_of(d, 4 lq + r)][16 v + lc]
     cfloat4 S[8];
     {
-      const int lane = tid & 63, lq = lane >> 4, lc = lane & 15;
+      const int lq = lane >> 4, lc = lane & 15;
       const float* s_in = p.state_in == nullptr ? nullptr : p.state_in + ((b * p.Hv + j) * DK) * DV + half_id * DVS;
 #pragma unroll
-      for (int d = 0; d < 8; ++d) {
+      for (int d = 0; d < 8; ++d)
 #pragma unroll
         for (int r = 0; r < 4; ++r) S[d][r] = s_in == nullptr ? 0.f : s_in[static_cast<int64_t>(dk_of(d, 4 * lq + r)) * DV + 16 * v + lc];
-        store4h(St + (16 * v + lc) * LD128 + dk_of(d, 4 * lq), S[d][0], S[d][1], S[d][2], S[d][3]);
-      }
+    }
+    // bf16 output rows with 16-byte aligned starts: each lane stores 16 bytes per token tile pair at
+    // a fixed offset from the chunk's base
+    const bool out16 = p.out_dtype == QA_BF16 && p.out_st % 8 == 0 && p.out_sb % 8 == 0;
+    uint32_t out_off[2];
+    {
+      const int lq = lane >> 4, lc = lane & 15, odd = lq & 1;
+#pragma unroll
+      for (int m = 0; m < 2; ++m) out_off[m] = static_cast<uint32_t>(16 * (2 * m + odd) + lc) * static_cast<uint32_t>(p.out_st) + 4 * (lq - odd);
     }
     lds_barrier();
+    lds_barrier();
     for (int64_t ci = 0; ci < p.nch; ++ci) {
-      // The lane index is re-derived opaquely each chunk, so the per-lane LDS addresses of the
-      // loop body are recomputed in it rather than hoisted out and held in VGPRs across it.
-      int lane = tid & 63;
-      asm volatile("" : "+v"(lane));
-      const int lq = lane >> 4;
-      const int lc = lane & 15;
-      const half_t* Ks = ks_of(ci);
-      const float* s_beta = sc_of(ci);
-      const float* s_G = s_beta + CH;
-      const float* s_gam = s_G + CH;
-
-      // ---------------- phase 1 (key wave): K (all 64 tokens) into registers; R = diag(beta)
-      // (V - diag(gamma) K S0) for dv tile v, with S0 from this wave's registers, kept for its
-      // substitution chain; the off-diagonal blocks n = v and v + 4 (< 6) of A from the same K
-      // registers, split once into fp16 hi + lo (to Ahl).  A = beta_i exp(G_i - G_l) K K^T
-      // (strictly lower) is computed as (K_l K_i^T), so lane (lq, lc) holds
-      // A[16 ti + lc][16 tl + 4 lq + r]: the A-operand layout of the 16x16x16 products that
-      // consume it.
-      cfloat4 R[4];  // R tiles (token block p, dv tile v), C layout
-      f16x8_v kr[4][DK / 32];
-#pragma unroll
-      for (int t = 0; t < 4; ++t)
-#pragma unroll
-        for (int k = 0; k < DK / 32; ++k) kr[t][k] = *reinterpret_cast<const f16x8_v*>(Ks + (16 * t + lc) * LD128 + 8 * kblk(k, lq));
-      // S0 as the B operand of K S0: slot e of lane (lq, lc) in k-step k is dk 8 kblk(k, lq) + e,
-      // which tile 2k (e < 4) or 2k + 1 (e >= 4) holds in register e % 4.  (The off-diagonal A
-      // blocks below use the same K registers for both operands, so the dk order is immaterial.)
-      f16x8_v sb[DK / 32];
-#pragma unroll
-      for (int k = 0; k < DK / 32; ++k) sb[k] = pack8h(S[2 * k], S[2 * k + 1]);
-      __builtin_amdgcn_sched_barrier(0);
-      cfloat4 acc[4];
-#pragma unroll
-      for (int t = 0; t < 4; ++t) acc[t] = cfloat4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (int k = 0; k < DK / 32; ++k)
-#pragma unroll
-        for (int t = 0; t < 4; ++t) acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kr[t][k], sb[k], acc[t], 0, 0, 0);
-      // the off-diagonal blocks of A this wave owns
-      cfloat4 aa[2];
-#pragma unroll
-      for (int n = 0; n < 6; ++n) {
-        if (n % 4 != v) continue;
-        int ti, tl;
-        lower_block(n, ti, tl);
-        cfloat4 x = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-        for (int k = 0; k < DK / 32; ++k) x = __builtin_amdgcn_mfma_f32_16x16x32_f16(kr[tl][k], kr[ti][k], x, 0, 0, 0);
-        aa[n / 4] = x;
-      }
-#pragma unroll
-      for (int t = 0; t < 4; ++t) {
-        const h4_v v4 = tr_read(Vs, LD64, 16 * t + 4 * lq, 16 * v, lane);
-        const cfloat4 bt = *reinterpret_cast<const cfloat4*>(s_beta + 16 * t + 4 * lq);
-        const cfloat4 gm = *reinterpret_cast<const cfloat4*>(s_gam + 16 * t + 4 * lq);
-#pragma unroll
-        for (int r = 0; r < 4; ++r) R[t][r] = bt[r] * __builtin_fmaf(-gm[r], acc[t][r], static_cast<float>(v4[r]));
-      }
-#pragma unroll
-      for (int n = 0; n < 6; ++n) {
-        if (n % 4 != v) continue;
-        int ti, tl;
-        lower_block(n, ti, tl);
-        const int i = 16 * ti + lc;
-        const float gi = s_G[i];
-        const float bi = s_beta[i];
-        const cfloat4 gl = *reinterpret_cast<const cfloat4*>(s_G + 16 * tl + 4 * lq);
-        cfloat4 a;
-#pragma unroll
-        for (int r = 0; r < 4; ++r) a[r] = bi * __expf(gi - gl[r]) * aa[n / 4][r];
-        h4_v hi, lo;
-        split4(a, hi, lo);
-        h4_v* dst = reinterpret_cast<h4_v*>(Ahl + n * 1024 + 16 * lane);
-        dst[0] = hi;
-        dst[1] = lo;
-      }
+      cfloat4 R[4], On[4];
+      key_phase_a(p, smem, S, ci, v, tid, R, On);
       lds_barrier();
-
-      // ---------------- phase 2 (key wave): (I + A) delta = R by blocked forward substitution
-      // over the 16-token blocks p, delta_p = D_p (R_p - sum_{k<p} A_pk delta_k).  A_pk and D_p
-      // enter as fp16 hi + lo A operands; R and delta stay fp32 in registers and are split into
-      // hi + lo B operands (the 16x16 accumulator layout is the B-operand layout).  delta^T goes
-      // to LDS for the output; then S = gamma_C S + K^T (exp(G_C - G) delta) from the same
-      // registers, and its fp16 copy to St.
-      h4_v dh[4], dl[4];
-#pragma unroll
-      for (int pb = 0; pb < 4; ++pb) split4(*reinterpret_cast<const cfloat4*>(Tb + (16 * pb + lc) * LDB + 4 * lq), dh[pb], dl[pb]);
-      h4_v ah[6], al[6];  // A_pk for (p, k) = (1,0) (2,0) (2,1) (3,0) (3,1) (3,2)
-#pragma unroll
-      for (int n = 0; n < 6; ++n) {
-        const h4_v* src = reinterpret_cast<const h4_v*>(Ahl + n * 1024 + 16 * lane);
-        ah[n] = src[0];
-        al[n] = src[1];
-      }
-      const float* s_dec = s_gam + CH;
-      h4_v xh[4], xl[4];
-      cfloat4 dd[4];  // exp(G_C - G) delta, C layout
-      // sum_{k<p} A_pk delta_k is accumulated as soon as each delta_k exists (pacc[p] takes the
-      // terms in the order k = 0, 1, ..), so only one product per block waits on the previous
-      // block's delta.
-      cfloat4 pacc[4];
-#pragma unroll
-      for (int pb = 0; pb < 4; ++pb) pacc[pb] = cfloat4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (int pb = 0; pb < 4; ++pb) {
-        const int i0 = 16 * pb + 4 * lq;
-        const cfloat4 de = *reinterpret_cast<const cfloat4*>(s_dec + i0);
-        h4_v rh, rl;
-        split4(R[pb] - pacc[pb], rh, rl);
-        const cfloat4 zero = {0.f, 0.f, 0.f, 0.f};
-        const cfloat4 d = mma3(dh[pb], dl[pb], rh, rl, zero);
-        split4(d, xh[pb], xl[pb]);
-#pragma unroll
-        for (int q = pb + 1; q < 4; ++q) {
-          const int n = q * (q - 1) / 2 + pb;
-          pacc[q] = mma3(ah[n], al[n], xh[pb], xl[pb], pacc[q]);
-        }
-        store4h(Dt + (ci & 1) * (DT_BYTES / 2) + (16 * v + lc) * LD64 + i0, d[0], d[1], d[2], d[3]);
-#pragma unroll
-        for (int r = 0; r < 4; ++r) dd[pb][r] = de[r] * d[r];
-      }
-      // S update.  k-step s covers tokens 32 s .. 32 s + 31, slot e of lane (lq, lc) being
-      // token 32 s + 4 lq + e (e < 4, block 2 s) or 32 s + 16 + 4 lq + e - 4 (block 2 s + 1):
-      // the registers of dd as they are.  The K^T operand uses the same token order and, for
-      // row lc of tile d, dk = dk_of(d, lc).
-      const float gamC = s_gam[CH - 1];
-      f16x8_v bd[2];
-#pragma unroll
-      for (int s = 0; s < 2; ++s) bd[s] = pack8h(dd[2 * s], dd[2 * s + 1]);
-#pragma unroll
-      for (int d = 0; d < 8; ++d) S[d] *= gamC;
-#pragma unroll
-      for (int d = 0; d < 8; ++d) {
-        f16x8_v ka[2];
-#pragma unroll
-        for (int s = 0; s < 2; ++s) ka[s] = ktr_operand(Ks, 32 * s + 4 * lq, d, lane);
-#pragma unroll
-        for (int s = 0; s < 2; ++s) S[d] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ka[s], bd[s], S[d], 0, 0, 0);
-      }
-#pragma unroll
-      for (int d = 0; d < 8; ++d)
-        store4h(St + ((ci + 1) & 1) * (ST_BYTES / 2) + (16 * v + lc) * LD128 + dk_of(d, 4 * lq), S[d][0], S[d][1], S[d][2], S[d][3]);
-      stage_next(ci);
+      key_phase_b(p, smem, S, ci, b, j, half_id, v, tid, R, On, out16, out_off);
       lds_barrier();
     }
     if (p.state_out != nullptr) {
-      const int lane = tid & 63, lq = lane >> 4, lc = lane & 15;
+      const int lq = lane >> 4, lc = lane & 15;
       float* s_out = p.state_out + ((b * p.Hv + j) * DK) * DV + half_id * DVS;
 #pragma unroll
       for (int d = 0; d < 8; ++d)
 #pragma unroll
         for (int r = 0; r < 4; ++r) s_out[static_cast<int64_t>(dk_of(d, 4 * lq + r)) * DV + 16 * v + lc] = S[d][r];
     }
-  } else {
-    cfloat4 O[4];  // O^T tiles (dv tile v, token tile t) of the newest chunk, C layout
-    // Output of chunk c, in phase 2 of chunk c + 1 (or after the loop): O^T += delta^T Aqk^T.
-    auto finish_chunk = [&](int64_t c, int lq, int lc) {
-      const int64_t tc0 = c * CH;
-      f16x8_v da[CH / 32], ab2[4][CH / 32];
-#pragma unroll
-      for (int k = 0; k < CH / 32; ++k) {
-        da[k] = *reinterpret_cast<const f16x8_v*>(Dt + (c & 1) * (DT_BYTES / 2) + (16 * v + lc) * LD64 + 32 * k + 8 * lq);
-#pragma unroll
-        for (int tt = 0; tt < 4; ++tt) ab2[tt][k] = *reinterpret_cast<const f16x8_v*>(Aqk + (c & 1) * (AQK_BYTES / 2) + (16 * tt + lc) * LD64 + 32 * k + 8 * lq);
-      }
-      __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-      for (int k = 0; k < CH / 32; ++k)
-#pragma unroll
-        for (int tt = 0; tt < 4; ++tt) O[tt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(da[k], ab2[tt][k], O[tt], 0, 0, 0);
-      if (p.out_dtype == QA_BF16 && p.out_st % 8 == 0 && p.out_sb % 8 == 0) {
-        // 16-byte stores: lanes 16 apart (rows lq, lq ^ 1) hold the adjacent dv quads of one
-        // token, so one row swap per element gives the even row both quads of token tile 2m and
-        // the odd row both quads of tile 2m + 1 (v_permlane16_swap of O[2m] and O[2m + 1]).
-        const int odd = lq & 1;
-#pragma unroll
-        for (int m = 0; m < 2; ++m) {
-          float lo[4], hi[4];
-#pragma unroll
-          for (int r = 0; r < 4; ++r) {
-            const auto sw = __builtin_amdgcn_permlane16_swap(__float_as_uint(O[2 * m][r]), __float_as_uint(O[2 * m + 1][r]), false, false);
-            lo[r] = __uint_as_float(sw[0]);
-            hi[r] = __uint_as_float(sw[1]);
-          }
-          const int64_t tg = tc0 + 16 * (2 * m + odd) + lc;
-          if (tg < p.T) {
-            const int64_t base = b * p.out_sb + tg * p.out_st + static_cast<int64_t>(j) * DV + half_id * DVS + 16 * v + 4 * (lq - odd);
-            uint4 packed;
-            packed.x = static_cast<uint32_t>(f32_to_bf16(lo[0])) | (static_cast<uint32_t>(f32_to_bf16(lo[1])) << 16);
-            packed.y = static_cast<uint32_t>(f32_to_bf16(lo[2])) | (static_cast<uint32_t>(f32_to_bf16(lo[3])) << 16);
-            packed.z = static_cast<uint32_t>(f32_to_bf16(hi[0])) | (static_cast<uint32_t>(f32_to_bf16(hi[1])) << 16);
-            packed.w = static_cast<uint32_t>(f32_to_bf16(hi[2])) | (static_cast<uint32_t>(f32_to_bf16(hi[3])) << 16);
-            *reinterpret_cast<uint4*>(reinterpret_cast<bf16_t*>(p.out) + base) = packed;
-          }
-        }
-        return;
-      }
-#pragma unroll
-      for (int tt = 0; tt < 4; ++tt) {
-        const int tok = 16 * tt + lc;
-        const int64_t tg = tc0 + tok;
-        if (tg < p.T) {
-          const int64_t base = b * p.out_sb + tg * p.out_st + static_cast<int64_t>(j) * DV + half_id * DVS + 16 * v + 4 * lq;
-          if (p.out_dtype == QA_BF16) {
-            bf16_t* o = reinterpret_cast<bf16_t*>(p.out) + base;
-            uint2 packed;
-            packed.x = static_cast<uint32_t>(f32_to_bf16(O[tt][0])) | (static_cast<uint32_t>(f32_to_bf16(O[tt][1])) << 16);
-            packed.y = static_cast<uint32_t>(f32_to_bf16(O[tt][2])) | (static_cast<uint32_t>(f32_to_bf16(O[tt][3])) << 16);
-            *reinterpret_cast<uint2*>(o) = packed;
-          } else {
-            *reinterpret_cast<float4*>(reinterpret_cast<float*>(p.out) + base) = make_float4(O[tt][0], O[tt][1], O[tt][2], O[tt][3]);
-          }
-        }
-      }
-    };
+  } else if (wave < 8) {
+    const int u = wave - 4;
+    // v channels 16 u + 8 .. 16 u + 15 of the workgroup's 64
+    const int64_t vch = 2 * static_cast<int64_t>(p.Hk) * DK + static_cast<int64_t>(j) * DV + half_id * DVS + 16 * u + 8;
+    float* taps = reinterpret_cast<float*>(smem + OFF_TAPS);
+    ConvState<1> cs;
+    conv_init<VEC16, 1>(p, b, vch, lane, taps, 16 * u + 8, cs);
+    const uint32_t row_off = rows_lane_offset(p, lane);
+    RowRegs kx = load_rows_g(p, p.kn, b, qh, 0, u, row_off);
+    cfloat4 gb = load_gate(p, b, j, 0, u, lane);
+    store_rows(ks_of(0), kx, u, lane);
+    store_gate(smem, gb, 0, u, lane);
+    kx = load_rows_g(p, p.kn, b, qh, min64(1, p.nch - 1), u, row_off);
+    gb = load_gate(p, b, j, min64(1, p.nch - 1), u, lane);
+    prepare_diagonal(smem, 0, u, lane);
+    lds_barrier();
+    prepare_a_blocks(smem, 0, u, lane);
+    conv_step<VEC16, 1>(p, vs_of(0), taps, b, vch, 0, lane, 16 * u + 8, cs);
     lds_barrier();
     for (int64_t ci = 0; ci < p.nch; ++ci) {
-      int lane = tid & 63;
-      asm volatile("" : "+v"(lane));
-      const int lq = lane >> 4;
-      const int lc = lane & 15;
-      const half_t* Ks = ks_of(ci);
-      const float* s_beta = sc_of(ci);
-      const float* s_G = s_beta + CH;
-      const float* s_gam = s_G + CH;
-
-      // ---------------- phase 1 (query wave): the diagonal block A_vv and D_v = (I + A_vv)^-1
-      // (to Tb); Q (all 64 tokens) into registers and gamma * (S0^T Q^T) for the output tiles
-      // of chunk c (dv tile v) from St[c % 2].
-      f16x8_v qr[4][DK / 32];  // Q rows 16 t + lc as 16x16x32 operands
-      f16x8_v kv[DK / 32];     // K rows 16 v + lc
-      cfloat4 On[4];           // gamma * (S0^T Q^T) of chunk c, until the output of chunk c - 1 is done
-      // A_vv (K_v K_v^T, one operand read serving both sides), then D_v
-#pragma unroll
-      for (int k = 0; k < DK / 32; ++k) kv[k] = *reinterpret_cast<const f16x8_v*>(Ks + (16 * v + lc) * LD128 + 32 * k + 8 * lq);
-      {
-        const int i = 16 * v + lc;
-        const float bi = s_beta[i];
-        const float gi = s_G[i];
-        const cfloat4 gl = *reinterpret_cast<const cfloat4*>(s_G + 16 * v + 4 * lq);
-        cfloat4 acc = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-        for (int k = 0; k < DK / 32; ++k) acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(kv[k], kv[k], acc, 0, 0, 0);
-        cfloat4 a;
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const float e = bi * __expf(gi - gl[r]) * acc[r];
-          a[r] = 4 * lq + r < lc ? e : 0.f;
-        }
-        *reinterpret_cast<cfloat4*>(Adg + (16 * v + lc) * LDB + 4 * lq) = a;
+      if (ci + 1 < p.nch) {
+        store_rows(ks_of(ci + 1), kx, u, lane);
+        store_gate(smem, gb, ci + 1, u, lane);
+        kx = load_rows_g(p, p.kn, b, qh, min64(ci + 2, p.nch - 1), u, row_off);
+        gb = load_gate(p, b, j, min64(ci + 2, p.nch - 1), u, lane);
+        prepare_diagonal(smem, ci + 1, u, lane);
       }
-      // The block was written by this wave just above, and one wave's LDS accesses are
-      // performed in order, so no barrier is needed.
-      solve_unit_lower16(Adg + (16 * v) * LDB, Tb + (16 * v) * LDB, lane);
-#pragma unroll
-      for (int t = 0; t < 4; ++t)
-#pragma unroll
-        for (int k = 0; k < DK / 32; ++k) qr[t][k] = *reinterpret_cast<const f16x8_v*>(Qs + (16 * t + lc) * LD128 + 32 * k + 8 * lq);
-      // O^T tiles (dv tile v, token tiles t) = gamma * (S0^T Q^T), the S0 rows shared
-      f16x8_v sa[DK / 32];
-#pragma unroll
-      for (int k = 0; k < DK / 32; ++k) sa[k] = *reinterpret_cast<const f16x8_v*>(St + (ci & 1) * (ST_BYTES / 2) + (16 * v + lc) * LD128 + 32 * k + 8 * lq);
-      __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-      for (int t = 0; t < 4; ++t) On[t] = cfloat4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (int k = 0; k < DK / 32; ++k)
-#pragma unroll
-        for (int t = 0; t < 4; ++t) On[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(sa[k], qr[t][k], On[t], 0, 0, 0);
-#pragma unroll
-      for (int t = 0; t < 4; ++t) On[t] *= s_gam[16 * t + lc];
       lds_barrier();
-      stage_next(ci);
-
-      // ---------------- phase 2 (query wave), alongside the chains: the output of chunk c - 1,
-      // then the lower tiles (i, v), v <= i <= v + 2, and for v = 3 also (3, 0), of
-      // Aqk[i][l] = exp(G_i - G_l) (q_i . k_l), l <= i, from the Q and K_v registers (to
-      // Aqk[c % 2]).
-      if (ci > 0) finish_chunk(ci - 1, lq, lc);
-#pragma unroll
-      for (int t = 0; t < 4; ++t) O[t] = On[t];
-      cfloat4 acc[4];  // tile (i, v) in acc[i]: indices known at compile time keep them in registers
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        if (i < v || i > v + 2) continue;
-        acc[i] = cfloat4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-        for (int k = 0; k < DK / 32; ++k) acc[i] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kv[k], qr[i][k], acc[i], 0, 0, 0);
+      if (ci + 1 < p.nch) {
+        prepare_a_blocks(smem, ci + 1, u, lane);
+        conv_step<VEC16, 1>(p, vs_of(ci + 1), taps, b, vch, ci + 1, lane, 16 * u + 8, cs);
       }
-      cfloat4 acc30 = {0.f, 0.f, 0.f, 0.f};
-      if (v == 3) {
-        f16x8_v k0[DK / 32];
-#pragma unroll
-        for (int k = 0; k < DK / 32; ++k) k0[k] = *reinterpret_cast<const f16x8_v*>(Ks + lc * LD128 + 32 * k + 8 * lq);
-#pragma unroll
-        for (int k = 0; k < DK / 32; ++k) acc30 = __builtin_amdgcn_mfma_f32_16x16x32_f16(k0[k], qr[3][k], acc30, 0, 0, 0);
-      }
-      auto aqk_store = [&](int ti, int tl, const cfloat4& x) {
-        const int i = 16 * ti + lc;
-        const float gi = s_G[i];
-        const cfloat4 gl = *reinterpret_cast<const cfloat4*>(s_G + 16 * tl + 4 * lq);
-        float e[4];
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const float y = __expf(gi - gl[r]) * x[r];
-          e[r] = 16 * tl + 4 * lq + r <= i ? y : 0.f;
-        }
-        store4h(Aqk + (ci & 1) * (AQK_BYTES / 2) + i * LD64 + 16 * tl + 4 * lq, e[0], e[1], e[2], e[3]);
-      };
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        if (i < v || i > v + 2) continue;
-        aqk_store(i, v, acc[i]);
-      }
-      if (v == 3) aqk_store(3, 0, acc30);
       lds_barrier();
     }
+    conv_tail<1>(p, b, vch, lane);
+  } else {
+    const int u = wave - 8;
+    // v channels 16 u .. 16 u + 7 of the workgroup's 64
+    const int64_t vch = 2 * static_cast<int64_t>(p.Hk) * DK + static_cast<int64_t>(j) * DV + half_id * DVS + 16 * u;
+    float* taps = reinterpret_cast<float*>(smem + OFF_TAPS);
+    ConvState<1> c0s;
+    conv_init<VEC16, 1>(p, b, vch, lane, taps, 16 * u, c0s);
+    const uint32_t row_off = rows_lane_offset(p, lane);
+    RowRegs qx = load_rows_g(p, p.qn, b, qh, 0, u, row_off);
+    store_rows(qs_of(0), qx, u, lane);
+    qx = load_rows_g(p, p.qn, b, qh, min64(1, p.nch - 1), u, row_off);
+    conv_step<VEC16, 1>(p, vs_of(0), taps, b, vch, 0, lane, 16 * u, c0s);
     {
-      const int lane = tid & 63;
-      finish_chunk(p.nch - 1, lane >> 4, lane & 15);
+      // the Aqk tiles above the diagonal that the output reads, (0, 1) and (2, 3), are zero for every
+      // chunk (both buffers): waves 8, 9 clear buffer 0, waves 10, 11 buffer 1
+      const int lq = lane >> 4, lc = lane & 15;
+      const int ti = (u & 1) ? 2 : 0;
+      half_t* Aqk = reinterpret_cast<half_t*>(smem + OFF_AQK + (u >> 1) * AQK_BYTES);
+      store4h(Aqk + (16 * ti + lc) * LD64 + aqk_col(16 * (ti + 1) + 4 * lq), 0.f, 0.f, 0.f, 0.f);
     }
-  }
-  // the conv state of this wave's v channels: the raw inputs of the last K - 1 tokens
-  if (p.conv_out != nullptr) {
-    const int lane = tid & 63;
-    if (lane < KCONV - 1) {
-      const int64_t t = p.T - (KCONV - 1) + lane;
-#pragma unroll
-      for (int c = 0; c < 8; ++c) {
-        float val = 0.f;
-        if (t >= 0)
-          val = bf16_to_f32(p.x[b * p.x_sb + t * p.x_st + vch + c]);
-        else if (p.conv_in != nullptr)
-          val = p.conv_in[(b * p.C + vch + c) * (KCONV - 1) + (KCONV - 1) + t];
-        p.conv_out[(b * p.C + vch + c) * (KCONV - 1) + lane] = val;
+    lds_barrier();
+    prepare_aqk(smem, 0, u, lane);
+    lds_barrier();
+    for (int64_t ci = 0; ci < p.nch; ++ci) {
+      if (ci + 1 < p.nch) {
+        store_rows(qs_of(ci + 1), qx, u, lane);
+        qx = load_rows_g(p, p.qn, b, qh, min64(ci + 2, p.nch - 1), u, row_off);
+        conv_step<VEC16, 1>(p, vs_of(ci + 1), taps, b, vch, ci + 1, lane, 16 * u, c0s);
       }
+      lds_barrier();
+      if (ci + 1 < p.nch) prepare_aqk(smem, ci + 1, u, lane);
+      lds_barrier();
     }
+    conv_tail<1>(p, b, vch, lane);
   }
 }
 
@@ -1041,6 +1153,9 @@ extern "C" int qa_chunk_gated_delta_rule(const void* mixed_qkv, int32_t x_dtype,
   QA_REQUIRE(out_dtype == QA_F32 || out_dtype == QA_BF16, "chunk_gated_delta_rule: out must be float32 or bfloat16");
   QA_REQUIRE(batch > 0 && seq > 0, "chunk_gated_delta_rule: batch and seq must be positive");
   QA_REQUIRE(batch * value_heads * 2 <= 0x7fffffff, "chunk_gated_delta_rule: too many workgroups");
+  QA_REQUIRE(x_stride_t > 0 && x_stride_t < (int64_t{1} << 25) && out_stride_t > 0 && out_stride_t < (int64_t{1} << 25) &&
+                 key_heads <= (1 << 16),
+             "chunk_gated_delta_rule: token strides must be positive and below 2^25 elements");
   QA_REQUIRE(out_stride_t % 4 == 0 && out_stride_b % 4 == 0 && (reinterpret_cast<uintptr_t>(out) & 15u) == 0,
              "chunk_gated_delta_rule: output rows must be 16-byte aligned");
   QA_REQUIRE((reinterpret_cast<uintptr_t>(conv_weight) & 15u) == 0, "chunk_gated_delta_rule: conv_weight must be 16-byte aligned");
