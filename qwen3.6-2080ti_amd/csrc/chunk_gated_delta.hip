@@ -361,12 +361,6 @@ __device__ __forceinline__ void split4(const cfloat4& v, h4_v& hi, h4_v& lo) {
   lo = __builtin_bit_cast(h4_v, u32x2{l0, l1});
 }
 
-// channel c of the raw bf16 pairs of a token (c even: low half)
-__device__ __forceinline__ float raw_chan(const u32x4& r, int c) {
-  const uint32_t u = r[c >> 1];
-  return __uint_as_float((c & 1) ? (u & 0xffff0000u) : (u << 16));
-}
-
 // x of lane l - 1 to lane l, and `first` (wave-uniform) to lane 0 (DPP wave_shr:1)
 __device__ __forceinline__ float from_prev_lane(float x, float first) {
   return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(__builtin_bit_cast(int, first), __builtin_bit_cast(int, x), 0x138, 0xf, 0xf, false));
@@ -522,106 +516,114 @@ __device__ __forceinline__ float rotate_in(float x) {
   return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, x), 0x13C, 0xf, 0xf, false));
 }
 
-// Chunk ci's v channels c0 .. c0 + 8 G - 1 of the workgroup's 64, convolved (conv1d + SiLU,
-// src/reference_ops.py:245-258) with one token per lane, into Vs.  prev[ch] holds the raw input of
-// channel ch at token ci * 64 - 64 + lane (the previous chunk; for chunk 0 lanes 61..63 hold the
+// Chunk ci's v channels c0 .. c0 + NC - 1 of the workgroup's 64 (NC = 4 or 8), convolved (conv1d +
+// SiLU, src/reference_ops.py:245-258) with one token per lane, into Vs.  prev[ch] holds the raw input
+// of channel ch at token ci * 64 - 64 + lane (the previous chunk; for chunk 0 lanes 61..63 hold the
 // initial conv state, tokens -3..-1); the three earlier tokens of lane l come from lanes l - 1 ..
 // l - 3 by DPP, and for the first lanes from prev rotated in.  The taps, read from LDS (one address
 // for the whole wave), are stored times -log2(e), so the tap sum is t = -log2(e) a and
 // silu(a) = a / (1 + 2^t); Vs receives t / (1 + 2^t) = -log2(e) silu(a), and R's factors carry the
-// constant back (beta' and gamma' of the scalars).  Tokens past the sequence get zero v.  prev is
-// advanced to this chunk.
-template <int G>
-__device__ __forceinline__ void conv_v(const ChunkParams& p, half_t* Vs, const u32x4 (&raw)[G], float (&prev)[8 * G],
-                                       const float* taps, int64_t ci, int lane, int c0) {
-  const bool ragged = (ci + 1) * CH > p.T;  // wave-uniform: only the last chunk can hold tokens past T
-  const float live = ci * CH + lane < p.T ? 1.f : 0.f;
+// constant back (beta' and gamma' of the scalars).  Tokens past the sequence enter as zero inputs
+// (load_v) and their v is never used: their beta is zero, so their rows of R and delta are zero.
+// prev is advanced to this chunk.
+template <int NC>
+__device__ __forceinline__ void conv_v(half_t* Vs, const uint32_t (&raw)[NC / 2], float (&prev)[NC], const float4 (&w)[NC], int lane, int c0) {
+  typedef __attribute__((__vector_size__(NC * sizeof(_Float16)))) _Float16 f16xn_v;
+  f16xn_v o;
 #pragma unroll
-  for (int g = 0; g < G; ++g) {
-    f16x8_v o;
-#pragma unroll
-    for (int c = 0; c < 8; ++c) {
-      const int ch = 8 * g + c;
-      const float x0 = raw_chan(raw[g], c);
-      const float r1 = rotate_in(prev[ch]);
-      const float x1 = from_prev_lane(x0, r1);
-      const float r2 = rotate_in(r1);
-      const float x2 = from_prev_lane(x1, r2);
-      const float r3 = rotate_in(r2);
-      const float x3 = from_prev_lane(x2, r3);
-      const float4 w = *reinterpret_cast<const float4*>(taps + KCONV * (c0 + ch));
-      const float t = w.x * x3 + w.y * x2 + w.z * x1 + w.w * x0;
-      float y = t * __builtin_amdgcn_rcpf(1.f + __builtin_amdgcn_exp2f(t));
-      if (ragged) y *= live;
-      o[c] = static_cast<half_t>(y);
-      prev[ch] = x0;
-    }
-    *reinterpret_cast<f16x8_v*>(Vs + lane * LD64 + c0 + 8 * g) = o;
+  for (int ch = 0; ch < NC; ++ch) {
+    const uint32_t w2 = raw[ch >> 1];
+    const float x0 = __uint_as_float((ch & 1) ? (w2 & 0xffff0000u) : (w2 << 16));
+    const float r1 = rotate_in(prev[ch]);
+    const float x1 = from_prev_lane(x0, r1);
+    const float r2 = rotate_in(r1);
+    const float x2 = from_prev_lane(x1, r2);
+    const float r3 = rotate_in(r2);
+    const float x3 = from_prev_lane(x2, r3);
+    const float t = w[ch].x * x3 + w[ch].y * x2 + w[ch].z * x1 + w[ch].w * x0;
+    o[ch] = static_cast<half_t>(t * __builtin_amdgcn_rcpf(1.f + __builtin_amdgcn_exp2f(t)));
+    prev[ch] = x0;
   }
+  *reinterpret_cast<f16xn_v*>(Vs + lane * LD64 + c0) = o;
 }
 
-// Raw bf16 v of token ci * 64 + lane in channels vch .. vch + 8 G - 1 (tokens past the sequence read
-// the last one; conv_v masks them).  The chunk's base is wave-uniform; lane_x = lane * x_st (32-bit).
-template <bool VEC16, int G>
-__device__ __forceinline__ void load_v(const ChunkParams& p, int64_t b, int64_t vch, int64_t ci, int lane, uint32_t lane_x, u32x4 (&r)[G]) {
+// Raw bf16 v of token ci * 64 + lane in channels vch .. vch + NC - 1; tokens past the sequence read
+// zero.  The chunk's base is wave-uniform; lane_x = lane * x_st (32-bit).  VEC16: 16-byte aligned
+// token rows (so 2 NC-byte vector loads are aligned).
+template <bool VEC16, int NC>
+__device__ __forceinline__ void load_v(const ChunkParams& p, int64_t b, int64_t vch, int64_t ci, int lane, uint32_t lane_x, uint32_t (&r)[NC / 2]) {
+  typedef unsigned int u32xn __attribute__((ext_vector_type(NC / 2)));
   const bf16_t* base = p.x + b * p.x_sb + ci * CH * p.x_st + vch;
   const int64_t left = p.T - 1 - ci * CH;  // the last token's lane in this chunk
-  const uint32_t off = left >= CH - 1 ? lane_x : static_cast<uint32_t>(min(lane, static_cast<int>(left))) * static_cast<uint32_t>(p.x_st);
+  const bool full = left >= CH - 1;        // wave-uniform
+  const uint32_t off = full ? lane_x : static_cast<uint32_t>(min(lane, static_cast<int>(left))) * static_cast<uint32_t>(p.x_st);
+  const bf16_t* src = base + off;
+  if constexpr (VEC16) {
+    const u32xn v = *reinterpret_cast<const u32xn*>(src);
 #pragma unroll
-  for (int g = 0; g < G; ++g) {
-    const bf16_t* src = base + off + 8 * g;
-    if constexpr (VEC16) {
-      r[g] = *reinterpret_cast<const u32x4*>(src);
-    } else {
+    for (int e = 0; e < NC / 2; ++e) r[e] = v[e];
+  } else {
 #pragma unroll
-      for (int e = 0; e < 4; ++e) r[g][e] = reinterpret_cast<const uint32_t*>(src)[e];
-    }
+    for (int e = 0; e < NC / 2; ++e) r[e] = reinterpret_cast<const uint32_t*>(src)[e];
+  }
+  if (!full && lane > left) {
+#pragma unroll
+    for (int e = 0; e < NC / 2; ++e) r[e] = 0u;
   }
 }
 
-// The v-conv state of one wave: the raw inputs of the chunk before the one to convolve, and the raw
-// inputs of the next chunk in flight.
-template <int G>
+// The v-conv state of one wave's NC channels: the raw inputs of the chunk before the one to
+// convolve, and the raw inputs of the next chunk in flight.
+template <int NC>
 struct ConvState {
-  float prev[8 * G];
-  u32x4 raw[G];
+  float prev[NC];
+  uint32_t raw[NC / 2];
   uint32_t lane_x;  // lane * x_st
 };
 
 // Also copies the channels' taps to LDS (taps: the workgroup's table, c0: the first channel's index
 // in it), read by this wave only.
-template <bool VEC16, int G>
-__device__ __forceinline__ void conv_init(const ChunkParams& p, int64_t b, int64_t vch, int lane, float* taps, int c0, ConvState<G>& cs) {
-  if (lane < 8 * G) {
+template <bool VEC16, int NC>
+__device__ __forceinline__ void conv_init(const ChunkParams& p, int64_t b, int64_t vch, int lane, float* taps, int c0, ConvState<NC>& cs) {
+  if (lane < NC) {
     constexpr float kNegLog2e = -1.4426950408889634f;
     const float4 w = *reinterpret_cast<const float4*>(p.conv_w + (vch + lane) * KCONV);
     *reinterpret_cast<float4*>(taps + KCONV * (c0 + lane)) = make_float4(kNegLog2e * w.x, kNegLog2e * w.y, kNegLog2e * w.z, kNegLog2e * w.w);
   }
 #pragma unroll
-  for (int c = 0; c < 8 * G; ++c) {
+  for (int c = 0; c < NC; ++c) {
     float h = 0.f;
     if (p.conv_in != nullptr && lane >= CH - (KCONV - 1)) h = p.conv_in[(b * p.C + vch + c) * (KCONV - 1) + lane - (CH - (KCONV - 1))];
     cs.prev[c] = h;
   }
   cs.lane_x = static_cast<uint32_t>(lane) * static_cast<uint32_t>(p.x_st);
-  load_v<VEC16, G>(p, b, vch, 0, lane, cs.lane_x, cs.raw);
+  load_v<VEC16, NC>(p, b, vch, 0, lane, cs.lane_x, cs.raw);
 }
 
-// Convolve chunk ci (its raw inputs are in cs.raw) into Vs and load chunk ci + 1's.
-template <bool VEC16, int G>
-__device__ __forceinline__ void conv_step(const ChunkParams& p, half_t* Vs, const float* taps, int64_t b, int64_t vch, int64_t ci, int lane,
-                                          int c0, ConvState<G>& cs) {
-  conv_v<G>(p, Vs, cs.raw, cs.prev, taps, ci, lane, c0);
-  load_v<VEC16, G>(p, b, vch, min64(ci + 1, p.nch - 1), lane, cs.lane_x, cs.raw);
+// The taps of channels c0 .. c0 + NC - 1 from the workgroup's table in LDS (one address for the
+// whole wave), read early in a phase so that their LDS latency is spent on other work.
+template <int NC>
+__device__ __forceinline__ void load_taps(const float* taps, int c0, float4 (&w)[NC]) {
+#pragma unroll
+  for (int ch = 0; ch < NC; ++ch) w[ch] = *reinterpret_cast<const float4*>(taps + KCONV * (c0 + ch));
+  __builtin_amdgcn_sched_barrier(0);  // keep the reads here: the scheduler would sink them to their uses
 }
 
-// the conv state of channels vch .. vch + 8 G - 1: the raw inputs of the last K - 1 tokens
-template <int G>
+// Convolve chunk ci (its raw inputs are in cs.raw) into Vs with taps w and load chunk ci + 1's.
+template <bool VEC16, int NC>
+__device__ __forceinline__ void conv_step(const ChunkParams& p, half_t* Vs, const float4 (&w)[NC], int64_t b, int64_t vch, int64_t ci, int lane,
+                                          int c0, ConvState<NC>& cs) {
+  conv_v<NC>(Vs, cs.raw, cs.prev, w, lane, c0);
+  load_v<VEC16, NC>(p, b, vch, min64(ci + 1, p.nch - 1), lane, cs.lane_x, cs.raw);
+}
+
+// the conv state of channels vch .. vch + NC - 1: the raw inputs of the last K - 1 tokens
+template <int NC>
 __device__ __forceinline__ void conv_tail(const ChunkParams& p, int64_t b, int64_t vch, int lane) {
   if (p.conv_out == nullptr || lane >= KCONV - 1) return;
   const int64_t t = p.T - (KCONV - 1) + lane;
 #pragma unroll
-  for (int c = 0; c < 8 * G; ++c) {
+  for (int c = 0; c < NC; ++c) {
     float val = 0.f;
     if (t >= 0)
       val = bf16_to_f32(p.x[b * p.x_sb + t * p.x_st + vch + c]);
@@ -1055,8 +1057,8 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(3, 3))) void
     // v channels 16 u + 8 .. 16 u + 15 of the workgroup's 64
     const int64_t vch = 2 * static_cast<int64_t>(p.Hk) * DK + static_cast<int64_t>(j) * DV + half_id * DVS + 16 * u + 8;
     float* taps = reinterpret_cast<float*>(smem + OFF_TAPS);
-    ConvState<1> cs;
-    conv_init<VEC16, 1>(p, b, vch, lane, taps, 16 * u + 8, cs);
+    ConvState<8> cs;
+    conv_init<VEC16, 8>(p, b, vch, lane, taps, 16 * u + 8, cs);
     const uint32_t row_off = rows_lane_offset(p, lane);
     RowRegs kx = load_rows_g(p, p.kn, b, qh, 0, u, row_off);
     cfloat4 gb = load_gate(p, b, j, 0, u, lane);
@@ -1066,9 +1068,15 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(3, 3))) void
     gb = load_gate(p, b, j, min64(1, p.nch - 1), u, lane);
     prepare_diagonal(smem, 0, u, lane);
     lds_barrier();
-    prepare_a_blocks(smem, 0, u, lane);
-    conv_step<VEC16, 1>(p, vs_of(0), taps, b, vch, 0, lane, 16 * u + 8, cs);
+    {
+      float4 w[8];
+      load_taps<8>(taps, 16 * u + 8, w);
+      prepare_a_blocks(smem, 0, u, lane);
+      conv_step<VEC16, 8>(p, vs_of(0), w, b, vch, 0, lane, 16 * u + 8, cs);
+    }
     lds_barrier();
+    float4 wa[8];
+    load_taps<8>(taps, 16 * u + 8, wa);
     for (int64_t ci = 0; ci < p.nch; ++ci) {
       if (ci + 1 < p.nch) {
         store_rows(ks_of(ci + 1), kx, u, lane);
@@ -1080,23 +1088,27 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(3, 3))) void
       lds_barrier();
       if (ci + 1 < p.nch) {
         prepare_a_blocks(smem, ci + 1, u, lane);
-        conv_step<VEC16, 1>(p, vs_of(ci + 1), taps, b, vch, ci + 1, lane, 16 * u + 8, cs);
+        conv_step<VEC16, 8>(p, vs_of(ci + 1), wa, b, vch, ci + 1, lane, 16 * u + 8, cs);
       }
       lds_barrier();
     }
-    conv_tail<1>(p, b, vch, lane);
+    conv_tail<8>(p, b, vch, lane);
   } else {
     const int u = wave - 8;
     // v channels 16 u .. 16 u + 7 of the workgroup's 64
     const int64_t vch = 2 * static_cast<int64_t>(p.Hk) * DK + static_cast<int64_t>(j) * DV + half_id * DVS + 16 * u;
     float* taps = reinterpret_cast<float*>(smem + OFF_TAPS);
-    ConvState<1> c0s;
-    conv_init<VEC16, 1>(p, b, vch, lane, taps, 16 * u, c0s);
+    ConvState<8> cs;
+    conv_init<VEC16, 8>(p, b, vch, lane, taps, 16 * u, cs);
     const uint32_t row_off = rows_lane_offset(p, lane);
     RowRegs qx = load_rows_g(p, p.qn, b, qh, 0, u, row_off);
-    store_rows(qs_of(0), qx, u, lane);
-    qx = load_rows_g(p, p.qn, b, qh, min64(1, p.nch - 1), u, row_off);
-    conv_step<VEC16, 1>(p, vs_of(0), taps, b, vch, 0, lane, 16 * u, c0s);
+    {
+      float4 w[8];
+      load_taps<8>(taps, 16 * u, w);
+      store_rows(qs_of(0), qx, u, lane);
+      qx = load_rows_g(p, p.qn, b, qh, min64(1, p.nch - 1), u, row_off);
+      conv_step<VEC16, 8>(p, vs_of(0), w, b, vch, 0, lane, 16 * u, cs);
+    }
     {
       // the Aqk tiles above the diagonal that the output reads, (0, 1) and (2, 3), are zero for every
       // chunk (both buffers): waves 8, 9 clear buffer 0, waves 10, 11 buffer 1
@@ -1108,17 +1120,19 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(3, 3))) void
     lds_barrier();
     prepare_aqk(smem, 0, u, lane);
     lds_barrier();
+    float4 wv[8];
+    load_taps<8>(taps, 16 * u, wv);
     for (int64_t ci = 0; ci < p.nch; ++ci) {
       if (ci + 1 < p.nch) {
         store_rows(qs_of(ci + 1), qx, u, lane);
         qx = load_rows_g(p, p.qn, b, qh, min64(ci + 2, p.nch - 1), u, row_off);
-        conv_step<VEC16, 1>(p, vs_of(ci + 1), taps, b, vch, ci + 1, lane, 16 * u, c0s);
+        conv_step<VEC16, 8>(p, vs_of(ci + 1), wv, b, vch, ci + 1, lane, 16 * u, cs);
       }
       lds_barrier();
       if (ci + 1 < p.nch) prepare_aqk(smem, ci + 1, u, lane);
       lds_barrier();
     }
-    conv_tail<1>(p, b, vch, lane);
+    conv_tail<8>(p, b, vch, lane);
   }
 }
 
