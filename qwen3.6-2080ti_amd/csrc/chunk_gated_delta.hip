@@ -494,7 +494,7 @@ constexpr int OFF_QS = 0;                // Qs x 2
 constexpr int OFF_KS = OFF_QS + 2 * KS_BYTES;
 constexpr int OFF_VS = OFF_KS + 2 * KS_BYTES;
 constexpr int OFF_DHL = OFF_VS + 2 * VS_BYTES;           // D_p, p = 0..3, x 2
-constexpr int OFF_AHL = OFF_DHL + 2 * 4 * HL_BLOCK;      // A_pk (p > k) in lower_block order, x 2
+constexpr int OFF_AHL = OFF_DHL + 2 * 4 * HL_BLOCK;      // M_pk = D_p A_pk (p > k) in lower_block order, x 2
 constexpr int OFF_AQK = OFF_AHL + 2 * 6 * HL_BLOCK;      // Aqk [tok][aqk_col(l)], x 2
 constexpr int OFF_SC = OFF_AQK + 2 * AQK_BYTES;          // the per-token scalars, x 2
 constexpr int OFF_ADG = OFF_SC + 2 * SC_BYTES;           // query scratch: A_pp, fp32 [block][row][LDB]
@@ -682,19 +682,28 @@ __device__ __forceinline__ void store_gate(unsigned char* smem, const cfloat4& g
 // lane (lq, lc) = [16 ti + lc][16 tl + 4 lq + r]:
 //  A[i][l] = beta_i exp(G_i - G_l) (k_i . k_l), l < i, as fp16 hi | lo A operands of the substitution;
 //  Aqk[i][l] = exp(G_i - G_l) (q_i . k_l), l <= i, in the output's column order.
-__device__ __forceinline__ void a_store(unsigned char* smem, int64_t ci, int ti, int tl, const cfloat4& x, int lane) {
+// M_pk = D_p A_pk for p = ti > k = tl, as fp16 hi | lo A operands of the substitution.  x is the
+// product (K_i K_l^T), lane (lq, lc) = [16 ti + 4 lq + r][16 tl + lc]: scaled to A[i][l] it is the
+// A-operand layout of A^T, and M^T = A^T D_p^T (D_p from its hi | lo operands, whose layout is the
+// B-operand layout of D_p^T) comes out as lane (lq, lc) = M[16 ti + lc][16 tl + 4 lq + r], the
+// A-operand layout of M.
+__device__ __forceinline__ void m_store(unsigned char* smem, int64_t ci, int ti, int tl, const cfloat4& x, int lane) {
   const int lq = lane >> 4, lc = lane & 15;
   const float* s_beta = reinterpret_cast<const float*>(smem + OFF_SC + (ci & 1) * SC_BYTES);
   const float* s_G = s_beta + CH;
-  const int i = 16 * ti + lc;
-  const float gi = s_G[i];
-  const float bi = s_beta[i];
-  const cfloat4 gl = *reinterpret_cast<const cfloat4*>(s_G + 16 * tl + 4 * lq);
+  const cfloat4 bi = *reinterpret_cast<const cfloat4*>(s_beta + 16 * ti + 4 * lq);
+  const cfloat4 gi = *reinterpret_cast<const cfloat4*>(s_G + 16 * ti + 4 * lq);
+  const float gl = s_G[16 * tl + lc];
   cfloat4 a;
 #pragma unroll
-  for (int r = 0; r < 4; ++r) a[r] = bi * __expf(gi - gl[r]) * x[r];
+  for (int r = 0; r < 4; ++r) a[r] = bi[r] * __expf(gi[r] - gl) * x[r];
+  h4_v ah, al;
+  split4(a, ah, al);
+  const h4_v* dsrc = reinterpret_cast<const h4_v*>(smem + OFF_DHL + (ci & 1) * 4 * HL_BLOCK + ti * HL_BLOCK + 16 * lane);
+  const cfloat4 zero = {0.f, 0.f, 0.f, 0.f};
+  const cfloat4 m = mma3(ah, al, dsrc[0], dsrc[1], zero);
   h4_v hi, lo;
-  split4(a, hi, lo);
+  split4(m, hi, lo);
   const int n = ti * (ti - 1) / 2 + tl;  // lower_block order
   h4_v* dst = reinterpret_cast<h4_v*>(smem + OFF_AHL + (ci & 1) * 6 * HL_BLOCK + n * HL_BLOCK + 16 * lane);
   dst[0] = hi;
@@ -765,7 +774,11 @@ __device__ __forceinline__ void prepare_diagonal(unsigned char* smem, int64_t ci
   dst[1] = lo;
 }
 
-// A wave u, phase B: the off-diagonal blocks n = u and u + 4 (< 6, lower_block order) of A.
+// Phase B products of chunk ci, three per V wave and one per A wave (which also convolves eight v
+// channels): the six blocks M_pk = D_p A_pk (p > k) and the ten lower Aqk tiles.
+//  A wave u: M(1,0), M(2,0), M(2,1), M(3,0) for u = 0..3;
+//  V wave 0: Aqk(0,0) Aqk(1,0) Aqk(2,0);  1: Aqk(1,1) Aqk(2,1) Aqk(3,1);
+//  V wave 2: Aqk(2,2) Aqk(3,2) M(3,2);    3: Aqk(3,3) Aqk(3,0) M(3,1).
 __device__ __forceinline__ void prepare_a_blocks(unsigned char* smem, int64_t ci, int u, int lane) {
   const half_t* Ks = reinterpret_cast<const half_t*>(smem + OFF_KS + (ci & 1) * KS_BYTES);
   int ti, tl;
@@ -773,22 +786,9 @@ __device__ __forceinline__ void prepare_a_blocks(unsigned char* smem, int64_t ci
   f16x8_v kl[DK / 32], ki[DK / 32];
   load_rows(Ks, tl, lane, kl);
   load_rows(Ks, ti, lane, ki);
-  if (u < 2) {
-    int ti2, tl2;
-    lower_block(u + 4, ti2, tl2);
-    f16x8_v kl2[DK / 32], ki2[DK / 32];
-    load_rows(Ks, tl2, lane, kl2);
-    load_rows(Ks, ti2, lane, ki2);
-    const cfloat4 x = rows_product(kl, ki);
-    const cfloat4 x2 = rows_product(kl2, ki2);
-    a_store(smem, ci, ti, tl, x, lane);
-    a_store(smem, ci, ti2, tl2, x2, lane);
-  } else {
-    a_store(smem, ci, ti, tl, rows_product(kl, ki), lane);
-  }
+  m_store(smem, ci, ti, tl, rows_product(ki, kl), lane);
 }
 
-// V wave u, phase B: the Aqk tiles (i, u), u <= i <= u + 2, and (3, 0) for u = 3.
 __device__ __forceinline__ void prepare_aqk(unsigned char* smem, int64_t ci, int u, int lane) {
   const half_t* Ks = reinterpret_cast<const half_t*>(smem + OFF_KS + (ci & 1) * KS_BYTES);
   const half_t* Qs = reinterpret_cast<const half_t*>(smem + OFF_QS + (ci & 1) * KS_BYTES);
@@ -805,26 +805,37 @@ __device__ __forceinline__ void prepare_aqk(unsigned char* smem, int64_t ci, int
     aqk_store(smem, ci, u, u, x0, lane);
     aqk_store(smem, ci, u + 1, u, x1, lane);
     aqk_store(smem, ci, u + 2, u, x2, lane);
-  } else {
-    // u = 2: (2, 2), (3, 2); u = 3: (3, 3), (3, 0)
-    f16x8_v q0[DK / 32], q3[DK / 32], k0[DK / 32];
-    load_rows(Qs, u, lane, q0);
+  } else if (u == 2) {
+    // Aqk(2,2), Aqk(3,2) from K_2; M(3,2) = D_3 A_32 from K_3, K_2
+    f16x8_v q2[DK / 32], q3[DK / 32], k3[DK / 32];
+    load_rows(Qs, 2, lane, q2);
     load_rows(Qs, 3, lane, q3);
-    if (u == 3) load_rows(Ks, 0, lane, k0);
-    const cfloat4 x0 = rows_product(kl, q0);
-    const cfloat4 x1 = u == 2 ? rows_product(kl, q3) : rows_product(k0, q3);
-    aqk_store(smem, ci, u, u, x0, lane);
-    if (u == 2)
-      aqk_store(smem, ci, 3, 2, x1, lane);
-    else
-      aqk_store(smem, ci, 3, 0, x1, lane);
+    load_rows(Ks, 3, lane, k3);
+    const cfloat4 x0 = rows_product(kl, q2);
+    const cfloat4 x1 = rows_product(kl, q3);
+    const cfloat4 x2 = rows_product(k3, kl);
+    aqk_store(smem, ci, 2, 2, x0, lane);
+    aqk_store(smem, ci, 3, 2, x1, lane);
+    m_store(smem, ci, 3, 2, x2, lane);
+  } else {
+    // Aqk(3,3) from K_3; Aqk(3,0) from K_0; M(3,1) = D_3 A_31 from K_3, K_1
+    f16x8_v q3[DK / 32], k0[DK / 32], k1[DK / 32];
+    load_rows(Qs, 3, lane, q3);
+    load_rows(Ks, 0, lane, k0);
+    load_rows(Ks, 1, lane, k1);
+    const cfloat4 x0 = rows_product(kl, q3);
+    const cfloat4 x1 = rows_product(k0, q3);
+    const cfloat4 x2 = rows_product(kl, k1);
+    aqk_store(smem, ci, 3, 3, x0, lane);
+    aqk_store(smem, ci, 3, 0, x1, lane);
+    m_store(smem, ci, 3, 1, x2, lane);
   }
 }
 
 // Key waves, chunk ci: phase A -- K S0, R, gamma (S0^T Q^T) -- and phase B -- the substitution,
 // the state update and the output stores.
-__device__ __forceinline__ void key_phase_a(const ChunkParams& p, unsigned char* smem, const cfloat4 (&S)[8], int64_t ci, int v, int tid,
-                                            cfloat4 (&R)[4], cfloat4 (&On)[4]) {
+__device__ __forceinline__ void key_phase_a(const ChunkParams& p, unsigned char* smem, cfloat4 (&S)[8], int64_t ci, int v, int tid,
+                                            cfloat4 (&Y)[4], cfloat4 (&On)[4]) {
   int lane = tid & 63;
   asm volatile("" : "+v"(lane));
   const int lq = lane >> 4, lc = lane & 15;
@@ -854,67 +865,71 @@ __device__ __forceinline__ void key_phase_a(const ChunkParams& p, unsigned char*
 #pragma unroll
     for (int s = 0; s < DK / 32; ++s) On[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(sb[s], qr[s], On[t], 0, 0, 0);
   }
+  // the state's decay over the chunk, S = gamma_C S (the update adds K^T (exp(G_C - G) delta) in phase B)
+  const float gamC = s_gam[CH - 1];
+#pragma unroll
+  for (int d = 0; d < 8; ++d) S[d] *= gamC;
+  // R = diag(beta) (V - diag(gamma) K S0) per token block, then Y_p = D_p R_p (hi + lo operand pairs):
+  // the first term of delta_p = D_p R_p - sum_{k<p} M_pk delta_k, off the substitution chain
+  const unsigned char* Dhl = smem + OFF_DHL + (ci & 1) * 4 * HL_BLOCK;
 #pragma unroll
   for (int t = 0; t < 4; ++t) {
     const h4_v v4 = tr_read(Vs, LD64, 16 * t + 4 * lq, 16 * v, lane);
     // V is stored as -log2(e) v: R = beta (v - gamma K S0) = beta' (V + gamma' K S0)
     const cfloat4 bt = *reinterpret_cast<const cfloat4*>(s_beta + 4 * CH + 16 * t + 4 * lq);
     const cfloat4 gm = *reinterpret_cast<const cfloat4*>(s_beta + 5 * CH + 16 * t + 4 * lq);
+    cfloat4 R;
 #pragma unroll
-    for (int r = 0; r < 4; ++r) R[t][r] = bt[r] * __builtin_fmaf(gm[r], acc[t][r], static_cast<float>(v4[r]));
+    for (int r = 0; r < 4; ++r) R[r] = bt[r] * __builtin_fmaf(gm[r], acc[t][r], static_cast<float>(v4[r]));
     On[t] *= s_gam[16 * t + lc];
+    h4_v rh, rl;
+    split4(R, rh, rl);
+    const h4_v* dsrc = reinterpret_cast<const h4_v*>(Dhl + t * HL_BLOCK + 16 * lane);
+    const cfloat4 zero = {0.f, 0.f, 0.f, 0.f};
+    Y[t] = mma3(dsrc[0], dsrc[1], rh, rl, zero);
   }
 }
 
 __device__ __forceinline__ void key_phase_b(const ChunkParams& p, unsigned char* smem, cfloat4 (&S)[8], int64_t ci, int64_t b, int j,
-                                            int half_id, int v, int tid, const cfloat4 (&R)[4], cfloat4 (&On)[4], bool out16,
+                                            int half_id, int v, int tid, const cfloat4 (&Y)[4], cfloat4 (&On)[4], bool out16,
                                             const uint32_t (&out_off)[2]) {
   int lane = tid & 63;
   asm volatile("" : "+v"(lane));
   const int lq = lane >> 4, lc = lane & 15;
   const half_t* Ks = reinterpret_cast<const half_t*>(smem + OFF_KS + (ci & 1) * KS_BYTES);
   const float* s_beta = reinterpret_cast<const float*>(smem + OFF_SC + (ci & 1) * SC_BYTES);
-  const float* s_gam = s_beta + 2 * CH;
   const float* s_dec = s_beta + 3 * CH;
-  const unsigned char* Dhl = smem + OFF_DHL + (ci & 1) * 4 * HL_BLOCK;
-  const unsigned char* Ahl = smem + OFF_AHL + (ci & 1) * 6 * HL_BLOCK;
+  const unsigned char* Mhl = smem + OFF_AHL + (ci & 1) * 6 * HL_BLOCK;
   const half_t* Aqk = reinterpret_cast<const half_t*>(smem + OFF_AQK + (ci & 1) * AQK_BYTES);
-  // (I + A) delta = R by blocked forward substitution over the 16-token blocks p,
-  // delta_p = D_p (R_p - sum_{k<p} A_pk delta_k), on hi + lo operand pairs; R and delta stay fp32
-  // in registers (the 16x16 accumulator layout is the B-operand layout)
-  h4_v dh[4], dl[4], ah[6], al[6];
-#pragma unroll
-  for (int pb = 0; pb < 4; ++pb) {
-    const h4_v* src = reinterpret_cast<const h4_v*>(Dhl + pb * HL_BLOCK + 16 * lane);
-    dh[pb] = src[0];
-    dl[pb] = src[1];
-  }
+  // (I + A) delta = R by blocked forward substitution over the 16-token blocks p:
+  // delta_p = Y_p - sum_{k<p} M_pk delta_k with Y_p = D_p R_p (phase A) and M_pk = D_p A_pk, on hi + lo
+  // operand pairs; delta stays fp32 in registers (the 16x16 accumulator layout is the B-operand layout)
+  h4_v mh[6], ml[6];
 #pragma unroll
   for (int n = 0; n < 6; ++n) {
-    const h4_v* src = reinterpret_cast<const h4_v*>(Ahl + n * HL_BLOCK + 16 * lane);
-    ah[n] = src[0];
-    al[n] = src[1];
+    const h4_v* src = reinterpret_cast<const h4_v*>(Mhl + n * HL_BLOCK + 16 * lane);
+    mh[n] = src[0];
+    ml[n] = src[1];
   }
-  h4_v xh[4], xl[4];
-  cfloat4 dlt[4];  // delta, C layout
-  cfloat4 pacc[4];  // sum_{k<p} A_pk delta_k, accumulated as soon as each delta_k exists
+  cfloat4 dlt[4];   // delta, C layout
+  cfloat4 pacc[4];  // sum_{k<p} M_pk delta_k, accumulated as soon as each delta_k exists
 #pragma unroll
   for (int pb = 0; pb < 4; ++pb) pacc[pb] = cfloat4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
   for (int pb = 0; pb < 4; ++pb) {
-    h4_v rh, rl;
-    split4(R[pb] - pacc[pb], rh, rl);
-    const cfloat4 zero = {0.f, 0.f, 0.f, 0.f};
-    dlt[pb] = mma3(dh[pb], dl[pb], rh, rl, zero);
-    split4(dlt[pb], xh[pb], xl[pb]);
+    dlt[pb] = Y[pb] - pacc[pb];
+    if (pb == 3) break;
+    h4_v xh, xl;
+    split4(dlt[pb], xh, xl);
 #pragma unroll
     for (int q = pb + 1; q < 4; ++q) {
       const int n = q * (q - 1) / 2 + pb;
-      pacc[q] = mma3(ah[n], al[n], xh[pb], xl[pb], pacc[q]);
+      pacc[q] = mma3(mh[n], ml[n], xh, xl, pacc[q]);
     }
   }
-  // S = gamma_C S + K^T (exp(G_C - G) delta): k-step s covers tokens 32 s .. 32 s + 31 in the order of
-  // pack8h(tile 2 s, tile 2 s + 1); delta^T in the same order is the A operand of the output
+  // S += K^T (exp(G_C - G) delta) (S was scaled by gamma_C in phase A): k-step s covers tokens
+  // 32 s .. 32 s + 31 in the order of pack8h(tile 2 s, tile 2 s + 1); delta^T in the same order is
+  // the A operand of the output
   f16x8_v bd[2], da[2];
 #pragma unroll
   for (int s = 0; s < 2; ++s) {
@@ -923,9 +938,6 @@ __device__ __forceinline__ void key_phase_b(const ChunkParams& p, unsigned char*
     bd[s] = pack8h(de0 * dlt[2 * s], de1 * dlt[2 * s + 1]);
     da[s] = pack8h(dlt[2 * s], dlt[2 * s + 1]);
   }
-  const float gamC = s_gam[CH - 1];
-#pragma unroll
-  for (int d = 0; d < 8; ++d) S[d] *= gamC;
 #pragma unroll
   for (int d = 0; d < 8; ++d) {
     f16x8_v ka[2];
@@ -1038,10 +1050,10 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(3, 3))) void
     lds_barrier();
     lds_barrier();
     for (int64_t ci = 0; ci < p.nch; ++ci) {
-      cfloat4 R[4], On[4];
-      key_phase_a(p, smem, S, ci, v, tid, R, On);
+      cfloat4 Y[4], On[4];
+      key_phase_a(p, smem, S, ci, v, tid, Y, On);
       lds_barrier();
-      key_phase_b(p, smem, S, ci, b, j, half_id, v, tid, R, On, out16, out_off);
+      key_phase_b(p, smem, S, ci, b, j, half_id, v, tid, Y, On, out16, out_off);
       lds_barrier();
     }
     if (p.state_out != nullptr) {
