@@ -39,11 +39,12 @@ HBM_PEAK_GBS = 8000.0  # MI355X HBM3E, GB/s
 # a plain 1 GiB device copy reads back in the same runs. Counters need rocprofv3, so the figures
 # are the committed profile's, not measured live.
 TRAFFIC_DECODE = 1959210677
-TRAFFIC_DELTA = 831122632  # chunk_kernel alone; the step (with prep_kernel) moves 1,416,943,509
+TRAFFIC_DELTA = 831154209  # chunk_kernel alone; the step (with prep_kernel) moves 1,417,016,639
 TRAFFIC_PREFILL = 888476672  # average over the eight per-chunk launches
 TRAFFIC_PROLOGUE = 675674420
 TRAFFIC_OUTPUT_NORM = 805417779
 TRAFFIC_FP8_LINEAR = 29648896  # x-resident kernel (one launch), from profiles/fp8_linear_config5_batch.md
+TRAFFIC_HYBRID = 122302416625  # config 5's 48-layer step: 12 x (kv append + paged decode + combine) + 36 delta steps
 SECONDARY_WARM_MS = 100.0  # wall time of untimed steps before each secondary (config 3, 4, 5) measurement
 MFMA_BF16_PEAK_TFLOPS = 2500.0  # MI355X dense bf16/fp16 MFMA, TFLOP/s
 
@@ -454,8 +455,20 @@ def prefill_workload(device: str, *, seed: int = 0, batch: int = 8, new: int = 4
     new_k = torch.randn((batch, kv_heads, new, dim), generator=dgen, device=device, dtype=torch.bfloat16)
     new_v = torch.randn((batch, kv_heads, new, dim), generator=dgen, device=device, dtype=torch.bfloat16)
     flops = sum(4 * heads * dim * (new * int(p) + new * (new + 1) / 2) for p in prefixes)
+    # algorithmic bytes of one step: per launch (a query chunk of n tokens at c0) and row, the K/V of
+    # the visible keys read once (prefix + c0 + n keys of 2 * kv_heads * dim bf16 each) with their
+    # table entries, and the chunk's q, gate and output rows (bf16)
+    algo_bytes = 0
+    launches = 0
+    for c0 in range(0, new, chunk):
+        n = min(chunk, new - c0)
+        launches += 1
+        for p in prefixes:
+            keys = int(p) + c0 + n
+            algo_bytes += keys * 2 * kv_heads * dim * 2 + (keys + bs - 1) // bs * 4 + 3 * n * heads * dim * 2
     return {"q": q, "gate": gate, "new_k": new_k, "new_v": new_v, "key_pool": key_pool, "value_pool": value_pool, "tables": tables.to(device),
-            "prefixes": prefixes, "batch": batch, "new": new, "chunk": chunk, "bs": bs, "flops": flops, "pool_blocks": pool_blocks}
+            "prefixes": prefixes, "batch": batch, "new": new, "chunk": chunk, "bs": bs, "flops": flops, "pool_blocks": pool_blocks,
+            "algo_bytes": algo_bytes, "launches": launches}
 
 
 def time_prefill(w, steps: int, warmup: int) -> float:
@@ -831,7 +844,8 @@ def main() -> int:
             "config": {"workload": "chunked causal paged prefill with sigmoid gate (BASELINE config 3)", "batch": 8, "new_tokens": 4096,
                        "prefix": "U[0, 8192] seed 0", "q_heads": 16, "kv_heads": 2, "head_dim": 256, "block_size": 16, "query_chunk": 512},
             "roofline": {"bound": "mfma", "achieved": round(ptf, 2), "peak": MFMA_BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
-                         "frac": round(ptf / MFMA_BF16_PEAK_TFLOPS, 4), "traffic": TRAFFIC_PREFILL, "algo_flop_per_launch": pw["flops"],
+                         "frac": round(ptf / MFMA_BF16_PEAK_TFLOPS, 4), "traffic": TRAFFIC_PREFILL, "algo_flop_per_step": pw["flops"],
+                         "algo_bytes_per_launch": round(pw["algo_bytes"] / pw["launches"]), "launches_per_step": pw["launches"],
                          "kernel": "qa::pfx::prefill_kernel<256, 1>, one launch per 512-token query chunk (kv_append between)",
                          "kernel_ms_per_step": round(pkern["paged_prefill"]["total_ms_per_step"], 4), "kernels": pkern},
         }
@@ -869,7 +883,7 @@ def main() -> int:
             "config": {"workload": "48-layer hybrid decode step, attention only (BASELINE config 5)", "batch": 128, "layers": "12 x (3 linear + 1 full)",
                        "context": "U[256, 65536] seed 0", "sum_context": hw["sum_ctx"], "pool_blocks_per_layer": hw["pool_blocks"]},
             "roofline": {"bound": "hbm", "achieved": round(hgbs, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(hgbs / HBM_PEAK_GBS, 4),
-                         "traffic": None, "algo_bytes_per_step": hw["algo_bytes"], "kernel": "whole step (12 paged-decode + 36 delta-step layers with the conv update fused in)",
+                         "traffic": TRAFFIC_HYBRID, "algo_bytes_per_step": hw["algo_bytes"], "kernel": "whole step (12 paged-decode + 36 delta-step layers with the conv update fused in)",
                          "kernels": hkern},
         }
         del hw
