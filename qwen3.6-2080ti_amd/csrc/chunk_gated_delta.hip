@@ -488,7 +488,7 @@ __device__ __forceinline__ void chunk_item(const ChunkParams& p, int& b, int& j,
 constexpr int VS_BYTES = CH * LD64 * 2;  // one V tile [tok][64 dv]
 // per-token scalars of a chunk: beta, G, gamma = exp(G), exp(G_C - G), and the factors of R for V
 // stored scaled by -log2(e) (see conv_v): beta' = -ln(2) beta, gamma' = log2(e) gamma
-constexpr int SC_BYTES = 6 * CH * 4;
+constexpr int SC_BYTES = 9 * CH * 4;
 constexpr int HL_BLOCK = 1024;           // one 16x16 block as fp16 hi | lo A operands, 16 bytes per lane
 constexpr int OFF_QS = 0;                // Qs x 2
 constexpr int OFF_KS = OFF_QS + 2 * KS_BYTES;
@@ -665,18 +665,32 @@ __device__ __forceinline__ cfloat4 load_gate(const ChunkParams& p, int64_t b, in
   return *reinterpret_cast<const cfloat4*>(base + 4 * (lane & 15));
 }
 
+// The per-token scalars of block u (tokens 16 u .. 16 u + 15, in lanes 0..15 of gb).  Besides
+// beta, G and the decays of the gate record: beta' and gamma' of the scaled SiLU, and the factors
+// of the off-diagonal decays.  For i in block p > k >= block of l, exp(G_i - G_l) =
+// rf_i exp(G_{16p} - G_{16k+15}) cf_l with rf_i = exp(G_i - G_{16p}) and cf_l = exp(G_{16k+15} - G_l);
+// G never increases, so all three factors lie in [0, 1] and none overflows.
 __device__ __forceinline__ void store_gate(unsigned char* smem, const cfloat4& gb, int64_t ci, int u, int lane) {
+  const float g_first = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, gb.x), 0));
+  const float g_last = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, gb.x), 15));
   if (lane < 16) {
     float* sc = reinterpret_cast<float*>(smem + OFF_SC + (ci & 1) * SC_BYTES);
     const int t = 16 * u + lane;
+    const float rf = __expf(gb.x - g_first);
     sc[t] = gb.y;           // beta
     sc[CH + t] = gb.x;      // G
     sc[2 * CH + t] = gb.z;  // gamma = exp(G)
     sc[3 * CH + t] = gb.w;  // exp(G_C - G)
     sc[4 * CH + t] = -0.69314718055994531f * gb.y;  // beta' = -ln(2) beta
     sc[5 * CH + t] = 1.4426950408889634f * gb.z;    // gamma' = log2(e) gamma
+    sc[6 * CH + t] = rf;                            // rf
+    sc[7 * CH + t] = gb.y * rf;                     // beta rf
+    sc[8 * CH + t] = __expf(g_last - gb.x);         // cf
   }
 }
+
+// exp(G_{16 ti} - G_{16 tl + 15}), the block factor of the off-diagonal decays (ti > tl)
+__device__ __forceinline__ float block_decay(const float* s_G, int ti, int tl) { return __expf(s_G[16 * ti] - s_G[16 * tl + 15]); }
 
 // Epilogues of the state-independent blocks of chunk ci, from a product x = X_l X_i^T held as
 // lane (lq, lc) = [16 ti + lc][16 tl + 4 lq + r]:
@@ -689,14 +703,13 @@ __device__ __forceinline__ void store_gate(unsigned char* smem, const cfloat4& g
 // A-operand layout of M.
 __device__ __forceinline__ void m_store(unsigned char* smem, int64_t ci, int ti, int tl, const cfloat4& x, int lane) {
   const int lq = lane >> 4, lc = lane & 15;
-  const float* s_beta = reinterpret_cast<const float*>(smem + OFF_SC + (ci & 1) * SC_BYTES);
-  const float* s_G = s_beta + CH;
-  const cfloat4 bi = *reinterpret_cast<const cfloat4*>(s_beta + 16 * ti + 4 * lq);
-  const cfloat4 gi = *reinterpret_cast<const cfloat4*>(s_G + 16 * ti + 4 * lq);
-  const float gl = s_G[16 * tl + lc];
+  const float* sc = reinterpret_cast<const float*>(smem + OFF_SC + (ci & 1) * SC_BYTES);
+  // A[i][l] = beta_i rf_i exp(G_{16 ti} - G_{16 tl + 15}) cf_l (K K^T)[i][l] (ti > tl)
+  const cfloat4 brf = *reinterpret_cast<const cfloat4*>(sc + 7 * CH + 16 * ti + 4 * lq);
+  const float cs = sc[8 * CH + 16 * tl + lc] * block_decay(sc + CH, ti, tl);
   cfloat4 a;
 #pragma unroll
-  for (int r = 0; r < 4; ++r) a[r] = bi[r] * __expf(gi[r] - gl) * x[r];
+  for (int r = 0; r < 4; ++r) a[r] = brf[r] * cs * x[r];
   h4_v ah, al;
   split4(a, ah, al);
   const h4_v* dsrc = reinterpret_cast<const h4_v*>(smem + OFF_DHL + (ci & 1) * 4 * HL_BLOCK + ti * HL_BLOCK + 16 * lane);
@@ -712,16 +725,25 @@ __device__ __forceinline__ void m_store(unsigned char* smem, int64_t ci, int ti,
 
 __device__ __forceinline__ void aqk_store(unsigned char* smem, int64_t ci, int ti, int tl, const cfloat4& x, int lane) {
   const int lq = lane >> 4, lc = lane & 15;
-  const float* s_G = reinterpret_cast<const float*>(smem + OFF_SC + (ci & 1) * SC_BYTES) + CH;
+  const float* sc = reinterpret_cast<const float*>(smem + OFF_SC + (ci & 1) * SC_BYTES);
+  const float* s_G = sc + CH;
   half_t* Aqk = reinterpret_cast<half_t*>(smem + OFF_AQK + (ci & 1) * AQK_BYTES);
   const int i = 16 * ti + lc;
-  const float gi = s_G[i];
-  const cfloat4 gl = *reinterpret_cast<const cfloat4*>(s_G + 16 * tl + 4 * lq);
   float e[4];
+  if (ti > tl) {
+    // off the diagonal: the decay from the row and column factors (no mask)
+    const float ri = sc[6 * CH + i] * block_decay(s_G, ti, tl);
+    const cfloat4 cl = *reinterpret_cast<const cfloat4*>(sc + 8 * CH + 16 * tl + 4 * lq);
 #pragma unroll
-  for (int r = 0; r < 4; ++r) {
-    const float y = __expf(gi - gl[r]) * x[r];
-    e[r] = 16 * tl + 4 * lq + r <= i ? y : 0.f;
+    for (int r = 0; r < 4; ++r) e[r] = ri * cl[r] * x[r];
+  } else {
+    const float gi = s_G[i];
+    const cfloat4 gl = *reinterpret_cast<const cfloat4*>(s_G + 16 * tl + 4 * lq);
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const float y = __expf(gi - gl[r]) * x[r];
+      e[r] = 16 * tl + 4 * lq + r <= i ? y : 0.f;
+    }
   }
   store4h(Aqk + i * LD64 + aqk_col(16 * tl + 4 * lq), e[0], e[1], e[2], e[3]);
 }
