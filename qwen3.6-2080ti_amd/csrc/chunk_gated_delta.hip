@@ -30,16 +30,17 @@
 // holds are not reserved in the others:
 //  * key waves 0..3 own a 16-column dv tile each and run only work that depends on the state,
 //    chunk c in iteration c: K S0 and the output's S0^T Q^T from one fp16 copy of the fp32 state
-//    registers, R, the blocked forward substitution of the delta system over 16-token blocks,
-//    delta_p = D_p (R_p - sum_{k<p} A_pk delta_k), on fp16 hi + lo operand pairs (mma3 below,
-//    which keeps the state within fp32-state tolerance), the state update, and the output
-//    O^T = gamma (S0^T Q^T) + delta^T Aqk^T with its stores.  They write no LDS.
+//    registers, R and Y_p = D_p R_p; after the mid-chunk barrier the blocked forward substitution
+//    of the delta system over 16-token blocks, delta_p = Y_p - sum_{k<p} M_pk delta_k with
+//    M_pk = D_p A_pk, on fp16 hi + lo operand pairs (mma3 below, which keeps the state within
+//    fp32-state tolerance), the state update, and the output O^T = gamma (S0^T Q^T) +
+//    delta^T Aqk^T with its stores.  They write no LDS.
 //  * A waves 4..7 prepare chunk c + 1: each stages its own 16 k rows and gate scalars, then
 //    (from its own rows, no barrier) the diagonal block A_uu and D_u = (I + A_uu)^-1 as hi | lo
-//    operands; after the mid-chunk barrier, the off-diagonal A blocks (hi | lo) and eight of the
-//    64 v channels of chunk c + 1 (conv1d + SiLU).
+//    operands; after the mid-chunk barrier, one block M_pk (hi | lo) and eight of the 64 v
+//    channels of chunk c + 1 (conv1d + SiLU).
 //  * V waves 8..11 stage chunk c + 1's q rows and convolve eight v channels each; after the
-//    mid-chunk barrier, its Aqk tiles.
+//    mid-chunk barrier, its Aqk tiles (and, on waves 10 and 11, the last two M blocks).
 // Every buffer another role reads in the same phase is double-buffered by chunk parity.  Matrix
 // products use v_mfma_f32_16x16x32_f16 / 16x16x16 (fp32 accumulation); the 16x16 accumulator
 // layout equals the B-operand layout, so delta feeds the next block, the state update and the
