@@ -521,8 +521,8 @@ __device__ __forceinline__ float rotate_in(float x) {
 // SiLU, src/reference_ops.py:245-258) with one token per lane, into Vs.  prev[ch] holds the raw input
 // of channel ch at token ci * 64 - 64 + lane (the previous chunk; for chunk 0 lanes 61..63 hold the
 // initial conv state, tokens -3..-1); the three earlier tokens of lane l come from lanes l - 1 ..
-// l - 3 by DPP, and for the first lanes from prev rotated in.  The taps, read from LDS (one address
-// for the whole wave), are stored times -log2(e), so the tap sum is t = -log2(e) a and
+// l - 3 by DPP, and for the first lanes from prev rotated in.  The taps w (wave-uniform, held in
+// registers by the caller) are stored times -log2(e), so the tap sum is t = -log2(e) a and
 // silu(a) = a / (1 + 2^t); Vs receives t / (1 + 2^t) = -log2(e) silu(a), and R's factors carry the
 // constant back (beta' and gamma' of the scalars).  Tokens past the sequence enter as zero inputs
 // (load_v) and their v is never used: their beta is zero, so their rows of R and delta are zero.
