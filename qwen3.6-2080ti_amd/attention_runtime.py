@@ -343,7 +343,8 @@ def _device_pool_reason(config: AttentionConfig, query: Any, key_blocks: Any, va
     """The dispatch ladder for a step on device page tables, checked before anything is written:
     the reference's reasons (one token per row), then what the native kernels need of the pool
     (a shared ``(P, H_kv, bs, D)`` bf16 pool with the tables' block size and block count)."""
-    reason = paged_attention_fallback_reason(config, query, key_blocks, value_blocks, seq_len=int(query.shape[2]), batched=False)
+    seq_len = int(query.shape[2]) if len(tuple(getattr(query, "shape", ()))) == 4 else 1
+    reason = paged_attention_fallback_reason(config, query, key_blocks, value_blocks, seq_len=seq_len, batched=False)
     if reason != "no_kernel":
         return reason
     if key_blocks.dim() != 4 or tuple(value_blocks.shape) != tuple(key_blocks.shape):
@@ -394,7 +395,7 @@ def full_attention_decode_step_device(
     rows = int(q_proj.shape[0])
     full = config.full_attention
     heads, head_dim, kv_heads = full.num_heads, full.head_dim, full.num_key_value_heads
-    probe = q_proj.view(rows, heads, 1, 2 * head_dim)[..., :head_dim]
+    probe = _query_probe(q_proj, heads, head_dim)
     reason = _device_pool_reason(config, probe, key_blocks, value_blocks, tables)
     if reason == "no_kernel" and (rows != tables.rows or int(key_blocks.shape[1]) != kv_heads or int(key_blocks.shape[3]) != head_dim
                                   or str(key_blocks.dtype) != "torch.bfloat16" or str(q_proj.dtype) != "torch.bfloat16"):
@@ -433,6 +434,16 @@ def _row_offsets(rows: int, device: Any) -> Any:
     return cached
 
 
+def _query_probe(q_proj: Any, heads: int, head_dim: int) -> Any:
+    """The query half of ``q_proj`` ``(rows, H*2D)`` as ``(rows, H, 1, D)`` for the reason ladder;
+    ``q_proj`` itself when it has another shape (the ladder then reports ``"shape"`` after its
+    ``"disabled"`` and ``"cpu"`` checks, instead of a view error)."""
+    shape = tuple(getattr(q_proj, "shape", ()))
+    if len(shape) != 2 or shape[1] != heads * 2 * head_dim or q_proj.stride(-1) != 1:
+        return q_proj
+    return q_proj.view(shape[0], heads, 1, 2 * head_dim)[..., :head_dim]
+
+
 def full_attention_prefill_device(
     q_proj: Any, k_proj: Any, v_proj: Any, q_norm_weight: Any, k_norm_weight: Any, key_blocks: Any, value_blocks: Any,
     step: PrefillStep, config: AttentionConfig, runtime: HotPathRuntime, rope: RopeConfig = RopeConfig(),
@@ -462,7 +473,9 @@ def full_attention_prefill_device(
     tokens = int(q_proj.shape[0])
     full = config.full_attention
     heads, head_dim, kv_heads = full.num_heads, full.head_dim, full.num_key_value_heads
-    probe = q_proj.view(tokens, heads, 1, 2 * head_dim)[:1, :, :, :head_dim]
+    probe = _query_probe(q_proj, heads, head_dim)
+    if probe.dim() == 4:
+        probe = probe[:1]  # one token stands for the step: the ladder reads heads and widths, not rows
     reason = paged_attention_fallback_reason(config, probe, key_blocks, value_blocks, seq_len=1, batched=False)
     if reason == "no_kernel":
         if key_blocks.dim() != 4:

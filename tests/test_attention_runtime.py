@@ -234,6 +234,36 @@ def test_prefill_and_decode_step_entries_follow_the_ladder_on_cpu(overrides, cou
     assert torch.count_nonzero(pool.key_blocks) == 0
 
 
+@pytest.mark.parametrize("overrides,counter", [({"native_paged_attention": False}, "fallback_disabled"), ({}, "fallback_cpu")])
+def test_projection_entries_take_the_ladder_on_misshaped_projections(overrides, counter) -> None:
+    """A q_proj whose width is not H*2D goes down the same ladder (no view error): the reasons
+    before the shape check still decide, and nothing is written."""
+    from decode_state import PrefillStep
+
+    pool, tables = _tables_on_cpu()
+    config = _small_enabled(**overrides)
+    runtime = ar.HotPathRuntime()
+    q_proj = torch.zeros(3, 2 * 2 * 4 + 1, dtype=torch.bfloat16)
+    kv = torch.zeros(3, 2 * 4, dtype=torch.bfloat16)
+    w = torch.zeros(4, dtype=torch.bfloat16)
+    step = PrefillStep(rows=(0,), counts=(3,), index=torch.tensor([0]), cu_seqlens=torch.tensor([0, 3], dtype=torch.int32),
+                       starts=torch.zeros(1, dtype=torch.int32), block_tables=torch.full((1, 4), -1, dtype=torch.int32), max_new=3,
+                       total_tokens=3, block_size=2)
+    assert ar.full_attention_prefill_device(q_proj, kv, kv, w, w, pool.key_blocks, pool.value_blocks, step, config, runtime) is None
+    assert ar.full_attention_decode_step_device(q_proj, kv, kv, w, w, pool.key_blocks, pool.value_blocks, tables, config, runtime) is None
+    assert runtime.paged_attention_stats.to_dict()[counter] == 2
+    assert torch.count_nonzero(pool.key_blocks) == 0
+
+
+def test_query_probe_is_the_query_half_or_the_projection_itself() -> None:
+    q_proj = torch.arange(2 * 3 * 2 * 4, dtype=torch.float32).reshape(2, 3 * 2 * 4)
+    probe = ar._query_probe(q_proj, 3, 4)
+    assert tuple(probe.shape) == (2, 3, 1, 4)
+    # head h's query is the first D of its 2D-wide slice of the row
+    assert torch.equal(probe[1, 2, 0], q_proj[1, 2 * 8 : 2 * 8 + 4])
+    assert ar._query_probe(q_proj[:, :-1], 3, 4) is not None and tuple(ar._query_probe(q_proj[:, :-1], 3, 4).shape) == (2, 23)
+
+
 def test_reserve_prefill_rejects_bad_steps_before_touching_the_device() -> None:
     _pool, tables = _tables_on_cpu()
     tables.add_request()
