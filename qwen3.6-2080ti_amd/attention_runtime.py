@@ -390,7 +390,10 @@ def full_attention_decode_step_device(
     layer's shared pool; the batched decode follows, and the gate (read in place from
     ``q_proj``) multiplies its output.  Returns ``(rows, 1, H*D)`` in bf16 (rows without a
     request give zeros), or ``None`` -- counted by the reference's ladder -- when the caller must
-    run its dense path; that is decided before anything is written.
+    run its dense path; that is decided before anything is written.  Once the step's K/V are
+    appended, errors raise instead of returning ``None``: with ``no_alloc`` a batch whose partials
+    exceed the library's 32 MiB scratch raises ``RuntimeError`` with the token already in the
+    cache, so the caller must not append it again.
     """
     rows = int(q_proj.shape[0])
     full = config.full_attention
