@@ -56,6 +56,20 @@ def test_chunked_prefill_zero_state_ragged_matches_oracle() -> None:
     torch.testing.assert_close(tail.cpu(), ref_tail, atol=0, rtol=0)
 
 
+@pytest.mark.parametrize("key_heads,value_heads", [(1, 3), (1, 4), (2, 6)])
+def test_value_head_groups_of_three_and_four_match_oracle(key_heads, value_heads) -> None:
+    # value heads j and j + 1 of one key head share its q/k rows; groups larger than the two of
+    # the baseline configurations map workgroups to key heads through the same division
+    shape = gd.LinearShape(key_heads=key_heads, value_heads=value_heads, key_head_dim=128, value_head_dim=128, conv_kernel_dim=4)
+    mixed, a, b, a_log, dt_bias, w = _inputs(47 + value_heads, 1, 130, shape, a_log_scale=0.5)
+    ref_core, ref_state, ref_tail = gd.linear_attention_core(mixed.float(), a, b, a_log, dt_bias, w, shape)
+    out, state, tail = _run(mixed, a, b, a_log, dt_bias, w, shape, out_dtype=torch.float32)
+    case = f"heads {key_heads}/{value_heads}"
+    torch.testing.assert_close(out.cpu(), ref_core, atol=2e-2, rtol=2e-2, msg=lambda m: f"{case}: {m}")
+    assert _rel(state, ref_state) < 1e-3, case
+    torch.testing.assert_close(tail.cpu(), ref_tail, atol=0, rtol=0, msg=lambda m: f"{case}: {m}")
+
+
 def test_chunked_prefill_with_initial_and_conv_state_fp32_out() -> None:
     mixed, a, b, a_log, dt_bias, w = _inputs(42, 1, 200, SHAPE, a_log_scale=0.5)
     gen = torch.Generator().manual_seed(43)
