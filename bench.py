@@ -39,7 +39,7 @@ HBM_PEAK_GBS = 8000.0  # MI355X HBM3E, GB/s
 # a plain 1 GiB device copy reads back in the same runs. Counters need rocprofv3, so the figures
 # are the committed profile's, not measured live.
 TRAFFIC_DECODE = 1959210677
-TRAFFIC_DELTA = 831154209  # chunk_kernel alone; the step (with prep_kernel) moves 1,417,016,639
+TRAFFIC_DELTA = 831048182  # chunk_kernel alone; the step (with prep_kernel) moves 1,416,829,956
 TRAFFIC_PREFILL = 888476672  # average over the eight per-chunk launches
 TRAFFIC_PROLOGUE = 675674420
 TRAFFIC_OUTPUT_NORM = 805417779
